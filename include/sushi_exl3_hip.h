@@ -1,0 +1,181 @@
+/*
+ * sushi_exl3_hip -- MI355X (gfx950) HIP implementation of beamivalice/sushi's EXL3/STQ trellis-quantized
+ * linear-layer hot path, behind a plain C ABI.
+ *
+ * This is the cut the reference's host would bind instead of its `sushi_exl3` Zig module
+ * (src/exl3/root.zig, src/exl3/linear.zig, src/exl3/expert_exl3_kernels.zig).  Conventions:
+ *   - every pointer is a device pointer unless stated; the caller owns all memory (inputs, outputs, workspace);
+ *   - nothing here allocates device memory: a call that needs scratch takes a caller workspace whose size the
+ *     matching *_workspace_size() reports (the reference allocates per call through MLX; this ABI does not);
+ *   - launches are asynchronous on the caller's stream; no entry point synchronises the host
+ *     (the reference never reads back on the decode path either, docs/mlx-serve-integration.md:186-191);
+ *   - every refusal happens before any launch and returns a negative status; exl3_last_error() describes it
+ *     (thread-local, valid until the next call on the same thread);
+ *   - not thread-safe per stream: call from the thread that owns the stream, as the reference requires
+ *     (docs/mlx-serve-integration.md:151-169).  The decode parameters travel with every call (no process-global
+ *     codebook, unlike kernels.setDecodeParams, src/exl3/expert_exl3_kernels.zig:937-944).
+ *
+ * Layouts (the reference's, src/exl3/root.zig:28-39):
+ *   trellis  u16 [E][in/16][out/16][n]   n = 16*K halfwords per 16x16 tile, even, 16..128
+ *   suh      f16 [E][in]                 input sign/scale vector
+ *   svh      f16 [E][out]                output sign/scale vector
+ *   x        [rows][in]  f16 | bf16 | f32  (exl3_dtype)
+ *   y        [rows][out] same dtype set
+ */
+#ifndef SUSHI_EXL3_HIP_H
+#define SUSHI_EXL3_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_ABI_VERSION 1
+
+/* Codebook: the reference's `Codebook` enum values (src/exl3/expert_exl3.zig:54-61), plus 3INST as an
+ * extension (QTIP's LCG codebook, not in the reference). */
+typedef enum {
+    EXL3_CB_MUL1 = 0,
+    EXL3_CB_MCG = 1,
+    EXL3_CB_SPEC1 = 2,
+    EXL3_CB_PAIR1 = 3,
+    EXL3_CB_STD1 = 4,
+    EXL3_CB_3INST = 5
+} exl3_codebook;
+
+/* Codebook tables, in the order of codebook_tables.zig `shipped` (:101-106). */
+typedef enum {
+    EXL3_TABLE_NONE = -1,
+    EXL3_TABLE_PAIR1_W16_V1 = 0,
+    EXL3_TABLE_SPEC1_W15 = 1,
+    EXL3_TABLE_SPEC1_W16 = 2,
+    EXL3_TABLE_STD1 = 3
+} exl3_table;
+
+/* `Decode` (src/exl3/expert_exl3.zig:141-174): codebook, codeword window width (8..16) and table. */
+typedef struct {
+    int32_t codebook;
+    int32_t window_bits;
+    int32_t table;
+} exl3_decode_t;
+
+typedef enum { EXL3_DT_F16 = 0, EXL3_DT_BF16 = 1, EXL3_DT_F32 = 2 } exl3_dtype;
+
+/* Status codes.  The reference's named Zig errors map one to one (src/exl3/root.zig:104-133, :421-423;
+ * src/exl3/expert_exl3_kernels.zig:2569, :1475); DECLINED is the reference's `null` = "take the fallback"
+ * (src/exl3/linear.zig:56-60, src/moe_gqmv.zig:574-577). */
+typedef enum {
+    EXL3_OK = 0,
+    EXL3_DECLINED = 1,
+    EXL3_ERR_BAD_SHAPE = -1,                 /* BadExl3Shape */
+    EXL3_ERR_BAD_DTYPE = -2,                 /* BadExl3Dtype */
+    EXL3_ERR_TABLE_UNKNOWN = -3,             /* Exl3CodebookTableUnknown */
+    EXL3_ERR_TOPK_EXCEEDS_REDUCE = -4,       /* Exl3TopKExceedsReduceBank */
+    EXL3_ERR_TOPK_UNSUPPORTED = -5,          /* Exl3TopkUnsupported */
+    EXL3_ERR_INVALID_CLAMP = -6,             /* InvalidExl3Clamp */
+    EXL3_ERR_SHARED_NEEDS_DECODE_ROWS = -7,  /* Exl3SharedNeedsDecodeRows */
+    EXL3_ERR_LAUNCH = -8,                    /* Exl3GemmLaunchFailed / a HIP launch error */
+    EXL3_ERR_WORKSPACE = -9,                 /* caller workspace too small or misaligned */
+    EXL3_ERR_RATE_MISSING = -10,             /* Exl3CodebookTableRateMissing */
+    EXL3_ERR_WINDOW = -11                    /* Exl3WindowUnsupported */
+} exl3_status;
+
+/* One projection's bank (`Proj`, src/exl3/root.zig:28-30). */
+typedef struct {
+    const uint16_t *trellis;
+    const uint16_t *suh;
+    const uint16_t *svh;
+    int32_t n;
+} exl3_proj_t;
+
+/* `Bank` (src/exl3/root.zig:39). */
+typedef struct {
+    exl3_proj_t gate, up, down;
+} exl3_bank_t;
+
+/* `Ragged` (src/exl3/rate_groups.zig:22-60): one ragged trellis per projection (experts' tiles contiguous, each
+ * at its own rate), scales concatenated over experts, and the per-expert meta table of META_WORDS = 8 u32:
+ * {n_gate, n_up, n_down, group, off_gate, off_up, off_down, local}, offsets in u32 words. */
+typedef struct {
+    const uint16_t *trellis[3];
+    const uint16_t *suh[3];
+    const uint16_t *svh[3];
+    const uint32_t *meta; /* device [experts][8] */
+    int32_t experts;
+} exl3_ragged_t;
+
+int32_t exl3_abi_version(void);
+const char *exl3_last_error(void);
+
+/* Decodes `count` codewords (low `window_bits` kept) at rate n to f16 bits; PAIR1 writes two weights per codeword
+ * (both weights of a pair come from the odd weight's codeword).  Replaces the Metal exhaustive-codeword test kernels
+ * (src/exl3/kernel_source.zig:409-517) and the host `decodeCodeword`/`decodeHashMask`/`decodePair`
+ * (src/exl3/expert_exl3.zig:267-311). */
+int32_t exl3_decode_codewords(const uint16_t *codewords, int64_t count, int32_t n, exl3_decode_t dec, uint16_t *out,
+                              hipStream_t stream);
+
+/* `reconstructInner` (src/exl3/expert_exl3.zig:416-438): the dequantized f16 inner matrix [in][out] of one bank,
+ * bit-exact with the reference decoder. */
+int32_t exl3_reconstruct_inner(const uint16_t *trellis, int32_t in_features, int32_t out_features, int32_t n,
+                               exl3_decode_t dec, uint16_t *out, hipStream_t stream);
+
+/* `linear.linear` / `linearWith` (src/exl3/linear.zig:27-34) and `trunk.matmul` (src/exl3/trunk.zig:53-92):
+ * y[rows][out] = finish(inner(prepare(x))) for one bank (trellis [1][in/16][out/16][n]).  Rows <= 8 take the
+ * decode GEMV (PROJECT_ROWS_MAX, src/exl3/project_rows.zig:456-459), wider the MFMA GEMM
+ * (`run`, src/exl3/linear.zig:317-336).  in and out must be multiples of 128. */
+size_t exl3_linear_workspace_size(int32_t rows, int32_t in_features, int32_t out_features, int32_t n);
+int32_t exl3_linear(const void *x, int32_t x_dtype, int32_t rows, int32_t in_features, int32_t out_features,
+                    const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
+                    void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* `linear.linearGrouped` (src/exl3/linear.zig:37-53): x [G][rows][in] through the G-bank projection
+ * (trellis [G][in/16][out/16][n], suh [G][in], svh [G][out]), bank g serving x[g] -> y [G][rows][out]. */
+size_t exl3_linear_grouped_workspace_size(int32_t groups, int32_t rows, int32_t in_features, int32_t out_features,
+                                          int32_t n);
+int32_t exl3_linear_grouped(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in_features,
+                            int32_t out_features, const uint16_t *trellis, int32_t n, const uint16_t *suh,
+                            const uint16_t *svh, exl3_decode_t dec, void *y, int32_t y_dtype, void *workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+/* Clears a workspace once after allocation (the fused-finish arrival counters must start at zero; every call
+ * leaves them at zero again).  A small fill kernel, never hipMemsetAsync. */
+int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Routed SwiGLU experts: `moe` (src/exl3/root.zig:51-53), `moeWithShared` (:56-67, `shared` [rows][hidden] in y's
+ * dtype, added after the routed output's rounding as REDUCE_SHARED_SOURCE does,
+ * src/exl3/expert_exl3_kernels.zig:2391-2406), `moeClamped` (:98-124, clamp_limit in 1..128, 0 = none).
+ * x [rows][hidden]; inds [rows][topk] u32 (i32 accepted: same bits); scores [rows][topk] f32.
+ * Banks: gate/up trellis [E][hidden/16][inter/16][n], down [E][inter/16][hidden/16][n].  The decode chain
+ * (pair GEMV -> fused SwiGLU mid + down GEMV -> score-weighted reduce) serves every row count. */
+size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
+int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
+                 const exl3_bank_t *bank, const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
+                 int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
+                 void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* `moeRagged` (src/exl3/root.zig:582-644) over a rate-grouped ragged bank (rate_groups.zig:22-140): each expert
+ * decodes at its own (n_gate, n_up, n_down) read from the meta table.  `max_n` bounds every rate in the table. */
+int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                        const exl3_ragged_t *bank, const uint32_t *inds, const float *scores, int32_t topk,
+                        exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
+                        void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Router chain `moeRoutingChainOn` (src/moe_router.zig:22-62): top-k over f32 logits [rows][experts]
+ * (ties to the lower expert index, listed in descending logit order), softmax over all experts, gathered and
+ * renormalised over the k picked.  experts <= 1024, k <= 32. */
+int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds,
+                        float *scores, hipStream_t stream);
+
+/* `layout.tileMajor` / `tileMajorInverse` (src/exl3/layout.zig:139-158): one projection of `experts` experts
+ * between the pack order [IT][OT][n] and the pair-major order [OT/2][IT][2][n]. */
+int32_t exl3_tile_major(const uint16_t *src, uint16_t *dst, int32_t experts, int32_t it, int32_t ot, int32_t n,
+                        int32_t inverse, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,462 @@
+// The C ABI (include/sushi_exl3_hip.h): validation, arm choice, workspace carving and launches.
+//
+// Every refusal happens before any launch (as the reference's `Exl3*` errors do, src/exl3/root.zig:104-133), and the
+// library never allocates device memory: scratch comes from the caller's workspace.
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "../../include/sushi_exl3_hip.h"
+#include "exl3_kernels.h"
+#include "exl3_tables.h"
+
+using namespace exl3;
+
+namespace {
+
+thread_local std::string g_err;
+
+int32_t fail(int32_t code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int32_t fail(int32_t code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int32_t ok() {
+    g_err.clear();
+    return EXL3_OK;
+}
+
+int32_t launched(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(EXL3_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+// The decode family and constants for (dec, n); status on refusal.
+int32_t resolve_decode(const exl3_decode_t &dec, int n, int *fam, DecodeK *k, bool per_rate_table = false) {
+    if (dec.window_bits < 8 || dec.window_bits > 16)
+        return fail(EXL3_ERR_WINDOW, "window %d is not a codeword width in 8..16", dec.window_bits);
+    k->wmask = dec.window_bits >= 16 ? 0xFFFFu : ((1u << dec.window_bits) - 1u);
+    k->mult = k->mask0 = k->mask1 = k->rot = 0;
+    switch (dec.codebook) {
+    case EXL3_CB_MCG: *fam = FAM_MCG; return ok();
+    case EXL3_CB_MUL1: *fam = FAM_MUL1; return ok();
+    case EXL3_CB_3INST: *fam = FAM_3INST; return ok();
+    case EXL3_CB_SPEC1:
+    case EXL3_CB_STD1: {
+        // Decode.requireTable (expert_exl3.zig:162-164): a tabled codebook without its table has no pair.
+        if (dec.table < 0 || dec.table > 3)
+            return fail(EXL3_ERR_TABLE_UNKNOWN, "codebook %d needs a codebook table", dec.codebook);
+        if (kTables[dec.table].codebook != dec.codebook)
+            return fail(EXL3_ERR_TABLE_UNKNOWN, "table %d does not belong to codebook %d", dec.table, dec.codebook);
+        *fam = FAM_HASH;
+        if (per_rate_table) return ok();
+        if (!table_row(dec.table, n, k->mult, k->mask0, k->mask1, k->rot))
+            return fail(EXL3_ERR_RATE_MISSING, "table %d has no row for n=%d", dec.table, n);
+        return ok();
+    }
+    case EXL3_CB_PAIR1: {
+        if (dec.table >= 0 && dec.table != TABLE_PAIR1_W16_V1)
+            return fail(EXL3_ERR_TABLE_UNKNOWN, "PAIR1 decodes only with table pair1-w16-v1");
+        *fam = FAM_PAIR;
+        if (per_rate_table) return ok();
+        if (!table_row(TABLE_PAIR1_W16_V1, n, k->mult, k->mask0, k->mask1, k->rot))
+            return fail(EXL3_ERR_RATE_MISSING, "PAIR1 has no pair row for n=%d (24..64 even)", n);
+        return ok();
+    }
+    default: return fail(EXL3_ERR_TABLE_UNKNOWN, "unknown codebook %d", dec.codebook);
+    }
+}
+
+bool dtype_ok(int dt) { return dt == EXL3_DT_F16 || dt == EXL3_DT_BF16 || dt == EXL3_DT_F32; }
+
+float out_scale_of(int fam) { return (fam == FAM_HASH || fam == FAM_PAIR) ? 4096.0f : 1.0f; }
+
+constexpr int kRowsMax = 8;  // PROJECT_ROWS_MAX, project_rows.zig:456-459
+
+struct GemvPlan {
+    int splits;
+    size_t counters_bytes, partial_bytes;
+};
+
+GemvPlan plan_gemv(int groups, int rows, int in, int out) {
+    GemvPlan p;
+    p.splits = env_int("EXL3_GEMV_SPLITS", 0);
+    const int blocks = in / 128;
+    if (p.splits <= 0 || blocks % p.splits != 0 || in / p.splits > 2048) p.splits = gemv_default_splits(in, out, rows, groups);
+    p.counters_bytes = align_up((size_t)groups * (out / 128) * sizeof(uint32_t));
+    p.partial_bytes = p.splits > 1 ? align_up((size_t)groups * p.splits * rows * out * sizeof(float)) : 0;
+    return p;
+}
+
+size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
+    size_t b = align_up((size_t)groups * rows * in * 2);
+    if (n % 16 != 0 || n > 64) b += align_up((size_t)groups * out * in * 2);
+    return b;
+}
+
+size_t linear_ws(int groups, int rows, int in, int out, int n) {
+    if (rows <= 0) return 0;
+    if (rows <= kRowsMax) {
+        GemvPlan p = plan_gemv(groups, rows, in, out);
+        return p.counters_bytes + p.partial_bytes;
+    }
+    return gemm_bytes(groups, rows, in, out, n);
+}
+
+int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in, int32_t out,
+                    const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
+                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+    if (groups <= 0 || rows < 0 || in <= 0 || out <= 0 || in % 128 || out % 128)
+        return fail(EXL3_ERR_BAD_SHAPE, "linear: groups=%d rows=%d in=%d out=%d (in and out must be multiples of 128)",
+                    groups, rows, in, out);
+    if (!rate_admitted(n)) return fail(EXL3_ERR_BAD_SHAPE, "linear: n=%d is not an admitted rate", n);
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(EXL3_ERR_BAD_DTYPE, "linear: unsupported dtype");
+    int fam;
+    DecodeK k;
+    int32_t rc = resolve_decode(dec, n, &fam, &k);
+    if (rc) return rc;
+    if (rows == 0) return ok();
+    if (!x || !trellis || !suh || !svh || !y) return fail(EXL3_ERR_BAD_SHAPE, "linear: null operand");
+    const size_t need = linear_ws(groups, rows, in, out, n);
+    if (ws_bytes < need || (need && (!ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))))
+        return fail(EXL3_ERR_WORKSPACE, "linear: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
+    char *w = static_cast<char *>(ws);
+    if (rows <= kRowsMax) {
+        GemvPlan p = plan_gemv(groups, rows, in, out);
+        GemvArgs a{};
+        a.x = x;
+        a.x_dtype = x_dtype;
+        a.rows = rows;
+        a.in = in;
+        a.out = out;
+        a.x_div = 1;
+        a.trellis[0] = trellis;
+        a.suh[0] = suh;
+        a.svh[0] = svh;
+        a.n = n;
+        a.bank_of = nullptr;
+        a.bank_limit = groups;
+        a.meta = nullptr;
+        a.table = dec.table;
+        a.k = k;
+        a.out_scale = out_scale_of(fam);
+        a.counters = reinterpret_cast<uint32_t *>(w);
+        a.partial[0] = p.partial_bytes ? reinterpret_cast<float *>(w + p.counters_bytes) : nullptr;
+        a.y = y;
+        a.y_dtype = y_dtype;
+        a.splits = p.splits;
+        a.groups = groups;
+        a.nproj = 1;
+        a.fused_finish = env_int("EXL3_GEMV_SEPARATE_FINISH", 0) ? 0 : 1;
+        a.partial_only = 0;
+        return launched(run_gemv(fam, PRO_X, a, stream), "exl3_linear (gemv)");
+    }
+    GemmArgs g{};
+    g.x = x;
+    g.x_dtype = x_dtype;
+    g.rows = rows;
+    g.in = in;
+    g.out = out;
+    g.trellis = trellis;
+    g.n = n;
+    g.suh = suh;
+    g.svh = svh;
+    g.k = k;
+    g.xp = reinterpret_cast<uint16_t *>(w);
+    g.wt = reinterpret_cast<uint16_t *>(w + align_up((size_t)groups * rows * in * 2));
+    g.y = y;
+    g.y_dtype = y_dtype;
+    g.groups = groups;
+    return launched(run_gemm(fam, g, stream), "exl3_linear (gemm)");
+}
+
+struct MoePlan {
+    int s1, s2;
+    size_t gu_bytes, down_bytes;
+};
+
+MoePlan plan_moe(int nslots, int hidden, int inter) {
+    MoePlan p;
+    p.s1 = gemv_default_splits(hidden, inter, 1, 2 * nslots);
+    p.s2 = gemv_default_splits(inter, hidden, 1, nslots);
+    p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
+    p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));
+    return p;
+}
+
+constexpr int kReduceMaxTopk = 32;  // REDUCE_MAX_TOPK, expert_exl3_kernels.zig:2562
+
+int32_t moe_common_checks(int32_t x_dtype, int32_t y_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                          int32_t topk, int32_t clamp_limit) {
+    if (clamp_limit < 0 || clamp_limit > 128)
+        return fail(EXL3_ERR_INVALID_CLAMP, "moe: clamp limit %d outside 1..128 (0 = none)", clamp_limit);
+    if (topk < 1 || topk > kReduceMaxTopk)
+        return fail(EXL3_ERR_TOPK_EXCEEDS_REDUCE, "moe: top-k %d exceeds the reduce bank (1..%d)", topk, kReduceMaxTopk);
+    if (rows < 0 || hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128)
+        return fail(EXL3_ERR_BAD_SHAPE, "moe: rows=%d hidden=%d inter=%d (multiples of 128)", rows, hidden, inter);
+    if ((long)rows * topk > (1L << 24)) return fail(EXL3_ERR_BAD_SHAPE, "moe: too many slots");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(EXL3_ERR_BAD_DTYPE, "moe: unsupported dtype");
+    return ok();
+}
+
+int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t x_dtype, int32_t rows,
+                   int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
+                   const uint16_t *const su[3], const uint16_t *const sv[3], int n_uniform, const uint32_t *meta,
+                   const uint32_t *inds, const float *scores, int32_t topk, int32_t clamp_limit, const void *shared,
+                   void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+    const int nslots = rows * topk;
+    MoePlan p = plan_moe(nslots, hidden, inter);
+    const size_t need = 2 * p.gu_bytes + p.down_bytes;
+    if (ws_bytes < need || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
+        return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
+    char *w = static_cast<char *>(ws);
+    float *gate_part = reinterpret_cast<float *>(w);
+    float *up_part = reinterpret_cast<float *>(w + p.gu_bytes);
+    float *down_part = reinterpret_cast<float *>(w + 2 * p.gu_bytes);
+    const float scale = out_scale_of(fam);
+
+    // 1) gate and up GEMVs of every slot (PAIR_GEMV_SOURCE): f32 planes [slot][split][inter]
+    GemvArgs a{};
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.rows = 1;
+    a.in = hidden;
+    a.out = inter;
+    a.x_div = topk;
+    for (int i = 0; i < 2; i++) {
+        a.trellis[i] = tr[i];
+        a.suh[i] = su[i];
+        a.svh[i] = sv[i];
+        a.meta_col[i] = i;
+    }
+    a.n = n_uniform;
+    a.bank_of = inds;
+    a.bank_limit = experts;
+    a.meta = meta;
+    a.table = table;
+    a.k = k;
+    a.out_scale = scale;
+    a.partial[0] = gate_part;
+    a.partial[1] = up_part;
+    a.splits = p.s1;
+    a.groups = nslots;
+    a.nproj = 2;
+    a.fused_finish = 0;
+    a.partial_only = 1;
+    hipError_t e = run_gemv(fam, PRO_X, a, stream);
+    if (e != hipSuccess) return launched(e, "exl3_moe (gate/up)");
+
+    // 2) SwiGLU mid + down GEMV of every slot (DOWN_FUSED_SOURCE): f32 planes [slot][split][hidden]
+    GemvArgs d{};
+    d.x = nullptr;
+    d.x_dtype = x_dtype;
+    d.rows = 1;
+    d.in = inter;
+    d.out = hidden;
+    d.x_div = 1;
+    d.mid_part[0] = gate_part;
+    d.mid_part[1] = up_part;
+    d.mid_splits = p.s1;
+    d.mid_svh[0] = sv[0];
+    d.mid_svh[1] = sv[1];
+    d.clamp_limit = (float)clamp_limit;
+    d.trellis[0] = tr[2];
+    d.suh[0] = su[2];
+    d.svh[0] = sv[2];
+    d.meta_col[0] = 2;
+    d.n = n_uniform;
+    d.bank_of = inds;
+    d.bank_limit = experts;
+    d.meta = meta;
+    d.table = table;
+    d.k = k;
+    d.out_scale = scale;
+    d.partial[0] = down_part;
+    d.splits = p.s2;
+    d.groups = nslots;
+    d.nproj = 1;
+    d.fused_finish = 0;
+    d.partial_only = 1;
+    e = run_gemv(fam, PRO_MID, d, stream);
+    if (e != hipSuccess) return launched(e, "exl3_moe (down)");
+
+    // 3) score-weighted reduce (+ shared expert)
+    ReduceArgs r{};
+    r.part = down_part;
+    r.splits = p.s2;
+    r.hidden = hidden;
+    r.topk = topk;
+    r.rows = rows;
+    r.slots = inds;
+    r.bank_limit = experts;
+    r.scores = scores;
+    r.svh = sv[2];
+    r.shared = shared;
+    r.y = y;
+    r.y_dtype = y_dtype;
+    r.out_scale = 1.0f;
+    return launched(run_moe_reduce(r, stream), "exl3_moe (reduce)");
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t exl3_abi_version(void) { return EXL3_ABI_VERSION; }
+
+const char *exl3_last_error(void) { return g_err.c_str(); }
+
+int32_t exl3_decode_codewords(const uint16_t *codewords, int64_t count, int32_t n, exl3_decode_t dec, uint16_t *out,
+                              hipStream_t stream) {
+    if (count < 0) return fail(EXL3_ERR_BAD_SHAPE, "decode_codewords: negative count");
+    if (!rate_admitted(n)) return fail(EXL3_ERR_BAD_SHAPE, "decode_codewords: n=%d is not an admitted rate", n);
+    int fam;
+    DecodeK k;
+    int32_t rc = resolve_decode(dec, n, &fam, &k);
+    if (rc) return rc;
+    if (count == 0) return ok();
+    if (!codewords || !out) return fail(EXL3_ERR_BAD_SHAPE, "decode_codewords: null operand");
+    return launched(run_decode_codewords(fam, codewords, count, k, out, stream), "exl3_decode_codewords");
+}
+
+int32_t exl3_reconstruct_inner(const uint16_t *trellis, int32_t in_features, int32_t out_features, int32_t n,
+                               exl3_decode_t dec, uint16_t *out, hipStream_t stream) {
+    if (in_features <= 0 || out_features <= 0 || in_features % 16 || out_features % 16)
+        return fail(EXL3_ERR_BAD_SHAPE, "reconstruct_inner: in=%d out=%d (multiples of 16)", in_features, out_features);
+    if (!rate_admitted(n)) return fail(EXL3_ERR_BAD_SHAPE, "reconstruct_inner: n=%d is not an admitted rate", n);
+    int fam;
+    DecodeK k;
+    int32_t rc = resolve_decode(dec, n, &fam, &k);
+    if (rc) return rc;
+    if (!trellis || !out) return fail(EXL3_ERR_BAD_SHAPE, "reconstruct_inner: null operand");
+    return launched(run_reconstruct_inner(fam, trellis, in_features / 16, out_features / 16, n, k, out, stream),
+                    "exl3_reconstruct_inner");
+}
+
+size_t exl3_linear_workspace_size(int32_t rows, int32_t in_features, int32_t out_features, int32_t n) {
+    if (rows <= 0 || in_features <= 0 || out_features <= 0 || in_features % 128 || out_features % 128) return 0;
+    return linear_ws(1, rows, in_features, out_features, n);
+}
+
+size_t exl3_linear_grouped_workspace_size(int32_t groups, int32_t rows, int32_t in_features, int32_t out_features,
+                                          int32_t n) {
+    if (groups <= 0 || rows <= 0 || in_features <= 0 || out_features <= 0 || in_features % 128 || out_features % 128)
+        return 0;
+    return linear_ws(groups, rows, in_features, out_features, n);
+}
+
+int32_t exl3_linear(const void *x, int32_t x_dtype, int32_t rows, int32_t in_features, int32_t out_features,
+                    const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
+                    void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    return linear_impl(x, x_dtype, 1, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype,
+                       workspace, workspace_bytes, stream);
+}
+
+int32_t exl3_linear_grouped(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in_features,
+                            int32_t out_features, const uint16_t *trellis, int32_t n, const uint16_t *suh,
+                            const uint16_t *svh, exl3_decode_t dec, void *y, int32_t y_dtype, void *workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+    return linear_impl(x, x_dtype, groups, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype,
+                       workspace, workspace_bytes, stream);
+}
+
+int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!workspace || workspace_bytes == 0) return ok();
+    if (reinterpret_cast<uintptr_t>(workspace) % 4) return fail(EXL3_ERR_WORKSPACE, "workspace_init: misaligned");
+    return launched(run_fill_zero(workspace, workspace_bytes, stream), "exl3_workspace_init");
+}
+
+size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
+    if (rows <= 0 || topk <= 0 || hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) return 0;
+    MoePlan p = plan_moe(rows * topk, hidden, inter);
+    return 2 * p.gu_bytes + p.down_bytes;
+}
+
+int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
+                 const exl3_bank_t *bank, const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
+                 int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
+                 void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    (void)verify_rows;  // every row count runs the decode chain here
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+    if (rc) return rc;
+    if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe: no bank");
+    const exl3_proj_t *pr[3] = {&bank->gate, &bank->up, &bank->down};
+    for (int i = 0; i < 3; i++)
+        if (!rate_admitted(pr[i]->n) || !pr[i]->trellis || !pr[i]->suh || !pr[i]->svh)
+            return fail(EXL3_ERR_BAD_SHAPE, "moe: projection %d has n=%d or a null operand", i, pr[i]->n);
+    if (bank->gate.n != bank->up.n || bank->gate.n != bank->down.n)
+        return fail(EXL3_ERR_BAD_SHAPE, "moe: gate/up/down rates differ (use exl3_moe_ragged)");
+    int fam;
+    DecodeK k;
+    rc = resolve_decode(dec, bank->gate.n, &fam, &k);
+    if (rc) return rc;
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe: null operand");
+    const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
+    const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
+    const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
+    return moe_launch(fam, k, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, bank->gate.n, nullptr,
+                      inds, scores, topk, clamp_limit, shared, y, y_dtype, workspace, workspace_bytes, stream);
+}
+
+int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                        const exl3_ragged_t *bank, const uint32_t *inds, const float *scores, int32_t topk,
+                        exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
+                        void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+    if (rc) return rc;
+    if (!bank || bank->experts <= 0 || !bank->meta) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: no bank");
+    for (int i = 0; i < 3; i++)
+        if (!bank->trellis[i] || !bank->suh[i] || !bank->svh[i])
+            return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: projection %d has a null operand", i);
+    int fam;
+    DecodeK k;
+    rc = resolve_decode(dec, 0, &fam, &k, /*per_rate_table=*/true);
+    if (rc) return rc;
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: null operand");
+    const int table = fam == FAM_PAIR ? (int)TABLE_PAIR1_W16_V1 : dec.table;
+    return moe_launch(fam, k, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
+                      bank->svh, 0, bank->meta, inds, scores, topk, clamp_limit, shared, y, y_dtype, workspace,
+                      workspace_bytes, stream);
+}
+
+int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds, float *scores,
+                        hipStream_t stream) {
+    if (rows < 0 || experts <= 0 || experts > 1024 || k <= 0 || k > 32 || k > experts)
+        return fail(EXL3_ERR_BAD_SHAPE, "route_topk: rows=%d experts=%d k=%d (experts <= 1024, k <= 32)", rows, experts,
+                    k);
+    if (rows == 0) return ok();
+    if (!logits || !inds || !scores) return fail(EXL3_ERR_BAD_SHAPE, "route_topk: null operand");
+    return launched(run_route_topk(logits, rows, experts, k, inds, scores, stream), "exl3_route_topk");
+}
+
+int32_t exl3_tile_major(const uint16_t *src, uint16_t *dst, int32_t experts, int32_t it, int32_t ot, int32_t n,
+                        int32_t inverse, hipStream_t stream) {
+    if (experts < 0 || it < 0 || ot < 0 || ot % 2 || n <= 0)
+        return fail(EXL3_ERR_BAD_SHAPE, "tile_major: experts=%d it=%d ot=%d n=%d (ot even)", experts, it, ot, n);
+    if (experts == 0 || it == 0 || ot == 0) return ok();
+    if (!src || !dst || src == dst) return fail(EXL3_ERR_BAD_SHAPE, "tile_major: null or aliased operand");
+    return launched(run_tile_major(src, dst, experts, it, ot, n, inverse, stream), "exl3_tile_major");
+}
+
+}  // extern "C"

@@ -1,0 +1,202 @@
+// Shared device code for the EXL3/STQ trellis kernels on gfx950 (CDNA4, wave64).
+//
+// Format facts the kernels rely on (beamivalice/sushi src/exl3/expert_exl3.zig):
+//  * A 16x16 tile of one projection is n u16 = n/2 u32 words, word i = hw[2i] | hw[2i+1] << 16, read as one
+//    MSB-first circular bitstream of 16n bits (unpackTile, :313-336).
+//  * Weight t (0..255) of a tile is the 16-bit window ending at bit floor((t+1)n/16) (Rate.bitEnd, :202-205),
+//    masked to the pack's window width (Window.mask, :124-126), decoded by the codebook (:267-311), and lands at
+//    row-major tile position tensorCorePerm[t] (:379-398): t = 8T + i, T = 4j + q, row = {2q, 2q+1, 2q+8, 2q+9}[i % 4],
+//    col = j + 8 * (i >= 4).  Row is the input (k) index, col the output index.
+//  * Tiles of one projection lie [E][in/16][out/16][n] (pack order).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+enum Codebook : int { CB_MUL1 = 0, CB_MCG = 1, CB_SPEC1 = 2, CB_PAIR1 = 3, CB_STD1 = 4, CB_3INST = 5 };
+// Kernel-side decode families: SPEC1 and STD1 share the hash-mask body with a per-rate (mult, mask) row.
+enum Family : int { FAM_MCG = 0, FAM_MUL1 = 1, FAM_HASH = 2, FAM_PAIR = 3, FAM_3INST = 4 };
+
+// Runtime decode constants for one (codebook, window, table, rate): filled on the host.
+struct DecodeK {
+    uint32_t wmask;  // codeword window mask (w16: 0xFFFF)
+    uint32_t mult;   // hash / pair multiplier
+    uint32_t mask0;  // hash mask / pair mask0
+    uint32_t mask1;  // pair mask1
+    uint32_t rot;    // pair rotate
+};
+
+__device__ __forceinline__ uint32_t pack_h2(__half lo, __half hi) {
+    return (uint32_t)__half_as_ushort(lo) | ((uint32_t)__half_as_ushort(hi) << 16);
+}
+
+// Sum of the two f16 halves of `h`, rounded to f16 (the reference's f32 add then f16 round; exact-sum arguments
+// make the two equal: for MCG/3INST both halves lie in [2^-3, 2), for hash masks both are < 2^-11).
+__device__ __forceinline__ __half half_sum(uint32_t h) {
+    return __hadd(__ushort_as_half((unsigned short)(h & 0xFFFFu)), __ushort_as_half((unsigned short)(h >> 16)));
+}
+
+// c * M mod 2^32 for a 16-bit codeword c (upper bits of c already clear).
+__device__ __forceinline__ uint32_t hash_mul(uint32_t c, uint32_t m) { return c * m; }
+
+// One weight from a 16-bit codeword for the scalar families, as f16 bits.  `c` holds the codeword in its low 16
+// bits; its high bits are ignored.
+template <int FAM>
+__device__ __forceinline__ __half decode1(uint32_t c, const DecodeK &k) {
+    c &= k.wmask;
+    if constexpr (FAM == FAM_MCG) {
+        uint32_t p = hash_mul(c, 0xCBAC1FEDu);
+        return half_sum((p & 0x8FFF8FFFu) ^ 0x3B603B60u);
+    } else if constexpr (FAM == FAM_3INST) {
+        uint32_t p = c * 89226354u + 64248484u;
+        return half_sum((p & 0x8FFF8FFFu) ^ 0x3B603B60u);
+    } else if constexpr (FAM == FAM_MUL1) {
+        uint32_t p = hash_mul(c, 0x83DCD12Du);
+        uint32_t s = (p & 0x00FF00FFu) + ((p >> 8) & 0x00FF00FFu);
+        uint32_t bsum = 0x6400u + (s & 0xFFFFu) + (s >> 16);
+        float h = __half2float(__ushort_as_half((unsigned short)bsum));
+        float r = __builtin_fmaf(h, __half2float(__ushort_as_half((unsigned short)0x1EEEu)),
+                                 __half2float(__ushort_as_half((unsigned short)0xC931u)));
+        return __float2half_rn(r);
+    } else {  // FAM_HASH: unscaled half sum; the x4096 scale is applied by the caller
+        uint32_t p = hash_mul(c, k.mult);
+        return half_sum(p & k.mask0);
+    }
+}
+
+// PAIR1: both weights of a pair from the odd weight's codeword (decodePair, expert_exl3.zig:298-301), unscaled.
+__device__ __forceinline__ uint32_t decode_pair_unscaled(uint32_t c, const DecodeK &k) {
+    c &= k.wmask;
+    uint32_t p = c * k.mult;
+    uint32_t r = (p << k.rot) | (p >> ((32u - k.rot) & 31u));
+    return pack_h2(half_sum(p & k.mask0), half_sum(r & k.mask1));
+}
+
+// Whether a family's decoded half is the weight over 4096 (hash masks and PAIR1 store unscaled sums; the scale
+// is a power of two, so applying it to the f32 result or to the f16 weight gives the same bytes).
+template <int FAM>
+__device__ __forceinline__ constexpr bool family_scaled() {
+    return FAM == FAM_HASH || FAM == FAM_PAIR;
+}
+
+// Weights (t, t+1) of a tile as packed f16 (lo = t, hi = t+1), from their codewords (c0 for t, c1 for t+1, t even).
+// Unscaled for hash/pair families.
+template <int FAM>
+__device__ __forceinline__ uint32_t decode_pair_h2(uint32_t c0, uint32_t c1, const DecodeK &k) {
+    if constexpr (FAM == FAM_PAIR) {
+        return decode_pair_unscaled(c1, k);
+    } else {
+        return pack_h2(decode1<FAM>(c0, k), decode1<FAM>(c1, k));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Bit windows.  A lane that owns codewords 32j..32j+31 of a tile (the 8 weights of fragment threads 4j..4j+3)
+// reads stream bits [2jn - 32, 2jn + 2n): codeword u (0..31) ends at 32 + floor((u+1) n / 16) in that range.
+
+template <int N>
+struct LaneBits {
+    static constexpr int NW = N / 2;                                 // words per tile
+    static constexpr bool ALIGNED = (N % 16) == 0;                   // 2jn is word aligned for every lane
+    static constexpr int AW = (2 * N + 32 + 31) / 32;                // aligned words the lane's range spans
+    __device__ static constexpr int end_of(int u) { return 32 + ((u + 1) * N) / 16; }
+};
+
+// Load the lane's aligned 32-bit words A[0..AW) for tile `words` (u32 view) and chunk j (0..7).  A[i] holds stream
+// bits [2jn - 32 + 32i, +32) of the circular tile stream.
+template <int N>
+__device__ __forceinline__ void load_lane_words(const uint32_t *__restrict__ words, int j, uint32_t (&A)[LaneBits<N>::AW]) {
+    constexpr int NW = LaneBits<N>::NW;
+    constexpr int AW = LaneBits<N>::AW;
+    if constexpr (LaneBits<N>::ALIGNED) {
+        const int w0 = j * (N / 16);  // first word of the lane's own chunk
+        A[0] = words[(w0 + NW - 1) % NW];
+#pragma unroll
+        for (int i = 1; i < AW; i++) A[i] = words[w0 + i - 1];
+    } else {
+        const int base = 2 * j * N - 32 + 32 * NW;  // offset by one lap to stay non-negative
+        const int wb = base >> 5;
+        const int s = base & 31;
+        uint32_t R[AW + 1];
+#pragma unroll
+        for (int i = 0; i < AW + 1; i++) R[i] = words[(wb + i) % NW];
+#pragma unroll
+        for (int i = 0; i < AW; i++) {
+            uint64_t two = ((uint64_t)R[i] << 32) | R[i + 1];
+            A[i] = (uint32_t)(two >> (32 - s));
+        }
+    }
+}
+
+// Codeword u (0..31) of the lane from its aligned words (low 16 bits valid).
+template <int N>
+__device__ __forceinline__ uint32_t lane_codeword(const uint32_t (&A)[LaneBits<N>::AW], int u) {
+    const int e = LaneBits<N>::end_of(u);  // exclusive end bit within A
+    const int a = (e - 1) >> 5;            // word holding the last bit
+    const int sh = 32 * (a + 1) - e;       // bits of word a after the window
+    if (a == 0) return A[0] >> sh;
+    return __builtin_amdgcn_alignbit(A[a - 1], A[a], sh);
+}
+
+// Codeword t of a tile at a runtime rate n: the 16 stream bits ending at floor((t+1)n/16), circular
+// (the generic reader for rates without a specialised kernel).
+__device__ __forceinline__ uint32_t codeword_at(const uint32_t *__restrict__ words, int n, int t) {
+    const int nw = n >> 1;
+    const int total = 16 * n;
+    const int end = ((t + 1) * n) >> 4;
+    const int last = (end + total - 1) % total;
+    const int wl = last >> 5;
+    const int wp = (wl + nw - 1) % nw;
+    return __builtin_amdgcn_alignbit(words[wp], words[wl], 31 - (last & 31)) & 0xFFFFu;
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Wave64 128-point Walsh-Hadamard: lane l holds v0 = x[l], v1 = x[l + 64].  Unnormalised (the caller scales by
+// 1/sqrt(128)).  Matches hadamard128 (expert_exl3.zig:400-414) up to f32 summation order.
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+__device__ __forceinline__ void fwht128_wave(float &v0, float &v1, int lane) {
+    {
+        float a = v0, b = v1;
+        v0 = a + b;
+        v1 = a - b;
+    }
+#pragma unroll
+    for (int h = 32; h >= 1; h >>= 1) {
+        float p0 = shfl_xor_f(v0, h), p1 = shfl_xor_f(v1, h);
+        bool up = (lane & h) != 0;
+        v0 = up ? (p0 - v0) : (v0 + p0);
+        v1 = up ? (p1 - v1) : (v1 + p1);
+    }
+}
+
+constexpr float HAD_SCALE = 0.08838834764831845f;
+
+// ------------------------------------------------------------------------------------------------------------
+// Activation dtypes at the boundary.
+enum DType : int { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+
+template <int DT>
+__device__ __forceinline__ float load_act(const void *p, size_t i) {
+    if constexpr (DT == DT_F16) return __half2float(reinterpret_cast<const __half *>(p)[i]);
+    else if constexpr (DT == DT_BF16) return __bfloat162float(reinterpret_cast<const __hip_bfloat16 *>(p)[i]);
+    else return reinterpret_cast<const float *>(p)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void store_act(void *p, size_t i, float v) {
+    if constexpr (DT == DT_F16) reinterpret_cast<__half *>(p)[i] = __float2half_rn(v);
+    else if constexpr (DT == DT_BF16) reinterpret_cast<__hip_bfloat16 *>(p)[i] = __float2bfloat16(v);
+    else reinterpret_cast<float *>(p)[i] = v;
+}
+
+__device__ __forceinline__ float f16r(float v) { return __half2float(__float2half_rn(v)); }
+
+__device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
+
+}  // namespace exl3

@@ -1,0 +1,96 @@
+// Trellis decode kernels: a codeword list (the exhaustive 65,536-codeword check) and the dense reconstruction
+// of one projection's inner matrix ("dequantized fp16 weights", bit-exact with reconstructInner,
+// beamivalice/sushi src/exl3/expert_exl3.zig:416-438).
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+template <int FAM>
+__global__ void decode_codewords_kernel(const uint16_t *__restrict__ cw, int64_t count, DecodeK k,
+                                        uint16_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t c = cw[i];
+    if constexpr (FAM == FAM_PAIR) {
+        uint32_t h = decode_pair_unscaled(c, k);
+        __half w0 = __hmul(__ushort_as_half((unsigned short)(h & 0xFFFFu)), __float2half(4096.0f));
+        __half w1 = __hmul(__ushort_as_half((unsigned short)(h >> 16)), __float2half(4096.0f));
+        out[2 * i] = __half_as_ushort(w0);
+        out[2 * i + 1] = __half_as_ushort(w1);
+    } else {
+        __half w = decode1<FAM>(c, k);
+        if constexpr (family_scaled<FAM>()) w = __hmul(w, __float2half(4096.0f));
+        out[i] = __half_as_ushort(w);
+    }
+}
+
+// One thread per weight pair (t, t+1), t even; 128 threads per tile.  grid.x = tiles.
+template <int FAM>
+__global__ void reconstruct_inner_kernel(const uint16_t *__restrict__ trellis, int it, int ot, int n, DecodeK k,
+                                         uint16_t *__restrict__ out) {
+    const int tile = blockIdx.x;
+    const int tk = tile / ot, tn = tile % ot;
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(trellis + (size_t)tile * n);
+    const int p = threadIdx.x;  // pair index 0..127
+    const int t = 2 * p;
+    const uint32_t c0 = codeword_at(words, n, t);
+    const uint32_t c1 = codeword_at(words, n, t + 1);
+    uint32_t h = decode_pair_h2<FAM>(c0, c1, k);
+    __half w0 = __ushort_as_half((unsigned short)(h & 0xFFFFu));
+    __half w1 = __ushort_as_half((unsigned short)(h >> 16));
+    if constexpr (family_scaled<FAM>()) {
+        w0 = __hmul(w0, __float2half(4096.0f));
+        w1 = __hmul(w1, __float2half(4096.0f));
+    }
+    // tensorCorePerm: t = 8T + i, T = 4j + q; rows {2q, 2q+1, 2q+8, 2q+9}[i%4], col j + 8*(i>=4).
+    const int T = t >> 3, i = t & 7, q = T & 3, j = T >> 2;
+    const int row = 2 * q + ((i & 2) ? 8 : 0) + (i & 1);
+    const int col = j + ((i & 4) ? 8 : 0);
+    const size_t of = (size_t)ot * 16;
+    const size_t base = ((size_t)tk * 16 + row) * of + (size_t)tn * 16 + col;
+    out[base] = __half_as_ushort(w0);
+    out[base + of] = __half_as_ushort(w1);  // weight t+1 is the next row (i odd), same column
+}
+
+template <int FAM>
+static hipError_t launch_decode_codewords(const uint16_t *cw, int64_t count, const DecodeK &k, uint16_t *out,
+                                          hipStream_t s) {
+    const int bs = 256;
+    const int64_t grid = (count + bs - 1) / bs;
+    hipLaunchKernelGGL(decode_codewords_kernel<FAM>, dim3((unsigned)grid), dim3(bs), 0, s, cw, count, k, out);
+    return hipGetLastError();
+}
+
+hipError_t run_decode_codewords(int fam, const uint16_t *cw, int64_t count, const DecodeK &k, uint16_t *out,
+                                hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    switch (fam) {
+    case FAM_MCG: return launch_decode_codewords<FAM_MCG>(cw, count, k, out, s);
+    case FAM_MUL1: return launch_decode_codewords<FAM_MUL1>(cw, count, k, out, s);
+    case FAM_HASH: return launch_decode_codewords<FAM_HASH>(cw, count, k, out, s);
+    case FAM_PAIR: return launch_decode_codewords<FAM_PAIR>(cw, count, k, out, s);
+    default: return launch_decode_codewords<FAM_3INST>(cw, count, k, out, s);
+    }
+}
+
+template <int FAM>
+static hipError_t launch_reconstruct(const uint16_t *trellis, int it, int ot, int n, const DecodeK &k, uint16_t *out,
+                                     hipStream_t s) {
+    hipLaunchKernelGGL(reconstruct_inner_kernel<FAM>, dim3((unsigned)(it * ot)), dim3(128), 0, s, trellis, it, ot, n,
+                       k, out);
+    return hipGetLastError();
+}
+
+hipError_t run_reconstruct_inner(int fam, const uint16_t *trellis, int it, int ot, int n, const DecodeK &k,
+                                 uint16_t *out, hipStream_t s) {
+    if (it * ot == 0) return hipSuccess;
+    switch (fam) {
+    case FAM_MCG: return launch_reconstruct<FAM_MCG>(trellis, it, ot, n, k, out, s);
+    case FAM_MUL1: return launch_reconstruct<FAM_MUL1>(trellis, it, ot, n, k, out, s);
+    case FAM_HASH: return launch_reconstruct<FAM_HASH>(trellis, it, ot, n, k, out, s);
+    case FAM_PAIR: return launch_reconstruct<FAM_PAIR>(trellis, it, ot, n, k, out, s);
+    default: return launch_reconstruct<FAM_3INST>(trellis, it, ot, n, k, out, s);
+    }
+}
+
+}  // namespace exl3

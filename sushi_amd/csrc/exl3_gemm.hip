@@ -1,0 +1,253 @@
+// Dense trellis GEMM for wide row counts (the prefill arm of linear.linear: prepareIndexed +
+// innerGemmSortedTable + finishIndexedAs, beamivalice/sushi src/exl3/linear.zig:322-335 and
+// src/exl3/expert_exl3_kernels.zig:1341-1620).
+//
+// MI355X layout.  A workgroup of 2 waves owns a 128-row x 128-column output tile (one Hadamard block wide, so
+// the output FWHT + svh finish runs in its epilogue) over the whole k range, in k-steps of 32 (two trellis
+// k-tiles).  The prepared input rows are staged through LDS; each wave owns 64 output columns (4 trellis tiles)
+// and decodes its weights straight into v_mfma_f32_16x16x32_f16 B fragments: lane l = 16h + c needs column c of a
+// 16-column block at k = 8h..8h+7, which is the codeword set {8q + 2p + e} (q = 0..3, e = 0..1) of chunk j = c % 8
+// with p = 2*(c / 8) + h % 2 (tensorCorePerm), i.e. eight codewords from one 2n-bit run of the tile stream.
+// Integer rates (n = 16K) use this reader; other rates are first decoded to a transposed f16 copy in workspace.
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t scale_h2_4096(uint32_t v) {
+    __half2 h = __builtin_bit_cast(__half2, v);
+    h = __hmul2(h, __half2(__float2half(4096.0f), __float2half(4096.0f)));
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+constexpr int GM_WAVES = 2;
+constexpr int GM_THREADS = 64 * GM_WAVES;
+constexpr int GM_MT = 128;    // rows per workgroup
+constexpr int GM_XP = 40;     // LDS pitch (halves) of a staged x row: 32 + 8 pad
+
+// ---- prepare: xp[g][r][:] = f16(H128(f16(x) * suh) / sqrt(128))  (prepareIndexed / PREPARE_SOURCE :852-885)
+__global__ __launch_bounds__(64) void gemm_prepare_kernel(GemmArgs a) {
+    const int b = blockIdx.x, r = blockIdx.y, g = blockIdx.z, lane = threadIdx.x;
+    const size_t xi = ((size_t)g * a.rows + r) * a.in + (size_t)b * 128;
+    const size_t si = (size_t)g * a.in + (size_t)b * 128;
+    float v0, v1;
+    if (a.x_dtype == DT_F16) {
+        v0 = load_act<DT_F16>(a.x, xi + lane);
+        v1 = load_act<DT_F16>(a.x, xi + lane + 64);
+    } else if (a.x_dtype == DT_BF16) {
+        v0 = f16r(load_act<DT_BF16>(a.x, xi + lane));
+        v1 = f16r(load_act<DT_BF16>(a.x, xi + lane + 64));
+    } else {
+        v0 = f16r(load_act<DT_F32>(a.x, xi + lane));
+        v1 = f16r(load_act<DT_F32>(a.x, xi + lane + 64));
+    }
+    v0 *= h2f(a.suh[si + lane]);
+    v1 *= h2f(a.suh[si + lane + 64]);
+    fwht128_wave(v0, v1, lane);
+    a.xp[xi + lane] = __half_as_ushort(__float2half_rn(v0 * HAD_SCALE));
+    a.xp[xi + lane + 64] = __half_as_ushort(__float2half_rn(v1 * HAD_SCALE));
+}
+
+// ---- dense fallback: tiles decoded to wt[g][out][in] f16 (transposed, so a B fragment is 16 contiguous bytes)
+template <int FAM>
+__global__ void gemm_decode_transposed_kernel(GemmArgs a, uint16_t *__restrict__ wt) {
+    const int IT = a.in >> 4, OT = a.out >> 4;
+    const int tile = blockIdx.x, g = blockIdx.y;
+    const int tk = tile / OT, tn = tile % OT;
+    const uint32_t *words =
+        reinterpret_cast<const uint32_t *>(a.trellis + ((size_t)g * IT * OT + (size_t)tile) * a.n);
+    const int t = 2 * threadIdx.x;
+    uint32_t h = decode_pair_h2<FAM>(codeword_at(words, a.n, t), codeword_at(words, a.n, t + 1), a.k);
+    const int T = t >> 3, i = t & 7, q = T & 3, j = T >> 2;
+    const int row = 2 * q + ((i & 2) ? 8 : 0);
+    const int col = j + ((i & 4) ? 8 : 0);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(wt + ((size_t)g * a.out + (size_t)tn * 16 + col) * a.in +
+                                                 (size_t)tk * 16 + row);
+    *dst = h;  // rows (row, row+1) of one column are adjacent in the transposed copy
+}
+
+template <int FAM, int N>
+__global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint16_t *__restrict__ wt) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int IT = a.in >> 4, OT = a.out >> 4;
+    const int og = blockIdx.x, mb = blockIdx.y, g = blockIdx.z;
+    const int m0 = mb * GM_MT;
+
+    __shared__ __align__(16) uint16_t xs[GM_MT * GM_XP];
+    __shared__ float outs[32][129];
+
+    const int c = lane & 15, h = lane >> 4;
+    const int kt_off = h >> 1, half = h & 1, j = c & 7, p = 2 * (c >> 3) + half;
+    const DecodeK k = a.k;
+    const uint16_t *tb = a.trellis + (size_t)g * IT * OT * a.n;
+
+    f4_t acc[8][4];
+#pragma unroll
+    for (int rb = 0; rb < 8; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Per-lane bit base of its eight codewords inside a tile: codeword (q, e) ends 32 + (e+1)K + q*n/2 bits past it.
+    constexpr int K = N ? N / 16 : 1;
+    constexpr int NW = N ? N / 2 : 1;
+    constexpr int AW = N ? (32 + 2 * K + 3 * (N / 2) + 16 + 31) / 32 + 1 : 1;  // words covering the span, +1 to funnel
+    const int span = 16 * (N ? N : 16);
+    const int base = ((2 * j * (N ? N : 16) - 32 + 2 * p * K) % span + span) % span;
+    const int wb = base >> 5, sb = base & 31;
+
+    const int nks = IT / 2;
+    for (int ks = 0; ks < nks; ks++) {
+        // stage 128 rows x 32 k of the prepared input
+        __syncthreads();
+        {
+            const int row = tid;  // GM_THREADS == GM_MT
+            const int m = m0 + row;
+            uint4 v0 = {0, 0, 0, 0}, v1 = v0, v2 = v0, v3 = v0;
+            if (m < a.rows) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(a.xp + ((size_t)g * a.rows + m) * a.in + ks * 32);
+                v0 = src[0];
+                v1 = src[1];
+                v2 = src[2];
+                v3 = src[3];
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(&xs[row * GM_XP]);
+            dst[0] = v0;
+            dst[1] = v1;
+            dst[2] = v2;
+            dst[3] = v3;
+        }
+        // B fragments for this wave's 4 column blocks
+        uint32_t B[4][4];
+        const int tk = 2 * ks + kt_off;
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) {
+            const int o = og * 8 + wave * 4 + cb;
+            if constexpr (N != 0) {
+                const uint32_t *words = reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * OT + o) * N);
+                uint32_t R[AW];
+#pragma unroll
+                for (int i = 0; i < AW; i++) R[i] = words[(wb + i) % NW];
+                uint32_t A[AW - 1];
+#pragma unroll
+                for (int i = 0; i < AW - 1; i++) A[i] = sb ? __builtin_amdgcn_alignbit(R[i], R[i + 1], 32 - sb) : R[i];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint32_t cw[2];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int end = 32 + (e + 1) * K + q * (N / 2);
+                        const int aw = (end - 1) >> 5;
+                        const int sh = 32 * (aw + 1) - end;
+                        cw[e] = aw == 0 ? (A[0] >> sh) : __builtin_amdgcn_alignbit(A[aw - 1], A[aw], sh);
+                    }
+                    B[cb][q] = decode_pair_h2<FAM>(cw[0], cw[1], k);
+                }
+                if constexpr (family_scaled<FAM>()) {  // MFMA takes the weight itself: fold the 2^12 back in (exact)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) B[cb][q] = scale_h2_4096(B[cb][q]);
+                }
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4 *>(
+                    wt + ((size_t)g * a.out + (size_t)o * 16 + c) * a.in + (size_t)tk * 16 + 8 * half);
+                B[cb][0] = v.x;
+                B[cb][1] = v.y;
+                B[cb][2] = v.z;
+                B[cb][3] = v.w;
+                if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) B[cb][q] = scale_h2_4096(B[cb][q]);
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rb = 0; rb < 8; rb++) {
+            const uint4 av = *reinterpret_cast<const uint4 *>(&xs[(rb * 16 + c) * GM_XP + 8 * h]);
+            const h8_t A8 = __builtin_bit_cast(h8_t, av);
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const uint4 bv = {B[cb][0], B[cb][1], B[cb][2], B[cb][3]};
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A8, __builtin_bit_cast(h8_t, bv), acc[rb][cb], 0,
+                                                                     0, 0);
+            }
+        }
+    }
+
+    // ---- epilogue: 32-row chunks through LDS, then FWHT-128 + svh per row
+    const size_t sv = (size_t)g * a.out + (size_t)og * 128;
+#pragma unroll
+    for (int ch = 0; ch < 4; ch++) {
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 2; rr++) {
+            const int rb = ch * 2 + rr;
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) outs[rr * 16 + 4 * h + i][wave * 64 + cb * 16 + c] = acc[rb][cb][i];
+        }
+        __syncthreads();
+        for (int r = wave; r < 32; r += GM_WAVES) {
+            const int m = m0 + ch * 32 + r;
+            if (m >= a.rows) break;
+            float v0 = outs[r][lane], v1 = outs[r][lane + 64];
+            fwht128_wave(v0, v1, lane);
+            const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128;
+            const float y0 = v0 * HAD_SCALE * h2f(a.svh[sv + lane]);
+            const float y1 = v1 * HAD_SCALE * h2f(a.svh[sv + lane + 64]);
+            if (a.y_dtype == DT_F16) {
+                store_act<DT_F16>(a.y, yo + lane, y0);
+                store_act<DT_F16>(a.y, yo + lane + 64, y1);
+            } else if (a.y_dtype == DT_BF16) {
+                store_act<DT_BF16>(a.y, yo + lane, y0);
+                store_act<DT_BF16>(a.y, yo + lane + 64, y1);
+            } else {
+                store_act<DT_F32>(a.y, yo + lane, y0);
+                store_act<DT_F32>(a.y, yo + lane + 64, y1);
+            }
+        }
+    }
+}
+
+template <int FAM, int N>
+static hipError_t launch_gemm_n(const GemmArgs &a, const uint16_t *wt, hipStream_t s) {
+    dim3 grid((unsigned)(a.out / 128), (unsigned)((a.rows + GM_MT - 1) / GM_MT), (unsigned)a.groups);
+    hipLaunchKernelGGL((gemm_kernel<FAM, N>), grid, dim3(GM_THREADS), 0, s, a, wt);
+    return hipGetLastError();
+}
+
+template <int FAM>
+static hipError_t launch_gemm_fam(const GemmArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(gemm_prepare_kernel, dim3((unsigned)(a.in / 128), (unsigned)a.rows, (unsigned)a.groups),
+                       dim3(64), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (a.n) {
+    case 16: return launch_gemm_n<FAM, 16>(a, nullptr, s);
+    case 32: return launch_gemm_n<FAM, 32>(a, nullptr, s);
+    case 48: return launch_gemm_n<FAM, 48>(a, nullptr, s);
+    case 64: return launch_gemm_n<FAM, 64>(a, nullptr, s);
+    default: break;
+    }
+    // Any other rate: decode to a transposed f16 copy in workspace (held after xp), then the same MFMA body.
+    uint16_t *wt = a.wt;
+    hipLaunchKernelGGL(gemm_decode_transposed_kernel<FAM>,
+                       dim3((unsigned)((a.in / 16) * (a.out / 16)), (unsigned)a.groups), dim3(128), 0, s, a, wt);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_gemm_n<FAM, 0>(a, wt, s);
+}
+
+hipError_t run_gemm(int fam, const GemmArgs &a, hipStream_t s) {
+    switch (fam) {
+    case FAM_MCG: return launch_gemm_fam<FAM_MCG>(a, s);
+    case FAM_MUL1: return launch_gemm_fam<FAM_MUL1>(a, s);
+    case FAM_HASH: return launch_gemm_fam<FAM_HASH>(a, s);
+    case FAM_PAIR: return launch_gemm_fam<FAM_PAIR>(a, s);
+    default: return launch_gemm_fam<FAM_3INST>(a, s);
+    }
+}
+
+}  // namespace exl3

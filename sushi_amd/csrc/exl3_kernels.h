@@ -1,0 +1,108 @@
+// Internal launch interface between the C-ABI layer (exl3_capi.hip) and the kernel translation units.
+#pragma once
+
+#include "exl3_common.cuh"
+
+namespace exl3 {
+
+hipError_t run_decode_codewords(int fam, const uint16_t *cw, int64_t count, const DecodeK &k, uint16_t *out,
+                                hipStream_t s);
+hipError_t run_reconstruct_inner(int fam, const uint16_t *trellis, int it, int ot, int n, const DecodeK &k,
+                                 uint16_t *out, hipStream_t s);
+
+enum Prologue : int { PRO_X = 0, PRO_MID = 1 };
+
+// Trellis GEMV over `groups` independent (bank, x-block) pairs, 1..8 rows each.
+//  * dense linear: groups = 1 (or G for linearGrouped), bank_of = null, x_div = 1;
+//  * MoE pair GEMV: groups = slots, bank_of = expert id per slot, x_div = topk, two projections (gate, up) on
+//    grid.z, partial_only (f32 planes for the mid);
+//  * MoE down GEMV: PRO_MID prologue builds its input from the gate/up planes (sum splits, FWHT, svh, clamp,
+//    SwiGLU, * suh_down, FWHT, f16) and writes f32 planes for the reduce.
+struct GemvArgs {
+    const void *x;
+    int x_dtype;
+    int rows;
+    int in;
+    int out;
+    int x_div;
+    // PRO_MID inputs: gate/up planes [groups][mid_splits][in] f32 and the gate/up svh banks ([E][in])
+    const float *mid_part[2];
+    int mid_splits;
+    const uint16_t *mid_svh[2];
+    float clamp_limit;  // 0 = none
+    // banks, one per projection (grid.z)
+    const uint16_t *trellis[2];
+    const uint16_t *suh[2];
+    const uint16_t *svh[2];
+    int n;                   // uniform rate; 0 with `meta` = per-expert rates
+    const uint32_t *bank_of; // [groups] expert id, or null (bank = group)
+    const uint32_t *meta;    // ragged meta [E][8]: n at col pi, word offset at col 4 + pi
+    int meta_col[2];
+    int table;               // codebook table for per-rate rows (ragged hash / pair families)
+    int bank_limit;          // expert count: ids are clamped below it (memory safety on bad routing)
+    DecodeK k;
+    float out_scale;
+    float *partial[2];       // [groups][splits][rows][out] f32
+    uint32_t *counters;      // [groups][out/128], zero between calls
+    void *y;
+    int y_dtype;
+    int splits;
+    int groups;
+    int nproj;
+    int fused_finish;
+    int partial_only;
+};
+
+hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s);
+hipError_t run_gemv_fam_FAM_MCG(int prologue, const GemvArgs &a, hipStream_t s);
+hipError_t run_gemv_fam_FAM_MUL1(int prologue, const GemvArgs &a, hipStream_t s);
+hipError_t run_gemv_fam_FAM_HASH(int prologue, const GemvArgs &a, hipStream_t s);
+hipError_t run_gemv_fam_FAM_PAIR(int prologue, const GemvArgs &a, hipStream_t s);
+hipError_t run_gemv_fam_FAM_3INST(int prologue, const GemvArgs &a, hipStream_t s);
+int gemv_default_splits(int in, int out, int rows, int groups_times_proj);
+
+// MoE finish: y[row] = sum_k score * (FWHT(sum_s down_part) * svh_down[e]) (+ shared), REDUCE_SOURCE.
+struct ReduceArgs {
+    const float *part;  // [slots][splits][hidden]
+    int splits;
+    int hidden;
+    int topk;
+    int rows;
+    const uint32_t *slots;
+    int bank_limit;
+    const float *scores;
+    const uint16_t *svh;  // [E][hidden]
+    const void *shared;   // [rows][hidden] in y dtype, or null
+    void *y;
+    int y_dtype;
+    float out_scale;
+};
+hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s);
+
+// Dense GEMM arm (prefill, rows > 8): prepare x -> xp f16, decode tiles to MFMA fragments, finish in the epilogue.
+struct GemmArgs {
+    const void *x;
+    int x_dtype;
+    int rows;
+    int in;
+    int out;
+    const uint16_t *trellis;
+    int n;
+    const uint16_t *suh;
+    const uint16_t *svh;
+    DecodeK k;
+    uint16_t *xp;     // workspace [groups][rows][in] f16
+    uint16_t *wt;     // workspace [groups][out][in] f16 (rates without a direct reader)
+    void *y;
+    int y_dtype;
+    int groups;
+};
+hipError_t run_gemm(int fam, const GemmArgs &a, hipStream_t s);
+
+hipError_t run_route_topk(const float *logits, int rows, int experts, int k, uint32_t *inds, float *scores,
+                          hipStream_t s);
+hipError_t run_tile_major(const uint16_t *src, uint16_t *dst, int experts, int it, int ot, int n, int inverse,
+                          hipStream_t s);
+hipError_t run_fill_zero(void *p, size_t bytes, hipStream_t s);
+
+}  // namespace exl3

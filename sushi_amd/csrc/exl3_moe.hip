@@ -1,0 +1,222 @@
+// MoE chain tail, routing and layout kernels, plus the GEMV family dispatcher.
+//
+//  * moe_reduce_kernel: the decode chain's score-weighted reduce (REDUCE_SOURCE / REDUCE_SHARED_SOURCE,
+//    beamivalice/sushi src/exl3/expert_exl3_kernels.zig:2338-2406): per (row, 128-block), each routed slot's down
+//    plane is summed over its k splits, FWHT-128'd and scaled by svh, then weighted by its score; the routed sum is
+//    rounded to the output dtype before a shared expert is added, as the reference does.
+//  * route_topk_kernel: moeRoutingChainOn (src/moe_router.zig:22-62).
+//  * tile_major_kernel: layout.tileMajor / tileMajorInverse (src/exl3/layout.zig:139-158).
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s) {
+    switch (fam) {
+    case FAM_MCG: return run_gemv_fam_FAM_MCG(prologue, a, s);
+    case FAM_MUL1: return run_gemv_fam_FAM_MUL1(prologue, a, s);
+    case FAM_HASH: return run_gemv_fam_FAM_HASH(prologue, a, s);
+    case FAM_PAIR: return run_gemv_fam_FAM_PAIR(prologue, a, s);
+    default: return run_gemv_fam_FAM_3INST(prologue, a, s);
+    }
+}
+
+constexpr int GEMV_MAX_KSPAN = 2048;
+
+int gemv_default_splits(int in, int out, int rows, int groups_times_proj) {
+    // Enough workgroups to have every CU's loads in flight (256 CUs), splits on whole Hadamard blocks.
+    const int blocks = in / 128;
+    const long G = (long)(out / 128) * groups_times_proj;
+    const long target = 1024;
+    int best = 1;
+    bool found = false;
+    for (int s = 1; s <= blocks; s++) {
+        if (blocks % s) continue;
+        if ((in / s) > GEMV_MAX_KSPAN) continue;
+        best = s;
+        found = true;
+        if (G * s >= target) break;
+    }
+    (void)rows;
+    return found ? best : blocks;
+}
+
+__device__ __forceinline__ void store_out(void *y, int dt, size_t i, float v) {
+    if (dt == DT_F16) store_act<DT_F16>(y, i, v);
+    else if (dt == DT_BF16) store_act<DT_BF16>(y, i, v);
+    else store_act<DT_F32>(y, i, v);
+}
+
+__device__ __forceinline__ float round_to(int dt, float v) {
+    if (dt == DT_F16) return __half2float(__float2half_rn(v));
+    if (dt == DT_BF16) return __bfloat162float(__float2bfloat16(v));
+    return v;
+}
+
+__global__ __launch_bounds__(64) void moe_reduce_kernel(ReduceArgs a) {
+    const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+    const size_t base = (size_t)blk * 128;
+    float y0 = 0.f, y1 = 0.f;
+    for (int kk = 0; kk < a.topk; kk++) {
+        const int slot = row * a.topk + kk;
+        const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
+        float v0 = 0.f, v1 = 0.f;
+        for (int s = 0; s < a.splits; s++) {
+            const float *pp = a.part + ((size_t)slot * a.splits + s) * a.hidden + base;
+            v0 += pp[lane];
+            v1 += pp[lane + 64];
+        }
+        fwht128_wave(v0, v1, lane);
+        const float sc = a.scores[slot];
+        const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
+        y0 += (v0 * HAD_SCALE * h2f(sv[lane])) * sc;
+        y1 += (v1 * HAD_SCALE * h2f(sv[lane + 64])) * sc;
+    }
+    const size_t yo = (size_t)row * a.hidden + base;
+    if (a.shared) {
+        float s0, s1;
+        if (a.y_dtype == DT_F16) {
+            s0 = load_act<DT_F16>(a.shared, yo + lane);
+            s1 = load_act<DT_F16>(a.shared, yo + lane + 64);
+        } else if (a.y_dtype == DT_BF16) {
+            s0 = load_act<DT_BF16>(a.shared, yo + lane);
+            s1 = load_act<DT_BF16>(a.shared, yo + lane + 64);
+        } else {
+            s0 = load_act<DT_F32>(a.shared, yo + lane);
+            s1 = load_act<DT_F32>(a.shared, yo + lane + 64);
+        }
+        y0 = round_to(a.y_dtype, y0) + s0;
+        y1 = round_to(a.y_dtype, y1) + s1;
+    }
+    store_out(a.y, a.y_dtype, yo + lane, y0);
+    store_out(a.y, a.y_dtype, yo + lane + 64, y1);
+}
+
+hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(moe_reduce_kernel, dim3((unsigned)(a.hidden / 128), (unsigned)a.rows), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+// One workgroup (256 threads) per row: k rounds of a block-wide argmax (ties to the lower index), then the softmax
+// mass of the picks over the full row, renormalised.
+__global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict__ logits, int experts, int k,
+                                                         uint32_t *__restrict__ inds, float *__restrict__ scores) {
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *l = logits + (size_t)row * experts;
+    __shared__ float vals[1024];
+    __shared__ float wv[4];
+    __shared__ int wi[4];
+    __shared__ int picked[32];
+    __shared__ float red[4];
+    float mx = -INFINITY;
+    for (int e = tid; e < experts; e += 256) {
+        vals[e] = l[e];
+        mx = fmaxf(mx, vals[e]);
+    }
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float den = 0.f;
+    for (int e = tid; e < experts; e += 256) den += __expf(vals[e] - mx);
+    for (int m = 32; m >= 1; m >>= 1) den += __shfl_xor(den, m, 64);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = den;
+    __syncthreads();
+    den = red[0] + red[1] + red[2] + red[3];
+    for (int j = 0; j < k; j++) {
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+        for (int e = tid; e < experts; e += 256) {
+            const float v = vals[e];
+            if (v > bv || (v == bv && e < bi)) {
+                bv = v;
+                bi = e;
+            }
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = __shfl_xor(bv, m, 64);
+            const int oi = __shfl_xor(bi, m, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((tid & 63) == 0) {
+            wv[tid >> 6] = bv;
+            wi[tid >> 6] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float b = wv[0];
+            int i = wi[0];
+            for (int w = 1; w < 4; w++)
+                if (wv[w] > b || (wv[w] == b && wi[w] < i)) {
+                    b = wv[w];
+                    i = wi[w];
+                }
+            picked[j] = i;
+            vals[i] = -INFINITY;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        float p[32];
+        float sum = 0.f;
+        for (int j = 0; j < k; j++) {
+            p[j] = __expf(l[picked[j]] - mx) / den;
+            sum += p[j];
+        }
+        for (int j = 0; j < k; j++) {
+            inds[(size_t)row * k + j] = (uint32_t)picked[j];
+            scores[(size_t)row * k + j] = p[j] / sum;
+        }
+    }
+}
+
+hipError_t run_route_topk(const float *logits, int rows, int experts, int k, uint32_t *inds, float *scores,
+                          hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, experts, k, inds, scores);
+    return hipGetLastError();
+}
+
+// One workgroup per (expert, tile) of the source; n halfwords copied by the first n threads.
+__global__ void tile_major_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst, int it, int ot, int n,
+                                  int inverse) {
+    const int e = blockIdx.y;
+    const int t = blockIdx.x;  // index in the pack order: tk * ot + tn
+    const int tk = t / ot, tn = t % ot;
+    const int pair = tn >> 1, o = tn & 1;
+    const size_t pack = ((size_t)tk * ot + tn) * n;
+    const size_t pm = (((size_t)pair * it + tk) * 2 + o) * n;
+    const size_t eb = (size_t)e * it * ot * n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        if (!inverse) dst[eb + pm + i] = src[eb + pack + i];
+        else dst[eb + pack + i] = src[eb + pm + i];
+    }
+}
+
+hipError_t run_tile_major(const uint16_t *src, uint16_t *dst, int experts, int it, int ot, int n, int inverse,
+                          hipStream_t s) {
+    if (experts == 0 || it * ot == 0) return hipSuccess;
+    hipLaunchKernelGGL(tile_major_kernel, dim3((unsigned)(it * ot), (unsigned)experts), dim3(64), 0, s, src, dst, it,
+                       ot, n, inverse);
+    return hipGetLastError();
+}
+
+__global__ void fill_zero_kernel(uint32_t *__restrict__ p, size_t words) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+hipError_t run_fill_zero(void *p, size_t bytes, hipStream_t s) {
+    const size_t words = bytes / 4;
+    if (words == 0) return hipSuccess;
+    size_t blocks = (words + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, reinterpret_cast<uint32_t *>(p),
+                       words);
+    return hipGetLastError();
+}
+
+}  // namespace exl3

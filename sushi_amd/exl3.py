@@ -1,0 +1,550 @@
+"""Host-side mirror of beamivalice/sushi's ``sushi_exl3`` operator API for the EXL3/STQ trellis hot path, on MI355X.
+
+Names, argument meaning and error behaviour follow the reference:
+
+* formats: ``Codebook``/``Window``/``Decode``/``Rate`` (src/exl3/expert_exl3.zig:54-226), ``Proj``/``Bank``
+  (src/exl3/root.zig:28-39), ``Ragged`` (src/exl3/rate_groups.zig:22-140);
+* dense: ``linear``/``linear_grouped`` (src/exl3/linear.zig:27-53), ``reconstruct_inner`` (expert_exl3.zig:416);
+* routed experts: ``moe``/``moe_with_shared``/``moe_clamped``/``moe_ragged`` (src/exl3/root.zig:51-124, :582-644);
+* routing: ``moe_routing_chain`` (src/moe_router.zig:16-62); layout: ``tile_major`` (src/exl3/layout.zig:139-158).
+
+Every call runs the HIP library through its C ABI on the caller's current torch stream; nothing falls back to the
+CPU.  Refusals raise the reference's named errors before any launch.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+# ---------------------------------------------------------------------------------------------------------------
+# Errors (src/exl3/root.zig:104-133, :421-423; src/exl3/expert_exl3_kernels.zig:2569, :1475)
+
+
+class Exl3Error(RuntimeError):
+    status = None
+
+
+class BadExl3Shape(Exl3Error):
+    status = -1
+
+
+class BadExl3Dtype(Exl3Error):
+    status = -2
+
+
+class Exl3CodebookTableUnknown(Exl3Error):
+    status = -3
+
+
+class Exl3TopKExceedsReduceBank(Exl3Error):
+    status = -4
+
+
+class Exl3TopkUnsupported(Exl3Error):
+    status = -5
+
+
+class InvalidExl3Clamp(Exl3Error):
+    status = -6
+
+
+class Exl3SharedNeedsDecodeRows(Exl3Error):
+    status = -7
+
+
+class Exl3LaunchFailed(Exl3Error):
+    status = -8
+
+
+class Exl3WorkspaceTooSmall(Exl3Error):
+    status = -9
+
+
+class Exl3CodebookTableRateMissing(Exl3Error):
+    status = -10
+
+
+class Exl3WindowUnsupported(Exl3Error):
+    status = -11
+
+
+_BY_STATUS = {c.status: c for c in Exl3Error.__subclasses__()}
+
+
+def _check(rc: int) -> None:
+    if rc == 0:
+        return
+    raise _BY_STATUS.get(rc, Exl3Error)(f"[exl3 status {rc}] {_lib.last_error()}")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Format types
+
+
+class Codebook(enum.IntEnum):
+    """`Codebook` (expert_exl3.zig:54-61) plus ``inst3``, QTIP's 3INST LCG codebook (an extension)."""
+
+    mul1 = 0
+    mcg = 1
+    spec1 = 2
+    pair1 = 3
+    std1 = 4
+    inst3 = 5
+
+    @classmethod
+    def from_name(cls, name: str) -> Optional["Codebook"]:
+        return {"mcg": cls.mcg, "mul1": cls.mul1, "std1": cls.std1, "spec1": cls.spec1, "pair1": cls.pair1,
+                "3inst": cls.inst3}.get(name)
+
+    def tabled_hash_mask(self) -> bool:
+        return self in (Codebook.spec1, Codebook.std1)
+
+    def has_table(self) -> bool:
+        return self.tabled_hash_mask() or self == Codebook.pair1
+
+
+class Table(enum.IntEnum):
+    """The shipped codebook tables, in codebook_tables.zig `shipped` order (:101-106)."""
+
+    pair1_w16_v1 = 0
+    spec1_w15 = 1
+    spec1_w16 = 2
+    std1 = 3
+
+
+TABLE_NAMES = {"pair1-w16-v1": Table.pair1_w16_v1, "spec1-w15": Table.spec1_w15, "spec1-w16": Table.spec1_w16,
+               "std1": Table.std1}
+
+
+@dataclass(frozen=True)
+class Window:
+    """The codeword width a pack's search hashed (`Window`, expert_exl3.zig:102-137)."""
+
+    bits: int = 16
+
+    MIN_BITS = 8
+
+    @classmethod
+    def from_bits(cls, w: int) -> Optional["Window"]:
+        return cls(w) if cls.MIN_BITS <= w <= 16 else None
+
+    def mask(self) -> int:
+        return (1 << self.bits) - 1
+
+
+@dataclass(frozen=True)
+class Decode:
+    """How a pack's trellis decodes (`Decode`, expert_exl3.zig:141-174)."""
+
+    codebook: Codebook
+    window: Window = field(default_factory=Window)
+    table: Optional[int] = None
+
+    @classmethod
+    def tabled(cls, codebook: Codebook, window: Window = Window()) -> "Decode":
+        table = {Codebook.spec1: Table.spec1_w15, Codebook.std1: Table.std1}.get(codebook)
+        return cls(codebook, window, table)
+
+    def require_table(self) -> None:
+        if self.codebook.tabled_hash_mask() and self.table is None:
+            raise Exl3CodebookTableUnknown(f"{self.codebook.name} decode needs a codebook table")
+
+    def c(self) -> _lib.DecodeT:
+        return _lib.DecodeT(int(self.codebook), int(self.window.bits), -1 if self.table is None else int(self.table))
+
+
+MUL1 = Decode(Codebook.mul1)
+MCG = Decode(Codebook.mcg)
+INST3 = Decode(Codebook.inst3)
+
+
+@dataclass(frozen=True)
+class Rate:
+    """K = n/16 bits per weight (`Rate`, expert_exl3.zig:180-226)."""
+
+    n: int
+
+    MIN_N = 16
+    MAX_N = 128
+
+    @classmethod
+    def from_k(cls, k: int) -> "Rate":
+        return cls(16 * k)
+
+    def bit_end(self, t: int) -> int:
+        return ((t + 1) * self.n) >> 4
+
+    def fresh_bits(self, t: int) -> int:
+        return self.bit_end(t) - (0 if t == 0 else self.bit_end(t - 1))
+
+    def words(self) -> int:
+        return self.n // 2
+
+    def total_bits(self) -> int:
+        return 16 * self.n
+
+    def is_integer(self) -> bool:
+        return self.n % 16 == 0
+
+
+def k_from_packed_dim(packed_hw: int) -> Optional[Rate]:
+    """`kFromPackedDim` (expert_exl3.zig:241-245): even n in 16..128."""
+    if packed_hw % 2 != 0 or packed_hw < Rate.MIN_N or packed_hw > Rate.MAX_N:
+        return None
+    return Rate(packed_hw)
+
+
+@dataclass
+class Proj:
+    """One projection's bank: trellis u16 [E, in/16, out/16, n], suh f16 [E, in], svh f16 [E, out]."""
+
+    trellis: torch.Tensor
+    suh: torch.Tensor
+    svh: torch.Tensor
+
+    @property
+    def n(self) -> int:
+        return int(self.trellis.shape[-1])
+
+    @property
+    def experts(self) -> int:
+        return int(self.trellis.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.trellis.shape[1]) * 16
+
+    @property
+    def out_features(self) -> int:
+        return int(self.trellis.shape[2]) * 16
+
+    def c(self) -> _lib.ProjT:
+        return _lib.ProjT(self.trellis.data_ptr(), self.suh.data_ptr(), self.svh.data_ptr(), self.n)
+
+
+@dataclass
+class Bank:
+    gate: Proj
+    up: Proj
+    down: Proj
+
+
+META_WORDS = 8
+
+
+@dataclass
+class Ragged:
+    """A rate-grouped layer as one ragged trellis per projection (`Ragged`, rate_groups.zig:22-140).
+
+    ``meta`` [E, 8] u32 per expert: {n_gate, n_up, n_down, group, off_gate, off_up, off_down, local}, offsets in u32
+    words into the ragged trellis of that projection.
+    """
+
+    trellis: list
+    suh: list
+    svh: list
+    meta: torch.Tensor
+    experts: int
+    hidden: int
+    inter: int
+    rates: list
+
+    @classmethod
+    def init(cls, banks: Sequence[Bank]) -> "Ragged":
+        if not banks:
+            raise BadExl3Shape("no rate groups")
+        hidden = banks[0].gate.in_features
+        inter = banks[0].gate.out_features
+        meta, words = [], [0, 0, 0]
+        rates = []
+        for g, bank in enumerate(banks):
+            projs = (bank.gate, bank.up, bank.down)
+            e = bank.gate.experts
+            for pi, p in enumerate(projs):
+                want_in, want_out = (inter, hidden) if pi == 2 else (hidden, inter)
+                if p.experts != e or p.in_features != want_in or p.out_features != want_out:
+                    raise BadExl3Shape(f"group {g} projection {pi} shape {tuple(p.trellis.shape)}")
+                if k_from_packed_dim(p.n) is None:
+                    raise BadExl3Shape(f"group {g} projection {pi} rate n={p.n}")
+            rates.append(tuple(p.n for p in projs))
+            tiles = (hidden // 16) * (inter // 16)
+            for local in range(e):
+                row = [projs[0].n, projs[1].n, projs[2].n, g]
+                row += [words[pi] + local * tiles * projs[pi].n // 2 for pi in range(3)]
+                row.append(local)
+                meta.append(row)
+            for pi in range(3):
+                words[pi] += e * tiles * projs[pi].n // 2
+        dev = banks[0].gate.trellis.device
+        trellis = [torch.cat([getattr(b, nm).trellis.reshape(-1) for b in banks]) for nm in ("gate", "up", "down")]
+        suh = [torch.cat([getattr(b, nm).suh for b in banks]) for nm in ("gate", "up", "down")]
+        svh = [torch.cat([getattr(b, nm).svh for b in banks]) for nm in ("gate", "up", "down")]
+        if max(max(r) for r in meta[:]) >= 2 ** 32:
+            raise BadExl3Shape("ragged offsets overflow u32")
+        meta_t = torch.tensor(meta, dtype=torch.int64).to(torch.int32).to(dev)
+        return cls(trellis, suh, svh, meta_t, len(meta), hidden, inter, rates)
+
+    def c(self) -> _lib.RaggedT:
+        r = _lib.RaggedT()
+        for i in range(3):
+            r.trellis[i] = self.trellis[i].data_ptr()
+            r.suh[i] = self.suh[i].data_ptr()
+            r.svh[i] = self.svh[i].data_ptr()
+        r.meta = self.meta.data_ptr()
+        r.experts = self.experts
+        return r
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Plumbing
+
+_DT = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+_U16 = {torch.int16, getattr(torch, "uint16", torch.int16)}
+
+
+def _dt(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise BadExl3Dtype(f"{what} dtype {t.dtype} (f16, bf16 or f32)") from None
+
+
+def _need_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise BadExl3Shape("operands must be device tensors (the HIP path has no CPU fallback)")
+        if not t.is_contiguous():
+            raise BadExl3Shape("operands must be contiguous")
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+class _Workspace:
+    """Per-device scratch owned by this host layer (the C ABI itself never allocates)."""
+
+    def __init__(self) -> None:
+        self._buf: dict = {}
+
+    def get(self, dev: torch.device, nbytes: int) -> torch.Tensor:
+        key = (dev.type, dev.index)
+        buf = self._buf.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 1 << 20, 0 if buf is None else buf.numel() * 2)
+            buf = torch.empty(size, dtype=torch.uint8, device=dev)
+            _check(_lib.load().exl3_workspace_init(buf.data_ptr(), buf.numel(), _stream(dev)))
+            self._buf[key] = buf
+        return buf
+
+
+workspace = _Workspace()
+
+
+def _u16_check(t: torch.Tensor, what: str) -> None:
+    if t.element_size() != 2 or t.dtype.is_floating_point:
+        raise BadExl3Dtype(f"{what} must be a 16-bit integer tensor (u16 codes)")
+
+
+def _f16_check(t: torch.Tensor, what: str) -> None:
+    if t.dtype != torch.float16:
+        raise BadExl3Dtype(f"{what} must be float16")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Decode / dequant
+
+
+def decode_codewords(codewords: torch.Tensor, n: int, dec: Decode) -> torch.Tensor:
+    """f16 weights of a flat list of codewords (PAIR1: two per codeword) -- the exhaustive decode check."""
+    _need_gpu(codewords)
+    _u16_check(codewords, "codewords")
+    count = codewords.numel()
+    per = 2 if dec.codebook == Codebook.pair1 else 1
+    out = torch.empty(count * per, dtype=torch.float16, device=codewords.device)
+    _check(_lib.load().exl3_decode_codewords(codewords.data_ptr(), count, n, dec.c(), out.data_ptr(),
+                                             _stream(codewords.device)))
+    return out
+
+
+def reconstruct_inner(trellis: torch.Tensor, dec: Decode) -> torch.Tensor:
+    """`reconstructInner` (expert_exl3.zig:416-438): f16 [in, out] of a [in/16, out/16, n] (or [1, ...]) trellis."""
+    t = trellis.reshape(trellis.shape[-3:]) if trellis.dim() == 4 else trellis
+    _need_gpu(t)
+    _u16_check(t, "trellis")
+    it, ot, n = (int(v) for v in t.shape)
+    out = torch.empty(it * 16, ot * 16, dtype=torch.float16, device=t.device)
+    _check(_lib.load().exl3_reconstruct_inner(t.data_ptr(), it * 16, ot * 16, n, dec.c(), out.data_ptr(),
+                                              _stream(t.device)))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Dense linears
+
+
+def linear(x: torch.Tensor, p: Proj, dec: Decode, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """`linear.linear` (linear.zig:27-34): x [rows, in] through the one-bank projection -> [rows, out]."""
+    if x.dim() != 2 or p.trellis.dim() != 4 or p.trellis.shape[0] != 1 or p.in_features != x.shape[1]:
+        raise BadExl3Shape(f"linear: x {tuple(x.shape)} vs trellis {tuple(p.trellis.shape)}")
+    dec.require_table()
+    _need_gpu(x, p.trellis, p.suh, p.svh)
+    _u16_check(p.trellis, "trellis")
+    _f16_check(p.suh, "suh")
+    _f16_check(p.svh, "svh")
+    rows, in_f, out_f = int(x.shape[0]), p.in_features, p.out_features
+    y = torch.empty(rows, out_f, dtype=out_dtype or x.dtype, device=x.device)
+    L = _lib.load()
+    ws_bytes = L.exl3_linear_workspace_size(rows, in_f, out_f, p.n)
+    ws = workspace.get(x.device, ws_bytes)
+    _check(L.exl3_linear(x.data_ptr(), _dt(x, "x"), rows, in_f, out_f, p.trellis.data_ptr(), p.n, p.suh.data_ptr(),
+                         p.svh.data_ptr(), dec.c(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
+                         _stream(x.device)))
+    return y
+
+
+def linear_grouped(x: torch.Tensor, p: Proj, dec: Decode) -> torch.Tensor:
+    """`linear.linearGrouped` (linear.zig:37-53): x [G, rows, in] through the G-bank projection -> [G, rows, out]."""
+    if x.dim() != 3 or p.trellis.dim() != 4 or p.trellis.shape[0] != x.shape[0] or p.in_features != x.shape[2]:
+        raise BadExl3Shape(f"linear_grouped: x {tuple(x.shape)} vs trellis {tuple(p.trellis.shape)}")
+    dec.require_table()
+    _need_gpu(x, p.trellis, p.suh, p.svh)
+    groups, rows = int(x.shape[0]), int(x.shape[1])
+    in_f, out_f = p.in_features, p.out_features
+    y = torch.empty(groups, rows, out_f, dtype=x.dtype, device=x.device)
+    L = _lib.load()
+    ws_bytes = L.exl3_linear_grouped_workspace_size(groups, rows, in_f, out_f, p.n)
+    ws = workspace.get(x.device, ws_bytes)
+    _check(L.exl3_linear_grouped(x.data_ptr(), _dt(x, "x"), groups, rows, in_f, out_f, p.trellis.data_ptr(), p.n,
+                                 p.suh.data_ptr(), p.svh.data_ptr(), dec.c(), y.data_ptr(), _dt(y, "y"),
+                                 ws.data_ptr(), ws.numel(), _stream(x.device)))
+    return y
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Routed experts
+
+REDUCE_MAX_TOPK = 32
+DECODE_ROWS_MAX = 16
+
+
+def admit_top_k(topk: int) -> None:
+    """`admitTopK` (root.zig:421-423)."""
+    if topk > REDUCE_MAX_TOPK:
+        raise Exl3TopKExceedsReduceBank(f"top-k {topk} > {REDUCE_MAX_TOPK}")
+
+
+def _moe_prep(x: torch.Tensor, inds: torch.Tensor, scores: torch.Tensor):
+    if x.dim() < 2 or inds.shape[:-1] != x.shape[:-1] or tuple(scores.shape) != tuple(inds.shape):
+        raise BadExl3Shape(f"moe: x {tuple(x.shape)}, inds {tuple(inds.shape)}, scores {tuple(scores.shape)}")
+    if inds.dtype not in (torch.int32, getattr(torch, "uint32", torch.int32)):
+        raise BadExl3Dtype(f"moe: inds dtype {inds.dtype} (u32/i32)")
+    if scores.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise BadExl3Dtype(f"moe: scores dtype {scores.dtype}")
+    topk = int(inds.shape[-1])
+    admit_top_k(topk)
+    rows = x.numel() // x.shape[-1]
+    x2 = x.reshape(rows, x.shape[-1])
+    inds2 = inds.reshape(rows * topk).contiguous()
+    sc2 = scores.reshape(rows * topk).to(torch.float32).contiguous()
+    return x2, inds2, sc2, rows, topk
+
+
+def _moe(x: torch.Tensor, bank: Bank, inds: torch.Tensor, scores: torch.Tensor, dec: Decode, verify_rows: bool,
+         shared: Optional[torch.Tensor], limit: int) -> torch.Tensor:
+    dec.require_table()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    g, u, d = bank.gate, bank.up, bank.down
+    experts = g.experts
+    inter = g.out_features
+    for p, (pin, pout) in ((g, (hidden, inter)), (u, (hidden, inter)), (d, (inter, hidden))):
+        if p.experts != experts or p.in_features != pin or p.out_features != pout:
+            raise BadExl3Shape(f"moe: projection shape {tuple(p.trellis.shape)}")
+        _u16_check(p.trellis, "trellis")
+        _f16_check(p.suh, "suh")
+        _f16_check(p.svh, "svh")
+        _need_gpu(p.trellis, p.suh, p.svh)
+    _need_gpu(x2, inds2, sc2, shared)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    if shared is not None:
+        if shared.numel() != y.numel() or shared.dtype != y.dtype:
+            raise BadExl3Shape("moe: shared expert output must match the routed output's size and dtype")
+        shared = shared.reshape(rows, hidden).contiguous()
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, inter))
+    cb = _lib.BankT(g.c(), u.c(), d.c())
+    _check(L.exl3_moe(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, experts, ctypes.byref(cb), inds2.data_ptr(),
+                      sc2.data_ptr(), topk, dec.c(), int(verify_rows), int(limit),
+                      None if shared is None else shared.data_ptr(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
+                      ws.numel(), _stream(x.device)))
+    return y.reshape(x.shape)
+
+
+def moe(x, bank: Bank, inds, scores, dec: Decode, verify_rows: bool = False) -> torch.Tensor:
+    """`moe` (root.zig:51-53): routed SwiGLU experts over x [..., D] for top-k inds/scores [..., K]."""
+    return _moe(x, bank, inds, scores, dec, verify_rows, None, 0)
+
+
+def moe_with_shared(x, bank: Bank, inds, scores, dec: Decode, verify_rows: bool, shared) -> torch.Tensor:
+    """`moeWithShared` (root.zig:56-67): adds an already gated shared expert after the routed output's rounding."""
+    return _moe(x, bank, inds, scores, dec, verify_rows, shared, 0)
+
+
+def moe_clamped(x, bank: Bank, inds, scores, dec: Decode, limit: int, shared=None) -> torch.Tensor:
+    """`moeClamped` / `moeClampedWithShared` (root.zig:98-124): gate upper-clamped, up clamped to [-limit, limit]."""
+    if limit <= 0 or limit > 128:
+        raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128")
+    return _moe(x, bank, inds, scores, dec, False, shared, limit)
+
+
+def moe_ragged(x, rb: Ragged, inds, scores, dec: Decode, verify_rows: bool = False, shared=None,
+               limit: int = 0) -> torch.Tensor:
+    """`moeRagged` (root.zig:582-644): each expert decodes at its own rate group's rates."""
+    dec.require_table()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    if hidden != rb.hidden:
+        raise BadExl3Shape(f"moe_ragged: hidden {hidden} vs bank {rb.hidden}")
+    _need_gpu(x2, inds2, sc2, shared, rb.meta)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    if shared is not None:
+        shared = shared.reshape(rows, hidden).contiguous()
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, rb.inter))
+    cr = rb.c()
+    _check(L.exl3_moe_ragged(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr), inds2.data_ptr(),
+                             sc2.data_ptr(), topk, dec.c(), int(limit), None if shared is None else shared.data_ptr(),
+                             y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device)))
+    return y.reshape(x.shape)
+
+
+def moe_routing_chain(router_logits: torch.Tensor, k: int):
+    """`moeRoutingChain` (moe_router.zig:16-62): (inds [.., k] i32, norm_scores [.., k] f32)."""
+    lg = router_logits.to(torch.float32).contiguous()
+    _need_gpu(lg)
+    experts = int(lg.shape[-1])
+    rows = lg.numel() // experts
+    inds = torch.empty(*lg.shape[:-1], k, dtype=torch.int32, device=lg.device)
+    scores = torch.empty(*lg.shape[:-1], k, dtype=torch.float32, device=lg.device)
+    _check(_lib.load().exl3_route_topk(lg.data_ptr(), rows, experts, k, inds.data_ptr(), scores.data_ptr(),
+                                       _stream(lg.device)))
+    return inds, scores
+
+
+def tile_major(trellis: torch.Tensor, inverse: bool = False) -> torch.Tensor:
+    """`layout.tileMajor` (layout.zig:139-158) over [E, IT, OT, n]; ``inverse`` undoes it."""
+    _need_gpu(trellis)
+    e, it, ot, n = (int(v) for v in trellis.shape)
+    out = torch.empty_like(trellis)
+    _check(_lib.load().exl3_tile_major(trellis.data_ptr(), out.data_ptr(), e, it, ot, n, int(inverse),
+                                       _stream(trellis.device)))
+    return out

@@ -1,0 +1,103 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares; host-side refusals happen before any
+launch.  No compute call here needs a GPU."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+import sushi_amd._lib as L
+from sushi_amd import exl3
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(exl3_[a-z0-9_]+)\s*\(", src))
+    return names
+
+
+def test_header_declares_the_exports_the_binding_uses():
+    assert set(L.EXPORTS) == _declared()
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(L.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_host_side_refusals():
+    lib = L.load()
+    assert lib.exl3_abi_version() == 1
+    d = L.DecodeT(1, 16, -1)
+    # bad shape: in not a multiple of 128 -> refused before any launch (null pointers never touched)
+    assert lib.exl3_linear(None, 0, 1, 100, 128, None, 64, None, None, d, None, 0, None, 0, None) == -1
+    assert "multiples of 128" in L.last_error()
+    # unadmitted rate
+    assert lib.exl3_linear(None, 0, 1, 128, 128, None, 130, None, None, d, None, 0, None, 0, None) == -1
+    # a tabled codebook without its table: Exl3CodebookTableUnknown
+    assert lib.exl3_linear(None, 0, 1, 128, 128, None, 64, None, None, L.DecodeT(2, 15, -1), None, 0, None, 0,
+                           None) == -3
+    # STD1 has no row at n=16: Exl3CodebookTableRateMissing
+    assert lib.exl3_linear(None, 0, 1, 128, 128, None, 16, None, None, L.DecodeT(4, 15, 3), None, 0, None, 0,
+                           None) == -10
+    # bad window
+    assert lib.exl3_linear(None, 0, 1, 128, 128, None, 64, None, None, L.DecodeT(1, 7, -1), None, 0, None, 0,
+                           None) == -11
+    # dtype
+    assert lib.exl3_linear(None, 9, 1, 128, 128, None, 64, None, None, d, None, 0, None, 0, None) == -2
+    # rows == 0 is a no-op
+    assert lib.exl3_linear(None, 0, 0, 128, 128, None, 64, None, None, d, None, 0, None, 0, None) == 0
+    # workspace too small (rows=1 needs counters)
+    assert lib.exl3_linear(1, 0, 1, 128, 128, 1, 64, 1, 1, d, 1, 0, None, 0, None) == -9
+
+
+def test_moe_refusals():
+    lib = L.load()
+    d = L.DecodeT(1, 16, -1)
+    bank = L.BankT()
+    args = lambda topk, clamp: (None, 0, 1, 128, 128, 4, ctypes.byref(bank), None, None, topk, d, 0, clamp, None,
+                                None, 0, None, 0, None)
+    assert lib.exl3_moe(*args(33, 0)) == -4  # Exl3TopKExceedsReduceBank
+    assert lib.exl3_moe(*args(8, 129)) == -6  # InvalidExl3Clamp
+    assert lib.exl3_moe(*args(8, 0)) == -1  # projections missing
+    assert lib.exl3_route_topk(None, 1, 2000, 8, None, None, None) == -1
+
+
+def test_workspace_sizes_are_aligned_and_monotone():
+    lib = L.load()
+    a = lib.exl3_linear_workspace_size(1, 4096, 4096, 64)
+    b = lib.exl3_linear_workspace_size(8, 4096, 4096, 64)
+    c = lib.exl3_linear_workspace_size(64, 4096, 4096, 64)
+    assert a % 256 == 0 and b >= a and c > 0
+    assert lib.exl3_moe_workspace_size(1, 8, 2048, 768) > 0
+
+
+def test_python_mirror_refuses_by_name():
+    with pytest.raises(exl3.Exl3CodebookTableUnknown):
+        exl3.Decode(exl3.Codebook.spec1).require_table()
+    with pytest.raises(exl3.InvalidExl3Clamp):
+        exl3.moe_clamped(None, None, None, None, exl3.MCG, 0)
+    with pytest.raises(exl3.Exl3TopKExceedsReduceBank):
+        exl3.admit_top_k(33)
+    assert exl3.k_from_packed_dim(41) is None and exl3.k_from_packed_dim(40).n == 40
+    assert exl3.Rate(44).fresh_bits(1) == 3 and exl3.Rate(64).bit_end(255) == 1024
+    assert exl3.Decode.tabled(exl3.Codebook.std1).table == exl3.Table.std1
+
+
+def test_synth_is_deterministic_and_name_keyed():
+    from sushi_amd import synth
+
+    a = synth.codes(0, "w", (4, 8))
+    b = synth.codes(0, "w", (4, 8))
+    c = synth.codes(0, "v", (4, 8))
+    assert (a == b).all() and not (a == c).all()
+    s = synth.sign_scale(0, "s", (1000,)).float()
+    assert ((s.abs() >= 0.5) & (s.abs() <= 1.5)).all() and (s < 0).any() and (s > 0).any()
+    x = synth.normal(0, "x", (20000,)).float()
+    assert abs(float(x.mean())) < 0.05 and abs(float(x.std()) - 1) < 0.05

@@ -1,0 +1,155 @@
+"""GPU parity of the dense trellis linear (GEMV arm for 1..8 rows, MFMA GEMM arm above) against the oracle.
+
+Bar: max |y - y_ref| / max |y_ref| <= 2e-3 with fp16 inputs and fp32 accumulation, where
+y_ref is the oracle's `project` (src/exl3/expert_exl3.zig:546-566).  The oracle rounds its inner sum to f16 and the
+GPU keeps it in f32, so the two differ by about one f16 ulp of the result; the bar leaves ample room.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from sushi_amd import exl3, synth
+from tests._util import max_abs_rel
+
+pytestmark = pytest.mark.gpu
+
+BAR = 2e-3
+
+DECODES = {
+    "mcg": (exl3.Decode(exl3.Codebook.mcg), O.decode(O.CB_MCG)),
+    "mul1": (exl3.Decode(exl3.Codebook.mul1), O.decode(O.CB_MUL1)),
+    "3inst": (exl3.Decode(exl3.Codebook.inst3), O.decode(O.CB_3INST)),
+    "spec1": (exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1), O.decode(O.CB_SPEC1, 15, 1)),
+    "std1": (exl3.Decode(exl3.Codebook.std1, exl3.Window(15), 3), O.decode(O.CB_STD1, 15, 3)),
+    "pair1": (exl3.Decode(exl3.Codebook.pair1), O.decode(O.CB_PAIR1)),
+    "mcg_w12": (exl3.Decode(exl3.Codebook.mcg, exl3.Window(12)), O.decode(O.CB_MCG, 12)),
+}
+
+
+def _case(dev, seed, rows, in_f, out_f, n, dtype=torch.float16):
+    p = synth.proj(seed, "lin", 1, in_f, out_f, n)
+    x = synth.normal(seed, "x", (rows, in_f))
+    pd = exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev))
+    return p, pd, x, x.to(dtype).to(dev)
+
+
+def _oracle(p, x, in_f, out_f, n, odec):
+    return O.project_rows(x.float().numpy(), p.trellis.numpy().view(np.uint16), p.suh.numpy().view(np.uint16),
+                          p.svh.numpy().view(np.uint16), in_f, out_f, n, odec, threads=8)
+
+
+def _run(pd, xd, dec):
+    y = exl3.linear(xd, pd, dec)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
+def test_gemv_rows_and_rates_mcg(dev, rows, n):
+    print(f"[gemv] rows={rows} n={n}", flush=True)
+    p, pd, x, xd = _case(dev, 100 + n, rows, 512, 384, n)
+    dec, odec = DECODES["mcg"]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 512, 384, n, odec)) < BAR
+
+
+@pytest.mark.parametrize("label", list(DECODES))
+@pytest.mark.parametrize("n", [32, 48, 64])
+def test_gemv_codebooks(dev, label, n):
+    print(f"[gemv] {label} n={n}", flush=True)
+    p, pd, x, xd = _case(dev, 7, 2, 256, 512, n)
+    dec, odec = DECODES[label]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 512, n, odec)) < BAR
+
+
+@pytest.mark.parametrize("n", [18, 22, 44, 58, 66, 96, 128])
+def test_gemv_generic_rates(dev, n):
+    print(f"[gemv] generic n={n}", flush=True)
+    p, pd, x, xd = _case(dev, 3, 3, 256, 256, n)
+    dec, odec = DECODES["spec1"] if n < 24 or n > 64 else DECODES["pair1"]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 256, n, odec)) < BAR
+
+
+@pytest.mark.parametrize("splits,separate", [("1", "0"), ("2", "0"), ("4", "1"), ("8", "0")])
+def test_gemv_split_and_finish_arms_agree(dev, splits, separate):
+    print(f"[gemv] splits={splits} separate={separate}", flush=True)
+    p, pd, x, xd = _case(dev, 9, 4, 1024, 256, 48)
+    dec, odec = DECODES["3inst"]
+    want = _oracle(p, x, 1024, 256, 48, odec)
+    os.environ["EXL3_GEMV_SPLITS"] = splits
+    os.environ["EXL3_GEMV_SEPARATE_FINISH"] = separate
+    try:
+        for _ in range(3):  # fused finish counters must come back to zero between calls
+            assert max_abs_rel(_run(pd, xd, dec), want) < BAR
+    finally:
+        del os.environ["EXL3_GEMV_SPLITS"]
+        del os.environ["EXL3_GEMV_SEPARATE_FINISH"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemv_activation_dtypes(dev, dtype):
+    p, pd, x, xd = _case(dev, 13, 2, 256, 256, 64, dtype)
+    dec, odec = DECODES["mcg"]
+    xo = xd.float().cpu()  # the oracle rounds its input to f16 as prepareInput does
+    want = _oracle(p, xo, 256, 256, 64, odec)
+    y = exl3.linear(xd, pd, dec)
+    assert y.dtype == dtype
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_linear_grouped(dev):
+    g, rows, in_f, out_f, n = 3, 2, 256, 384, 32
+    p = synth.proj(21, "grp", g, in_f, out_f, n)
+    x = synth.normal(21, "x", (g, rows, in_f))
+    pd = exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev))
+    y = exl3.linear_grouped(x.to(dev), pd, exl3.MCG).float().cpu().numpy()
+    for b in range(g):
+        want = O.project_rows(x[b].float().numpy(), p.trellis[b].numpy().view(np.uint16),
+                              p.suh[b].numpy().view(np.uint16), p.svh[b].numpy().view(np.uint16), in_f, out_f, n,
+                              O.decode(O.CB_MCG), threads=8)
+        assert max_abs_rel(y[b], want) < BAR
+
+
+@pytest.mark.parametrize("rows", [9, 16, 33, 130])
+@pytest.mark.parametrize("n", [32, 48, 64, 40])
+def test_gemm_arm(dev, rows, n):
+    print(f"[gemm] rows={rows} n={n}", flush=True)
+    p, pd, x, xd = _case(dev, 40 + rows, rows, 512, 256, n)
+    dec, odec = DECODES["3inst"]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 512, 256, n, odec)) < BAR
+
+
+@pytest.mark.parametrize("label", ["spec1", "pair1", "mul1"])
+def test_gemm_codebooks(dev, label):
+    p, pd, x, xd = _case(dev, 77, 24, 256, 256, 48)
+    dec, odec = DECODES[label]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 256, 48, odec)) < BAR
+
+
+def test_gemm_rows_equal_gemv_rows(dev):
+    """Byte-exactness is not claimed between arms, but the two arms agree to the bar on the same rows."""
+    p, pd, x, xd = _case(dev, 5, 12, 512, 512, 64)
+    dec = DECODES["mcg"][0]
+    wide = _run(pd, xd, dec)
+    narrow = np.concatenate([_run(pd, xd[i:i + 4].contiguous(), dec) for i in range(0, 12, 4)])
+    assert max_abs_rel(wide, narrow) < BAR
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_c1_full_size_3inst_k4(dev, rows):
+    """Config 1's shape at full size: 4096 x 4096, K4, 3INST, against the oracle."""
+    print(f"[c1] rows={rows}", flush=True)
+    p, pd, x, xd = _case(dev, 0, rows, 4096, 4096, 64)
+    dec, odec = DECODES["3inst"]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 4096, 4096, 64, odec)) < BAR
+
+
+@pytest.mark.parametrize("in_f,out_f,n", [(4096, 14336, 32), (14336, 4096, 48), (2048, 2048, 64)])
+def test_c2_shapes_mcg(dev, in_f, out_f, n):
+    print(f"[c2] {in_f}x{out_f} n={n}", flush=True)
+    p, pd, x, xd = _case(dev, 1, 4, in_f, out_f, n)
+    dec, odec = DECODES["mcg"]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, in_f, out_f, n, odec)) < BAR

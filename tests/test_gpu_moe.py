@@ -1,0 +1,126 @@
+"""GPU parity of the routed SwiGLU expert chain (moe / moeWithShared / moeClamped / moeRagged) and the router.
+
+Reference oracle: moeSwigluHost (src/exl3/expert_exl3_kernels.zig:3059-3114), per row.  Bar: max-abs-rel 2e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from sushi_amd import exl3, synth
+from tests._util import max_abs_rel
+
+pytestmark = pytest.mark.gpu
+
+BAR = 2e-3
+
+
+def _np(p):
+    return (p.trellis.numpy().view(np.uint16), p.suh.numpy().view(np.uint16), p.svh.numpy().view(np.uint16))
+
+
+def _to(b, dev):
+    return exl3.Bank(*(exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev)) for p in (b.gate, b.up, b.down)))
+
+
+def _route(seed, rows, experts, k):
+    logits = synth.normal(seed, "logits", (rows, experts), dtype=torch.float32).numpy()
+    return O.route_topk(logits, k)
+
+
+def _oracle_moe(b, x, inds, scores, hidden, inter, n, odec, clamp=0.0):
+    ys = []
+    for r in range(x.shape[0]):
+        ys.append(O.moe_swiglu_host(x[r], _np(b.gate), _np(b.up), _np(b.down), inds[r], scores[r], hidden, inter,
+                                    (n, n, n), odec, clamp))
+    return np.stack(ys)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8, 17])
+@pytest.mark.parametrize("n", [32, 48])
+def test_moe_decode_chain(dev, rows, n):
+    print(f"[moe] rows={rows} n={n}", flush=True)
+    E, hidden, inter, k = 16, 256, 384, 4
+    b = synth.bank(3, "moe", E, hidden, inter, n)
+    x = synth.normal(3, "x", (rows, hidden))
+    inds, scores = _route(3 + rows, rows, E, k)
+    want = _oracle_moe(b, x.float().numpy(), inds, scores, hidden, inter, n, O.decode(O.CB_MCG))
+    y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                 torch.from_numpy(scores).to(dev), exl3.MCG)
+    assert y.shape == x.shape and y.dtype == torch.float16
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+@pytest.mark.parametrize("label,dec,odec", [
+    ("spec1", exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1), O.decode(O.CB_SPEC1, 15, 1)),
+    ("pair1", exl3.Decode(exl3.Codebook.pair1), O.decode(O.CB_PAIR1)),
+    ("3inst", exl3.INST3, O.decode(O.CB_3INST)),
+])
+def test_moe_codebooks(dev, label, dec, odec):
+    E, hidden, inter, k, rows, n = 8, 256, 256, 3, 2, 32
+    b = synth.bank(8, "moe" + label, E, hidden, inter, n)
+    x = synth.normal(8, "x", (rows, hidden))
+    inds, scores = _route(8, rows, E, k)
+    want = _oracle_moe(b, x.float().numpy(), inds, scores, hidden, inter, n, odec)
+    y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                 torch.from_numpy(scores).to(dev), dec)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_moe_with_shared_and_clamped(dev):
+    E, hidden, inter, k, rows, n = 8, 256, 128, 2, 3, 32
+    b = synth.bank(4, "moes", E, hidden, inter, n)
+    x = synth.normal(4, "x", (rows, hidden)) * 3
+    inds, scores = _route(4, rows, E, k)
+    shared = synth.normal(4, "shared", (rows, hidden))
+    bd = _to(b, dev)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    want = _oracle_moe(b, x.float().numpy(), inds, scores, hidden, inter, n, O.decode(O.CB_MCG))
+    y = exl3.moe_with_shared(x.to(dev), bd, xi, sc, exl3.MCG, False, shared.to(dev))
+    assert max_abs_rel(y.float().cpu().numpy(), want + shared.float().numpy()) < BAR
+    wantc = _oracle_moe(b, x.float().numpy(), inds, scores, hidden, inter, n, O.decode(O.CB_MCG), clamp=2.0)
+    yc = exl3.moe_clamped(x.to(dev), bd, xi, sc, exl3.MCG, 2)
+    assert max_abs_rel(yc.float().cpu().numpy(), wantc) < BAR
+    assert max_abs_rel(wantc, want) > 10 * BAR  # the clamp is live on this data
+
+
+def test_moe_ragged_rate_groups(dev):
+    hidden, inter, k, rows = 256, 256, 4, 3
+    groups = [(6, (32, 32, 48)), (10, (16, 16, 32))]
+    banks = [synth.bank(20 + g, f"rg{g}", e, hidden, inter, rates) for g, (e, rates) in enumerate(groups)]
+    rb = exl3.Ragged.init([_to(b, dev) for b in banks])
+    E = sum(e for e, _ in groups)
+    x = synth.normal(20, "x", (rows, hidden))
+    inds, scores = _route(20, rows, E, k)
+    want = np.zeros((rows, hidden))
+    odec = O.decode(O.CB_MCG)
+    for r in range(rows):
+        for j in range(k):
+            e = int(inds[r, j])
+            g = 0 if e < groups[0][0] else 1
+            local = e - (0 if g == 0 else groups[0][0])
+            b = banks[g]
+            want[r] += O.moe_swiglu_host(x[r].float().numpy(), _np(b.gate), _np(b.up), _np(b.down), [local],
+                                         [scores[r, j]], hidden, inter, groups[g][1], odec)
+    y = exl3.moe_ragged(x.to(dev), rb, torch.from_numpy(inds.view(np.int32)).to(dev),
+                        torch.from_numpy(scores).to(dev), exl3.MCG)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_router_matches_oracle(dev):
+    logits = synth.normal(2, "logits", (9, 256), dtype=torch.float32)
+    inds, scores = exl3.moe_routing_chain(logits.to(dev), 8)
+    oi, os_ = O.route_topk(logits.numpy(), 8)
+    assert (inds.cpu().numpy().view(np.uint32) == oi).all()
+    assert np.allclose(scores.cpu().numpy(), os_, rtol=1e-5, atol=1e-7)
+
+
+def test_tile_major_matches_oracle(dev):
+    t = synth.codes(1, "tm", (3, 4, 6, 40))
+    got = exl3.tile_major(t.to(dev)).cpu().numpy().view(np.uint16)
+    src = t.numpy().view(np.uint16)
+    for e in range(3):
+        assert (got[e].reshape(-1) == O.tile_major(src[e].reshape(-1), 4, 6, 40)).all()
+    back = exl3.tile_major(torch.from_numpy(got.view(np.int16)).to(dev), inverse=True).cpu().numpy()
+    assert (back.view(np.uint16) == src).all()

@@ -1,0 +1,129 @@
+"""Pins the oracle's arithmetic layer: Hadamard, project, decodeDense, the MoE host oracle, routing and layout.
+
+Each restatement is checked against something independent of its own code: the reference's fixtures (`public`),
+closed forms (Sylvester Hadamard, H*H = I) and numpy products built from the fixture/dense weights.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests._util import LINEAR_FIXTURES, f16_bits_to_f32, load_fixture, rel_rms
+
+CB = {"mul1": O.CB_MUL1, "mcg": O.CB_MCG}
+
+
+def _sylvester(n=128):
+    h = np.array([[1.0]])
+    while h.shape[0] < n:
+        h = np.block([[h, h], [h, -h]])
+    return h / np.sqrt(n)
+
+
+def test_hadamard128_is_the_scaled_sylvester_matrix():
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(128).astype(np.float32)
+    h = _sylvester()
+    assert np.allclose(O.hadamard128(v), h @ v, atol=1e-5)
+    assert np.allclose(O.hadamard128(O.hadamard128(v)), v, atol=1e-5)  # H is an involution
+    assert np.allclose(O.fwht128(v), O.hadamard128(v), atol=1e-5)
+
+
+@pytest.mark.parametrize("name,n,cb,w", LINEAR_FIXTURES)
+def test_project_matches_dense_matvec_over_public(name, n, cb, w):
+    """The reference's own bar (expert_exl3.zig:897-914): project() vs x . public, relRms < 0.02."""
+    d = load_fixture(name)
+    rng = np.random.default_rng(7)
+    x = (rng.random(128, dtype=np.float32) * 2 - 1)
+    dec = O.decode(CB[cb], w)
+    y = O.project(x, d["trellis"], d["suh"], d["svh"], 128, 128, n, dec)
+    dense = x.astype(np.float64) @ f16_bits_to_f32(d["public"]).astype(np.float64)
+    assert rel_rms(y, dense) < 0.02
+
+
+@pytest.mark.parametrize("name,n,cb,w", LINEAR_FIXTURES)
+def test_decode_dense_is_suh_h_m_h_svh(name, n, cb, w):
+    d = load_fixture(name)
+    dec = O.decode(CB[cb], w)
+    dense = O.decode_dense(d["trellis"], d["suh"], d["svh"], 128, 128, n, dec)
+    m = f16_bits_to_f32(d["inner"]).astype(np.float64)
+    h = _sylvester()
+    want = np.diag(f16_bits_to_f32(d["suh"])) @ h @ m @ h @ np.diag(f16_bits_to_f32(d["svh"]))
+    assert np.allclose(dense, want, atol=1e-4)
+    # and it is the public matrix before its f16 rounding
+    assert np.allclose(dense, f16_bits_to_f32(d["public"]), rtol=2e-3, atol=2e-4)
+
+
+def _bank(rng, e, i, o, n):
+    t = rng.integers(0, 1 << 16, size=(e, i // 16, o // 16, n), dtype=np.uint32).astype(np.uint16)
+    su = (rng.choice([-1.0, 1.0], size=(e, i)) * rng.uniform(0.5, 1.5, size=(e, i))).astype(np.float16).view(np.uint16)
+    sv = (rng.choice([-1.0, 1.0], size=(e, o)) * rng.uniform(0.5, 1.5, size=(e, o))).astype(np.float16).view(np.uint16)
+    return t, su, sv
+
+
+def test_project_rows_threads_give_the_same_bytes():
+    rng = np.random.default_rng(11)
+    t, su, sv = _bank(rng, 1, 256, 384, 48)
+    x = rng.standard_normal((5, 256)).astype(np.float32)
+    dec = O.decode(O.CB_MCG)
+    one = O.project_rows(x, t, su, sv, 256, 384, 48, dec, threads=1)
+    many = O.project_rows(x, t, su, sv, 256, 384, 48, dec, threads=4)
+    assert (one == many).all()
+
+
+def test_moe_swiglu_host_against_numpy_over_dense_weights():
+    rng = np.random.default_rng(5)
+    e, hid, inter, n = 6, 256, 128, 32
+    g, u, d = _bank(rng, e, hid, inter, n), _bank(rng, e, hid, inter, n), _bank(rng, e, inter, hid, n)
+    dec = O.decode(O.CB_MCG)
+    x = rng.standard_normal(hid).astype(np.float16).astype(np.float32)
+    slots = np.array([4, 1, 3], np.uint32)
+    wts = np.array([0.5, 0.3, 0.2], np.float32)
+    y = O.moe_swiglu_host(x, g, u, d, slots, wts, hid, inter, (n, n, n), dec)
+
+    def dense(p, ex, i, o):
+        return O.decode_dense(p[0][ex], p[1][ex], p[2][ex], i, o, n, dec).astype(np.float64)
+
+    want = np.zeros(hid)
+    for s, w in zip(slots, wts):
+        gy = x @ dense(g, s, hid, inter)
+        uy = x @ dense(u, s, hid, inter)
+        h = gy / (1 + np.exp(-gy)) * uy
+        want += w * (h @ dense(d, s, inter, hid))
+    assert rel_rms(y, want) < 5e-3
+
+
+def test_moe_clamp_limits_gate_above_and_up_both_ways():
+    rng = np.random.default_rng(6)
+    e, hid, inter, n = 2, 128, 128, 32
+    g, u, d = _bank(rng, e, hid, inter, n), _bank(rng, e, hid, inter, n), _bank(rng, e, inter, hid, n)
+    dec = O.decode(O.CB_MCG)
+    x = (4 * rng.standard_normal(hid)).astype(np.float16).astype(np.float32)
+    a = O.moe_swiglu_host(x, g, u, d, [0, 1], [0.5, 0.5], hid, inter, (n, n, n), dec, clamp_limit=1.0)
+    b = O.moe_swiglu_host(x, g, u, d, [0, 1], [0.5, 0.5], hid, inter, (n, n, n), dec)
+    assert not np.allclose(a, b)
+
+
+def test_route_topk_against_numpy():
+    rng = np.random.default_rng(2)
+    logits = rng.standard_normal((5, 64)).astype(np.float32)
+    logits[0, 3] = logits[0, 9] = 9.0  # a tie: the lower index comes first
+    inds, scores = O.route_topk(logits, 8)
+    for r in range(5):
+        order = sorted(range(64), key=lambda i: (-logits[r, i], i))[:8]
+        assert inds[r].tolist() == order
+        p = np.exp(logits[r] - logits[r].max())
+        p /= p.sum()
+        assert np.allclose(scores[r], p[order] / p[order].sum(), rtol=1e-6)
+    assert inds[0, 0] == 3 and inds[0, 1] == 9
+
+
+def test_tile_major_round_trip_and_reference_layout_case():  # layout.zig:160-175
+    it, ot, n = 5, 4, 3
+    src = np.arange(it * ot * n, dtype=np.uint16)
+    dst = O.tile_major(src, it, ot, n)
+    for pair in range(ot // 2):
+        for tk in range(it):
+            for o in range(2):
+                want = src[(tk * ot + pair * 2 + o) * n:][:n]
+                assert (dst[((pair * it + tk) * 2 + o) * n:][:n] == want).all()
+    assert (O.tile_major_inverse(dst, it, ot, n) == src).all()
