@@ -8,7 +8,7 @@
 #include <cstring>
 #include <string>
 
-#include "../../include/sushi_exl3_hip.h"
+#include "sushi_exl3_hip.h"
 #include "exl3_kernels.h"
 #include "exl3_tables.h"
 
@@ -41,6 +41,12 @@ int32_t launched(hipError_t e, const char *what) {
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Every workspace starts with a fixed region of fused-finish arrival counters.  Only the fused-finish GEMV touches
+// it, and every such launch leaves its counters at zero again, so the region stays valid across calls of any arm
+// (exl3_workspace_init zeroes it once after allocation).  Scratch of every arm begins after it.
+constexpr size_t kCounterSlots = 65536;
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(uint32_t);
 
 bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
 
@@ -102,13 +108,13 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
     p.splits = env_int("EXL3_GEMV_SPLITS", 0);
     const int blocks = in / 128;
     if (p.splits <= 0 || blocks % p.splits != 0 || in / p.splits > 2048) p.splits = gemv_default_splits(in, out, rows, groups);
-    p.counters_bytes = align_up((size_t)groups * (out / 128) * sizeof(uint32_t));
+    p.counters_bytes = kCounterBytes;
     p.partial_bytes = p.splits > 1 ? align_up((size_t)groups * p.splits * rows * out * sizeof(float)) : 0;
     return p;
 }
 
 size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
-    size_t b = align_up((size_t)groups * rows * in * 2);
+    size_t b = kCounterBytes + align_up((size_t)groups * rows * in * 2);
     if (n % 16 != 0 || n > 64) b += align_up((size_t)groups * out * in * 2);
     return b;
 }
@@ -166,7 +172,8 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.splits = p.splits;
         a.groups = groups;
         a.nproj = 1;
-        a.fused_finish = env_int("EXL3_GEMV_SEPARATE_FINISH", 0) ? 0 : 1;
+        a.fused_finish = (env_int("EXL3_GEMV_SEPARATE_FINISH", 0) == 0 &&
+                          (size_t)groups * (out / 128) <= kCounterSlots) ? 1 : 0;
         a.partial_only = 0;
         return launched(run_gemv(fam, PRO_X, a, stream), "exl3_linear (gemv)");
     }
@@ -181,8 +188,8 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     g.suh = suh;
     g.svh = svh;
     g.k = k;
-    g.xp = reinterpret_cast<uint16_t *>(w);
-    g.wt = reinterpret_cast<uint16_t *>(w + align_up((size_t)groups * rows * in * 2));
+    g.xp = reinterpret_cast<uint16_t *>(w + kCounterBytes);
+    g.wt = reinterpret_cast<uint16_t *>(w + kCounterBytes + align_up((size_t)groups * rows * in * 2));
     g.y = y;
     g.y_dtype = y_dtype;
     g.groups = groups;
@@ -225,10 +232,10 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
     const int nslots = rows * topk;
     MoePlan p = plan_moe(nslots, hidden, inter);
-    const size_t need = 2 * p.gu_bytes + p.down_bytes;
+    const size_t need = kCounterBytes + 2 * p.gu_bytes + p.down_bytes;
     if (ws_bytes < need || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
         return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
-    char *w = static_cast<char *>(ws);
+    char *w = static_cast<char *>(ws) + kCounterBytes;
     float *gate_part = reinterpret_cast<float *>(w);
     float *up_part = reinterpret_cast<float *>(w + p.gu_bytes);
     float *down_part = reinterpret_cast<float *>(w + 2 * p.gu_bytes);
@@ -388,7 +395,7 @@ int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t
 size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
     if (rows <= 0 || topk <= 0 || hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) return 0;
     MoePlan p = plan_moe(rows * topk, hidden, inter);
-    return 2 * p.gu_bytes + p.down_bytes;
+    return kCounterBytes + 2 * p.gu_bytes + p.down_bytes;
 }
 
 int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,

@@ -95,6 +95,68 @@ __device__ __forceinline__ uint32_t decode_pair_h2(uint32_t c0, uint32_t c1, con
 }
 
 // ------------------------------------------------------------------------------------------------------------
+// Hand-scheduled gfx950 decode primitives for the GEMV's hot loop.  A 32-bit funnel window `x` holds one codeword
+// in its low half and (for rates K = 1, 2, 4) the codeword 16/K positions earlier in its high half; HI selects it.
+// Every op here is full rate: the 32-bit hash multiply c*M (a quarter-rate v_mul_lo_u32) becomes
+//   t = lo16(c * hi16(M)) << 16        v_mul_lo_u16 (SDWA: reads the 16-bit half, writes the high half)
+//   p = c * lo16(M) + t                v_mad_u32_u16 (op_sel picks the half)
+// which equals c*M mod 2^32 because c < 2^16.
+
+template <bool HI>
+__device__ __forceinline__ uint32_t mul16x32(uint32_t x, uint32_t mh, uint32_t ml) {
+    uint32_t t, p;
+    if constexpr (HI) {
+        asm("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0"
+            : "=v"(t) : "v"(x), "v"(mh));
+        asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(x), "v"(ml), "v"(t));
+    } else {
+        asm("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_0"
+            : "=v"(t) : "v"(x), "v"(mh));
+        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(x), "v"(ml), "v"(t));
+    }
+    return p;
+}
+
+// 3INST's LCG step c*A + B (mod 2^32) in two full-rate ops.  `q` must hold lo16(B) in its low half: v_mad_u16 with
+// op_sel dst=1 writes lo16(c*hi16(A) + hi16(B)) into the high half and keeps the low half.
+constexpr uint32_t LCG_A = 89226354u, LCG_B = 64248484u;
+template <bool HI>
+__device__ __forceinline__ uint32_t lcg16(uint32_t x, uint32_t &q) {
+    uint32_t p;
+    if constexpr (HI) {
+        asm("v_mad_u16 %0, %1, %2, %3 op_sel:[1,0,0,1]" : "+v"(q) : "v"(x), "v"(LCG_A >> 16), "v"(LCG_B >> 16));
+        asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(x), "v"(LCG_A & 0xFFFFu), "v"(q));
+    } else {
+        asm("v_mad_u16 %0, %1, %2, %3 op_sel:[0,0,0,1]" : "+v"(q) : "v"(x), "v"(LCG_A >> 16), "v"(LCG_B >> 16));
+        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(x), "v"(LCG_A & 0xFFFFu), "v"(q));
+    }
+    return p;
+}
+
+// Packed f16 (lo = h0.lo + h0.hi, hi = h1.lo + h1.hi): two SDWA adds, the second writing the high half in place.
+__device__ __forceinline__ uint32_t pack_sums(uint32_t h0, uint32_t h1) {
+    uint32_t w;
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=v"(w) : "v"(h0));
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "+v"(w) : "v"(h1));
+    return w;
+}
+
+// The pre-sum halves of one codeword (the f16 pair whose sum is the weight, unscaled for hash masks).
+// `q` is the LCG scratch of lcg16; `k` carries the hash row.
+template <int FAM, bool HI>
+__device__ __forceinline__ uint32_t halves_of(uint32_t x, const DecodeK &k, uint32_t &q) {
+    if constexpr (FAM == FAM_MCG) {
+        return (mul16x32<HI>(x, 0xCBACu, 0x1FEDu) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    } else if constexpr (FAM == FAM_3INST) {
+        return (lcg16<HI>(x, q) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    } else {  // FAM_HASH
+        return mul16x32<HI>(x, k.mult >> 16, k.mult & 0xFFFFu) & k.mask0;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------
 // Bit windows.  A lane that owns codewords 32j..32j+31 of a tile (the 8 weights of fragment threads 4j..4j+3)
 // reads stream bits [2jn - 32, 2jn + 2n): codeword u (0..31) ends at 32 + floor((u+1) n / 16) in that range.
 

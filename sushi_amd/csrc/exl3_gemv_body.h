@@ -5,15 +5,17 @@
 // src/exl3/expert_exl3_kernels.zig).
 //
 // MI355X layout.  A workgroup (4 waves) owns one output group of 8 tiles (128 outputs, one Hadamard block) of one
-// (bank, x-block) pair over one k split (whole 128-blocks).  Per k-tile row a wave streams the group's 8 tiles,
-// which lie contiguous in the pack order [IT][OT][n] (8*n*2 bytes, 1 KiB at K4): lane = 8*o + j reads chunk j of
-// tile o, the words carrying codewords 32j..32j+31 = fragment threads 4j..4j+3 of tensorCorePerm = output columns
-// j and j+8 over all 16 k rows.  Every lane owns two output columns outright, decodes its 32 weights into registers
-// as packed f16 pairs (t, t+1) = rows (r, r+1) of one column and feeds v_dot2_f32_f16 against the prepared input
-// held in LDS.  No cross-lane reduction happens inside a wave; the 4 waves (different k-tiles) meet once in LDS.
-// The prologue prepares the split's k range (x * suh, FWHT-128, f16) or, for the MoE down projection, builds the
-// SwiGLU mid from the gate/up planes.  The finish (FWHT-128, * svh) runs in the same launch when there is one
-// split, in the last workgroup of an output group to arrive (fused finish), or in a small second kernel.
+// (bank, x-block) pair over one k split of at most 16 k-tiles (whole 128-blocks).  Per k-tile row a wave streams the
+// group's 8 tiles, which lie contiguous in the pack order [IT][OT][n] (8*n*2 bytes, 1 KiB at K4): lane = 8*o + j
+// reads chunk j of tile o, the words carrying codewords 32j..32j+31 = fragment threads 4j..4j+3 of tensorCorePerm =
+// output columns j and j+8 over all 16 k rows.  Every lane owns two output columns outright, decodes its 32 weights
+// into registers as packed f16 pairs (t, t+1) = rows (r, r+1) of one column and feeds v_dot2_f32_f16 against the
+// prepared input held in LDS.  No cross-lane reduction happens inside a wave; the 4 waves meet once in LDS.
+//
+// Latency: a wave issues the loads of all its tiles (<= 4) before the prologue, so HBM latency overlaps the input
+// preparation (x * suh, FWHT-128, f16 -- or the MoE SwiGLU mid).  The finish (FWHT-128, * svh) runs in the same
+// launch: with one split directly, otherwise in the last workgroup of an output group to arrive.  Partials travel
+// by write-through stores and a relaxed arrival counter (no L2 write-back fence, which costs ~1 us per workgroup).
 #pragma once
 #include "exl3_kernels.h"
 #include "exl3_tables.h"
@@ -29,6 +31,7 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
 constexpr int GEMV_WAVES = 4;
 constexpr int GEMV_THREADS = 64 * GEMV_WAVES;
 constexpr int MAX_KSPAN = 2048;
+constexpr int TPW = 4;  // tiles a wave loads before the prologue
 
 __device__ __forceinline__ float load_x(const void *x, int dt, size_t i) {
     if (dt == DT_F16) return load_act<DT_F16>(x, i);
@@ -63,108 +66,135 @@ __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c
     store_y(a.y, a.y_dtype, yo + lane + 64, v1 * HAD_SCALE * h2f(a.svh[c.proj][sv + lane + 64]));
 }
 
-template <int FAM, int N, int RT>
-__device__ __forceinline__ void gemv_main(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
-                                          int n, const DecodeK &k, const uint16_t (*xs)[MAX_KSPAN], int wave, int lane,
-                                          float (&acc0)[RT], float (&acc1)[RT]) {
-    const int o = lane >> 3, j = lane & 7;
-    for (int kk = wave; kk < c.KS; kk += GEMV_WAVES) {
-        const int tk = c.kt0 + kk;
-        const uint32_t *words = reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n);
-        uint4 X[RT], Y[RT];
+// Codeword v of the lane as (window index, high half?): for K = 1, 2, 4 the window ending at codeword v + 16/K
+// carries codeword v in its high half, so half the windows serve two codewords.
+template <int N>
+struct Pairing {
+    static constexpr bool ON = N == 16 || N == 32 || N == 64;
+    static constexpr int STEP = ON ? 256 / N : 32;
+    __device__ static constexpr bool hi(int v) { return ON && ((v / STEP) % 2 == 0); }
+    __device__ static constexpr int win(int v) { return hi(v) ? v + STEP : v; }
+};
+
+// The 32 weights of one tile chunk (lane-owned columns j and j+8), dotted into acc0 (column j) / acc1 (column j+8).
+// Written in phases (windows, products, masks, low sums, high sums, dots) so each partial-register write has many
+// independent instructions before its reader and the hazard recognizer inserts no wait states.
+template <int FAM, int N, int RT, bool MASKED>
+__device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint4 (&X)[RT],
+                                            const uint4 (&Y)[RT], const DecodeK &k, uint32_t (&q)[32],
+                                            float (&acc0)[RT], float (&acc1)[RT]) {
+    using P = Pairing<N>;
+    uint32_t win[32];
+#pragma unroll
+    for (int v = 0; v < 32; v++) {
+        if (P::win(v) == v) {
+            win[v] = lane_codeword<N>(A, v);
+            if constexpr (MASKED) win[v] &= k.wmask | (k.wmask << 16);
+        }
+    }
+    uint32_t w[16];
+    if constexpr (FAM == FAM_PAIR) {
+        // both weights of a pair decode from the odd codeword (decodePair, expert_exl3.zig:298-301)
+        uint32_t pr[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int v = 2 * i + 1;
+            pr[i] = P::hi(v) ? mul16x32<true>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu)
+                             : mul16x32<false>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu);
+        }
+        uint32_t h0[16], h1[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            h0[i] = pr[i] & k.mask0;
+            h1[i] = __builtin_amdgcn_alignbit(pr[i], pr[i], 32u - k.rot) & k.mask1;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = pack_sums(h0[i], h1[i]);
+    } else if constexpr (FAM == FAM_MUL1) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t x0 = win[P::win(2 * i)], x1 = win[P::win(2 * i + 1)];
+            const uint32_t c0 = P::hi(2 * i) ? x0 >> 16 : x0, c1 = P::hi(2 * i + 1) ? x1 >> 16 : x1;
+            w[i] = pack_h2(decode1<FAM_MUL1>(c0, k), decode1<FAM_MUL1>(c1, k));
+        }
+    } else {
+        uint32_t h[32];
+#pragma unroll
+        for (int v = 0; v < 32; v++)
+            h[v] = P::hi(v) ? halves_of<FAM, true>(win[P::win(v)], k, q[v]) : halves_of<FAM, false>(win[P::win(v)], k, q[v]);
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+                : "=v"(w[i]) : "v"(h[2 * i]));
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+                : "+v"(w[i]) : "v"(h[2 * i + 1]));
+    }
+    // pair i = (u, u+1), u = 2i = 8qq + 2p: p = 0/1 -> column j rows 2qq(+8), p = 2/3 -> column j+8
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int qq = i >> 2, p = i & 3;
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            X[r] = *reinterpret_cast<const uint4 *>(&xs[r][kk * 16]);
-            Y[r] = *reinterpret_cast<const uint4 *>(&xs[r][kk * 16 + 8]);
+            const uint4 &V = (p & 1) ? Y[r] : X[r];
+            const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
+            if (p < 2) acc0[r] = dot2(w[i], xv, acc0[r]);
+            else acc1[r] = dot2(w[i], xv, acc1[r]);
         }
-        if constexpr (N != 0) {
-            uint32_t A[LaneBits<N>::AW];
-            load_lane_words<N>(words, j, A);
+    }
+}
+
+// The prologue's input loads for a wave's first jobs, issued ahead of the tile loads: loads retire in order, so an
+// input load issued behind 16 KiB of tile loads would hold the prologue back until all of them had landed.
+constexpr int PRE_JOBS = 4;
+struct PrologueRegs {
+    float x0[PRE_JOBS], x1[PRE_JOBS], s0[PRE_JOBS], s1[PRE_JOBS];
+};
+
+template <int PRO>
+__device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx &c, int RT, int wave, int lane,
+                                               PrologueRegs &pr) {
+    if constexpr (PRO == PRO_X) {
+        const int nblk = c.KS >> 3;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int u = 8 * q + 2 * p;
-                    const uint32_t h = decode_pair_h2<FAM>(lane_codeword<N>(A, u), lane_codeword<N>(A, u + 1), k);
-#pragma unroll
-                    for (int r = 0; r < RT; r++) {
-                        const uint4 &V = (p & 1) ? Y[r] : X[r];
-                        const uint32_t xv = q == 0 ? V.x : q == 1 ? V.y : q == 2 ? V.z : V.w;
-                        if (p < 2) acc0[r] = dot2(h, xv, acc0[r]);
-                        else acc1[r] = dot2(h, xv, acc1[r]);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int t = 32 * j + 8 * q + 2 * p;
-                    const uint32_t h = decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
-#pragma unroll
-                    for (int r = 0; r < RT; r++) {
-                        const uint4 &V = (p & 1) ? Y[r] : X[r];
-                        const uint32_t xv = q == 0 ? V.x : q == 1 ? V.y : q == 2 ? V.z : V.w;
-                        if (p < 2) acc0[r] = dot2(h, xv, acc0[r]);
-                        else acc1[r] = dot2(h, xv, acc1[r]);
-                    }
-                }
+        for (int i = 0; i < PRE_JOBS; i++) {
+            const int job = wave + GEMV_WAVES * i;
+            const int rho = job / nblk, b = job - rho * nblk;
+            pr.x0[i] = pr.x1[i] = pr.s0[i] = pr.s1[i] = 0.f;
+            if (job < nblk * RT && rho < a.rows) {
+                const int kb = c.kt0 * 16 + b * 128;
+                const size_t si = (size_t)c.bank * a.in + kb;
+                const size_t xi = ((size_t)(c.g / a.x_div) * a.rows + rho) * a.in + kb;
+                pr.x0[i] = load_x(a.x, a.x_dtype, xi + lane);
+                pr.x1[i] = load_x(a.x, a.x_dtype, xi + lane + 64);
+                pr.s0[i] = h2f(a.suh[c.proj][si + lane]);
+                pr.s1[i] = h2f(a.suh[c.proj][si + lane + 64]);
             }
         }
     }
 }
 
-// Per-rate decode constants for a ragged bank (hash rows and pair rows differ by rate; the window mask does not).
-template <int FAM>
-__device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
-    DecodeK k = a.k;
-    if constexpr (FAM == FAM_HASH || FAM == FAM_PAIR) {
-        table_row(a.table, n, k.mult, k.mask0, k.mask1, k.rot);
-    }
-    return k;
-}
-
-// N > 0: one rate for the launch; N < 0: per-expert rate from the ragged meta table, dispatched per workgroup.
-template <int FAM, int N, int RT, int PRO>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    GemvCtx c;
-    c.IT = a.in >> 4;
-    c.OT = a.out >> 4;
-    c.G = c.OT >> 3;
-    c.S = a.splits;
-    const int L = blockIdx.x;
-    if ((c.G & 7) == 0) {  // keep an output group's splits on one XCD (workgroups go round-robin over 8 XCDs)
-        const int xcd = L & 7, r = L >> 3;
-        c.og = (r / c.S) * 8 + xcd;
-        c.sp = r % c.S;
-    } else {
-        c.og = L / c.S;
-        c.sp = L % c.S;
-    }
-    c.g = blockIdx.y;
-    c.proj = blockIdx.z;
-    c.bank = a.bank_of ? (int)min(a.bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
-    c.KS = c.IT / c.S;
-    c.kt0 = c.sp * c.KS;
-
-    __shared__ __align__(16) uint16_t xs[RT][MAX_KSPAN];
-    __shared__ float red[GEMV_WAVES][RT][128];
-    __shared__ int last_flag;
-
-    // ---- prologue over this split's k range
+template <int PRO>
+__device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, int RT, uint16_t (*xs)[MAX_KSPAN],
+                                         int wave, int lane, const PrologueRegs &pr) {
     const int nblk = c.KS >> 3;
     for (int job = wave; job < nblk * RT; job += GEMV_WAVES) {
         const int rho = job / nblk, b = job - rho * nblk;
         const int kb = c.kt0 * 16 + b * 128;
+        const int i = (job - wave) / GEMV_WAVES;
         float v0 = 0.f, v1 = 0.f;
         if (rho < a.rows) {
             const size_t si = (size_t)c.bank * a.in + kb;
             if constexpr (PRO == PRO_X) {  // prepareInput (expert_exl3.zig:490-501)
-                const size_t xi = ((size_t)(c.g / a.x_div) * a.rows + rho) * a.in + kb;
-                v0 = f16r(load_x(a.x, a.x_dtype, xi + lane));
-                v1 = f16r(load_x(a.x, a.x_dtype, xi + lane + 64));
+                if (i < PRE_JOBS) {
+                    v0 = f16r(pr.x0[i]) * pr.s0[i];
+                    v1 = f16r(pr.x1[i]) * pr.s1[i];
+                } else {
+                    const size_t xi = ((size_t)(c.g / a.x_div) * a.rows + rho) * a.in + kb;
+                    v0 = f16r(load_x(a.x, a.x_dtype, xi + lane)) * h2f(a.suh[c.proj][si + lane]);
+                    v1 = f16r(load_x(a.x, a.x_dtype, xi + lane + 64)) * h2f(a.suh[c.proj][si + lane + 64]);
+                }
             } else {  // the SwiGLU mid of the decode chain (DOWN_FUSED_SOURCE prologue, :1838-1920)
                 float gv[2], uv[2];
 #pragma unroll
@@ -193,11 +223,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
                         uv[i] = fminf(fmaxf(uv[i], -a.clamp_limit), a.clamp_limit);
                     }
                 }
-                v0 = silu(gv[0]) * uv[0];
-                v1 = silu(gv[1]) * uv[1];
+                v0 = silu(gv[0]) * uv[0] * h2f(a.suh[c.proj][si + lane]);
+                v1 = silu(gv[1]) * uv[1] * h2f(a.suh[c.proj][si + lane + 64]);
             }
-            v0 *= h2f(a.suh[c.proj][si + lane]);
-            v1 *= h2f(a.suh[c.proj][si + lane + 64]);
             fwht128_wave(v0, v1, lane);
             v0 *= HAD_SCALE;
             v1 *= HAD_SCALE;
@@ -205,42 +233,109 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
         xs[rho][b * 128 + lane] = __half_as_ushort(__float2half_rn(v0));
         xs[rho][b * 128 + lane + 64] = __half_as_ushort(__float2half_rn(v1));
     }
-    __syncthreads();
+}
 
-    // ---- decode + dot
+template <int RT>
+__device__ __forceinline__ void load_x_frag(const uint16_t (*xs)[MAX_KSPAN], int kk, uint4 (&X)[RT], uint4 (&Y)[RT]) {
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        X[r] = *reinterpret_cast<const uint4 *>(&xs[r][kk * 16]);
+        Y[r] = *reinterpret_cast<const uint4 *>(&xs[r][kk * 16 + 8]);
+    }
+}
+
+// Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
+template <int FAM, int N, int RT, int PRO>
+__device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
+                                          int n, const DecodeK &k, uint16_t (*xs)[MAX_KSPAN], float (*red)[RT][128],
+                                          int *last_flag) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int o = lane >> 3, j = lane & 7;
     float acc0[RT], acc1[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
-    if constexpr (N >= 0) {
-        const int n = N ? N : a.n;
-        const uint16_t *tb = a.trellis[c.proj] + (size_t)c.bank * c.IT * c.OT * n;
-        gemv_main<FAM, N, RT>(a, c, tb, n, a.k, xs, wave, lane, acc0, acc1);
-    } else {
-        const uint32_t *m = a.meta + (size_t)c.bank * 8;
-        const int n = (int)m[a.meta_col[c.proj]];
-        const uint16_t *tb = a.trellis[c.proj] + 2 * (size_t)m[4 + a.meta_col[c.proj]];
-        const DecodeK k = rate_constants<FAM>(a, n);
-        switch (n) {
-        case 16: gemv_main<FAM, 16, RT>(a, c, tb, n, k, xs, wave, lane, acc0, acc1); break;
-        case 24: gemv_main<FAM, 24, RT>(a, c, tb, n, k, xs, wave, lane, acc0, acc1); break;
-        case 32: gemv_main<FAM, 32, RT>(a, c, tb, n, k, xs, wave, lane, acc0, acc1); break;
-        case 48: gemv_main<FAM, 48, RT>(a, c, tb, n, k, xs, wave, lane, acc0, acc1); break;
-        case 64: gemv_main<FAM, 64, RT>(a, c, tb, n, k, xs, wave, lane, acc0, acc1); break;
-        default: gemv_main<FAM, 0, RT>(a, c, tb, n, k, xs, wave, lane, acc0, acc1); break;
+    uint32_t q[32];  // 3INST's per-codeword LCG scratch: the low half holds lo16(B) for good
+#pragma unroll
+    for (int i = 0; i < 32; i++) q[i] = LCG_B & 0xFFFFu;
+
+    if constexpr (N != 0) {
+        constexpr int AW = LaneBits<N>::AW;
+        const int ntiles = (c.KS - wave + GEMV_WAVES - 1) / GEMV_WAVES;  // this wave's k-tiles: wave, wave+4, ...
+        PrologueRegs pr;
+        prologue_fetch<PRO>(a, c, RT, wave, lane, pr);
+        uint32_t Aw[TPW][AW];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            if (t < ntiles) {
+                const int tk = c.kt0 + wave + GEMV_WAVES * t;
+                load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
+                                   Aw[t]);
+            }
+        }
+        prologue<PRO>(a, c, RT, xs, wave, lane, pr);
+        __syncthreads();
+        const bool masked = k.wmask != 0xFFFFu;
+        for (int t0 = 0; t0 < ntiles; t0 += TPW) {
+            if (t0 > 0) {  // splits longer than TPW tiles per wave: load the next batch in place
+#pragma unroll
+                for (int t = 0; t < TPW; t++) {
+                    if (t0 + t < ntiles) {
+                        const int tk = c.kt0 + wave + GEMV_WAVES * (t0 + t);
+                        load_lane_words<N>(
+                            reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j, Aw[t]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                if (t0 + t < ntiles) {
+                    uint4 X[RT], Y[RT];
+                    load_x_frag<RT>(xs, wave + GEMV_WAVES * (t0 + t), X, Y);
+                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], X, Y, k, q, acc0, acc1);
+                    else decode_tile<FAM, N, RT, false>(Aw[t], X, Y, k, q, acc0, acc1);
+                }
+            }
+        }
+    } else {  // any other rate: the generic reader (runtime funnel per codeword)
+        PrologueRegs pr;
+        prologue_fetch<PRO>(a, c, RT, wave, lane, pr);
+        prologue<PRO>(a, c, RT, xs, wave, lane, pr);
+        __syncthreads();
+        for (int kk = wave; kk < c.KS; kk += GEMV_WAVES) {
+            const int tk = c.kt0 + kk;
+            const uint32_t *words = reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n);
+            uint4 X[RT], Y[RT];
+            load_x_frag<RT>(xs, kk, X, Y);
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int t = 32 * j + 8 * qq + 2 * p;
+                    const uint32_t w =
+                        decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
+#pragma unroll
+                    for (int r = 0; r < RT; r++) {
+                        const uint4 &V = (p & 1) ? Y[r] : X[r];
+                        const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
+                        if (p < 2) acc0[r] = dot2(w, xv, acc0[r]);
+                        else acc1[r] = dot2(w, xv, acc1[r]);
+                    }
+                }
+            }
         }
     }
 
     // ---- cross-wave reduction
-    {
-        const int o = lane >> 3, j = lane & 7;
 #pragma unroll
-        for (int r = 0; r < RT; r++) {
-            red[wave][r][o * 16 + j] = acc0[r];
-            red[wave][r][o * 16 + j + 8] = acc1[r];
-        }
+    for (int r = 0; r < RT; r++) {
+        red[wave][r][o * 16 + j] = acc0[r];
+        red[wave][r][o * 16 + j + 8] = acc1[r];
     }
     __syncthreads();
     const bool direct = c.S == 1 && !a.partial_only;
+    // An output group's splits share one XCD (and so one L2) when the workgroup remap applies (G % 8 == 0): its
+    // partials then meet in that L2.  Otherwise they are written through to memory.
+    const bool xcd_local = (c.G & 7) == 0;
     float *part = a.partial[c.proj];
     for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
         const int r = idx >> 7, col = idx & 127;
@@ -248,8 +343,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int w = 0; w < GEMV_WAVES; w++) s += red[w][r][col];
         s *= a.out_scale;
-        if (direct) red[0][r][col] = s;
-        else if (r < a.rows) part[(((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out + (size_t)c.og * 128 + col] = s;
+        if (direct) {
+            red[0][r][col] = s;
+        } else if (r < a.rows) {
+            float *dst = part + (((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out + (size_t)c.og * 128 + col;
+            if (a.partial_only || xcd_local) *dst = s;  // L1 is write-through: the store lands in the XCD's L2
+            else __hip_atomic_store(dst, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // write-through to memory
+        }
     }
     if (direct) {
         __syncthreads();
@@ -258,27 +358,97 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     }
     if (a.partial_only || !a.fused_finish) return;
 
-    // ---- fused finish: the last split of this output group to arrive sums the partials and finishes.
-    __threadfence();
+    // ---- single-launch finish: the last split of this output group to arrive sums the partials and finishes.
+    // Each thread's write-through partial stores are acknowledged (s_waitcnt vmcnt(0)) before the barrier, so they
+    // are in memory before thread 0 bumps the counter; the last arriver reads them with cache-bypassing loads.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     uint32_t *ctr = &a.counters[((size_t)c.proj * a.groups + c.g) * c.G + c.og];
     if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = old == (uint32_t)(c.S - 1);
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = old == (uint32_t)(c.S - 1);
     }
     __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    for (int r = wave; r < a.rows; r += GEMV_WAVES) {
-        float v0 = 0.f, v1 = 0.f;
-        for (int s2 = 0; s2 < c.S; s2++) {
-            const float *pp = part + (((size_t)c.g * c.S + s2) * a.rows + r) * a.out + (size_t)c.og * 128;
-            v0 += __builtin_nontemporal_load(pp + lane);
-            v1 += __builtin_nontemporal_load(pp + lane + 64);
+    if (!*last_flag) return;
+    if (xcd_local) {
+        // This CU's L1 may hold lines of these partials from an earlier call: drop them, then read the XCD's L2.
+        asm volatile("buffer_inv sc0" ::: "memory");
+        for (int r = wave; r < a.rows; r += GEMV_WAVES) {
+            float v0 = 0.f, v1 = 0.f;
+            for (int s2 = 0; s2 < c.S; s2++) {
+                const float *pp = part + (((size_t)c.g * c.S + s2) * a.rows + r) * a.out + (size_t)c.og * 128;
+                v0 += pp[lane];
+                v1 += pp[lane + 64];
+            }
+            finish_block(a, c, r, v0, v1, lane);
         }
-        finish_block(a, c, r, v0, v1, lane);
+    } else {
+        for (int r = wave; r < a.rows; r += GEMV_WAVES) {
+            float v0 = 0.f, v1 = 0.f;
+            for (int s2 = 0; s2 < c.S; s2++) {
+                float *pp = part + (((size_t)c.g * c.S + s2) * a.rows + r) * a.out + (size_t)c.og * 128;
+                v0 += __hip_atomic_load(pp + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                v1 += __hip_atomic_load(pp + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            finish_block(a, c, r, v0, v1, lane);
+        }
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Per-rate decode constants for a ragged bank (hash rows and pair rows differ by rate; the window mask does not).
+template <int FAM>
+__device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
+    DecodeK k = a.k;
+    if constexpr (FAM == FAM_HASH || FAM == FAM_PAIR) table_row(a.table, n, k.mult, k.mask0, k.mask1, k.rot);
+    return k;
+}
+
+// N > 0: one rate for the launch; N == 0: the generic reader; N < 0: per-expert rate from the ragged meta table,
+// dispatched per workgroup.
+template <int FAM, int N, int RT, int PRO>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
+    GemvCtx c;
+    c.IT = a.in >> 4;
+    c.OT = a.out >> 4;
+    c.G = c.OT >> 3;
+    c.S = a.splits;
+    const int L = blockIdx.x;
+    if ((c.G & 7) == 0) {  // keep an output group's splits on one XCD (workgroups go round-robin over 8 XCDs)
+        const int xcd = L & 7, r = L >> 3;
+        c.og = (r / c.S) * 8 + xcd;
+        c.sp = r % c.S;
+    } else {
+        c.og = L / c.S;
+        c.sp = L % c.S;
+    }
+    c.g = blockIdx.y;
+    c.proj = blockIdx.z;
+    c.bank = a.bank_of ? (int)min(a.bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
+    c.KS = c.IT / c.S;
+    c.kt0 = c.sp * c.KS;
+
+    __shared__ __align__(16) uint16_t xs[RT][MAX_KSPAN];
+    __shared__ float red[GEMV_WAVES][RT][128];
+    __shared__ int last_flag;
+
+    if constexpr (N >= 0) {
+        const int n = N ? N : a.n;
+        const uint16_t *tb = a.trellis[c.proj] + (size_t)c.bank * c.IT * c.OT * n;
+        gemv_body<FAM, N, RT, PRO>(a, c, tb, n, a.k, xs, red, &last_flag);
+    } else {
+        const uint32_t *m = a.meta + (size_t)c.bank * 8;
+        const int n = (int)m[a.meta_col[c.proj]];
+        const uint16_t *tb = a.trellis[c.proj] + 2 * (size_t)m[4 + a.meta_col[c.proj]];
+        const DecodeK k = rate_constants<FAM>(a, n);
+        switch (n) {
+        case 16: gemv_body<FAM, 16, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
+        case 32: gemv_body<FAM, 32, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
+        case 48: gemv_body<FAM, 48, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
+        case 64: gemv_body<FAM, 64, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
+        default: gemv_body<FAM, 0, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
+        }
+    }
 }
 
 // Separate finish: one wave per (output group, row, group, projection).
@@ -342,7 +512,8 @@ static hipError_t launch_gemv_fam(const GemvArgs &a, hipStream_t s) {
 #define EXL3_CAT2(a, b) a##b
 #define EXL3_CAT(a, b) EXL3_CAT2(a, b)
 hipError_t EXL3_CAT(run_gemv_fam_, EXL3_GEMV_FAM)(int prologue, const GemvArgs &a, hipStream_t s) {
-    return prologue == PRO_MID ? launch_gemv_fam<EXL3_GEMV_FAM, PRO_MID>(a, s) : launch_gemv_fam<EXL3_GEMV_FAM, PRO_X>(a, s);
+    return prologue == PRO_MID ? launch_gemv_fam<EXL3_GEMV_FAM, PRO_MID>(a, s)
+                               : launch_gemv_fam<EXL3_GEMV_FAM, PRO_X>(a, s);
 }
 #endif
 

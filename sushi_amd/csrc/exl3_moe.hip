@@ -23,21 +23,22 @@ hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s) {
 constexpr int GEMV_MAX_KSPAN = 2048;
 
 int gemv_default_splits(int in, int out, int rows, int groups_times_proj) {
-    // Enough workgroups to have every CU's loads in flight (256 CUs), splits on whole Hadamard blocks.
+    // Splits cut k on whole Hadamard blocks.  A split of at most 16 k-tiles lets every wave issue all of its tile
+    // loads before the prologue (4 waves x 4 tiles); past that, more splits only add partial traffic unless the
+    // grid is still short of ~2 workgroups per CU (256 CUs).
     const int blocks = in / 128;
+    const int it = in / 16;
     const long G = (long)(out / 128) * groups_times_proj;
-    const long target = 1024;
-    int best = 1;
-    bool found = false;
+    const long target = 512;
+    int best = blocks;
     for (int s = 1; s <= blocks; s++) {
         if (blocks % s) continue;
-        if ((in / s) > GEMV_MAX_KSPAN) continue;
+        if (it / s > 16) continue;
         best = s;
-        found = true;
         if (G * s >= target) break;
     }
     (void)rows;
-    return found ? best : blocks;
+    return best;
 }
 
 __device__ __forceinline__ void store_out(void *y, int dt, size_t i, float v) {

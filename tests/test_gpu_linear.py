@@ -89,15 +89,44 @@ def test_gemv_split_and_finish_arms_agree(dev, splits, separate):
         del os.environ["EXL3_GEMV_SEPARATE_FINISH"]
 
 
+@pytest.mark.parametrize("rows", [2, 12])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_gemv_activation_dtypes(dev, dtype):
-    p, pd, x, xd = _case(dev, 13, 2, 256, 256, 64, dtype)
+def test_activation_dtypes(dev, dtype, rows):
+    p, pd, x, xd = _case(dev, 13, rows, 256, 256, 64, dtype)
     dec, odec = DECODES["mcg"]
     xo = xd.float().cpu()  # the oracle rounds its input to f16 as prepareInput does
     want = _oracle(p, xo, 256, 256, 64, odec)
+    y32 = exl3.linear(xd, pd, dec, out_dtype=torch.float32)  # the input dtype's own path, f32 out
+    assert max_abs_rel(y32.cpu().numpy(), want) < BAR
     y = exl3.linear(xd, pd, dec)
     assert y.dtype == dtype
-    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+    # a bf16 result carries its own rounding (2^-9 relative) on top of the f16 bar
+    bar = BAR + (2.0 ** -8 if dtype == torch.bfloat16 else 0.0)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < bar
+
+
+def test_arms_share_one_workspace(dev):
+    """GEMM and MoE scratch never lands on the GEMV's fused-finish counters: interleave the arms on one workspace."""
+    p, pd, x, xd = _case(dev, 17, 40, 1024, 1024, 64)
+    dec, odec = DECODES["mcg"]
+    want = _oracle(p, x, 1024, 1024, 64, odec)
+    for _ in range(3):
+        assert max_abs_rel(_run(pd, xd, dec), want) < BAR                      # GEMM arm (40 rows)
+        assert max_abs_rel(_run(pd, xd[:3].contiguous(), dec), want[:3]) < BAR  # GEMV arm, fused finish
+
+
+def test_fused_finish_repeated_across_shapes(dev):
+    """The single-launch finish (arrival counters, partials in the XCD's L2 or written through) stays correct over
+    back-to-back calls on one workspace, across shapes whose output groups map to different XCDs."""
+    cases = []
+    for seed, in_f, out_f in ((31, 4096, 4096), (32, 2048, 3584), (33, 1024, 384)):
+        p, pd, x, xd = _case(dev, seed, 1, in_f, out_f, 64)
+        cases.append((pd, xd, _oracle(p, x, in_f, out_f, 64, DECODES["mcg"][1])))
+    for _ in range(3):
+        for pd, xd, want in cases:
+            exl3.linear(xd, pd, DECODES["mcg"][0])  # queued back to back, no host sync in between
+        for pd, xd, want in cases:
+            assert max_abs_rel(_run(pd, xd, DECODES["mcg"][0]), want) < BAR
 
 
 def test_linear_grouped(dev):
