@@ -29,6 +29,22 @@ def _algorithmic_bytes(in_f: int, out_f: int, n: int, rows: int) -> int:
     return in_f * out_f * n // 128 + 2 * (in_f + out_f) + 2 * rows * (in_f + out_f)
 
 
+def _capture(calls, dev):
+    """One HIP graph holding `calls()` (captured on a side stream, outside any timed region)."""
+    import torch
+
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            calls()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    g.replay()
+    torch.cuda.synchronize()
+    return g
+
+
 def bench_linear(steps: int, warmup: int, graph_mode: bool = True):
     import torch
 
@@ -47,30 +63,24 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True):
     for i in range(warmup):
         exl3.linear(x, projs[i % COPIES], dec)
     torch.cuda.synchronize()
-    # The host side of a call (Python checks + ctypes) costs more than the kernel, so the calls are captured once,
-    # one per weight copy, into a HIP graph (outside the timed region) and the graph is replayed: the timed region
-    # then holds exactly `steps` library launches back to back, as a native caller would issue them.
-    graph = None
+    # The host side of a call (Python checks + ctypes) costs more than the kernel, so the calls are captured, one per
+    # weight copy, into HIP graphs (outside the timed region) and replayed: the timed region then holds exactly
+    # `steps` library launches back to back, as a native caller would issue them.
+    full = tail = None
     if graph_mode:
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=side):
-                for i in range(COPIES):
-                    y = exl3.linear(x, projs[i], dec)
-        torch.cuda.current_stream(dev).wait_stream(side)
-        graph.replay()
-        torch.cuda.synchronize()
-        steps = (steps + COPIES - 1) // COPIES * COPIES
+        full = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(COPIES)], dev)
+        if steps % COPIES:
+            tail = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(steps % COPIES)], dev)
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(stream)
-    if graph is not None:
+    if graph_mode:
         for _ in range(steps // COPIES):
-            graph.replay()
+            full.replay()
+        if tail is not None:
+            tail.replay()
     else:
         for i in range(steps):
             exl3.linear(x, projs[i % COPIES], dec)
@@ -82,9 +92,12 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True):
     return dict(wall_s=wall, event_ms=ev_ms, bytes=bytes_per_call, rows=rows, y=y, steps=steps)
 
 
-def bench_moe(steps: int, warmup: int):
-    """configs[3] at batch 1: E=256 routed + shared, hidden 2048, inter 768, K2, top-8; us per token."""
-    import numpy as np
+def bench_moe(batch: int, layers: int = 16, replays: int = 8):
+    """E=256 routed + shared, hidden 2048, inter 768, K2 MCG, top-8; microseconds per token.
+
+    A dependent chain of `layers` MoE layers (each layer's output is the next layer's input, the reference's
+    bench_util.zig:20-58 method), captured once as a HIP graph and replayed; every layer has its own routing so the
+    distinct experts hit change from layer to layer."""
     import torch
 
     from sushi_amd import exl3, synth
@@ -93,27 +106,62 @@ def bench_moe(steps: int, warmup: int):
     E, hidden, inter, n, k = 256, 2048, 768, 32, 8
     bank = synth.bank(3, "c4", E, hidden, inter, n, device=dev)
     shared = synth.bank(3, "c4.shared", 1, hidden, inter, n, device=dev)
-    x = synth.normal(3, "c4.x", (1, hidden), device=dev)
-    logits = synth.normal(3, "c4.logits", (1, E), dtype=torch.float32).to(dev)
-    inds, scores = exl3.moe_routing_chain(logits, k)
-    sh_inds = torch.zeros(1, 1, dtype=torch.int32, device=dev)
-    sh_sc = torch.ones(1, 1, dtype=torch.float32, device=dev)
+    x0 = synth.normal(3, f"c4.x{batch}", (batch, hidden), device=dev)
+    routes = []
+    for layer in range(layers):
+        logits = synth.normal(3, f"c4.logits{batch}.{layer}", (batch, E), dtype=torch.float32).to(dev)
+        routes.append(exl3.moe_routing_chain(logits, k))
+    sh_inds = torch.zeros(batch, 1, dtype=torch.int32, device=dev)
+    sh_sc = torch.ones(batch, 1, dtype=torch.float32, device=dev)
 
-    def layer():
-        s = exl3.moe(x, shared, sh_inds, sh_sc, exl3.MCG)  # the shared expert: a one-expert chain
-        return exl3.moe_with_shared(x, bank, inds, scores, exl3.MCG, False, s)
+    def chain():
+        x = x0
+        for inds, scores in routes:
+            s = exl3.moe(x, shared, sh_inds, sh_sc, exl3.MCG)  # the shared expert: a one-expert chain
+            x = exl3.moe_with_shared(x, bank, inds, scores, exl3.MCG, False, s)
+        return x
 
-    for _ in range(warmup):
-        layer()
+    chain()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        layer()
+    g = _capture(chain, dev)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    distinct = len(set(inds.flatten().tolist()))
-    per_expert = 3 * (hidden * inter * n // 16 + 2 * (hidden + inter))
-    return dict(us_per_token=wall / steps * 1e6, bytes=(distinct + 1) * per_expert, distinct=distinct)
+    layer_us = e0.elapsed_time(e1) * 1e3 / (replays * layers)
+    distinct = sum(len(set(i.flatten().tolist())) for i, _ in routes) / layers
+    per_expert = 3 * (hidden * inter * n // 128 + 2 * (hidden + inter))
+    return dict(batch=batch, layer_us=layer_us, us_per_token=layer_us / batch, distinct=distinct,
+                bytes=(distinct + 1) * per_expert)
+
+
+def copy_calibration(mib: int, reps: int = 4):
+    """A plain device-to-device copy of `mib` MiB, `reps` times: the reference kernel whose FETCH_SIZE/WRITE_SIZE
+    counters calibrate the HBM-traffic figures of the GEMV (expected: exactly `mib` MiB read and written)."""
+    import torch
+
+    src = torch.empty(mib << 19, dtype=torch.float16, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def _profiled_traffic():
+    """HBM bytes per GEMV launch from the committed counter summary (two rocprofv3 --pmc passes, FETCH_SIZE then
+    WRITE_SIZE, scaled by the same counters read over a plain copy kernel), or None if it is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_c1_3inst_k4_b1_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(sample_calls: int):
@@ -142,22 +190,27 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--cpu-sample", type=int, default=40)
+    ap.add_argument("--cpu-sample", type=int, default=120)
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="issue every call from Python instead of a HIP graph")
+    ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
               "note (expert/output-tile sharding), not a runnable path", file=sys.stderr)
         return 2
 
+    if args.copy_calibration > 0:
+        copy_calibration(args.copy_calibration)
     lin = bench_linear(args.steps, args.warmup, not args.no_graph)
     steps = lin["steps"]
     ms_per_step = lin["wall_s"] / steps * 1e3
     value = lin["bytes"] / (lin["wall_s"] / steps) / 1e9
     launch_s = lin["event_ms"] / 1e3 / steps
     achieved = lin["bytes"] / launch_s / 1e9
-    moe = None if args.no_moe else bench_moe(max(50, args.steps // 10), 10)
+    moe = [] if args.no_moe else [bench_moe(int(b)) for b in args.moe_batches.split(",") if b]
     cpu = cpu_baseline(args.cpu_sample) if args.cpu_sample > 0 else None
     out = {
         "metric": "effective HBM GB/s + tok/s, EXL3 K=4 4096x4096 GEMV b=1; MoE layer us/token",
@@ -175,15 +228,21 @@ def main() -> int:
         "config": {"workload": "EXL3 dense linear 4096x4096, K=4 (n=64), 3INST codebook, 16x16 tiles, batch 1, "
                                "64 rotating weight copies", "global_batch": 1, "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1.0 / (lin["wall_s"] / steps), 1),
-        "launch_mode": "hip graph of 64 library calls, replayed" if not args.no_graph else "python loop",
+        "launch_mode": "hip graphs of library calls (64 weight copies), replayed" if not args.no_graph else "python loop",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _profiled_traffic(),
+                     "algorithmic_bytes": lin["bytes"], "launch_us": round(launch_s * 1e6, 3)},
         "cpu_baseline": cpu,
     }
     if moe:
-        out["moe_layer"] = {"config": "E=256 routed + 1 shared, hidden 2048, inter 768, K2 MCG, top-8, batch 1",
-                            "us_per_token": round(moe["us_per_token"], 3), "distinct_experts": moe["distinct"],
-                            "effective_GBps": round(moe["bytes"] / (moe["us_per_token"] * 1e-6) / 1e9, 2)}
+        out["moe_layer"] = {"config": "E=256 routed + 1 shared, hidden 2048, inter 768, K2 MCG, top-8; dependent "
+                                      "chain of 16 layers in a HIP graph",
+                            "us_per_token": round(moe[0]["us_per_token"], 3),
+                            "batches": [{"batch": m["batch"], "layer_us": round(m["layer_us"], 3),
+                                         "us_per_token": round(m["us_per_token"], 3),
+                                         "distinct_experts": round(m["distinct"], 2),
+                                         "effective_GBps": round(m["bytes"] / (m["layer_us"] * 1e-6) / 1e9, 2)}
+                                        for m in moe]}
     print(json.dumps(out))
     return 0
 
