@@ -45,8 +45,10 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // Every workspace starts with a fixed region of fused-finish arrival counters.  Only the fused-finish GEMV touches
 // it, and every such launch leaves its counters at zero again, so the region stays valid across calls of any arm
 // (exl3_workspace_init zeroes it once after allocation).  Scratch of every arm begins after it.
-constexpr size_t kCounterSlots = 65536;
-constexpr size_t kCounterBytes = kCounterSlots * sizeof(uint32_t);
+// Each counter owns a 128-byte line (COUNTER_STRIDE words): the splits of different output groups then never
+// contend for one line in the L2's atomic unit.
+constexpr size_t kCounterBytes = size_t(1) << 20;
+constexpr size_t kCounterSlots = kCounterBytes / (sizeof(uint32_t) * COUNTER_STRIDE);
 
 bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
 
@@ -210,7 +212,7 @@ MoePlan plan_moe(int nslots, int hidden, int inter) {
     return p;
 }
 
-constexpr int kReduceMaxTopk = 32;  // REDUCE_MAX_TOPK, expert_exl3_kernels.zig:2562
+constexpr int kReduceMaxTopk = kMoeReduceMaxTopk;  // REDUCE_MAX_TOPK, expert_exl3_kernels.zig:2562
 
 int32_t moe_common_checks(int32_t x_dtype, int32_t y_dtype, int32_t rows, int32_t hidden, int32_t inter,
                           int32_t topk, int32_t clamp_limit) {

@@ -117,20 +117,58 @@ __device__ __forceinline__ uint32_t mul16x32(uint32_t x, uint32_t mh, uint32_t m
     return p;
 }
 
-// 3INST's LCG step c*A + B (mod 2^32) in two full-rate ops.  `q` must hold lo16(B) in its low half: v_mad_u16 with
-// op_sel dst=1 writes lo16(c*hi16(A) + hi16(B)) into the high half and keeps the low half.
+// The hash products of the GEMV hot loop as two full-rate steps, so a tile's codewords can run each step as one
+// batch (no instruction then reads the result of the one just before it, and the hazard recognizer inserts no wait
+// states):
+//   MCG / hash rows: step 1  t = lo16(c * hi16(M)) << 16       v_mul_lo_u16 (SDWA, high half written, low cleared)
+//                    step 2  t = c * lo16(M) + t               v_mad_u32_u16, in place     -> c*M mod 2^32
+//   3INST (LCG):     step 1  p = c * lo16(A) + B               v_mad_u32_u16
+//                    step 2  p.hi = lo16(c * hi16(A) + p.hi)   v_mad_u16 op_sel (high half written, low kept)
+//                                                              -> c*A + B mod 2^32
 constexpr uint32_t LCG_A = 89226354u, LCG_B = 64248484u;
-template <bool HI>
-__device__ __forceinline__ uint32_t lcg16(uint32_t x, uint32_t &q) {
+
+template <int FAM>
+__device__ __forceinline__ uint32_t hash_mult(const DecodeK &k) {
+    return FAM == FAM_MCG ? 0xCBAC1FEDu : FAM == FAM_3INST ? LCG_A : k.mult;
+}
+
+template <int FAM, bool HI>
+__device__ __forceinline__ uint32_t hash_step1(uint32_t x, const DecodeK &k) {
+    const uint32_t m = hash_mult<FAM>(k);
     uint32_t p;
-    if constexpr (HI) {
-        asm("v_mad_u16 %0, %1, %2, %3 op_sel:[1,0,0,1]" : "+v"(q) : "v"(x), "v"(LCG_A >> 16), "v"(LCG_B >> 16));
-        asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(x), "v"(LCG_A & 0xFFFFu), "v"(q));
+    if constexpr (FAM == FAM_3INST) {
+        if constexpr (HI)
+            asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(x), "v"(m & 0xFFFFu), "v"(LCG_B));
+        else
+            asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(x), "v"(m & 0xFFFFu), "v"(LCG_B));
     } else {
-        asm("v_mad_u16 %0, %1, %2, %3 op_sel:[0,0,0,1]" : "+v"(q) : "v"(x), "v"(LCG_A >> 16), "v"(LCG_B >> 16));
-        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(x), "v"(LCG_A & 0xFFFFu), "v"(q));
+        if constexpr (HI)
+            asm("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0"
+                : "=v"(p) : "v"(x), "v"(m >> 16));
+        else
+            asm("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_0"
+                : "=v"(p) : "v"(x), "v"(m >> 16));
     }
     return p;
+}
+
+template <int FAM, bool HI>
+__device__ __forceinline__ void hash_step2(uint32_t x, const DecodeK &k, uint32_t &p) {
+    const uint32_t m = hash_mult<FAM>(k);
+    if constexpr (FAM == FAM_3INST) {
+        if constexpr (HI) asm("v_mad_u16 %0, %1, %2, %0 op_sel:[1,0,1,1]" : "+v"(p) : "v"(x), "v"(m >> 16));
+        else asm("v_mad_u16 %0, %1, %2, %0 op_sel:[0,0,1,1]" : "+v"(p) : "v"(x), "v"(m >> 16));
+    } else {
+        if constexpr (HI) asm("v_mad_u32_u16 %0, %1, %2, %0 op_sel:[1,0,0,0]" : "+v"(p) : "v"(x), "v"(m & 0xFFFFu));
+        else asm("v_mad_u32_u16 %0, %1, %2, %0" : "+v"(p) : "v"(x), "v"(m & 0xFFFFu));
+    }
+}
+
+// The masked product: the f16 pair whose sum is the weight (unscaled for hash rows).
+template <int FAM>
+__device__ __forceinline__ uint32_t hash_halves(uint32_t p, const DecodeK &k) {
+    if constexpr (FAM == FAM_HASH) return p & k.mask0;
+    else return (p & 0x8FFF8FFFu) ^ 0x3B603B60u;
 }
 
 // Packed f16 (lo = h0.lo + h0.hi, hi = h1.lo + h1.hi): two SDWA adds, the second writing the high half in place.
@@ -141,19 +179,6 @@ __device__ __forceinline__ uint32_t pack_sums(uint32_t h0, uint32_t h1) {
     asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
         : "+v"(w) : "v"(h1));
     return w;
-}
-
-// The pre-sum halves of one codeword (the f16 pair whose sum is the weight, unscaled for hash masks).
-// `q` is the LCG scratch of lcg16; `k` carries the hash row.
-template <int FAM, bool HI>
-__device__ __forceinline__ uint32_t halves_of(uint32_t x, const DecodeK &k, uint32_t &q) {
-    if constexpr (FAM == FAM_MCG) {
-        return (mul16x32<HI>(x, 0xCBACu, 0x1FEDu) & 0x8FFF8FFFu) ^ 0x3B603B60u;
-    } else if constexpr (FAM == FAM_3INST) {
-        return (lcg16<HI>(x, q) & 0x8FFF8FFFu) ^ 0x3B603B60u;
-    } else {  // FAM_HASH
-        return mul16x32<HI>(x, k.mult >> 16, k.mult & 0xFFFFu) & k.mask0;
-    }
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -220,7 +245,26 @@ __device__ __forceinline__ uint32_t codeword_at(const uint32_t *__restrict__ wor
 // Wave64 128-point Walsh-Hadamard: lane l holds v0 = x[l], v1 = x[l + 64].  Unnormalised (the caller scales by
 // 1/sqrt(128)).  Matches hadamard128 (expert_exl3.zig:400-414) up to f32 summation order.
 
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+// The value of lane (lane ^ H): DPP quad permutes for H = 1, 2 (plain VALU), the LDS crossbar's swizzle (bitmask
+// mode, and 0x1F / xor H, within each 32-lane half) for H = 4..16, one bpermute for H = 32.
+template <int H>
+__device__ __forceinline__ float xor_lane(float v, int lane) {
+    const int b = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (H == 1) r = __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+    else if constexpr (H == 2) r = __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else if constexpr (H <= 16) r = __builtin_amdgcn_ds_swizzle(b, 0x1F | (H << 10));
+    else r = __builtin_amdgcn_ds_bpermute((lane ^ H) << 2, b);
+    return __builtin_bit_cast(float, r);
+}
+
+template <int H>
+__device__ __forceinline__ void fwht_stage(float &v0, float &v1, int lane) {
+    const float p0 = xor_lane<H>(v0, lane), p1 = xor_lane<H>(v1, lane);
+    const bool up = (lane & H) != 0;
+    v0 = up ? (p0 - v0) : (v0 + p0);
+    v1 = up ? (p1 - v1) : (v1 + p1);
+}
 
 __device__ __forceinline__ void fwht128_wave(float &v0, float &v1, int lane) {
     {
@@ -228,16 +272,44 @@ __device__ __forceinline__ void fwht128_wave(float &v0, float &v1, int lane) {
         v0 = a + b;
         v1 = a - b;
     }
-#pragma unroll
-    for (int h = 32; h >= 1; h >>= 1) {
-        float p0 = shfl_xor_f(v0, h), p1 = shfl_xor_f(v1, h);
-        bool up = (lane & h) != 0;
-        v0 = up ? (p0 - v0) : (v0 + p0);
-        v1 = up ? (p1 - v1) : (v1 + p1);
-    }
+    fwht_stage<32>(v0, v1, lane);
+    fwht_stage<16>(v0, v1, lane);
+    fwht_stage<8>(v0, v1, lane);
+    fwht_stage<4>(v0, v1, lane);
+    fwht_stage<2>(v0, v1, lane);
+    fwht_stage<1>(v0, v1, lane);
 }
 
 constexpr float HAD_SCALE = 0.08838834764831845f;
+
+// Sum over s = 0..S-1 (in that order) of the f32 planes p + s * stride at (lane, lane + 64).  Loads go out eight
+// planes at a time before any add: a loop that adds as it loads waits out one memory round trip per plane.
+// BYPASS reads with system-scope atomic loads (data another workgroup wrote through to memory).
+template <bool BYPASS>
+__device__ __forceinline__ void sum_planes(const float *p, size_t stride, int S, int lane, float &v0, float &v1) {
+    constexpr int CH = 8;
+    v0 = v1 = 0.f;
+    for (int s0 = 0; s0 < S; s0 += CH) {
+        float t0[CH], t1[CH];
+#pragma unroll
+        for (int q = 0; q < CH; q++) {
+            const float *pp = p + (size_t)min(s0 + q, S - 1) * stride;
+            if constexpr (BYPASS) {
+                t0[q] = __hip_atomic_load(pp + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                t1[q] = __hip_atomic_load(pp + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            } else {
+                t0[q] = pp[lane];
+                t1[q] = pp[lane + 64];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < CH; q++) {
+            const bool in = s0 + q < S;
+            v0 += in ? t0[q] : 0.f;
+            v1 += in ? t1[q] : 0.f;
+        }
+    }
+}
 
 // ------------------------------------------------------------------------------------------------------------
 // Activation dtypes at the boundary.

@@ -53,17 +53,19 @@ __device__ __forceinline__ float silu(float g) {
 }
 
 struct GemvCtx {
-    int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G;
+    int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div;
+    const uint16_t *suh, *svh;  // this projection's banks (selected once: an indexed kernel-argument read would be
+    float *part;                // a dependent scalar load)
+    float sv0, sv1;             // svh of this lane's two outputs, fetched at entry for the finish
 };
 
 // Output FWHT + svh for one row of a 128-output block held as (v0 = col lane, v1 = col lane + 64).
 __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c, int rho, float v0, float v1,
                                              int lane) {
     fwht128_wave(v0, v1, lane);
-    const size_t sv = (size_t)c.bank * a.out + (size_t)c.og * 128;
     const size_t yo = ((size_t)c.g * a.rows + rho) * a.out + (size_t)c.og * 128;
-    store_y(a.y, a.y_dtype, yo + lane, v0 * HAD_SCALE * h2f(a.svh[c.proj][sv + lane]));
-    store_y(a.y, a.y_dtype, yo + lane + 64, v1 * HAD_SCALE * h2f(a.svh[c.proj][sv + lane + 64]));
+    store_y(a.y, a.y_dtype, yo + lane, v0 * HAD_SCALE * c.sv0);
+    store_y(a.y, a.y_dtype, yo + lane + 64, v1 * HAD_SCALE * c.sv1);
 }
 
 // Codeword v of the lane as (window index, high half?): for K = 1, 2, 4 the window ending at codeword v + 16/K
@@ -76,13 +78,17 @@ struct Pairing {
     __device__ static constexpr int win(int v) { return hi(v) ? v + STEP : v; }
 };
 
+// A scheduling fence: nothing moves across it, so each phase below stays one batch of independent instructions.
+__device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 // The 32 weights of one tile chunk (lane-owned columns j and j+8), dotted into acc0 (column j) / acc1 (column j+8).
-// Written in phases (windows, products, masks, low sums, high sums, dots) so each partial-register write has many
-// independent instructions before its reader and the hazard recognizer inserts no wait states.
+// Written in fenced phases (windows, product step 1, step 2, masks, low sums, high sums, dots): within a phase no
+// instruction depends on another, so no result is read by the instruction right after it and the hazard recognizer
+// inserts no wait states (gfx950 needs one between a 16-bit-lane or SDWA write and its reader).
 template <int FAM, int N, int RT, bool MASKED>
 __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint4 (&X)[RT],
-                                            const uint4 (&Y)[RT], const DecodeK &k, uint32_t (&q)[32],
-                                            float (&acc0)[RT], float (&acc1)[RT]) {
+                                            const uint4 (&Y)[RT], const DecodeK &k, float (&acc0)[RT],
+                                            float (&acc1)[RT]) {
     using P = Pairing<N>;
     uint32_t win[32];
 #pragma unroll
@@ -119,17 +125,30 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
         }
     } else {
         uint32_t h[32];
+        phase_fence();
 #pragma unroll
         for (int v = 0; v < 32; v++)
-            h[v] = P::hi(v) ? halves_of<FAM, true>(win[P::win(v)], k, q[v]) : halves_of<FAM, false>(win[P::win(v)], k, q[v]);
+            h[v] = P::hi(v) ? hash_step1<FAM, true>(win[P::win(v)], k) : hash_step1<FAM, false>(win[P::win(v)], k);
+        phase_fence();
+#pragma unroll
+        for (int v = 0; v < 32; v++) {
+            if (P::hi(v)) hash_step2<FAM, true>(win[P::win(v)], k, h[v]);
+            else hash_step2<FAM, false>(win[P::win(v)], k, h[v]);
+        }
+        phase_fence();
+#pragma unroll
+        for (int v = 0; v < 32; v++) h[v] = hash_halves<FAM>(h[v], k);
+        phase_fence();
 #pragma unroll
         for (int i = 0; i < 16; i++)
             asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
                 : "=v"(w[i]) : "v"(h[2 * i]));
+        phase_fence();
 #pragma unroll
         for (int i = 0; i < 16; i++)
             asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
                 : "+v"(w[i]) : "v"(h[2 * i + 1]));
+        phase_fence();
     }
     // pair i = (u, u+1), u = 2i = 8qq + 2p: p = 0/1 -> column j rows 2qq(+8), p = 2/3 -> column j+8
 #pragma unroll
@@ -145,39 +164,81 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
     }
 }
 
-// The prologue's input loads for a wave's first jobs, issued ahead of the tile loads: loads retire in order, so an
-// input load issued behind 16 KiB of tile loads would hold the prologue back until all of them had landed.
-constexpr int PRE_JOBS = 4;
+// x[i] as f32 from an f16 / bf16 / f32 array without branching on the dtype: one 32-bit load of the aligned word
+// that holds the element, then selects.  (A branch per dtype joins through a register copy, and that copy makes the
+// load wait for its data right there.)  Rows are multiples of 128 elements, so the word never leaves the row's span
+// when the array starts 4-byte aligned; a 2-byte aligned start reads at most 2 bytes past the end of the array.
+__device__ __forceinline__ float load_x_nb(const void *x, int dt, size_t i) {
+    const bool wide = dt == DT_F32;
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(x) + (wide ? i * 4 : i * 2);
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(addr & ~(uintptr_t)3);
+    const uint32_t h = (addr & 2) ? (w >> 16) : (w & 0xFFFFu);
+    const float narrow = dt == DT_F16 ? h2f((uint16_t)h) : __uint_as_float(h << 16);
+    return wide ? __uint_as_float(w) : narrow;
+}
+
+// The prologue's input loads for a wave's first jobs, issued ahead of the tile loads (loads retire in order, so an
+// input load issued behind 16 KiB of tile loads would hold the prologue back until all of them had landed).  Loads
+// are unconditional (a job past the end re-reads job 0 and is then discarded): no branch, so no early wait.
+template <int RT>
 struct PrologueRegs {
-    float x0[PRE_JOBS], x1[PRE_JOBS], s0[PRE_JOBS], s1[PRE_JOBS];
+    static constexpr int JOBS = RT < 2 ? 1 : RT / 2;  // jobs per wave with a split of <= 16 k-tiles (2 blocks) per row
+    float x0[JOBS], x1[JOBS], s0[JOBS], s1[JOBS];
 };
 
-template <int PRO>
-__device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx &c, int RT, int wave, int lane,
-                                               PrologueRegs &pr) {
+template <int PRO, int RT>
+__device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx &c, int wave, int lane,
+                                               PrologueRegs<RT> &pr) {
     if constexpr (PRO == PRO_X) {
         const int nblk = c.KS >> 3;
 #pragma unroll
-        for (int i = 0; i < PRE_JOBS; i++) {
-            const int job = wave + GEMV_WAVES * i;
-            const int rho = job / nblk, b = job - rho * nblk;
-            pr.x0[i] = pr.x1[i] = pr.s0[i] = pr.s1[i] = 0.f;
-            if (job < nblk * RT && rho < a.rows) {
-                const int kb = c.kt0 * 16 + b * 128;
-                const size_t si = (size_t)c.bank * a.in + kb;
-                const size_t xi = ((size_t)(c.g / a.x_div) * a.rows + rho) * a.in + kb;
-                pr.x0[i] = load_x(a.x, a.x_dtype, xi + lane);
-                pr.x1[i] = load_x(a.x, a.x_dtype, xi + lane + 64);
-                pr.s0[i] = h2f(a.suh[c.proj][si + lane]);
-                pr.s1[i] = h2f(a.suh[c.proj][si + lane + 64]);
+        for (int i = 0; i < PrologueRegs<RT>::JOBS; i++) {
+            int job = wave + GEMV_WAVES * i;
+            int rho = job / nblk, b = job - rho * nblk;
+            if (!(job < nblk * RT && rho < a.rows)) rho = b = 0;
+            const int kb = c.kt0 * 16 + b * 128;
+            const size_t si = (size_t)c.bank * a.in + kb;
+            const size_t xi = ((size_t)(c.g / c.x_div) * a.rows + rho) * a.in + kb;
+            pr.x0[i] = load_x_nb(a.x, a.x_dtype, xi + lane);
+            pr.x1[i] = load_x_nb(a.x, a.x_dtype, xi + lane + 64);
+            pr.s0[i] = h2f(c.suh[si + lane]);
+            pr.s1[i] = h2f(c.suh[si + lane + 64]);
+        }
+    }
+}
+
+// Sums the gate and up planes of one 128-block over the previous launch's k splits, issuing a chunk of loads before
+// any add (a loop that adds as it loads would wait out one memory round trip per split).
+constexpr int MID_CHUNK = 8;
+__device__ __forceinline__ void mid_planes(const GemvArgs &a, const GemvCtx &c, int kb, int lane, float (&w)[2][2]) {
+    w[0][0] = w[0][1] = w[1][0] = w[1][1] = 0.f;
+    for (int s0 = 0; s0 < a.mid_splits; s0 += MID_CHUNK) {
+        float t[2][2][MID_CHUNK];
+#pragma unroll
+        for (int pj = 0; pj < 2; pj++) {
+#pragma unroll
+            for (int q = 0; q < MID_CHUNK; q++) {
+                const int s2 = min(s0 + q, a.mid_splits - 1);
+                const float *pp = a.mid_part[pj] + ((size_t)c.g * a.mid_splits + s2) * a.in + kb;
+                t[pj][0][q] = pp[lane];
+                t[pj][1][q] = pp[lane + 64];
+            }
+        }
+#pragma unroll
+        for (int pj = 0; pj < 2; pj++) {
+#pragma unroll
+            for (int q = 0; q < MID_CHUNK; q++) {
+                const bool in = s0 + q < a.mid_splits;
+                w[pj][0] += in ? t[pj][0][q] : 0.f;
+                w[pj][1] += in ? t[pj][1][q] : 0.f;
             }
         }
     }
 }
 
-template <int PRO>
-__device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, int RT, uint16_t (*xs)[MAX_KSPAN],
-                                         int wave, int lane, const PrologueRegs &pr) {
+template <int PRO, int RT>
+__device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[MAX_KSPAN], int wave,
+                                         int lane, const PrologueRegs<RT> &pr) {
     const int nblk = c.KS >> 3;
     for (int job = wave; job < nblk * RT; job += GEMV_WAVES) {
         const int rho = job / nblk, b = job - rho * nblk;
@@ -187,24 +248,21 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, in
         if (rho < a.rows) {
             const size_t si = (size_t)c.bank * a.in + kb;
             if constexpr (PRO == PRO_X) {  // prepareInput (expert_exl3.zig:490-501)
-                if (i < PRE_JOBS) {
+                if (i < PrologueRegs<RT>::JOBS) {
                     v0 = f16r(pr.x0[i]) * pr.s0[i];
                     v1 = f16r(pr.x1[i]) * pr.s1[i];
                 } else {
-                    const size_t xi = ((size_t)(c.g / a.x_div) * a.rows + rho) * a.in + kb;
-                    v0 = f16r(load_x(a.x, a.x_dtype, xi + lane)) * h2f(a.suh[c.proj][si + lane]);
-                    v1 = f16r(load_x(a.x, a.x_dtype, xi + lane + 64)) * h2f(a.suh[c.proj][si + lane + 64]);
+                    const size_t xi = ((size_t)(c.g / c.x_div) * a.rows + rho) * a.in + kb;
+                    v0 = f16r(load_x_nb(a.x, a.x_dtype, xi + lane)) * h2f(c.suh[si + lane]);
+                    v1 = f16r(load_x_nb(a.x, a.x_dtype, xi + lane + 64)) * h2f(c.suh[si + lane + 64]);
                 }
             } else {  // the SwiGLU mid of the decode chain (DOWN_FUSED_SOURCE prologue, :1838-1920)
+                float w[2][2];
+                mid_planes(a, c, kb, lane, w);
                 float gv[2], uv[2];
 #pragma unroll
                 for (int pj = 0; pj < 2; pj++) {
-                    float w0 = 0.f, w1 = 0.f;
-                    for (int s2 = 0; s2 < a.mid_splits; s2++) {
-                        const float *pp = a.mid_part[pj] + ((size_t)c.g * a.mid_splits + s2) * a.in + kb;
-                        w0 += pp[lane];
-                        w1 += pp[lane + 64];
-                    }
+                    float w0 = w[pj][0], w1 = w[pj][1];
                     fwht128_wave(w0, w1, lane);
                     w0 *= HAD_SCALE * h2f(a.mid_svh[pj][si + lane]);
                     w1 *= HAD_SCALE * h2f(a.mid_svh[pj][si + lane + 64]);
@@ -223,8 +281,8 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, in
                         uv[i] = fminf(fmaxf(uv[i], -a.clamp_limit), a.clamp_limit);
                     }
                 }
-                v0 = silu(gv[0]) * uv[0] * h2f(a.suh[c.proj][si + lane]);
-                v1 = silu(gv[1]) * uv[1] * h2f(a.suh[c.proj][si + lane + 64]);
+                v0 = silu(gv[0]) * uv[0] * h2f(c.suh[si + lane]);
+                v1 = silu(gv[1]) * uv[1] * h2f(c.suh[si + lane + 64]);
             }
             fwht128_wave(v0, v1, lane);
             v0 *= HAD_SCALE;
@@ -247,43 +305,39 @@ __device__ __forceinline__ void load_x_frag(const uint16_t (*xs)[MAX_KSPAN], int
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 template <int FAM, int N, int RT, int PRO>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
-                                          int n, const DecodeK &k, uint16_t (*xs)[MAX_KSPAN], float (*red)[RT][128],
-                                          int *last_flag) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                          int n, const DecodeK &k, uint16_t (*xs)[MAX_KSPAN], float (*red)[RT][128]) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
     const int o = lane >> 3, j = lane & 7;
     float acc0[RT], acc1[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
-    uint32_t q[32];  // 3INST's per-codeword LCG scratch: the low half holds lo16(B) for good
-#pragma unroll
-    for (int i = 0; i < 32; i++) q[i] = LCG_B & 0xFFFFu;
 
     if constexpr (N != 0) {
         constexpr int AW = LaneBits<N>::AW;
-        const int ntiles = (c.KS - wave + GEMV_WAVES - 1) / GEMV_WAVES;  // this wave's k-tiles: wave, wave+4, ...
-        PrologueRegs pr;
-        prologue_fetch<PRO>(a, c, RT, wave, lane, pr);
+        // This wave's k-tiles are wave, wave + 4, ...; a split spans whole 128-blocks (8 k-tiles), so every wave has
+        // at least two.  The first TPW loads are issued unconditionally (a wave with fewer tiles re-reads its last
+        // one), so the compiler counts them and each tile's decode waits only for that tile's own loads.
+        const int ntiles = (c.KS - wave + GEMV_WAVES - 1) / GEMV_WAVES;
+        PrologueRegs<RT> pr;
+        prologue_fetch<PRO, RT>(a, c, wave, lane, pr);
         uint32_t Aw[TPW][AW];
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
-            if (t < ntiles) {
-                const int tk = c.kt0 + wave + GEMV_WAVES * t;
-                load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
-                                   Aw[t]);
-            }
+            const int tk = c.kt0 + wave + GEMV_WAVES * min(t, ntiles - 1);
+            load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
+                               Aw[t]);
         }
-        prologue<PRO>(a, c, RT, xs, wave, lane, pr);
+        prologue<PRO, RT>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
         for (int t0 = 0; t0 < ntiles; t0 += TPW) {
             if (t0 > 0) {  // splits longer than TPW tiles per wave: load the next batch in place
 #pragma unroll
                 for (int t = 0; t < TPW; t++) {
-                    if (t0 + t < ntiles) {
-                        const int tk = c.kt0 + wave + GEMV_WAVES * (t0 + t);
-                        load_lane_words<N>(
-                            reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j, Aw[t]);
-                    }
+                    const int tk = c.kt0 + wave + GEMV_WAVES * min(t0 + t, ntiles - 1);
+                    load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n),
+                                       j, Aw[t]);
                 }
             }
 #pragma unroll
@@ -291,15 +345,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
                 if (t0 + t < ntiles) {
                     uint4 X[RT], Y[RT];
                     load_x_frag<RT>(xs, wave + GEMV_WAVES * (t0 + t), X, Y);
-                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], X, Y, k, q, acc0, acc1);
-                    else decode_tile<FAM, N, RT, false>(Aw[t], X, Y, k, q, acc0, acc1);
+                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], X, Y, k, acc0, acc1);
+                    else decode_tile<FAM, N, RT, false>(Aw[t], X, Y, k, acc0, acc1);
                 }
             }
         }
     } else {  // any other rate: the generic reader (runtime funnel per codeword)
-        PrologueRegs pr;
-        prologue_fetch<PRO>(a, c, RT, wave, lane, pr);
-        prologue<PRO>(a, c, RT, xs, wave, lane, pr);
+        PrologueRegs<RT> pr;
+        prologue_fetch<PRO, RT>(a, c, wave, lane, pr);
+        prologue<PRO, RT>(a, c, xs, wave, lane, pr);
         __syncthreads();
         for (int kk = wave; kk < c.KS; kk += GEMV_WAVES) {
             const int tk = c.kt0 + kk;
@@ -333,67 +387,67 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
     }
     __syncthreads();
     const bool direct = c.S == 1 && !a.partial_only;
-    // An output group's splits share one XCD (and so one L2) when the workgroup remap applies (G % 8 == 0): its
-    // partials then meet in that L2.  Otherwise they are written through to memory.
-    const bool xcd_local = (c.G & 7) == 0;
-    float *part = a.partial[c.proj];
-    for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
-        const int r = idx >> 7, col = idx & 127;
-        float s = 0.f;
-#pragma unroll
-        for (int w = 0; w < GEMV_WAVES; w++) s += red[w][r][col];
-        s *= a.out_scale;
-        if (direct) {
-            red[0][r][col] = s;
-        } else if (r < a.rows) {
-            float *dst = part + (((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out + (size_t)c.og * 128 + col;
-            if (a.partial_only || xcd_local) *dst = s;  // L1 is write-through: the store lands in the XCD's L2
-            else __hip_atomic_store(dst, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // write-through to memory
-        }
-    }
     if (direct) {
+        for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
+            const int r = idx >> 7, col = idx & 127;
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < GEMV_WAVES; w++) s += red[w][r][col];
+            red[0][r][col] = s * a.out_scale;
+        }
         __syncthreads();
         for (int r = wave; r < a.rows; r += GEMV_WAVES) finish_block(a, c, r, red[0][r][lane], red[0][r][lane + 64], lane);
         return;
     }
+    // Split k: wave 0 alone sums the workgroup's partial, stores it, arrives at the output group's counter and, if it
+    // is the last split to arrive, finishes the group.  Its own stores are then the only ones the arrival has to
+    // follow, so no workgroup barrier sits between the stores, the arrival and the finish.
+    if (wave != 0) return;
+    // An output group's splits share one XCD (and so one L2) when the workgroup remap applies (G % 8 == 0): its
+    // partials then meet in that L2.  Otherwise they are written through to memory.
+    const bool xcd_local = (c.G & 7) == 0;
+    float *part = c.part;
+    for (int r = 0; r < a.rows; r++) {
+        float *dst = part + (((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out + (size_t)c.og * 128;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int col = lane + 64 * h;
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < GEMV_WAVES; w++) s += red[w][r][col];
+            s *= a.out_scale;
+            if (a.partial_only || xcd_local) dst[col] = s;  // L1 is write-through: the store lands in the XCD's L2
+            else __hip_atomic_store(dst + col, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // through to memory
+        }
+    }
     if (a.partial_only || !a.fused_finish) return;
 
-    // ---- single-launch finish: the last split of this output group to arrive sums the partials and finishes.
-    // Each thread's write-through partial stores are acknowledged (s_waitcnt vmcnt(0)) before the barrier, so they
-    // are in memory before thread 0 bumps the counter; the last arriver reads them with cache-bypassing loads.
+    // ---- single-launch finish.  The partial stores are acknowledged (s_waitcnt vmcnt(0)) before lane 0 bumps the
+    // counter, so they are in the L2 / memory before any later arriver can see the count.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    uint32_t *ctr = &a.counters[((size_t)c.proj * a.groups + c.g) * c.G + c.og];
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = old == (uint32_t)(c.S - 1);
-    }
-    __syncthreads();
-    if (!*last_flag) return;
+    uint32_t *ctr = &a.counters[(((size_t)c.proj * a.groups + c.g) * c.G + c.og) * COUNTER_STRIDE];
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != (uint32_t)(c.S - 1)) return;
     if (xcd_local) {
         // This CU's L1 may hold lines of these partials from an earlier call: drop them, then read the XCD's L2.
         asm volatile("buffer_inv sc0" ::: "memory");
-        for (int r = wave; r < a.rows; r += GEMV_WAVES) {
-            float v0 = 0.f, v1 = 0.f;
-            for (int s2 = 0; s2 < c.S; s2++) {
-                const float *pp = part + (((size_t)c.g * c.S + s2) * a.rows + r) * a.out + (size_t)c.og * 128;
-                v0 += pp[lane];
-                v1 += pp[lane + 64];
-            }
+        for (int r = 0; r < a.rows; r++) {
+            float v0, v1;
+            sum_planes<false>(part + (((size_t)c.g * c.S) * a.rows + r) * a.out + (size_t)c.og * 128,
+                              (size_t)a.rows * a.out, c.S, lane, v0, v1);
             finish_block(a, c, r, v0, v1, lane);
         }
     } else {
-        for (int r = wave; r < a.rows; r += GEMV_WAVES) {
-            float v0 = 0.f, v1 = 0.f;
-            for (int s2 = 0; s2 < c.S; s2++) {
-                float *pp = part + (((size_t)c.g * c.S + s2) * a.rows + r) * a.out + (size_t)c.og * 128;
-                v0 += __hip_atomic_load(pp + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                v1 += __hip_atomic_load(pp + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            }
+        for (int r = 0; r < a.rows; r++) {
+            float v0, v1;
+            sum_planes<true>(part + (((size_t)c.g * c.S) * a.rows + r) * a.out + (size_t)c.og * 128,
+                             (size_t)a.rows * a.out, c.S, lane, v0, v1);
             finish_block(a, c, r, v0, v1, lane);
         }
     }
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Per-rate decode constants for a ragged bank (hash rows and pair rows differ by rate; the window mask does not).
@@ -408,45 +462,58 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
 // dispatched per workgroup.
 template <int FAM, int N, int RT, int PRO>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
+    // Everything below reads kernel arguments at fixed offsets and selects between projections instead of indexing
+    // by blockIdx.z, and the workgroup remap is branch free: all argument loads then issue in one batch.
     GemvCtx c;
-    c.IT = a.in >> 4;
-    c.OT = a.out >> 4;
+    // The scalar arguments the entry needs, pinned into registers together: one batch of argument loads, one wait.
+    int in = a.in, out = a.out, splits = a.splits, x_div = a.x_div, bank_limit = a.bank_limit;
+    const uint32_t *bank_of = a.bank_of;
+    asm volatile("" : "+s"(in), "+s"(out), "+s"(splits), "+s"(x_div), "+s"(bank_limit), "+s"(bank_of));
+    c.x_div = x_div;
+    c.IT = in >> 4;
+    c.OT = out >> 4;
     c.G = c.OT >> 3;
-    c.S = a.splits;
+    c.S = splits;
     const int L = blockIdx.x;
-    if ((c.G & 7) == 0) {  // keep an output group's splits on one XCD (workgroups go round-robin over 8 XCDs)
-        const int xcd = L & 7, r = L >> 3;
-        c.og = (r / c.S) * 8 + xcd;
-        c.sp = r % c.S;
-    } else {
-        c.og = L / c.S;
-        c.sp = L % c.S;
-    }
+    // keep an output group's splits on one XCD when G % 8 == 0 (workgroups go round-robin over the 8 XCDs)
+    const bool remap = (c.G & 7) == 0;
+    const int r8 = L >> 3;
+    c.og = remap ? (r8 / c.S) * 8 + (L & 7) : L / c.S;
+    c.sp = remap ? r8 % c.S : L % c.S;
     c.g = blockIdx.y;
     c.proj = blockIdx.z;
-    c.bank = a.bank_of ? (int)min(a.bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
+    const bool p1 = c.proj != 0;
+    c.suh = p1 ? a.suh[1] : a.suh[0];
+    c.svh = p1 ? a.svh[1] : a.svh[0];
+    c.part = p1 ? a.partial[1] : a.partial[0];
+    const uint16_t *trellis = p1 ? a.trellis[1] : a.trellis[0];
+    c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(bank_limit - 1)) : c.g;
     c.KS = c.IT / c.S;
     c.kt0 = c.sp * c.KS;
+    const int lane = threadIdx.x & 63;
+    const size_t sv = (size_t)c.bank * out + (size_t)c.og * 128;
+    c.sv0 = h2f(c.svh[sv + lane]);
+    c.sv1 = h2f(c.svh[sv + lane + 64]);
 
     __shared__ __align__(16) uint16_t xs[RT][MAX_KSPAN];
     __shared__ float red[GEMV_WAVES][RT][128];
-    __shared__ int last_flag;
 
     if constexpr (N >= 0) {
         const int n = N ? N : a.n;
-        const uint16_t *tb = a.trellis[c.proj] + (size_t)c.bank * c.IT * c.OT * n;
-        gemv_body<FAM, N, RT, PRO>(a, c, tb, n, a.k, xs, red, &last_flag);
+        const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
+        gemv_body<FAM, N, RT, PRO>(a, c, tb, n, a.k, xs, red);
     } else {
+        const int col = p1 ? a.meta_col[1] : a.meta_col[0];
         const uint32_t *m = a.meta + (size_t)c.bank * 8;
-        const int n = (int)m[a.meta_col[c.proj]];
-        const uint16_t *tb = a.trellis[c.proj] + 2 * (size_t)m[4 + a.meta_col[c.proj]];
+        const int n = (int)m[col];
+        const uint16_t *tb = trellis + 2 * (size_t)m[4 + col];
         const DecodeK k = rate_constants<FAM>(a, n);
         switch (n) {
-        case 16: gemv_body<FAM, 16, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
-        case 32: gemv_body<FAM, 32, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
-        case 48: gemv_body<FAM, 48, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
-        case 64: gemv_body<FAM, 64, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
-        default: gemv_body<FAM, 0, RT, PRO>(a, c, tb, n, k, xs, red, &last_flag); break;
+        case 16: gemv_body<FAM, 16, RT, PRO>(a, c, tb, n, k, xs, red); break;
+        case 32: gemv_body<FAM, 32, RT, PRO>(a, c, tb, n, k, xs, red); break;
+        case 48: gemv_body<FAM, 48, RT, PRO>(a, c, tb, n, k, xs, red); break;
+        case 64: gemv_body<FAM, 64, RT, PRO>(a, c, tb, n, k, xs, red); break;
+        default: gemv_body<FAM, 0, RT, PRO>(a, c, tb, n, k, xs, red); break;
         }
     }
 }
@@ -459,14 +526,17 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
     const int r = blockIdx.y % a.rows;
     c.g = blockIdx.y / a.rows;
     c.proj = blockIdx.z;
+    const bool p1 = c.proj != 0;
+    c.svh = p1 ? a.svh[1] : a.svh[0];
+    const float *part = p1 ? a.partial[1] : a.partial[0];
     c.bank = a.bank_of ? (int)min(a.bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
     const int lane = threadIdx.x;
-    float v0 = 0.f, v1 = 0.f;
-    for (int s = 0; s < a.splits; s++) {
-        const float *pp = a.partial[c.proj] + (((size_t)c.g * a.splits + s) * a.rows + r) * a.out + (size_t)c.og * 128;
-        v0 += pp[lane];
-        v1 += pp[lane + 64];
-    }
+    const size_t sv = (size_t)c.bank * a.out + (size_t)c.og * 128;
+    c.sv0 = h2f(c.svh[sv + lane]);
+    c.sv1 = h2f(c.svh[sv + lane + 64]);
+    float v0, v1;
+    sum_planes<false>(part + (((size_t)c.g * a.splits) * a.rows + r) * a.out + (size_t)c.og * 128,
+                      (size_t)a.rows * a.out, a.splits, lane, v0, v1);
     finish_block(a, c, r, v0, v1, lane);
 }
 

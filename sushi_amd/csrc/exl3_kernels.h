@@ -12,6 +12,9 @@ hipError_t run_reconstruct_inner(int fam, const uint16_t *trellis, int it, int o
 
 enum Prologue : int { PRO_X = 0, PRO_MID = 1 };
 
+// Fused-finish arrival counters sit one per 128-byte line (32 words) in the workspace's counter region.
+constexpr int COUNTER_STRIDE = 32;
+
 // Trellis GEMV over `groups` independent (bank, x-block) pairs, 1..8 rows each.
 //  * dense linear: groups = 1 (or G for linearGrouped), bank_of = null, x_div = 1;
 //  * MoE pair GEMV: groups = slots, bank_of = expert id per slot, x_div = topk, two projections (gate, up) on
@@ -60,6 +63,9 @@ hipError_t run_gemv_fam_FAM_HASH(int prologue, const GemvArgs &a, hipStream_t s)
 hipError_t run_gemv_fam_FAM_PAIR(int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_3INST(int prologue, const GemvArgs &a, hipStream_t s);
 int gemv_default_splits(int in, int out, int rows, int groups_times_proj);
+
+// Top-k the MoE reduce holds per row (REDUCE_MAX_TOPK, src/exl3/expert_exl3_kernels.zig:2562).
+constexpr int kMoeReduceMaxTopk = 32;
 
 // MoE finish: y[row] = sum_k score * (FWHT(sum_s down_part) * svh_down[e]) (+ shared), REDUCE_SOURCE.
 struct ReduceArgs {

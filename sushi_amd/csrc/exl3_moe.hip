@@ -53,24 +53,32 @@ __device__ __forceinline__ float round_to(int dt, float v) {
     return v;
 }
 
-__global__ __launch_bounds__(64) void moe_reduce_kernel(ReduceArgs a) {
-    const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+// One workgroup per (128-block, row): wave w handles slots w, w + RW, ... (sum of the slot's k splits, FWHT, svh,
+// score) into LDS, in parallel; wave 0 then adds the slots in slot order (the reference's order) and finishes.
+constexpr int RW = 8;
+__global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
+    const int blk = blockIdx.x, row = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t base = (size_t)blk * 128;
-    float y0 = 0.f, y1 = 0.f;
-    for (int kk = 0; kk < a.topk; kk++) {
+    __shared__ float contrib[kMoeReduceMaxTopk][128];
+    for (int kk = wave; kk < a.topk; kk += RW) {
         const int slot = row * a.topk + kk;
         const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
-        float v0 = 0.f, v1 = 0.f;
-        for (int s = 0; s < a.splits; s++) {
-            const float *pp = a.part + ((size_t)slot * a.splits + s) * a.hidden + base;
-            v0 += pp[lane];
-            v1 += pp[lane + 64];
-        }
-        fwht128_wave(v0, v1, lane);
         const float sc = a.scores[slot];
         const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
-        y0 += (v0 * HAD_SCALE * h2f(sv[lane])) * sc;
-        y1 += (v1 * HAD_SCALE * h2f(sv[lane + 64])) * sc;
+        const float s0 = h2f(sv[lane]), s1 = h2f(sv[lane + 64]);
+        float v0, v1;
+        sum_planes<false>(a.part + (size_t)slot * a.splits * a.hidden + base, a.hidden, a.splits, lane, v0, v1);
+        fwht128_wave(v0, v1, lane);
+        contrib[kk][lane] = (v0 * HAD_SCALE * s0) * sc;
+        contrib[kk][lane + 64] = (v1 * HAD_SCALE * s1) * sc;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float y0 = 0.f, y1 = 0.f;
+    for (int kk = 0; kk < a.topk; kk++) {
+        y0 += contrib[kk][lane];
+        y1 += contrib[kk][lane + 64];
     }
     const size_t yo = (size_t)row * a.hidden + base;
     if (a.shared) {
@@ -93,7 +101,8 @@ __global__ __launch_bounds__(64) void moe_reduce_kernel(ReduceArgs a) {
 }
 
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(moe_reduce_kernel, dim3((unsigned)(a.hidden / 128), (unsigned)a.rows), dim3(64), 0, s, a);
+    if (a.topk > kMoeReduceMaxTopk) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_reduce_kernel, dim3((unsigned)(a.hidden / 128), (unsigned)a.rows), dim3(64 * RW), 0, s, a);
     return hipGetLastError();
 }
 
