@@ -19,7 +19,7 @@
  *   trellis  u16 [E][in/16][out/16][n]   n = 16*K halfwords per 16x16 tile, even, 16..128
  *   suh      f16 [E][in]                 input sign/scale vector
  *   svh      f16 [E][out]                output sign/scale vector
- *   x        [rows][in]  f16 | bf16 | f32  (exl3_dtype)
+ *   x        [rows][in]  f16 | bf16 | f32  (exl3_dtype), 4-byte aligned
  *   y        [rows][out] same dtype set
  */
 #ifndef SUSHI_EXL3_HIP_H

@@ -144,6 +144,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !trellis || !suh || !svh || !y) return fail(EXL3_ERR_BAD_SHAPE, "linear: null operand");
+    if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "linear: x must be 4-byte aligned");
     const size_t need = linear_ws(groups, rows, in, out, n);
     if (ws_bytes < need || (need && (!ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))))
         return fail(EXL3_ERR_WORKSPACE, "linear: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
@@ -232,6 +233,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
                    const uint16_t *const su[3], const uint16_t *const sv[3], int n_uniform, const uint32_t *meta,
                    const uint32_t *inds, const float *scores, int32_t topk, int32_t clamp_limit, const void *shared,
                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+    if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
     MoePlan p = plan_moe(nslots, hidden, inter);
     const size_t need = kCounterBytes + 2 * p.gu_bytes + p.down_bytes;

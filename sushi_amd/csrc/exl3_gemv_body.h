@@ -4,13 +4,14 @@
 // and of the routed MoE chain (PAIR_GEMV_SOURCE :2082-2241, DOWN_FUSED_SOURCE :1820-2023 in
 // src/exl3/expert_exl3_kernels.zig).
 //
-// MI355X layout.  A workgroup (4 waves) owns one output group of 8 tiles (128 outputs, one Hadamard block) of one
-// (bank, x-block) pair over one k split of at most 16 k-tiles (whole 128-blocks).  Per k-tile row a wave streams the
+// MI355X layout.  A workgroup (GEMV_WAVES = 8 waves, one workgroup per CU at C1) owns one output group of 8 tiles
+// (128 outputs, one Hadamard block) of one (bank, x-block) pair over one k split of at most 32 k-tiles (whole
+// 128-blocks).  Per k-tile row a wave streams the
 // group's 8 tiles, which lie contiguous in the pack order [IT][OT][n] (8*n*2 bytes, 1 KiB at K4): lane = 8*o + j
 // reads chunk j of tile o, the words carrying codewords 32j..32j+31 = fragment threads 4j..4j+3 of tensorCorePerm =
 // output columns j and j+8 over all 16 k rows.  Every lane owns two output columns outright, decodes its 32 weights
 // into registers as packed f16 pairs (t, t+1) = rows (r, r+1) of one column and feeds v_dot2_f32_f16 against the
-// prepared input held in LDS.  No cross-lane reduction happens inside a wave; the 4 waves meet once in LDS.
+// prepared input held in LDS.  No cross-lane reduction happens inside a wave; the waves meet once in LDS.
 //
 // Latency: a wave issues the loads of all its tiles (<= 4) before the prologue, so HBM latency overlaps the input
 // preparation (x * suh, FWHT-128, f16 -- or the MoE SwiGLU mid).  The finish (FWHT-128, * svh) runs in the same
@@ -28,10 +29,8 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, w), __builtin_bit_cast(h2_t, x), acc, false);
 }
 
-constexpr int GEMV_WAVES = 4;
 constexpr int GEMV_THREADS = 64 * GEMV_WAVES;
 constexpr int MAX_KSPAN = 2048;
-constexpr int TPW = 4;  // tiles a wave loads before the prologue
 
 __device__ __forceinline__ float load_x(const void *x, int dt, size_t i) {
     if (dt == DT_F16) return load_act<DT_F16>(x, i);
@@ -54,6 +53,7 @@ __device__ __forceinline__ float silu(float g) {
 
 struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div;
+    const void *x;
     const uint16_t *suh, *svh;  // this projection's banks (selected once: an indexed kernel-argument read would be
     float *part;                // a dependent scalar load)
     float sv0, sv1;             // svh of this lane's two outputs, fetched at entry for the finish
@@ -165,16 +165,19 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
 }
 
 // x[i] as f32 from an f16 / bf16 / f32 array without branching on the dtype: one 32-bit load of the aligned word
-// that holds the element, then selects.  (A branch per dtype joins through a register copy, and that copy makes the
-// load wait for its data right there.)  Rows are multiples of 128 elements, so the word never leaves the row's span
-// when the array starts 4-byte aligned; a 2-byte aligned start reads at most 2 bytes past the end of the array.
+// that holds the element, then bit-mask selects.  (A branch per dtype joins through a register copy, and that copy
+// makes the load wait for its data right there.)  The array starts 4-byte aligned (the C ABI checks it) and rows
+// are multiples of 128 elements, so the word never leaves the array.  The load is addressed as global memory: a flat
+// load would also count against lgkmcnt and be waited for with the scalar loads.
 __device__ __forceinline__ float load_x_nb(const void *x, int dt, size_t i) {
     const bool wide = dt == DT_F32;
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(x) + (wide ? i * 4 : i * 2);
-    const uint32_t w = *reinterpret_cast<const uint32_t *>(addr & ~(uintptr_t)3);
-    const uint32_t h = (addr & 2) ? (w >> 16) : (w & 0xFFFFu);
-    const float narrow = dt == DT_F16 ? h2f((uint16_t)h) : __uint_as_float(h << 16);
-    return wide ? __uint_as_float(w) : narrow;
+    const size_t byte = wide ? i * 4 : i * 2;
+    typedef __attribute__((address_space(1))) const uint32_t global_u32;
+    const uint32_t w = *(global_u32 *)(static_cast<const char *>(x) + (byte & ~(size_t)3));
+    const uint32_t h = __builtin_amdgcn_alignbit(w, w, (uint32_t)(byte & 2) * 8u) & 0xFFFFu;
+    const uint32_t f16b = __float_as_uint(h2f((uint16_t)h)), bf16b = h << 16;
+    const uint32_t m_wide = 0u - (uint32_t)wide, m_f16 = 0u - (uint32_t)(dt == DT_F16);
+    return __uint_as_float((w & m_wide) | (~m_wide & ((f16b & m_f16) | (bf16b & ~m_f16))));
 }
 
 // The prologue's input loads for a wave's first jobs, issued ahead of the tile loads (loads retire in order, so an
@@ -182,7 +185,8 @@ __device__ __forceinline__ float load_x_nb(const void *x, int dt, size_t i) {
 // are unconditional (a job past the end re-reads job 0 and is then discarded): no branch, so no early wait.
 template <int RT>
 struct PrologueRegs {
-    static constexpr int JOBS = RT < 2 ? 1 : RT / 2;  // jobs per wave with a split of <= 16 k-tiles (2 blocks) per row
+    // jobs per wave when a split spans at most TPW * GEMV_WAVES k-tiles (TPW * GEMV_WAVES / 8 blocks per row)
+    static constexpr int JOBS = (RT * TPW / 8) < 1 ? 1 : (RT * TPW / 8);
     float x0[JOBS], x1[JOBS], s0[JOBS], s1[JOBS];
 };
 
@@ -199,8 +203,8 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx 
             const int kb = c.kt0 * 16 + b * 128;
             const size_t si = (size_t)c.bank * a.in + kb;
             const size_t xi = ((size_t)(c.g / c.x_div) * a.rows + rho) * a.in + kb;
-            pr.x0[i] = load_x_nb(a.x, a.x_dtype, xi + lane);
-            pr.x1[i] = load_x_nb(a.x, a.x_dtype, xi + lane + 64);
+            pr.x0[i] = load_x_nb(c.x, a.x_dtype, xi + lane);
+            pr.x1[i] = load_x_nb(c.x, a.x_dtype, xi + lane + 64);
             pr.s0[i] = h2f(c.suh[si + lane]);
             pr.s1[i] = h2f(c.suh[si + lane + 64]);
         }
@@ -253,8 +257,8 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                     v1 = f16r(pr.x1[i]) * pr.s1[i];
                 } else {
                     const size_t xi = ((size_t)(c.g / c.x_div) * a.rows + rho) * a.in + kb;
-                    v0 = f16r(load_x_nb(a.x, a.x_dtype, xi + lane)) * h2f(c.suh[si + lane]);
-                    v1 = f16r(load_x_nb(a.x, a.x_dtype, xi + lane + 64)) * h2f(c.suh[si + lane + 64]);
+                    v0 = f16r(load_x_nb(c.x, a.x_dtype, xi + lane)) * h2f(c.suh[si + lane]);
+                    v1 = f16r(load_x_nb(c.x, a.x_dtype, xi + lane + 64)) * h2f(c.suh[si + lane + 64]);
                 }
             } else {  // the SwiGLU mid of the decode chain (DOWN_FUSED_SOURCE prologue, :1838-1920)
                 float w[2][2];
@@ -315,12 +319,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
 
     if constexpr (N != 0) {
         constexpr int AW = LaneBits<N>::AW;
-        // This wave's k-tiles are wave, wave + 4, ...; a split spans whole 128-blocks (8 k-tiles), so every wave has
-        // at least two.  The first TPW loads are issued unconditionally (a wave with fewer tiles re-reads its last
-        // one), so the compiler counts them and each tile's decode waits only for that tile's own loads.
+        // This wave's k-tiles are wave, wave + GEMV_WAVES, ...; a split spans whole 128-blocks (8 k-tiles), so every
+        // wave has at least one.  The first TPW loads are issued unconditionally (a wave with fewer tiles re-reads its
+        // last one), so the compiler counts them and each tile's decode waits only for that tile's own loads.
         const int ntiles = (c.KS - wave + GEMV_WAVES - 1) / GEMV_WAVES;
         PrologueRegs<RT> pr;
         prologue_fetch<PRO, RT>(a, c, wave, lane, pr);
+        __builtin_amdgcn_sched_barrier(0);  // the input loads stay ahead of the tile loads (vmcnt retires in order)
         uint32_t Aw[TPW][AW];
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
@@ -468,7 +473,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     // The scalar arguments the entry needs, pinned into registers together: one batch of argument loads, one wait.
     int in = a.in, out = a.out, splits = a.splits, x_div = a.x_div, bank_limit = a.bank_limit;
     const uint32_t *bank_of = a.bank_of;
-    asm volatile("" : "+s"(in), "+s"(out), "+s"(splits), "+s"(x_div), "+s"(bank_limit), "+s"(bank_of));
+    const void *x = a.x;
+    asm volatile("" : "+s"(in), "+s"(out), "+s"(splits), "+s"(x_div), "+s"(bank_limit), "+s"(bank_of), "+s"(x));
+    c.x = x;
     c.x_div = x_div;
     c.IT = in >> 4;
     c.OT = out >> 4;

@@ -15,6 +15,12 @@ enum Prologue : int { PRO_X = 0, PRO_MID = 1 };
 // Fused-finish arrival counters sit one per 128-byte line (32 words) in the workspace's counter region.
 constexpr int COUNTER_STRIDE = 32;
 
+// GEMV workgroup shape: GEMV_WAVES waves, each loading up to TPW k-tiles of the output group before its prologue.
+// One workgroup per CU (256 CUs) is the target grid.
+constexpr int GEMV_WAVES = 8;
+constexpr int TPW = 4;
+constexpr int GEMV_TARGET_WGS = 256;
+
 // Trellis GEMV over `groups` independent (bank, x-block) pairs, 1..8 rows each.
 //  * dense linear: groups = 1 (or G for linearGrouped), bank_of = null, x_div = 1;
 //  * MoE pair GEMV: groups = slots, bank_of = expert id per slot, x_div = topk, two projections (gate, up) on

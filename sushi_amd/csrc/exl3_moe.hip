@@ -20,22 +20,19 @@ hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s) {
     }
 }
 
-constexpr int GEMV_MAX_KSPAN = 2048;
-
 int gemv_default_splits(int in, int out, int rows, int groups_times_proj) {
-    // Splits cut k on whole Hadamard blocks.  A split of at most 16 k-tiles lets every wave issue all of its tile
-    // loads before the prologue (4 waves x 4 tiles); past that, more splits only add partial traffic unless the
-    // grid is still short of ~2 workgroups per CU (256 CUs).
+    // Splits cut k on whole Hadamard blocks.  A split of at most TPW * GEMV_WAVES k-tiles lets every wave issue all
+    // of its tile loads before the prologue; past that, more splits only add partial traffic unless the grid is
+    // still short of one workgroup per CU.
     const int blocks = in / 128;
     const int it = in / 16;
     const long G = (long)(out / 128) * groups_times_proj;
-    const long target = 512;
     int best = blocks;
     for (int s = 1; s <= blocks; s++) {
         if (blocks % s) continue;
-        if (it / s > 16) continue;
+        if (it / s > TPW * GEMV_WAVES) continue;
         best = s;
-        if (G * s >= target) break;
+        if (G * s >= GEMV_TARGET_WGS) break;
     }
     (void)rows;
     return best;

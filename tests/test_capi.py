@@ -54,7 +54,10 @@ def test_abi_version_and_host_side_refusals():
     # rows == 0 is a no-op
     assert lib.exl3_linear(None, 0, 0, 128, 128, None, 64, None, None, d, None, 0, None, 0, None) == 0
     # workspace too small (rows=1 needs counters)
-    assert lib.exl3_linear(1, 0, 1, 128, 128, 1, 64, 1, 1, d, 1, 0, None, 0, None) == -9
+    assert lib.exl3_linear(4, 0, 1, 128, 128, 1, 64, 1, 1, d, 1, 0, None, 0, None) == -9
+    # x must be 4-byte aligned (the kernels read activations as aligned 32-bit words)
+    assert lib.exl3_linear(2, 0, 1, 128, 128, 1, 64, 1, 1, d, 1, 0, None, 0, None) == -1
+    assert "aligned" in L.last_error()
 
 
 def test_moe_refusals():
