@@ -21,6 +21,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure (no sparsity)
 COPIES = 64
 
 
@@ -138,6 +139,64 @@ def bench_moe(batch: int, layers: int = 16, replays: int = 8):
                 bytes=(distinct + 1) * per_expert)
 
 
+def _time_linear(in_f, out_f, n, rows, dec, codec_name, seed, min_pool_bytes=640 << 20, replays=6):
+    """Average microseconds per exl3.linear call over a rotating pool of weight copies (pool > the 256 MB Infinity
+    Cache), timed as HIP-graph replays between HIP events."""
+    import torch
+
+    from sushi_amd import exl3, synth
+
+    dev = torch.device("cuda:0")
+    wbytes = in_f * out_f * n // 8
+    copies = max(2, min(256, -(-min_pool_bytes // wbytes)))
+    trellis = synth.codes(seed, f"sw.{codec_name}.{in_f}x{out_f}.{n}", (copies, in_f // 16, out_f // 16, n), device=dev)
+    suh = synth.sign_scale(seed, "sw.suh", (1, in_f), device=dev)
+    svh = synth.sign_scale(seed, "sw.svh", (1, out_f), device=dev)
+    x = synth.normal(seed, f"sw.x{rows}", (rows, in_f), device=dev)
+    projs = [exl3.Proj(trellis[i:i + 1], suh, svh) for i in range(copies)]
+    exl3.linear(x, projs[0], dec)
+    torch.cuda.synchronize()
+    g = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(copies)], dev)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * copies)
+    del g, trellis, projs
+    torch.cuda.empty_cache()
+    return us, copies
+
+
+def sweep(which: str):
+    """configs[1] (C2: MCG GEMV sweep) and configs[2] (C3: prefill GEMM): one JSON line per case."""
+    from sushi_amd import exl3
+
+    cases = []
+    if which in ("c2", "all"):
+        for in_f, out_f in ((2048, 2048), (4096, 14336), (14336, 4096)):
+            for n in (32, 48, 64):
+                for rows in (1, 4, 16):
+                    cases.append(("c2", in_f, out_f, n, rows, exl3.MCG, "mcg"))
+    if which in ("c3", "all"):
+        for rows in (512, 2048):
+            cases.append(("c3", 4096, 14336, 48, rows, exl3.INST3, "3inst"))
+    for cfg, in_f, out_f, n, rows, dec, name in cases:
+        us, copies = _time_linear(in_f, out_f, n, rows, dec, name, 1 if cfg == "c2" else 2)
+        alg = _algorithmic_bytes(in_f, out_f, n, rows)
+        line = {"config": cfg, "codebook": name, "in": in_f, "out": out_f, "K": n // 16, "rows": rows,
+                "us_per_call": round(us, 3), "copies": copies, "tok_per_s": round(rows / (us * 1e-6), 1),
+                "effective_GBps": round(alg / (us * 1e-6) / 1e9, 1),
+                "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if cfg == "c3":
+            tflops = 2.0 * rows * in_f * out_f / (us * 1e-6) / 1e12
+            line["TFLOPs"] = round(tflops, 1)
+            line["mfma_frac_f16_dense"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
+        print(json.dumps(line), flush=True)
+
+
 def copy_calibration(mib: int, reps: int = 4):
     """A plain device-to-device copy of `mib` MiB, `reps` times: the reference kernel whose FETCH_SIZE/WRITE_SIZE
     counters calibrate the HBM-traffic figures of the GEMV (expected: exactly `mib` MiB read and written)."""
@@ -196,7 +255,11 @@ def main() -> int:
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
+    ap.add_argument("--sweep", choices=("c2", "c3", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     args = ap.parse_args()
+    if args.sweep:
+        sweep(args.sweep)
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
               "note (expert/output-tile sharding), not a runnable path", file=sys.stderr)

@@ -124,9 +124,9 @@ int32_t exl3_reconstruct_inner(const uint16_t *trellis, int32_t in_features, int
                                exl3_decode_t dec, uint16_t *out, hipStream_t stream);
 
 /* `linear.linear` / `linearWith` (src/exl3/linear.zig:27-34) and `trunk.matmul` (src/exl3/trunk.zig:53-92):
- * y[rows][out] = finish(inner(prepare(x))) for one bank (trellis [1][in/16][out/16][n]).  Rows <= 8 take the
- * decode GEMV (PROJECT_ROWS_MAX, src/exl3/project_rows.zig:456-459), wider the MFMA GEMM
- * (`run`, src/exl3/linear.zig:317-336).  in and out must be multiples of 128. */
+ * y[rows][out] = finish(inner(prepare(x))) for one bank (trellis [1][in/16][out/16][n]).  Rows <= 16 take the
+ * decode GEMV (projectRows, src/exl3/project_rows.zig:456-459, whose 8-row limit is raised to 16 here), wider the
+ * MFMA GEMM (`run`, src/exl3/linear.zig:317-336).  in and out must be multiples of 128. */
 size_t exl3_linear_workspace_size(int32_t rows, int32_t in_features, int32_t out_features, int32_t n);
 int32_t exl3_linear(const void *x, int32_t x_dtype, int32_t rows, int32_t in_features, int32_t out_features,
                     const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,

@@ -98,7 +98,10 @@ bool dtype_ok(int dt) { return dt == EXL3_DT_F16 || dt == EXL3_DT_BF16 || dt == 
 
 float out_scale_of(int fam) { return (fam == FAM_HASH || fam == FAM_PAIR) ? 4096.0f : 1.0f; }
 
-constexpr int kRowsMax = 8;  // PROJECT_ROWS_MAX, project_rows.zig:456-459
+// Rows the decode GEMV serves (each weight decoded once, dotted against every row).  The reference's
+// PROJECT_ROWS_MAX is 8 (project_rows.zig:456-459) with a 16-row mode beside it; here up to 16 rows stay on the
+// GEMV, which beats a 128-row MFMA tile by far at such row counts.
+constexpr int kRowsMax = 16;
 
 struct GemvPlan {
     int splits;

@@ -85,11 +85,30 @@ __device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0
 // Written in fenced phases (windows, product step 1, step 2, masks, low sums, high sums, dots): within a phase no
 // instruction depends on another, so no result is read by the instruction right after it and the hazard recognizer
 // inserts no wait states (gfx950 needs one between a 16-bit-lane or SDWA write and its reader).
+// Rows of the prepared input are read from LDS in chunks of XCH (all at once up to 8 rows): the fragments of the
+// first chunk are requested before the decode, so their LDS latency hides behind it.
+template <int RT>
+struct XChunk {
+    static constexpr int CH = RT <= 8 ? RT : 4;
+};
+
+template <int RT>
+__device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[MAX_KSPAN], int kk, int r0,
+                                             uint4 (&X)[XChunk<RT>::CH], uint4 (&Y)[XChunk<RT>::CH]) {
+#pragma unroll
+    for (int c = 0; c < XChunk<RT>::CH; c++) {
+        X[c] = *reinterpret_cast<const uint4 *>(&xs[r0 + c][kk * 16]);
+        Y[c] = *reinterpret_cast<const uint4 *>(&xs[r0 + c][kk * 16 + 8]);
+    }
+}
+
 template <int FAM, int N, int RT, bool MASKED>
-__device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint4 (&X)[RT],
-                                            const uint4 (&Y)[RT], const DecodeK &k, float (&acc0)[RT],
-                                            float (&acc1)[RT]) {
+__device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[MAX_KSPAN],
+                                            int kk, const DecodeK &k, float (&acc0)[RT], float (&acc1)[RT]) {
     using P = Pairing<N>;
+    constexpr int CH = XChunk<RT>::CH;
+    uint4 X[CH], Y[CH];
+    load_x_chunk<RT>(xs, kk, 0, X, Y);
     uint32_t win[32];
 #pragma unroll
     for (int v = 0; v < 32; v++) {
@@ -152,14 +171,18 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
     }
     // pair i = (u, u+1), u = 2i = 8qq + 2p: p = 0/1 -> column j rows 2qq(+8), p = 2/3 -> column j+8
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int qq = i >> 2, p = i & 3;
+    for (int r0 = 0; r0 < RT; r0 += CH) {
+        if (r0 > 0) load_x_chunk<RT>(xs, kk, r0, X, Y);
 #pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const uint4 &V = (p & 1) ? Y[r] : X[r];
-            const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
-            if (p < 2) acc0[r] = dot2(w[i], xv, acc0[r]);
-            else acc1[r] = dot2(w[i], xv, acc1[r]);
+        for (int i = 0; i < 16; i++) {
+            const int qq = i >> 2, p = i & 3;
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const uint4 &V = (p & 1) ? Y[c] : X[c];
+                const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
+                if (p < 2) acc0[r0 + c] = dot2(w[i], xv, acc0[r0 + c]);
+                else acc1[r0 + c] = dot2(w[i], xv, acc1[r0 + c]);
+            }
         }
     }
 }
@@ -297,15 +320,6 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
     }
 }
 
-template <int RT>
-__device__ __forceinline__ void load_x_frag(const uint16_t (*xs)[MAX_KSPAN], int kk, uint4 (&X)[RT], uint4 (&Y)[RT]) {
-#pragma unroll
-    for (int r = 0; r < RT; r++) {
-        X[r] = *reinterpret_cast<const uint4 *>(&xs[r][kk * 16]);
-        Y[r] = *reinterpret_cast<const uint4 *>(&xs[r][kk * 16 + 8]);
-    }
-}
-
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 template <int FAM, int N, int RT, int PRO>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
@@ -348,10 +362,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
 #pragma unroll
             for (int t = 0; t < TPW; t++) {
                 if (t0 + t < ntiles) {
-                    uint4 X[RT], Y[RT];
-                    load_x_frag<RT>(xs, wave + GEMV_WAVES * (t0 + t), X, Y);
-                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], X, Y, k, acc0, acc1);
-                    else decode_tile<FAM, N, RT, false>(Aw[t], X, Y, k, acc0, acc1);
+                    const int kk = wave + GEMV_WAVES * (t0 + t);
+                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, k, acc0, acc1);
+                    else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, k, acc0, acc1);
                 }
             }
         }
@@ -363,21 +376,26 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
         for (int kk = wave; kk < c.KS; kk += GEMV_WAVES) {
             const int tk = c.kt0 + kk;
             const uint32_t *words = reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n);
-            uint4 X[RT], Y[RT];
-            load_x_frag<RT>(xs, kk, X, Y);
+            uint32_t w[16];
 #pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
+            for (int i = 0; i < 16; i++) {
+                const int t = 32 * j + 2 * i;
+                w[i] = decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
+            }
+            constexpr int CH = XChunk<RT>::CH;
 #pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int t = 32 * j + 8 * qq + 2 * p;
-                    const uint32_t w =
-                        decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
+            for (int r0 = 0; r0 < RT; r0 += CH) {
+                uint4 X[CH], Y[CH];
+                load_x_chunk<RT>(xs, kk, r0, X, Y);
 #pragma unroll
-                    for (int r = 0; r < RT; r++) {
-                        const uint4 &V = (p & 1) ? Y[r] : X[r];
+                for (int i = 0; i < 16; i++) {
+                    const int qq = i >> 2, p = i & 3;
+#pragma unroll
+                    for (int cc = 0; cc < CH; cc++) {
+                        const uint4 &V = (p & 1) ? Y[cc] : X[cc];
                         const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
-                        if (p < 2) acc0[r] = dot2(w, xv, acc0[r]);
-                        else acc1[r] = dot2(w, xv, acc1[r]);
+                        if (p < 2) acc0[r0 + cc] = dot2(w[i], xv, acc0[r0 + cc]);
+                        else acc1[r0 + cc] = dot2(w[i], xv, acc1[r0 + cc]);
                     }
                 }
             }
@@ -555,7 +573,8 @@ static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
         if (a.rows <= 1) hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
         else if (a.rows <= 2) hipLaunchKernelGGL((gemv_kernel<FAM, N, 2, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
         else if (a.rows <= 4) hipLaunchKernelGGL((gemv_kernel<FAM, N, 4, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<FAM, N, 8, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
+        else if (a.rows <= 8) hipLaunchKernelGGL((gemv_kernel<FAM, N, 8, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
+        else hipLaunchKernelGGL((gemv_kernel<FAM, N, 16, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
     } else {  // the MoE stages run one row per (slot, bank) pair
         if (a.rows != 1) return hipErrorInvalidValue;
         hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);

@@ -47,7 +47,7 @@ def _run(pd, xd, dec):
     return y.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 8, 12, 16])
 @pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
 def test_gemv_rows_and_rates_mcg(dev, rows, n):
     print(f"[gemv] rows={rows} n={n}", flush=True)
@@ -89,7 +89,7 @@ def test_gemv_split_and_finish_arms_agree(dev, splits, separate):
         del os.environ["EXL3_GEMV_SEPARATE_FINISH"]
 
 
-@pytest.mark.parametrize("rows", [2, 12])
+@pytest.mark.parametrize("rows", [2, 12, 24])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_activation_dtypes(dev, dtype, rows):
     p, pd, x, xd = _case(dev, 13, rows, 256, 256, 64, dtype)
@@ -142,7 +142,7 @@ def test_linear_grouped(dev):
         assert max_abs_rel(y[b], want) < BAR
 
 
-@pytest.mark.parametrize("rows", [9, 16, 33, 130])
+@pytest.mark.parametrize("rows", [17, 33, 130])
 @pytest.mark.parametrize("n", [32, 48, 64, 40])
 def test_gemm_arm(dev, rows, n):
     print(f"[gemm] rows={rows} n={n}", flush=True)
@@ -160,14 +160,14 @@ def test_gemm_codebooks(dev, label):
 
 def test_gemm_rows_equal_gemv_rows(dev):
     """Byte-exactness is not claimed between arms, but the two arms agree to the bar on the same rows."""
-    p, pd, x, xd = _case(dev, 5, 12, 512, 512, 64)
+    p, pd, x, xd = _case(dev, 5, 24, 512, 512, 64)
     dec = DECODES["mcg"][0]
     wide = _run(pd, xd, dec)
-    narrow = np.concatenate([_run(pd, xd[i:i + 4].contiguous(), dec) for i in range(0, 12, 4)])
+    narrow = np.concatenate([_run(pd, xd[i:i + 4].contiguous(), dec) for i in range(0, 24, 4)])
     assert max_abs_rel(wide, narrow) < BAR
 
 
-@pytest.mark.parametrize("rows", [1, 16])
+@pytest.mark.parametrize("rows", [1, 16, 24])
 def test_c1_full_size_3inst_k4(dev, rows):
     """Config 1's shape at full size: 4096 x 4096, K4, 3INST, against the oracle."""
     print(f"[c1] rows={rows}", flush=True)
