@@ -171,7 +171,8 @@ def _time_linear(in_f, out_f, n, rows, dec, codec_name, seed, min_pool_bytes=640
 
 
 def sweep(which: str):
-    """configs[1] (C2: MCG GEMV sweep) and configs[2] (C3: prefill GEMM): one JSON line per case."""
+    """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
+    one JSON line per case."""
     from sushi_amd import exl3
 
     cases = []
@@ -183,6 +184,8 @@ def sweep(which: str):
     if which in ("c3", "all"):
         for rows in (512, 2048):
             cases.append(("c3", 4096, 14336, 48, rows, exl3.INST3, "3inst"))
+    if which in ("c5", "all"):
+        print(json.dumps(bench_moe_c5()), flush=True)
     for cfg, in_f, out_f, n, rows, dec, name in cases:
         us, copies = _time_linear(in_f, out_f, n, rows, dec, name, 1 if cfg == "c2" else 2)
         alg = _algorithmic_bytes(in_f, out_f, n, rows)
@@ -195,6 +198,60 @@ def sweep(which: str):
             line["TFLOPs"] = round(tflops, 1)
             line["mfma_frac_f16_dense"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
         print(json.dumps(line), flush=True)
+
+
+def bench_moe_c5(batch: int = 64, layers: int = 4, replays: int = 4):
+    """configs[4] in the reference-expressible form: the per-expert rate groups of rate_groups.zig (64 experts at
+    K=1, 192 at K=2: 1.75 bpw on average) as one ragged bank, hidden 4096, inter 2048, SPEC1 (spec1-w15 table: the one with K=1 rows),
+    top-8 over N(0,1) logits, batch 64, plus a K=4 shared expert.  A dependent chain of `layers` layers."""
+    import torch
+
+    from sushi_amd import exl3, synth
+
+    dev = torch.device("cuda:0")
+    E1, E2, hidden, inter, k = 64, 192, 4096, 2048, 8
+    dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
+    g1 = synth.bank(5, "c5.k1", E1, hidden, inter, 16, device=dev)
+    g2 = synth.bank(5, "c5.k2", E2, hidden, inter, 32, device=dev)
+    rb = exl3.Ragged.init([g1, g2])
+    del g1, g2
+    shared = synth.bank(5, "c5.shared", 1, hidden, inter, 64, device=dev)
+    x0 = synth.normal(5, f"c5.x{batch}", (batch, hidden), device=dev)
+    routes = []
+    for layer in range(layers):
+        logits = synth.normal(5, f"c5.logits{batch}.{layer}", (batch, E1 + E2), dtype=torch.float32).to(dev)
+        routes.append(exl3.moe_routing_chain(logits, k))
+    sh_inds = torch.zeros(batch, 1, dtype=torch.int32, device=dev)
+    sh_sc = torch.ones(batch, 1, dtype=torch.float32, device=dev)
+
+    def chain():
+        x = x0
+        for inds, scores in routes:
+            s = exl3.moe(x, shared, sh_inds, sh_sc, dec)
+            x = exl3.moe_ragged(x, rb, inds, scores, dec, shared=s)
+        return x
+
+    chain()
+    torch.cuda.synchronize()
+    g = _capture(chain, dev)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    layer_us = e0.elapsed_time(e1) * 1e3 / (replays * layers)
+    tiles = (hidden // 16) * (inter // 16)
+    bytes_k = {16: 3 * tiles * 16 * 2, 32: 3 * tiles * 32 * 2}
+    distinct = []
+    for inds, _ in routes:
+        ids = set(inds.flatten().tolist())
+        distinct.append(sum(bytes_k[16] if e < E1 else bytes_k[32] for e in ids) + 6 * len(ids) * (hidden + inter))
+    alg = sum(distinct) / layers + 3 * (hidden * inter * 64 // 8 + 2 * (hidden + inter))
+    return {"config": "c5", "batch": batch, "experts": E1 + E2, "bpw": 1.75, "layer_us": round(layer_us, 3),
+            "us_per_token": round(layer_us / batch, 3), "effective_GBps": round(alg / (layer_us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(alg / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def copy_calibration(mib: int, reps: int = 4):
@@ -255,7 +312,7 @@ def main() -> int:
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
-    ap.add_argument("--sweep", choices=("c2", "c3", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
+    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     args = ap.parse_args()
     if args.sweep:
         sweep(args.sweep)

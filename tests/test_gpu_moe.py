@@ -108,6 +108,35 @@ def test_moe_ragged_rate_groups(dev):
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
+def test_moe_ragged_stq_rates_k1_k2(dev):
+    """configs[4]'s layer in its reference-expressible form: per-expert rate groups at K=1 and K=2 (1:3), SPEC1
+    with the spec1-w15 table (the SPEC1 table with K=1 rows), plus a shared expert, against the oracle."""
+    hidden, inter, k, rows = 256, 128, 8, 5
+    groups = [(4, (16, 16, 16)), (12, (32, 32, 32))]
+    banks = [synth.bank(40 + g, f"stq{g}", e, hidden, inter, rates) for g, (e, rates) in enumerate(groups)]
+    rb = exl3.Ragged.init([_to(b, dev) for b in banks])
+    E = sum(e for e, _ in groups)
+    dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
+    odec = O.decode(O.CB_SPEC1, 15, 1)
+    x = synth.normal(40, "x", (rows, hidden))
+    inds, scores = _route(40, rows, E, k)
+    sh = synth.normal(41, "shared", (rows, hidden))
+    want = np.zeros((rows, hidden))
+    for r in range(rows):
+        for j in range(k):
+            e = int(inds[r, j])
+            g = 0 if e < groups[0][0] else 1
+            local = e - (0 if g == 0 else groups[0][0])
+            b = banks[g]
+            want[r] += O.moe_swiglu_host(x[r].float().numpy(), _np(b.gate), _np(b.up), _np(b.down), [local],
+                                         [scores[r, j]], hidden, inter, groups[g][1], odec)
+    # the routed sum is rounded to the output dtype before the shared expert is added
+    want = want.astype(np.float16).astype(np.float64) + sh.float().numpy()
+    y = exl3.moe_ragged(x.to(dev), rb, torch.from_numpy(inds.view(np.int32)).to(dev),
+                        torch.from_numpy(scores).to(dev), dec, shared=sh.to(dev))
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
 def test_router_matches_oracle(dev):
     logits = synth.normal(2, "logits", (9, 256), dtype=torch.float32)
     inds, scores = exl3.moe_routing_chain(logits.to(dev), 8)
