@@ -2,6 +2,7 @@
 //
 // Every refusal happens before any launch (as the reference's `Exl3*` errors do, src/exl3/root.zig:104-133), and the
 // library never allocates device memory: scratch comes from the caller's workspace.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -202,19 +203,41 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     return launched(run_gemm(fam, g, stream), "exl3_linear (gemm)");
 }
 
+// Rows above which the routed layer takes the sorted arm (slots grouped into expert windows, each expert's tiles
+// decoded once per window): the reference's decode chain serves up to DECODE_ROWS_MAX = 16 rows and sends wider
+// batches to moePrefill (src/exl3/root.zig:45-53).
+constexpr int kMoeDecodeRowsMax = 16;
+
 struct MoePlan {
+    bool windowed;
     int s1, s2;
-    size_t gu_bytes, down_bytes;
+    size_t gu_bytes, down_bytes, table_bytes;
+    size_t total() const { return kCounterBytes + 2 * gu_bytes + down_bytes + table_bytes; }
 };
 
-MoePlan plan_moe(int nslots, int hidden, int inter) {
+MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
     MoePlan p;
-    p.s1 = gemv_default_splits(hidden, inter, 1, 2 * nslots);
-    p.s2 = gemv_default_splits(inter, hidden, 1, nslots);
+    p.windowed = windowed;
+    // Window count lies between ceil(nslots / MOE_WINDOW_ROWS) and nslots; splits are planned for the fewest windows
+    // (the most splits), so the planes fit whatever the routing turns out to be.
+    const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS : nslots;
+    const int rows = windowed ? MOE_WINDOW_ROWS : 1;
+    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups);
+    p.s2 = gemv_default_splits(inter, hidden, rows, groups);
     p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
     p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));
+    p.table_bytes = windowed ? align_up(sizeof(uint32_t)) + 2 * align_up((size_t)nslots * sizeof(uint32_t)) +
+                                   align_up((size_t)nslots * MOE_WINDOW_ROWS * sizeof(uint32_t))
+                             : 0;
     return p;
 }
+
+bool moe_windowed(int rows, int nslots, int experts) {
+    return rows > kMoeDecodeRowsMax && nslots <= kMoeWindowMaxSlots && experts <= kMoeWindowMaxExperts;
+}
+
+// EXL3_MOE_WINDOWS=0 keeps every row count on the per-slot chain (for comparing the arms).
+bool moe_windows_enabled() { return env_int("EXL3_MOE_WINDOWS", 1) != 0; }
 
 constexpr int kReduceMaxTopk = kMoeReduceMaxTopk;  // REDUCE_MAX_TOPK, expert_exl3_kernels.zig:2562
 
@@ -238,8 +261,8 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    MoePlan p = plan_moe(nslots, hidden, inter);
-    const size_t need = kCounterBytes + 2 * p.gu_bytes + p.down_bytes;
+    MoePlan p = plan_moe(nslots, hidden, inter, moe_windows_enabled() && moe_windowed(rows, nslots, experts));
+    const size_t need = p.total();
     if (ws_bytes < need || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
         return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
     char *w = static_cast<char *>(ws) + kCounterBytes;
@@ -247,15 +270,36 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     float *up_part = reinterpret_cast<float *>(w + p.gu_bytes);
     float *down_part = reinterpret_cast<float *>(w + 2 * p.gu_bytes);
     const float scale = out_scale_of(fam);
+    // 0) sorted arm: group the slots into expert windows
+    uint32_t *win_count = nullptr, *win_expert = nullptr, *win_rows = nullptr, *win_slots = nullptr;
+    int groups = nslots, grows = 1;
+    if (p.windowed) {
+        char *t = w + 2 * p.gu_bytes + p.down_bytes;
+        win_count = reinterpret_cast<uint32_t *>(t);
+        t += align_up(sizeof(uint32_t));
+        win_expert = reinterpret_cast<uint32_t *>(t);
+        t += align_up((size_t)nslots * sizeof(uint32_t));
+        win_rows = reinterpret_cast<uint32_t *>(t);
+        t += align_up((size_t)nslots * sizeof(uint32_t));
+        win_slots = reinterpret_cast<uint32_t *>(t);
+        hipError_t e = run_moe_windows(inds, nslots, experts, win_count, win_expert, win_rows, win_slots, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (windows)");
+        groups = std::min(nslots, experts + (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS);
+        grows = MOE_WINDOW_ROWS;
+    }
 
     // 1) gate and up GEMVs of every slot (PAIR_GEMV_SOURCE): f32 planes [slot][split][inter]
     GemvArgs a{};
     a.x = x;
     a.x_dtype = x_dtype;
-    a.rows = 1;
+    a.rows = grows;
     a.in = hidden;
     a.out = inter;
     a.x_div = topk;
+    a.win_count = win_count;
+    a.win_expert = win_expert;
+    a.win_rows = win_rows;
+    a.win_slots = win_slots;
     for (int i = 0; i < 2; i++) {
         a.trellis[i] = tr[i];
         a.suh[i] = su[i];
@@ -272,7 +316,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     a.partial[0] = gate_part;
     a.partial[1] = up_part;
     a.splits = p.s1;
-    a.groups = nslots;
+    a.groups = groups;
     a.nproj = 2;
     a.fused_finish = 0;
     a.partial_only = 1;
@@ -283,10 +327,14 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     GemvArgs d{};
     d.x = nullptr;
     d.x_dtype = x_dtype;
-    d.rows = 1;
+    d.rows = grows;
     d.in = inter;
     d.out = hidden;
     d.x_div = 1;
+    d.win_count = win_count;
+    d.win_expert = win_expert;
+    d.win_rows = win_rows;
+    d.win_slots = win_slots;
     d.mid_part[0] = gate_part;
     d.mid_part[1] = up_part;
     d.mid_splits = p.s1;
@@ -306,7 +354,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     d.out_scale = scale;
     d.partial[0] = down_part;
     d.splits = p.s2;
-    d.groups = nslots;
+    d.groups = groups;
     d.nproj = 1;
     d.fused_finish = 0;
     d.partial_only = 1;
@@ -401,8 +449,10 @@ int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t
 
 size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
     if (rows <= 0 || topk <= 0 || hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) return 0;
-    MoePlan p = plan_moe(rows * topk, hidden, inter);
-    return kCounterBytes + 2 * p.gu_bytes + p.down_bytes;
+    const int nslots = rows * topk;
+    size_t need = plan_moe(nslots, hidden, inter, false).total();
+    if (moe_windowed(rows, nslots, 1)) need = std::max(need, plan_moe(nslots, hidden, inter, true).total());
+    return need;
 }
 
 int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,

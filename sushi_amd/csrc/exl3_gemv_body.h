@@ -53,6 +53,8 @@ __device__ __forceinline__ float silu(float g) {
 
 struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div;
+    int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
+    const uint32_t *wslots;     // the window's slots, or null (group = slot, or plain rows)
     const void *x;
     const uint16_t *suh, *svh;  // this projection's banks (selected once: an indexed kernel-argument read would be
     float *part;                // a dependent scalar load)
@@ -66,6 +68,24 @@ __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c
     const size_t yo = ((size_t)c.g * a.rows + rho) * a.out + (size_t)c.og * 128;
     store_y(a.y, a.y_dtype, yo + lane, v0 * HAD_SCALE * c.sv0);
     store_y(a.y, a.y_dtype, yo + lane + 64, v1 * HAD_SCALE * c.sv1);
+}
+
+// Row r of this group: its input row, its partial plane (elements into [.][S][.][out]) and, for the MoE mid, its slot.
+// WIN: the group is an expert window (the sorted MoE arm), a compile-time choice so the dense kernels carry none of it.
+template <bool WIN>
+__device__ __forceinline__ size_t x_row(const GemvArgs &a, const GemvCtx &c, int r) {
+    if constexpr (WIN) return (size_t)(c.wslots[r] / c.x_div);
+    else return (size_t)(c.g / c.x_div) * a.rows + r;
+}
+template <bool WIN>
+__device__ __forceinline__ size_t part_row(const GemvArgs &a, const GemvCtx &c, int r) {
+    if constexpr (WIN) return ((size_t)c.wslots[r] * c.S + c.sp) * a.out;
+    else return (((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out;
+}
+template <bool WIN>
+__device__ __forceinline__ int slot_of(const GemvCtx &c, int r) {
+    if constexpr (WIN) return (int)c.wslots[r];
+    else return c.g;
 }
 
 // Codeword v of the lane as (window index, high half?): for K = 1, 2, 4 the window ending at codeword v + 16/K
@@ -89,7 +109,7 @@ __device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0
 // first chunk are requested before the decode, so their LDS latency hides behind it.
 template <int RT>
 struct XChunk {
-    static constexpr int CH = RT <= 8 ? RT : 4;
+    static constexpr int CH = RT == 4 ? 2 : RT <= 8 ? RT : 4;
 };
 
 template <int RT>
@@ -102,9 +122,11 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[MAX_KSPAN], in
     }
 }
 
+// `rows` (wave-uniform, <= RT) bounds the chunks that are dotted: rows past it hold zeros.
 template <int FAM, int N, int RT, bool MASKED>
 __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[MAX_KSPAN],
-                                            int kk, const DecodeK &k, float (&acc0)[RT], float (&acc1)[RT]) {
+                                            int kk, int rows, const DecodeK &k, float (&acc0)[RT],
+                                            float (&acc1)[RT]) {
     using P = Pairing<N>;
     constexpr int CH = XChunk<RT>::CH;
     uint4 X[CH], Y[CH];
@@ -172,7 +194,10 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
     // pair i = (u, u+1), u = 2i = 8qq + 2p: p = 0/1 -> column j rows 2qq(+8), p = 2/3 -> column j+8
 #pragma unroll
     for (int r0 = 0; r0 < RT; r0 += CH) {
-        if (r0 > 0) load_x_chunk<RT>(xs, kk, r0, X, Y);
+        if (r0 > 0) {
+            if (r0 >= rows) break;
+            load_x_chunk<RT>(xs, kk, r0, X, Y);
+        }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int qq = i >> 2, p = i & 3;
@@ -213,7 +238,7 @@ struct PrologueRegs {
     float x0[JOBS], x1[JOBS], s0[JOBS], s1[JOBS];
 };
 
-template <int PRO, int RT>
+template <int PRO, int RT, bool WIN>
 __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx &c, int wave, int lane,
                                                PrologueRegs<RT> &pr) {
     if constexpr (PRO == PRO_X) {
@@ -222,10 +247,10 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx 
         for (int i = 0; i < PrologueRegs<RT>::JOBS; i++) {
             int job = wave + GEMV_WAVES * i;
             int rho = job / nblk, b = job - rho * nblk;
-            if (!(job < nblk * RT && rho < a.rows)) rho = b = 0;
+            if (!(job < nblk * RT && rho < c.rows)) rho = b = 0;
             const int kb = c.kt0 * 16 + b * 128;
             const size_t si = (size_t)c.bank * a.in + kb;
-            const size_t xi = ((size_t)(c.g / c.x_div) * a.rows + rho) * a.in + kb;
+            const size_t xi = x_row<WIN>(a, c, rho) * a.in + kb;
             pr.x0[i] = load_x_nb(c.x, a.x_dtype, xi + lane);
             pr.x1[i] = load_x_nb(c.x, a.x_dtype, xi + lane + 64);
             pr.s0[i] = h2f(c.suh[si + lane]);
@@ -237,7 +262,7 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx 
 // Sums the gate and up planes of one 128-block over the previous launch's k splits, issuing a chunk of loads before
 // any add (a loop that adds as it loads would wait out one memory round trip per split).
 constexpr int MID_CHUNK = 8;
-__device__ __forceinline__ void mid_planes(const GemvArgs &a, const GemvCtx &c, int kb, int lane, float (&w)[2][2]) {
+__device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, int lane, float (&w)[2][2]) {
     w[0][0] = w[0][1] = w[1][0] = w[1][1] = 0.f;
     for (int s0 = 0; s0 < a.mid_splits; s0 += MID_CHUNK) {
         float t[2][2][MID_CHUNK];
@@ -246,7 +271,7 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, const GemvCtx &c, 
 #pragma unroll
             for (int q = 0; q < MID_CHUNK; q++) {
                 const int s2 = min(s0 + q, a.mid_splits - 1);
-                const float *pp = a.mid_part[pj] + ((size_t)c.g * a.mid_splits + s2) * a.in + kb;
+                const float *pp = a.mid_part[pj] + ((size_t)slot * a.mid_splits + s2) * a.in + kb;
                 t[pj][0][q] = pp[lane];
                 t[pj][1][q] = pp[lane + 64];
             }
@@ -263,7 +288,7 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, const GemvCtx &c, 
     }
 }
 
-template <int PRO, int RT>
+template <int PRO, int RT, bool WIN>
 __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[MAX_KSPAN], int wave,
                                          int lane, const PrologueRegs<RT> &pr) {
     const int nblk = c.KS >> 3;
@@ -272,20 +297,20 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
         const int kb = c.kt0 * 16 + b * 128;
         const int i = (job - wave) / GEMV_WAVES;
         float v0 = 0.f, v1 = 0.f;
-        if (rho < a.rows) {
+        if (rho < c.rows) {
             const size_t si = (size_t)c.bank * a.in + kb;
             if constexpr (PRO == PRO_X) {  // prepareInput (expert_exl3.zig:490-501)
                 if (i < PrologueRegs<RT>::JOBS) {
                     v0 = f16r(pr.x0[i]) * pr.s0[i];
                     v1 = f16r(pr.x1[i]) * pr.s1[i];
                 } else {
-                    const size_t xi = ((size_t)(c.g / c.x_div) * a.rows + rho) * a.in + kb;
+                    const size_t xi = x_row<WIN>(a, c, rho) * a.in + kb;
                     v0 = f16r(load_x_nb(c.x, a.x_dtype, xi + lane)) * h2f(c.suh[si + lane]);
                     v1 = f16r(load_x_nb(c.x, a.x_dtype, xi + lane + 64)) * h2f(c.suh[si + lane + 64]);
                 }
             } else {  // the SwiGLU mid of the decode chain (DOWN_FUSED_SOURCE prologue, :1838-1920)
                 float w[2][2];
-                mid_planes(a, c, kb, lane, w);
+                mid_planes(a, slot_of<WIN>(c, rho), kb, lane, w);
                 float gv[2], uv[2];
 #pragma unroll
                 for (int pj = 0; pj < 2; pj++) {
@@ -321,7 +346,7 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
 }
 
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
-template <int FAM, int N, int RT, int PRO>
+template <int FAM, int N, int RT, int PRO, bool WIN>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
                                           int n, const DecodeK &k, uint16_t (*xs)[MAX_KSPAN], float (*red)[RT][128]) {
     const int tid = threadIdx.x, lane = tid & 63;
@@ -338,7 +363,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
         // last one), so the compiler counts them and each tile's decode waits only for that tile's own loads.
         const int ntiles = (c.KS - wave + GEMV_WAVES - 1) / GEMV_WAVES;
         PrologueRegs<RT> pr;
-        prologue_fetch<PRO, RT>(a, c, wave, lane, pr);
+        prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
         __builtin_amdgcn_sched_barrier(0);  // the input loads stay ahead of the tile loads (vmcnt retires in order)
         uint32_t Aw[TPW][AW];
 #pragma unroll
@@ -347,7 +372,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
             load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
                                Aw[t]);
         }
-        prologue<PRO, RT>(a, c, xs, wave, lane, pr);
+        prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
         for (int t0 = 0; t0 < ntiles; t0 += TPW) {
@@ -363,15 +388,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
             for (int t = 0; t < TPW; t++) {
                 if (t0 + t < ntiles) {
                     const int kk = wave + GEMV_WAVES * (t0 + t);
-                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, k, acc0, acc1);
-                    else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, k, acc0, acc1);
+                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, acc0, acc1);
+                    else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, acc0, acc1);
                 }
             }
         }
     } else {  // any other rate: the generic reader (runtime funnel per codeword)
         PrologueRegs<RT> pr;
-        prologue_fetch<PRO, RT>(a, c, wave, lane, pr);
-        prologue<PRO, RT>(a, c, xs, wave, lane, pr);
+        prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
+        prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();
         for (int kk = wave; kk < c.KS; kk += GEMV_WAVES) {
             const int tk = c.kt0 + kk;
@@ -385,6 +410,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
             constexpr int CH = XChunk<RT>::CH;
 #pragma unroll
             for (int r0 = 0; r0 < RT; r0 += CH) {
+                if (r0 > 0 && r0 >= c.rows) break;
                 uint4 X[CH], Y[CH];
                 load_x_chunk<RT>(xs, kk, r0, X, Y);
 #pragma unroll
@@ -430,8 +456,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
     // partials then meet in that L2.  Otherwise they are written through to memory.
     const bool xcd_local = (c.G & 7) == 0;
     float *part = c.part;
-    for (int r = 0; r < a.rows; r++) {
-        float *dst = part + (((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out + (size_t)c.og * 128;
+    for (int r = 0; r < c.rows; r++) {
+        float *dst = part + part_row<WIN>(a, c, r) + (size_t)c.og * 128;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int col = lane + 64 * h;
@@ -483,7 +509,7 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
 
 // N > 0: one rate for the launch; N == 0: the generic reader; N < 0: per-expert rate from the ragged meta table,
 // dispatched per workgroup.
-template <int FAM, int N, int RT, int PRO>
+template <int FAM, int N, int RT, int PRO, bool WIN>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     // Everything below reads kernel arguments at fixed offsets and selects between projections instead of indexing
     // by blockIdx.z, and the workgroup remap is branch free: all argument loads then issue in one batch.
@@ -512,7 +538,16 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     c.svh = p1 ? a.svh[1] : a.svh[0];
     c.part = p1 ? a.partial[1] : a.partial[0];
     const uint16_t *trellis = p1 ? a.trellis[1] : a.trellis[0];
-    c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(bank_limit - 1)) : c.g;
+    c.rows = a.rows;
+    c.wslots = nullptr;
+    if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
+        if ((uint32_t)c.g >= *a.win_count) return;
+        c.bank = (int)min(a.win_expert[c.g], (uint32_t)(bank_limit - 1));
+        c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
+        c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
+    } else {
+        c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(bank_limit - 1)) : c.g;
+    }
     c.KS = c.IT / c.S;
     c.kt0 = c.sp * c.KS;
     const int lane = threadIdx.x & 63;
@@ -526,7 +561,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     if constexpr (N >= 0) {
         const int n = N ? N : a.n;
         const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
-        gemv_body<FAM, N, RT, PRO>(a, c, tb, n, a.k, xs, red);
+        gemv_body<FAM, N, RT, PRO, WIN>(a, c, tb, n, a.k, xs, red);
     } else {
         const int col = p1 ? a.meta_col[1] : a.meta_col[0];
         const uint32_t *m = a.meta + (size_t)c.bank * 8;
@@ -534,11 +569,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
         const uint16_t *tb = trellis + 2 * (size_t)m[4 + col];
         const DecodeK k = rate_constants<FAM>(a, n);
         switch (n) {
-        case 16: gemv_body<FAM, 16, RT, PRO>(a, c, tb, n, k, xs, red); break;
-        case 32: gemv_body<FAM, 32, RT, PRO>(a, c, tb, n, k, xs, red); break;
-        case 48: gemv_body<FAM, 48, RT, PRO>(a, c, tb, n, k, xs, red); break;
-        case 64: gemv_body<FAM, 64, RT, PRO>(a, c, tb, n, k, xs, red); break;
-        default: gemv_body<FAM, 0, RT, PRO>(a, c, tb, n, k, xs, red); break;
+        case 16: gemv_body<FAM, 16, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+        case 32: gemv_body<FAM, 32, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+        case 48: gemv_body<FAM, 48, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+        case 64: gemv_body<FAM, 64, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+        default: gemv_body<FAM, 0, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
         }
     }
 }
@@ -569,15 +604,18 @@ template <int FAM, int N, int PRO>
 static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
     const int G = a.out / 128;
     dim3 grid((unsigned)(G * a.splits), (unsigned)a.groups, (unsigned)a.nproj);
-    if constexpr (PRO == PRO_X && N >= 0) {
-        if (a.rows <= 1) hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else if (a.rows <= 2) hipLaunchKernelGGL((gemv_kernel<FAM, N, 2, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else if (a.rows <= 4) hipLaunchKernelGGL((gemv_kernel<FAM, N, 4, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else if (a.rows <= 8) hipLaunchKernelGGL((gemv_kernel<FAM, N, 8, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<FAM, N, 16, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
-    } else {  // the MoE stages run one row per (slot, bank) pair
+    if (a.win_count) {  // the sorted MoE arm: expert windows of MOE_WINDOW_ROWS rows, f32 planes out
+        if (a.rows != MOE_WINDOW_ROWS || !a.partial_only) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemv_kernel<FAM, N, MOE_WINDOW_ROWS, PRO, true>), grid, dim3(GEMV_THREADS), 0, s, a);
+    } else if constexpr (PRO == PRO_X && N >= 0) {
+        if (a.rows <= 1) hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+        else if (a.rows <= 2) hipLaunchKernelGGL((gemv_kernel<FAM, N, 2, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+        else if (a.rows <= 4) hipLaunchKernelGGL((gemv_kernel<FAM, N, 4, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+        else if (a.rows <= 8) hipLaunchKernelGGL((gemv_kernel<FAM, N, 8, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+        else hipLaunchKernelGGL((gemv_kernel<FAM, N, 16, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+    } else {  // the MoE decode chain: one row per (slot, bank) pair
         if (a.rows != 1) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO>), grid, dim3(GEMV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -60,7 +60,16 @@ struct GemvArgs {
     int nproj;
     int fused_finish;
     int partial_only;
+    // Expert windows (the sorted MoE arm): group g is window g, whose win_rows[g] (<= MOE_WINDOW_ROWS) rows are the
+    // slots win_slots[g][r] of expert win_expert[g]; windows past *win_count exit at once.  Null: group g is slot g.
+    const uint32_t *win_count;
+    const uint32_t *win_expert;
+    const uint32_t *win_rows;
+    const uint32_t *win_slots;
 };
+
+// Rows per expert window in the sorted MoE arm.
+constexpr int MOE_WINDOW_ROWS = 4;
 
 hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_MCG(int prologue, const GemvArgs &a, hipStream_t s);
@@ -90,6 +99,13 @@ struct ReduceArgs {
     float out_scale;
 };
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s);
+
+// Groups the slots of a routing by expert into windows of up to MOE_WINDOW_ROWS rows, slots in ascending order
+// within an expert (a stable counting sort): one workgroup; slots <= kMoeWindowMaxSlots, experts <= kMoeWindowMaxExperts.
+constexpr int kMoeWindowMaxSlots = 8192;
+constexpr int kMoeWindowMaxExperts = 4096;
+hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32_t *win_count, uint32_t *win_expert,
+                           uint32_t *win_rows, uint32_t *win_slots, hipStream_t s);
 
 // Dense GEMM arm (prefill, rows > 8): prepare x -> xp f16, decode tiles to MFMA fragments, finish in the epilogue.
 struct GemmArgs {

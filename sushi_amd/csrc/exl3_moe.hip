@@ -103,6 +103,69 @@ hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Expert windows for the sorted MoE arm (the grouping moePrefill's sort does, expert_exl3_kernels.zig:2861-2931 with
+// sorted_windows.zig:10-165): slot s (expert e = inds[s], clamped below `experts`) gets rank r = the number of slots
+// before it with the same expert, and lands in window wbase[e] + r / MOE_WINDOW_ROWS at row r % MOE_WINDOW_ROWS, where
+// wbase is the exclusive scan of ceil(count[e] / MOE_WINDOW_ROWS) over experts.  Ranks come from a direct count, so
+// the result does not depend on thread timing.
+constexpr int WIN_THREADS = 1024;
+__global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
+                                                                  int experts, uint32_t *__restrict__ win_count,
+                                                                  uint32_t *__restrict__ win_expert,
+                                                                  uint32_t *__restrict__ win_rows,
+                                                                  uint32_t *__restrict__ win_slots) {
+    __shared__ uint16_t ex[kMoeWindowMaxSlots];
+    __shared__ uint32_t cnt[kMoeWindowMaxExperts];
+    __shared__ uint32_t wbase[kMoeWindowMaxExperts];
+    __shared__ uint32_t part[WIN_THREADS];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < experts; e += WIN_THREADS) cnt[e] = 0;
+    for (int s = tid; s < nslots; s += WIN_THREADS) ex[s] = (uint16_t)min(inds[s], (uint32_t)(experts - 1));
+    __syncthreads();
+    for (int s = tid; s < nslots; s += WIN_THREADS) atomicAdd(&cnt[ex[s]], 1u);
+    __syncthreads();
+    // exclusive scan of windows per expert: each thread sums a contiguous run of experts, then a scan of the runs
+    const int per = (experts + WIN_THREADS - 1) / WIN_THREADS;
+    const int e0 = min(tid * per, experts), e1 = min(e0 + per, experts);
+    uint32_t local = 0;
+    for (int e = e0; e < e1; e++) local += (cnt[e] + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS;
+    part[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < WIN_THREADS; off <<= 1) {
+        const uint32_t v = tid >= off ? part[tid - off] : 0u;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    uint32_t run = part[tid] - local;
+    for (int e = e0; e < e1; e++) {
+        wbase[e] = run;
+        run += (cnt[e] + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS;
+    }
+    if (tid == WIN_THREADS - 1) *win_count = part[tid];
+    __syncthreads();
+    for (int s = tid; s < nslots; s += WIN_THREADS) {
+        const uint32_t e = ex[s];
+        uint32_t rank = 0;
+        for (int q = 0; q < s; q++) rank += ex[q] == e ? 1u : 0u;
+        const uint32_t w = wbase[e] + rank / MOE_WINDOW_ROWS, r = rank % MOE_WINDOW_ROWS;
+        win_slots[(size_t)w * MOE_WINDOW_ROWS + r] = (uint32_t)s;
+        if (r == 0) {
+            win_expert[w] = e;
+            win_rows[w] = min(cnt[e] - rank, (uint32_t)MOE_WINDOW_ROWS);
+        }
+    }
+}
+
+hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32_t *win_count, uint32_t *win_expert,
+                           uint32_t *win_rows, uint32_t *win_slots, hipStream_t s) {
+    if (nslots <= 0 || nslots > kMoeWindowMaxSlots || experts <= 0 || experts > kMoeWindowMaxExperts)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_windows_kernel, dim3(1), dim3(WIN_THREADS), 0, s, inds, nslots, experts, win_count,
+                       win_expert, win_rows, win_slots);
+    return hipGetLastError();
+}
+
 // One workgroup (256 threads) per row: k rounds of a block-wide argmax (ties to the lower index), then the softmax
 // mass of the picks over the full row, renormalised.
 __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict__ logits, int experts, int k,

@@ -36,9 +36,10 @@ def _oracle_moe(b, x, inds, scores, hidden, inter, n, odec, clamp=0.0):
     return np.stack(ys)
 
 
-@pytest.mark.parametrize("rows", [1, 3, 8, 17])
+@pytest.mark.parametrize("rows", [1, 3, 8, 16, 17, 40])
 @pytest.mark.parametrize("n", [32, 48])
 def test_moe_decode_chain(dev, rows, n):
+    """Up to 16 rows: the per-slot decode chain; above: the sorted arm (slots grouped into expert windows)."""
     print(f"[moe] rows={rows} n={n}", flush=True)
     E, hidden, inter, k = 16, 256, 384, 4
     b = synth.bank(3, "moe", E, hidden, inter, n)
@@ -56,8 +57,9 @@ def test_moe_decode_chain(dev, rows, n):
     ("pair1", exl3.Decode(exl3.Codebook.pair1), O.decode(O.CB_PAIR1)),
     ("3inst", exl3.INST3, O.decode(O.CB_3INST)),
 ])
-def test_moe_codebooks(dev, label, dec, odec):
-    E, hidden, inter, k, rows, n = 8, 256, 256, 3, 2, 32
+@pytest.mark.parametrize("rows", [2, 20])
+def test_moe_codebooks(dev, label, dec, odec, rows):
+    E, hidden, inter, k, n = 8, 256, 256, 3, 32
     b = synth.bank(8, "moe" + label, E, hidden, inter, n)
     x = synth.normal(8, "x", (rows, hidden))
     inds, scores = _route(8, rows, E, k)
@@ -67,8 +69,9 @@ def test_moe_codebooks(dev, label, dec, odec):
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
-def test_moe_with_shared_and_clamped(dev):
-    E, hidden, inter, k, rows, n = 8, 256, 128, 2, 3, 32
+@pytest.mark.parametrize("rows", [3, 24])
+def test_moe_with_shared_and_clamped(dev, rows):
+    E, hidden, inter, k, n = 8, 256, 128, 2, 32
     b = synth.bank(4, "moes", E, hidden, inter, n)
     x = synth.normal(4, "x", (rows, hidden))
     inds, scores = _route(4, rows, E, k)
@@ -85,8 +88,9 @@ def test_moe_with_shared_and_clamped(dev):
     assert max_abs_rel(wantc, want) > 10 * BAR  # the clamp is live on this data
 
 
-def test_moe_ragged_rate_groups(dev):
-    hidden, inter, k, rows = 256, 256, 4, 3
+@pytest.mark.parametrize("rows", [3, 21])
+def test_moe_ragged_rate_groups(dev, rows):
+    hidden, inter, k = 256, 256, 4
     groups = [(6, (32, 32, 48)), (10, (16, 16, 32))]
     banks = [synth.bank(20 + g, f"rg{g}", e, hidden, inter, rates) for g, (e, rates) in enumerate(groups)]
     rb = exl3.Ragged.init([_to(b, dev) for b in banks])
@@ -135,6 +139,39 @@ def test_moe_ragged_stq_rates_k1_k2(dev):
     y = exl3.moe_ragged(x.to(dev), rb, torch.from_numpy(inds.view(np.int32)).to(dev),
                         torch.from_numpy(scores).to(dev), dec, shared=sh.to(dev))
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_moe_sorted_arm_concentrated_routing(dev):
+    """Every row routes to the same experts (40 slots per expert, ten windows each) and some ids sit past the bank
+    (clamped to the last expert, as the decode chain does)."""
+    E, hidden, inter, k, rows, n = 6, 256, 128, 4, 40, 32
+    b = synth.bank(9, "moec", E, hidden, inter, n)
+    x = synth.normal(9, "x", (rows, hidden))
+    inds = np.tile(np.array([[3, 0, 5, 1]], dtype=np.uint32), (rows, 1))
+    inds[::7, 2] = 9  # past the bank: clamped to expert 5
+    _, scores = _route(9, rows, E, k)
+    want = _oracle_moe(b, x.float().numpy(), np.minimum(inds, E - 1), scores, hidden, inter, n, O.decode(O.CB_MCG))
+    y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                 torch.from_numpy(scores).to(dev), exl3.MCG)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_moe_sorted_and_per_slot_arms_agree(dev):
+    """The sorted arm (expert windows) and the per-slot chain give the same layer to the bar on one routing."""
+    import os
+
+    E, hidden, inter, k, rows, n = 32, 256, 256, 8, 24, 32
+    b = _to(synth.bank(11, "moea", E, hidden, inter, n), dev)
+    x = synth.normal(11, "x", (rows, hidden)).to(dev)
+    inds, scores = _route(11, rows, E, k)
+    xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
+    sorted_arm = exl3.moe(x, b, xi, sc, exl3.MCG).float().cpu().numpy()
+    os.environ["EXL3_MOE_WINDOWS"] = "0"
+    try:
+        per_slot = exl3.moe(x, b, xi, sc, exl3.MCG).float().cpu().numpy()
+    finally:
+        del os.environ["EXL3_MOE_WINDOWS"]
+    assert max_abs_rel(sorted_arm, per_slot) < BAR
 
 
 def test_router_matches_oracle(dev):
