@@ -121,7 +121,8 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
 
 size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
     size_t b = kCounterBytes + align_up((size_t)groups * rows * in * 2);
-    if (n % 16 != 0 || n > 64) b += align_up((size_t)groups * out * in * 2);
+    const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
+    if (!lane_reader) b += align_up((size_t)groups * out * in * 2);  // the transposed f16 copy of other rates
     return b;
 }
 

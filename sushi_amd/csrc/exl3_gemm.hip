@@ -10,6 +10,7 @@
 // with p = 2*(c / 8) + h % 2 (tensorCorePerm), i.e. eight codewords from one 2n-bit run of the tile stream.
 // Integer rates (n = 16K) use this reader; other rates are first decoded to a transposed f16 copy in workspace.
 #include "exl3_kernels.h"
+#include "exl3_lane_decode.h"
 
 namespace exl3 {
 
@@ -211,6 +212,164 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
     }
 }
 
+// ---- the decode-once GEMM (integer and half-integer rates with a lane reader: n = 16, 24, 32, 40, 48, 64)
+//
+// A workgroup (4 waves) owns a 256-row x 128-column output tile (one Hadamard block wide, so the FWHT + svh finish
+// runs in its epilogue) over all of k, in k-steps of 64 (four trellis k-tiles).  Per k-step, wave w decodes k-tile
+// row w of the group's 8 tiles with the GEMV's lane decoder (lane 8o + j: codewords 32j..32j+31 of tile o = columns
+// j and j+8 over 16 k rows) and writes the f16 weights once into an LDS slab held column-major (B[col][k]), double
+// buffered so the next slab is decoded while the current one feeds the MFMAs.  Each wave then runs its 64 rows x 128
+// columns as 4 x 8 v_mfma_f32_16x16x32_f16 tiles per 32 k, taking A fragments (16 rows x 8 k per lane) straight
+// from the prepared input in global memory and B fragments from the slab.  Every weight is decoded once per
+// 256-row tile instead of once per 128 rows per wave.
+constexpr int G2_WAVES = 4;
+constexpr int G2_THREADS = 64 * G2_WAVES;
+constexpr int G2_MT = 64 * G2_WAVES;  // rows per workgroup
+constexpr int G2_BP = 72;             // LDS pitch (halves) of one slab column: 64 k + 8 pad (16-byte aligned rows)
+constexpr int G2_EP = 129;            // epilogue staging pitch (floats)
+
+template <int FAM, int N>
+__global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int IT = a.in >> 4, OT = a.out >> 4;
+    const int og = blockIdx.x, g = blockIdx.z;
+    const int m0 = blockIdx.y * G2_MT + wave * 64;
+    __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
+
+    const int o = lane >> 3, j = lane & 7;   // decode lane: tile o of the group, chunk j
+    const int c = lane & 15, h = lane >> 4;  // MFMA lane: row / column c, k group h
+    constexpr int AW = LaneBits<N>::AW;
+    const DecodeK k = a.k;
+    const bool masked = k.wmask != 0xFFFFu;
+    const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N;
+
+    // A rows of this lane (rows past the end read row 0 and are zeroed)
+    const uint16_t *xrow[4];
+    bool rowok[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++) {
+        const int m = m0 + rb * 16 + c;
+        rowok[rb] = m < a.rows;
+        xrow[rb] = a.xp + ((size_t)g * a.rows + (rowok[rb] ? m : 0)) * a.in + 8 * h;
+    }
+    auto load_a = [&](int ks, uint4 (&A)[4][2]) {
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(xrow[rb] + ks * 64 + kb * 32);
+                A[rb][kb] = rowok[rb] ? v : uint4{0u, 0u, 0u, 0u};
+            }
+    };
+    auto load_tile = [&](int ks, uint32_t (&W)[AW]) {
+        const int tk = ks * 4 + wave;
+        load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * OT + og * 8 + o) * N), j, W);
+    };
+    auto decode_store = [&](const uint32_t (&W)[AW], uint16_t *slab) {
+        uint32_t w[16];
+        if (masked) decode_weights<FAM, N, true>(W, k, w);
+        else decode_weights<FAM, N, false>(W, k, w);
+        if constexpr (family_scaled<FAM>()) {  // MFMA takes the weight itself: fold the 2^12 back in (exact)
+#pragma unroll
+            for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
+        }
+        // column j: rows 0-7 = pairs 0, 4, 8, 12; rows 8-15 = 1, 5, 9, 13; column j + 8: 2, 6, 10, 14 and 3, 7, 11, 15
+        uint16_t *cj = slab + (o * 16 + j) * G2_BP + wave * 16;
+        uint16_t *cj8 = cj + 8 * G2_BP;
+        *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
+        *reinterpret_cast<uint4 *>(cj + 8) = uint4{w[1], w[5], w[9], w[13]};
+        *reinterpret_cast<uint4 *>(cj8) = uint4{w[2], w[6], w[10], w[14]};
+        *reinterpret_cast<uint4 *>(cj8 + 8) = uint4{w[3], w[7], w[11], w[15]};
+    };
+
+    f4_t acc[4][8];
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int nks = IT / 4;
+    uint4 Af[4][2];
+    {
+        uint32_t W[AW];
+        load_tile(0, W);
+        load_a(0, Af);
+        decode_store(W, Bs[0]);
+    }
+    __syncthreads();
+    for (int ks = 0; ks < nks; ks++) {
+        const bool more = ks + 1 < nks;
+        uint32_t Wn[AW];
+        uint4 An[4][2];
+        if (more) {
+            load_tile(ks + 1, Wn);
+            load_a(ks + 1, An);
+        }
+        const uint16_t *slab = Bs[ks & 1];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+            for (int cb = 0; cb < 8; cb++) {
+                const uint4 bv = *reinterpret_cast<const uint4 *>(slab + (cb * 16 + c) * G2_BP + kb * 32 + 8 * h);
+                const h8_t B8 = __builtin_bit_cast(h8_t, bv);
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, Af[rb][kb]), B8,
+                                                                         acc[rb][cb], 0, 0, 0);
+            }
+        }
+        if (more) {
+            decode_store(Wn, Bs[(ks + 1) & 1]);
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) Af[rb][kb] = An[rb][kb];
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: each wave stages 16 of its rows at a time in LDS (its own region of the slab space), then
+    // FWHT-128 + svh per row
+    float *ep = reinterpret_cast<float *>(&Bs[0][0]) + wave * 16 * G2_EP;
+    const size_t sv = (size_t)g * a.out + (size_t)og * 128;
+    const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++) {
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) ep[(4 * h + i) * G2_EP + cb * 16 + c] = acc[rb][cb][i];
+        __builtin_amdgcn_wave_barrier();
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + rb * 16 + r;
+            if (m >= a.rows) break;
+            float v0 = ep[r * G2_EP + lane], v1 = ep[r * G2_EP + lane + 64];
+            fwht128_wave(v0, v1, lane);
+            const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128;
+            const float y0 = v0 * HAD_SCALE * s0, y1 = v1 * HAD_SCALE * s1;
+            if (a.y_dtype == DT_F16) {
+                store_act<DT_F16>(a.y, yo + lane, y0);
+                store_act<DT_F16>(a.y, yo + lane + 64, y1);
+            } else if (a.y_dtype == DT_BF16) {
+                store_act<DT_BF16>(a.y, yo + lane, y0);
+                store_act<DT_BF16>(a.y, yo + lane + 64, y1);
+            } else {
+                store_act<DT_F32>(a.y, yo + lane, y0);
+                store_act<DT_F32>(a.y, yo + lane + 64, y1);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <int FAM, int N>
+static hipError_t launch_gemm2_n(const GemmArgs &a, hipStream_t s) {
+    dim3 grid((unsigned)(a.out / 128), (unsigned)((a.rows + G2_MT - 1) / G2_MT), (unsigned)a.groups);
+    hipLaunchKernelGGL((gemm2_kernel<FAM, N>), grid, dim3(G2_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int FAM, int N>
 static hipError_t launch_gemm_n(const GemmArgs &a, const uint16_t *wt, hipStream_t s) {
     dim3 grid((unsigned)(a.out / 128), (unsigned)((a.rows + GM_MT - 1) / GM_MT), (unsigned)a.groups);
@@ -225,10 +384,12 @@ static hipError_t launch_gemm_fam(const GemmArgs &a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     switch (a.n) {
-    case 16: return launch_gemm_n<FAM, 16>(a, nullptr, s);
-    case 32: return launch_gemm_n<FAM, 32>(a, nullptr, s);
-    case 48: return launch_gemm_n<FAM, 48>(a, nullptr, s);
-    case 64: return launch_gemm_n<FAM, 64>(a, nullptr, s);
+    case 16: return launch_gemm2_n<FAM, 16>(a, s);
+    case 24: return launch_gemm2_n<FAM, 24>(a, s);
+    case 32: return launch_gemm2_n<FAM, 32>(a, s);
+    case 40: return launch_gemm2_n<FAM, 40>(a, s);
+    case 48: return launch_gemm2_n<FAM, 48>(a, s);
+    case 64: return launch_gemm2_n<FAM, 64>(a, s);
     default: break;
     }
     // Any other rate: decode to a transposed f16 copy in workspace (held after xp), then the same MFMA body.

@@ -20,6 +20,7 @@
 #pragma once
 #include "exl3_kernels.h"
 #include "exl3_tables.h"
+#include "exl3_lane_decode.h"
 
 namespace exl3 {
 
@@ -88,23 +89,6 @@ __device__ __forceinline__ int slot_of(const GemvCtx &c, int r) {
     else return c.g;
 }
 
-// Codeword v of the lane as (window index, high half?): for K = 1, 2, 4 the window ending at codeword v + 16/K
-// carries codeword v in its high half, so half the windows serve two codewords.
-template <int N>
-struct Pairing {
-    static constexpr bool ON = N == 16 || N == 32 || N == 64;
-    static constexpr int STEP = ON ? 256 / N : 32;
-    __device__ static constexpr bool hi(int v) { return ON && ((v / STEP) % 2 == 0); }
-    __device__ static constexpr int win(int v) { return hi(v) ? v + STEP : v; }
-};
-
-// A scheduling fence: nothing moves across it, so each phase below stays one batch of independent instructions.
-__device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// The 32 weights of one tile chunk (lane-owned columns j and j+8), dotted into acc0 (column j) / acc1 (column j+8).
-// Written in fenced phases (windows, product step 1, step 2, masks, low sums, high sums, dots): within a phase no
-// instruction depends on another, so no result is read by the instruction right after it and the hazard recognizer
-// inserts no wait states (gfx950 needs one between a 16-bit-lane or SDWA write and its reader).
 // Rows of the prepared input are read from LDS in chunks of XCH (all at once up to 8 rows): the fragments of the
 // first chunk are requested before the decode, so their LDS latency hides behind it.
 template <int RT>
@@ -122,75 +106,17 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[MAX_KSPAN], in
     }
 }
 
+// The 32 weights of one tile chunk (lane-owned columns j and j+8), dotted into acc0 (column j) / acc1 (column j+8).
 // `rows` (wave-uniform, <= RT) bounds the chunks that are dotted: rows past it hold zeros.
 template <int FAM, int N, int RT, bool MASKED>
 __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[MAX_KSPAN],
                                             int kk, int rows, const DecodeK &k, float (&acc0)[RT],
                                             float (&acc1)[RT]) {
-    using P = Pairing<N>;
     constexpr int CH = XChunk<RT>::CH;
     uint4 X[CH], Y[CH];
     load_x_chunk<RT>(xs, kk, 0, X, Y);
-    uint32_t win[32];
-#pragma unroll
-    for (int v = 0; v < 32; v++) {
-        if (P::win(v) == v) {
-            win[v] = lane_codeword<N>(A, v);
-            if constexpr (MASKED) win[v] &= k.wmask | (k.wmask << 16);
-        }
-    }
     uint32_t w[16];
-    if constexpr (FAM == FAM_PAIR) {
-        // both weights of a pair decode from the odd codeword (decodePair, expert_exl3.zig:298-301)
-        uint32_t pr[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int v = 2 * i + 1;
-            pr[i] = P::hi(v) ? mul16x32<true>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu)
-                             : mul16x32<false>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu);
-        }
-        uint32_t h0[16], h1[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            h0[i] = pr[i] & k.mask0;
-            h1[i] = __builtin_amdgcn_alignbit(pr[i], pr[i], 32u - k.rot) & k.mask1;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; i++) w[i] = pack_sums(h0[i], h1[i]);
-    } else if constexpr (FAM == FAM_MUL1) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t x0 = win[P::win(2 * i)], x1 = win[P::win(2 * i + 1)];
-            const uint32_t c0 = P::hi(2 * i) ? x0 >> 16 : x0, c1 = P::hi(2 * i + 1) ? x1 >> 16 : x1;
-            w[i] = pack_h2(decode1<FAM_MUL1>(c0, k), decode1<FAM_MUL1>(c1, k));
-        }
-    } else {
-        uint32_t h[32];
-        phase_fence();
-#pragma unroll
-        for (int v = 0; v < 32; v++)
-            h[v] = P::hi(v) ? hash_step1<FAM, true>(win[P::win(v)], k) : hash_step1<FAM, false>(win[P::win(v)], k);
-        phase_fence();
-#pragma unroll
-        for (int v = 0; v < 32; v++) {
-            if (P::hi(v)) hash_step2<FAM, true>(win[P::win(v)], k, h[v]);
-            else hash_step2<FAM, false>(win[P::win(v)], k, h[v]);
-        }
-        phase_fence();
-#pragma unroll
-        for (int v = 0; v < 32; v++) h[v] = hash_halves<FAM>(h[v], k);
-        phase_fence();
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
-                : "=v"(w[i]) : "v"(h[2 * i]));
-        phase_fence();
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-                : "+v"(w[i]) : "v"(h[2 * i + 1]));
-        phase_fence();
-    }
+    decode_weights<FAM, N, MASKED>(A, k, w);
     // pair i = (u, u+1), u = 2i = 8qq + 2p: p = 0/1 -> column j rows 2qq(+8), p = 2/3 -> column j+8
 #pragma unroll
     for (int r0 = 0; r0 < RT; r0 += CH) {

@@ -1,0 +1,93 @@
+// The lane decoder shared by the GEMV and the GEMM: one lane's 32 codewords of a 16x16 trellis tile, from its
+// aligned stream words, to 16 packed f16 weight pairs (t, t+1).  Lane chunk j of a tile holds codewords 32j..32j+31,
+// the weights of output columns j and j+8 over all 16 k rows (tensorCorePerm, beamivalice/sushi
+// src/exl3/expert_exl3.zig:379-398): pair i = 4qq + p covers rows 2qq + 8(p & 1) + {0, 1} of column j (p < 2) or
+// j + 8 (p >= 2).
+#pragma once
+#include "exl3_common.cuh"
+
+namespace exl3 {
+
+// Codeword v of the lane as (window index, high half?): for K = 1, 2, 4 the window ending at codeword v + 16/K
+// carries codeword v in its high half, so half the windows serve two codewords.
+template <int N>
+struct Pairing {
+    static constexpr bool ON = N == 16 || N == 32 || N == 64;
+    static constexpr int STEP = ON ? 256 / N : 32;
+    __device__ static constexpr bool hi(int v) { return ON && ((v / STEP) % 2 == 0); }
+    __device__ static constexpr int win(int v) { return hi(v) ? v + STEP : v; }
+};
+
+// A scheduling fence: nothing moves across it, so each phase below stays one batch of independent instructions.
+__device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// The weights of the lane's chunk, unscaled for the hash / pair families (the x4096 is applied by the caller).
+// Written in fenced phases (windows, product step 1, step 2, masks, low sums, high sums): within a phase no
+// instruction depends on another, so no result is read by the instruction right after it and the hazard recognizer
+// inserts no wait states (gfx950 needs one between a 16-bit-lane or SDWA write and its reader).
+template <int FAM, int N, bool MASKED>
+__device__ __forceinline__ void decode_weights(const uint32_t (&A)[LaneBits<N>::AW], const DecodeK &k,
+                                               uint32_t (&w)[16]) {
+    using P = Pairing<N>;
+    uint32_t win[32];
+#pragma unroll
+    for (int v = 0; v < 32; v++) {
+        if (P::win(v) == v) {
+            win[v] = lane_codeword<N>(A, v);
+            if constexpr (MASKED) win[v] &= k.wmask | (k.wmask << 16);
+        }
+    }
+    if constexpr (FAM == FAM_PAIR) {
+        // both weights of a pair decode from the odd codeword (decodePair, expert_exl3.zig:298-301)
+        uint32_t pr[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int v = 2 * i + 1;
+            pr[i] = P::hi(v) ? mul16x32<true>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu)
+                             : mul16x32<false>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu);
+        }
+        uint32_t h0[16], h1[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            h0[i] = pr[i] & k.mask0;
+            h1[i] = __builtin_amdgcn_alignbit(pr[i], pr[i], 32u - k.rot) & k.mask1;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = pack_sums(h0[i], h1[i]);
+    } else if constexpr (FAM == FAM_MUL1) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t x0 = win[P::win(2 * i)], x1 = win[P::win(2 * i + 1)];
+            const uint32_t c0 = P::hi(2 * i) ? x0 >> 16 : x0, c1 = P::hi(2 * i + 1) ? x1 >> 16 : x1;
+            w[i] = pack_h2(decode1<FAM_MUL1>(c0, k), decode1<FAM_MUL1>(c1, k));
+        }
+    } else {
+        uint32_t h[32];
+        phase_fence();
+#pragma unroll
+        for (int v = 0; v < 32; v++)
+            h[v] = P::hi(v) ? hash_step1<FAM, true>(win[P::win(v)], k) : hash_step1<FAM, false>(win[P::win(v)], k);
+        phase_fence();
+#pragma unroll
+        for (int v = 0; v < 32; v++) {
+            if (P::hi(v)) hash_step2<FAM, true>(win[P::win(v)], k, h[v]);
+            else hash_step2<FAM, false>(win[P::win(v)], k, h[v]);
+        }
+        phase_fence();
+#pragma unroll
+        for (int v = 0; v < 32; v++) h[v] = hash_halves<FAM>(h[v], k);
+        phase_fence();
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+                : "=v"(w[i]) : "v"(h[2 * i]));
+        phase_fence();
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+                : "+v"(w[i]) : "v"(h[2 * i + 1]));
+        phase_fence();
+    }
+}
+
+}  // namespace exl3
