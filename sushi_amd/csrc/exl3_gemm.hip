@@ -218,10 +218,10 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
 // runs in its epilogue) over all of k, in k-steps of 64 (four trellis k-tiles).  Per k-step, wave w decodes k-tile
 // row w of the group's 8 tiles with the GEMV's lane decoder (lane 8o + j: codewords 32j..32j+31 of tile o = columns
 // j and j+8 over 16 k rows) and writes the f16 weights once into an LDS slab held column-major (B[col][k]), double
-// buffered so the next slab is decoded while the current one feeds the MFMAs.  Each wave then runs its 64 rows x 128
+// buffered so the next slab is decoded while the current one feeds the MFMAs.  Each wave runs its 64 rows x 128
 // columns as 4 x 8 v_mfma_f32_16x16x32_f16 tiles per 32 k, taking A fragments (16 rows x 8 k per lane) straight
-// from the prepared input in global memory and B fragments from the slab.  Every weight is decoded once per
-// 256-row tile instead of once per 128 rows per wave.
+// from the prepared input in global memory (two register sets, alternating steps) and B fragments from the slab.
+// Every weight is decoded once per 256-row tile instead of once per 128 rows per wave.
 constexpr int G2_WAVES = 4;
 constexpr int G2_THREADS = 64 * G2_WAVES;
 constexpr int G2_MT = 64 * G2_WAVES;  // rows per workgroup
@@ -233,8 +233,22 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int IT = a.in >> 4, OT = a.out >> 4;
-    const int og = blockIdx.x, g = blockIdx.z;
-    const int m0 = blockIdx.y * G2_MT + wave * 64;
+    // Workgroups go round-robin over the 8 XCDs (block L on XCD L % 8), and each XCD has its own L2.  When the row
+    // tiles divide the XCDs, give every XCD whole row tiles: the A rows a tile reads then stay in that XCD's L2 for
+    // all of its column blocks.
+    const int nog = a.out / 128, nm = (a.rows + G2_MT - 1) / G2_MT;
+    const int L = blockIdx.x;
+    int og, mt;
+    if (nm <= 8 && 8 % nm == 0 && nog % (8 / nm) == 0) {
+        const int xcd = L & 7, per = 8 / nm;
+        mt = xcd / per;
+        og = (L >> 3) * per + xcd % per;
+    } else {
+        og = L % nog;
+        mt = L / nog;
+    }
+    const int g = blockIdx.z;
+    const int m0 = mt * G2_MT + wave * 64;
     __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
 
     const int o = lane >> 3, j = lane & 7;   // decode lane: tile o of the group, chunk j
@@ -244,23 +258,20 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
     const bool masked = k.wmask != 0xFFFFu;
     const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N;
 
-    // A rows of this lane (rows past the end read row 0 and are zeroed)
+    // A rows of this lane.  A row past the end reads row 0 instead: each output row depends on its own A row only,
+    // and the epilogue never stores rows past the end, so nothing has to be zeroed (a select on the loaded value would
+    // make every prefetch wait for its data where it is issued).
     const uint16_t *xrow[4];
-    bool rowok[4];
 #pragma unroll
     for (int rb = 0; rb < 4; rb++) {
         const int m = m0 + rb * 16 + c;
-        rowok[rb] = m < a.rows;
-        xrow[rb] = a.xp + ((size_t)g * a.rows + (rowok[rb] ? m : 0)) * a.in + 8 * h;
+        xrow[rb] = a.xp + ((size_t)g * a.rows + (m < a.rows ? m : 0)) * a.in + 8 * h;
     }
     auto load_a = [&](int ks, uint4 (&A)[4][2]) {
 #pragma unroll
         for (int rb = 0; rb < 4; rb++)
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(xrow[rb] + ks * 64 + kb * 32);
-                A[rb][kb] = rowok[rb] ? v : uint4{0u, 0u, 0u, 0u};
-            }
+            for (int kb = 0; kb < 2; kb++) A[rb][kb] = *reinterpret_cast<const uint4 *>(xrow[rb] + ks * 64 + kb * 32);
     };
     auto load_tile = [&](int ks, uint32_t (&W)[AW]) {
         const int tk = ks * 4 + wave;
@@ -289,23 +300,18 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
 #pragma unroll
         for (int cb = 0; cb < 8; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int nks = IT / 4;
-    uint4 Af[4][2];
-    {
-        uint32_t W[AW];
-        load_tile(0, W);
-        load_a(0, Af);
-        decode_store(W, Bs[0]);
-    }
-    __syncthreads();
-    for (int ks = 0; ks < nks; ks++) {
-        const bool more = ks + 1 < nks;
+    // One k-step: issue the loads of the next step (tile words, A fragments into `an`), run this step's MFMAs from
+    // the slab and `ac`, decode the next slab, barrier.  Steps alternate the two A register sets, so each MFMA reads
+    // fragments loaded a whole step earlier and no register copy waits for a load.  The next step's loads and decode
+    // are unconditional (the last step re-reads step nks - 1 and decodes into the idle slab): a branch around them
+    // would make the compiler's load counting assume the branch-free path and wait for loads issued in this step.
+    const int nks = IT / 4;  // even: in is a multiple of 128
+    auto step = [&](int ks, const uint4 (&ac)[4][2], uint4 (&an)[4][2]) {
+        const int kn = min(ks + 1, nks - 1);
         uint32_t Wn[AW];
-        uint4 An[4][2];
-        if (more) {
-            load_tile(ks + 1, Wn);
-            load_a(ks + 1, An);
-        }
+        load_tile(kn, Wn);
+        load_a(kn, an);
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads at the top of the step (the scheduler sinks them)
         const uint16_t *slab = Bs[ks & 1];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
@@ -315,18 +321,24 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
                 const h8_t B8 = __builtin_bit_cast(h8_t, bv);
 #pragma unroll
                 for (int rb = 0; rb < 4; rb++)
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, Af[rb][kb]), B8,
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, ac[rb][kb]), B8,
                                                                          acc[rb][cb], 0, 0, 0);
             }
         }
-        if (more) {
-            decode_store(Wn, Bs[(ks + 1) & 1]);
-#pragma unroll
-            for (int rb = 0; rb < 4; rb++)
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) Af[rb][kb] = An[rb][kb];
-        }
+        decode_store(Wn, Bs[(ks + 1) & 1]);
         __syncthreads();
+    };
+    uint4 A0[4][2], A1[4][2];
+    {
+        uint32_t W[AW];
+        load_tile(0, W);
+        load_a(0, A0);
+        decode_store(W, Bs[0]);
+    }
+    __syncthreads();
+    for (int ks = 0; ks < nks; ks += 2) {
+        step(ks, A0, A1);
+        step(ks + 1, A1, A0);
     }
 
     // ---- epilogue: each wave stages 16 of its rows at a time in LDS (its own region of the slab space), then
@@ -365,7 +377,7 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
 
 template <int FAM, int N>
 static hipError_t launch_gemm2_n(const GemmArgs &a, hipStream_t s) {
-    dim3 grid((unsigned)(a.out / 128), (unsigned)((a.rows + G2_MT - 1) / G2_MT), (unsigned)a.groups);
+    dim3 grid((unsigned)((a.out / 128) * ((a.rows + G2_MT - 1) / G2_MT)), 1, (unsigned)a.groups);
     hipLaunchKernelGGL((gemm2_kernel<FAM, N>), grid, dim3(G2_THREADS), 0, s, a);
     return hipGetLastError();
 }

@@ -151,6 +151,15 @@ def test_gemm_arm(dev, rows, n):
     assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 512, 256, n, odec)) < BAR
 
 
+@pytest.mark.parametrize("in_f,rows", [(128, 20), (384, 40), (640, 300)])
+def test_gemm_odd_k_steps_and_row_tails(dev, in_f, rows):
+    """k spans of 1, 3 and 5 GEMM k-steps (the unrolled step pair plus a tail step) and row counts that leave a
+    partial 256-row tile."""
+    p, pd, x, xd = _case(dev, 60 + in_f, rows, in_f, 256, 48)
+    dec, odec = DECODES["3inst"]
+    assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, in_f, 256, 48, odec)) < BAR
+
+
 @pytest.mark.parametrize("label", ["spec1", "pair1", "mul1"])
 def test_gemm_codebooks(dev, label):
     p, pd, x, xd = _case(dev, 77, 24, 256, 256, 48)
