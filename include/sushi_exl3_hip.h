@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 1
+#define EXL3_ABI_VERSION 2
 
 /* Codebook: the reference's `Codebook` enum values (src/exl3/expert_exl3.zig:54-61), plus 3INST as an
  * extension (QTIP's LCG codebook, not in the reference). */
@@ -106,6 +106,10 @@ typedef struct {
     const uint16_t *svh[3];
     const uint32_t *meta; /* device [experts][8] */
     int32_t experts;
+    /* Nonzero promises that every rate in `meta` is one of 16, 24, 32, 40, 48, 64 (the host builder knows the
+     * rates, `rate_groups.zig` groups them); the library then skips the launch that serves any other rate.
+     * Zero (the default of a zeroed struct) is always correct. */
+    int32_t lane_rates_only;
 } exl3_ragged_t;
 
 int32_t exl3_abi_version(void);

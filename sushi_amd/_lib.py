@@ -43,7 +43,7 @@ class BankT(ctypes.Structure):
 
 class RaggedT(ctypes.Structure):
     _fields_ = [("trellis", ctypes.c_void_p * 3), ("suh", ctypes.c_void_p * 3), ("svh", ctypes.c_void_p * 3),
-                ("meta", ctypes.c_void_p), ("experts", ctypes.c_int32)]
+                ("meta", ctypes.c_void_p), ("experts", ctypes.c_int32), ("lane_rates_only", ctypes.c_int32)]
 
 
 _lib = None

@@ -258,7 +258,7 @@ int32_t moe_common_checks(int32_t x_dtype, int32_t y_dtype, int32_t rows, int32_
 int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t x_dtype, int32_t rows,
                    int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
                    const uint16_t *const su[3], const uint16_t *const sv[3], int n_uniform, const uint32_t *meta,
-                   const uint32_t *inds, const float *scores, int32_t topk, int32_t clamp_limit, const void *shared,
+                   int meta_lane_only, const uint32_t *inds, const float *scores, int32_t topk, int32_t clamp_limit, const void *shared,
                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
@@ -311,6 +311,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     a.bank_of = inds;
     a.bank_limit = experts;
     a.meta = meta;
+    a.meta_lane_only = meta_lane_only;
     a.table = table;
     a.k = k;
     a.out_scale = scale;
@@ -350,6 +351,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     d.bank_of = inds;
     d.bank_limit = experts;
     d.meta = meta;
+    d.meta_lane_only = meta_lane_only;
     d.table = table;
     d.k = k;
     d.out_scale = scale;
@@ -480,7 +482,7 @@ int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, i
     const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
     const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
     return moe_launch(fam, k, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, bank->gate.n, nullptr,
-                      inds, scores, topk, clamp_limit, shared, y, y_dtype, workspace, workspace_bytes, stream);
+                      0, inds, scores, topk, clamp_limit, shared, y, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
@@ -501,8 +503,8 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: null operand");
     const int table = fam == FAM_PAIR ? (int)TABLE_PAIR1_W16_V1 : dec.table;
     return moe_launch(fam, k, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
-                      bank->svh, 0, bank->meta, inds, scores, topk, clamp_limit, shared, y, y_dtype, workspace,
-                      workspace_bytes, stream);
+                      bank->svh, 0, bank->meta, bank->lane_rates_only != 0, inds, scores, topk, clamp_limit, shared,
+                      y, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds, float *scores,

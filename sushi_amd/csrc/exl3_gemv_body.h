@@ -159,8 +159,9 @@ __device__ __forceinline__ float load_x_nb(const void *x, int dt, size_t i) {
 // are unconditional (a job past the end re-reads job 0 and is then discarded): no branch, so no early wait.
 template <int RT>
 struct PrologueRegs {
-    // jobs per wave when a split spans at most TPW * GEMV_WAVES k-tiles (TPW * GEMV_WAVES / 8 blocks per row)
-    static constexpr int JOBS = (RT * TPW / 8) < 1 ? 1 : (RT * TPW / 8);
+    // jobs per wave when a split spans at most TPW * GEMV_WAVES k-tiles (TPW * GEMV_WAVES / 8 blocks per row), at
+    // most 4 held in registers (past that the prologue loads as it goes: 16 rows would otherwise spill)
+    static constexpr int JOBS = (RT * TPW / 8) < 1 ? 1 : (RT * TPW / 8) > 4 ? 4 : (RT * TPW / 8);
     float x0[JOBS], x1[JOBS], s0[JOBS], s1[JOBS];
 };
 
@@ -433,7 +434,8 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
     return k;
 }
 
-// N > 0: one rate for the launch; N == 0: the generic reader; N < 0: per-expert rate from the ragged meta table,
+// N > 0: one rate for the launch; N == 0: the generic reader; N == -1 / -2: per-expert rate from the ragged meta table
+// (lane-reader rates / the other rates),
 // dispatched per workgroup.
 template <int FAM, int N, int RT, int PRO, bool WIN>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
@@ -489,17 +491,27 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
         const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
         gemv_body<FAM, N, RT, PRO, WIN>(a, c, tb, n, a.k, xs, red);
     } else {
+        // Ragged bank: the rate comes from the expert's meta row.  N == -1 serves the rates with a lane reader and
+        // skips the rest; N == -2 (a second launch over the same grid) serves only the rest, with the generic reader
+        // (kept out of the first kernel, whose registers it would otherwise set).
         const int col = p1 ? a.meta_col[1] : a.meta_col[0];
         const uint32_t *m = a.meta + (size_t)c.bank * 8;
         const int n = (int)m[col];
         const uint16_t *tb = trellis + 2 * (size_t)m[4 + col];
         const DecodeK k = rate_constants<FAM>(a, n);
-        switch (n) {
-        case 16: gemv_body<FAM, 16, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-        case 32: gemv_body<FAM, 32, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-        case 48: gemv_body<FAM, 48, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-        case 64: gemv_body<FAM, 64, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-        default: gemv_body<FAM, 0, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+        const bool lane_rate = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
+        if constexpr (N == -1) {
+            switch (n) {
+            case 16: gemv_body<FAM, 16, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            case 24: gemv_body<FAM, 24, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            case 32: gemv_body<FAM, 32, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            case 40: gemv_body<FAM, 40, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            case 48: gemv_body<FAM, 48, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            case 64: gemv_body<FAM, 64, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            default: break;
+            }
+        } else {
+            if (!lane_rate) gemv_body<FAM, 0, RT, PRO, WIN>(a, c, tb, n, k, xs, red);
         }
     }
 }
@@ -555,7 +567,10 @@ static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
 
 template <int FAM, int PRO>
 static hipError_t launch_gemv_fam(const GemvArgs &a, hipStream_t s) {
-    if (a.meta) return launch_gemv_n<FAM, -1, PRO>(a, s);
+    if (a.meta) {  // ragged: the lane-reader rates, then any other rate (unless the host ruled them out)
+        hipError_t e = launch_gemv_n<FAM, -1, PRO>(a, s);
+        return e != hipSuccess || a.meta_lane_only ? e : launch_gemv_n<FAM, -2, PRO>(a, s);
+    }
     switch (a.n) {
     case 16: return launch_gemv_n<FAM, 16, PRO>(a, s);
     case 24: return launch_gemv_n<FAM, 24, PRO>(a, s);

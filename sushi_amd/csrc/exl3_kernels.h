@@ -46,6 +46,7 @@ struct GemvArgs {
     int n;                   // uniform rate; 0 with `meta` = per-expert rates
     const uint32_t *bank_of; // [groups] expert id, or null (bank = group)
     const uint32_t *meta;    // ragged meta [E][8]: n at col pi, word offset at col 4 + pi
+    int meta_lane_only;      // every ragged rate is a lane-reader rate: no launch for the other rates
     int meta_col[2];
     int table;               // codebook table for per-rate rows (ragged hash / pair families)
     int bank_limit;          // expert count: ids are clamped below it (memory safety on bad routing)

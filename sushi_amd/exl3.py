@@ -237,6 +237,9 @@ class Bank:
 
 META_WORDS = 8
 
+# Rates the kernels read with a per-lane fixed-width reader; any other rate takes the generic reader.
+LANE_RATES = (16, 24, 32, 40, 48, 64)
+
 
 @dataclass
 class Ragged:
@@ -298,6 +301,7 @@ class Ragged:
             r.svh[i] = self.svh[i].data_ptr()
         r.meta = self.meta.data_ptr()
         r.experts = self.experts
+        r.lane_rates_only = int(all(n in LANE_RATES for group in self.rates for n in group))
         return r
 
 

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_host_side_refusals():
     lib = L.load()
-    assert lib.exl3_abi_version() == 1
+    assert lib.exl3_abi_version() == 2
     d = L.DecodeT(1, 16, -1)
     # bad shape: in not a multiple of 128 -> refused before any launch (null pointers never touched)
     assert lib.exl3_linear(None, 0, 1, 100, 128, None, 64, None, None, d, None, 0, None, 0, None) == -1

@@ -88,10 +88,15 @@ def test_moe_with_shared_and_clamped(dev, rows):
     assert max_abs_rel(wantc, want) > 10 * BAR  # the clamp is live on this data
 
 
-@pytest.mark.parametrize("rows", [3, 21])
-def test_moe_ragged_rate_groups(dev, rows):
+@pytest.mark.parametrize("rows,groups", [
+    (3, [(6, (32, 32, 48)), (10, (16, 16, 32))]),
+    (21, [(6, (32, 32, 48)), (10, (16, 16, 32))]),
+    # rates off the lane-reader set (20, 36, 56) beside lane rates: both ragged launches must run
+    (3, [(6, (20, 32, 56)), (10, (16, 36, 32))]),
+    (21, [(6, (20, 32, 56)), (10, (16, 36, 32))]),
+])
+def test_moe_ragged_rate_groups(dev, rows, groups):
     hidden, inter, k = 256, 256, 4
-    groups = [(6, (32, 32, 48)), (10, (16, 16, 32))]
     banks = [synth.bank(20 + g, f"rg{g}", e, hidden, inter, rates) for g, (e, rates) in enumerate(groups)]
     rb = exl3.Ragged.init([_to(b, dev) for b in banks])
     E = sum(e for e, _ in groups)
@@ -110,6 +115,31 @@ def test_moe_ragged_rate_groups(dev, rows):
     y = exl3.moe_ragged(x.to(dev), rb, torch.from_numpy(inds.view(np.int32)).to(dev),
                         torch.from_numpy(scores).to(dev), exl3.MCG)
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+    lane_only = all(n in exl3.LANE_RATES for _, rates in groups for n in rates)
+    assert rb.c().lane_rates_only == int(lane_only)
+
+
+def test_moe_ragged_lane_flag_clear_is_correct(dev, monkeypatch):
+    """A zeroed `lane_rates_only` (the C default) also runs the generic-rate launch; the result must not change."""
+    hidden, inter, k, rows = 256, 128, 4, 5
+    groups = [(5, (16, 32, 48)), (7, (64, 24, 40))]
+    banks = [synth.bank(60 + g, f"lf{g}", e, hidden, inter, rates) for g, (e, rates) in enumerate(groups)]
+    rb = exl3.Ragged.init([_to(b, dev) for b in banks])
+    E = sum(e for e, _ in groups)
+    x = synth.normal(60, "x", (rows, hidden)).to(dev)
+    inds, scores = _route(60, rows, E, k)
+    xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
+    assert rb.c().lane_rates_only == 1
+    y1 = exl3.moe_ragged(x, rb, xi, sc, exl3.MCG)
+    c0 = exl3.Ragged.c
+
+    def cleared(self):
+        r = c0(self)
+        r.lane_rates_only = 0
+        return r
+    monkeypatch.setattr(exl3.Ragged, "c", cleared)
+    y0 = exl3.moe_ragged(x, rb, xi, sc, exl3.MCG)
+    assert torch.equal(y0, y1)
 
 
 def test_moe_ragged_stq_rates_k1_k2(dev):
