@@ -145,9 +145,9 @@ int32_t exl3_linear_grouped(const void *x, int32_t x_dtype, int32_t groups, int3
                             const uint16_t *svh, exl3_decode_t dec, void *y, int32_t y_dtype, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
-/* Clears a workspace once after allocation.  Every workspace begins with a 1 MiB region of fused-finish
- * arrival counters that must start at zero; the calls that use them always leave them at zero again, and no other
- * call writes there, so one init per allocation suffices.  Calls that share a workspace must not overlap in time
+/* Clears a workspace once after allocation.  Every workspace begins with a 4 MiB region of fused-finish
+ * arrival counters and accumulators that must start at zero; the calls that use them always leave them at zero
+ * again, and no other call writes there, so one init per allocation suffices.  Calls that share a workspace must not overlap in time
  * (they would race on its scratch).  A small fill kernel, never hipMemsetAsync. */
 int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
 

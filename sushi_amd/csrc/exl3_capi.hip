@@ -43,13 +43,15 @@ int32_t launched(hipError_t e, const char *what) {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Every workspace starts with a fixed region of fused-finish arrival counters.  Only the fused-finish GEMV touches
-// it, and every such launch leaves its counters at zero again, so the region stays valid across calls of any arm
+// Every workspace starts with a fixed region that stays zero between calls.  Only the fused-finish GEMV touches it,
+// either as arrival counters (its first MiB) or as the fold's 64-bit accumulators (the whole region), and every such
+// launch leaves what it touched at zero again, so the region stays valid across calls of any arm
 // (exl3_workspace_init zeroes it once after allocation).  Scratch of every arm begins after it.
 // Each counter owns a 128-byte line (COUNTER_STRIDE words): the splits of different output groups then never
 // contend for one line in the L2's atomic unit.
-constexpr size_t kCounterBytes = size_t(1) << 20;
-constexpr size_t kCounterSlots = kCounterBytes / (sizeof(uint32_t) * COUNTER_STRIDE);
+constexpr size_t kZeroBytes = size_t(4) << 20;
+constexpr size_t kCounterSlots = (size_t(1) << 20) / (sizeof(uint32_t) * COUNTER_STRIDE);
+constexpr size_t kFoldWords = kZeroBytes / sizeof(unsigned long long);
 
 bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
 
@@ -114,13 +116,13 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
     p.splits = env_int("EXL3_GEMV_SPLITS", 0);
     const int blocks = in / 128;
     if (p.splits <= 0 || blocks % p.splits != 0 || in / p.splits > 2048) p.splits = gemv_default_splits(in, out, rows, groups);
-    p.counters_bytes = kCounterBytes;
+    p.counters_bytes = kZeroBytes;
     p.partial_bytes = p.splits > 1 ? align_up((size_t)groups * p.splits * rows * out * sizeof(float)) : 0;
     return p;
 }
 
 size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
-    size_t b = kCounterBytes + align_up((size_t)groups * rows * in * 2);
+    size_t b = kZeroBytes + align_up((size_t)groups * rows * in * 2);
     const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
     if (!lane_reader) b += align_up((size_t)groups * out * in * 2);  // the transposed f16 copy of other rates
     return b;
@@ -183,6 +185,12 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.fused_finish = (env_int("EXL3_GEMV_SEPARATE_FINISH", 0) == 0 &&
                           (size_t)groups * (out / 128) <= kCounterSlots) ? 1 : 0;
         a.partial_only = 0;
+        // The fold (exact fixed-point accumulation, one atomic round trip per split) serves the fused finish whenever
+        // its words fit the zeroed region and the splits fit its count field; the counters + planes arm otherwise.
+        a.fold = (a.fused_finish && p.splits > 1 && p.splits <= FOLD_MAX_SPLITS &&
+                  (size_t)groups * rows * out <= kFoldWords && env_int("EXL3_GEMV_FOLD", 1) != 0)
+                     ? reinterpret_cast<unsigned long long *>(w)
+                     : nullptr;
         return launched(run_gemv(fam, PRO_X, a, stream), "exl3_linear (gemv)");
     }
     GemmArgs g{};
@@ -196,8 +204,8 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     g.suh = suh;
     g.svh = svh;
     g.k = k;
-    g.xp = reinterpret_cast<uint16_t *>(w + kCounterBytes);
-    g.wt = reinterpret_cast<uint16_t *>(w + kCounterBytes + align_up((size_t)groups * rows * in * 2));
+    g.xp = reinterpret_cast<uint16_t *>(w + kZeroBytes);
+    g.wt = reinterpret_cast<uint16_t *>(w + kZeroBytes + align_up((size_t)groups * rows * in * 2));
     g.y = y;
     g.y_dtype = y_dtype;
     g.groups = groups;
@@ -213,7 +221,7 @@ struct MoePlan {
     bool windowed;
     int s1, s2;
     size_t gu_bytes, down_bytes, table_bytes;
-    size_t total() const { return kCounterBytes + 2 * gu_bytes + down_bytes + table_bytes; }
+    size_t total() const { return kZeroBytes + 2 * gu_bytes + down_bytes + table_bytes; }
 };
 
 MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
@@ -266,7 +274,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     const size_t need = p.total();
     if (ws_bytes < need || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
         return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
-    char *w = static_cast<char *>(ws) + kCounterBytes;
+    char *w = static_cast<char *>(ws) + kZeroBytes;
     float *gate_part = reinterpret_cast<float *>(w);
     float *up_part = reinterpret_cast<float *>(w + p.gu_bytes);
     float *down_part = reinterpret_cast<float *>(w + 2 * p.gu_bytes);

@@ -272,6 +272,61 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
     }
 }
 
+// One output's fixed-point term: the arrival count plus either the biased 24-bit-fraction value or, for a value that
+// is not finite or not below 2^21 in magnitude, a mark in the non-finite field.  v * 2^24 is exact in f32 and below
+// 2^45, and rintf rounds it to the nearest integer.
+__device__ __forceinline__ unsigned long long fold_term(float v) {
+    const unsigned long long one = 1ull << FOLD_COUNT_SHIFT;
+    if (!(fabsf(v) < 2097152.0f)) return one | (1ull << FOLD_BAD_SHIFT);  // NaN fails the compare as well
+    const long long q = (long long)rintf(v * 16777216.0f);
+    return one + (unsigned long long)(q + FOLD_BIAS);
+}
+
+// The output value of a word that holds all S arrivals: NaN if any contribution was marked, else the exact sum.
+__device__ __forceinline__ float fold_value(unsigned long long t, int S) {
+    const int bad = (int)((t >> FOLD_BAD_SHIFT) & 63u);
+    const long long sum = (long long)(t & ((1ull << FOLD_BAD_SHIFT) - 1)) - (long long)(S - bad) * FOLD_BIAS;
+    return bad ? __builtin_nanf("") : (float)((double)sum * (1.0 / 16777216.0));
+}
+
+// Fused split-k finish by exact accumulation.  The output transform (FWHT-128, then * svh) is linear, so each split
+// applies it to its own partial and the sum of the transformed partials is the transformed sum.  Each split adds
+// its 24-bit-fraction fixed-point terms, together with an arrival count, into one 64-bit word per output with a
+// single atomic that returns the previous word; the split whose add completes the count holds the whole sum, stores
+// y and clears the word for the next call.  Integer addition makes the result independent of arrival order, and
+// neither partial planes nor a second round trip (store acknowledgement, then counter) sit on the path.  Wave w
+// finishes rows w, w + GEMV_WAVES, ...
+template <int RT>
+__device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c, float (*red)[RT][128], int wave,
+                                            int lane) {
+    for (int r = wave; r < c.rows; r += GEMV_WAVES) {
+        float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < GEMV_WAVES; w++) {
+            v0 += red[w][r][lane];
+            v1 += red[w][r][lane + 64];
+        }
+        v0 *= a.out_scale;
+        v1 *= a.out_scale;
+        fwht128_wave(v0, v1, lane);
+        const unsigned long long t0 = fold_term(v0 * HAD_SCALE * c.sv0);
+        const unsigned long long t1 = fold_term(v1 * HAD_SCALE * c.sv1);
+        const size_t yo = ((size_t)c.g * a.rows + r) * a.out + (size_t)c.og * 128;
+        unsigned long long *w0 = a.fold + yo + lane, *w1 = w0 + 64;
+        const unsigned long long o0 = __hip_atomic_fetch_add(w0, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long o1 = __hip_atomic_fetch_add(w1, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long last = (unsigned long long)(c.S - 1);
+        if ((o0 >> FOLD_COUNT_SHIFT) == last) {
+            store_y(a.y, a.y_dtype, yo + lane, fold_value(o0 + t0, c.S));
+            __hip_atomic_store(w0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if ((o1 >> FOLD_COUNT_SHIFT) == last) {
+            store_y(a.y, a.y_dtype, yo + lane + 64, fold_value(o1 + t1, c.S));
+            __hip_atomic_store(w1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 template <int FAM, int N, int RT, int PRO, bool WIN>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
@@ -373,6 +428,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
         }
         __syncthreads();
         for (int r = wave; r < a.rows; r += GEMV_WAVES) finish_block(a, c, r, red[0][r][lane], red[0][r][lane + 64], lane);
+        return;
+    }
+    if (a.fold) {
+        fold_finish(a, c, red, wave, lane);
         return;
     }
     // Split k: wave 0 alone sums the workgroup's partial, stores it, arrives at the output group's counter and, if it

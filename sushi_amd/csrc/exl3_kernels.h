@@ -15,6 +15,15 @@ enum Prologue : int { PRO_X = 0, PRO_MID = 1 };
 // Fused-finish arrival counters sit one per 128-byte line (32 words) in the workspace's counter region.
 constexpr int COUNTER_STRIDE = 32;
 
+// Fixed-point fused finish (the fold): one 64-bit word per output holds the arrival count in bits 63..58 (so at
+// most FOLD_MAX_SPLITS splits), the count of non-finite or out-of-range contributions in bits 57..52, and in bits
+// 51..0 the sum of the splits' biased terms q + FOLD_BIAS, q = round(v * 2^FOLD_FRAC) for |v| < 2^21.
+constexpr int FOLD_MAX_SPLITS = 63;
+constexpr int FOLD_COUNT_SHIFT = 58;
+constexpr int FOLD_BAD_SHIFT = 52;
+constexpr int FOLD_FRAC = 24;
+constexpr long long FOLD_BIAS = 1LL << 45;
+
 // GEMV workgroup shape: GEMV_WAVES waves, each loading up to TPW k-tiles of the output group before its prologue.
 // One workgroup per CU (256 CUs) is the target grid.
 constexpr int GEMV_WAVES = 8;
@@ -54,6 +63,7 @@ struct GemvArgs {
     float out_scale;
     float *partial[2];       // [groups][splits][rows][out] f32
     uint32_t *counters;      // [groups][out/128], zero between calls
+    unsigned long long *fold; // fixed-point fused finish: [groups][rows][out] words, zero between calls; null = off
     void *y;
     int y_dtype;
     int splits;

@@ -73,20 +73,46 @@ def test_gemv_generic_rates(dev, n):
     assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 256, n, odec)) < BAR
 
 
-@pytest.mark.parametrize("splits,separate", [("1", "0"), ("2", "0"), ("4", "1"), ("8", "0")])
-def test_gemv_split_and_finish_arms_agree(dev, splits, separate):
-    print(f"[gemv] splits={splits} separate={separate}", flush=True)
+@pytest.mark.parametrize("splits,separate,fold", [("1", "0", "1"), ("2", "0", "1"), ("2", "0", "0"), ("4", "1", "1"),
+                                                  ("8", "0", "1"), ("8", "0", "0")])
+def test_gemv_split_and_finish_arms_agree(dev, splits, separate, fold):
+    """Direct finish, the fold (fixed-point accumulation), counters + planes, and the separate finish kernel."""
+    print(f"[gemv] splits={splits} separate={separate} fold={fold}", flush=True)
     p, pd, x, xd = _case(dev, 9, 4, 1024, 256, 48)
     dec, odec = DECODES["3inst"]
     want = _oracle(p, x, 1024, 256, 48, odec)
     os.environ["EXL3_GEMV_SPLITS"] = splits
     os.environ["EXL3_GEMV_SEPARATE_FINISH"] = separate
+    os.environ["EXL3_GEMV_FOLD"] = fold
     try:
-        for _ in range(3):  # fused finish counters must come back to zero between calls
+        for _ in range(3):  # fused finish counters / accumulators must come back to zero between calls
             assert max_abs_rel(_run(pd, xd, dec), want) < BAR
     finally:
         del os.environ["EXL3_GEMV_SPLITS"]
         del os.environ["EXL3_GEMV_SEPARATE_FINISH"]
+        del os.environ["EXL3_GEMV_FOLD"]
+
+
+@pytest.mark.parametrize("fold", ["1", "0"])
+def test_gemv_non_finite_rows(dev, fold):
+    """A row whose input holds an inf comes out non-finite in every output under both split finishes (the fold marks
+    non-finite contributions and yields NaN); the other rows stay within the bar and the accumulators stay clean."""
+    print(f"[gemv] non-finite fold={fold}", flush=True)
+    p, pd, x, xd = _case(dev, 11, 3, 1024, 256, 64)
+    dec, odec = DECODES["mcg"]
+    want = _oracle(p, x, 1024, 256, 64, odec)
+    xbad = xd.clone()
+    xbad[1, 5] = float("inf")
+    os.environ["EXL3_GEMV_SPLITS"] = "8"
+    os.environ["EXL3_GEMV_FOLD"] = fold
+    try:
+        y = _run(pd, xbad, dec)
+        assert not np.isfinite(y[1]).any()
+        assert max_abs_rel(y[[0, 2]], want[[0, 2]]) < BAR
+        assert max_abs_rel(_run(pd, xd, dec), want) < BAR  # the next call starts from clean words
+    finally:
+        del os.environ["EXL3_GEMV_SPLITS"]
+        del os.environ["EXL3_GEMV_FOLD"]
 
 
 @pytest.mark.parametrize("rows", [2, 12, 24])
