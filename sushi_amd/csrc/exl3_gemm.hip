@@ -17,12 +17,6 @@ namespace exl3 {
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t scale_h2_4096(uint32_t v) {
-    __half2 h = __builtin_bit_cast(__half2, v);
-    h = __hmul2(h, __half2(__float2half(4096.0f), __float2half(4096.0f)));
-    return __builtin_bit_cast(uint32_t, h);
-}
-
 constexpr int GM_WAVES = 2;
 constexpr int GM_THREADS = 64 * GM_WAVES;
 constexpr int GM_MT = 128;    // rows per workgroup

@@ -32,6 +32,26 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
 
 constexpr int GEMV_THREADS = 64 * GEMV_WAVES;
 constexpr int MAX_KSPAN = 2048;
+// LDS pitch (halves) of a prepared input row: 16 bytes past MAX_KSPAN, so the rows that the four lane groups of a
+// matrix instruction read at one k fall in different LDS banks.
+constexpr int XS_PITCH = MAX_KSPAN + 8;
+
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// v_mfma_f32_4x4x4_16b_f16: sixteen independent 4x4x4 products, block b on lanes 4b..4b+3.  Lane 4b+i holds row i of
+// the block's A (4 k values) and column i of its B (the same 4 k), and receives column i of the block's D (rows 0..3).
+__device__ __forceinline__ f4_t mfma4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f4_t c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4_t, u2_t{a0, a1}),
+                                              __builtin_bit_cast(h4_t, u2_t{b0, b1}), c, 0, 0, 0);
+}
+
+// Batch rows are served four at a time (one set of matrix instructions per group of four).
+template <int RT>
+struct RowGroups {
+    static constexpr int G = (RT + 3) / 4;
+};
 
 __device__ __forceinline__ float load_x(const void *x, int dt, size_t i) {
     if (dt == DT_F16) return load_act<DT_F16>(x, i);
@@ -97,7 +117,7 @@ struct XChunk {
 };
 
 template <int RT>
-__device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[MAX_KSPAN], int kk, int r0,
+__device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[XS_PITCH], int kk, int r0,
                                              uint4 (&X)[XChunk<RT>::CH], uint4 (&Y)[XChunk<RT>::CH]) {
 #pragma unroll
     for (int c = 0; c < XChunk<RT>::CH; c++) {
@@ -106,35 +126,41 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[MAX_KSPAN], in
     }
 }
 
-// The 32 weights of one tile chunk (lane-owned columns j and j+8), dotted into acc0 (column j) / acc1 (column j+8).
-// `rows` (wave-uniform, <= RT) bounds the chunks that are dotted: rows past it hold zeros.
+// The 32 weights of one tile chunk (lane-owned columns j and j+8) against every batch row, on the matrix cores.
+// Lane 8o + j is lane 4b + i of block b = 2o + j/4 with i = j % 4: its decoded pairs of column j over k rows 4s..4s+3
+// (pairs (0, 4), (8, 12), (1, 5), (9, 13) for s = 0..3; column j + 8: (2, 6), (10, 14), (3, 7), (11, 15)) are the B
+// column i of that block as they stand, and its A row is batch row 4g + i of the prepared input at the same k, so
+// accA[g] / accB[g] collect rows 4g..4g+3 of columns j / j + 8.  Rows past RT read row RT - 1 (their results are
+// never used); rows at or past `rows` (wave-uniform) hold zeros in LDS, and whole groups past it are skipped.
 template <int FAM, int N, int RT, bool MASKED>
-__device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[MAX_KSPAN],
-                                            int kk, int rows, const DecodeK &k, float (&acc0)[RT],
-                                            float (&acc1)[RT]) {
-    constexpr int CH = XChunk<RT>::CH;
-    uint4 X[CH], Y[CH];
-    load_x_chunk<RT>(xs, kk, 0, X, Y);
+__device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[XS_PITCH],
+                                            int kk, int rows, const DecodeK &k, f4_t (&accA)[RowGroups<RT>::G],
+                                            f4_t (&accB)[RowGroups<RT>::G], int i4) {
+    const uint16_t *xr = &xs[min(i4, RT - 1)][kk * 16];
+    uint4 X = *reinterpret_cast<const uint4 *>(xr);
+    uint4 Y = *reinterpret_cast<const uint4 *>(xr + 8);
     uint32_t w[16];
     decode_weights<FAM, N, MASKED>(A, k, w);
-    // pair i = (u, u+1), u = 2i = 8qq + 2p: p = 0/1 -> column j rows 2qq(+8), p = 2/3 -> column j+8
+    if constexpr (family_scaled<FAM>()) {  // the caller takes the 2^12 back out of the sums (exact)
 #pragma unroll
-    for (int r0 = 0; r0 < RT; r0 += CH) {
-        if (r0 > 0) {
-            if (r0 >= rows) break;
-            load_x_chunk<RT>(xs, kk, r0, X, Y);
+        for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
+    }
+#pragma unroll
+    for (int g = 0; g < RowGroups<RT>::G; g++) {
+        if (g > 0) {
+            if (4 * g >= rows) break;
+            const uint16_t *xg = &xs[min(4 * g + i4, RT - 1)][kk * 16];
+            X = *reinterpret_cast<const uint4 *>(xg);
+            Y = *reinterpret_cast<const uint4 *>(xg + 8);
         }
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int qq = i >> 2, p = i & 3;
-#pragma unroll
-            for (int c = 0; c < CH; c++) {
-                const uint4 &V = (p & 1) ? Y[c] : X[c];
-                const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
-                if (p < 2) acc0[r0 + c] = dot2(w[i], xv, acc0[r0 + c]);
-                else acc1[r0 + c] = dot2(w[i], xv, acc1[r0 + c]);
-            }
-        }
+        accA[g] = mfma4(X.x, X.y, w[0], w[4], accA[g]);
+        accB[g] = mfma4(X.x, X.y, w[2], w[6], accB[g]);
+        accA[g] = mfma4(X.z, X.w, w[8], w[12], accA[g]);
+        accB[g] = mfma4(X.z, X.w, w[10], w[14], accB[g]);
+        accA[g] = mfma4(Y.x, Y.y, w[1], w[5], accA[g]);
+        accB[g] = mfma4(Y.x, Y.y, w[3], w[7], accB[g]);
+        accA[g] = mfma4(Y.z, Y.w, w[9], w[13], accA[g]);
+        accB[g] = mfma4(Y.z, Y.w, w[11], w[15], accB[g]);
     }
 }
 
@@ -216,7 +242,7 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, 
 }
 
 template <int PRO, int RT, bool WIN>
-__device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[MAX_KSPAN], int wave,
+__device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[XS_PITCH], int wave,
                                          int lane, const PrologueRegs<RT> &pr) {
     const int nblk = c.KS >> 3;
     for (int job = wave; job < nblk * RT; job += GEMV_WAVES) {
@@ -330,7 +356,7 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 template <int FAM, int N, int RT, int PRO, bool WIN>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
-                                          int n, const DecodeK &k, uint16_t (*xs)[MAX_KSPAN], float (*red)[RT][128]) {
+                                          int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
     const int o = lane >> 3, j = lane & 7;
@@ -357,6 +383,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
         prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
+        constexpr int RG = RowGroups<RT>::G;
+        f4_t accA[RG], accB[RG];
+#pragma unroll
+        for (int g = 0; g < RG; g++) accA[g] = accB[g] = f4_t{0.f, 0.f, 0.f, 0.f};
         for (int t0 = 0; t0 < ntiles; t0 += TPW) {
             if (t0 > 0) {  // splits longer than TPW tiles per wave: load the next batch in place
 #pragma unroll
@@ -370,10 +400,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
             for (int t = 0; t < TPW; t++) {
                 if (t0 + t < ntiles) {
                     const int kk = wave + GEMV_WAVES * (t0 + t);
-                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, acc0, acc1);
-                    else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, acc0, acc1);
+                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
+                    else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
                 }
             }
+        }
+        // the hash / pair weights went in times 2^12; out_scale applies the codebook scale to every arm alike
+        constexpr float unscale = family_scaled<FAM>() ? 1.0f / 4096.0f : 1.0f;
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            acc0[r] = accA[r >> 2][r & 3] * unscale;
+            acc1[r] = accB[r >> 2][r & 3] * unscale;
         }
     } else {  // any other rate: the generic reader (runtime funnel per codeword)
         PrologueRegs<RT> pr;
@@ -542,7 +579,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     c.sv0 = h2f(c.svh[sv + lane]);
     c.sv1 = h2f(c.svh[sv + lane + 64]);
 
-    __shared__ __align__(16) uint16_t xs[RT][MAX_KSPAN];
+    __shared__ __align__(16) uint16_t xs[RT][XS_PITCH];
     __shared__ float red[GEMV_WAVES][RT][128];
 
     if constexpr (N >= 0) {

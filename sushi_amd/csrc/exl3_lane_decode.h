@@ -21,6 +21,14 @@ struct Pairing {
 // A scheduling fence: nothing moves across it, so each phase below stays one batch of independent instructions.
 __device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// A pair of hash / pair family weights times 2^12 (exact: they are the codebook values over 4096).  Matrix
+// instructions take these scaled, since the unscaled values include f16 subnormals.
+__device__ __forceinline__ uint32_t scale_h2_4096(uint32_t v) {
+    __half2 h = __builtin_bit_cast(__half2, v);
+    h = __hmul2(h, __half2(__float2half(4096.0f), __float2half(4096.0f)));
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 // The weights of the lane's chunk, unscaled for the hash / pair families (the x4096 is applied by the caller).
 // Written in fenced phases (windows, product step 1, step 2, masks, low sums, high sums): within a phase no
 // instruction depends on another, so no result is read by the instruction right after it and the hazard recognizer
@@ -29,64 +37,85 @@ template <int FAM, int N, bool MASKED>
 __device__ __forceinline__ void decode_weights(const uint32_t (&A)[LaneBits<N>::AW], const DecodeK &k,
                                                uint32_t (&w)[16]) {
     using P = Pairing<N>;
-    uint32_t win[32];
-#pragma unroll
-    for (int v = 0; v < 32; v++) {
-        if (P::win(v) == v) {
-            win[v] = lane_codeword<N>(A, v);
-            if constexpr (MASKED) win[v] &= k.wmask | (k.wmask << 16);
-        }
-    }
-    if constexpr (FAM == FAM_PAIR) {
-        // both weights of a pair decode from the odd codeword (decodePair, expert_exl3.zig:298-301)
-        uint32_t pr[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int v = 2 * i + 1;
-            pr[i] = P::hi(v) ? mul16x32<true>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu)
-                             : mul16x32<false>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu);
-        }
-        uint32_t h0[16], h1[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            h0[i] = pr[i] & k.mask0;
-            h1[i] = __builtin_amdgcn_alignbit(pr[i], pr[i], 32u - k.rot) & k.mask1;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; i++) w[i] = pack_sums(h0[i], h1[i]);
-    } else if constexpr (FAM == FAM_MUL1) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t x0 = win[P::win(2 * i)], x1 = win[P::win(2 * i + 1)];
-            const uint32_t c0 = P::hi(2 * i) ? x0 >> 16 : x0, c1 = P::hi(2 * i + 1) ? x1 >> 16 : x1;
-            w[i] = pack_h2(decode1<FAM_MUL1>(c0, k), decode1<FAM_MUL1>(c1, k));
-        }
-    } else {
-        uint32_t h[32];
-        phase_fence();
-#pragma unroll
-        for (int v = 0; v < 32; v++)
-            h[v] = P::hi(v) ? hash_step1<FAM, true>(win[P::win(v)], k) : hash_step1<FAM, false>(win[P::win(v)], k);
-        phase_fence();
+    if constexpr (FAM == FAM_PAIR || FAM == FAM_MUL1) {
+        uint32_t win[32];
 #pragma unroll
         for (int v = 0; v < 32; v++) {
-            if (P::hi(v)) hash_step2<FAM, true>(win[P::win(v)], k, h[v]);
-            else hash_step2<FAM, false>(win[P::win(v)], k, h[v]);
+            if (P::win(v) == v) {
+                win[v] = lane_codeword<N>(A, v);
+                if constexpr (MASKED) win[v] &= k.wmask | (k.wmask << 16);
+            }
         }
-        phase_fence();
+        if constexpr (FAM == FAM_PAIR) {
+            // both weights of a pair decode from the odd codeword (decodePair, expert_exl3.zig:298-301)
+            uint32_t pr[16];
 #pragma unroll
-        for (int v = 0; v < 32; v++) h[v] = hash_halves<FAM>(h[v], k);
-        phase_fence();
+            for (int i = 0; i < 16; i++) {
+                const int v = 2 * i + 1;
+                pr[i] = P::hi(v) ? mul16x32<true>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu)
+                                 : mul16x32<false>(win[P::win(v)], k.mult >> 16, k.mult & 0xFFFFu);
+            }
+            uint32_t h0[16], h1[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
-                : "=v"(w[i]) : "v"(h[2 * i]));
-        phase_fence();
+            for (int i = 0; i < 16; i++) {
+                h0[i] = pr[i] & k.mask0;
+                h1[i] = __builtin_amdgcn_alignbit(pr[i], pr[i], 32u - k.rot) & k.mask1;
+            }
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-                : "+v"(w[i]) : "v"(h[2 * i + 1]));
-        phase_fence();
+            for (int i = 0; i < 16; i++) w[i] = pack_sums(h0[i], h1[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t x0 = win[P::win(2 * i)], x1 = win[P::win(2 * i + 1)];
+                const uint32_t c0 = P::hi(2 * i) ? x0 >> 16 : x0, c1 = P::hi(2 * i + 1) ? x1 >> 16 : x1;
+                w[i] = pack_h2(decode1<FAM_MUL1>(c0, k), decode1<FAM_MUL1>(c1, k));
+            }
+        }
+    } else {
+        // Rates without pairing (one window per codeword) run the phases over two halves of the chunk, so only half
+        // the windows and products are live at once; paired windows serve codewords up to 16 apart, so paired rates
+        // run all 32 together.
+        constexpr int H = P::ON ? 1 : 2;
+        constexpr int V = 32 / H;
+#pragma unroll
+        for (int hh = 0; hh < H; hh++) {
+            const int v0 = hh * V;
+            uint32_t win[V], h[V];
+#pragma unroll
+            for (int v = 0; v < V; v++) {
+                if (P::win(v0 + v) == v0 + v) {
+                    win[v] = lane_codeword<N>(A, v0 + v);
+                    if constexpr (MASKED) win[v] &= k.wmask | (k.wmask << 16);
+                }
+            }
+            phase_fence();
+#pragma unroll
+            for (int v = 0; v < V; v++) {
+                const int wv = P::win(v0 + v) - v0;
+                h[v] = P::hi(v0 + v) ? hash_step1<FAM, true>(win[wv], k) : hash_step1<FAM, false>(win[wv], k);
+            }
+            phase_fence();
+#pragma unroll
+            for (int v = 0; v < V; v++) {
+                const int wv = P::win(v0 + v) - v0;
+                if (P::hi(v0 + v)) hash_step2<FAM, true>(win[wv], k, h[v]);
+                else hash_step2<FAM, false>(win[wv], k, h[v]);
+            }
+            phase_fence();
+#pragma unroll
+            for (int v = 0; v < V; v++) h[v] = hash_halves<FAM>(h[v], k);
+            phase_fence();
+#pragma unroll
+            for (int i = 0; i < V / 2; i++)
+                asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+                    : "=v"(w[v0 / 2 + i]) : "v"(h[2 * i]));
+            phase_fence();
+#pragma unroll
+            for (int i = 0; i < V / 2; i++)
+                asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+                    : "+v"(w[v0 / 2 + i]) : "v"(h[2 * i + 1]));
+            phase_fence();
+        }
     }
 }
 
