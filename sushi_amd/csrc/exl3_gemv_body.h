@@ -1,22 +1,24 @@
 // (Kernel body shared by the per-family translation units exl3_gemv_<family>.hip.)
-// Trellis GEMV for 1..8 rows: the decode arm of the dense linear (linear.linear, beamivalice/sushi
+// Trellis GEMV for 1..16 rows: the decode arm of the dense linear (linear.linear, beamivalice/sushi
 // src/exl3/linear.zig:317-336, Metal ROWS_SOURCE/ROWS_FINISH_SOURCE in src/exl3/project_rows.zig:145-249, :345-362)
 // and of the routed MoE chain (PAIR_GEMV_SOURCE :2082-2241, DOWN_FUSED_SOURCE :1820-2023 in
 // src/exl3/expert_exl3_kernels.zig).
 //
 // MI355X layout.  A workgroup (GEMV_WAVES = 8 waves, one workgroup per CU at C1) owns one output group of 8 tiles
 // (128 outputs, one Hadamard block) of one (bank, x-block) pair over one k split of at most 32 k-tiles (whole
-// 128-blocks).  Per k-tile row a wave streams the
-// group's 8 tiles, which lie contiguous in the pack order [IT][OT][n] (8*n*2 bytes, 1 KiB at K4): lane = 8*o + j
-// reads chunk j of tile o, the words carrying codewords 32j..32j+31 = fragment threads 4j..4j+3 of tensorCorePerm =
-// output columns j and j+8 over all 16 k rows.  Every lane owns two output columns outright, decodes its 32 weights
-// into registers as packed f16 pairs (t, t+1) = rows (r, r+1) of one column and feeds v_dot2_f32_f16 against the
-// prepared input held in LDS.  No cross-lane reduction happens inside a wave; the waves meet once in LDS.
+// 128-blocks).  Per k-tile row a wave streams the group's 8 tiles, which lie contiguous in the pack order
+// [IT][OT][n] (8*n*2 bytes, 1 KiB at K4): lane = 8*o + j reads chunk j of tile o, the words carrying codewords
+// 32j..32j+31 = output columns j and j+8 over all 16 k rows (tensorCorePerm).  Every lane owns two output columns
+// outright and decodes its 32 weights into registers as packed f16 pairs (t, t+1) = rows (r, r+1) of one column.
+// Those pairs are, as they stand, B columns of v_mfma_f32_4x4x4_16b_f16, whose A rows are batch rows of the
+// prepared input in LDS: the matrix cores take the dot products, four batch rows per instruction set, and the VALU
+// keeps the decode.  No cross-lane reduction happens inside a wave; the waves meet once in LDS.
 //
 // Latency: a wave issues the loads of all its tiles (<= 4) before the prologue, so HBM latency overlaps the input
 // preparation (x * suh, FWHT-128, f16 -- or the MoE SwiGLU mid).  The finish (FWHT-128, * svh) runs in the same
-// launch: with one split directly, otherwise in the last workgroup of an output group to arrive.  Partials travel
-// by write-through stores and a relaxed arrival counter (no L2 write-back fence, which costs ~1 us per workgroup).
+// launch: with one split directly; otherwise each split folds its transformed partial into exact fixed-point
+// accumulators with one returning atomic per output and the split that completes an output stores it (fold_finish),
+// or, past the fold's limits, the last workgroup of an output group to arrive sums the partial planes.
 #pragma once
 #include "exl3_kernels.h"
 #include "exl3_tables.h"
