@@ -191,6 +191,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
                   (size_t)groups * rows * out <= kFoldWords && env_int("EXL3_GEMV_FOLD", 1) != 0)
                      ? reinterpret_cast<unsigned long long *>(w)
                      : nullptr;
+        a.fold_arrivals = p.splits;
         return launched(run_gemv(fam, PRO_X, a, stream), "exl3_linear (gemv)");
     }
     GemmArgs g{};
@@ -369,8 +370,25 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     d.nproj = 1;
     d.fused_finish = 0;
     d.partial_only = 1;
+    // The down projection folds straight into y (score-weighted, exact fixed point, shared expert added by the
+    // completing arrival) when every token's topk * splits arrivals fit the count field and its rows fit the zeroed
+    // region; the planes + reduce launch otherwise.
+    const bool fold = topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)rows * hidden <= kFoldWords &&
+                      env_int("EXL3_MOE_FOLD", 1) != 0;
+    if (fold) {
+        d.partial_only = 0;
+        d.fused_finish = 1;
+        d.fold = static_cast<unsigned long long *>(ws);
+        d.fold_arrivals = topk * p.s2;
+        d.fold_topk = topk;
+        d.fold_scores = scores;
+        d.fold_shared = shared;
+        d.y = y;
+        d.y_dtype = y_dtype;
+    }
     e = run_gemv(fam, PRO_MID, d, stream);
     if (e != hipSuccess) return launched(e, "exl3_moe (down)");
+    if (fold) return ok();
 
     // 3) score-weighted reduce (+ shared expert)
     ReduceArgs r{};

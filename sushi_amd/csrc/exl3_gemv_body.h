@@ -67,6 +67,19 @@ __device__ __forceinline__ void store_y(void *y, int dt, size_t i, float v) {
     else store_act<DT_F32>(y, i, v);
 }
 
+__device__ __forceinline__ float load_y(const void *y, int dt, size_t i) {
+    if (dt == DT_F16) return load_act<DT_F16>(y, i);
+    if (dt == DT_BF16) return load_act<DT_BF16>(y, i);
+    return load_act<DT_F32>(y, i);
+}
+
+// v rounded to y's dtype and back (the routed sum's rounding before a shared expert is added).
+__device__ __forceinline__ float round_y(int dt, float v) {
+    if (dt == DT_F16) return __half2float(__float2half_rn(v));
+    if (dt == DT_BF16) return __bfloat162float(__float2bfloat16(v));
+    return v;
+}
+
 __device__ __forceinline__ float silu(float g) {
     // g * sigmoid(g), evaluated on exp(-|g|) so neither branch overflows (the reference's mid uses the same split)
     const float e = __expf(-fabsf(g));
@@ -324,9 +337,13 @@ __device__ __forceinline__ float fold_value(unsigned long long t, int S) {
 // y and clears the word for the next call.  Integer addition makes the result independent of arrival order, and
 // neither partial planes nor a second round trip (store acknowledgement, then counter) sit on the path.  Wave w
 // finishes rows w, w + GEMV_WAVES, ...
-template <int RT>
+// The MoE down projection folds the same way across slots: slot s adds its score-weighted output into row
+// s / topk (the score-weighted reduce of REDUCE_SOURCE / REDUCE_SHARED_SOURCE, expert_exl3_kernels.zig:2338-2406),
+// and the completing arrival rounds the routed sum to y's dtype before adding the shared expert.
+template <int RT, bool WIN>
 __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c, float (*red)[RT][128], int wave,
                                             int lane) {
+    const bool moe = a.fold_topk > 0;
     for (int r = wave; r < c.rows; r += GEMV_WAVES) {
         float v0 = 0.f, v1 = 0.f;
 #pragma unroll
@@ -337,20 +354,31 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
         v0 *= a.out_scale;
         v1 *= a.out_scale;
         fwht128_wave(v0, v1, lane);
-        const unsigned long long t0 = fold_term(v0 * HAD_SCALE * c.sv0);
-        const unsigned long long t1 = fold_term(v1 * HAD_SCALE * c.sv1);
-        const size_t yo = ((size_t)c.g * a.rows + r) * a.out + (size_t)c.og * 128;
+        size_t yrow;
+        float sc = 1.0f;
+        if (moe) {
+            const int slot = slot_of<WIN>(c, r);
+            yrow = (size_t)(slot / a.fold_topk);
+            sc = a.fold_scores[slot];
+        } else {
+            yrow = (size_t)c.g * a.rows + r;
+        }
+        const unsigned long long t0 = fold_term((v0 * HAD_SCALE * c.sv0) * sc);
+        const unsigned long long t1 = fold_term((v1 * HAD_SCALE * c.sv1) * sc);
+        const size_t yo = yrow * a.out + (size_t)c.og * 128;
         unsigned long long *w0 = a.fold + yo + lane, *w1 = w0 + 64;
         const unsigned long long o0 = __hip_atomic_fetch_add(w0, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long o1 = __hip_atomic_fetch_add(w1, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long last = (unsigned long long)(c.S - 1);
-        if ((o0 >> FOLD_COUNT_SHIFT) == last) {
-            store_y(a.y, a.y_dtype, yo + lane, fold_value(o0 + t0, c.S));
-            __hip_atomic_store(w0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if ((o1 >> FOLD_COUNT_SHIFT) == last) {
-            store_y(a.y, a.y_dtype, yo + lane + 64, fold_value(o1 + t1, c.S));
-            __hip_atomic_store(w1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long last = (unsigned long long)(a.fold_arrivals - 1);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const unsigned long long o = h ? o1 : o0, t = h ? t1 : t0;
+            if ((o >> FOLD_COUNT_SHIFT) != last) continue;
+            const size_t i = yo + lane + 64 * h;
+            float v = fold_value(o + t, a.fold_arrivals);
+            if (a.fold_shared) v = round_y(a.y_dtype, v) + load_y(a.fold_shared, a.y_dtype, i);
+            store_y(a.y, a.y_dtype, i, v);
+            __hip_atomic_store(h ? w1 : w0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -456,6 +484,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
         red[wave][r][o * 16 + j + 8] = acc1[r];
     }
     __syncthreads();
+    if (a.fold) {  // the host enables the fold only for split dense launches and the MoE down projection
+        fold_finish<RT, WIN>(a, c, red, wave, lane);
+        return;
+    }
     const bool direct = c.S == 1 && !a.partial_only;
     if (direct) {
         for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
@@ -469,10 +501,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
         for (int r = wave; r < a.rows; r += GEMV_WAVES) finish_block(a, c, r, red[0][r][lane], red[0][r][lane + 64], lane);
         return;
     }
-    if (a.fold) {
-        fold_finish(a, c, red, wave, lane);
-        return;
-    }
+
     // Split k: wave 0 alone sums the workgroup's partial, stores it, arrives at the output group's counter and, if it
     // is the last split to arrive, finishes the group.  Its own stores are then the only ones the arrival has to
     // follow, so no workgroup barrier sits between the stores, the arrival and the finish.
@@ -640,8 +669,8 @@ template <int FAM, int N, int PRO>
 static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
     const int G = a.out / 128;
     dim3 grid((unsigned)(G * a.splits), (unsigned)a.groups, (unsigned)a.nproj);
-    if (a.win_count) {  // the sorted MoE arm: expert windows of MOE_WINDOW_ROWS rows, f32 planes out
-        if (a.rows != MOE_WINDOW_ROWS || !a.partial_only) return hipErrorInvalidValue;
+    if (a.win_count) {  // the sorted MoE arm: expert windows of MOE_WINDOW_ROWS rows, f32 planes or the fold out
+        if (a.rows != MOE_WINDOW_ROWS || !(a.partial_only || a.fold)) return hipErrorInvalidValue;
         hipLaunchKernelGGL((gemv_kernel<FAM, N, MOE_WINDOW_ROWS, PRO, true>), grid, dim3(GEMV_THREADS), 0, s, a);
     } else if constexpr (PRO == PRO_X && N >= 0) {
         if (a.rows <= 1) hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);

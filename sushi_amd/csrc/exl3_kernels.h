@@ -63,7 +63,11 @@ struct GemvArgs {
     float out_scale;
     float *partial[2];       // [groups][splits][rows][out] f32
     uint32_t *counters;      // [groups][out/128], zero between calls
-    unsigned long long *fold; // fixed-point fused finish: [groups][rows][out] words, zero between calls; null = off
+    unsigned long long *fold; // fixed-point fused finish: one word per output, zero between calls; null = off
+    int fold_arrivals;        // contributions per output word (the dense GEMV's splits; topk * splits for the MoE down)
+    int fold_topk;            // > 0: MoE down -- slot s folds into output row s / fold_topk, scaled by fold_scores[s]
+    const float *fold_scores;
+    const void *fold_shared;  // MoE: [rows][out] in y's dtype, added after the routed sum's rounding; null = none
     void *y;
     int y_dtype;
     int splits;

@@ -204,6 +204,41 @@ def test_moe_sorted_and_per_slot_arms_agree(dev):
     assert max_abs_rel(sorted_arm, per_slot) < BAR
 
 
+@pytest.mark.parametrize("rows", [1, 5, 24])
+@pytest.mark.parametrize("with_shared", [False, True])
+def test_moe_fold_and_reduce_arms_agree(dev, rows, with_shared):
+    """The down projection folded straight into y and the planes + reduce launch agree to the bar against the
+    oracle (per-slot arm up to 16 rows, sorted arm above), with and without a shared expert, and the accumulators
+    are clean for the next call."""
+    import os
+
+    print(f"[moe] fold arms rows={rows} shared={with_shared}", flush=True)
+    E, hidden, inter, k, n = 24, 256, 384, 6, 32
+    b = synth.bank(13, "moef", E, hidden, inter, n)
+    bd = _to(b, dev)
+    x = synth.normal(13, "x", (rows, hidden))
+    inds, scores = _route(13 + rows, rows, E, k)
+    want = _oracle_moe(b, x.float().numpy(), inds, scores, hidden, inter, n, O.decode(O.CB_MCG))
+    sh = synth.normal(14, "shared", (rows, hidden)) if with_shared else None
+    if with_shared:
+        want = want.astype(np.float16).astype(np.float64) + sh.float().numpy()
+    xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
+    shd = None if sh is None else sh.to(dev)
+    got = {}
+    for fold in ("1", "0", "1"):
+        os.environ["EXL3_MOE_FOLD"] = fold
+        try:
+            y = exl3.moe_with_shared(x.to(dev), bd, xi, sc, exl3.MCG, False, shd) if with_shared else \
+                exl3.moe(x.to(dev), bd, xi, sc, exl3.MCG)
+        finally:
+            del os.environ["EXL3_MOE_FOLD"]
+        got.setdefault(fold, []).append(y.float().cpu().numpy())
+    for ys in got.values():
+        for y in ys:
+            assert max_abs_rel(y, want) < BAR
+    assert np.array_equal(got["1"][0], got["1"][1])  # exact accumulation: the same bytes on every call
+
+
 def test_router_matches_oracle(dev):
     logits = synth.normal(2, "logits", (9, 256), dtype=torch.float32)
     inds, scores = exl3.moe_routing_chain(logits.to(dev), 8)
