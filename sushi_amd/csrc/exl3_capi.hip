@@ -121,8 +121,11 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
     return p;
 }
 
+// Prepared-input rows of the GEMM arm: whole 16-row tiles (the fragment-order layout pads the last tile).
+size_t gemm_xp_bytes(int groups, int rows, int in) { return align_up((size_t)groups * ((rows + 15) / 16 * 16) * in * 2); }
+
 size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
-    size_t b = kZeroBytes + align_up((size_t)groups * rows * in * 2);
+    size_t b = kZeroBytes + gemm_xp_bytes(groups, rows, in);
     const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
     if (!lane_reader) b += align_up((size_t)groups * out * in * 2);  // the transposed f16 copy of other rates
     return b;
@@ -206,7 +209,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     g.svh = svh;
     g.k = k;
     g.xp = reinterpret_cast<uint16_t *>(w + kZeroBytes);
-    g.wt = reinterpret_cast<uint16_t *>(w + kZeroBytes + align_up((size_t)groups * rows * in * 2));
+    g.wt = reinterpret_cast<uint16_t *>(w + kZeroBytes + gemm_xp_bytes(groups, rows, in));
     g.y = y;
     g.y_dtype = y_dtype;
     g.groups = groups;

@@ -45,6 +45,49 @@ __global__ __launch_bounds__(64) void gemm_prepare_kernel(GemmArgs a) {
     a.xp[xi + lane + 64] = __half_as_ushort(__float2half_rn(v1 * HAD_SCALE));
 }
 
+// ---- prepare into MFMA A-fragment order: for 16-row tile rt and 32-k block kb of group g, the 1 KiB at
+// xp[((g * RT + rt) * (in / 32) + kb) * 512] holds lane l = 16h + c's fragment (row 16 rt + c, k = 32 kb + 8h .. +7)
+// at l * 8 halves, so one MFMA wave's load of a fragment is one contiguous 1 KiB.  RT = ceil(rows / 16); rows past
+// the end of the last tile are zeros.  A workgroup (4 waves) prepares 16 rows x one 128-block: each wave runs the
+// FWHT of 4 rows into an LDS tile, then every thread writes one 16-byte fragment.
+__global__ __launch_bounds__(256) void gemm_prepare_frag_kernel(GemmArgs a) {
+    const int b = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int RT = (a.rows + 15) / 16;
+    __shared__ __align__(16) uint16_t t[16][128 + 8];
+    const size_t si = (size_t)g * a.in + (size_t)b * 128;
+    const float u0 = h2f(a.suh[si + lane]), u1 = h2f(a.suh[si + lane + 64]);
+    for (int rr = 0; rr < 4; rr++) {
+        const int r = wave * 4 + rr, m = rt * 16 + r;
+        float v0 = 0.f, v1 = 0.f;
+        if (m < a.rows) {
+            const size_t xi = ((size_t)g * a.rows + m) * a.in + (size_t)b * 128;
+            if (a.x_dtype == DT_F16) {
+                v0 = load_act<DT_F16>(a.x, xi + lane);
+                v1 = load_act<DT_F16>(a.x, xi + lane + 64);
+            } else if (a.x_dtype == DT_BF16) {
+                v0 = f16r(load_act<DT_BF16>(a.x, xi + lane));
+                v1 = f16r(load_act<DT_BF16>(a.x, xi + lane + 64));
+            } else {
+                v0 = f16r(load_act<DT_F32>(a.x, xi + lane));
+                v1 = f16r(load_act<DT_F32>(a.x, xi + lane + 64));
+            }
+            v0 *= u0;
+            v1 *= u1;
+            fwht128_wave(v0, v1, lane);
+            v0 *= HAD_SCALE;
+            v1 *= HAD_SCALE;
+        }
+        t[r][lane] = __half_as_ushort(__float2half_rn(v0));
+        t[r][lane + 64] = __half_as_ushort(__float2half_rn(v1));
+    }
+    __syncthreads();
+    const int kq = tid >> 6, c = lane & 15, h = lane >> 4;  // 32-k block kq of this 128-block, fragment lane (c, h)
+    const uint4 v = *reinterpret_cast<const uint4 *>(&t[c][kq * 32 + 8 * h]);
+    const size_t kb = (size_t)b * 4 + kq;
+    *reinterpret_cast<uint4 *>(a.xp + (((size_t)g * RT + rt) * (a.in / 32) + kb) * 512 + (size_t)lane * 8) = v;
+}
+
 // ---- dense fallback: tiles decoded to wt[g][out][in] f16 (transposed, so a B fragment is 16 contiguous bytes)
 template <int FAM>
 __global__ void gemm_decode_transposed_kernel(GemmArgs a, uint16_t *__restrict__ wt) {
@@ -208,28 +251,27 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
 
 // ---- the decode-once GEMM (integer and half-integer rates with a lane reader: n = 16, 24, 32, 40, 48, 64)
 //
-// A workgroup (4 waves) owns a 256-row x 128-column output tile (one Hadamard block wide, so the FWHT + svh finish
-// runs in its epilogue) over all of k, in k-steps of 64 (four trellis k-tiles).  Per k-step, wave w decodes k-tile
-// row w of the group's 8 tiles with the GEMV's lane decoder (lane 8o + j: codewords 32j..32j+31 of tile o = columns
-// j and j+8 over 16 k rows) and writes the f16 weights once into an LDS slab held column-major (B[col][k]), double
-// buffered so the next slab is decoded while the current one feeds the MFMAs.  Each wave runs its 64 rows x 128
-// columns as 4 x 8 v_mfma_f32_16x16x32_f16 tiles per 32 k, taking A fragments (16 rows x 8 k per lane) straight
-// from the prepared input in global memory (two register sets, alternating steps) and B fragments from the slab.
-// Every weight is decoded once per 256-row tile instead of once per 128 rows per wave.
-constexpr int G2_WAVES = 4;
-constexpr int G2_THREADS = 64 * G2_WAVES;
-constexpr int G2_MT = 64 * G2_WAVES;  // rows per workgroup
-constexpr int G2_BP = 72;             // LDS pitch (halves) of one slab column: 64 k + 8 pad (16-byte aligned rows)
-constexpr int G2_EP = 129;            // epilogue staging pitch (floats)
+// A workgroup owns a 256-row x 128-column output tile (one Hadamard block wide, so the FWHT + svh finish runs in its
+// epilogue) over all of k, in k-steps of 64 (four trellis k-tiles), with the decode and the MFMAs on different waves.
+// Waves 4-7 decode: wave 4 + r decodes k-tile row r of every step (lane 8o + j: codewords 32j..32j+31 of tile o =
+// columns j and j+8 over 16 k rows, the GEMV's lane decoder) into a double-buffered LDS slab held column-major
+// (B[col][k]), its tile words loaded two steps ahead.  Waves 0-3 run the MFMAs: 64 rows x 128 columns each, as
+// 4 x 8 v_mfma_f32_16x16x32_f16 tiles per 32 k, with A fragments read from the prepared input in fragment order (one
+// contiguous 1 KiB per load) and B fragments from the slab.  Each SIMD then holds one MFMA wave and one decode wave,
+// so the matrix core and the VALU work at the same time.  One workgroup barrier per step hands the slab over: after
+// barrier ks + 1 the MFMA waves have finished reading slab ks & 1 and the decode waves have finished writing slab
+// (ks + 1) & 1.  Every weight is decoded once per 256-row tile.
+constexpr int G2_MT = 256;   // rows per workgroup
+constexpr int G2_BP = 72;    // LDS pitch (halves) of one slab column: 64 k + 8 pad (16-byte aligned rows)
+constexpr int G2_EP = 129;   // epilogue staging pitch (floats)
+constexpr int G3_WAVES = 8;
+constexpr int G3_THREADS = 64 * G3_WAVES;
 
 template <int FAM, int N>
-__global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
+__global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int IT = a.in >> 4, OT = a.out >> 4;
-    // Workgroups go round-robin over the 8 XCDs (block L on XCD L % 8), and each XCD has its own L2.  When the row
-    // tiles divide the XCDs, give every XCD whole row tiles: the A rows a tile reads then stay in that XCD's L2 for
-    // all of its column blocks.
     const int nog = a.out / 128, nm = (a.rows + G2_MT - 1) / G2_MT;
     const int L = blockIdx.x;
     int og, mt;
@@ -242,101 +284,114 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
         mt = L / nog;
     }
     const int g = blockIdx.z;
-    const int m0 = mt * G2_MT + wave * 64;
     __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
-
-    const int o = lane >> 3, j = lane & 7;   // decode lane: tile o of the group, chunk j
-    const int c = lane & 15, h = lane >> 4;  // MFMA lane: row / column c, k group h
+    const int nks = IT / 4;  // even: in is a multiple of 128
     constexpr int AW = LaneBits<N>::AW;
-    const DecodeK k = a.k;
-    const bool masked = k.wmask != 0xFFFFu;
-    const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N;
 
-    // A rows of this lane.  A row past the end reads row 0 instead: each output row depends on its own A row only,
-    // and the epilogue never stores rows past the end, so nothing has to be zeroed (a select on the loaded value would
-    // make every prefetch wait for its data where it is issued).
-    const uint16_t *xrow[4];
+    if (wave >= 4) {
+        // ---- decode waves
+        const int r = wave - 4;
+        const int o = lane >> 3, j = lane & 7;
+        const DecodeK k = a.k;
+        const bool masked = k.wmask != 0xFFFFu;
+        const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8 + o) * N;
+        const size_t kstep = (size_t)4 * OT * N;  // halves from one k-step's row r to the next
+        auto load_tile = [&](int ks, uint32_t (&W)[AW]) __attribute__((always_inline)) {
+            load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(ks, nks - 1) * kstep), j, W);
+        };
+        auto decode_store = [&](const uint32_t (&W)[AW], uint16_t *slab) __attribute__((always_inline)) {
+            uint32_t w[16];
+            if (masked) decode_weights<FAM, N, true>(W, k, w);
+            else decode_weights<FAM, N, false>(W, k, w);
+            if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
+            }
+            uint16_t *cj = slab + (o * 16 + j) * G2_BP + r * 16;
+            uint16_t *cj8 = cj + 8 * G2_BP;
+            *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
+            *reinterpret_cast<uint4 *>(cj + 8) = uint4{w[1], w[5], w[9], w[13]};
+            *reinterpret_cast<uint4 *>(cj8) = uint4{w[2], w[6], w[10], w[14]};
+            *reinterpret_cast<uint4 *>(cj8 + 8) = uint4{w[3], w[7], w[11], w[15]};
+        };
+        uint32_t W0[AW], W1[AW];
+        load_tile(0, W0);
+        load_tile(1, W1);
+        __builtin_amdgcn_sched_barrier(0);
+        decode_store(W0, Bs[0]);
+        __syncthreads();  // barrier 0: slab 0 is ready
+        // Step ks: words of step ks + 1 are in hand; load step ks + 2 into the set just freed, decode ks + 1 into
+        // the idle slab (the last step decodes a repeat into it, never read), barrier.  Two steps per pass so the
+        // word sets alternate without copies.
+        auto dstep = [&](int ks, const uint32_t (&Wc)[AW], uint32_t (&Wn)[AW]) __attribute__((always_inline)) {
+            load_tile(ks + 2, Wn);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_store(Wc, Bs[(ks + 1) & 1]);
+            __syncthreads();
+        };
+        for (int ks = 0; ks < nks; ks += 2) {
+            dstep(ks, W1, W0);
+            dstep(ks + 1, W0, W1);
+        }
+        return;
+    }
+
+    // ---- MFMA waves
+    const int m0 = mt * G2_MT + wave * 64;
+    const int c = lane & 15, h = lane >> 4;
+    // A fragments in fragment order: tile rt's 32-k block kb is 1 KiB at ((g * RT + rt) * in/32 + kb) * 512 halves.
+    // Row tiles past the last (a 256-row tile over fewer rows) read the last one: their rows are never stored.
+    const int RT = (a.rows + 15) / 16;
+    const uint16_t *xfrag[4];
 #pragma unroll
     for (int rb = 0; rb < 4; rb++) {
-        const int m = m0 + rb * 16 + c;
-        xrow[rb] = a.xp + ((size_t)g * a.rows + (m < a.rows ? m : 0)) * a.in + 8 * h;
+        const int rt = min(m0 / 16 + rb, RT - 1);
+        xfrag[rb] = a.xp + ((size_t)g * RT + rt) * (size_t)(a.in / 32) * 512 + (size_t)lane * 8;
     }
-    auto load_a = [&](int ks, uint4 (&A)[4][2]) {
-#pragma unroll
-        for (int rb = 0; rb < 4; rb++)
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) A[rb][kb] = *reinterpret_cast<const uint4 *>(xrow[rb] + ks * 64 + kb * 32);
-    };
-    auto load_tile = [&](int ks, uint32_t (&W)[AW]) {
-        const int tk = ks * 4 + wave;
-        load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * OT + og * 8 + o) * N), j, W);
-    };
-    auto decode_store = [&](const uint32_t (&W)[AW], uint16_t *slab) {
-        uint32_t w[16];
-        if (masked) decode_weights<FAM, N, true>(W, k, w);
-        else decode_weights<FAM, N, false>(W, k, w);
-        if constexpr (family_scaled<FAM>()) {  // MFMA takes the weight itself: fold the 2^12 back in (exact)
-#pragma unroll
-            for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
-        }
-        // column j: rows 0-7 = pairs 0, 4, 8, 12; rows 8-15 = 1, 5, 9, 13; column j + 8: 2, 6, 10, 14 and 3, 7, 11, 15
-        uint16_t *cj = slab + (o * 16 + j) * G2_BP + wave * 16;
-        uint16_t *cj8 = cj + 8 * G2_BP;
-        *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
-        *reinterpret_cast<uint4 *>(cj + 8) = uint4{w[1], w[5], w[9], w[13]};
-        *reinterpret_cast<uint4 *>(cj8) = uint4{w[2], w[6], w[10], w[14]};
-        *reinterpret_cast<uint4 *>(cj8 + 8) = uint4{w[3], w[7], w[11], w[15]};
-    };
-
     f4_t acc[4][8];
 #pragma unroll
     for (int rb = 0; rb < 4; rb++)
 #pragma unroll
         for (int cb = 0; cb < 8; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-    // One k-step: issue the loads of the next step (tile words, A fragments into `an`), run this step's MFMAs from
-    // the slab and `ac`, decode the next slab, barrier.  Steps alternate the two A register sets, so each MFMA reads
-    // fragments loaded a whole step earlier and no register copy waits for a load.  The next step's loads and decode
-    // are unconditional (the last step re-reads step nks - 1 and decodes into the idle slab): a branch around them
-    // would make the compiler's load counting assume the branch-free path and wait for loads issued in this step.
-    const int nks = IT / 4;  // even: in is a multiple of 128
-    auto step = [&](int ks, const uint4 (&ac)[4][2], uint4 (&an)[4][2]) {
-        const int kn = min(ks + 1, nks - 1);
-        uint32_t Wn[AW];
-        load_tile(kn, Wn);
-        load_a(kn, an);
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads at the top of the step (the scheduler sinks them)
+    // One A register set: after the MFMAs of k-half kb the fragments A[.][kb] are dead, and the next step's are
+    // loaded into them at once (half a step ahead of their use).  The registers that frees double-buffer the B
+    // fragments: the slab read of (kb, cb + 1) is in flight while the MFMAs of (kb, cb) run.
+    uint4 A[4][2];
+    auto load_a_half = [&](int ks, int kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+            A[rb][kb] = *reinterpret_cast<const uint4 *>(xfrag[rb] + (size_t)(ks * 2 + kb) * 512);
+    };
+    auto read_b = [&](const uint16_t *slab, int kb, int cb) __attribute__((always_inline)) {
+        return *reinterpret_cast<const uint4 *>(slab + (cb * 16 + c) * G2_BP + kb * 32 + 8 * h);
+    };
+    load_a_half(0, 0);
+    load_a_half(0, 1);
+    __syncthreads();  // barrier 0
+    for (int ks = 0; ks < nks; ks++) {
         const uint16_t *slab = Bs[ks & 1];
+        const int kn = min(ks + 1, nks - 1);
+        uint4 b0 = read_b(slab, 0, 0), b1;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
             for (int cb = 0; cb < 8; cb++) {
-                const uint4 bv = *reinterpret_cast<const uint4 *>(slab + (cb * 16 + c) * G2_BP + kb * 32 + 8 * h);
-                const h8_t B8 = __builtin_bit_cast(h8_t, bv);
+                const bool more = kb == 0 || cb < 7;
+                if (more) b1 = read_b(slab, cb < 7 ? kb : 1, cb < 7 ? cb + 1 : 0);
+                const h8_t B8 = __builtin_bit_cast(h8_t, b0);
 #pragma unroll
                 for (int rb = 0; rb < 4; rb++)
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, ac[rb][kb]), B8,
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, A[rb][kb]), B8,
                                                                          acc[rb][cb], 0, 0, 0);
+                if (more) b0 = b1;
             }
+            load_a_half(kn, kb);
         }
-        decode_store(Wn, Bs[(ks + 1) & 1]);
         __syncthreads();
-    };
-    uint4 A0[4][2], A1[4][2];
-    {
-        uint32_t W[AW];
-        load_tile(0, W);
-        load_a(0, A0);
-        decode_store(W, Bs[0]);
-    }
-    __syncthreads();
-    for (int ks = 0; ks < nks; ks += 2) {
-        step(ks, A0, A1);
-        step(ks + 1, A1, A0);
     }
 
-    // ---- epilogue: each wave stages 16 of its rows at a time in LDS (its own region of the slab space), then
-    // FWHT-128 + svh per row
+    // ---- epilogue (MFMA waves only; the decode waves have left): each wave stages 16 of its rows at a time in LDS
+    // (its own region of the slab space), then FWHT-128 + svh per row
     float *ep = reinterpret_cast<float *>(&Bs[0][0]) + wave * 16 * G2_EP;
     const size_t sv = (size_t)g * a.out + (size_t)og * 128;
     const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
@@ -370,9 +425,13 @@ __global__ __launch_bounds__(G2_THREADS) void gemm2_kernel(GemmArgs a) {
 }
 
 template <int FAM, int N>
-static hipError_t launch_gemm2_n(const GemmArgs &a, hipStream_t s) {
+static hipError_t launch_gemm3_n(const GemmArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(gemm_prepare_frag_kernel, dim3((unsigned)(a.in / 128), (unsigned)((a.rows + 15) / 16),
+                                                      (unsigned)a.groups), dim3(256), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     dim3 grid((unsigned)((a.out / 128) * ((a.rows + G2_MT - 1) / G2_MT)), 1, (unsigned)a.groups);
-    hipLaunchKernelGGL((gemm2_kernel<FAM, N>), grid, dim3(G2_THREADS), 0, s, a);
+    hipLaunchKernelGGL((gemm3_kernel<FAM, N>), grid, dim3(G3_THREADS), 0, s, a);
     return hipGetLastError();
 }
 
@@ -385,19 +444,19 @@ static hipError_t launch_gemm_n(const GemmArgs &a, const uint16_t *wt, hipStream
 
 template <int FAM>
 static hipError_t launch_gemm_fam(const GemmArgs &a, hipStream_t s) {
+    switch (a.n) {
+    case 16: return launch_gemm3_n<FAM, 16>(a, s);
+    case 24: return launch_gemm3_n<FAM, 24>(a, s);
+    case 32: return launch_gemm3_n<FAM, 32>(a, s);
+    case 40: return launch_gemm3_n<FAM, 40>(a, s);
+    case 48: return launch_gemm3_n<FAM, 48>(a, s);
+    case 64: return launch_gemm3_n<FAM, 64>(a, s);
+    default: break;
+    }
     hipLaunchKernelGGL(gemm_prepare_kernel, dim3((unsigned)(a.in / 128), (unsigned)a.rows, (unsigned)a.groups),
                        dim3(64), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    switch (a.n) {
-    case 16: return launch_gemm2_n<FAM, 16>(a, s);
-    case 24: return launch_gemm2_n<FAM, 24>(a, s);
-    case 32: return launch_gemm2_n<FAM, 32>(a, s);
-    case 40: return launch_gemm2_n<FAM, 40>(a, s);
-    case 48: return launch_gemm2_n<FAM, 48>(a, s);
-    case 64: return launch_gemm2_n<FAM, 64>(a, s);
-    default: break;
-    }
     // Any other rate: decode to a transposed f16 copy in workspace (held after xp), then the same MFMA body.
     uint16_t *wt = a.wt;
     hipLaunchKernelGGL(gemm_decode_transposed_kernel<FAM>,

@@ -134,7 +134,7 @@ struct GemmArgs {
     const uint16_t *suh;
     const uint16_t *svh;
     DecodeK k;
-    uint16_t *xp;     // workspace [groups][rows][in] f16
+    uint16_t *xp;     // workspace: prepared input, f16 -- [groups][rows][in], or in MFMA A-fragment order (see gemm)
     uint16_t *wt;     // workspace [groups][out][in] f16 (rates without a direct reader)
     void *y;
     int y_dtype;
