@@ -253,22 +253,23 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
 //
 // A workgroup owns a 256-row x 128-column output tile (one Hadamard block wide, so the FWHT + svh finish runs in its
 // epilogue) over all of k, in k-steps of 64 (four trellis k-tiles), with the decode and the MFMAs on different waves.
-// Waves 4-7 decode: wave 4 + r decodes k-tile row r of every step (lane 8o + j: codewords 32j..32j+31 of tile o =
+// Waves 8-11 decode: wave 8 + r decodes k-tile row r of every step (lane 8o + j: codewords 32j..32j+31 of tile o =
 // columns j and j+8 over 16 k rows, the GEMV's lane decoder) into a double-buffered LDS slab held column-major
-// (B[col][k]), its tile words loaded two steps ahead.  Waves 0-3 run the MFMAs: 64 rows x 128 columns each, as
-// 4 x 8 v_mfma_f32_16x16x32_f16 tiles per 32 k, with A fragments read from the prepared input in fragment order (one
-// contiguous 1 KiB per load) and B fragments from the slab.  Each SIMD then holds one MFMA wave and one decode wave,
-// so the matrix core and the VALU work at the same time.  One workgroup barrier per step hands the slab over: after
-// barrier ks + 1 the MFMA waves have finished reading slab ks & 1 and the decode waves have finished writing slab
-// (ks + 1) & 1.  Every weight is decoded once per 256-row tile.
+// (B[col][k]), its tile words loaded two steps ahead.  Waves 0-7 run the MFMAs: wave w owns rows 64 (w >> 1) .. + 63
+// and columns 64 (w & 1) .. + 63 as 4 x 4 v_mfma_f32_16x16x32_f16 tiles per 32 k, with A fragments read from the
+// prepared input in fragment order (one contiguous 1 KiB per load, half a step ahead) and all B fragments of a step
+// read from the slab before its first MFMA.  Each SIMD holds two MFMA waves and one decode wave, so the matrix core
+// has a second wave to issue from and the VALU decodes beside it.  One workgroup barrier per step hands the slab
+// over: after barrier ks + 1 the MFMA waves have finished reading slab ks & 1 and the decode waves have finished
+// writing slab (ks + 1) & 1.  Every weight is decoded once per 256-row tile.
 constexpr int G2_MT = 256;   // rows per workgroup
 constexpr int G2_BP = 72;    // LDS pitch (halves) of one slab column: 64 k + 8 pad (16-byte aligned rows)
 constexpr int G2_EP = 129;   // epilogue staging pitch (floats)
-constexpr int G3_WAVES = 8;
-constexpr int G3_THREADS = 64 * G3_WAVES;
+constexpr int G4_WAVES = 12;
+constexpr int G4_THREADS = 64 * G4_WAVES;
 
 template <int FAM, int N>
-__global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
+__global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int IT = a.in >> 4, OT = a.out >> 4;
@@ -288,9 +289,9 @@ __global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
     const int nks = IT / 4;  // even: in is a multiple of 128
     constexpr int AW = LaneBits<N>::AW;
 
-    if (wave >= 4) {
+    if (wave >= 8) {
         // ---- decode waves
-        const int r = wave - 4;
+        const int r = wave - 8;
         const int o = lane >> 3, j = lane & 7;
         const DecodeK k = a.k;
         const bool masked = k.wmask != 0xFFFFu;
@@ -320,9 +321,6 @@ __global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         decode_store(W0, Bs[0]);
         __syncthreads();  // barrier 0: slab 0 is ready
-        // Step ks: words of step ks + 1 are in hand; load step ks + 2 into the set just freed, decode ks + 1 into
-        // the idle slab (the last step decodes a repeat into it, never read), barrier.  Two steps per pass so the
-        // word sets alternate without copies.
         auto dstep = [&](int ks, const uint32_t (&Wc)[AW], uint32_t (&Wn)[AW]) __attribute__((always_inline)) {
             load_tile(ks + 2, Wn);
             __builtin_amdgcn_sched_barrier(0);
@@ -337,10 +335,8 @@ __global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
     }
 
     // ---- MFMA waves
-    const int m0 = mt * G2_MT + wave * 64;
+    const int m0 = mt * G2_MT + (wave >> 1) * 64, cb0 = (wave & 1) * 4;
     const int c = lane & 15, h = lane >> 4;
-    // A fragments in fragment order: tile rt's 32-k block kb is 1 KiB at ((g * RT + rt) * in/32 + kb) * 512 halves.
-    // Row tiles past the last (a 256-row tile over fewer rows) read the last one: their rows are never stored.
     const int RT = (a.rows + 15) / 16;
     const uint16_t *xfrag[4];
 #pragma unroll
@@ -348,22 +344,16 @@ __global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
         const int rt = min(m0 / 16 + rb, RT - 1);
         xfrag[rb] = a.xp + ((size_t)g * RT + rt) * (size_t)(a.in / 32) * 512 + (size_t)lane * 8;
     }
-    f4_t acc[4][8];
+    f4_t acc[4][4];
 #pragma unroll
     for (int rb = 0; rb < 4; rb++)
 #pragma unroll
-        for (int cb = 0; cb < 8; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
-    // One A register set: after the MFMAs of k-half kb the fragments A[.][kb] are dead, and the next step's are
-    // loaded into them at once (half a step ahead of their use).  The registers that frees double-buffer the B
-    // fragments: the slab read of (kb, cb + 1) is in flight while the MFMAs of (kb, cb) run.
+        for (int cb = 0; cb < 4; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
     uint4 A[4][2];
     auto load_a_half = [&](int ks, int kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int rb = 0; rb < 4; rb++)
             A[rb][kb] = *reinterpret_cast<const uint4 *>(xfrag[rb] + (size_t)(ks * 2 + kb) * 512);
-    };
-    auto read_b = [&](const uint16_t *slab, int kb, int cb) __attribute__((always_inline)) {
-        return *reinterpret_cast<const uint4 *>(slab + (cb * 16 + c) * G2_BP + kb * 32 + 8 * h);
     };
     load_a_half(0, 0);
     load_a_half(0, 1);
@@ -371,38 +361,42 @@ __global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
     for (int ks = 0; ks < nks; ks++) {
         const uint16_t *slab = Bs[ks & 1];
         const int kn = min(ks + 1, nks - 1);
-        uint4 b0 = read_b(slab, 0, 0), b1;
+        uint4 bv[2][4];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++)
+                bv[kb][cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G2_BP + kb * 32 + 8 * h);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
-            for (int cb = 0; cb < 8; cb++) {
-                const bool more = kb == 0 || cb < 7;
-                if (more) b1 = read_b(slab, cb < 7 ? kb : 1, cb < 7 ? cb + 1 : 0);
-                const h8_t B8 = __builtin_bit_cast(h8_t, b0);
+            for (int cb = 0; cb < 4; cb++) {
+                const h8_t B8 = __builtin_bit_cast(h8_t, bv[kb][cb]);
 #pragma unroll
                 for (int rb = 0; rb < 4; rb++)
                     acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, A[rb][kb]), B8,
                                                                          acc[rb][cb], 0, 0, 0);
-                if (more) b0 = b1;
             }
             load_a_half(kn, kb);
         }
         __syncthreads();
     }
 
-    // ---- epilogue (MFMA waves only; the decode waves have left): each wave stages 16 of its rows at a time in LDS
-    // (its own region of the slab space), then FWHT-128 + svh per row
-    float *ep = reinterpret_cast<float *>(&Bs[0][0]) + wave * 16 * G2_EP;
+    // ---- epilogue (the decode waves have left, so the barriers below join the 8 MFMA waves): per 16-row block, the
+    // two waves of a row group stage their column halves side by side in LDS, then each finishes 8 of the rows
+    // (FWHT-128 + svh).
+    float *ep = reinterpret_cast<float *>(&Bs[0][0]) + (wave >> 1) * 16 * G2_EP;
     const size_t sv = (size_t)g * a.out + (size_t)og * 128;
     const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
 #pragma unroll
     for (int rb = 0; rb < 4; rb++) {
 #pragma unroll
-        for (int cb = 0; cb < 8; cb++)
+        for (int cb = 0; cb < 4; cb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) ep[(4 * h + i) * G2_EP + cb * 16 + c] = acc[rb][cb][i];
-        __builtin_amdgcn_wave_barrier();
-        for (int r = 0; r < 16; r++) {
+            for (int i = 0; i < 4; i++) ep[(4 * h + i) * G2_EP + (cb0 + cb) * 16 + c] = acc[rb][cb][i];
+        __syncthreads();
+        for (int r = (wave & 1) * 8; r < (wave & 1) * 8 + 8; r++) {
             const int m = m0 + rb * 16 + r;
             if (m >= a.rows) break;
             float v0 = ep[r * G2_EP + lane], v1 = ep[r * G2_EP + lane + 64];
@@ -420,18 +414,18 @@ __global__ __launch_bounds__(G3_THREADS) void gemm3_kernel(GemmArgs a) {
                 store_act<DT_F32>(a.y, yo + lane + 64, y1);
             }
         }
-        __builtin_amdgcn_wave_barrier();
+        __syncthreads();
     }
 }
 
 template <int FAM, int N>
-static hipError_t launch_gemm3_n(const GemmArgs &a, hipStream_t s) {
+static hipError_t launch_gemm_lane_n(const GemmArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(gemm_prepare_frag_kernel, dim3((unsigned)(a.in / 128), (unsigned)((a.rows + 15) / 16),
                                                       (unsigned)a.groups), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     dim3 grid((unsigned)((a.out / 128) * ((a.rows + G2_MT - 1) / G2_MT)), 1, (unsigned)a.groups);
-    hipLaunchKernelGGL((gemm3_kernel<FAM, N>), grid, dim3(G3_THREADS), 0, s, a);
+    hipLaunchKernelGGL((gemm4_kernel<FAM, N>), grid, dim3(G4_THREADS), 0, s, a);
     return hipGetLastError();
 }
 
@@ -445,12 +439,12 @@ static hipError_t launch_gemm_n(const GemmArgs &a, const uint16_t *wt, hipStream
 template <int FAM>
 static hipError_t launch_gemm_fam(const GemmArgs &a, hipStream_t s) {
     switch (a.n) {
-    case 16: return launch_gemm3_n<FAM, 16>(a, s);
-    case 24: return launch_gemm3_n<FAM, 24>(a, s);
-    case 32: return launch_gemm3_n<FAM, 32>(a, s);
-    case 40: return launch_gemm3_n<FAM, 40>(a, s);
-    case 48: return launch_gemm3_n<FAM, 48>(a, s);
-    case 64: return launch_gemm3_n<FAM, 64>(a, s);
+    case 16: return launch_gemm_lane_n<FAM, 16>(a, s);
+    case 24: return launch_gemm_lane_n<FAM, 24>(a, s);
+    case 32: return launch_gemm_lane_n<FAM, 32>(a, s);
+    case 40: return launch_gemm_lane_n<FAM, 40>(a, s);
+    case 48: return launch_gemm_lane_n<FAM, 48>(a, s);
+    case 64: return launch_gemm_lane_n<FAM, 64>(a, s);
     default: break;
     }
     hipLaunchKernelGGL(gemm_prepare_kernel, dim3((unsigned)(a.in / 128), (unsigned)a.rows, (unsigned)a.groups),
