@@ -40,6 +40,8 @@ CFLAGS = [
     "-Wno-unused-variable",
     # Packed FP32 (v_pk_*_f32) stays off: hipcc would otherwise form it from scalar float code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar kernel arguments arrive preloaded in SGPRs (the GEMV's first loads need no argument load).
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 

@@ -88,7 +88,7 @@ __device__ __forceinline__ float silu(float g) {
 }
 
 struct GemvCtx {
-    int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div;
+    int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div, x_dtype;
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
     const uint32_t *wslots;     // the window's slots, or null (group = slot, or plain rows)
     const void *x;
@@ -111,7 +111,7 @@ __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c
 template <bool WIN>
 __device__ __forceinline__ size_t x_row(const GemvArgs &a, const GemvCtx &c, int r) {
     if constexpr (WIN) return (size_t)(c.wslots[r] / c.x_div);
-    else return (size_t)(c.g / c.x_div) * a.rows + r;
+    else return (size_t)(c.g / c.x_div) * c.rows + r;
 }
 template <bool WIN>
 __device__ __forceinline__ size_t part_row(const GemvArgs &a, const GemvCtx &c, int r) {
@@ -217,10 +217,11 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx 
             int rho = job / nblk, b = job - rho * nblk;
             if (!(job < nblk * RT && rho < c.rows)) rho = b = 0;
             const int kb = c.kt0 * 16 + b * 128;
-            const size_t si = (size_t)c.bank * a.in + kb;
-            const size_t xi = x_row<WIN>(a, c, rho) * a.in + kb;
-            pr.x0[i] = load_x_nb(c.x, a.x_dtype, xi + lane);
-            pr.x1[i] = load_x_nb(c.x, a.x_dtype, xi + lane + 64);
+            const size_t in = (size_t)c.IT << 4;
+            const size_t si = (size_t)c.bank * in + kb;
+            const size_t xi = x_row<WIN>(a, c, rho) * in + kb;
+            pr.x0[i] = load_x_nb(c.x, c.x_dtype, xi + lane);
+            pr.x1[i] = load_x_nb(c.x, c.x_dtype, xi + lane + 64);
             pr.s0[i] = h2f(c.suh[si + lane]);
             pr.s1[i] = h2f(c.suh[si + lane + 64]);
         }
@@ -383,9 +384,16 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
     }
 }
 
+// svh of this lane's two outputs, for the finish.
+__device__ __forceinline__ void fetch_svh(GemvCtx &c, int lane) {
+    const size_t sv = (size_t)c.bank * ((size_t)c.OT << 4) + (size_t)c.og * 128;
+    c.sv0 = h2f(c.svh[sv + lane]);
+    c.sv1 = h2f(c.svh[sv + lane + 64]);
+}
+
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 template <int FAM, int N, int RT, int PRO, bool WIN>
-__device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, const uint16_t *__restrict__ tb,
+__device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const uint16_t *__restrict__ tb,
                                           int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
@@ -410,6 +418,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
             load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
                                Aw[t]);
         }
+        fetch_svh(c, lane);
         prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
@@ -443,6 +452,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, const GemvCtx &c, c
             acc1[r] = accB[r >> 2][r & 3] * unscale;
         }
     } else {  // any other rate: the generic reader (runtime funnel per codeword)
+        fetch_svh(c, lane);
         PrologueRegs<RT> pr;
         prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
         prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
@@ -565,17 +575,16 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
 // (lane-reader rates / the other rates),
 // dispatched per workgroup.
 template <int FAM, int N, int RT, int PRO, bool WIN>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
-    // Everything below reads kernel arguments at fixed offsets and selects between projections instead of indexing
-    // by blockIdx.z, and the workgroup remap is branch free: all argument loads then issue in one batch.
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
+                                                            const uint32_t *bank_of, int in, int out, int splits,
+                                                            int rows, int x_dtype, int x_div, GemvArgs a) {
+    // The leading scalar arguments are the ones the first loads need (the input and suh of the prologue, the tile
+    // words): the build preloads them into SGPRs, so those loads issue without waiting for an argument load.  The
+    // struct `a` holds everything (the same values included) for the rest of the kernel.
     GemvCtx c;
-    // The scalar arguments the entry needs, pinned into registers together: one batch of argument loads, one wait.
-    int in = a.in, out = a.out, splits = a.splits, x_div = a.x_div, bank_limit = a.bank_limit;
-    const uint32_t *bank_of = a.bank_of;
-    const void *x = a.x;
-    asm volatile("" : "+s"(in), "+s"(out), "+s"(splits), "+s"(x_div), "+s"(bank_limit), "+s"(bank_of), "+s"(x));
     c.x = x;
     c.x_div = x_div;
+    c.x_dtype = x_dtype;
     c.IT = in >> 4;
     c.OT = out >> 4;
     c.G = c.OT >> 3;
@@ -583,32 +592,29 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     const int L = blockIdx.x;
     // keep an output group's splits on one XCD when G % 8 == 0 (workgroups go round-robin over the 8 XCDs)
     const bool remap = (c.G & 7) == 0;
-    const int r8 = L >> 3;
-    c.og = remap ? (r8 / c.S) * 8 + (L & 7) : L / c.S;
-    c.sp = remap ? r8 % c.S : L % c.S;
+    const unsigned us = (unsigned)c.S, q = remap ? (unsigned)L >> 3 : (unsigned)L, qs = q / us;
+    c.og = remap ? (int)qs * 8 + (L & 7) : (int)qs;
+    c.sp = (int)(q - qs * us);
     c.g = blockIdx.y;
     c.proj = blockIdx.z;
     const bool p1 = c.proj != 0;
-    c.suh = p1 ? a.suh[1] : a.suh[0];
+    c.suh = p1 ? a.suh[1] : suh0;
     c.svh = p1 ? a.svh[1] : a.svh[0];
     c.part = p1 ? a.partial[1] : a.partial[0];
-    const uint16_t *trellis = p1 ? a.trellis[1] : a.trellis[0];
-    c.rows = a.rows;
+    const uint16_t *trellis = p1 ? a.trellis[1] : tr0;
+    c.rows = rows;
     c.wslots = nullptr;
     if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
         if ((uint32_t)c.g >= *a.win_count) return;
-        c.bank = (int)min(a.win_expert[c.g], (uint32_t)(bank_limit - 1));
+        c.bank = (int)min(a.win_expert[c.g], (uint32_t)(a.bank_limit - 1));
         c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
         c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
     } else {
-        c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(bank_limit - 1)) : c.g;
+        c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
     }
     c.KS = c.IT / c.S;
     c.kt0 = c.sp * c.KS;
-    const int lane = threadIdx.x & 63;
-    const size_t sv = (size_t)c.bank * out + (size_t)c.og * 128;
-    c.sv0 = h2f(c.svh[sv + lane]);
-    c.sv1 = h2f(c.svh[sv + lane + 64]);
+    c.sv0 = c.sv1 = 0.f;  // fetched by gemv_body once the tile loads are out
 
     __shared__ __align__(16) uint16_t xs[RT][XS_PITCH];
     __shared__ float red[GEMV_WAVES][RT][128];
@@ -665,22 +671,28 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
     finish_block(a, c, r, v0, v1, lane);
 }
 
+template <int FAM, int N, int RT, int PRO, bool WIN>
+static void launch_one(const GemvArgs &a, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_kernel<FAM, N, RT, PRO, WIN>), grid, dim3(GEMV_THREADS), 0, s, a.x, a.trellis[0], a.suh[0],
+                       a.bank_of, a.in, a.out, a.splits, a.rows, a.x_dtype, a.x_div, a);
+}
+
 template <int FAM, int N, int PRO>
 static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
     const int G = a.out / 128;
     dim3 grid((unsigned)(G * a.splits), (unsigned)a.groups, (unsigned)a.nproj);
     if (a.win_count) {  // the sorted MoE arm: expert windows of MOE_WINDOW_ROWS rows, f32 planes or the fold out
         if (a.rows != MOE_WINDOW_ROWS || !(a.partial_only || a.fold)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemv_kernel<FAM, N, MOE_WINDOW_ROWS, PRO, true>), grid, dim3(GEMV_THREADS), 0, s, a);
+        launch_one<FAM, N, MOE_WINDOW_ROWS, PRO, true>(a, grid, s);
     } else if constexpr (PRO == PRO_X && N >= 0) {
-        if (a.rows <= 1) hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else if (a.rows <= 2) hipLaunchKernelGGL((gemv_kernel<FAM, N, 2, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else if (a.rows <= 4) hipLaunchKernelGGL((gemv_kernel<FAM, N, 4, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else if (a.rows <= 8) hipLaunchKernelGGL((gemv_kernel<FAM, N, 8, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<FAM, N, 16, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+        if (a.rows <= 1) launch_one<FAM, N, 1, PRO, false>(a, grid, s);
+        else if (a.rows <= 2) launch_one<FAM, N, 2, PRO, false>(a, grid, s);
+        else if (a.rows <= 4) launch_one<FAM, N, 4, PRO, false>(a, grid, s);
+        else if (a.rows <= 8) launch_one<FAM, N, 8, PRO, false>(a, grid, s);
+        else launch_one<FAM, N, 16, PRO, false>(a, grid, s);
     } else {  // the MoE decode chain: one row per (slot, bank) pair
         if (a.rows != 1) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemv_kernel<FAM, N, 1, PRO, false>), grid, dim3(GEMV_THREADS), 0, s, a);
+        launch_one<FAM, N, 1, PRO, false>(a, grid, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
