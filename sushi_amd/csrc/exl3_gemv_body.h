@@ -26,12 +26,6 @@
 
 namespace exl3 {
 
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, w), __builtin_bit_cast(h2_t, x), acc, false);
-}
-
 constexpr int GEMV_THREADS = 64 * GEMV_WAVES;
 constexpr int MAX_KSPAN = 2048;
 // LDS pitch (halves) of a prepared input row: 16 bytes past MAX_KSPAN, so the rows that the four lane groups of a
@@ -124,20 +118,33 @@ __device__ __forceinline__ int slot_of(const GemvCtx &c, int r) {
     else return c.g;
 }
 
-// Rows of the prepared input are read from LDS in chunks of XCH (all at once up to 8 rows): the fragments of the
-// first chunk are requested before the decode, so their LDS latency hides behind it.
+// The lane's 16 decoded pairs (w, already scaled for the matrix cores) against every batch row of k-tile kk.
 template <int RT>
-struct XChunk {
-    static constexpr int CH = RT == 4 ? 2 : RT <= 8 ? RT : 4;
-};
-
-template <int RT>
-__device__ __forceinline__ void load_x_chunk(const uint16_t (*xs)[XS_PITCH], int kk, int r0,
-                                             uint4 (&X)[XChunk<RT>::CH], uint4 (&Y)[XChunk<RT>::CH]) {
+__device__ __forceinline__ void mfma_dot(const uint32_t (&w)[16], const uint16_t (*xs)[XS_PITCH], int kk, int rows,
+                                         f4_t (&accA)[RowGroups<RT>::G], f4_t (&accB)[RowGroups<RT>::G], int i4) {
 #pragma unroll
-    for (int c = 0; c < XChunk<RT>::CH; c++) {
-        X[c] = *reinterpret_cast<const uint4 *>(&xs[r0 + c][kk * 16]);
-        Y[c] = *reinterpret_cast<const uint4 *>(&xs[r0 + c][kk * 16 + 8]);
+    for (int g = 0; g < RowGroups<RT>::G; g++) {
+        if (g > 0 && 4 * g >= rows) break;
+        const uint16_t *xg = &xs[min(4 * g + i4, RT - 1)][kk * 16];
+        const uint4 X = *reinterpret_cast<const uint4 *>(xg);
+        const uint4 Y = *reinterpret_cast<const uint4 *>(xg + 8);
+        accA[g] = mfma4(X.x, X.y, w[0], w[4], accA[g]);
+        accB[g] = mfma4(X.x, X.y, w[2], w[6], accB[g]);
+        accA[g] = mfma4(X.z, X.w, w[8], w[12], accA[g]);
+        accB[g] = mfma4(X.z, X.w, w[10], w[14], accB[g]);
+        accA[g] = mfma4(Y.x, Y.y, w[1], w[5], accA[g]);
+        accB[g] = mfma4(Y.x, Y.y, w[3], w[7], accB[g]);
+        accA[g] = mfma4(Y.z, Y.w, w[9], w[13], accA[g]);
+        accB[g] = mfma4(Y.z, Y.w, w[11], w[15], accB[g]);
+    }
+}
+
+// Matrix instructions take the hash / pair weights times 2^12 (the caller takes it back out of the sums, exactly).
+template <int FAM>
+__device__ __forceinline__ void scale_for_mfma(uint32_t (&w)[16]) {
+    if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
     }
 }
 
@@ -151,32 +158,10 @@ template <int FAM, int N, int RT, bool MASKED>
 __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[XS_PITCH],
                                             int kk, int rows, const DecodeK &k, f4_t (&accA)[RowGroups<RT>::G],
                                             f4_t (&accB)[RowGroups<RT>::G], int i4) {
-    const uint16_t *xr = &xs[min(i4, RT - 1)][kk * 16];
-    uint4 X = *reinterpret_cast<const uint4 *>(xr);
-    uint4 Y = *reinterpret_cast<const uint4 *>(xr + 8);
     uint32_t w[16];
     decode_weights<FAM, N, MASKED>(A, k, w);
-    if constexpr (family_scaled<FAM>()) {  // the caller takes the 2^12 back out of the sums (exact)
-#pragma unroll
-        for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
-    }
-#pragma unroll
-    for (int g = 0; g < RowGroups<RT>::G; g++) {
-        if (g > 0) {
-            if (4 * g >= rows) break;
-            const uint16_t *xg = &xs[min(4 * g + i4, RT - 1)][kk * 16];
-            X = *reinterpret_cast<const uint4 *>(xg);
-            Y = *reinterpret_cast<const uint4 *>(xg + 8);
-        }
-        accA[g] = mfma4(X.x, X.y, w[0], w[4], accA[g]);
-        accB[g] = mfma4(X.x, X.y, w[2], w[6], accB[g]);
-        accA[g] = mfma4(X.z, X.w, w[8], w[12], accA[g]);
-        accB[g] = mfma4(X.z, X.w, w[10], w[14], accB[g]);
-        accA[g] = mfma4(Y.x, Y.y, w[1], w[5], accA[g]);
-        accB[g] = mfma4(Y.x, Y.y, w[3], w[7], accB[g]);
-        accA[g] = mfma4(Y.z, Y.w, w[9], w[13], accA[g]);
-        accB[g] = mfma4(Y.z, Y.w, w[11], w[15], accB[g]);
-    }
+    scale_for_mfma<FAM>(w);
+    mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4);
 }
 
 // x[i] as f32 from an f16 / bf16 / f32 array without branching on the dtype: one 32-bit load of the aligned word
@@ -398,9 +383,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
     const int o = lane >> 3, j = lane & 7;
-    float acc0[RT], acc1[RT];
+    constexpr int RG = RowGroups<RT>::G;
+    f4_t accA[RG], accB[RG];
 #pragma unroll
-    for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
+    for (int g = 0; g < RG; g++) accA[g] = accB[g] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     if constexpr (N != 0) {
         constexpr int AW = LaneBits<N>::AW;
@@ -422,10 +408,6 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
-        constexpr int RG = RowGroups<RT>::G;
-        f4_t accA[RG], accB[RG];
-#pragma unroll
-        for (int g = 0; g < RG; g++) accA[g] = accB[g] = f4_t{0.f, 0.f, 0.f, 0.f};
         for (int t0 = 0; t0 < ntiles; t0 += TPW) {
             if (t0 > 0) {  // splits longer than TPW tiles per wave: load the next batch in place
 #pragma unroll
@@ -444,13 +426,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
                 }
             }
         }
-        // the hash / pair weights went in times 2^12; out_scale applies the codebook scale to every arm alike
-        constexpr float unscale = family_scaled<FAM>() ? 1.0f / 4096.0f : 1.0f;
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            acc0[r] = accA[r >> 2][r & 3] * unscale;
-            acc1[r] = accB[r >> 2][r & 3] * unscale;
-        }
+
     } else {  // any other rate: the generic reader (runtime funnel per codeword)
         fetch_svh(c, lane);
         PrologueRegs<RT> pr;
@@ -466,25 +442,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
                 const int t = 32 * j + 2 * i;
                 w[i] = decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
             }
-            constexpr int CH = XChunk<RT>::CH;
-#pragma unroll
-            for (int r0 = 0; r0 < RT; r0 += CH) {
-                if (r0 > 0 && r0 >= c.rows) break;
-                uint4 X[CH], Y[CH];
-                load_x_chunk<RT>(xs, kk, r0, X, Y);
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int qq = i >> 2, p = i & 3;
-#pragma unroll
-                    for (int cc = 0; cc < CH; cc++) {
-                        const uint4 &V = (p & 1) ? Y[cc] : X[cc];
-                        const uint32_t xv = qq == 0 ? V.x : qq == 1 ? V.y : qq == 2 ? V.z : V.w;
-                        if (p < 2) acc0[r0 + cc] = dot2(w[i], xv, acc0[r0 + cc]);
-                        else acc1[r0 + cc] = dot2(w[i], xv, acc1[r0 + cc]);
-                    }
-                }
-            }
+            scale_for_mfma<FAM>(w);
+            mfma_dot<RT>(w, xs, kk, c.rows, accA, accB, lane & 3);
         }
+    }
+    // the hash / pair weights went in times 2^12; out_scale applies the codebook scale to every arm alike
+    constexpr float unscale = family_scaled<FAM>() ? 1.0f / 4096.0f : 1.0f;
+    float acc0[RT], acc1[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        acc0[r] = accA[r >> 2][r & 3] * unscale;
+        acc1[r] = accB[r >> 2][r & 3] * unscale;
     }
 
     // ---- cross-wave reduction

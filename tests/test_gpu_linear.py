@@ -65,10 +65,11 @@ def test_gemv_codebooks(dev, label, n):
     assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 512, n, odec)) < BAR
 
 
-@pytest.mark.parametrize("n", [18, 22, 44, 58, 66, 96, 128])
-def test_gemv_generic_rates(dev, n):
-    print(f"[gemv] generic n={n}", flush=True)
-    p, pd, x, xd = _case(dev, 3, 3, 256, 256, n)
+@pytest.mark.parametrize("n,rows", [(18, 3), (22, 3), (44, 3), (58, 3), (66, 3), (96, 3), (128, 3), (22, 12), (66, 16),
+                                    (44, 16)])
+def test_gemv_generic_rates(dev, n, rows):
+    print(f"[gemv] generic n={n} rows={rows}", flush=True)
+    p, pd, x, xd = _case(dev, 3, rows, 256, 256, n)
     dec, odec = DECODES["spec1"] if n < 24 or n > 64 else DECODES["pair1"]
     assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 256, n, odec)) < BAR
 
