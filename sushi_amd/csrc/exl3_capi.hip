@@ -235,7 +235,7 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
     // (the most splits), so the planes fit whatever the routing turns out to be.
     const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS : nslots;
     const int rows = windowed ? MOE_WINDOW_ROWS : 1;
-    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups);
+    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 2);  // up to two tile batches per wave
     p.s2 = gemv_default_splits(inter, hidden, rows, groups);
     p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
     p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));

@@ -183,21 +183,22 @@ __device__ __forceinline__ float load_x_nb(const void *x, int dt, size_t i) {
 // The prologue's input loads for a wave's first jobs, issued ahead of the tile loads (loads retire in order, so an
 // input load issued behind 16 KiB of tile loads would hold the prologue back until all of them had landed).  Loads
 // are unconditional (a job past the end re-reads job 0 and is then discarded): no branch, so no early wait.
-template <int RT>
+template <int RT, bool WIN>
 struct PrologueRegs {
     // jobs per wave when a split spans at most TPW * GEMV_WAVES k-tiles (TPW * GEMV_WAVES / 8 blocks per row), at
-    // most 4 held in registers (past that the prologue loads as it goes: 16 rows would otherwise spill)
-    static constexpr int JOBS = (RT * TPW / 8) < 1 ? 1 : (RT * TPW / 8) > 4 ? 4 : (RT * TPW / 8);
+    // most 4 held in registers (past that the prologue loads as it goes: 16 rows would otherwise spill); the sorted
+    // MoE arm's splits span up to two such batches, so its windows hold 4
+    static constexpr int JOBS = WIN ? 4 : (RT * TPW / 8) < 1 ? 1 : (RT * TPW / 8) > 4 ? 4 : (RT * TPW / 8);
     float x0[JOBS], x1[JOBS], s0[JOBS], s1[JOBS];
 };
 
 template <int PRO, int RT, bool WIN>
 __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx &c, int wave, int lane,
-                                               PrologueRegs<RT> &pr) {
+                                               PrologueRegs<RT, WIN> &pr) {
     if constexpr (PRO == PRO_X) {
         const int nblk = c.KS >> 3;
 #pragma unroll
-        for (int i = 0; i < PrologueRegs<RT>::JOBS; i++) {
+        for (int i = 0; i < PrologueRegs<RT, WIN>::JOBS; i++) {
             int job = wave + GEMV_WAVES * i;
             int rho = job / nblk, b = job - rho * nblk;
             if (!(job < nblk * RT && rho < c.rows)) rho = b = 0;
@@ -244,7 +245,7 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, 
 
 template <int PRO, int RT, bool WIN>
 __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[XS_PITCH], int wave,
-                                         int lane, const PrologueRegs<RT> &pr) {
+                                         int lane, const PrologueRegs<RT, WIN> &pr) {
     const int nblk = c.KS >> 3;
     for (int job = wave; job < nblk * RT; job += GEMV_WAVES) {
         const int rho = job / nblk, b = job - rho * nblk;
@@ -254,7 +255,7 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
         if (rho < c.rows) {
             const size_t si = (size_t)c.bank * a.in + kb;
             if constexpr (PRO == PRO_X) {  // prepareInput (expert_exl3.zig:490-501)
-                if (i < PrologueRegs<RT>::JOBS) {
+                if (i < PrologueRegs<RT, WIN>::JOBS) {
                     v0 = f16r(pr.x0[i]) * pr.s0[i];
                     v1 = f16r(pr.x1[i]) * pr.s1[i];
                 } else {
@@ -394,7 +395,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         // wave has at least one.  The first TPW loads are issued unconditionally (a wave with fewer tiles re-reads its
         // last one), so the compiler counts them and each tile's decode waits only for that tile's own loads.
         const int ntiles = (c.KS - wave + GEMV_WAVES - 1) / GEMV_WAVES;
-        PrologueRegs<RT> pr;
+        PrologueRegs<RT, WIN> pr;
         prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
         __builtin_amdgcn_sched_barrier(0);  // the input loads stay ahead of the tile loads (vmcnt retires in order)
         uint32_t Aw[TPW][AW];
@@ -408,28 +409,31 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
-        for (int t0 = 0; t0 < ntiles; t0 += TPW) {
-            if (t0 > 0) {  // splits longer than TPW tiles per wave: load the next batch in place
-#pragma unroll
-                for (int t = 0; t < TPW; t++) {
-                    const int tk = c.kt0 + wave + GEMV_WAVES * min(t0 + t, ntiles - 1);
-                    load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n),
-                                       j, Aw[t]);
-                }
-            }
+        auto decode_at = [&](int t, int tt) __attribute__((always_inline)) {  // slot t holds the wave's tile tt
+            const int kk = wave + GEMV_WAVES * tt;
+            if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
+            else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
+        };
+        int t0 = 0;
+        // Splits longer than TPW tiles per wave: every batch but the last refills each slot with the same slot of the
+        // next batch as soon as it is decoded, so the next batch's words are in flight while this batch's remaining
+        // tiles decode (a slot past the end re-reads the wave's last tile).
+        for (; t0 + TPW < ntiles; t0 += TPW) {
 #pragma unroll
             for (int t = 0; t < TPW; t++) {
-                if (t0 + t < ntiles) {
-                    const int kk = wave + GEMV_WAVES * (t0 + t);
-                    if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
-                    else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
-                }
+                decode_at(t, t0 + t);
+                const int tk = c.kt0 + wave + GEMV_WAVES * min(t0 + TPW + t, ntiles - 1);
+                load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
+                                   Aw[t]);
             }
         }
+#pragma unroll
+        for (int t = 0; t < TPW; t++)
+            if (t0 + t < ntiles) decode_at(t, t0 + t);
 
     } else {  // any other rate: the generic reader (runtime funnel per codeword)
         fetch_svh(c, lane);
-        PrologueRegs<RT> pr;
+        PrologueRegs<RT, WIN> pr;
         prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
         prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
         __syncthreads();

@@ -20,17 +20,19 @@ hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s) {
     }
 }
 
-int gemv_default_splits(int in, int out, int rows, int groups_times_proj) {
+int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches) {
     // Splits cut k on whole Hadamard blocks.  A split of at most TPW * GEMV_WAVES k-tiles lets every wave issue all
-    // of its tile loads before the prologue; past that, more splits only add partial traffic unless the grid is
-    // still short of one workgroup per CU.
+    // of its tile loads before the prologue; up to max_batches such batches per wave are allowed where the grid is
+    // large (each workgroup then pays its start-up latency once for more work, the later batches' loads overlapping
+    // the decode).  Past that, more splits only add partial traffic unless the grid is still short of one workgroup
+    // per CU.
     const int blocks = in / 128;
     const int it = in / 16;
     const long G = (long)(out / 128) * groups_times_proj;
     int best = blocks;
     for (int s = 1; s <= blocks; s++) {
         if (blocks % s) continue;
-        if (it / s > TPW * GEMV_WAVES) continue;
+        if (it / s > TPW * GEMV_WAVES * max_batches) continue;
         best = s;
         if (G * s >= GEMV_TARGET_WGS) break;
     }
