@@ -115,7 +115,10 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
     GemvPlan p;
     p.splits = env_int("EXL3_GEMV_SPLITS", 0);
     const int blocks = in / 128;
-    if (p.splits <= 0 || blocks % p.splits != 0 || in / p.splits > 2048) p.splits = gemv_default_splits(in, out, rows, groups);
+    // Up to two tile batches per wave (four from 8 rows): later batches' loads overlap the decode, and fewer splits
+    // mean fewer fold arrivals.
+    if (p.splits <= 0 || blocks % p.splits != 0 || in / p.splits > 2048)
+        p.splits = gemv_default_splits(in, out, rows, groups, rows >= 8 ? 4 : 2);
     p.counters_bytes = kZeroBytes;
     p.partial_bytes = p.splits > 1 ? align_up((size_t)groups * p.splits * rows * out * sizeof(float)) : 0;
     return p;

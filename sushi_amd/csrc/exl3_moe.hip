@@ -26,17 +26,19 @@ int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int ma
     // large (each workgroup then pays its start-up latency once for more work, the later batches' loads overlapping
     // the decode).  Past that, more splits only add partial traffic unless the grid is still short of one workgroup
     // per CU.
+    // With 8 or more rows a workgroup carries enough work per tile that half the workgroup target fills the chip, and
+    // every split it saves is one fewer fold arrival per output.
     const int blocks = in / 128;
     const int it = in / 16;
     const long G = (long)(out / 128) * groups_times_proj;
+    const long target = rows >= 8 ? GEMV_TARGET_WGS / 2 : GEMV_TARGET_WGS;
     int best = blocks;
     for (int s = 1; s <= blocks; s++) {
         if (blocks % s) continue;
         if (it / s > TPW * GEMV_WAVES * max_batches) continue;
         best = s;
-        if (G * s >= GEMV_TARGET_WGS) break;
+        if (G * s >= target) break;
     }
-    (void)rows;
     return best;
 }
 
