@@ -238,8 +238,10 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
     // (the most splits), so the planes fit whatever the routing turns out to be.
     const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS : nslots;
     const int rows = windowed ? MOE_WINDOW_ROWS : 1;
-    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 2);  // up to two tile batches per wave
-    p.s2 = gemv_default_splits(inter, hidden, rows, groups);
+    // Up to four tile batches per wave: the grids are large, so each workgroup's start-up latency is paid once for
+    // more work (later batches' loads overlap the decode), and fewer splits mean fewer partials and fold arrivals.
+    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 4);
+    p.s2 = gemv_default_splits(inter, hidden, rows, groups, 4);
     p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
     p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));
     p.table_bytes = windowed ? align_up(sizeof(uint32_t)) + 2 * align_up((size_t)nslots * sizeof(uint32_t)) +
