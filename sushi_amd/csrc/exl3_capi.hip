@@ -115,10 +115,10 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
     GemvPlan p;
     p.splits = env_int("EXL3_GEMV_SPLITS", 0);
     const int blocks = in / 128;
-    // Up to two tile batches per wave (four from 8 rows): later batches' loads overlap the decode, and fewer splits
-    // mean fewer fold arrivals.
+    // Up to four tile batches of TPW tiles per wave (eight from 8 rows): later batches' loads overlap the decode, and
+    // fewer splits mean fewer fold arrivals.
     if (p.splits <= 0 || blocks % p.splits != 0 || in / p.splits > 2048)
-        p.splits = gemv_default_splits(in, out, rows, groups, rows >= 8 ? 4 : 2);
+        p.splits = gemv_default_splits(in, out, rows, groups, rows >= 8 ? 8 : 4);
     p.counters_bytes = kZeroBytes;
     p.partial_bytes = p.splits > 1 ? align_up((size_t)groups * p.splits * rows * out * sizeof(float)) : 0;
     return p;
@@ -238,10 +238,11 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
     // (the most splits), so the planes fit whatever the routing turns out to be.
     const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS : nslots;
     const int rows = windowed ? MOE_WINDOW_ROWS : 1;
-    // Up to four tile batches per wave: the grids are large, so each workgroup's start-up latency is paid once for
-    // more work (later batches' loads overlap the decode), and fewer splits mean fewer partials and fold arrivals.
-    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 4);
-    p.s2 = gemv_default_splits(inter, hidden, rows, groups, 4);
+    // Up to eight tile batches of TPW tiles per wave: the grids are large, so each workgroup's start-up latency is
+    // paid once for more work (later batches' loads overlap the decode), and fewer splits mean fewer partials and
+    // fold arrivals.
+    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 8);
+    p.s2 = gemv_default_splits(inter, hidden, rows, groups, 8);
     p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
     p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));
     p.table_bytes = windowed ? align_up(sizeof(uint32_t)) + 2 * align_up((size_t)nslots * sizeof(uint32_t)) +

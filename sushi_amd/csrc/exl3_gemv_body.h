@@ -365,7 +365,9 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
             float v = fold_value(o + t, a.fold_arrivals);
             if (a.fold_shared) v = round_y(a.y_dtype, v) + load_y(a.fold_shared, a.y_dtype, i);
             store_y(a.y, a.y_dtype, i, v);
-            __hip_atomic_store(h ? w1 : w0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // No split of this launch touches the word again, and the next launch reads it after the kernel boundary:
+            // a plain store suffices (a device-scope store would be written through and hold up the kernel's end).
+            *(h ? w1 : w0) = 0ull;
         }
     }
 }
@@ -532,7 +534,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
             finish_block(a, c, r, v0, v1, lane);
         }
     }
-    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) *ctr = 0u;  // every split has arrived: the next launch reads it after the kernel boundary
 }
 
 // Per-rate decode constants for a ragged bank (hash rows and pair rows differ by rate; the window mask does not).

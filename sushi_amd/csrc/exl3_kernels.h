@@ -24,10 +24,12 @@ constexpr int FOLD_BAD_SHIFT = 52;
 constexpr int FOLD_FRAC = 24;
 constexpr long long FOLD_BIAS = 1LL << 45;
 
-// GEMV workgroup shape: GEMV_WAVES waves, each loading up to TPW k-tiles of the output group before its prologue.
+// GEMV workgroup shape: GEMV_WAVES waves, each loading up to TPW k-tiles of the output group before its prologue
+// and refilling each slot as it is decoded.  Two slots rather than four: with fewer requests in flight at the start,
+// the first tiles (and the input of the prologue) come back sooner, and two waves per SIMD keep the VALU busy.
 // One workgroup per CU (256 CUs) is the target grid.
 constexpr int GEMV_WAVES = 8;
-constexpr int TPW = 4;
+constexpr int TPW = 2;
 constexpr int GEMV_TARGET_WGS = 256;
 
 // Trellis GEMV over `groups` independent (bank, x-block) pairs, 1..8 rows each.
