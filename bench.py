@@ -112,14 +112,12 @@ def bench_moe(batch: int, layers: int = 16, replays: int = 8):
     for layer in range(layers):
         logits = synth.normal(3, f"c4.logits{batch}.{layer}", (batch, E), dtype=torch.float32).to(dev)
         routes.append(exl3.moe_routing_chain(logits, k))
-    sh_inds = torch.zeros(batch, 1, dtype=torch.int32, device=dev)
-    sh_sc = torch.ones(batch, 1, dtype=torch.float32, device=dev)
-
     def chain():
+        # routed experts + the shared expert in one call: up to 16 rows both run in the same two launches; wider
+        # batches the library declines and the wrapper runs the shared expert as a one-expert chain first
         x = x0
         for inds, scores in routes:
-            s = exl3.moe(x, shared, sh_inds, sh_sc, exl3.MCG)  # the shared expert: a one-expert chain
-            x = exl3.moe_with_shared(x, bank, inds, scores, exl3.MCG, False, s)
+            x = exl3.moe_with_shared_bank(x, bank, shared, inds, scores, exl3.MCG)
         return x
 
     chain()

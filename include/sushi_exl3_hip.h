@@ -170,6 +170,28 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
                         exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
                         void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* A routed layer and its shared expert in one call.  Replaces the caller's pair of calls: the shared expert as a
+ * one-expert chain (inds 0, score 1; the pattern of src/dsv41/dsv41_model.zig:3000) and then `moeWithShared`
+ * (src/exl3/root.zig:56-67) with that output.  The shared bank's rows run inside the routed launches (two launches
+ * in all instead of four) and y = T(T(routed) + T(shared)), the rounding of the pair of calls (their k splits may
+ * differ, so the f32 partial sums may round differently; both meet the same parity bar).  shared_bank is a
+ * one-expert bank (trellis [1][hidden/16][inter/16][n] for gate/up, [1][inter/16][hidden/16][n] for down) with the
+ * routed layer's inter; clamp_limit applies to both.  Returns EXL3_DECLINED (nothing launched) where the fused form
+ * does not serve: rows > 16, y dtype f32, a shared rate other than the routed one (uniform banks), or more fold
+ * arrivals than the fused finish holds; the caller then makes the two calls.  The _ragged form takes
+ * `moeRagged`'s rate-grouped bank (src/exl3/root.zig:582-644); its shared bank keeps its own rate. */
+size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
+int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                  int32_t experts, const exl3_bank_t *bank, const exl3_bank_t *shared_bank,
+                                  const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
+                                  int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
+int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                         const exl3_ragged_t *bank, const exl3_bank_t *shared_bank,
+                                         const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
+                                         int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
+                                         size_t workspace_bytes, hipStream_t stream);
+
 /* Router chain `moeRoutingChainOn` (src/moe_router.zig:22-62): top-k over f32 logits [rows][experts]
  * (ties to the lower expert index, listed in descending logit order), softmax over all experts, gathered and
  * renormalised over the k picked.  experts <= 1024, k <= 32. */

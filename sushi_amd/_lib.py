@@ -23,6 +23,9 @@ EXPORTS = (
     "exl3_moe_workspace_size",
     "exl3_moe",
     "exl3_moe_ragged",
+    "exl3_moe_with_shared_bank_workspace_size",
+    "exl3_moe_with_shared_bank",
+    "exl3_moe_ragged_with_shared_bank",
     "exl3_route_topk",
     "exl3_tile_major",
 )
@@ -75,6 +78,13 @@ def load() -> ctypes.CDLL:
                            vp, i32, vp, sz, vp]
     L.exl3_moe_ragged.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(RaggedT), vp, vp, i32, DecodeT, i32, vp,
                                   vp, i32, vp, sz, vp]
+    L.exl3_moe_with_shared_bank_workspace_size.restype = sz
+    L.exl3_moe_with_shared_bank_workspace_size.argtypes = [i32, i32, i32, i32]
+    L.exl3_moe_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(BankT), ctypes.POINTER(BankT),
+                                            vp, vp, i32, DecodeT, i32, vp, i32, vp, sz, vp]
+    L.exl3_moe_ragged_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(RaggedT),
+                                                   ctypes.POINTER(BankT), vp, vp, i32, DecodeT, i32, vp, i32, vp, sz,
+                                                   vp]
     L.exl3_route_topk.argtypes = [vp, i32, i32, i32, vp, vp, vp]
     L.exl3_tile_major.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp]
     for name in EXPORTS:

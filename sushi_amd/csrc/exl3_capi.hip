@@ -273,14 +273,35 @@ int32_t moe_common_checks(int32_t x_dtype, int32_t y_dtype, int32_t rows, int32_
     return ok();
 }
 
+// A one-expert shared bank run inside the routed launches (exl3_moe_with_shared_bank): its rows are appended to the
+// per-slot groups.
+struct SharedBank {
+    const uint16_t *tr[3], *su[3], *sv[3];
+    int n;
+};
+
+// The shared bank's rows need the per-slot arm, a 16-bit output dtype (the combine word holds both rounded sums),
+// the routed and shared folds (routed, shared and combine words: three per output), and, for a uniform bank, the
+// routed rate.
+bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype) {
+    const int nslots = rows * topk;
+    if (rows > kMoeDecodeRowsMax || y_dtype == EXL3_DT_F32) return false;
+    const MoePlan p = plan_moe(nslots + rows, hidden, inter, false);
+    return topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)3 * rows * hidden <= kFoldWords;
+}
+
 int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t x_dtype, int32_t rows,
                    int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
                    const uint16_t *const su[3], const uint16_t *const sv[3], int n_uniform, const uint32_t *meta,
                    int meta_lane_only, const uint32_t *inds, const float *scores, int32_t topk, int32_t clamp_limit, const void *shared,
-                   void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+                   void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream,
+                   const SharedBank *sb = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    MoePlan p = plan_moe(nslots, hidden, inter, moe_windows_enabled() && moe_windowed(rows, nslots, experts));
+    // With a fused shared bank its rows are groups nslots .. nslots + rows - 1 of the per-slot arm.
+    const int ngroups = sb ? nslots + rows : nslots;
+    MoePlan p = sb ? plan_moe(ngroups, hidden, inter, false)
+                   : plan_moe(nslots, hidden, inter, moe_windows_enabled() && moe_windowed(rows, nslots, experts));
     const size_t need = p.total();
     if (ws_bytes < need || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
         return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
@@ -291,7 +312,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     const float scale = out_scale_of(fam);
     // 0) sorted arm: group the slots into expert windows
     uint32_t *win_count = nullptr, *win_expert = nullptr, *win_rows = nullptr, *win_slots = nullptr;
-    int groups = nslots, grows = 1;
+    int groups = ngroups, grows = 1;
     if (p.windowed) {
         char *t = w + 2 * p.gu_bytes + p.down_bytes;
         win_count = reinterpret_cast<uint32_t *>(t);
@@ -340,6 +361,15 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     a.nproj = 2;
     a.fused_finish = 0;
     a.partial_only = 1;
+    if (sb) {
+        a.sh_from = nslots;
+        a.sh_n = sb->n;
+        for (int i = 0; i < 2; i++) {
+            a.sh_trellis[i] = sb->tr[i];
+            a.sh_suh[i] = sb->su[i];
+            a.sh_svh[i] = sb->sv[i];
+        }
+    }
     hipError_t e = run_gemv(fam, PRO_X, a, stream);
     if (e != hipSuccess) return launched(e, "exl3_moe (gate/up)");
 
@@ -382,8 +412,8 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     // The down projection folds straight into y (score-weighted, exact fixed point, shared expert added by the
     // completing arrival) when every token's topk * splits arrivals fit the count field and its rows fit the zeroed
     // region; the planes + reduce launch otherwise.
-    const bool fold = topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)rows * hidden <= kFoldWords &&
-                      env_int("EXL3_MOE_FOLD", 1) != 0;
+    const bool fold = sb || (topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)rows * hidden <= kFoldWords &&
+                             env_int("EXL3_MOE_FOLD", 1) != 0);
     if (fold) {
         d.partial_only = 0;
         d.fused_finish = 1;
@@ -394,6 +424,18 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         d.fold_shared = shared;
         d.y = y;
         d.y_dtype = y_dtype;
+    }
+    if (sb) {  // moe_shared_fusable checked that the three word sets fit the zeroed region
+        d.sh_from = nslots;
+        d.sh_n = sb->n;
+        d.sh_trellis[0] = sb->tr[2];
+        d.sh_suh[0] = sb->su[2];
+        d.sh_svh[0] = sb->sv[2];
+        d.sh_mid_svh[0] = sb->sv[0];
+        d.sh_mid_svh[1] = sb->sv[1];
+        d.sh_fold = d.fold + (size_t)rows * hidden;
+        d.fold_comb = d.fold + (size_t)2 * rows * hidden;
+        d.fold_shared = nullptr;
     }
     e = run_gemv(fam, PRO_MID, d, stream);
     if (e != hipSuccess) return launched(e, "exl3_moe (down)");
@@ -415,6 +457,36 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     r.y_dtype = y_dtype;
     r.out_scale = 1.0f;
     return launched(run_moe_reduce(r, stream), "exl3_moe (reduce)");
+}
+
+int32_t declined(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int32_t declined(const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return EXL3_DECLINED;
+}
+
+bool lane_rate(int n) { return n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64; }
+
+// A bank whose three projections share one admitted rate, as a SharedBank (expert 0 of it serves).
+int32_t shared_bank_checks(const exl3_bank_t *b, const char *what, SharedBank *out) {
+    if (!b) return fail(EXL3_ERR_BAD_SHAPE, "%s: no bank", what);
+    const exl3_proj_t *pr[3] = {&b->gate, &b->up, &b->down};
+    for (int i = 0; i < 3; i++) {
+        if (!rate_admitted(pr[i]->n) || !pr[i]->trellis || !pr[i]->suh || !pr[i]->svh)
+            return fail(EXL3_ERR_BAD_SHAPE, "%s: projection %d has n=%d or a null operand", what, i, pr[i]->n);
+        out->tr[i] = pr[i]->trellis;
+        out->su[i] = pr[i]->suh;
+        out->sv[i] = pr[i]->svh;
+    }
+    if (b->gate.n != b->up.n || b->gate.n != b->down.n)
+        return fail(EXL3_ERR_BAD_SHAPE, "%s: gate/up/down rates differ", what);
+    out->n = b->gate.n;
+    return ok();
 }
 
 }  // namespace
@@ -540,6 +612,80 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
     return moe_launch(fam, k, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
                       bank->svh, 0, bank->meta, bank->lane_rates_only != 0, inds, scores, topk, clamp_limit, shared,
                       y, y_dtype, workspace, workspace_bytes, stream);
+}
+
+size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
+    const size_t routed = exl3_moe_workspace_size(rows, topk, hidden, inter);
+    if (routed == 0) return 0;
+    return std::max(routed, plan_moe(rows * topk + rows, hidden, inter, false).total());
+}
+
+int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                  int32_t experts, const exl3_bank_t *bank, const exl3_bank_t *shared_bank,
+                                  const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
+                                  int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+    if (rc) return rc;
+    if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: no bank");
+    SharedBank sb;
+    rc = shared_bank_checks(bank, "moe_with_shared_bank (routed)", &sb);
+    if (rc) return rc;
+    const int routed_n = sb.n;
+    rc = shared_bank_checks(shared_bank, "moe_with_shared_bank (shared)", &sb);
+    if (rc) return rc;
+    int fam;
+    DecodeK k;
+    rc = resolve_decode(dec, routed_n, &fam, &k);
+    if (rc) return rc;
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: null operand");
+    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype))
+        return declined("moe_with_shared_bank: declined (rows=%d, y dtype %d, rates %d/%d): run the shared expert as "
+                        "a one-expert exl3_moe and pass it to exl3_moe as `shared`", rows, y_dtype, routed_n, sb.n);
+    const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
+    const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
+    const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
+    return moe_launch(fam, k, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, routed_n, nullptr, 0,
+                      inds, scores, topk, clamp_limit, nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb);
+}
+
+int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                         const exl3_ragged_t *bank, const exl3_bank_t *shared_bank,
+                                         const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
+                                         int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+    if (rc) return rc;
+    if (!bank || bank->experts <= 0 || !bank->meta)
+        return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: no bank");
+    for (int i = 0; i < 3; i++)
+        if (!bank->trellis[i] || !bank->suh[i] || !bank->svh[i])
+            return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: projection %d has a null operand", i);
+    SharedBank sb;
+    rc = shared_bank_checks(shared_bank, "moe_ragged_with_shared_bank (shared)", &sb);
+    if (rc) return rc;
+    int fam;
+    DecodeK k;
+    rc = resolve_decode(dec, 0, &fam, &k, /*per_rate_table=*/true);
+    if (rc) return rc;
+    const int table = fam == FAM_PAIR ? (int)TABLE_PAIR1_W16_V1 : dec.table;
+    // the shared bank decodes with the routed codebook at its own rate: its table must have that rate
+    if ((fam == FAM_HASH || fam == FAM_PAIR)) {
+        uint32_t m0, m1, m2, m3;
+        if (!table_row(table, sb.n, m0, m1, m2, m3))
+            return fail(EXL3_ERR_RATE_MISSING, "moe_ragged_with_shared_bank: table %d has no row for n=%d", table,
+                        sb.n);
+    }
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: null operand");
+    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype))
+        return declined("moe_ragged_with_shared_bank: declined (rows=%d, y dtype %d): run the shared expert as a "
+                        "one-expert exl3_moe and pass it to exl3_moe_ragged as `shared`", rows, y_dtype);
+    const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);
+    return moe_launch(fam, k, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
+                      bank->svh, 0, bank->meta, lane_only, inds, scores, topk, clamp_limit, nullptr, y, y_dtype,
+                      workspace, workspace_bytes, stream, &sb);
 }
 
 int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds, float *scores,

@@ -74,6 +74,16 @@ __device__ __forceinline__ float round_y(int dt, float v) {
     return v;
 }
 
+// v rounded to y's 16-bit dtype (f16 or bf16), as its bit pattern, and back.
+__device__ __forceinline__ uint32_t y_bits16(int dt, float v) {
+    if (dt == DT_F16) return __half_as_ushort(__float2half_rn(v));
+    return __bfloat16_as_ushort(__float2bfloat16(v));
+}
+__device__ __forceinline__ float y_from_bits16(int dt, uint32_t b) {
+    if (dt == DT_F16) return __half2float(__ushort_as_half((unsigned short)b));
+    return __uint_as_float(b << 16);
+}
+
 __device__ __forceinline__ float silu(float g) {
     // g * sigmoid(g), evaluated on exp(-|g|) so neither branch overflows (the reference's mid uses the same split)
     const float e = __expf(-fabsf(g));
@@ -84,6 +94,8 @@ __device__ __forceinline__ float silu(float g) {
 struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div, x_dtype;
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
+    int xg;                     // the input rows' block: x rows xg * rows .. (per-slot and dense arms)
+    bool shared;                // a shared expert's row fused into the routed launch
     const uint32_t *wslots;     // the window's slots, or null (group = slot, or plain rows)
     const void *x;
     const uint16_t *suh, *svh;  // this projection's banks (selected once: an indexed kernel-argument read would be
@@ -105,7 +117,7 @@ __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c
 template <bool WIN>
 __device__ __forceinline__ size_t x_row(const GemvArgs &a, const GemvCtx &c, int r) {
     if constexpr (WIN) return (size_t)(c.wslots[r] / c.x_div);
-    else return (size_t)(c.g / c.x_div) * c.rows + r;
+    else return (size_t)c.xg * c.rows + r;
 }
 template <bool WIN>
 __device__ __forceinline__ size_t part_row(const GemvArgs &a, const GemvCtx &c, int r) {
@@ -271,8 +283,9 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                 for (int pj = 0; pj < 2; pj++) {
                     float w0 = w[pj][0], w1 = w[pj][1];
                     fwht128_wave(w0, w1, lane);
-                    w0 *= HAD_SCALE * h2f(a.mid_svh[pj][si + lane]);
-                    w1 *= HAD_SCALE * h2f(a.mid_svh[pj][si + lane + 64]);
+                    const uint16_t *msv = c.shared ? a.sh_mid_svh[pj] : a.mid_svh[pj];
+                    w0 *= HAD_SCALE * h2f(msv[si + lane]);
+                    w1 *= HAD_SCALE * h2f(msv[si + lane + 64]);
                     if (pj == 0) {
                         gv[0] = w0;
                         gv[1] = w1;
@@ -326,11 +339,12 @@ __device__ __forceinline__ float fold_value(unsigned long long t, int S) {
 // finishes rows w, w + GEMV_WAVES, ...
 // The MoE down projection folds the same way across slots: slot s adds its score-weighted output into row
 // s / topk (the score-weighted reduce of REDUCE_SOURCE / REDUCE_SHARED_SOURCE, expert_exl3_kernels.zig:2338-2406),
-// and the completing arrival rounds the routed sum to y's dtype before adding the shared expert.
-template <int RT, bool WIN>
+// and the completing arrival rounds the routed sum to y's dtype before adding the shared expert.  MOE (the down
+// projection's PRO_MID kernels) is a compile-time choice: the dense kernels carry none of the slot, score and
+// shared-expert handling.
+template <int RT, bool WIN, bool MOE>
 __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c, float (*red)[RT][128], int wave,
                                             int lane) {
-    const bool moe = a.fold_topk > 0;
     for (int r = wave; r < c.rows; r += GEMV_WAVES) {
         float v0 = 0.f, v1 = 0.f;
 #pragma unroll
@@ -343,28 +357,56 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
         fwht128_wave(v0, v1, lane);
         size_t yrow;
         float sc = 1.0f;
-        if (moe) {
+        bool shared = false;
+        if constexpr (MOE) {
             const int slot = slot_of<WIN>(c, r);
-            yrow = (size_t)(slot / a.fold_topk);
-            sc = a.fold_scores[slot];
+            shared = c.shared;
+            if (shared) {  // the shared expert's own row, score 1, into its own words
+                yrow = (size_t)(slot - a.sh_from);
+            } else {
+                yrow = (size_t)(slot / a.fold_topk);
+                sc = a.fold_scores[slot];
+            }
         } else {
             yrow = (size_t)c.g * a.rows + r;
         }
+        const int arrivals = shared ? c.S : a.fold_arrivals;
         const unsigned long long t0 = fold_term((v0 * HAD_SCALE * c.sv0) * sc);
         const unsigned long long t1 = fold_term((v1 * HAD_SCALE * c.sv1) * sc);
         const size_t yo = yrow * a.out + (size_t)c.og * 128;
-        unsigned long long *w0 = a.fold + yo + lane, *w1 = w0 + 64;
+        unsigned long long *w0 = (shared ? a.sh_fold : a.fold) + yo + lane, *w1 = w0 + 64;
         const unsigned long long o0 = __hip_atomic_fetch_add(w0, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long o1 = __hip_atomic_fetch_add(w1, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long last = (unsigned long long)(a.fold_arrivals - 1);
+        // Both adds go out before either result is examined: one memory round trip for the pair, not two.
+        __builtin_amdgcn_sched_barrier(0);
+        const unsigned long long last = (unsigned long long)(arrivals - 1);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const unsigned long long o = h ? o1 : o0, t = h ? t1 : t0;
             if ((o >> FOLD_COUNT_SHIFT) != last) continue;
             const size_t i = yo + lane + 64 * h;
-            float v = fold_value(o + t, a.fold_arrivals);
-            if (a.fold_shared) v = round_y(a.y_dtype, v) + load_y(a.fold_shared, a.y_dtype, i);
-            store_y(a.y, a.y_dtype, i, v);
+            float v = fold_value(o + t, arrivals);
+            if (!MOE) {
+                store_y(a.y, a.y_dtype, i, v);
+            } else if (a.fold_comb) {
+                // The routed sum and the shared expert's, each rounded to y's 16-bit dtype, meet in one word: each
+                // adds its bit pattern into its own half-word with a flag; whichever arrives second holds both and
+                // stores T(T(routed) + T(shared)), the rounding moeWithShared keeps (REDUCE_SHARED_SOURCE,
+                // expert_exl3_kernels.zig:2391-2406).
+                const uint32_t b = y_bits16(a.y_dtype, v);
+                const unsigned long long term = shared ? (1ull << 62) | b : (1ull << 63) | ((unsigned long long)b << 16);
+                unsigned long long *cw = a.fold_comb + i;
+                const unsigned long long old = __hip_atomic_fetch_add(cw, term, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (old != 0) {
+                    const uint32_t rb = shared ? (uint32_t)(old >> 16) & 0xFFFFu : b;
+                    const uint32_t hb = shared ? b : (uint32_t)old & 0xFFFFu;
+                    store_y(a.y, a.y_dtype, i, y_from_bits16(a.y_dtype, rb) + y_from_bits16(a.y_dtype, hb));
+                    *cw = 0ull;
+                }
+            } else {
+                if (a.fold_shared) v = round_y(a.y_dtype, v) + load_y(a.fold_shared, a.y_dtype, i);
+                store_y(a.y, a.y_dtype, i, v);
+            }
             // No split of this launch touches the word again, and the next launch reads it after the kernel boundary:
             // a plain store suffices (a device-scope store would be written through and hold up the kernel's end).
             *(h ? w1 : w0) = 0ull;
@@ -469,7 +511,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
     }
     __syncthreads();
     if (a.fold) {  // the host enables the fold only for split dense launches and the MoE down projection
-        fold_finish<RT, WIN>(a, c, red, wave, lane);
+        fold_finish<RT, WIN, PRO == PRO_MID>(a, c, red, wave, lane);
         return;
     }
     const bool direct = c.S == 1 && !a.partial_only;
@@ -551,10 +593,12 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
 template <int FAM, int N, int RT, int PRO, bool WIN>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
                                                             const uint32_t *bank_of, int in, int out, int splits,
-                                                            int rows, int x_dtype, int x_div, GemvArgs a) {
+                                                            int rows_dt, int x_div, int sh_from, GemvArgs a) {
     // The leading scalar arguments are the ones the first loads need (the input and suh of the prologue, the tile
-    // words): the build preloads them into SGPRs, so those loads issue without waiting for an argument load.  The
-    // struct `a` holds everything (the same values included) for the rest of the kernel.
+    // words, and whether this group is a fused shared expert's): the build preloads them into SGPRs (14 dwords,
+    // rows and x's dtype sharing one), so those loads issue without waiting for an argument load.  The struct `a`
+    // holds everything (the same values included) for the rest of the kernel.
+    const int rows = rows_dt & 0xFFFF, x_dtype = rows_dt >> 16;
     GemvCtx c;
     c.x = x;
     c.x_div = x_div;
@@ -575,16 +619,28 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
     c.suh = p1 ? a.suh[1] : suh0;
     c.svh = p1 ? a.svh[1] : a.svh[0];
     c.part = p1 ? a.partial[1] : a.partial[0];
-    const uint16_t *trellis = p1 ? a.trellis[1] : tr0;
+    const uint16_t *trellis = p1 ? a.trellis[1] : tr0;  // (the shared expert's rows switch it below)
     c.rows = rows;
     c.wslots = nullptr;
+    c.shared = false;
+    c.xg = 0;
     if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
         if ((uint32_t)c.g >= *a.win_count) return;
         c.bank = (int)min(a.win_expert[c.g], (uint32_t)(a.bank_limit - 1));
         c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
         c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
     } else {
-        c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
+        c.xg = c.g / x_div;
+        if (sh_from > 0 && c.g >= sh_from) {  // a shared expert's token row, fused into this launch
+            c.shared = true;
+            c.bank = 0;
+            c.xg = c.g - a.sh_from;
+            c.suh = a.sh_suh[c.proj];
+            c.svh = a.sh_svh[c.proj];
+            trellis = a.sh_trellis[c.proj];
+        } else {
+            c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
+        }
     }
     c.KS = c.IT / c.S;
     c.kt0 = c.sp * c.KS;
@@ -603,8 +659,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
         // (kept out of the first kernel, whose registers it would otherwise set).
         const int col = p1 ? a.meta_col[1] : a.meta_col[0];
         const uint32_t *m = a.meta + (size_t)c.bank * 8;
-        const int n = (int)m[col];
-        const uint16_t *tb = trellis + 2 * (size_t)m[4 + col];
+        const int n = c.shared ? a.sh_n : (int)m[col];
+        const uint16_t *tb = c.shared ? trellis : trellis + 2 * (size_t)m[4 + col];
         const DecodeK k = rate_constants<FAM>(a, n);
         const bool lane_rate = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
         if constexpr (N == -1) {
@@ -648,7 +704,7 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
 template <int FAM, int N, int RT, int PRO, bool WIN>
 static void launch_one(const GemvArgs &a, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((gemv_kernel<FAM, N, RT, PRO, WIN>), grid, dim3(GEMV_THREADS), 0, s, a.x, a.trellis[0], a.suh[0],
-                       a.bank_of, a.in, a.out, a.splits, a.rows, a.x_dtype, a.x_div, a);
+                       a.bank_of, a.in, a.out, a.splits, a.rows | (a.x_dtype << 16), a.x_div, a.sh_from, a);
 }
 
 template <int FAM, int N, int PRO>

@@ -70,6 +70,10 @@ struct GemvArgs {
     int fold_topk;            // > 0: MoE down -- slot s folds into output row s / fold_topk, scaled by fold_scores[s]
     const float *fold_scores;
     const void *fold_shared;  // MoE: [rows][out] in y's dtype, added after the routed sum's rounding; null = none
+    // A fused shared expert's own fold words [rows][out] and the words where the rounded routed and shared sums
+    // meet (see sh_from below); beside the fold's other fields, which the finish reads together.
+    unsigned long long *sh_fold;
+    unsigned long long *fold_comb;
     void *y;
     int y_dtype;
     int splits;
@@ -83,6 +87,17 @@ struct GemvArgs {
     const uint32_t *win_expert;
     const uint32_t *win_rows;
     const uint32_t *win_slots;
+    // A shared expert fused into the routed launches (per-slot arm): groups from sh_from on are the shared expert's
+    // token rows (row = group - sh_from), decoded from the one-expert bank sh_* at rate sh_n with score 1.  The
+    // down projection folds them into their own words (sh_fold); the rounded routed and shared sums then meet in
+    // fold_comb, whose second arrival stores T(T(routed) + T(shared)).  sh_from = 0: no shared expert (the kernel
+    // takes it as a preloaded leading argument).
+    int sh_from;
+    int sh_n;
+    const uint16_t *sh_trellis[2];
+    const uint16_t *sh_suh[2];
+    const uint16_t *sh_svh[2];
+    const uint16_t *sh_mid_svh[2];  // PRO_MID: the shared expert's gate / up svh
 };
 
 // Rows per expert window in the sorted MoE arm.

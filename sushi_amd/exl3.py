@@ -462,11 +462,8 @@ def _moe_prep(x: torch.Tensor, inds: torch.Tensor, scores: torch.Tensor):
     return x2, inds2, sc2, rows, topk
 
 
-def _moe(x: torch.Tensor, bank: Bank, inds: torch.Tensor, scores: torch.Tensor, dec: Decode, verify_rows: bool,
-         shared: Optional[torch.Tensor], limit: int) -> torch.Tensor:
-    dec.require_table()
-    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
-    hidden = int(x.shape[-1])
+def _bank_shape(bank: Bank, hidden: int):
+    """(experts, inter) of a bank over hidden features (validateClampedProjection, root.zig:126-135)."""
     g, u, d = bank.gate, bank.up, bank.down
     experts = g.experts
     inter = g.out_features
@@ -477,6 +474,16 @@ def _moe(x: torch.Tensor, bank: Bank, inds: torch.Tensor, scores: torch.Tensor, 
         _f16_check(p.suh, "suh")
         _f16_check(p.svh, "svh")
         _need_gpu(p.trellis, p.suh, p.svh)
+    return experts, inter
+
+
+def _moe(x: torch.Tensor, bank: Bank, inds: torch.Tensor, scores: torch.Tensor, dec: Decode, verify_rows: bool,
+         shared: Optional[torch.Tensor], limit: int) -> torch.Tensor:
+    dec.require_table()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    g, u, d = bank.gate, bank.up, bank.down
+    experts, inter = _bank_shape(bank, hidden)
     _need_gpu(x2, inds2, sc2, shared)
     y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
     if shared is not None:
@@ -528,6 +535,75 @@ def moe_ragged(x, rb: Ragged, inds, scores, dec: Decode, verify_rows: bool = Fal
     _check(L.exl3_moe_ragged(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr), inds2.data_ptr(),
                              sc2.data_ptr(), topk, dec.c(), int(limit), None if shared is None else shared.data_ptr(),
                              y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device)))
+    return y.reshape(x.shape)
+
+
+EXL3_DECLINED = 1
+
+
+def _shared_rows(x: torch.Tensor, shared_bank: Bank, dec: Decode, limit: int) -> torch.Tensor:
+    """The shared expert as a one-expert chain (inds 0, score 1), the reference callers' pattern
+    (src/dsv41/dsv41_model.zig:3000)."""
+    lead = tuple(x.shape[:-1])
+    z = torch.zeros(*lead, 1, dtype=torch.int32, device=x.device)
+    o = torch.ones(*lead, 1, dtype=torch.float32, device=x.device)
+    return _moe(x, shared_bank, z, o, dec, False, None, limit)
+
+
+def moe_with_shared_bank(x, bank: Bank, shared_bank: Bank, inds, scores, dec: Decode, limit: int = 0) -> torch.Tensor:
+    """The routed layer and its shared expert in one call: T(T(routed) + T(shared)), the rounding of the reference
+    callers' pair of calls (the shared expert as a one-expert chain, then `moeWithShared`, root.zig:56-67).  Where
+    the fused form declines (rows > 16, f32 output, a shared rate other than the routed one) it makes those two
+    calls itself.  ``limit`` > 0 clamps both as `moeClamped` does (root.zig:98-124)."""
+    if limit < 0 or limit > 128:
+        raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128 (0 = none)")
+    dec.require_table()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    experts, inter = _bank_shape(bank, hidden)
+    if _bank_shape(shared_bank, hidden) != (1, inter):
+        raise BadExl3Shape("moe_with_shared_bank: the shared bank must be one expert of the routed inter")
+    _need_gpu(x2, inds2, sc2)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_with_shared_bank_workspace_size(rows, topk, hidden, inter))
+    cb = _lib.BankT(bank.gate.c(), bank.up.c(), bank.down.c())
+    cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
+    rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, experts, ctypes.byref(cb),
+                                     ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), topk, dec.c(), int(limit),
+                                     y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device))
+    if rc == EXL3_DECLINED:
+        return _moe(x, bank, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
+    _check(rc)
+    return y.reshape(x.shape)
+
+
+def moe_ragged_with_shared_bank(x, rb: Ragged, shared_bank: Bank, inds, scores, dec: Decode,
+                                limit: int = 0) -> torch.Tensor:
+    """`moeRagged` (root.zig:582-644) with its shared expert in the same launches (see moe_with_shared_bank); the
+    shared bank decodes with the routed codebook at its own rate."""
+    if limit < 0 or limit > 128:
+        raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128 (0 = none)")
+    dec.require_table()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    if hidden != rb.hidden:
+        raise BadExl3Shape(f"moe_ragged_with_shared_bank: hidden {hidden} vs bank {rb.hidden}")
+    if _bank_shape(shared_bank, hidden) != (1, rb.inter):
+        raise BadExl3Shape("moe_ragged_with_shared_bank: the shared bank must be one expert of the routed inter")
+    _need_gpu(x2, inds2, sc2, rb.meta)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_with_shared_bank_workspace_size(rows, topk, hidden, rb.inter))
+    cr = rb.c()
+    cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
+    rc = L.exl3_moe_ragged_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr),
+                                            ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), topk, dec.c(),
+                                            int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
+                                            _stream(x.device))
+    if rc == EXL3_DECLINED:
+        return moe_ragged(x, rb, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
+    _check(rc)
     return y.reshape(x.shape)
 
 

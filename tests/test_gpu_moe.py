@@ -2,6 +2,8 @@
 
 Reference oracle: moeSwigluHost (src/exl3/expert_exl3_kernels.zig:3059-3114), per row.  Bar: max-abs-rel 2e-3.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -255,3 +257,98 @@ def test_tile_major_matches_oracle(dev):
         assert (got[e].reshape(-1) == O.tile_major(src[e].reshape(-1), 4, 6, 40)).all()
     back = exl3.tile_major(torch.from_numpy(got.view(np.int16)).to(dev), inverse=True).cpu().numpy()
     assert (back.view(np.uint16) == src).all()
+
+
+def _two_calls(x, bd, sd, xi, sc, dec, limit=0):
+    """The reference callers' pair: the shared expert as a one-expert chain, then moeWithShared / moeClamped."""
+    rows = x.shape[0]
+    z = torch.zeros(rows, 1, dtype=torch.int32, device=x.device)
+    o = torch.ones(rows, 1, dtype=torch.float32, device=x.device)
+    if limit:
+        s = exl3.moe_clamped(x, sd, z, o, dec, limit)
+        return exl3.moe_clamped(x, bd, xi, sc, dec, limit, shared=s)
+    s = exl3.moe(x, sd, z, o, dec)
+    return exl3.moe_with_shared(x, bd, xi, sc, dec, False, s)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8, 16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("limit", [0, 4])
+def test_moe_with_shared_bank_is_the_two_calls(dev, rows, dtype, limit):
+    """The fused shared expert (two launches) against the two calls it replaces (four launches), T(T(routed) +
+    T(shared)) in both (their k splits may differ, so the f32 partial sums may round an output to a neighbouring
+    value), and against the oracle (routed + shared expert) at the bar."""
+    print(f"[moe shared bank] rows={rows} dtype={dtype} limit={limit}", flush=True)
+    E, hidden, inter, k, n = 8, 256, 256, 4, 32
+    b = synth.bank(31, "msb", E, hidden, inter, n)
+    s = synth.bank(31, "msb.shared", 1, hidden, inter, n)
+    x = synth.normal(31, f"x{rows}", (rows, hidden)).to(dtype)
+    inds, scores = _route(31 + rows, rows, E, k)
+    bd, sd = _to(b, dev), _to(s, dev)
+    xd = x.to(dev)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    y = exl3.moe_with_shared_bank(xd, bd, sd, xi, sc, exl3.MCG, limit)
+    ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG, limit)
+    assert y.dtype == dtype and y.shape == x.shape
+    bar = BAR if dtype == torch.float16 else 8e-3  # bf16 output rounding alone is 2^-9 relative
+    assert max_abs_rel(y.float().cpu().numpy(), ref.float().cpu().numpy()) < bar
+    odec = O.decode(O.CB_MCG)
+    xf = x.float().numpy()
+    want = _oracle_moe(b, xf, inds, scores, hidden, inter, n, odec, clamp=float(limit))
+    want = want + _oracle_moe(s, xf, np.zeros((rows, 1), np.uint32), np.ones((rows, 1), np.float32), hidden, inter,
+                              n, odec, clamp=float(limit))
+    assert max_abs_rel(y.float().cpu().numpy(), want) < bar
+
+
+@pytest.mark.parametrize("case", ["rows17", "f32", "rates"])
+def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
+    """Where the fused form does not serve, the C ABI declines before any launch and the wrapper makes the two
+    calls; the result is the two calls' own."""
+    E, hidden, inter, k, n = 8, 256, 128, 2, 32
+    rows = 17 if case == "rows17" else 2
+    b = synth.bank(33, "msd", E, hidden, inter, n)
+    s = synth.bank(33, "msd.shared", 1, hidden, inter, 48 if case == "rates" else n)
+    x = synth.normal(33, "x", (rows, hidden)).to(torch.float32 if case == "f32" else torch.float16)
+    inds, scores = _route(33, rows, E, k)
+    bd, sd = _to(b, dev), _to(s, dev)
+    xd = x.to(dev)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    L = exl3._lib.load()
+    cb = exl3._lib.BankT(bd.gate.c(), bd.up.c(), bd.down.c())
+    cs = exl3._lib.BankT(sd.gate.c(), sd.up.c(), sd.down.c())
+    ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
+    y0 = torch.full_like(xd, 7.0)
+    x2 = xd.contiguous()
+    rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), k, exl3.MCG.c(), 0,
+                                     y0.data_ptr(), exl3._dt(y0, "y"), ws.data_ptr(), ws.numel(),
+                                     exl3._stream(dev))
+    torch.cuda.synchronize()
+    assert rc == exl3.EXL3_DECLINED and bool((y0 == 7.0).all())  # nothing launched
+    y = exl3.moe_with_shared_bank(xd, bd, sd, xi, sc, exl3.MCG)
+    ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
+    assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("rows", [1, 5])
+def test_moe_ragged_with_shared_bank_is_the_two_calls(dev, rows):
+    """Rate-grouped routed experts (K1/K2 under SPEC1, lane and generic readers both) with a K4 shared expert in the
+    same launches, against the shared one-expert chain followed by moeRagged with `shared`."""
+    hidden, inter, k = 256, 256, 4
+    dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
+    groups = [(6, (16, 16, 16)), (10, (32, 36, 32))]
+    banks = [synth.bank(40 + g, f"rgs{g}", e, hidden, inter, rates) for g, (e, rates) in enumerate(groups)]
+    rb = exl3.Ragged.init([_to(b, dev) for b in banks])
+    sd = _to(synth.bank(40, "rgs.shared", 1, hidden, inter, 64), dev)
+    E = sum(e for e, _ in groups)
+    x = synth.normal(40, "x", (rows, hidden)).to(dev)
+    inds, scores = _route(40, rows, E, k)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    y = exl3.moe_ragged_with_shared_bank(x, rb, sd, xi, sc, dec)
+    z = torch.zeros(rows, 1, dtype=torch.int32, device=dev)
+    o = torch.ones(rows, 1, dtype=torch.float32, device=dev)
+    ref = exl3.moe_ragged(x, rb, xi, sc, dec, shared=exl3.moe(x, sd, z, o, dec))
+    assert max_abs_rel(y.float().cpu().numpy(), ref.float().cpu().numpy()) < BAR
