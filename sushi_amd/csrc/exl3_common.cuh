@@ -219,6 +219,30 @@ __device__ __forceinline__ void load_lane_words(const uint32_t *__restrict__ wor
     }
 }
 
+// The same words for a tile at `row` (wave-uniform: the group's first tile of a k-tile row) plus the lane's own tile
+// offset `lane_words` (u32 words, per lane).  For the rates whose chunks start on a word (N % 16 == 0), each load is
+// addressed as the uniform base plus a 32-bit byte offset, so it takes the scalar-base form and a tile costs no 64-bit
+// vector address arithmetic; the other rates keep the per-lane pointer, whose contiguous words load as one wide access.
+template <int N>
+__device__ __forceinline__ void load_lane_words_u(const uint32_t *__restrict__ row, uint32_t lane_words, int j,
+                                                  uint32_t (&A)[LaneBits<N>::AW]) {
+    if constexpr (LaneBits<N>::ALIGNED) {
+        constexpr int NW = LaneBits<N>::NW;
+        constexpr int AW = LaneBits<N>::AW;
+        typedef __attribute__((address_space(1))) const uint32_t global_u32;
+        const char *base = reinterpret_cast<const char *>(row);
+        auto at = [&](uint32_t w) __attribute__((always_inline)) {
+            return *(global_u32 *)(base + (uint32_t)((lane_words + w) * 4u));
+        };
+        const int w0 = j * (N / 16);
+        A[0] = at((uint32_t)((w0 + NW - 1) % NW));
+#pragma unroll
+        for (int i = 1; i < AW; i++) A[i] = at((uint32_t)(w0 + i - 1));
+    } else {
+        load_lane_words<N>(row + lane_words, j, A);
+    }
+}
+
 // Codeword u (0..31) of the lane from its aligned words (low 16 bits valid).
 template <int N>
 __device__ __forceinline__ uint32_t lane_codeword(const uint32_t (&A)[LaneBits<N>::AW], int u) {

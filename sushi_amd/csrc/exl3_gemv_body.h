@@ -95,7 +95,6 @@ struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div, x_dtype;
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
     int xg;                     // the input rows' block: x rows xg * rows .. (per-slot and dense arms)
-    bool shared;                // a shared expert's row fused into the routed launch
     const uint32_t *wslots;     // the window's slots, or null (group = slot, or plain rows)
     const void *x;
     const uint16_t *suh, *svh;  // this projection's banks (selected once: an indexed kernel-argument read would be
@@ -255,7 +254,7 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, 
     }
 }
 
-template <int PRO, int RT, bool WIN>
+template <int PRO, int RT, bool WIN, bool SH>
 __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[XS_PITCH], int wave,
                                          int lane, const PrologueRegs<RT, WIN> &pr) {
     const int nblk = c.KS >> 3;
@@ -283,7 +282,7 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                 for (int pj = 0; pj < 2; pj++) {
                     float w0 = w[pj][0], w1 = w[pj][1];
                     fwht128_wave(w0, w1, lane);
-                    const uint16_t *msv = c.shared ? a.sh_mid_svh[pj] : a.mid_svh[pj];
+                    const uint16_t *msv = SH ? a.sh_mid_svh[pj] : a.mid_svh[pj];
                     w0 *= HAD_SCALE * h2f(msv[si + lane]);
                     w1 *= HAD_SCALE * h2f(msv[si + lane + 64]);
                     if (pj == 0) {
@@ -342,7 +341,7 @@ __device__ __forceinline__ float fold_value(unsigned long long t, int S) {
 // and the completing arrival rounds the routed sum to y's dtype before adding the shared expert.  MOE (the down
 // projection's PRO_MID kernels) is a compile-time choice: the dense kernels carry none of the slot, score and
 // shared-expert handling.
-template <int RT, bool WIN, bool MOE>
+template <int RT, bool WIN, bool MOE, bool SH>
 __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c, float (*red)[RT][128], int wave,
                                             int lane) {
     for (int r = wave; r < c.rows; r += GEMV_WAVES) {
@@ -360,7 +359,7 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
         bool shared = false;
         if constexpr (MOE) {
             const int slot = slot_of<WIN>(c, r);
-            shared = c.shared;
+            shared = SH;
             if (shared) {  // the shared expert's own row, score 1, into its own words
                 yrow = (size_t)(slot - a.sh_from);
             } else {
@@ -380,15 +379,27 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
         // Both adds go out before either result is examined: one memory round trip for the pair, not two.
         __builtin_amdgcn_sched_barrier(0);
         const unsigned long long last = (unsigned long long)(arrivals - 1);
+        if constexpr (!MOE) {
+            // Both outcomes are settled before either store, so no store waits on the other output's check.
+            const bool d0 = (o0 >> FOLD_COUNT_SHIFT) == last, d1 = (o1 >> FOLD_COUNT_SHIFT) == last;
+            const float y0 = fold_value(o0 + t0, arrivals), y1 = fold_value(o1 + t1, arrivals);
+            if (d0) {
+                store_y(a.y, a.y_dtype, yo + lane, y0);
+                *w0 = 0ull;  // no split of this launch touches it again; the next launch reads it after the boundary
+            }
+            if (d1) {
+                store_y(a.y, a.y_dtype, yo + lane + 64, y1);
+                *w1 = 0ull;
+            }
+            continue;
+        }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const unsigned long long o = h ? o1 : o0, t = h ? t1 : t0;
             if ((o >> FOLD_COUNT_SHIFT) != last) continue;
             const size_t i = yo + lane + 64 * h;
             float v = fold_value(o + t, arrivals);
-            if (!MOE) {
-                store_y(a.y, a.y_dtype, i, v);
-            } else if (a.fold_comb) {
+            if (a.fold_comb) {
                 // The routed sum and the shared expert's, each rounded to y's 16-bit dtype, meet in one word: each
                 // adds its bit pattern into its own half-word with a flag; whichever arrives second holds both and
                 // stores T(T(routed) + T(shared)), the rounding moeWithShared keeps (REDUCE_SHARED_SOURCE,
@@ -422,7 +433,7 @@ __device__ __forceinline__ void fetch_svh(GemvCtx &c, int lane) {
 }
 
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
-template <int FAM, int N, int RT, int PRO, bool WIN>
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const uint16_t *__restrict__ tb,
                                           int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
     const int tid = threadIdx.x, lane = tid & 63;
@@ -443,14 +454,18 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
         __builtin_amdgcn_sched_barrier(0);  // the input loads stay ahead of the tile loads (vmcnt retires in order)
         uint32_t Aw[TPW][AW];
+        // tile (tk, og * 8 + o): the uniform start of k-tile row tk of the group plus the lane's tile offset
+        const uint32_t lane_words = (uint32_t)(o * N) >> 1;
+        auto row_of = [&](int tk) __attribute__((always_inline)) {
+            return reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8) * N);
+        };
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
             const int tk = c.kt0 + wave + GEMV_WAVES * min(t, ntiles - 1);
-            load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
-                               Aw[t]);
+            load_lane_words_u<N>(row_of(tk), lane_words, j, Aw[t]);
         }
         fetch_svh(c, lane);
-        prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
+        prologue<PRO, RT, WIN, SH>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
         auto decode_at = [&](int t, int tt) __attribute__((always_inline)) {  // slot t holds the wave's tile tt
@@ -467,8 +482,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
             for (int t = 0; t < TPW; t++) {
                 decode_at(t, t0 + t);
                 const int tk = c.kt0 + wave + GEMV_WAVES * min(t0 + TPW + t, ntiles - 1);
-                load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8 + o) * n), j,
-                                   Aw[t]);
+                load_lane_words_u<N>(row_of(tk), lane_words, j, Aw[t]);
             }
         }
 #pragma unroll
@@ -479,7 +493,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         fetch_svh(c, lane);
         PrologueRegs<RT, WIN> pr;
         prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
-        prologue<PRO, RT, WIN>(a, c, xs, wave, lane, pr);
+        prologue<PRO, RT, WIN, SH>(a, c, xs, wave, lane, pr);
         __syncthreads();
         for (int kk = wave; kk < c.KS; kk += GEMV_WAVES) {
             const int tk = c.kt0 + kk;
@@ -511,7 +525,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
     }
     __syncthreads();
     if (a.fold) {  // the host enables the fold only for split dense launches and the MoE down projection
-        fold_finish<RT, WIN, PRO == PRO_MID>(a, c, red, wave, lane);
+        fold_finish<RT, WIN, PRO == PRO_MID, SH>(a, c, red, wave, lane);
         return;
     }
     const bool direct = c.S == 1 && !a.partial_only;
@@ -587,18 +601,13 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
     return k;
 }
 
-// N > 0: one rate for the launch; N == 0: the generic reader; N == -1 / -2: per-expert rate from the ragged meta table
-// (lane-reader rates / the other rates),
-// dispatched per workgroup.
-template <int FAM, int N, int RT, int PRO, bool WIN>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
-                                                            const uint32_t *bank_of, int in, int out, int splits,
-                                                            int rows_dt, int x_div, int sh_from, GemvArgs a) {
-    // The leading scalar arguments are the ones the first loads need (the input and suh of the prologue, the tile
-    // words, and whether this group is a fused shared expert's): the build preloads them into SGPRs (14 dwords,
-    // rows and x's dtype sharing one), so those loads issue without waiting for an argument load.  The struct `a`
-    // holds everything (the same values included) for the rest of the kernel.
-    const int rows = rows_dt & 0xFFFF, x_dtype = rows_dt >> 16;
+// One workgroup's work.  SH: the group is a fused shared expert's token row (compiled into the per-slot kernels only;
+// the other groups run the SH = false copy, whose set-up is that of a launch without a shared expert).
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
+__device__ __forceinline__ void gemv_group(const void *x, const uint16_t *tr0, const uint16_t *suh0,
+                                           const uint32_t *bank_of, int in, int out, int splits, int rows,
+                                           int x_dtype, int x_div, int sh_from, const GemvArgs &a,
+                                           uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
     GemvCtx c;
     c.x = x;
     c.x_div = x_div;
@@ -616,29 +625,28 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
     c.g = blockIdx.y;
     c.proj = blockIdx.z;
     const bool p1 = c.proj != 0;
-    c.suh = p1 ? a.suh[1] : suh0;
-    c.svh = p1 ? a.svh[1] : a.svh[0];
+    const uint16_t *trellis;
     c.part = p1 ? a.partial[1] : a.partial[0];
-    const uint16_t *trellis = p1 ? a.trellis[1] : tr0;  // (the shared expert's rows switch it below)
     c.rows = rows;
     c.wslots = nullptr;
-    c.shared = false;
-    c.xg = 0;
-    if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
-        if ((uint32_t)c.g >= *a.win_count) return;
-        c.bank = (int)min(a.win_expert[c.g], (uint32_t)(a.bank_limit - 1));
-        c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
-        c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
+    if constexpr (SH) {  // the shared expert's rows: expert 0 of the one-expert bank, x row g - sh_from
+        c.suh = a.sh_suh[c.proj];
+        c.svh = a.sh_svh[c.proj];
+        trellis = a.sh_trellis[c.proj];
+        c.bank = 0;
+        c.xg = c.g - sh_from;
     } else {
-        c.xg = c.g / x_div;
-        if (sh_from > 0 && c.g >= sh_from) {  // a shared expert's token row, fused into this launch
-            c.shared = true;
-            c.bank = 0;
-            c.xg = c.g - a.sh_from;
-            c.suh = a.sh_suh[c.proj];
-            c.svh = a.sh_svh[c.proj];
-            trellis = a.sh_trellis[c.proj];
+        c.suh = p1 ? a.suh[1] : suh0;
+        c.svh = p1 ? a.svh[1] : a.svh[0];
+        trellis = p1 ? a.trellis[1] : tr0;
+        c.xg = 0;
+        if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
+            if ((uint32_t)c.g >= *a.win_count) return;
+            c.bank = (int)min(a.win_expert[c.g], (uint32_t)(a.bank_limit - 1));
+            c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
+            c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
         } else {
+            c.xg = c.g / x_div;
             c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
         }
     }
@@ -646,37 +654,66 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
     c.kt0 = c.sp * c.KS;
     c.sv0 = c.sv1 = 0.f;  // fetched by gemv_body once the tile loads are out
 
-    __shared__ __align__(16) uint16_t xs[RT][XS_PITCH];
-    __shared__ float red[GEMV_WAVES][RT][128];
-
     if constexpr (N >= 0) {
         const int n = N ? N : a.n;
         const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
-        gemv_body<FAM, N, RT, PRO, WIN>(a, c, tb, n, a.k, xs, red);
+        gemv_body<FAM, N, RT, PRO, WIN, SH>(a, c, tb, n, a.k, xs, red);
     } else {
-        // Ragged bank: the rate comes from the expert's meta row.  N == -1 serves the rates with a lane reader and
-        // skips the rest; N == -2 (a second launch over the same grid) serves only the rest, with the generic reader
-        // (kept out of the first kernel, whose registers it would otherwise set).
-        const int col = p1 ? a.meta_col[1] : a.meta_col[0];
-        const uint32_t *m = a.meta + (size_t)c.bank * 8;
-        const int n = c.shared ? a.sh_n : (int)m[col];
-        const uint16_t *tb = c.shared ? trellis : trellis + 2 * (size_t)m[4 + col];
+        // Ragged bank: the rate comes from the expert's meta row (a shared expert has its own uniform rate).
+        // N == -1 serves the rates with a lane reader and skips the rest; N == -2 (a second launch over the same
+        // grid) serves only the rest, with the generic reader (kept out of the first kernel, whose registers it
+        // would otherwise set).
+        int n;
+        const uint16_t *tb;
+        if constexpr (SH) {
+            n = a.sh_n;
+            tb = trellis;
+        } else {
+            const int col = p1 ? a.meta_col[1] : a.meta_col[0];
+            const uint32_t *m = a.meta + (size_t)c.bank * 8;
+            n = (int)m[col];
+            tb = trellis + 2 * (size_t)m[4 + col];
+        }
         const DecodeK k = rate_constants<FAM>(a, n);
         const bool lane_rate = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
         if constexpr (N == -1) {
             switch (n) {
-            case 16: gemv_body<FAM, 16, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-            case 24: gemv_body<FAM, 24, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-            case 32: gemv_body<FAM, 32, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-            case 40: gemv_body<FAM, 40, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-            case 48: gemv_body<FAM, 48, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
-            case 64: gemv_body<FAM, 64, RT, PRO, WIN>(a, c, tb, n, k, xs, red); break;
+            case 16: gemv_body<FAM, 16, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red); break;
+            case 24: gemv_body<FAM, 24, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red); break;
+            case 32: gemv_body<FAM, 32, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red); break;
+            case 40: gemv_body<FAM, 40, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red); break;
+            case 48: gemv_body<FAM, 48, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red); break;
+            case 64: gemv_body<FAM, 64, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red); break;
             default: break;
             }
         } else {
-            if (!lane_rate) gemv_body<FAM, 0, RT, PRO, WIN>(a, c, tb, n, k, xs, red);
+            if (!lane_rate) gemv_body<FAM, 0, RT, PRO, WIN, SH>(a, c, tb, n, k, xs, red);
         }
     }
+}
+
+// N > 0: one rate for the launch; N == 0: the generic reader; N == -1 / -2: per-expert rate from the ragged meta table
+// (lane-reader rates / the other rates), dispatched per workgroup.
+template <int FAM, int N, int RT, int PRO, bool WIN>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
+                                                            const uint32_t *bank_of, int in, int out, int splits,
+                                                            int rows_dt, int x_div, int sh_from, GemvArgs a) {
+    // The leading scalar arguments are the ones the first loads need (the input and suh of the prologue, the tile
+    // words, and whether this group is a fused shared expert's): the build preloads them into SGPRs (14 dwords,
+    // rows and x's dtype sharing one), so those loads issue without waiting for an argument load.  The struct `a`
+    // holds everything (the same values included) for the rest of the kernel.
+    const int rows = rows_dt & 0xFFFF, x_dtype = rows_dt >> 16;
+    __shared__ __align__(16) uint16_t xs[RT][XS_PITCH];
+    __shared__ float red[GEMV_WAVES][RT][128];
+    if constexpr (RT == 1 && !WIN) {  // the per-slot MoE arm may carry a shared expert's rows
+        if (sh_from > 0 && (int)blockIdx.y >= sh_from) {
+            gemv_group<FAM, N, RT, PRO, WIN, true>(x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div,
+                                                   sh_from, a, xs, red);
+            return;
+        }
+    }
+    gemv_group<FAM, N, RT, PRO, WIN, false>(x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div, sh_from, a,
+                                            xs, red);
 }
 
 // Separate finish: one wave per (output group, row, group, projection).
