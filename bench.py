@@ -23,6 +23,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure (no sparsity)
 COPIES = 64
+SWEEP_GRAPHS = True  # --no-graph: the sweep issues every call from Python (for counter passes, one dispatch each)
 
 
 def _algorithmic_bytes(in_f: int, out_f: int, n: int, rows: int) -> int:
@@ -145,7 +146,7 @@ def _time_linear(in_f, out_f, n, rows, dec, codec_name, seed, min_pool_bytes=640
     from sushi_amd import exl3, synth
 
     dev = torch.device("cuda:0")
-    wbytes = in_f * out_f * n // 8
+    wbytes = in_f * out_f * n // 128  # n halfwords per 256-weight tile
     copies = max(2, min(256, -(-min_pool_bytes // wbytes)))
     trellis = synth.codes(seed, f"sw.{codec_name}.{in_f}x{out_f}.{n}", (copies, in_f // 16, out_f // 16, n), device=dev)
     suh = synth.sign_scale(seed, "sw.suh", (1, in_f), device=dev)
@@ -154,12 +155,13 @@ def _time_linear(in_f, out_f, n, rows, dec, codec_name, seed, min_pool_bytes=640
     projs = [exl3.Proj(trellis[i:i + 1], suh, svh) for i in range(copies)]
     exl3.linear(x, projs[0], dec)
     torch.cuda.synchronize()
-    g = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(copies)], dev)
+    calls = lambda: [exl3.linear(x, projs[i], dec) for i in range(copies)]  # noqa: E731
+    g = _capture(calls, dev) if SWEEP_GRAPHS else None
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(replays):
-        g.replay()
+        g.replay() if g is not None else calls()
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (replays * copies)
@@ -313,6 +315,8 @@ def main() -> int:
     ap.add_argument("--sweep", choices=("c2", "c3", "c5", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     args = ap.parse_args()
     if args.sweep:
+        global SWEEP_GRAPHS
+        SWEEP_GRAPHS = not args.no_graph
         sweep(args.sweep)
         return 0
     if args.gpus != 1:
