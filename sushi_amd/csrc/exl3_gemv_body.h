@@ -694,7 +694,9 @@ __device__ __forceinline__ void gemv_group(const void *x, const uint16_t *tr0, c
 
 // N > 0: one rate for the launch; N == 0: the generic reader; N == -1 / -2: per-expert rate from the ragged meta table
 // (lane-reader rates / the other rates), dispatched per workgroup.
-template <int FAM, int N, int RT, int PRO, bool WIN>
+// SHP: the launch carries a fused shared expert's rows (per-slot MoE arm): a separate instantiation, so launches
+// without them keep a kernel whose registers hold none of it.
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
                                                             const uint32_t *bank_of, int in, int out, int splits,
                                                             int rows_dt, int x_div, int sh_from, GemvArgs a) {
@@ -705,8 +707,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
     const int rows = rows_dt & 0xFFFF, x_dtype = rows_dt >> 16;
     __shared__ __align__(16) uint16_t xs[RT][XS_PITCH];
     __shared__ float red[GEMV_WAVES][RT][128];
-    if constexpr (RT == 1 && !WIN) {  // the per-slot MoE arm may carry a shared expert's rows
-        if (sh_from > 0 && (int)blockIdx.y >= sh_from) {
+    if constexpr (SHP && RT == 1 && !WIN) {  // the per-slot MoE arm may carry a shared expert's rows
+        if ((int)blockIdx.y >= sh_from) {
             gemv_group<FAM, N, RT, PRO, WIN, true>(x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div,
                                                    sh_from, a, xs, red);
             return;
@@ -738,10 +740,16 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
     finish_block(a, c, r, v0, v1, lane);
 }
 
-template <int FAM, int N, int RT, int PRO, bool WIN>
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP = false>
 static void launch_one(const GemvArgs &a, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_kernel<FAM, N, RT, PRO, WIN>), grid, dim3(GEMV_THREADS), 0, s, a.x, a.trellis[0], a.suh[0],
-                       a.bank_of, a.in, a.out, a.splits, a.rows | (a.x_dtype << 16), a.x_div, a.sh_from, a);
+    hipLaunchKernelGGL((gemv_kernel<FAM, N, RT, PRO, WIN, SHP>), grid, dim3(GEMV_THREADS), 0, s, a.x, a.trellis[0],
+                       a.suh[0], a.bank_of, a.in, a.out, a.splits, a.rows | (a.x_dtype << 16), a.x_div, a.sh_from, a);
+}
+
+template <int FAM, int N, int PRO>
+static void launch_slot(const GemvArgs &a, dim3 grid, hipStream_t s) {  // one row per group; shared rows or not
+    if (a.sh_from > 0) launch_one<FAM, N, 1, PRO, false, true>(a, grid, s);
+    else launch_one<FAM, N, 1, PRO, false, false>(a, grid, s);
 }
 
 template <int FAM, int N, int PRO>
@@ -752,14 +760,14 @@ static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
         if (a.rows != MOE_WINDOW_ROWS || !(a.partial_only || a.fold)) return hipErrorInvalidValue;
         launch_one<FAM, N, MOE_WINDOW_ROWS, PRO, true>(a, grid, s);
     } else if constexpr (PRO == PRO_X && N >= 0) {
-        if (a.rows <= 1) launch_one<FAM, N, 1, PRO, false>(a, grid, s);
+        if (a.rows <= 1) launch_slot<FAM, N, PRO>(a, grid, s);
         else if (a.rows <= 2) launch_one<FAM, N, 2, PRO, false>(a, grid, s);
         else if (a.rows <= 4) launch_one<FAM, N, 4, PRO, false>(a, grid, s);
         else if (a.rows <= 8) launch_one<FAM, N, 8, PRO, false>(a, grid, s);
         else launch_one<FAM, N, 16, PRO, false>(a, grid, s);
     } else {  // the MoE decode chain: one row per (slot, bank) pair
         if (a.rows != 1) return hipErrorInvalidValue;
-        launch_one<FAM, N, 1, PRO, false>(a, grid, s);
+        launch_slot<FAM, N, PRO>(a, grid, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
