@@ -223,6 +223,11 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
 // decoded once per window): the reference's decode chain serves up to DECODE_ROWS_MAX = 16 rows and sends wider
 // batches to moePrefill (src/exl3/root.zig:45-53).
 constexpr int kMoeDecodeRowsMax = 16;
+// EXL3_MOE_DECODE_ROWS_MAX moves that bound (tuning and tests; read by the workspace queries too).
+int moe_decode_rows_max() { return env_int("EXL3_MOE_DECODE_ROWS_MAX", kMoeDecodeRowsMax); }
+
+// Workgroups the per-slot MoE launches aim for: 1.5 per CU.
+constexpr int kMoeSlotTargetWgs = 384;
 
 struct MoePlan {
     bool windowed;
@@ -238,11 +243,20 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
     // (the most splits), so the planes fit whatever the routing turns out to be.
     const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS : nslots;
     const int rows = windowed ? MOE_WINDOW_ROWS : 1;
-    // Up to eight tile batches of TPW tiles per wave: the grids are large, so each workgroup's start-up latency is
-    // paid once for more work (later batches' loads overlap the decode), and fewer splits mean fewer partials and
-    // fold arrivals.
-    p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 8);
-    p.s2 = gemv_default_splits(inter, hidden, rows, groups, 8);
+    // Per-slot arm: at least 1.5 workgroups per CU and at most four batches of TPW tiles per wave (measured at C4's
+    // shape, b = 1 and 8: the best of every split pair tried).  Sorted arm: up to eight batches (each window's
+    // workgroup carries four rows per tile) and one workgroup per CU.
+    if (windowed) {
+        p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 8);
+        p.s2 = gemv_default_splits(inter, hidden, rows, groups, 8);
+    } else {
+        p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 4, kMoeSlotTargetWgs);
+        p.s2 = gemv_default_splits(inter, hidden, rows, groups, 4, kMoeSlotTargetWgs);
+    }
+    // EXL3_MOE_SPLITS1 / _SPLITS2 pin the gate/up and down split counts (whole 128-blocks; tuning and tests)
+    const int f1 = env_int("EXL3_MOE_SPLITS1", 0), f2 = env_int("EXL3_MOE_SPLITS2", 0);
+    if (f1 > 0 && (hidden / 128) % f1 == 0) p.s1 = f1;
+    if (f2 > 0 && (inter / 128) % f2 == 0) p.s2 = f2;
     p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
     p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));
     p.table_bytes = windowed ? align_up(sizeof(uint32_t)) + 2 * align_up((size_t)nslots * sizeof(uint32_t)) +
@@ -252,7 +266,7 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
 }
 
 bool moe_windowed(int rows, int nslots, int experts) {
-    return rows > kMoeDecodeRowsMax && nslots <= kMoeWindowMaxSlots && experts <= kMoeWindowMaxExperts;
+    return rows > moe_decode_rows_max() && nslots <= kMoeWindowMaxSlots && experts <= kMoeWindowMaxExperts;
 }
 
 // EXL3_MOE_WINDOWS=0 keeps every row count on the per-slot chain (for comparing the arms).
@@ -285,7 +299,7 @@ struct SharedBank {
 // routed rate.
 bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype) {
     const int nslots = rows * topk;
-    if (rows > kMoeDecodeRowsMax || y_dtype == EXL3_DT_F32) return false;
+    if (rows > moe_decode_rows_max() || y_dtype == EXL3_DT_F32) return false;
     const MoePlan p = plan_moe(nslots + rows, hidden, inter, false);
     return topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)3 * rows * hidden <= kFoldWords;
 }

@@ -109,7 +109,7 @@ hipError_t run_gemv_fam_FAM_MUL1(int prologue, const GemvArgs &a, hipStream_t s)
 hipError_t run_gemv_fam_FAM_HASH(int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_PAIR(int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_3INST(int prologue, const GemvArgs &a, hipStream_t s);
-int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches = 1);
+int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches = 1, int target_wgs = 0);
 
 // Top-k the MoE reduce holds per row (REDUCE_MAX_TOPK, src/exl3/expert_exl3_kernels.zig:2562).
 constexpr int kMoeReduceMaxTopk = 32;

@@ -20,7 +20,7 @@ hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s) {
     }
 }
 
-int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches) {
+int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches, int target_wgs) {
     // Splits cut k on whole Hadamard blocks.  A split of at most TPW * GEMV_WAVES k-tiles lets every wave issue all
     // of its tile loads before the prologue; up to max_batches such batches per wave are allowed where the grid is
     // large (each workgroup then pays its start-up latency once for more work, the later batches' loads overlapping
@@ -31,7 +31,8 @@ int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int ma
     const int blocks = in / 128;
     const int it = in / 16;
     const long G = (long)(out / 128) * groups_times_proj;
-    const long target = rows >= 8 ? GEMV_TARGET_WGS / 2 : GEMV_TARGET_WGS;
+    const long base = target_wgs > 0 ? target_wgs : GEMV_TARGET_WGS;
+    const long target = rows >= 8 ? base / 2 : base;
     int best = blocks;
     for (int s = 1; s <= blocks; s++) {
         if (blocks % s) continue;
