@@ -40,6 +40,17 @@ int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int ma
         best = s;
         if (G * s >= target) break;
     }
+    if (target_wgs > 0) return best;
+    // A grid that leaves part of its last round of CUs idle (448 workgroups are 1.75 per CU) gives way to the next
+    // split count if that fills its rounds better and still leaves every wave two tiles or more: 14336x4096 takes
+    // 16 splits (512 workgroups) rather than 14, and 16 rows at 4096x4096 take 256 workgroups rather than 128.
+    auto fill = [](long w) { return (double)w / (double)(((w + 255) / 256) * 256); };
+    for (int s = best + 1; s <= blocks; s++) {
+        if (blocks % s) continue;
+        if (it / s < 2 * GEMV_WAVES) break;
+        if (fill(G * s) > fill(G * best) + 0.05) best = s;
+        break;
+    }
     return best;
 }
 
