@@ -349,38 +349,43 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
     for (int rb = 0; rb < 4; rb++)
 #pragma unroll
         for (int cb = 0; cb < 4; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
-    uint4 A[4][2];
-    auto load_a_half = [&](int ks, int kb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int rb = 0; rb < 4; rb++)
-            A[rb][kb] = *reinterpret_cast<const uint4 *>(xfrag[rb] + (size_t)(ks * 2 + kb) * 512);
-    };
-    load_a_half(0, 0);
-    load_a_half(0, 1);
-    __syncthreads();  // barrier 0
-    for (int ks = 0; ks < nks; ks++) {
-        const uint16_t *slab = Bs[ks & 1];
-        const int kn = min(ks + 1, nks - 1);
-        uint4 bv[2][4];
+    // A fragments in two register sets, a full step apart: set X serves even steps and set Y odd ones; each set is
+    // refilled for the step after next as soon as its MFMAs have issued, so a fragment has a whole step to arrive.
+    uint4 AX[4][2], AY[4][2];
+    auto load_a = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
+        const int kk = min(ks, nks - 1);
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++)
-                bv[kb][cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G2_BP + kb * 32 + 8 * h);
-        __builtin_amdgcn_sched_barrier(0);
+            for (int rb = 0; rb < 4; rb++)
+                A[rb][kb] = *reinterpret_cast<const uint4 *>(xfrag[rb] + (size_t)(kk * 2 + kb) * 512);
+    };
+    load_a(0, AX);
+    load_a(1, AY);
+    __syncthreads();  // barrier 0
+    auto mstep = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
+        const uint16_t *slab = Bs[ks & 1];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
+            uint4 bv[4];  // this half-step's B fragments (the A sets hold the registers a whole step of B would take)
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++)
+                bv[cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G2_BP + kb * 32 + 8 * h);
 #pragma unroll
             for (int cb = 0; cb < 4; cb++) {
-                const h8_t B8 = __builtin_bit_cast(h8_t, bv[kb][cb]);
+                const h8_t B8 = __builtin_bit_cast(h8_t, bv[cb]);
 #pragma unroll
                 for (int rb = 0; rb < 4; rb++)
                     acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, A[rb][kb]), B8,
                                                                          acc[rb][cb], 0, 0, 0);
             }
-            load_a_half(kn, kb);
         }
+        load_a(ks + 2, A);
         __syncthreads();
+    };
+    for (int ks = 0; ks < nks; ks += 2) {  // nks is even
+        mstep(ks, AX);
+        mstep(ks + 1, AY);
     }
 
     // ---- epilogue (the decode waves have left, so the barriers below join the 8 MFMA waves): per 16-row block, the
