@@ -312,8 +312,10 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
                    const SharedBank *sb = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    // With a fused shared bank its rows are groups nslots .. nslots + rows - 1 of the per-slot arm.
+    // With a fused shared bank its rows follow the slots as groups of SH_ROWS rows; planes are kept per row (slots
+    // nslots .. nslots + rows - 1), so the plan counts nslots + rows.
     const int ngroups = sb ? nslots + rows : nslots;
+    const int grid_groups = sb ? nslots + (rows + SH_ROWS - 1) / SH_ROWS : nslots;
     MoePlan p = sb ? plan_moe(ngroups, hidden, inter, false)
                    : plan_moe(nslots, hidden, inter, moe_windows_enabled() && moe_windowed(rows, nslots, experts));
     const size_t need = p.total();
@@ -326,7 +328,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     const float scale = out_scale_of(fam);
     // 0) sorted arm: group the slots into expert windows
     uint32_t *win_count = nullptr, *win_expert = nullptr, *win_rows = nullptr, *win_slots = nullptr;
-    int groups = ngroups, grows = 1;
+    int groups = grid_groups, grows = 1;
     if (p.windowed) {
         char *t = w + 2 * p.gu_bytes + p.down_bytes;
         win_count = reinterpret_cast<uint32_t *>(t);
@@ -376,7 +378,9 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     a.fused_finish = 0;
     a.partial_only = 1;
     if (sb) {
+        a.sh_groups = grid_groups - nslots;
         a.sh_from = nslots;
+        a.sh_rows = rows;
         a.sh_n = sb->n;
         for (int i = 0; i < 2; i++) {
             a.sh_trellis[i] = sb->tr[i];
@@ -440,7 +444,9 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         d.y_dtype = y_dtype;
     }
     if (sb) {  // moe_shared_fusable checked that the three word sets fit the zeroed region
+        d.sh_groups = grid_groups - nslots;
         d.sh_from = nslots;
+        d.sh_rows = rows;
         d.sh_n = sb->n;
         d.sh_trellis[0] = sb->tr[2];
         d.sh_suh[0] = sb->su[2];

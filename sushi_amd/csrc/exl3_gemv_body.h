@@ -94,7 +94,8 @@ __device__ __forceinline__ float silu(float g) {
 struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div, x_dtype;
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
-    int xg;                     // the input rows' block: x rows xg * rows .. (per-slot and dense arms)
+    int xg;                     // x row of the group's row 0 (per-slot and dense arms, a shared expert's rows)
+    int slot0;                  // MoE slot of the group's row 0 (a shared expert's rows: virtual slots past the routed)
     const uint32_t *wslots;     // the window's slots, or null (group = slot, or plain rows)
     const void *x;
     const uint16_t *suh, *svh;  // this projection's banks (selected once: an indexed kernel-argument read would be
@@ -116,17 +117,19 @@ __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c
 template <bool WIN>
 __device__ __forceinline__ size_t x_row(const GemvArgs &a, const GemvCtx &c, int r) {
     if constexpr (WIN) return (size_t)(c.wslots[r] / c.x_div);
-    else return (size_t)c.xg * c.rows + r;
+    else return (size_t)c.xg + r;
 }
-template <bool WIN>
+// SH: a shared expert's rows keep one plane per row (slot slot0 + r), as the per-slot rows do.
+template <bool WIN, bool SH>
 __device__ __forceinline__ size_t part_row(const GemvArgs &a, const GemvCtx &c, int r) {
     if constexpr (WIN) return ((size_t)c.wslots[r] * c.S + c.sp) * a.out;
+    else if constexpr (SH) return ((size_t)(c.slot0 + r) * c.S + c.sp) * a.out;
     else return (((size_t)c.g * c.S + c.sp) * a.rows + r) * a.out;
 }
 template <bool WIN>
 __device__ __forceinline__ int slot_of(const GemvCtx &c, int r) {
     if constexpr (WIN) return (int)c.wslots[r];
-    else return c.g;
+    else return c.slot0 + r;  // per-slot groups hold one row
 }
 
 // The lane's 16 decoded pairs (w, already scaled for the matrix cores) against every batch row of k-tile kk.
@@ -551,7 +554,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
     const bool xcd_local = (c.G & 7) == 0;
     float *part = c.part;
     for (int r = 0; r < c.rows; r++) {
-        float *dst = part + part_row<WIN>(a, c, r) + (size_t)c.og * 128;
+        float *dst = part + part_row<WIN, SH>(a, c, r) + (size_t)c.og * 128;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int col = lane + 64 * h;
@@ -601,13 +604,14 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
     return k;
 }
 
-// One workgroup's work.  SH: the group is a fused shared expert's token row (compiled into the per-slot kernels only;
-// the other groups run the SH = false copy, whose set-up is that of a launch without a shared expert).
+// One workgroup's work for group g.  SH: g is a fused shared expert's group of token rows (compiled into the
+// per-slot kernels only; the other groups run the SH = false copy, whose set-up is that of a launch without a
+// shared expert).
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
-__device__ __forceinline__ void gemv_group(const void *x, const uint16_t *tr0, const uint16_t *suh0,
+__device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t *tr0, const uint16_t *suh0,
                                            const uint32_t *bank_of, int in, int out, int splits, int rows,
-                                           int x_dtype, int x_div, int sh_from, const GemvArgs &a,
-                                           uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
+                                           int x_dtype, int x_div, const GemvArgs &a, uint16_t (*xs)[XS_PITCH],
+                                           float (*red)[RT][128]) {
     GemvCtx c;
     c.x = x;
     c.x_div = x_div;
@@ -622,31 +626,35 @@ __device__ __forceinline__ void gemv_group(const void *x, const uint16_t *tr0, c
     const unsigned us = (unsigned)c.S, q = remap ? (unsigned)L >> 3 : (unsigned)L, qs = q / us;
     c.og = remap ? (int)qs * 8 + (L & 7) : (int)qs;
     c.sp = (int)(q - qs * us);
-    c.g = blockIdx.y;
+    c.g = g;
     c.proj = blockIdx.z;
     const bool p1 = c.proj != 0;
     const uint16_t *trellis;
     c.part = p1 ? a.partial[1] : a.partial[0];
     c.rows = rows;
     c.wslots = nullptr;
-    if constexpr (SH) {  // the shared expert's rows: expert 0 of the one-expert bank, x row g - sh_from
+    if constexpr (SH) {  // the shared expert: expert 0 of the one-expert bank, token rows RT g .. RT g + RT - 1
         c.suh = a.sh_suh[c.proj];
         c.svh = a.sh_svh[c.proj];
         trellis = a.sh_trellis[c.proj];
         c.bank = 0;
-        c.xg = c.g - sh_from;
+        c.xg = RT * g;
+        c.rows = min(RT, a.sh_rows - c.xg);
+        c.slot0 = a.sh_from + c.xg;
     } else {
         c.suh = p1 ? a.suh[1] : suh0;
         c.svh = p1 ? a.svh[1] : a.svh[0];
         trellis = p1 ? a.trellis[1] : tr0;
         c.xg = 0;
+        c.slot0 = 0;
         if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
             if ((uint32_t)c.g >= *a.win_count) return;
             c.bank = (int)min(a.win_expert[c.g], (uint32_t)(a.bank_limit - 1));
             c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
             c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
         } else {
-            c.xg = c.g / x_div;
+            c.xg = (c.g / x_div) * rows;
+            c.slot0 = c.g;
             c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
         }
     }
@@ -699,23 +707,29 @@ __device__ __forceinline__ void gemv_group(const void *x, const uint16_t *tr0, c
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
                                                             const uint32_t *bank_of, int in, int out, int splits,
-                                                            int rows_dt, int x_div, int sh_from, GemvArgs a) {
+                                                            int rows_dt, int x_div, int sh_groups, GemvArgs a) {
     // The leading scalar arguments are the ones the first loads need (the input and suh of the prologue, the tile
     // words, and whether this group is a fused shared expert's): the build preloads them into SGPRs (14 dwords,
     // rows and x's dtype sharing one), so those loads issue without waiting for an argument load.  The struct `a`
     // holds everything (the same values included) for the rest of the kernel.
     const int rows = rows_dt & 0xFFFF, x_dtype = rows_dt >> 16;
-    __shared__ __align__(16) uint16_t xs[RT][XS_PITCH];
-    __shared__ float red[GEMV_WAVES][RT][128];
-    if constexpr (SHP && RT == 1 && !WIN) {  // the per-slot MoE arm may carry a shared expert's rows
-        if ((int)blockIdx.y >= sh_from) {
-            gemv_group<FAM, N, RT, PRO, WIN, true>(x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div,
-                                                   sh_from, a, xs, red);
+    // A shared expert's groups hold SH_ROWS token rows each, so its weights are decoded once per SH_ROWS rows.
+    constexpr int RX = (SHP && RT < SH_ROWS) ? SH_ROWS : RT;
+    __shared__ __align__(16) uint16_t xs[RX][XS_PITCH];
+    __shared__ float red[GEMV_WAVES * RX * 128];
+    int g = blockIdx.y;
+    if constexpr (SHP && RT == 1 && !WIN) {
+        // The per-slot MoE arm with a shared expert: its groups come first (they carry SH_ROWS rows each, the
+        // heaviest workgroups, so they start in the first round), then the routed slots.
+        if (g < sh_groups) {
+            gemv_group<FAM, N, SH_ROWS, PRO, WIN, true>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype,
+                                                        x_div, a, xs, reinterpret_cast<float (*)[SH_ROWS][128]>(red));
             return;
         }
+        g -= sh_groups;
     }
-    gemv_group<FAM, N, RT, PRO, WIN, false>(x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div, sh_from, a,
-                                            xs, red);
+    gemv_group<FAM, N, RT, PRO, WIN, false>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div, a, xs,
+                                            reinterpret_cast<float (*)[RT][128]>(red));
 }
 
 // Separate finish: one wave per (output group, row, group, projection).
@@ -743,12 +757,12 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP = false>
 static void launch_one(const GemvArgs &a, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((gemv_kernel<FAM, N, RT, PRO, WIN, SHP>), grid, dim3(GEMV_THREADS), 0, s, a.x, a.trellis[0],
-                       a.suh[0], a.bank_of, a.in, a.out, a.splits, a.rows | (a.x_dtype << 16), a.x_div, a.sh_from, a);
+                       a.suh[0], a.bank_of, a.in, a.out, a.splits, a.rows | (a.x_dtype << 16), a.x_div, a.sh_groups, a);
 }
 
 template <int FAM, int N, int PRO>
 static void launch_slot(const GemvArgs &a, dim3 grid, hipStream_t s) {  // one row per group; shared rows or not
-    if (a.sh_from > 0) launch_one<FAM, N, 1, PRO, false, true>(a, grid, s);
+    if (a.sh_groups > 0) launch_one<FAM, N, 1, PRO, false, true>(a, grid, s);
     else launch_one<FAM, N, 1, PRO, false, false>(a, grid, s);
 }
 

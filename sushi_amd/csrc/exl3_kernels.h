@@ -87,12 +87,15 @@ struct GemvArgs {
     const uint32_t *win_expert;
     const uint32_t *win_rows;
     const uint32_t *win_slots;
-    // A shared expert fused into the routed launches (per-slot arm): groups from sh_from on are the shared expert's
-    // token rows (row = group - sh_from), decoded from the one-expert bank sh_* at rate sh_n with score 1.  The
-    // down projection folds them into their own words (sh_fold); the rounded routed and shared sums then meet in
-    // fold_comb, whose second arrival stores T(T(routed) + T(shared)).  sh_from = 0: no shared expert (the kernel
-    // takes it as a preloaded leading argument).
+    // A shared expert fused into the routed launches (per-slot arm): the first sh_groups groups of the grid are the
+    // shared expert's token rows, SH_ROWS per group, decoded from the one-expert bank sh_* at rate sh_n with score 1
+    // (the routed slots follow); their planes and slots are sh_from + row, past the routed slots (sh_from = their
+    // count).  The down projection folds them into their own words (sh_fold); the rounded routed and shared sums then
+    // meet in fold_comb, whose second arrival stores T(T(routed) + T(shared)).  sh_groups = 0: no shared expert (the
+    // kernel takes it as a preloaded leading argument).
+    int sh_groups;
     int sh_from;
+    int sh_rows;   // token rows (the shared groups hold SH_ROWS of them each)
     int sh_n;
     const uint16_t *sh_trellis[2];
     const uint16_t *sh_suh[2];
@@ -102,6 +105,9 @@ struct GemvArgs {
 
 // Rows per expert window in the sorted MoE arm.
 constexpr int MOE_WINDOW_ROWS = 4;
+
+// Token rows per group of a fused shared expert (its weights are decoded once per group).
+constexpr int SH_ROWS = 4;
 
 hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_MCG(int prologue, const GemvArgs &a, hipStream_t s);
