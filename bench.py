@@ -170,6 +170,69 @@ def _time_linear(in_f, out_f, n, rows, dec, codec_name, seed, min_pool_bytes=640
     return us, copies
 
 
+def measured_ceilings():
+    """Practical ceilings measured on this box beside the vendor peaks: a streaming read (torch's sum over 2 GiB of
+    f16, read-only), a device copy (read + write of 1 GiB), and a copy moving 8 MiB (4 MiB read + 4 MiB written, C1's
+    packed-weight bytes), launched back to back from a HIP graph over 64 rotating pairs: the per-launch floor a kernel
+    of that traffic sits on."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    big = torch.ones(1 << 30, dtype=torch.float16, device=dev)
+    read_s = timed(lambda: big.sum(), 10)
+    src, dst = big[: 1 << 29], torch.empty(1 << 29, dtype=torch.float16, device=dev)
+    copy_s = timed(lambda: dst.copy_(src), 10)
+    del big, src, dst
+    small = [torch.ones(2 << 20, dtype=torch.float16, device=dev) for _ in range(64)]
+    outs = [torch.empty(2 << 20, dtype=torch.float16, device=dev) for _ in range(64)]
+    calls = lambda: [o.copy_(t) for t, o in zip(small, outs)]  # noqa: E731
+    g = _capture(calls, dev)
+    small_s = timed(g.replay, 20) / 64
+    del g, small, outs
+    torch.cuda.empty_cache()
+    return {"hbm_read_GBps": round((2 << 30) / read_s / 1e9, 1), "hbm_copy_GBps": round((2 << 30) / copy_s / 1e9, 1),
+            "copy_8MiB_graph_us": round(small_s * 1e6, 3),
+            "how": "torch sum over 2 GiB f16 (read); copy of 1 GiB (read + write, 2 GiB moved); copy of 4 MiB (8 MiB "
+                   "moved) over 64 rotating pairs replayed from a HIP graph (per launch)"}
+
+
+def blas_f16_gemm_us(rows: int, in_f: int, out_f: int, reps: int = 20) -> float:
+    """The practical MFMA ceiling: a plain f16 GEMM [rows, in] x [in, out] through torch.matmul (hipBLASLt), f32
+    accumulate, both operands contiguous."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(rows, in_f, device=dev, generator=g).to(torch.float16)
+    w = torch.randn(in_f, out_f, device=dev, generator=g).to(torch.float16)
+    y = torch.matmul(x, w)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        torch.matmul(x, w, out=y)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del x, w, y
+    torch.cuda.empty_cache()
+    return us
+
+
 def sweep(which: str):
     """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
     one JSON line per case."""
@@ -197,6 +260,12 @@ def sweep(which: str):
             tflops = 2.0 * rows * in_f * out_f / (us * 1e-6) / 1e12
             line["TFLOPs"] = round(tflops, 1)
             line["mfma_frac_f16_dense"] = round(tflops / MFMA_F16_PEAK_TFLOPS, 4)
+            blas_us = blas_f16_gemm_us(rows, in_f, out_f)
+            blas_tflops = 2.0 * rows * in_f * out_f / (blas_us * 1e-6) / 1e12
+            line["blas_f16_gemm"] = {"us_per_call": round(blas_us, 3), "TFLOPs": round(blas_tflops, 1),
+                                     "mfma_frac_f16_dense": round(blas_tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                     "what": "torch.matmul f16 (hipBLASLt) of the same shape on decoded weights"}
+            line["frac_of_blas_f16"] = round(tflops / blas_tflops, 4)
         print(json.dumps(line), flush=True)
 
 
@@ -308,6 +377,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-sample", type=int, default=120)
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the measured read/copy/8 MiB-launch ceilings")
     ap.add_argument("--no-graph", action="store_true", help="issue every call from Python instead of a HIP graph")
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -334,6 +404,7 @@ def main() -> int:
     achieved = lin["bytes"] / launch_s / 1e9
     moe = [] if args.no_moe else [bench_moe(int(b)) for b in args.moe_batches.split(",") if b]
     cpu = cpu_baseline(args.cpu_sample) if args.cpu_sample > 0 else None
+    ceilings = measured_ceilings() if not args.no_ceilings else None
     out = {
         "metric": "effective HBM GB/s + tok/s, EXL3 K=4 4096x4096 GEMV b=1; MoE layer us/token",
         "value": round(value, 2),
@@ -353,7 +424,8 @@ def main() -> int:
         "launch_mode": "hip graphs of library calls (64 weight copies), replayed" if not args.no_graph else "python loop",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _profiled_traffic(),
-                     "algorithmic_bytes": lin["bytes"], "launch_us": round(launch_s * 1e6, 3)},
+                     "algorithmic_bytes": lin["bytes"], "launch_us": round(launch_s * 1e6, 3),
+                     "measured_ceilings": ceilings},
         "cpu_baseline": cpu,
     }
     if moe:
