@@ -233,6 +233,31 @@ def blas_f16_gemm_us(rows: int, in_f: int, out_f: int, reps: int = 20) -> float:
     return us
 
 
+def bench_encode(cb_name: str, n: int, w: int, tiles: int, replays: int = 2):
+    """The trellis encoder search (exl3.encode_tiles) over `tiles` random N(0,1) tiles: microseconds per tile, timed
+    between HIP events after one untimed call."""
+    import torch
+
+    from sushi_amd import exl3, synth
+
+    dev = torch.device("cuda:0")
+    dec = exl3.Decode(exl3.Codebook.from_name(cb_name), exl3.Window(w))
+    x = synth.normal(7, f"enc.{cb_name}.{n}.{w}", (tiles, 256), device=dev, dtype=torch.float32)
+    exl3.encode_tiles(x[:64], n, dec)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        exl3.encode_tiles(x, n, dec)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / replays
+    return {"config": "encode", "codebook": cb_name, "K": n / 16, "window": w, "tiles": tiles,
+            "us_per_call": round(us, 1), "us_per_tile": round(us / tiles, 3), "tiles_per_s": round(tiles / (us * 1e-6)),
+            "weights_per_s": round(256 * tiles / (us * 1e-6))}
+
+
 def sweep(which: str):
     """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
     one JSON line per case."""
@@ -249,6 +274,10 @@ def sweep(which: str):
             cases.append(("c3", 4096, 14336, 48, rows, exl3.INST3, "3inst"))
     if which in ("c5", "all"):
         print(json.dumps(bench_moe_c5()), flush=True)
+    if which in ("enc", "all"):
+        for cb_name, n, w, tiles in (("mcg", 32, 12, 65536), ("mcg", 40, 15, 8192), ("mcg", 64, 16, 4096),
+                                     ("mul1", 48, 15, 8192), ("mcg", 32, 16, 2048)):
+            print(json.dumps(bench_encode(cb_name, n, w, tiles)), flush=True)
     for cfg, in_f, out_f, n, rows, dec, name in cases:
         us, copies = _time_linear(in_f, out_f, n, rows, dec, name, 1 if cfg == "c2" else 2)
         alg = _algorithmic_bytes(in_f, out_f, n, rows)
@@ -382,7 +411,7 @@ def main() -> int:
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
-    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
+    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "enc", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     args = ap.parse_args()
     if args.sweep:
         global SWEEP_GRAPHS

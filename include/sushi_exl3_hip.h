@@ -81,7 +81,10 @@ typedef enum {
     EXL3_ERR_LAUNCH = -8,                    /* Exl3GemmLaunchFailed / a HIP launch error */
     EXL3_ERR_WORKSPACE = -9,                 /* caller workspace too small or misaligned */
     EXL3_ERR_RATE_MISSING = -10,             /* Exl3CodebookTableRateMissing */
-    EXL3_ERR_WINDOW = -11                    /* Exl3WindowUnsupported */
+    EXL3_ERR_WINDOW = -11,                   /* Exl3WindowUnsupported; the encoder's WindowUnsupported */
+    EXL3_ERR_CODEBOOK_UNSUPPORTED = -12,     /* encoder: CodebookUnsupported (src/encoder/encode.zig:7) */
+    EXL3_ERR_RATE_UNSUPPORTED = -13,         /* encoder: RateUnsupported */
+    EXL3_ERR_WINDOW_TOO_NARROW = -14         /* encoder: WindowTooNarrow */
 } exl3_status;
 
 /* One projection's bank (`Proj`, src/exl3/root.zig:28-30). */
@@ -202,6 +205,19 @@ int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int3
  * between the pack order [IT][OT][n] and the pair-major order [OT/2][IT][2][n]. */
 int32_t exl3_tile_major(const uint16_t *src, uint16_t *dst, int32_t experts, int32_t it, int32_t ot, int32_t n,
                         int32_t inverse, hipStream_t stream);
+
+/* Trellis encoder search, `Encoder.encodeTile` (src/encoder/encode.zig:170-309) over `count` tiles: each row-major
+ * 16x16 f32 tile of `tiles` [count][256] gets the packed codes [count][n] u16 of its least-squares tail-biting path
+ * through the codebook (two passes: a free pass over the tile rolled by half pins the closing register, a pinned
+ * pass writes the path), and, when `sse` is non-null, that path's f64 squared error [count].  Codes and errors are
+ * the reference search's: f32 squared errors fused with the predecessor's f16 path cost, first minimum wins.
+ * Codebooks MCG and MUL1 (and the 3INST extension), windows 12..16, every admitted rate whose fresh bits fit the
+ * window; refusals: EXL3_ERR_CODEBOOK_UNSUPPORTED, EXL3_ERR_RATE_UNSUPPORTED, EXL3_ERR_WINDOW,
+ * EXL3_ERR_WINDOW_TOO_NARROW.  The workspace holds the backpointers of the searches in flight; a smaller one than
+ * exl3_encode_workspace_size() asks (but at least one workgroup's share) runs fewer searches at once. */
+size_t exl3_encode_workspace_size(int32_t n, exl3_decode_t dec, int64_t count);
+int32_t exl3_encode_tiles(const float *tiles, int64_t count, int32_t n, exl3_decode_t dec, uint16_t *packed,
+                          double *sse, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

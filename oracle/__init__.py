@@ -97,6 +97,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.ox_route_topk.argtypes = [vp, sz, sz, sz, vp, vp]
     L.ox_tile_major.argtypes = [vp, vp, sz, sz, sz]
     L.ox_tile_major_inverse.argtypes = [vp, vp, sz, sz, sz]
+    L.ox_viterbi_pass.argtypes = [vp, vp, sz, vp, u32, ctypes.c_int64, vp]
+    L.ox_viterbi_pass.restype = ctypes.c_double
+    L.ox_exact_tail_biting.argtypes = [vp, vp, sz, vp, u32, vp]
+    L.ox_exact_tail_biting.restype = ctypes.c_double
+    L.ox_pack_states.argtypes = [u32, vp, vp]
+    L.ox_encode_tile.argtypes = [vp, u32, Decode, vp, vp, ctypes.POINTER(ctypes.c_double)]
 
 
 def _u16(a) -> np.ndarray:
@@ -317,3 +323,46 @@ def tile_major_inverse(src, it: int, ot: int, n: int) -> np.ndarray:
     dst = np.zeros_like(s)
     lib().ox_tile_major_inverse(_p(s), _p(dst), it, ot, n)
     return dst
+
+
+# ---- encoder search (src/encoder/encode.zig) ------------------------------------------------------------------
+
+
+def viterbi_pass(x, ks, table, w: int, pin=None):
+    """`viterbiPass` (encode.zig:46-101) in f64: (cost, path)."""
+    xs = np.ascontiguousarray(x, np.float64)
+    k = np.ascontiguousarray(ks, np.uint8)
+    t = np.ascontiguousarray(table, np.float64)
+    path = np.zeros(len(xs), np.uint16)
+    c = lib().ox_viterbi_pass(_p(xs), _p(k), len(xs), _p(t), w, -1 if pin is None else int(pin), _p(path))
+    return c, path
+
+
+def exact_tail_biting(x, ks, table, w: int):
+    xs = np.ascontiguousarray(x, np.float64)
+    k = np.ascontiguousarray(ks, np.uint8)
+    t = np.ascontiguousarray(table, np.float64)
+    path = np.zeros(len(xs), np.uint16)
+    return lib().ox_exact_tail_biting(_p(xs), _p(k), len(xs), _p(t), w, _p(path)), path
+
+
+def pack_states(n: int, states) -> np.ndarray:
+    s = _u16(states)
+    out = np.zeros(n, np.uint16)
+    lib().ox_pack_states(n, _p(s), _p(out))
+    return out
+
+
+ENCODE_ERRORS = {-1: "CodebookUnsupported", -2: "RateUnsupported", -3: "WindowUnsupported", -4: "WindowTooNarrow"}
+
+
+def encode_tile(tile, n: int, dec: Decode):
+    """`Encoder.encodeTile` (encode.zig:170-294): (packed [n] u16, sse f64, recon [256] f32) of one row-major tile."""
+    x = _f32(tile).reshape(256)
+    packed = np.zeros(n, np.uint16)
+    recon = np.zeros(256, np.float32)
+    sse = ctypes.c_double()
+    rc = lib().ox_encode_tile(_p(x), n, dec, _p(packed), _p(recon), ctypes.byref(sse))
+    if rc != 0:
+        raise ValueError(ENCODE_ERRORS.get(rc, str(rc)))
+    return packed, sse.value, recon

@@ -675,3 +675,188 @@ void ox_tile_major_inverse(const uint16_t *src, uint16_t *dst, size_t it, size_t
             for (size_t o = 0; o < 2; o++)
                 memcpy(dst + (tk * ot + pair * 2 + o) * n, src + ((pair * it + tk) * 2 + o) * n, n * 2);
 }
+
+/* ------------------------------------------------------------------------------------------------ */
+/* Encoder search: src/encoder/encode.zig                                                            */
+
+/* viterbiPass (encode.zig:46-101): least-squares path of x through table[0..2^w), one codeword per step,
+ * cw_t = ((cw_{t-1} << k_t) | f_t) & (2^w - 1).  pin >= 0 fixes the register entering step 0 (cw_0 >> k_0) and
+ * requires the last codeword to carry it in its low w - k_0 bits.  f64 throughout; the first minimum wins. */
+double ox_viterbi_pass(const double *x, const uint8_t *ks, size_t steps, const double *table, uint32_t w,
+                       int64_t pin, uint16_t *path) {
+    const size_t states = (size_t)1 << w;
+    uint32_t kmin = 31;
+    for (size_t i = 0; i < steps; i++) kmin = ks[i] < kmin ? ks[i] : kmin;
+    const size_t stride = (size_t)1 << (w - kmin);
+    double *prev = malloc(states * sizeof(double)), *next = malloc(states * sizeof(double));
+    double *best = malloc(stride * sizeof(double));
+    uint8_t *back = calloc(steps * stride, 1);
+    const uint32_t k0 = ks[0];
+    for (size_t cw = 0; cw < states; cw++) {
+        double d = x[0] - table[cw];
+        prev[cw] = (pin >= 0 && (int64_t)(cw >> k0) != pin) ? INFINITY : d * d;
+    }
+    for (size_t i = 1; i < steps; i++) {
+        const uint32_t k = ks[i];
+        const size_t s = (size_t)1 << (w - k), kk = (size_t)1 << k;
+        uint8_t *row = back + i * stride;
+        for (size_t low = 0; low < s; low++) { best[low] = prev[low]; row[low] = 0; }
+        for (size_t j = 1; j < kk; j++)
+            for (size_t low = 0; low < s; low++)
+                if (prev[j * s + low] < best[low]) { best[low] = prev[j * s + low]; row[low] = (uint8_t)j; }
+        for (size_t low = 0; low < s; low++)
+            for (size_t f = 0; f < kk; f++) {
+                double d = x[i] - table[low * kk + f];
+                next[low * kk + f] = best[low] + d * d;
+            }
+        double *t = prev; prev = next; next = t;
+    }
+    double best_cost = INFINITY;
+    size_t cur = 0;
+    const size_t reg_mask = ((size_t)1 << (w - k0)) - 1;
+    for (size_t cw = 0; cw < states; cw++) {
+        if (pin >= 0 && (int64_t)(cw & reg_mask) != pin) continue;
+        if (prev[cw] < best_cost) { best_cost = prev[cw]; cur = cw; }
+    }
+    path[steps - 1] = (uint16_t)cur;
+    for (size_t i = steps - 1; i > 0; i--) {
+        const uint32_t k = ks[i];
+        size_t low = cur >> k;
+        cur = ((size_t)back[i * stride + low] << (w - k)) | low;
+        path[i - 1] = (uint16_t)cur;
+    }
+    free(prev); free(next); free(best); free(back);
+    return best_cost;
+}
+
+/* exactTailBiting (encode.zig:104-118): every register in turn, the cheapest pinned pass. */
+double ox_exact_tail_biting(const double *x, const uint8_t *ks, size_t steps, const double *table, uint32_t w,
+                            uint16_t *path) {
+    uint16_t *tmp = malloc(steps * sizeof(uint16_t));
+    double best = INFINITY;
+    for (int64_t reg = 0; reg < ((int64_t)1 << (w - ks[0])); reg++) {
+        double c = ox_viterbi_pass(x, ks, steps, table, w, reg, tmp);
+        if (c < best) { best = c; memcpy(path, tmp, steps * sizeof(uint16_t)); }
+    }
+    free(tmp);
+    return best;
+}
+
+/* Encoder.packStates (encode.zig:296-309): the fresh k_t low bits of each state, MSB first, at the bits ending at
+ * bitEnd(t), in the loader's stream order (32-bit big-endian words of two swapped halfwords). */
+void ox_pack_states(uint32_t n, const uint16_t states[256], uint16_t *out) {
+    memset(out, 0, n * sizeof(uint16_t));
+    for (uint32_t t = 0; t < 256; t++) {
+        const uint32_t end = ox_bit_end(n, t);
+        const uint32_t k = end - (t == 0 ? 0 : ox_bit_end(n, t - 1));
+        for (uint32_t b = 0; b < k; b++) {
+            const uint16_t bit = (states[t] >> (k - 1 - b)) & 1u;
+            const uint32_t p = end - k + b;
+            const uint32_t half = (p / 32) * 2 + (p % 32 < 16 ? 1 : 0);
+            out[half] |= (uint16_t)(bit << (15 - p % 16));
+        }
+    }
+}
+
+/* Encoder.encodeTile (encode.zig:170-294): the two-pass tail-biting search of one row-major 16x16 tile.  Pass 0 runs
+ * free over the tile rolled by half and traces back to the register entering step 0; pass 1 is pinned to it and
+ * writes the path.  Costs follow the reference's arithmetic: f32 squared error (fused with the predecessor's cost),
+ * f16 path costs clamped at 65504, one-byte backpointers, first minimum wins.  Returns 0 and the path's f64 squared
+ * error, or -1 codebook (not MCG/MUL1, or this build's 3INST extension), -2 rate, -3 window outside 12..16, -4 window
+ * too narrow for the rate. */
+int ox_encode_tile(const float tile[256], uint32_t n, ox_decode dec, uint16_t *packed, float recon[256],
+                   double *sse_out) {
+    if (dec.codebook != OX_CB_MCG && dec.codebook != OX_CB_MUL1 && dec.codebook != OX_CB_3INST) return -1;
+    if (!ox_rate_admitted(n)) return -2;
+    if (dec.window_bits < 12 || dec.window_bits > 16) return -3;
+    const uint32_t w = (uint32_t)dec.window_bits;
+    uint8_t ks[256];
+    uint32_t kmin = 31, kmax = 0;
+    for (uint32_t t = 0; t < 256; t++) {
+        ks[t] = (uint8_t)(ox_bit_end(n, t) - (t == 0 ? 0 : ox_bit_end(n, t - 1)));
+        kmin = ks[t] < kmin ? ks[t] : kmin;
+        kmax = ks[t] > kmax ? ks[t] : kmax;
+    }
+    if (kmax >= w) return -4;
+    uint32_t perm[256];
+    ox_tensor_core_perm(perm);
+    const size_t stride = (size_t)1 << (w - kmin);
+    float *table = malloc(((size_t)1 << w) * sizeof(float));
+    for (size_t cw = 0; cw < ((size_t)1 << w); cw++)
+        table[cw] = ox_f16_to_f32(dec.codebook == OX_CB_MCG    ? ox_decode_mcg((uint16_t)cw)
+                                  : dec.codebook == OX_CB_MUL1 ? ox_decode_mul1((uint16_t)cw)
+                                                               : ox_decode_3inst((uint16_t)cw));
+    uint16_t *costs[2] = {malloc(stride * sizeof(uint16_t)), malloc(stride * sizeof(uint16_t))};
+    uint8_t *back = calloc(256 * stride, 1);
+    float x[256];
+    uint16_t path[256];
+    for (int i = 0; i < 256; i++) x[i] = tile[perm[i]];
+    const float h_inf = 65504.0f;
+    size_t pin = 0;
+    int pinned = 0;
+    for (int pass = 0; pass < 2; pass++) {
+        const size_t roll = pass == 0 ? 128 : 0;
+        uint16_t *prev = costs[0], *curr = costs[1];
+        for (size_t step = 0; step < 256; step++) {
+            const size_t ri = (step + roll) & 255;
+            const uint32_t k = ks[ri], k_next = ks[(ri + 1) & 255];
+            const uint32_t kr = w - k_next;
+            const size_t kk = (size_t)1 << k_next, edges = (size_t)1 << kr;
+            const float target = x[ri];
+            uint8_t *row = back + ri * stride;
+            for (size_t e = 0; e < edges; e++) {
+                float best = h_inf;
+                uint8_t best_fresh = 0;
+                for (size_t fresh = 0; fresh < kk; fresh++) {
+                    const size_t cw = (fresh << kr) | e;
+                    const size_t pred = cw >> k;
+                    const float dh = table[cw] - target;
+                    float err;
+                    if (step == 0) {
+                        if (pinned && pred != pin) err = h_inf;
+                        else { float sq = dh * dh; err = sq < h_inf ? sq : h_inf; }
+                    } else {
+                        err = fmaf(dh, dh, ox_f16_to_f32(prev[pred]));
+                    }
+                    if (err < best) { best = err; best_fresh = (uint8_t)fresh; }
+                }
+                curr[e] = ox_f32_to_f16(best);
+                row[e] = best_fresh;
+            }
+            uint16_t *t = prev; prev = curr; curr = t;
+        }
+        size_t edge = pin;
+        if (pass == 0) {
+            const size_t final_edges = (size_t)1 << (w - ks[0]);
+            float best = h_inf;
+            edge = 0;
+            for (size_t e = 0; e < final_edges; e++) {
+                const float v = ox_f16_to_f32(prev[e]);
+                if (v < best) { best = v; edge = e; }
+            }
+        }
+        for (size_t step_i = 256; step_i > 0;) {
+            step_i--;
+            const size_t ri = (step_i + roll) & 255;
+            const uint32_t k = ks[ri], k_next = ks[(ri + 1) & 255];
+            const uint32_t kr = w - k_next;
+            const size_t state = ((size_t)back[ri * stride + edge] << kr) | edge;
+            edge = state >> k;
+            if (pass == 1) path[ri] = (uint16_t)state;
+            else if (ri == 0) break;
+        }
+        pin = edge;
+        pinned = 1;
+    }
+    ox_pack_states(n, path, packed);
+    double sse = 0.0;
+    for (int i = 0; i < 256; i++) {
+        const double d = (double)x[i] - (double)table[path[i]];
+        sse += d * d;
+    }
+    if (recon)
+        for (int i = 0; i < 256; i++) recon[perm[i]] = table[path[i]];
+    *sse_out = sse;
+    free(table); free(costs[0]); free(costs[1]); free(back);
+    return 0;
+}

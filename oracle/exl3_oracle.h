@@ -29,6 +29,12 @@
  *   ox_decode_dense               : equals the dense product diag(suh) H M H diag(svh) built by numpy.
  *   ox_route_topk                 : closed form (softmax, top-k, renormalise) vs numpy.
  *   ox_tile_major(_inverse)       : round trip + the reference's layout test (layout.zig:160-175).
+ *   ox_viterbi_pass               : brute force over every tail-biting path on small windows (encode.zig:337-393).
+ *   ox_exact_tail_biting          : the minimum of the brute force over every register.
+ *   ox_encode_tile / ox_pack_states : the reference's search fixture (exl3_encode_tiles: packed codes and costs of
+ *                                   the reference search, 13 codebook x rate x window configs, bit-exact); every
+ *                                   packed tile decodes (ox_decode_tile) to the values the search scored; the
+ *                                   half-roll warm-up pin reaches the exact tail-biting optimum (encode.zig:396-431).
  */
 #ifndef SUSHI_EXL3_ORACLE_H
 #define SUSHI_EXL3_ORACLE_H
@@ -124,6 +130,15 @@ int ox_decode_dense(const uint16_t *words, const uint16_t *suh, const uint16_t *
 void ox_route_topk(const float *logits, size_t rows, size_t experts, size_t k, uint32_t *inds, float *scores);
 
 void ox_tile_major(const uint16_t *src, uint16_t *dst, size_t it, size_t ot, size_t n);
+
+/* Encoder search (src/encoder/encode.zig) */
+double ox_viterbi_pass(const double *x, const uint8_t *ks, size_t steps, const double *table, uint32_t w,
+                       int64_t pin, uint16_t *path);
+double ox_exact_tail_biting(const double *x, const uint8_t *ks, size_t steps, const double *table, uint32_t w,
+                            uint16_t *path);
+void ox_pack_states(uint32_t n, const uint16_t states[256], uint16_t *out);
+int ox_encode_tile(const float tile[256], uint32_t n, ox_decode dec, uint16_t *packed, float recon[256],
+                   double *sse_out);
 void ox_tile_major_inverse(const uint16_t *src, uint16_t *dst, size_t it, size_t ot, size_t n);
 
 #ifdef __cplusplus

@@ -28,6 +28,8 @@ EXPORTS = (
     "exl3_moe_ragged_with_shared_bank",
     "exl3_route_topk",
     "exl3_tile_major",
+    "exl3_encode_workspace_size",
+    "exl3_encode_tiles",
 )
 
 
@@ -87,6 +89,9 @@ def load() -> ctypes.CDLL:
                                                    vp]
     L.exl3_route_topk.argtypes = [vp, i32, i32, i32, vp, vp, vp]
     L.exl3_tile_major.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp]
+    L.exl3_encode_workspace_size.restype = sz
+    L.exl3_encode_workspace_size.argtypes = [i32, DecodeT, ctypes.c_int64]
+    L.exl3_encode_tiles.argtypes = [vp, ctypes.c_int64, i32, DecodeT, vp, vp, vp, sz, vp]
     for name in EXPORTS:
         if name in ("exl3_abi_version", "exl3_last_error") or name.endswith("workspace_size"):
             continue

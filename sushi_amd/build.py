@@ -28,6 +28,7 @@ SOURCES = [
     "exl3_gemv_hash.hip",
     "exl3_gemv_pair.hip",
     "exl3_gemv_3inst.hip",
+    "exl3_encode.hip",
 ]
 
 CFLAGS = [

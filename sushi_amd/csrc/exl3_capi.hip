@@ -727,4 +727,85 @@ int32_t exl3_tile_major(const uint16_t *src, uint16_t *dst, int32_t experts, int
     return launched(run_tile_major(src, dst, experts, it, ot, n, inverse, stream), "exl3_tile_major");
 }
 
+// ---- Trellis encoder search ------------------------------------------------------------------------------------
+
+namespace {
+
+struct EncodePlan {
+    int w, stride, tiles_per_wg, grid_max;
+    size_t per_wg;
+};
+
+// Encoder.init (src/encoder/encode.zig:120-160): the searchable codebooks (MCG, MUL1; 3INST as this build's
+// extension), an admitted rate, a window of 12..16 bits wider than every step's fresh bits.
+int32_t encode_plan(int32_t n, const exl3_decode_t &dec, int64_t count, EncodePlan *p) {
+    if (dec.codebook != EXL3_CB_MCG && dec.codebook != EXL3_CB_MUL1 && dec.codebook != EXL3_CB_3INST)
+        return fail(EXL3_ERR_CODEBOOK_UNSUPPORTED, "encode: codebook %d is not searchable (MCG, MUL1, 3INST)",
+                    dec.codebook);
+    if (!rate_admitted(n)) return fail(EXL3_ERR_RATE_UNSUPPORTED, "encode: n=%d is not an admitted rate", n);
+    if (dec.window_bits < 12 || dec.window_bits > 16)
+        return fail(EXL3_ERR_WINDOW, "encode: window %d is outside 12..16", dec.window_bits);
+    if (count < 0) return fail(EXL3_ERR_BAD_SHAPE, "encode: negative tile count");
+    int kmin = 31, kmax = 0;
+    for (int t = 0; t < 256; t++) {
+        const int k = (((t + 1) * n) >> 4) - ((t * n) >> 4);
+        kmin = k < kmin ? k : kmin;
+        kmax = k > kmax ? k : kmax;
+    }
+    if (kmax >= dec.window_bits)
+        return fail(EXL3_ERR_WINDOW_TOO_NARROW, "encode: window %d carries no state at n=%d", dec.window_bits, n);
+    p->w = dec.window_bits;
+    p->stride = 1 << (p->w - kmin);
+    // Tiles per workgroup: as many as keep the workgroup's LDS within about half a CU's 160 KB.
+    p->tiles_per_wg = 1;
+    for (int t = 16; t >= 2; t >>= 1)
+        if (encode_lds_bytes(t, p->stride) <= 78 * 1024) { p->tiles_per_wg = t; break; }
+    const size_t lds = encode_lds_bytes(p->tiles_per_wg, p->stride);
+    int per_cu = (int)((160 * 1024) / lds);
+    per_cu = per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu;
+    const int64_t batches = (count + p->tiles_per_wg - 1) / p->tiles_per_wg;
+    const int64_t cap = 256LL * per_cu;
+    p->grid_max = (int)(batches < cap ? batches : cap);
+    p->per_wg = (size_t)p->tiles_per_wg * 256 * p->stride;
+    return ok();
+}
+
+}  // namespace
+
+size_t exl3_encode_workspace_size(int32_t n, exl3_decode_t dec, int64_t count) {
+    EncodePlan p;
+    if (encode_plan(n, dec, count, &p) != EXL3_OK) return 0;
+    return (size_t)p.grid_max * p.per_wg;
+}
+
+int32_t exl3_encode_tiles(const float *tiles, int64_t count, int32_t n, exl3_decode_t dec, uint16_t *packed,
+                          double *sse, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    EncodePlan p;
+    int32_t rc = encode_plan(n, dec, count, &p);
+    if (rc) return rc;
+    if (count == 0) return ok();
+    if (!tiles || !packed) return fail(EXL3_ERR_BAD_SHAPE, "encode: null operand");
+    const size_t fit = workspace ? workspace_bytes / p.per_wg : 0;
+    if (fit < 1)
+        return fail(EXL3_ERR_WORKSPACE, "encode: workspace of %zu bytes holds no search (%zu per workgroup)",
+                    workspace_bytes, p.per_wg);
+    int fam;
+    DecodeK k;
+    rc = resolve_decode(dec, n, &fam, &k);
+    if (rc) return rc;
+    EncodeArgs a;
+    a.tiles = tiles;
+    a.count = count;
+    a.n = n;
+    a.w = p.w;
+    a.k = k;
+    a.packed = packed;
+    a.sse = sse;
+    a.back = static_cast<uint8_t *>(workspace);
+    a.stride = p.stride;
+    a.tiles_per_wg = p.tiles_per_wg;
+    a.grid = (int)((size_t)p.grid_max < fit ? (size_t)p.grid_max : fit);
+    return launched(run_encode(fam, a, stream), "exl3_encode_tiles");
+}
+
 }  // extern "C"

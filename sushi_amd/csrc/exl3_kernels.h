@@ -171,4 +171,23 @@ hipError_t run_tile_major(const uint16_t *src, uint16_t *dst, int experts, int i
                           hipStream_t s);
 hipError_t run_fill_zero(void *p, size_t bytes, hipStream_t s);
 
+// Trellis encoder search (src/encoder/encode.zig:170-309): `count` row-major 16x16 f32 tiles -> packed codes [count][n]
+// and, when `sse` is set, each path's f64 squared error.  `tiles_per_wg` tiles share a workgroup; `back` holds
+// grid x tiles_per_wg x 256 x stride backpointer bytes (stride = 2^(w - kmin)).
+struct EncodeArgs {
+    const float *tiles;
+    int64_t count;
+    int n;
+    int w;
+    DecodeK k;
+    uint16_t *packed;
+    double *sse;
+    uint8_t *back;
+    int stride;
+    int tiles_per_wg;
+    int grid;
+};
+size_t encode_lds_bytes(int tiles_per_wg, int stride);
+hipError_t run_encode(int fam, const EncodeArgs &a, hipStream_t s);
+
 }  // namespace exl3

@@ -74,6 +74,19 @@ class Exl3WindowUnsupported(Exl3Error):
     status = -11
 
 
+class CodebookUnsupported(Exl3Error):
+    """The encoder searches MCG and MUL1 (and the 3INST extension) only (src/encoder/encode.zig:7-12)."""
+    status = -12
+
+
+class RateUnsupported(Exl3Error):
+    status = -13
+
+
+class WindowTooNarrow(Exl3Error):
+    status = -14
+
+
 _BY_STATUS = {c.status: c for c in Exl3Error.__subclasses__()}
 
 
@@ -628,3 +641,24 @@ def tile_major(trellis: torch.Tensor, inverse: bool = False) -> torch.Tensor:
     _check(_lib.load().exl3_tile_major(trellis.data_ptr(), out.data_ptr(), e, it, ot, n, int(inverse),
                                        _stream(trellis.device)))
     return out
+
+
+def encode_tiles(tiles: torch.Tensor, n: int, dec: Decode, with_sse: bool = True):
+    """`Encoder.encodeTile` (src/encoder/encode.zig:170-309) over a batch on the GPU: row-major 16x16 f32 tiles
+    [..., 256] (or [..., 16, 16]) -> (packed codes [..., n] as int16, f64 squared errors [...] or None)."""
+    t = tiles.to(torch.float32).contiguous()
+    _need_gpu(t)
+    count = t.numel() // 256
+    if t.numel() != count * 256:
+        raise BadExl3Shape(f"tiles of {t.numel()} values are not whole 16x16 tiles")
+    lead = t.shape[:-2] if t.dim() >= 2 and tuple(t.shape[-2:]) == (16, 16) else t.shape[:-1]
+    L = _lib.load()
+    ws_bytes = L.exl3_encode_workspace_size(n, dec.c(), count)
+    if ws_bytes == 0 and count > 0:
+        _check(L.exl3_encode_tiles(0, count, n, dec.c(), 0, 0, 0, 0, _stream(t.device)))
+    packed = torch.empty(count, n, dtype=torch.int16, device=t.device)
+    sse = torch.empty(count, dtype=torch.float64, device=t.device) if with_sse else None
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=t.device)
+    _check(L.exl3_encode_tiles(t.data_ptr(), count, n, dec.c(), packed.data_ptr(),
+                               0 if sse is None else sse.data_ptr(), ws.data_ptr(), ws.numel(), _stream(t.device)))
+    return packed.reshape(*lead, n), (None if sse is None else sse.reshape(lead))
