@@ -84,7 +84,8 @@ typedef enum {
     EXL3_ERR_WINDOW = -11,                   /* Exl3WindowUnsupported; the encoder's WindowUnsupported */
     EXL3_ERR_CODEBOOK_UNSUPPORTED = -12,     /* encoder: CodebookUnsupported (src/encoder/encode.zig:7) */
     EXL3_ERR_RATE_UNSUPPORTED = -13,         /* encoder: RateUnsupported */
-    EXL3_ERR_WINDOW_TOO_NARROW = -14         /* encoder: WindowTooNarrow */
+    EXL3_ERR_WINDOW_TOO_NARROW = -14,        /* encoder: WindowTooNarrow */
+    EXL3_ERR_HESSIAN = -15                   /* quantizer: HessianNotPositiveDefinite (src/encoder/quantize.zig:351) */
 } exl3_status;
 
 /* One projection's bank (`Proj`, src/exl3/root.zig:28-30). */
@@ -218,6 +219,21 @@ int32_t exl3_tile_major(const uint16_t *src, uint16_t *dst, int32_t experts, int
 size_t exl3_encode_workspace_size(int32_t n, exl3_decode_t dec, int64_t count);
 int32_t exl3_encode_tiles(const float *tiles, int64_t count, int32_t n, exl3_decode_t dec, uint16_t *packed,
                           double *sse, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Whole-tensor quantizer, `quantizeTensor` (src/encoder/quantize.zig:600-626): a public weight w [in][out] f32 and
+ * its input Hessian h [in][in] f32, with the sign vectors sign_in [in] / sign_out [out] (+-1), to the three tensors of
+ * a pack: packed [in/16][out/16][n] u16, suh [in] and svh [out] as f16 bits, and the global scale g.  Regularizes
+ * into the Hadamard basis (block-RMS input/output scales; out_scales 0 auto, 1 always, 2 never), rotates and
+ * damps the Hessian and factors it as a 16-row block LDL, picks g by golden section over the codebook's bracket, and
+ * searches the tiles in reverse LDLQ order with the error fed back through the factor -- the reference's arithmetic
+ * throughout, so its codes.  The host pointers are read and written synchronously (the call returns when done); the
+ * searches and the LDLQ run on `stream` in `workspace` (exl3_quantize_workspace_size bytes of device memory).
+ * in and out are multiples of 128; refusals as exl3_encode_tiles, and EXL3_ERR_HESSIAN. */
+size_t exl3_quantize_workspace_size(int32_t in, int32_t out, int32_t n, exl3_decode_t dec);
+int32_t exl3_quantize_tensor(const float *w, const float *h, int32_t in, int32_t out, const float *sign_in,
+                             const float *sign_out, int32_t n, exl3_decode_t dec, int32_t out_scales, uint16_t *packed,
+                             uint16_t *suh, uint16_t *svh, float *g, void *workspace, size_t workspace_bytes,
+                             hipStream_t stream);
 
 #ifdef __cplusplus
 }

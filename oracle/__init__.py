@@ -103,6 +103,15 @@ def _declare(L: ctypes.CDLL) -> None:
     L.ox_exact_tail_biting.restype = ctypes.c_double
     L.ox_pack_states.argtypes = [u32, vp, vp]
     L.ox_encode_tile.argtypes = [vp, u32, Decode, vp, vp, ctypes.POINTER(ctypes.c_double)]
+    L.ox_quant_regularize.argtypes = [vp, sz, sz, vp, vp, ctypes.c_int, vp, vp, vp, vp]
+    L.ox_quant_rotated_hessian.argtypes = [vp, vp, sz, vp]
+    L.ox_cholesky_lower.argtypes = [vp, sz]
+    L.ox_cholesky_lower.restype = sz
+    L.ox_quant_ldl_factor.argtypes = [vp, sz, vp]
+    L.ox_quant_global_scale.argtypes = [vp, sz, sz, u32, Decode, vp]
+    L.ox_quant_ldlq.argtypes = [vp, vp, sz, sz, u32, Decode, vp, vp]
+    L.ox_quant_signs.argtypes = [ctypes.c_uint64, ctypes.c_char_p, sz, vp]
+    L.ox_quantize_tensor.argtypes = [vp, vp, sz, sz, vp, vp, u32, Decode, ctypes.c_int, vp, vp, vp, vp]
 
 
 def _u16(a) -> np.ndarray:
@@ -366,3 +375,79 @@ def encode_tile(tile, n: int, dec: Decode):
     if rc != 0:
         raise ValueError(ENCODE_ERRORS.get(rc, str(rc)))
     return packed, sse.value, recon
+
+
+# ---- quantizer (src/encoder/quantize.zig) ------------------------------------------------------------------------
+
+OUT_SCALES = {"auto": 0, "always": 1, "never": 2}
+
+
+def quant_regularize(w, sign_in, sign_out, mode: str, hdiag=None):
+    w = _f32(w)
+    rows, cols = w.shape
+    inner = np.zeros_like(w)
+    suh = np.zeros(rows, np.float32)
+    svh = np.zeros(cols, np.float32)
+    hd = None if hdiag is None else _f32(hdiag)
+    rc = lib().ox_quant_regularize(_p(w), rows, cols, _p(_f32(sign_in)), _p(_f32(sign_out)), OUT_SCALES[mode],
+                                   None if hd is None else _p(hd), _p(inner), _p(suh), _p(svh))
+    _check(rc, "quant_regularize")
+    return inner, suh, svh
+
+
+def quant_rotated_hessian(h, suh) -> np.ndarray:
+    h = _f32(h)
+    out = np.zeros_like(h)
+    _check(lib().ox_quant_rotated_hessian(_p(h), _p(_f32(suh)), h.shape[0], _p(out)), "rotated_hessian")
+    return out
+
+
+def cholesky_lower(a):
+    m = np.ascontiguousarray(a, np.float64).copy()
+    bad = lib().ox_cholesky_lower(_p(m), m.shape[0])
+    return bad, m
+
+
+def quant_ldl_factor(h) -> np.ndarray:
+    h = _f32(h)
+    out = np.zeros_like(h)
+    rc = lib().ox_quant_ldl_factor(_p(h), h.shape[0], _p(out))
+    if rc != 0:
+        raise ValueError("HessianNotPositiveDefinite" if rc == -2 else "GeometryUnsupported")
+    return out
+
+
+def quant_global_scale(inner, n: int, dec: Decode) -> float:
+    x = _f32(inner)
+    g = np.zeros(1, np.float32)
+    _check(lib().ox_quant_global_scale(_p(x), x.shape[0], x.shape[1], n, dec, _p(g)), "global_scale")
+    return float(g[0])
+
+
+def quant_ldlq(inner, l, n: int, dec: Decode):
+    x = _f32(inner)
+    rows, cols = x.shape
+    packed = np.zeros((rows // 16, cols // 16, n), np.uint16)
+    recon = np.zeros_like(x)
+    _check(lib().ox_quant_ldlq(_p(x), _p(_f32(l)), rows, cols, n, dec, _p(packed), _p(recon)), "ldlq")
+    return packed, recon
+
+
+def quant_signs(seed: int, name: str, length: int) -> np.ndarray:
+    out = np.zeros(length, np.float32)
+    lib().ox_quant_signs(seed, name.encode(), length, _p(out))
+    return out
+
+
+def quantize_tensor(w, h, sign_in, sign_out, n: int, dec: Decode, mode: str):
+    """`quantizeTensor` (quantize.zig:600-626): (packed [in/16, out/16, n] u16, suh f16 bits, svh f16 bits, g)."""
+    w = _f32(w)
+    rows, cols = w.shape
+    packed = np.zeros((rows // 16, cols // 16, n), np.uint16)
+    suh = np.zeros(rows, np.uint16)
+    svh = np.zeros(cols, np.uint16)
+    g = np.zeros(1, np.float32)
+    rc = lib().ox_quantize_tensor(_p(w), _p(_f32(h)), rows, cols, _p(_f32(sign_in)), _p(_f32(sign_out)), n, dec,
+                                  OUT_SCALES[mode], _p(packed), _p(suh), _p(svh), _p(g))
+    _check(rc, "quantize_tensor")
+    return packed, suh, svh, float(g[0])

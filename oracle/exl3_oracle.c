@@ -860,3 +860,412 @@ int ox_encode_tile(const float tile[256], uint32_t n, ox_decode dec, uint16_t *p
     free(table); free(costs[0]); free(costs[1]); free(back);
     return 0;
 }
+
+/* ------------------------------------------------------------------------------------------------ */
+/* Quantizer: src/encoder/quantize.zig (regularize, rotatedHessian, ldlFactor, globalScale, ldlq)     */
+
+#define OXQ_HAD 128
+static const float OXQ_SIGMA_REG = 0.025f;
+static const float OXQ_CODEBOOK_SCALE = 1.24371088f;
+
+/* fwht (quantize.zig:33-47) on a strided vector: butterflies, then x * (1/sqrt(128)) in T. */
+static void oxq_fwht_f32(float *v, size_t step) {
+    for (size_t h = 1; h < OXQ_HAD; h *= 2)
+        for (size_t i = 0; i < OXQ_HAD; i += 2 * h)
+            for (size_t j = i; j < i + h; j++) {
+                const float a = v[j * step], b = v[(j + h) * step];
+                v[j * step] = a + b;
+                v[(j + h) * step] = a - b;
+            }
+    const float scale = 1.0f / sqrtf((float)OXQ_HAD);
+    for (size_t k = 0; k < OXQ_HAD; k++) v[k * step] *= scale;
+}
+
+static void oxq_fwht_f64(double *v, size_t step) {
+    for (size_t h = 1; h < OXQ_HAD; h *= 2)
+        for (size_t i = 0; i < OXQ_HAD; i += 2 * h)
+            for (size_t j = i; j < i + h; j++) {
+                const double a = v[j * step], b = v[(j + h) * step];
+                v[j * step] = a + b;
+                v[(j + h) * step] = a - b;
+            }
+    const double scale = 1.0 / sqrt((double)OXQ_HAD);
+    for (size_t k = 0; k < OXQ_HAD; k++) v[k * step] *= scale;
+}
+
+static int oxq_desc(const void *a, const void *b) {
+    const float x = *(const float *)a, y = *(const float *)b;
+    return (x < y) - (x > y);
+}
+
+/* chooseApplyOutScales (quantize.zig:88-116); mode 0 auto, 1 always, 2 never. */
+static int oxq_apply_out_scales(int mode, const float *hdiag, size_t len) {
+    const int forced = mode == 1 ? 1 : mode == 2 ? 0 : -1;
+    if (!hdiag) return forced >= 0 ? forced : 1;
+    double sum = 0;
+    for (size_t i = 0; i < len; i++) sum += hdiag[i] > 0 ? hdiag[i] : 0.0f;
+    const double mean = sum / (double)len;
+    if (!isfinite(mean) || mean < 1e-20) return forced >= 0 ? forced : 0;
+    if (forced >= 0) return forced;
+    float *diag = malloc(len * sizeof(float));
+    const float damp = (float)((double)OXQ_SIGMA_REG * mean);
+    for (size_t i = 0; i < len; i++) diag[i] = sqrtf((hdiag[i] > 0 ? hdiag[i] : 0.0f) + damp);
+    qsort(diag, len, sizeof(float), oxq_desc);
+    const size_t cutoff = len / 50 > 1 ? len / 50 : 1;
+    double top = 0, all = 0;
+    for (size_t i = 0; i < len; i++) {
+        if (i < cutoff) top += diag[i];
+        all += diag[i];
+    }
+    free(diag);
+    return top / all < 0.15;
+}
+
+/* regularize (quantize.zig:129-189): public weight [in][out] -> inner, suh, svh (f32), public =
+ * diag(suh) H_L inner H_R diag(svh).  Returns 0, -1 geometry. */
+int ox_quant_regularize(const float *w, size_t in, size_t out, const float *sign_in, const float *sign_out, int mode,
+                        const float *hdiag, float *inner, float *suh, float *svh) {
+    if (in == 0 || out == 0 || in % OXQ_HAD || out % OXQ_HAD) return -1;
+    memcpy(inner, w, in * out * sizeof(float));
+    memcpy(svh, sign_out, out * sizeof(float));
+    float *os = calloc(out, sizeof(float));
+    int apply = oxq_apply_out_scales(mode, hdiag, in);
+    for (size_t c = 0; c < out; c++) {
+        float total = 0;
+        for (size_t r0 = 0; r0 < in; r0 += 32) {
+            float block = 0;
+            for (size_t r = r0; r < r0 + 32 && r < in; r++) block += inner[r * out + c] * inner[r * out + c];
+            total += block;
+        }
+        os[c] = sqrtf(total / (float)in);
+    }
+    double mean_sum = 0;
+    for (size_t c = 0; c < out; c++) mean_sum += os[c];
+    const double out_mean = mean_sum / (double)out;
+    if (out_mean <= 1e-30) {
+        memset(os, 0, out * sizeof(float));
+        if (mode != 0) apply = 1;
+    } else {
+        const float m = (float)out_mean;
+        for (size_t c = 0; c < out; c++) os[c] /= m;
+    }
+    if (apply)
+        for (size_t c = 0; c < out; c++) svh[c] = svh[c] * (fabsf(os[c]) < 1e-30f ? 0.1f : os[c]) + 1e-10f;
+    for (size_t r = 0; r < in; r++)
+        for (size_t c = 0; c < out; c++) inner[r * out + c] /= svh[c];
+    for (size_t c = 0; c < out; c++)
+        if (fabsf(os[c]) < 1e-30f) svh[c] = 0;
+    for (size_t r = 0; r < in; r++)
+        for (size_t b = 0; b < out; b += OXQ_HAD) oxq_fwht_f32(inner + r * out + b, 1);
+    for (size_t r = 0; r < in; r++) {
+        float total = 0;
+        for (size_t c0 = 0; c0 < out; c0 += 32) {
+            float block = 0;
+            for (size_t c = c0; c < c0 + 32 && c < out; c++) block += inner[r * out + c] * inner[r * out + c];
+            total += block;
+        }
+        float in_scale = sqrtf(total / (float)out);
+        if (fabsf(in_scale) < 1e-30f) in_scale = 0.1f;
+        suh[r] = sign_in[r] * in_scale / -OXQ_CODEBOOK_SCALE + 1e-10f;
+    }
+    for (size_t r = 0; r < in; r++)
+        for (size_t c = 0; c < out; c++) inner[r * out + c] /= suh[r];
+    for (size_t b = 0; b < in; b += OXQ_HAD)
+        for (size_t c = 0; c < out; c++) oxq_fwht_f32(inner + b * out + c, out);
+    free(os);
+    return 0;
+}
+
+/* rotatedHessian (quantize.zig:192-207): H_L diag(suh) H diag(suh) H_L in f64, rounded to f32. */
+int ox_quant_rotated_hessian(const float *h, const float *suh, size_t n, float *out) {
+    if (n == 0 || n % OXQ_HAD) return -1;
+    double *m = malloc(n * n * sizeof(double));
+    for (size_t i = 0; i < n; i++)
+        for (size_t j = 0; j < n; j++) m[i * n + j] = (double)h[i * n + j] * (double)suh[i] * (double)suh[j];
+    for (size_t b = 0; b < n; b += OXQ_HAD)
+        for (size_t c = 0; c < n; c++) oxq_fwht_f64(m + b * n + c, n);
+    for (size_t r = 0; r < n; r++)
+        for (size_t b = 0; b < n; b += OXQ_HAD) oxq_fwht_f64(m + r * n + b, 1);
+    for (size_t i = 0; i < n * n; i++) out[i] = (float)m[i];
+    free(m);
+    return 0;
+}
+
+/* dotRows (quantize.zig:212-223): four f64 lanes over whole quads, reduced lane 0..3 in order, then the tail. */
+static double oxq_dot(const double *a, const double *b, size_t len) {
+    double acc[4] = {0, 0, 0, 0};
+    size_t m = 0;
+    for (; m + 4 <= len; m += 4)
+        for (int l = 0; l < 4; l++) acc[l] += a[m + l] * b[m + l];
+    double sum = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    for (; m < len; m++) sum += a[m] * b[m];
+    return sum;
+}
+
+/* choleskyLower (quantize.zig:225-247): blocked by 64, each block's contribution subtracted in block order. Returns
+ * 0 or the 1-based index of the first pivot that is not positive. */
+size_t ox_cholesky_lower(double *a, size_t n) {
+    for (size_t k = 0; k < n; k += 64) {
+        const size_t kb = n - k < 64 ? n - k : 64;
+        for (size_t j = 0; j < kb; j++) {
+            const size_t jj = k + j;
+            const double d = a[jj * n + jj] - oxq_dot(a + jj * n + k, a + jj * n + k, j);
+            if (!(d > 0)) return jj + 1;
+            const double root = sqrt(d);
+            a[jj * n + jj] = root;
+            for (size_t i = j + 1; i < kb; i++) {
+                const size_t ii = k + i;
+                a[ii * n + jj] = (a[ii * n + jj] - oxq_dot(a + ii * n + k, a + jj * n + k, j)) / root;
+            }
+        }
+        for (size_t i = k + kb; i < n; i++)
+            for (size_t j = 0; j < kb; j++) {
+                const size_t jj = k + j;
+                a[i * n + jj] = (a[i * n + jj] - oxq_dot(a + i * n + k, a + jj * n + k, j)) / a[jj * n + jj];
+            }
+        for (size_t i = k + kb; i < n; i++)
+            for (size_t j = k + kb; j <= i; j++) a[i * n + j] -= oxq_dot(a + i * n + k, a + j * n + k, kb);
+    }
+    return 0;
+}
+
+/* invertLowerBlock (quantize.zig:289-303) on a 16x16 block. */
+static int oxq_invert_lower16(double *blk) {
+    double inv[256] = {0};
+    for (int c = 0; c < 16; c++) {
+        const double d = blk[c * 16 + c];
+        if (d == 0 || !isfinite(d)) return 0;
+        inv[c * 16 + c] = 1.0 / d;
+        for (int r = c + 1; r < 16; r++) {
+            double sum = 0;
+            for (int m = c; m < r; m++) sum += blk[r * 16 + m] * inv[m * 16 + c];
+            inv[r * 16 + c] = -sum / blk[r * 16 + r];
+        }
+    }
+    memcpy(blk, inv, sizeof(inv));
+    return 1;
+}
+
+/* ldlFactor (quantize.zig:305-378): dampDiagonal, Cholesky in f64 (bumping the diagonal on a failed pivot, up to
+ * 10 times), then each 16-column block of the f32 factor times its diagonal block's inverse, diagonal blocks
+ * zeroed.  `h` [n][n] is taken as is (not modified).  Returns 0, -1 geometry, -2 not positive definite. */
+int ox_quant_ldl_factor(const float *h_in, size_t n, float *l) {
+    if (n == 0 || n % 16) return -1;
+    float *h = malloc(n * n * sizeof(float));
+    memcpy(h, h_in, n * n * sizeof(float));
+    double diag_sum = 0;
+    for (size_t i = 0; i < n; i++) {
+        if (h[i * n + i] == 0) h[i * n + i] = 1;
+        diag_sum += h[i * n + i];
+    }
+    const double diag_mean = diag_sum / (double)n;
+    if (diag_mean > 0) {
+        const float damp = (float)((double)OXQ_SIGMA_REG * diag_mean);
+        for (size_t i = 0; i < n; i++) h[i * n + i] += damp;
+    }
+    double damped_sum = 0;
+    for (size_t i = 0; i < n; i++) damped_sum += h[i * n + i];
+    const double damped_mean = damped_sum / (double)n;
+    double *c64 = malloc(n * n * sizeof(double));
+    int rc = 0;
+    for (int retries = 0;; retries++) {
+        for (size_t i = 0; i < n * n; i++) c64[i] = h[i];
+        if (ox_cholesky_lower(c64, n) == 0) break;
+        if (retries + 1 > 10 || damped_mean <= 0) { rc = -2; break; }
+        const float bump = (float)(2.0 * (double)OXQ_SIGMA_REG * damped_mean);
+        for (size_t i = 0; i < n; i++) h[i * n + i] += bump;
+    }
+    if (rc == 0) {
+        float *chol = malloc(n * n * sizeof(float));
+        for (size_t i = 0; i < n; i++)
+            for (size_t j = 0; j < n; j++) chol[i * n + j] = j <= i ? (float)c64[i * n + j] : 0.0f;
+        memcpy(l, chol, n * n * sizeof(float));
+        double blk[256];
+        float inv[256];
+        for (size_t c0 = 0; c0 < n && rc == 0; c0 += 16) {
+            for (int i = 0; i < 16; i++)
+                for (int j = 0; j < 16; j++) blk[i * 16 + j] = j <= i ? chol[(c0 + i) * n + c0 + j] : 0.0;
+            if (!oxq_invert_lower16(blk)) { rc = -2; break; }
+            for (int i = 0; i < 16; i++)
+                for (int j = 0; j < 16; j++) inv[i * 16 + j] = j <= i ? (float)blk[i * 16 + j] : 0.0f;
+            for (size_t r = c0 + 16; r < n; r++) {
+                float row[16];
+                for (int x = 0; x < 16; x++) {
+                    float acc = 0;
+                    for (int m = 0; m < 16; m++) acc += chol[r * n + c0 + m] * inv[m * 16 + x];
+                    row[x] = acc;
+                }
+                memcpy(l + r * n + c0, row, sizeof(row));
+            }
+            for (int i = 0; i < 16; i++) memset(l + (c0 + i) * n + c0, 0, 16 * sizeof(float));
+        }
+        free(chol);
+    }
+    free(c64);
+    free(h);
+    return rc;
+}
+
+/* globalScale (quantize.zig:400-483): golden section over the codebook's bracket, scoring the mean squared error of
+ * a wrapped diagonal of up to 128 sample tiles searched at inner * g and read back at 1/g. */
+int ox_quant_global_scale(const float *inner, size_t rows, size_t cols, uint32_t n, ox_decode dec, float *g_out) {
+    if (rows == 0 || cols == 0 || rows % OXQ_HAD || cols % OXQ_HAD) return -1;
+    const size_t tk = rows / 16, tn = cols / 16;
+    const size_t pair_count = (tk > tn ? tk : tn) * 3;
+    const size_t stride = pair_count / 128 > 1 ? pair_count / 128 : 1;
+    float *tiles = malloc(128 * 256 * sizeof(float));
+    size_t count = 0;
+    for (size_t p = 0; p < pair_count && count < 128; p += stride) {
+        const size_t i = p / 3, wv = p % 3;
+        const size_t r0 = (i % tk) * 16, c0 = ((i + wv) % tn) * 16;
+        for (int r = 0; r < 16; r++) memcpy(tiles + count * 256 + r * 16, inner + (r0 + r) * cols + c0, 16 * sizeof(float));
+        count++;
+    }
+    const double resphi64 = 2.0 - (1.0 + sqrt(5.0)) / 2.0;
+    const float resphi = (float)resphi64;
+    const float lo = dec.codebook == OX_CB_MUL1 ? 0.4f : 0.5f, hi = dec.codebook == OX_CB_MUL1 ? 1.2f : 1.5f;
+    uint16_t packed[128];
+    float scaled[256], recon[256];
+    int rc = 0;
+#define OXQ_SCORE(G, OUT)                                                                          \
+    do {                                                                                           \
+        double sse_ = 0;                                                                           \
+        for (size_t t_ = 0; t_ < count; t_++) {                                                    \
+            double dummy_;                                                                         \
+            for (int v_ = 0; v_ < 256; v_++) scaled[v_] = tiles[t_ * 256 + v_] * (G);             \
+            rc = ox_encode_tile(scaled, n, dec, packed, recon, &dummy_);                           \
+            if (rc) break;                                                                         \
+            for (int v_ = 0; v_ < 256; v_++) {                                                     \
+                const float d_ = recon[v_] / (G) - tiles[t_ * 256 + v_];                           \
+                sse_ += (double)(d_ * d_);                                                         \
+            }                                                                                      \
+        }                                                                                          \
+        (OUT) = sse_ / (double)(count * 256);                                                      \
+    } while (0)
+    float a = lo, b = hi;
+    float x1 = a + resphi * (b - a);
+    float x2 = b - resphi * (b - a);
+    double f1 = 0, f2 = 0;
+    OXQ_SCORE(x1, f1);
+    if (!rc) OXQ_SCORE(x2, f2);
+    double width = (double)hi - (double)lo;
+    size_t steps = 0;
+    while (width > 0.03 && steps < 8) {
+        width *= 1.0 - resphi64;
+        steps++;
+    }
+    for (size_t s = 0; s < steps && !rc; s++) {
+        const int left = f1 < f2;
+        const float a_n = left ? a : x1, b_n = left ? x2 : b;
+        const float probe = left ? a_n + resphi * (b_n - a_n) : b_n - resphi * (b_n - a_n);
+        double fp;
+        OXQ_SCORE(probe, fp);
+        a = a_n;
+        b = b_n;
+        if (left) { x2 = x1; f2 = f1; x1 = probe; f1 = fp; }
+        else { x1 = x2; f1 = f2; x2 = probe; f2 = fp; }
+    }
+#undef OXQ_SCORE
+    free(tiles);
+    if (rc) return rc;
+    *g_out = (a + b) / 2.0f;
+    return 0;
+}
+
+/* ldlq (quantize.zig:485-540): 16-row groups from the bottom, each searched after the error of the rows below it
+ * is fed back through l; 128-row chunks carry the error of finished chunks to every row above in `prod`. */
+int ox_quant_ldlq(const float *inner, const float *l, size_t rows, size_t cols, uint32_t n, ox_decode dec,
+                  uint16_t *packed, float *recon_out) {
+    const size_t out_tiles = cols / 16;
+    float *rec = calloc(rows * cols, sizeof(float));
+    float *prod = calloc(rows * cols, sizeof(float));
+    float *comp = malloc(16 * cols * sizeof(float));
+    float *err = malloc(cols * sizeof(float));
+    int rc = 0;
+    for (size_t j = rows; j > 0 && !rc;) {
+        const size_t i = j > 128 ? j - 128 : 0;
+        const size_t chunk = j - i;
+        for (size_t bj = chunk; bj > 0 && !rc; bj -= 16) {
+            const size_t bi = bj > 16 ? bj - 16 : 0;
+            const size_t height = bj - bi;
+            memcpy(comp, prod + (i + bi) * cols, height * cols * sizeof(float));
+            for (size_t m = bj; m < chunk; m++) {
+                for (size_t c = 0; c < cols; c++) err[c] = inner[(i + m) * cols + c] - rec[(i + m) * cols + c];
+                for (size_t r = 0; r < height; r++) {
+                    const float lv = l[(i + m) * rows + i + bi + r];
+                    for (size_t c = 0; c < cols; c++) comp[r * cols + c] += lv * err[c];
+                }
+            }
+            for (size_t r = 0; r < height; r++)
+                for (size_t c = 0; c < cols; c++) comp[r * cols + c] = inner[(i + bi + r) * cols + c] + comp[r * cols + c];
+            const size_t tk = (i + bi) / 16;
+            for (size_t tn = 0; tn < out_tiles && !rc; tn++) {
+                float tile[256], tile_rec[256];
+                double sse;
+                for (int r = 0; r < 16; r++) memcpy(tile + r * 16, comp + r * cols + tn * 16, 16 * sizeof(float));
+                rc = ox_encode_tile(tile, n, dec, packed + (tk * out_tiles + tn) * n, tile_rec, &sse);
+                for (int r = 0; r < 16; r++)
+                    memcpy(rec + (i + bi + r) * cols + tn * 16, tile_rec + r * 16, 16 * sizeof(float));
+            }
+        }
+        if (i > 0 && !rc)
+            for (size_t m = 0; m < chunk; m++) {
+                for (size_t c = 0; c < cols; c++) err[c] = inner[(i + m) * cols + c] - rec[(i + m) * cols + c];
+                for (size_t r = 0; r < i; r++) {
+                    const float lv = l[(i + m) * rows + r];
+                    for (size_t c = 0; c < cols; c++) prod[r * cols + c] += lv * err[c];
+                }
+            }
+        j = i;
+    }
+    if (recon_out && !rc) memcpy(recon_out, rec, rows * cols * sizeof(float));
+    free(rec); free(prod); free(comp); free(err);
+    return rc;
+}
+
+/* signs (quantize.zig:567-590): splitmix64 seeded by mixing `seed` with each byte of `name`; -1 where bit 0 is set. */
+static uint64_t oxq_splitmix(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void ox_quant_signs(uint64_t seed, const char *name, size_t len, float *out) {
+    uint64_t state = seed;
+    for (const unsigned char *p = (const unsigned char *)name; *p; p++) state = oxq_splitmix(state ^ *p);
+    state = oxq_splitmix(state);
+    for (size_t i = 0; i < len; i++) {
+        state = oxq_splitmix(state);
+        out[i] = (state & 1) == 0 ? 1.0f : -1.0f;
+    }
+}
+
+/* quantizeTensor (quantize.zig:600-626): public weight [in][out] and input Hessian [in][in] -> packed
+ * [in/16][out/16][n], suh [in] and svh [out] as f16 bits, and the global scale g. */
+int ox_quantize_tensor(const float *w, const float *h, size_t in, size_t out, const float *sign_in,
+                       const float *sign_out, uint32_t n, ox_decode dec, int mode, uint16_t *packed, uint16_t *suh16,
+                       uint16_t *svh16, float *g_out) {
+    if (in == 0 || out == 0) return -10;
+    if (in % OXQ_HAD || out % OXQ_HAD) return -11;
+    float *hdiag = malloc(in * sizeof(float));
+    for (size_t i = 0; i < in; i++) hdiag[i] = h[i * in + i];
+    float *inner = malloc(in * out * sizeof(float)), *suh = malloc(in * sizeof(float)), *svh = malloc(out * sizeof(float));
+    float *rot = malloc(in * in * sizeof(float)), *l = malloc(in * in * sizeof(float));
+    int rc = ox_quant_regularize(w, in, out, sign_in, sign_out, mode, hdiag, inner, suh, svh);
+    if (!rc) rc = ox_quant_rotated_hessian(h, suh, in, rot);
+    if (!rc) rc = ox_quant_ldl_factor(rot, in, l);
+    float g = 1.0f;
+    if (!rc) rc = ox_quant_global_scale(inner, in, out, n, dec, &g);
+    if (!rc) {
+        for (size_t i = 0; i < in * out; i++) inner[i] *= g;
+        rc = ox_quant_ldlq(inner, l, in, out, n, dec, packed, NULL);
+    }
+    if (!rc) {
+        for (size_t i = 0; i < in; i++) suh16[i] = ox_f32_to_f16(suh[i] / g);
+        for (size_t i = 0; i < out; i++) svh16[i] = ox_f32_to_f16(svh[i]);
+        *g_out = g;
+    }
+    free(hdiag); free(inner); free(suh); free(svh); free(rot); free(l);
+    return rc;
+}

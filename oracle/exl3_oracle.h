@@ -35,6 +35,11 @@
  *                                   the reference search, 13 codebook x rate x window configs, bit-exact); every
  *                                   packed tile decodes (ox_decode_tile) to the values the search scored; the
  *                                   half-roll warm-up pin reaches the exact tail-biting optimum (encode.zig:396-431).
+ *   ox_quant_* / ox_quantize_tensor : the reference's tensor fixture (exl3_encode_tensor: regularized scales and
+ *                                   inner matrix, and the packed codes, f16 scales and global scale of five whole
+ *                                   tensors, bit-exact codes); the Cholesky factor multiplies back to its matrix and
+ *                                   names the failing pivot; L carries H10 = L10 H00; the decoder's transform chain
+ *                                   turns the regularized inner matrix back into the weight (quantize.zig:683-993).
  */
 #ifndef SUSHI_EXL3_ORACLE_H
 #define SUSHI_EXL3_ORACLE_H
@@ -139,6 +144,20 @@ double ox_exact_tail_biting(const double *x, const uint8_t *ks, size_t steps, co
 void ox_pack_states(uint32_t n, const uint16_t states[256], uint16_t *out);
 int ox_encode_tile(const float tile[256], uint32_t n, ox_decode dec, uint16_t *packed, float recon[256],
                    double *sse_out);
+
+/* Quantizer (src/encoder/quantize.zig); mode 0 auto, 1 always, 2 never (OutScales). */
+int ox_quant_regularize(const float *w, size_t in, size_t out, const float *sign_in, const float *sign_out, int mode,
+                        const float *hdiag, float *inner, float *suh, float *svh);
+int ox_quant_rotated_hessian(const float *h, const float *suh, size_t n, float *out);
+size_t ox_cholesky_lower(double *a, size_t n);
+int ox_quant_ldl_factor(const float *h, size_t n, float *l);
+int ox_quant_global_scale(const float *inner, size_t rows, size_t cols, uint32_t n, ox_decode dec, float *g_out);
+int ox_quant_ldlq(const float *inner, const float *l, size_t rows, size_t cols, uint32_t n, ox_decode dec,
+                  uint16_t *packed, float *recon_out);
+void ox_quant_signs(uint64_t seed, const char *name, size_t len, float *out);
+int ox_quantize_tensor(const float *w, const float *h, size_t in, size_t out, const float *sign_in,
+                       const float *sign_out, uint32_t n, ox_decode dec, int mode, uint16_t *packed, uint16_t *suh16,
+                       uint16_t *svh16, float *g_out);
 void ox_tile_major_inverse(const uint16_t *src, uint16_t *dst, size_t it, size_t ot, size_t n);
 
 #ifdef __cplusplus

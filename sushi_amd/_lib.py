@@ -30,6 +30,8 @@ EXPORTS = (
     "exl3_tile_major",
     "exl3_encode_workspace_size",
     "exl3_encode_tiles",
+    "exl3_quantize_workspace_size",
+    "exl3_quantize_tensor",
 )
 
 
@@ -92,6 +94,9 @@ def load() -> ctypes.CDLL:
     L.exl3_encode_workspace_size.restype = sz
     L.exl3_encode_workspace_size.argtypes = [i32, DecodeT, ctypes.c_int64]
     L.exl3_encode_tiles.argtypes = [vp, ctypes.c_int64, i32, DecodeT, vp, vp, vp, sz, vp]
+    L.exl3_quantize_workspace_size.restype = sz
+    L.exl3_quantize_workspace_size.argtypes = [i32, i32, i32, DecodeT]
+    L.exl3_quantize_tensor.argtypes = [vp, vp, i32, i32, vp, vp, i32, DecodeT, i32, vp, vp, vp, vp, vp, sz, vp]
     for name in EXPORTS:
         if name in ("exl3_abi_version", "exl3_last_error") or name.endswith("workspace_size"):
             continue

@@ -29,6 +29,7 @@ SOURCES = [
     "exl3_gemv_pair.hip",
     "exl3_gemv_3inst.hip",
     "exl3_encode.hip",
+    "exl3_quantize.hip",
 ]
 
 CFLAGS = [

@@ -770,6 +770,25 @@ int32_t encode_plan(int32_t n, const exl3_decode_t &dec, int64_t count, EncodePl
     return ok();
 }
 
+EncodeTuning tuning_of(const EncodePlan &p) { return EncodeTuning{p.stride, p.tiles_per_wg, p.grid_max, p.per_wg}; }
+
+// quantizeTensor's admission (quantize.zig:118-127, :600-606) and the two search shapes it launches.
+int32_t quantize_plan(int32_t in, int32_t out, int32_t n, const exl3_decode_t &dec, int32_t mode, EncodeTuning *tg,
+                      EncodeTuning *tr) {
+    if (in <= 0 || out <= 0) return fail(EXL3_ERR_BAD_SHAPE, "quantize: empty tensor %dx%d", in, out);
+    if (in % 128 || out % 128)
+        return fail(EXL3_ERR_BAD_SHAPE, "quantize: %dx%d is off the 128 grid (GeometryUnsupported)", in, out);
+    if (mode < 0 || mode > 2) return fail(EXL3_ERR_BAD_SHAPE, "quantize: out_scales mode %d (0 auto, 1 always, 2 never)", mode);
+    EncodePlan pg, pr;
+    int32_t rc = encode_plan(n, dec, 128, &pg);
+    if (rc) return rc;
+    rc = encode_plan(n, dec, out / 16, &pr);
+    if (rc) return rc;
+    *tg = tuning_of(pg);
+    *tr = tuning_of(pr);
+    return ok();
+}
+
 }  // namespace
 
 size_t exl3_encode_workspace_size(int32_t n, exl3_decode_t dec, int64_t count) {
@@ -801,11 +820,64 @@ int32_t exl3_encode_tiles(const float *tiles, int64_t count, int32_t n, exl3_dec
     a.k = k;
     a.packed = packed;
     a.sse = sse;
+    a.recon = nullptr;
     a.back = static_cast<uint8_t *>(workspace);
     a.stride = p.stride;
     a.tiles_per_wg = p.tiles_per_wg;
     a.grid = (int)((size_t)p.grid_max < fit ? (size_t)p.grid_max : fit);
     return launched(run_encode(fam, a, stream), "exl3_encode_tiles");
+}
+
+size_t exl3_quantize_workspace_size(int32_t in, int32_t out, int32_t n, exl3_decode_t dec) {
+    EncodeTuning tg, tr;
+    if (quantize_plan(in, out, n, dec, 0, &tg, &tr) != EXL3_OK) return 0;
+    return quantize_workspace_bytes(in, out, tg, tr);
+}
+
+int32_t exl3_quantize_tensor(const float *w, const float *h, int32_t in, int32_t out, const float *sign_in,
+                             const float *sign_out, int32_t n, exl3_decode_t dec, int32_t out_scales, uint16_t *packed,
+                             uint16_t *suh, uint16_t *svh, float *g, void *workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+    EncodeTuning tg, tr;
+    int32_t rc = quantize_plan(in, out, n, dec, out_scales, &tg, &tr);
+    if (rc) return rc;
+    if (!w || !h || !sign_in || !sign_out || !packed || !suh || !svh || !g)
+        return fail(EXL3_ERR_BAD_SHAPE, "quantize: null operand");
+    if (!workspace || workspace_bytes < quantize_workspace_bytes(in, out, tg, tr))
+        return fail(EXL3_ERR_WORKSPACE, "quantize: workspace of %zu bytes, %zu needed", workspace_bytes,
+                    quantize_workspace_bytes(in, out, tg, tr));
+    int fam;
+    DecodeK k;
+    rc = resolve_decode(dec, n, &fam, &k);
+    if (rc) return rc;
+    QuantArgs q{};
+    q.w = w;
+    q.h = h;
+    q.sign_in = sign_in;
+    q.sign_out = sign_out;
+    q.in = in;
+    q.out = out;
+    q.n = n;
+    q.w_bits = dec.window_bits;
+    q.mode = out_scales;
+    q.fam = fam;
+    q.k = k;
+    q.tune_g = tg;
+    q.tune_rows = tr;
+    q.packed = packed;
+    q.suh = suh;
+    q.svh = svh;
+    q.g = g;
+    q.workspace = workspace;
+    q.workspace_bytes = workspace_bytes;
+    q.stream = stream;
+    std::string msg;
+    switch (quantize_tensor(q, &msg)) {
+    case QUANT_OK: return ok();
+    case QUANT_HESSIAN: return fail(EXL3_ERR_HESSIAN, "quantize: %s (HessianNotPositiveDefinite)", msg.c_str());
+    case QUANT_WORKSPACE: return fail(EXL3_ERR_WORKSPACE, "quantize: %s", msg.c_str());
+    default: return fail(EXL3_ERR_LAUNCH, "quantize: %s", msg.c_str());
+    }
 }
 
 }  // extern "C"

@@ -92,6 +92,7 @@ __global__ __launch_bounds__(ENC_THREADS) void encode_search_kernel(const float 
                                                                     int n, int w, DecodeK dk,
                                                                     uint16_t *__restrict__ packed,
                                                                     double *__restrict__ sse,
+                                                                    float *__restrict__ recon,
                                                                     uint8_t *__restrict__ back_ws, int stride) {
     extern __shared__ __align__(16) unsigned char enc_lds[];
     // LDS: cost rows [T][2][stride] u16, then x [T][256] f32, paths [T][256] u16, packed words [T][64] u32,
@@ -202,6 +203,13 @@ __global__ __launch_bounds__(ENC_THREADS) void encode_search_kernel(const float 
                 packed[(tile0 + t) * n + 2 * j + 1] = (uint16_t)(v >> 16);
             }
         }
+        // The values the decoder will produce, back in row-major tile order.
+        if (recon != nullptr)
+            for (int i = tid; i < T * 256; i += ENC_THREADS) {
+                const int t = i >> 8, j = i & 255;
+                if (tile0 + t < count)
+                    recon[(tile0 + t) * 256 + tensor_core_perm(j)] = __half2float(decode1<FAM>(path[i], dk));
+            }
         // The path's squared error in f64, summed in trellis order as the reference does.
         if (sse != nullptr && tid < T && tile0 + tid < count) {
             double acc = 0.0;
@@ -224,7 +232,7 @@ hipError_t launch_encode(const EncodeArgs &a, hipStream_t s) {
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL((encode_search_kernel<FAM, T>), dim3((unsigned)a.grid), dim3(ENC_THREADS), lds, s, a.tiles,
-                       a.count, a.n, a.w, a.k, a.packed, a.sse, a.back, a.stride);
+                       a.count, a.n, a.w, a.k, a.packed, a.sse, a.recon, a.back, a.stride);
     return hipGetLastError();
 }
 

@@ -1,6 +1,8 @@
 // Internal launch interface between the C-ABI layer (exl3_capi.hip) and the kernel translation units.
 #pragma once
 
+#include <string>
+
 #include "exl3_common.cuh"
 
 namespace exl3 {
@@ -182,6 +184,7 @@ struct EncodeArgs {
     DecodeK k;
     uint16_t *packed;
     double *sse;
+    float *recon;   // optional: the decoded values of each tile's path, row-major [count][256]
     uint8_t *back;
     int stride;
     int tiles_per_wg;
@@ -189,5 +192,36 @@ struct EncodeArgs {
 };
 size_t encode_lds_bytes(int tiles_per_wg, int stride);
 hipError_t run_encode(int fam, const EncodeArgs &a, hipStream_t s);
+
+// A search launch's shape for a tile count: backpointer stride, tiles per workgroup, the grid that fills the GPU
+// (grid_cap) and the backpointer bytes of one workgroup.
+struct EncodeTuning {
+    int stride;
+    int tiles_per_wg;
+    int grid_cap;
+    size_t per_wg;
+};
+
+// Whole-tensor quantizer (src/encoder/quantize.zig:600-626): host pointers in and out, a device workspace.
+enum QuantStatus : int { QUANT_OK = 0, QUANT_LAUNCH = 1, QUANT_WORKSPACE = 2, QUANT_HESSIAN = 3 };
+struct QuantArgs {
+    const float *w;         // [in][out]
+    const float *h;         // [in][in]
+    const float *sign_in;   // [in]
+    const float *sign_out;  // [out]
+    int in, out, n, w_bits, mode, fam;
+    DecodeK k;
+    EncodeTuning tune_g;     // the global scale's sample tiles (up to 128)
+    EncodeTuning tune_rows;  // one 16-row group's out/16 tiles
+    uint16_t *packed;        // [in/16][out/16][n]
+    uint16_t *suh;           // [in] f16 bits
+    uint16_t *svh;           // [out] f16 bits
+    float *g;
+    void *workspace;
+    size_t workspace_bytes;
+    hipStream_t stream;
+};
+size_t quantize_workspace_bytes(int in, int out, const EncodeTuning &tune_g, const EncodeTuning &tune_rows);
+int quantize_tensor(const QuantArgs &q, std::string *msg);
 
 }  // namespace exl3

@@ -87,6 +87,10 @@ class WindowTooNarrow(Exl3Error):
     status = -14
 
 
+class HessianNotPositiveDefinite(Exl3Error):
+    status = -15
+
+
 _BY_STATUS = {c.status: c for c in Exl3Error.__subclasses__()}
 
 
@@ -662,3 +666,65 @@ def encode_tiles(tiles: torch.Tensor, n: int, dec: Decode, with_sse: bool = True
     _check(L.exl3_encode_tiles(t.data_ptr(), count, n, dec.c(), packed.data_ptr(),
                                0 if sse is None else sse.data_ptr(), ws.data_ptr(), ws.numel(), _stream(t.device)))
     return packed.reshape(*lead, n), (None if sse is None else sse.reshape(lead))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Quantizer (src/encoder/quantize.zig)
+
+OUT_SCALES = {"auto": 0, "always": 1, "never": 2}
+_M64 = (1 << 64) - 1
+
+
+def _splitmix(x: int) -> int:
+    z = (x + 0x9E3779B97F4A7C15) & _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def signs(seed: int, name: str, length: int):
+    """`signs` (quantize.zig:567-583): a +-1 f32 vector, a pure function of (seed, name, length): splitmix64 seeded by
+    mixing `seed` with every byte of `name`, -1 where bit 0 of the i-th output is set."""
+    import numpy as np
+
+    state = seed & _M64
+    for b in name.encode():
+        state = _splitmix(state ^ b)
+    state = _splitmix(state)
+    out = np.empty(length, np.float32)
+    for i in range(length):
+        state = _splitmix(state)
+        out[i] = -1.0 if state & 1 else 1.0
+    return out
+
+
+def quantize_tensor(w, h, sign_in, sign_out, n: int, dec: Decode, out_scales: str = "auto", device="cuda"):
+    """`quantizeTensor` (quantize.zig:600-626) on the GPU: public weight w [in, out] and input Hessian h [in, in] (host
+    arrays) -> (packed [in/16, out/16, n] u16, suh [in] and svh [out] as f16 bits, global scale g)."""
+    import numpy as np
+
+    w = np.ascontiguousarray(w, np.float32)
+    h = np.ascontiguousarray(h, np.float32)
+    si = np.ascontiguousarray(sign_in, np.float32)
+    so = np.ascontiguousarray(sign_out, np.float32)
+    if w.ndim != 2 or h.shape != (w.shape[0], w.shape[0]) or si.shape != (w.shape[0],) or so.shape != (w.shape[1],):
+        raise BadExl3Shape(f"w {w.shape}, h {h.shape}, signs {si.shape} / {so.shape}")
+    rows, cols = w.shape
+    L = _lib.load()
+    dev = torch.device(device)
+    ws_bytes = L.exl3_quantize_workspace_size(rows, cols, n, dec.c())
+    packed = np.zeros((max(rows // 16, 0), max(cols // 16, 0), n), np.uint16)
+    suh = np.zeros(rows, np.uint16)
+    svh = np.zeros(cols, np.uint16)
+    g = np.zeros(1, np.float32)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    _check(L.exl3_quantize_tensor(p(w), p(h), rows, cols, p(si), p(so), n, dec.c(), OUT_SCALES[out_scales], p(packed),
+                                  p(suh), p(svh), p(g), ws.data_ptr(), ws.numel(), _stream(dev)))
+    return packed, suh, svh, float(g[0])
+
+
+def quantize_named(w, h, seed: int, name: str, n: int, dec: Decode, out_scales: str = "auto", device="cuda"):
+    """`quantizeNamed` (quantize.zig:592-598): `quantize_tensor` with the sign vectors of (seed, name)."""
+    both = signs(seed, name, w.shape[0] + w.shape[1])
+    return quantize_tensor(w, h, both[:w.shape[0]], both[w.shape[0]:], n, dec, out_scales, device)
