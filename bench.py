@@ -258,6 +258,35 @@ def bench_encode(cb_name: str, n: int, w: int, tiles: int, replays: int = 2):
             "weights_per_s": round(256 * tiles / (us * 1e-6))}
 
 
+def bench_quantize(in_f: int, out_f: int, n: int, cb_name: str, w: int):
+    """The whole-tensor quantizer (exl3.quantize_named) on a random weight [in, out] with a random SPD Hessian: wall
+    seconds per tensor (host factor + GPU searches), and the decoded weight's relative error."""
+    import numpy as np
+    import torch
+
+    from sushi_amd import exl3
+
+    rng = np.random.default_rng(in_f + out_f)
+    wt = (rng.standard_normal((in_f, out_f)) * 0.02).astype(np.float32)
+    x = (rng.standard_normal((in_f, 256)) * 0.1).astype(np.float32)
+    h = (x @ x.T).astype(np.float32)
+    h[np.arange(in_f), np.arange(in_f)] += 0.01
+    dec = exl3.Decode(exl3.Codebook.from_name(cb_name), exl3.Window(w))
+    torch.cuda.synchronize()
+    t0 = time.time()
+    packed, suh, svh, g = exl3.quantize_named(wt, h, 1, f"bench.{in_f}x{out_f}", n, dec, "auto")
+    secs = time.time() - t0
+    dev = torch.device("cuda:0")
+    proj = exl3.Proj(torch.from_numpy(packed.view(np.int16)).reshape(1, in_f // 16, out_f // 16, n).to(dev),
+                     torch.from_numpy(suh.view(np.float16)).reshape(1, in_f).to(dev),
+                     torch.from_numpy(svh.view(np.float16)).reshape(1, out_f).to(dev))
+    dense = exl3.linear(torch.eye(in_f, dtype=torch.float16, device=dev), proj, dec).float().cpu().numpy()
+    rel = float(np.linalg.norm(dense - wt) / np.linalg.norm(wt))
+    return {"config": "quantize", "codebook": cb_name, "K": n / 16, "window": w, "in": in_f, "out": out_f,
+            "seconds": round(secs, 3), "tiles_per_s": round(in_f * out_f / 256 / secs), "g": round(g, 5),
+            "decoded_rel_err": round(rel, 4)}
+
+
 def sweep(which: str):
     """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
     one JSON line per case."""
@@ -278,6 +307,8 @@ def sweep(which: str):
         for cb_name, n, w, tiles in (("mcg", 32, 12, 65536), ("mcg", 40, 15, 8192), ("mcg", 64, 16, 4096),
                                      ("mul1", 48, 15, 8192), ("mcg", 32, 16, 2048)):
             print(json.dumps(bench_encode(cb_name, n, w, tiles)), flush=True)
+        for in_f, out_f, n, cb_name, w in ((2048, 768, 32, "mcg", 15), (4096, 4096, 32, "mcg", 12)):
+            print(json.dumps(bench_quantize(in_f, out_f, n, cb_name, w)), flush=True)
     for cfg, in_f, out_f, n, rows, dec, name in cases:
         us, copies = _time_linear(in_f, out_f, n, rows, dec, name, 1 if cfg == "c2" else 2)
         alg = _algorithmic_bytes(in_f, out_f, n, rows)

@@ -760,6 +760,9 @@ int32_t encode_plan(int32_t n, const exl3_decode_t &dec, int64_t count, EncodePl
     p->tiles_per_wg = 1;
     for (int t = 16; t >= 2; t >>= 1)
         if (encode_lds_bytes(t, p->stride) <= 78 * 1024) { p->tiles_per_wg = t; break; }
+    // A small batch (the quantizer's 16-row groups, the global scale's samples) spreads over the CUs first: fewer
+    // tiles per workgroup until there is a workgroup per CU.
+    while (p->tiles_per_wg > 1 && (count + p->tiles_per_wg - 1) / p->tiles_per_wg < 256) p->tiles_per_wg >>= 1;
     const size_t lds = encode_lds_bytes(p->tiles_per_wg, p->stride);
     int per_cu = (int)((160 * 1024) / lds);
     per_cu = per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu;

@@ -86,6 +86,45 @@ void fwht(T *v, size_t step) {
     for (size_t k = 0; k < HAD; k++) v[k * step] *= scale;
 }
 
+// f(i) for i in [lo, hi), interleaved over up to 16 host threads when there are at least min_count of them.
+template <typename F>
+void parallel_rows(size_t lo, size_t hi, F &&f, size_t min_count = 64);
+
+// hadamardRows (quantize.zig:52-73): the FWHT down every column of each 128-row block, run as butterflies on whole
+// rows so the inner loops are contiguous (each element sees the column transform's adds, subtracts and scale);
+// column ranges go to host threads.
+template <typename T>
+void hadamard_down(T *m, size_t rows, size_t cols) {
+    const size_t span = 256;
+    parallel_rows(0, (cols + span - 1) / span, [&](size_t piece) {
+        const size_t c0 = piece * span, c1 = std::min(cols, c0 + span);
+        const T scale = T(1) / std::sqrt(T(HAD));
+        for (size_t b = 0; b < rows; b += HAD) {
+            T *blk = m + b * cols;
+            for (size_t h = 1; h < HAD; h *= 2)
+                for (size_t i = 0; i < HAD; i += 2 * h)
+                    for (size_t j = i; j < i + h; j++) {
+                        T *x = blk + j * cols, *y = blk + (j + h) * cols;
+                        for (size_t c = c0; c < c1; c++) {
+                            const T a = x[c], d = y[c];
+                            x[c] = a + d;
+                            y[c] = a - d;
+                        }
+                    }
+            for (size_t r = 0; r < HAD; r++)
+                for (size_t c = c0; c < c1; c++) blk[r * cols + c] *= scale;
+        }
+    }, 1);
+}
+
+// hadamardCols (quantize.zig:75-85): the FWHT along each row's 128-column blocks, rows over host threads.
+template <typename T>
+void hadamard_along(T *m, size_t rows, size_t cols) {
+    parallel_rows(0, rows, [&](size_t r) {
+        for (size_t b = 0; b < cols; b += HAD) fwht<T>(m + r * cols + b, 1);
+    });
+}
+
 // chooseApplyOutScales (quantize.zig:88-116); mode 0 auto, 1 always, 2 never.
 bool apply_out_scales(int mode, const std::vector<float> &hdiag) {
     const int forced = mode == 1 ? 1 : mode == 2 ? 0 : -1;
@@ -116,14 +155,15 @@ void regularize(const float *w, size_t in, size_t out, const float *sign_in, con
     suh.assign(in, 0.0f);
     std::vector<float> os(out, 0.0f);
     bool apply = apply_out_scales(mode, hdiag);
-    for (size_t c = 0; c < out; c++) {
-        float total = 0;
+    {
+        std::vector<float> total(out, 0.0f), block(out);
         for (size_t r0 = 0; r0 < in; r0 += 32) {
-            float block = 0;
-            for (size_t r = r0; r < std::min(r0 + 32, in); r++) block += inner[r * out + c] * inner[r * out + c];
-            total += block;
+            std::fill(block.begin(), block.end(), 0.0f);
+            for (size_t r = r0; r < std::min(r0 + 32, in); r++)
+                for (size_t c = 0; c < out; c++) block[c] += inner[r * out + c] * inner[r * out + c];
+            for (size_t c = 0; c < out; c++) total[c] += block[c];
         }
-        os[c] = std::sqrt(total / (float)in);
+        for (size_t c = 0; c < out; c++) os[c] = std::sqrt(total[c] / (float)in);
     }
     double mean_sum = 0;
     for (float v : os) mean_sum += v;
@@ -141,8 +181,7 @@ void regularize(const float *w, size_t in, size_t out, const float *sign_in, con
         for (size_t c = 0; c < out; c++) inner[r * out + c] /= svh[c];
     for (size_t c = 0; c < out; c++)
         if (std::fabs(os[c]) < 1e-30f) svh[c] = 0;
-    for (size_t r = 0; r < in; r++)
-        for (size_t b = 0; b < out; b += HAD) fwht<float>(inner.data() + r * out + b, 1);
+    hadamard_along<float>(inner.data(), in, out);
     for (size_t r = 0; r < in; r++) {
         float total = 0;
         for (size_t c0 = 0; c0 < out; c0 += 32) {
@@ -156,8 +195,7 @@ void regularize(const float *w, size_t in, size_t out, const float *sign_in, con
     }
     for (size_t r = 0; r < in; r++)
         for (size_t c = 0; c < out; c++) inner[r * out + c] /= suh[r];
-    for (size_t b = 0; b < in; b += HAD)
-        for (size_t c = 0; c < out; c++) fwht<float>(inner.data() + b * out + c, out);
+    hadamard_down<float>(inner.data(), in, out);
 }
 
 // rotatedHessian (quantize.zig:192-207).
@@ -165,10 +203,8 @@ void rotated_hessian(const float *h, const std::vector<float> &suh, size_t n, st
     std::vector<double> m(n * n);
     for (size_t i = 0; i < n; i++)
         for (size_t j = 0; j < n; j++) m[i * n + j] = (double)h[i * n + j] * (double)suh[i] * (double)suh[j];
-    for (size_t b = 0; b < n; b += HAD)
-        for (size_t c = 0; c < n; c++) fwht<double>(m.data() + b * n + c, n);
-    for (size_t r = 0; r < n; r++)
-        for (size_t b = 0; b < n; b += HAD) fwht<double>(m.data() + r * n + b, 1);
+    hadamard_down<double>(m.data(), n, n);
+    hadamard_along<double>(m.data(), n, n);
     out.resize(n * n);
     for (size_t i = 0; i < n * n; i++) out[i] = (float)m[i];
 }
@@ -189,10 +225,10 @@ inline double dot_rows(const double *a, const double *b, size_t len) {
 }
 
 template <typename F>
-void parallel_rows(size_t lo, size_t hi, F &&f) {
+void parallel_rows(size_t lo, size_t hi, F &&f, size_t min_count) {
     const size_t count = hi > lo ? hi - lo : 0;
     unsigned threads = std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
-    if (count < 64 || threads == 1) {
+    if (count < min_count || count < 2 || threads == 1) {
         for (size_t i = lo; i < hi; i++) f(i);
         return;
     }
