@@ -253,9 +253,20 @@ def bench_encode(cb_name: str, n: int, w: int, tiles: int, replays: int = 2):
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / replays
+    # The reference's CPU search (the single-threaded C port of Encoder.encodeTile) on a few of the same tiles.
+    import oracle as O
+
+    sample = x[:4].cpu().numpy()
+    cb = {"mcg": O.CB_MCG, "mul1": O.CB_MUL1, "3inst": O.CB_3INST}[cb_name]
+    t0 = time.perf_counter()
+    for tile in sample:
+        O.encode_tile(tile, n, O.decode(cb, w))
+    cpu_us = (time.perf_counter() - t0) / len(sample) * 1e6
     return {"config": "encode", "codebook": cb_name, "K": n / 16, "window": w, "tiles": tiles,
             "us_per_call": round(us, 1), "us_per_tile": round(us / tiles, 3), "tiles_per_s": round(tiles / (us * 1e-6)),
-            "weights_per_s": round(256 * tiles / (us * 1e-6))}
+            "weights_per_s": round(256 * tiles / (us * 1e-6)),
+            "cpu_baseline": {"us_per_tile": round(cpu_us, 1), "cores": 1, "kind": "port",
+                             "sample": f"{len(sample)} of the same tiles through the C port of encodeTile"}}
 
 
 def bench_quantize(in_f: int, out_f: int, n: int, cb_name: str, w: int):
