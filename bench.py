@@ -298,6 +298,66 @@ def bench_quantize(in_f: int, out_f: int, n: int, cb_name: str, w: int):
             "decoded_rel_err": round(rel, 4)}
 
 
+def bench_pack(pair_major: bool, experts: int = 256, hidden: int = 2048, inter: int = 768, n: int = 32):
+    """The pack loader on one C4-shaped routed layer (E=256, hidden 2048, inter 768, K2: 302 MB of trellis) written as
+    a safetensors pack under a temporary directory: seconds from Pack() to the device bank (page cache warm: the
+    shard was just written; after one untimed load), against reading the same shard bytes and copying them to the
+    device raw."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from sushi_amd import pack as P
+
+    root = tempfile.mkdtemp(prefix="exl3pack")
+    try:
+        rng = np.random.default_rng(1)
+        tensors = {}
+        for g in range(2):  # two rate groups of experts / 2 each (pair-major packs are rate-grouped)
+            e = experts // 2
+            for proj in P.PROJECTIONS:
+                inp, out = (inter, hidden) if proj == "down_proj" else (hidden, inter)
+                tr = rng.integers(0, 1 << 16, size=(e, inp // 16, out // 16, n), dtype=np.uint16)
+                key = f"model.layers.0.mlp.switch_mlp.{proj}.g{g}"
+                if pair_major:
+                    tr = tr.reshape(e, inp // 16, out // 32, 2, n).transpose(0, 2, 1, 3, 4).copy()
+                    tensors[key + ".trellis_pm"] = tr
+                else:
+                    tensors[key + ".trellis"] = tr
+                tensors[key + ".suh"] = np.ones((e, inp), np.float16)
+                tensors[key + ".svh"] = np.ones((e, out), np.float16)
+        eq = {"format": "exl3", "k": n / 16, "codebook": "mcg"}
+        if pair_major:
+            eq["tile_order"] = "pair_major"
+        with open(os.path.join(root, "config.json"), "w") as f:
+            json.dump({"hidden_size": hidden, "moe_intermediate_size": inter, "num_experts_per_tok": 8,
+                       "expert_quant": eq}, f)
+        P.write_shard(os.path.join(root, P.SINGLE_FILE), tensors, {"tile_order": "pair_major"} if pair_major else {})
+        nbytes = sum(a.nbytes for a in tensors.values())
+        del tensors
+        dev = torch.device("cuda:0")
+        del P.Pack(root).moe_layer(0, device=dev).meta  # untimed: library load and first-use set-up
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pk = P.Pack(root)
+        layer = pk.moe_layer(0, device=dev)
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t0
+        del layer
+        t0 = time.perf_counter()
+        raw = np.fromfile(os.path.join(root, P.SINGLE_FILE), dtype=np.uint8)
+        torch.from_numpy(raw).to(dev)
+        torch.cuda.synchronize()
+        raw_secs = time.perf_counter() - t0
+        return {"config": "pack_load", "tile_order": "pair_major" if pair_major else "pack", "bytes": nbytes,
+                "seconds": round(secs, 3), "GBps": round(nbytes / secs / 1e9, 2),
+                "raw_read_copy_GBps": round(raw.nbytes / raw_secs / 1e9, 2)}
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 def sweep(which: str):
     """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
     one JSON line per case."""
@@ -314,6 +374,9 @@ def sweep(which: str):
             cases.append(("c3", 4096, 14336, 48, rows, exl3.INST3, "3inst"))
     if which in ("c5", "all"):
         print(json.dumps(bench_moe_c5()), flush=True)
+    if which in ("pack", "all"):
+        for pm in (False, True):
+            print(json.dumps(bench_pack(pm)), flush=True)
     if which in ("enc", "all"):
         for cb_name, n, w, tiles in (("mcg", 32, 12, 65536), ("mcg", 40, 15, 8192), ("mcg", 64, 16, 4096),
                                      ("mul1", 48, 15, 8192), ("mcg", 32, 16, 2048)):
@@ -453,7 +516,7 @@ def main() -> int:
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
-    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "enc", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
+    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     args = ap.parse_args()
     if args.sweep:
         global SWEEP_GRAPHS
