@@ -236,12 +236,15 @@ struct MoePlan {
     size_t total() const { return kZeroBytes + 2 * gu_bytes + down_bytes + table_bytes; }
 };
 
-MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
+// `extra`: token rows of a fused shared expert, whose planes follow the slots' (and whose groups of SH_ROWS rows join
+// the grid).
+MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0) {
     MoePlan p;
     p.windowed = windowed;
     // Window count lies between ceil(nslots / MOE_WINDOW_ROWS) and nslots; splits are planned for the fewest windows
     // (the most splits), so the planes fit whatever the routing turns out to be.
-    const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS : nslots;
+    const int groups = windowed ? (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS + (extra + SH_ROWS - 1) / SH_ROWS
+                                : nslots + extra;
     const int rows = windowed ? MOE_WINDOW_ROWS : 1;
     // Per-slot arm: at least 1.5 workgroups per CU and at most four batches of TPW tiles per wave (measured at C4's
     // shape, b = 1 and 8: the best of every split pair tried).  Sorted arm: up to eight batches (each window's
@@ -257,8 +260,8 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed) {
     const int f1 = env_int("EXL3_MOE_SPLITS1", 0), f2 = env_int("EXL3_MOE_SPLITS2", 0);
     if (f1 > 0 && (hidden / 128) % f1 == 0) p.s1 = f1;
     if (f2 > 0 && (inter / 128) % f2 == 0) p.s2 = f2;
-    p.gu_bytes = align_up((size_t)nslots * p.s1 * inter * sizeof(float));
-    p.down_bytes = align_up((size_t)nslots * p.s2 * hidden * sizeof(float));
+    p.gu_bytes = align_up((size_t)(nslots + extra) * p.s1 * inter * sizeof(float));
+    p.down_bytes = align_up((size_t)(nslots + extra) * p.s2 * hidden * sizeof(float));
     p.table_bytes = windowed ? align_up(sizeof(uint32_t)) + 2 * align_up((size_t)nslots * sizeof(uint32_t)) +
                                    align_up((size_t)nslots * MOE_WINDOW_ROWS * sizeof(uint32_t))
                              : 0;
@@ -297,10 +300,12 @@ struct SharedBank {
 // The shared bank's rows need the per-slot arm, a 16-bit output dtype (the combine word holds both rounded sums),
 // the routed and shared folds (routed, shared and combine words: three per output), and, for a uniform bank, the
 // routed rate.
-bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype) {
+bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts) {
     const int nslots = rows * topk;
-    if (rows > moe_decode_rows_max() || y_dtype == EXL3_DT_F32) return false;
-    const MoePlan p = plan_moe(nslots + rows, hidden, inter, false);
+    if (y_dtype == EXL3_DT_F32) return false;
+    const bool windowed = rows > moe_decode_rows_max();
+    if (windowed && !(moe_windows_enabled() && moe_windowed(rows, nslots, experts))) return false;
+    const MoePlan p = plan_moe(nslots, hidden, inter, windowed, rows);
     return topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)3 * rows * hidden <= kFoldWords;
 }
 
@@ -312,12 +317,11 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
                    const SharedBank *sb = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    // With a fused shared bank its rows follow the slots as groups of SH_ROWS rows; planes are kept per row (slots
-    // nslots .. nslots + rows - 1), so the plan counts nslots + rows.
-    const int ngroups = sb ? nslots + rows : nslots;
-    const int grid_groups = sb ? nslots + (rows + SH_ROWS - 1) / SH_ROWS : nslots;
-    MoePlan p = sb ? plan_moe(ngroups, hidden, inter, false)
-                   : plan_moe(nslots, hidden, inter, moe_windows_enabled() && moe_windowed(rows, nslots, experts));
+    // With a fused shared bank its rows join either arm as groups of SH_ROWS rows placed first in the grid; planes
+    // are kept per row (slots nslots .. nslots + rows - 1), so the plan counts rows more.
+    const int sh_groups = sb ? (rows + SH_ROWS - 1) / SH_ROWS : 0;
+    MoePlan p = plan_moe(nslots, hidden, inter, moe_windows_enabled() && moe_windowed(rows, nslots, experts),
+                         sb ? rows : 0);
     const size_t need = p.total();
     if (ws_bytes < need || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
         return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
@@ -328,7 +332,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     const float scale = out_scale_of(fam);
     // 0) sorted arm: group the slots into expert windows
     uint32_t *win_count = nullptr, *win_expert = nullptr, *win_rows = nullptr, *win_slots = nullptr;
-    int groups = grid_groups, grows = 1;
+    int groups = nslots + sh_groups, grows = 1;
     if (p.windowed) {
         char *t = w + 2 * p.gu_bytes + p.down_bytes;
         win_count = reinterpret_cast<uint32_t *>(t);
@@ -340,7 +344,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         win_slots = reinterpret_cast<uint32_t *>(t);
         hipError_t e = run_moe_windows(inds, nslots, experts, win_count, win_expert, win_rows, win_slots, stream);
         if (e != hipSuccess) return launched(e, "exl3_moe (windows)");
-        groups = std::min(nslots, experts + (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS);
+        groups = std::min(nslots, experts + (nslots + MOE_WINDOW_ROWS - 1) / MOE_WINDOW_ROWS) + sh_groups;
         grows = MOE_WINDOW_ROWS;
     }
 
@@ -378,7 +382,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     a.fused_finish = 0;
     a.partial_only = 1;
     if (sb) {
-        a.sh_groups = grid_groups - nslots;
+        a.sh_groups = sh_groups;
         a.sh_from = nslots;
         a.sh_rows = rows;
         a.sh_n = sb->n;
@@ -444,7 +448,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         d.y_dtype = y_dtype;
     }
     if (sb) {  // moe_shared_fusable checked that the three word sets fit the zeroed region
-        d.sh_groups = grid_groups - nslots;
+        d.sh_groups = sh_groups;
         d.sh_from = nslots;
         d.sh_rows = rows;
         d.sh_n = sb->n;
@@ -637,7 +641,9 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
     const size_t routed = exl3_moe_workspace_size(rows, topk, hidden, inter);
     if (routed == 0) return 0;
-    return std::max(routed, plan_moe(rows * topk + rows, hidden, inter, false).total());
+    size_t need = std::max(routed, plan_moe(rows * topk, hidden, inter, false, rows).total());
+    if (moe_windowed(rows, rows * topk, 1)) need = std::max(need, plan_moe(rows * topk, hidden, inter, true, rows).total());
+    return need;
 }
 
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
@@ -660,7 +666,7 @@ int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, 
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: null operand");
-    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype))
+    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts))
         return declined("moe_with_shared_bank: declined (rows=%d, y dtype %d, rates %d/%d): run the shared expert as "
                         "a one-expert exl3_moe and pass it to exl3_moe as `shared`", rows, y_dtype, routed_n, sb.n);
     const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
@@ -699,7 +705,7 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
     }
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: null operand");
-    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype))
+    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts))
         return declined("moe_ragged_with_shared_bank: declined (rows=%d, y dtype %d): run the shared expert as a "
                         "one-expert exl3_moe and pass it to exl3_moe_ragged as `shared`", rows, y_dtype);
     const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);

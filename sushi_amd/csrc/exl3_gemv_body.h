@@ -702,7 +702,7 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
 
 // N > 0: one rate for the launch; N == 0: the generic reader; N == -1 / -2: per-expert rate from the ragged meta table
 // (lane-reader rates / the other rates), dispatched per workgroup.
-// SHP: the launch carries a fused shared expert's rows (per-slot MoE arm): a separate instantiation, so launches
+// SHP: the launch carries a fused shared expert's rows (either MoE arm): a separate instantiation, so launches
 // without them keep a kernel whose registers hold none of it.
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
@@ -724,6 +724,18 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
         if (g < sh_groups) {
             gemv_group<FAM, N, SH_ROWS, PRO, WIN, true>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype,
                                                         x_div, a, xs, reinterpret_cast<float (*)[SH_ROWS][128]>(red));
+            return;
+        }
+        g -= sh_groups;
+    }
+    if constexpr (SHP && WIN) {
+        // The sorted MoE arm with a shared expert: its groups of SH_ROWS (= MOE_WINDOW_ROWS) token rows come first,
+        // then the expert windows.
+        static_assert(RT == SH_ROWS, "a window holds as many rows as a shared group");
+        if (g < sh_groups) {
+            gemv_group<FAM, N, SH_ROWS, PRO, false, true>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype,
+                                                          x_div, a, xs,
+                                                          reinterpret_cast<float (*)[SH_ROWS][128]>(red));
             return;
         }
         g -= sh_groups;
@@ -772,7 +784,8 @@ static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
     dim3 grid((unsigned)(G * a.splits), (unsigned)a.groups, (unsigned)a.nproj);
     if (a.win_count) {  // the sorted MoE arm: expert windows of MOE_WINDOW_ROWS rows, f32 planes or the fold out
         if (a.rows != MOE_WINDOW_ROWS || !(a.partial_only || a.fold)) return hipErrorInvalidValue;
-        launch_one<FAM, N, MOE_WINDOW_ROWS, PRO, true>(a, grid, s);
+        if (a.sh_groups > 0) launch_one<FAM, N, MOE_WINDOW_ROWS, PRO, true, true>(a, grid, s);
+        else launch_one<FAM, N, MOE_WINDOW_ROWS, PRO, true, false>(a, grid, s);
     } else if constexpr (PRO == PRO_X && N >= 0) {
         if (a.rows <= 1) launch_slot<FAM, N, PRO>(a, grid, s);
         else if (a.rows <= 2) launch_one<FAM, N, 2, PRO, false>(a, grid, s);

@@ -558,20 +558,35 @@ def moe_ragged(x, rb: Ragged, inds, scores, dec: Decode, verify_rows: bool = Fal
 EXL3_DECLINED = 1
 
 
+_ONE_EXPERT: dict = {}
+
+
+def _one_expert_routing(rows: int, device: torch.device):
+    """Routing of a one-expert chain (every row to expert 0 with score 1), kept per device and grown on demand so a
+    call launches no fill kernels (the tensors are never written after they are made)."""
+    z, o = _ONE_EXPERT.get(device, (None, None))
+    if z is None or z.shape[0] < rows:
+        cap = max(rows, 64, 2 * (0 if z is None else z.shape[0]))
+        z = torch.zeros(cap, 1, dtype=torch.int32, device=device)
+        o = torch.ones(cap, 1, dtype=torch.float32, device=device)
+        _ONE_EXPERT[device] = (z, o)
+    return z[:rows], o[:rows]
+
+
 def _shared_rows(x: torch.Tensor, shared_bank: Bank, dec: Decode, limit: int) -> torch.Tensor:
     """The shared expert as a one-expert chain (inds 0, score 1), the reference callers' pattern
     (src/dsv41/dsv41_model.zig:3000)."""
     lead = tuple(x.shape[:-1])
-    z = torch.zeros(*lead, 1, dtype=torch.int32, device=x.device)
-    o = torch.ones(*lead, 1, dtype=torch.float32, device=x.device)
-    return _moe(x, shared_bank, z, o, dec, False, None, limit)
+    rows = x.numel() // int(x.shape[-1])
+    z, o = _one_expert_routing(rows, x.device)
+    return _moe(x, shared_bank, z.reshape(*lead, 1), o.reshape(*lead, 1), dec, False, None, limit)
 
 
 def moe_with_shared_bank(x, bank: Bank, shared_bank: Bank, inds, scores, dec: Decode, limit: int = 0) -> torch.Tensor:
     """The routed layer and its shared expert in one call: T(T(routed) + T(shared)), the rounding of the reference
     callers' pair of calls (the shared expert as a one-expert chain, then `moeWithShared`, root.zig:56-67).  Where
-    the fused form declines (rows > 16, f32 output, a shared rate other than the routed one) it makes those two
-    calls itself.  ``limit`` > 0 clamps both as `moeClamped` does (root.zig:98-124)."""
+    the fused form declines (f32 output, a shared rate other than the routed one, rows past the fused finish's
+    region) it makes those two calls itself.  ``limit`` > 0 clamps both as `moeClamped` does (root.zig:98-124)."""
     if limit < 0 or limit > 128:
         raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128 (0 = none)")
     dec.require_table()

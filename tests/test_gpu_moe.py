@@ -271,7 +271,7 @@ def _two_calls(x, bd, sd, xi, sc, dec, limit=0):
     return exl3.moe_with_shared(x, bd, xi, sc, dec, False, s)
 
 
-@pytest.mark.parametrize("rows", [1, 3, 8, 16])
+@pytest.mark.parametrize("rows", [1, 3, 8, 16, 17, 33])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("limit", [0, 4])
 def test_moe_with_shared_bank_is_the_two_calls(dev, rows, dtype, limit):
@@ -301,12 +301,41 @@ def test_moe_with_shared_bank_is_the_two_calls(dev, rows, dtype, limit):
     assert max_abs_rel(y.float().cpu().numpy(), want) < bar
 
 
-@pytest.mark.parametrize("case", ["rows17", "f32", "rates"])
+@pytest.mark.parametrize("rows", [17, 40])
+def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
+    """Past 16 rows the fused form runs in the expert-window launches (the C ABI does not decline) and equals the two
+    calls at the bar."""
+    E, hidden, inter, k, n = 16, 256, 128, 4, 32
+    b = synth.bank(35, "msw", E, hidden, inter, n)
+    s = synth.bank(35, "msw.shared", 1, hidden, inter, n)
+    x = synth.normal(35, f"x{rows}", (rows, hidden))
+    inds, scores = _route(35 + rows, rows, E, k)
+    bd, sd = _to(b, dev), _to(s, dev)
+    xd = x.to(dev)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    L = exl3._lib.load()
+    cb = exl3._lib.BankT(bd.gate.c(), bd.up.c(), bd.down.c())
+    cs = exl3._lib.BankT(sd.gate.c(), sd.up.c(), sd.down.c())
+    ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
+    y = torch.empty_like(xd)
+    x2 = xd.contiguous()
+    rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), k, exl3.MCG.c(), 0,
+                                     y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
+    assert rc == 0, exl3._lib.last_error()
+    ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
+    torch.cuda.synchronize()
+    assert max_abs_rel(y.float().cpu().numpy(), ref.float().cpu().numpy()) < BAR
+
+
+@pytest.mark.parametrize("case", ["rows700", "f32", "rates"])
 def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
     """Where the fused form does not serve, the C ABI declines before any launch and the wrapper makes the two
-    calls; the result is the two calls' own."""
+    calls; the result is the two calls' own.  700 rows: the routed, shared and combine fold words (3 x 700 x 256)
+    exceed the fused finish's region."""
     E, hidden, inter, k, n = 8, 256, 128, 2, 32
-    rows = 17 if case == "rows17" else 2
+    rows = 700 if case == "rows700" else 2
     b = synth.bank(33, "msd", E, hidden, inter, n)
     s = synth.bank(33, "msd.shared", 1, hidden, inter, 48 if case == "rates" else n)
     x = synth.normal(33, "x", (rows, hidden)).to(torch.float32 if case == "f32" else torch.float16)
@@ -332,7 +361,7 @@ def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
     assert torch.equal(y, ref)
 
 
-@pytest.mark.parametrize("rows", [1, 5])
+@pytest.mark.parametrize("rows", [1, 5, 20])
 def test_moe_ragged_with_shared_bank_is_the_two_calls(dev, rows):
     """Rate-grouped routed experts (K1/K2 under SPEC1, lane and generic readers both) with a K4 shared expert in the
     same launches, against the shared one-expert chain followed by moeRagged with `shared`."""
