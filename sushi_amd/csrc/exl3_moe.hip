@@ -122,8 +122,10 @@ hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
 // Expert windows for the sorted MoE arm (the grouping moePrefill's sort does, expert_exl3_kernels.zig:2861-2931 with
 // sorted_windows.zig:10-165): slot s (expert e = inds[s], clamped below `experts`) gets rank r = the number of slots
 // before it with the same expert, and lands in window wbase[e] + r / MOE_WINDOW_ROWS at row r % MOE_WINDOW_ROWS, where
-// wbase is the exclusive scan of ceil(count[e] / MOE_WINDOW_ROWS) over experts.  Ranks come from a direct count, so
-// the result does not depend on thread timing.
+// wbase is the exclusive scan of ceil(count[e] / MOE_WINDOW_ROWS) over experts.  Ranks come from one wave walking the
+// slots in order, 64 at a time: a slot's rank is its expert's running count plus the lanes before it in the same
+// round with the same expert (found by one ballot per bit of the expert id), so the result does not depend on thread
+// timing.
 constexpr int WIN_THREADS = 1024;
 __global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
                                                                   int experts, uint32_t *__restrict__ win_count,
@@ -134,8 +136,9 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t
     __shared__ uint32_t cnt[kMoeWindowMaxExperts];
     __shared__ uint32_t wbase[kMoeWindowMaxExperts];
     __shared__ uint32_t part[WIN_THREADS];
+    __shared__ uint32_t fill[kMoeWindowMaxExperts];
     const int tid = threadIdx.x;
-    for (int e = tid; e < experts; e += WIN_THREADS) cnt[e] = 0;
+    for (int e = tid; e < experts; e += WIN_THREADS) cnt[e] = fill[e] = 0;
     for (int s = tid; s < nslots; s += WIN_THREADS) ex[s] = (uint16_t)min(inds[s], (uint32_t)(experts - 1));
     __syncthreads();
     for (int s = tid; s < nslots; s += WIN_THREADS) atomicAdd(&cnt[ex[s]], 1u);
@@ -160,15 +163,32 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t
     }
     if (tid == WIN_THREADS - 1) *win_count = part[tid];
     __syncthreads();
-    for (int s = tid; s < nslots; s += WIN_THREADS) {
-        const uint32_t e = ex[s];
-        uint32_t rank = 0;
-        for (int q = 0; q < s; q++) rank += ex[q] == e ? 1u : 0u;
-        const uint32_t w = wbase[e] + rank / MOE_WINDOW_ROWS, r = rank % MOE_WINDOW_ROWS;
-        win_slots[(size_t)w * MOE_WINDOW_ROWS + r] = (uint32_t)s;
-        if (r == 0) {
-            win_expert[w] = e;
-            win_rows[w] = min(cnt[e] - rank, (uint32_t)MOE_WINDOW_ROWS);
+    if (tid < 64) {  // wave 0 ranks the slots in order
+        const int lane = tid;
+        const int id_bits = experts > 1 ? 32 - __clz(experts - 1) : 0;
+        for (int base = 0; base < nslots; base += 64) {
+            const int s = base + lane;
+            const bool live = s < nslots;
+            const int e = live ? (int)ex[s] : 0;
+            // The lanes holding this lane's expert: one ballot per bit of the expert id, and the live lanes.
+            unsigned long long same = __ballot(live);
+            for (int b = 0; b < id_bits; b++) {
+                const unsigned long long set = __ballot((e >> b) & 1);
+                same &= ((e >> b) & 1) ? set : ~set;
+            }
+            const unsigned long long below = (1ull << lane) - 1ull;
+            const uint32_t before = (uint32_t)__popcll(same & below);
+            const bool last = live && (same & ~below & ~(1ull << lane)) == 0ull;
+            if (live) {
+                const uint32_t rank = fill[e] + before;
+                const uint32_t w = wbase[e] + rank / MOE_WINDOW_ROWS, r = rank % MOE_WINDOW_ROWS;
+                win_slots[(size_t)w * MOE_WINDOW_ROWS + r] = (uint32_t)s;
+                if (r == 0) {
+                    win_expert[w] = (uint32_t)e;
+                    win_rows[w] = min(cnt[e] - rank, (uint32_t)MOE_WINDOW_ROWS);
+                }
+                if (last) fill[e] = rank + 1;  // the expert's last slot this round carries its count forward
+            }
         }
     }
 }
