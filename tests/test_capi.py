@@ -104,3 +104,14 @@ def test_synth_is_deterministic_and_name_keyed():
     assert ((s.abs() >= 0.5) & (s.abs() <= 1.5)).all() and (s < 0).any() and (s > 0).any()
     x = synth.normal(0, "x", (20000,)).float()
     assert abs(float(x.mean())) < 0.05 and abs(float(x.std()) - 1) < 0.05
+
+
+def test_bench_refuses_more_than_one_gpu_before_touching_one():
+    """bench.py measures one GPU: N > 1 exits with status 2 and a message saying so (no GPU is touched)."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "4"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
