@@ -248,10 +248,12 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0
     const int rows = windowed ? MOE_WINDOW_ROWS : 1;
     // Per-slot arm: at least 1.5 workgroups per CU and at most four batches of TPW tiles per wave (measured at C4's
     // shape, b = 1 and 8: the best of every split pair tried).  Sorted arm: up to eight batches (each window's
-    // workgroup carries four rows per tile) and one workgroup per CU.
+    // workgroup carries four rows per tile) and one workgroup per CU (measured at C4 b = 24 and 32).
     if (windowed) {
-        p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 8);
-        p.s2 = gemv_default_splits(inter, hidden, rows, groups, 8);
+        // The window count is planned at its fewest, so the CU-round fill of the split tie-break would be judged on
+        // the wrong grid: the plain target (one workgroup per CU) instead (C4 b = 32: splits 1/2 -> 1/1, -10%).
+        p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 8, GEMV_TARGET_WGS);
+        p.s2 = gemv_default_splits(inter, hidden, rows, groups, 8, GEMV_TARGET_WGS);
     } else {
         p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 4, kMoeSlotTargetWgs);
         p.s2 = gemv_default_splits(inter, hidden, rows, groups, 4, kMoeSlotTargetWgs);
