@@ -220,9 +220,10 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
 }
 
 // Rows above which the routed layer takes the sorted arm (slots grouped into expert windows, each expert's tiles
-// decoded once per window): the reference's decode chain serves up to DECODE_ROWS_MAX = 16 rows and sends wider
-// batches to moePrefill (src/exl3/root.zig:45-53).
-constexpr int kMoeDecodeRowsMax = 16;
+// decoded once per window).  The reference's decode chain serves up to DECODE_ROWS_MAX = 16 rows and sends wider
+// batches to moePrefill (src/exl3/root.zig:45-53); here the windows win from 9 rows on (measured at C4's shape:
+// 12 rows 90.5 -> 88.2 us, 16 rows 115 -> 106 us; 4 and 6 rows stay faster per slot, 8 rows equal).
+constexpr int kMoeDecodeRowsMax = 8;
 // EXL3_MOE_DECODE_ROWS_MAX moves that bound (tuning and tests; read by the workspace queries too).
 int moe_decode_rows_max() { return env_int("EXL3_MOE_DECODE_ROWS_MAX", kMoeDecodeRowsMax); }
 
