@@ -41,7 +41,7 @@ def _oracle_moe(b, x, inds, scores, hidden, inter, n, odec, clamp=0.0):
 @pytest.mark.parametrize("rows", [1, 3, 8, 16, 17, 40])
 @pytest.mark.parametrize("n", [32, 48])
 def test_moe_decode_chain(dev, rows, n):
-    """Up to 16 rows: the per-slot decode chain; above: the sorted arm (slots grouped into expert windows)."""
+    """Up to 8 rows: the per-slot decode chain; above: the sorted arm (slots grouped into expert windows)."""
     print(f"[moe] rows={rows} n={n}", flush=True)
     E, hidden, inter, k = 16, 256, 384, 4
     b = synth.bank(3, "moe", E, hidden, inter, n)
@@ -210,7 +210,7 @@ def test_moe_sorted_and_per_slot_arms_agree(dev):
 @pytest.mark.parametrize("with_shared", [False, True])
 def test_moe_fold_and_reduce_arms_agree(dev, rows, with_shared):
     """The down projection folded straight into y and the planes + reduce launch agree to the bar against the
-    oracle (per-slot arm up to 16 rows, sorted arm above), with and without a shared expert, and the accumulators
+    oracle (per-slot arm up to 8 rows, sorted arm above), with and without a shared expert, and the accumulators
     are clean for the next call."""
     import os
 
@@ -303,7 +303,7 @@ def test_moe_with_shared_bank_is_the_two_calls(dev, rows, dtype, limit):
 
 @pytest.mark.parametrize("rows", [17, 40])
 def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
-    """Past 16 rows the fused form runs in the expert-window launches (the C ABI does not decline) and equals the two
+    """Past 8 rows the fused form runs in the expert-window launches (the C ABI does not decline) and equals the two
     calls at the bar."""
     E, hidden, inter, k, n = 16, 256, 128, 4, 32
     b = synth.bank(35, "msw", E, hidden, inter, n)
