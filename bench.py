@@ -32,12 +32,15 @@ def _algorithmic_bytes(in_f: int, out_f: int, n: int, rows: int) -> int:
 
 
 def _capture(calls, dev):
-    """One HIP graph holding `calls()` (captured on a side stream, outside any timed region)."""
+    """One HIP graph holding `calls()` (captured on a side stream, outside any timed region).  One eager pass on the
+    side stream first: the library's per-stream workspace is allocated and zeroed there before the capture."""
     import torch
 
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
+        calls()
+        side.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=side):
             calls()

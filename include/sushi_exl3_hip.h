@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 2
+#define EXL3_ABI_VERSION 3
 
 /* Codebook: the reference's `Codebook` enum values (src/exl3/expert_exl3.zig:54-61), plus 3INST as an
  * extension (QTIP's LCG codebook, not in the reference). */
@@ -119,6 +119,23 @@ typedef struct {
 int32_t exl3_abi_version(void);
 const char *exl3_last_error(void);
 
+/* Arm overrides for tests and tuning sweeps: no counterpart in the reference, whose arms are fixed per build, and
+ * nothing a production caller needs.  Every knob starts unset (the library's own choice); exl3_set_override(knob,
+ * value, 1) pins it and (knob, 0, 0) unsets it.  Process-wide, read at each call; change them only while no call
+ * is being issued.  Nothing in the environment changes an arm. */
+typedef enum {
+    EXL3_KNOB_GEMV_SPLITS = 0,          /* k splits of the dense decode GEMV (must divide in/128; else ignored) */
+    EXL3_KNOB_GEMV_SEPARATE_FINISH = 1, /* 1: split GEMVs finish in a second kernel */
+    EXL3_KNOB_GEMV_FOLD = 2,            /* 0: split GEMVs finish through arrival counters + partial planes */
+    EXL3_KNOB_MOE_DECODE_ROWS_MAX = 3,  /* rows up to which a routed layer takes the per-slot arm */
+    EXL3_KNOB_MOE_SPLITS1 = 4,          /* k splits of the routed gate/up GEMV */
+    EXL3_KNOB_MOE_SPLITS2 = 5,          /* k splits of the routed down GEMV */
+    EXL3_KNOB_MOE_WINDOWS = 6,          /* 0: no sorted (expert-window) arm */
+    EXL3_KNOB_MOE_FOLD = 7,             /* 0: the down projection writes planes and a reduce kernel finishes */
+    EXL3_KNOB_COUNT = 8
+} exl3_knob;
+int32_t exl3_set_override(int32_t knob, int32_t value, int32_t enable);
+
 /* Decodes `count` codewords (low `window_bits` kept) at rate n to f16 bits; PAIR1 writes two weights per codeword
  * (both weights of a pair come from the odd weight's codeword).  Replaces the Metal exhaustive-codeword test kernels
  * (src/exl3/kernel_source.zig:409-517) and the host `decodeCodeword`/`decodeHashMask`/`decodePair`
@@ -149,8 +166,8 @@ int32_t exl3_linear_grouped(const void *x, int32_t x_dtype, int32_t groups, int3
                             const uint16_t *svh, exl3_decode_t dec, void *y, int32_t y_dtype, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
-/* Clears a workspace once after allocation.  Every workspace begins with a 4 MiB region of fused-finish
- * arrival counters and accumulators that must start at zero; the calls that use them always leave them at zero
+/* Clears a workspace once after allocation.  Every workspace begins with an 8 MiB region of fused-finish
+ * arrival counters, accumulators and their overflow words that must start at zero; the calls that use them always leave them at zero
  * again, and no other call writes there, so one init per allocation suffices.  Calls that share a workspace must not overlap in time
  * (they would race on its scratch).  A small fill kernel, never hipMemsetAsync. */
 int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);

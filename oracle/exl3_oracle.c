@@ -630,6 +630,10 @@ int ox_decode_dense(const uint16_t *words, const uint16_t *suh, const uint16_t *
 /* ------------------------------------------------------------------------------------------------ */
 /* Router: moe_router.zig:22-62.  Top-k by logit (ties: lower expert index first, listed in          */
 /* descending logit order), softmax over all experts, gathered and renormalised over the k picked.  */
+/* A NaN logit selects as -inf (the fused router's "v > best" never takes it, moe_router.zig:137-141) */
+/* and no expert is picked twice; the NaN still reaches the softmax, so the row's scores are NaN.   */
+
+static double ox_route_key(float v) { return v != v ? -INFINITY : (double)v; }
 
 void ox_route_topk(const float *logits, size_t rows, size_t experts, size_t k, uint32_t *inds, float *scores) {
     for (size_t r = 0; r < rows; r++) {
@@ -645,7 +649,7 @@ void ox_route_topk(const float *logits, size_t rows, size_t experts, size_t k, u
                 int taken = 0;
                 for (size_t q = 0; q < j; q++) taken |= ir[q] == e;
                 if (taken) continue;
-                if (best == (size_t)-1 || l[e] > l[best]) best = e;
+                if (best == (size_t)-1 || ox_route_key(l[e]) > ox_route_key(l[best])) best = e;
             }
             ir[j] = (uint32_t)best;
         }

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "libsushi_exl3_hip.so")
 EXPORTS = (
     "exl3_abi_version",
     "exl3_last_error",
+    "exl3_set_override",
     "exl3_decode_codewords",
     "exl3_reconstruct_inner",
     "exl3_linear_workspace_size",
@@ -67,6 +68,7 @@ def load() -> ctypes.CDLL:
     i32, vp, sz, i64 = ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64
     L.exl3_abi_version.restype = i32
     L.exl3_last_error.restype = ctypes.c_char_p
+    L.exl3_set_override.argtypes = [i32, i32, i32]
     L.exl3_decode_codewords.argtypes = [vp, i64, i32, DecodeT, vp, vp]
     L.exl3_reconstruct_inner.argtypes = [vp, i32, i32, i32, DecodeT, vp, vp]
     L.exl3_linear_workspace_size.restype = sz

@@ -3,6 +3,8 @@
 // Every refusal happens before any launch (as the reference's `Exl3*` errors do, src/exl3/root.zig:104-133), and the
 // library never allocates device memory: scratch comes from the caller's workspace.
 #include <algorithm>
+#include <atomic>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -44,21 +46,29 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Every workspace starts with a fixed region that stays zero between calls.  Only the fused-finish GEMV touches it,
-// either as arrival counters (its first MiB) or as the fold's 64-bit accumulators (the whole region), and every such
-// launch leaves what it touched at zero again, so the region stays valid across calls of any arm
-// (exl3_workspace_init zeroes it once after allocation).  Scratch of every arm begins after it.
-// Each counter owns a 128-byte line (COUNTER_STRIDE words): the splits of different output groups then never
-// contend for one line in the L2's atomic unit.
-constexpr size_t kZeroBytes = size_t(4) << 20;
+// either as arrival counters (its first MiB) or as the fold's 64-bit accumulators (the first 4 MiB) and their f64
+// overflow words (the next 4 MiB), and every such launch leaves what it touched at zero again, so the region stays
+// valid across calls of any arm (exl3_workspace_init zeroes it once after allocation).  Scratch of every arm begins
+// after it.  Each counter owns a 128-byte line (COUNTER_STRIDE words): the splits of different output groups then
+// never contend for one line in the L2's atomic unit.
+constexpr size_t kFoldWords = FOLD_WORDS;
+constexpr size_t kZeroBytes = 2 * kFoldWords * sizeof(unsigned long long);
 constexpr size_t kCounterSlots = (size_t(1) << 20) / (sizeof(uint32_t) * COUNTER_STRIDE);
-constexpr size_t kFoldWords = kZeroBytes / sizeof(unsigned long long);
 
 bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    if (!v || !*v) return dflt;
-    return atoi(v);
+// Arm overrides (exl3_set_override): one word per knob, INT32_MIN = unset.  Read with a relaxed load at each call,
+// so an unset knob costs one load and nothing in the environment changes an arm.
+std::atomic<int32_t> g_override[EXL3_KNOB_COUNT] = {};
+struct OverrideInit {
+    OverrideInit() {
+        for (auto &o : g_override) o.store(INT32_MIN, std::memory_order_relaxed);
+    }
+} g_override_init;
+
+int knob(exl3_knob k, int dflt) {
+    const int32_t v = g_override[k].load(std::memory_order_relaxed);
+    return v == INT32_MIN ? dflt : v;
 }
 
 // The decode family and constants for (dec, n); status on refusal.
@@ -113,7 +123,7 @@ struct GemvPlan {
 
 GemvPlan plan_gemv(int groups, int rows, int in, int out) {
     GemvPlan p;
-    p.splits = env_int("EXL3_GEMV_SPLITS", 0);
+    p.splits = knob(EXL3_KNOB_GEMV_SPLITS, 0);
     const int blocks = in / 128;
     // Up to four tile batches of TPW tiles per wave (eight from 8 rows): later batches' loads overlap the decode, and
     // fewer splits mean fewer fold arrivals.
@@ -188,13 +198,14 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.splits = p.splits;
         a.groups = groups;
         a.nproj = 1;
-        a.fused_finish = (env_int("EXL3_GEMV_SEPARATE_FINISH", 0) == 0 &&
+        a.fused_finish = (knob(EXL3_KNOB_GEMV_SEPARATE_FINISH, 0) == 0 &&
                           (size_t)groups * (out / 128) <= kCounterSlots) ? 1 : 0;
         a.partial_only = 0;
-        // The fold (exact fixed-point accumulation, one atomic round trip per split) serves the fused finish whenever
-        // its words fit the zeroed region and the splits fit its count field; the counters + planes arm otherwise.
-        a.fold = (a.fused_finish && p.splits > 1 && p.splits <= FOLD_MAX_SPLITS &&
-                  (size_t)groups * rows * out <= kFoldWords && env_int("EXL3_GEMV_FOLD", 1) != 0)
+        // The fold (exact fixed-point accumulation, one atomic round trip per split) serves the fused finish of a
+        // 16-bit output whenever its words fit the zeroed region and the splits fit its count field; the counters +
+        // planes arm otherwise.  An f32 output never folds: the fold's 2^-24 fixed point would quantise it.
+        a.fold = (a.fused_finish && p.splits > 1 && p.splits <= FOLD_MAX_SPLITS && y_dtype != EXL3_DT_F32 &&
+                  (size_t)groups * rows * out <= kFoldWords && knob(EXL3_KNOB_GEMV_FOLD, 1) != 0)
                      ? reinterpret_cast<unsigned long long *>(w)
                      : nullptr;
         a.fold_arrivals = p.splits;
@@ -224,8 +235,8 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
 // batches to moePrefill (src/exl3/root.zig:45-53); here the windows win from 9 rows on (measured at C4's shape:
 // 12 rows 90.5 -> 88.2 us, 16 rows 115 -> 106 us; 4 and 6 rows stay faster per slot, 8 rows equal).
 constexpr int kMoeDecodeRowsMax = 8;
-// EXL3_MOE_DECODE_ROWS_MAX moves that bound (tuning and tests; read by the workspace queries too).
-int moe_decode_rows_max() { return env_int("EXL3_MOE_DECODE_ROWS_MAX", kMoeDecodeRowsMax); }
+// EXL3_KNOB_MOE_DECODE_ROWS_MAX moves that bound (tuning and tests; read by the workspace queries too).
+int moe_decode_rows_max() { return knob(EXL3_KNOB_MOE_DECODE_ROWS_MAX, kMoeDecodeRowsMax); }
 
 // Workgroups the per-slot MoE launches aim for: 1.5 per CU.
 constexpr int kMoeSlotTargetWgs = 384;
@@ -259,8 +270,8 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0
         p.s1 = gemv_default_splits(hidden, inter, rows, 2 * groups, 4, kMoeSlotTargetWgs);
         p.s2 = gemv_default_splits(inter, hidden, rows, groups, 4, kMoeSlotTargetWgs);
     }
-    // EXL3_MOE_SPLITS1 / _SPLITS2 pin the gate/up and down split counts (whole 128-blocks; tuning and tests)
-    const int f1 = env_int("EXL3_MOE_SPLITS1", 0), f2 = env_int("EXL3_MOE_SPLITS2", 0);
+    // EXL3_KNOB_MOE_SPLITS1 / _SPLITS2 pin the gate/up and down split counts (whole 128-blocks; tuning and tests)
+    const int f1 = knob(EXL3_KNOB_MOE_SPLITS1, 0), f2 = knob(EXL3_KNOB_MOE_SPLITS2, 0);
     if (f1 > 0 && (hidden / 128) % f1 == 0) p.s1 = f1;
     if (f2 > 0 && (inter / 128) % f2 == 0) p.s2 = f2;
     p.gu_bytes = align_up((size_t)(nslots + extra) * p.s1 * inter * sizeof(float));
@@ -275,8 +286,8 @@ bool moe_windowed(int rows, int nslots, int experts) {
     return rows > moe_decode_rows_max() && nslots <= kMoeWindowMaxSlots && experts <= kMoeWindowMaxExperts;
 }
 
-// EXL3_MOE_WINDOWS=0 keeps every row count on the per-slot chain (for comparing the arms).
-bool moe_windows_enabled() { return env_int("EXL3_MOE_WINDOWS", 1) != 0; }
+// EXL3_KNOB_MOE_WINDOWS = 0 keeps every row count on the per-slot chain (for comparing the arms).
+bool moe_windows_enabled() { return knob(EXL3_KNOB_MOE_WINDOWS, 1) != 0; }
 
 constexpr int kReduceMaxTopk = kMoeReduceMaxTopk;  // REDUCE_MAX_TOPK, expert_exl3_kernels.zig:2562
 
@@ -434,11 +445,11 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     d.nproj = 1;
     d.fused_finish = 0;
     d.partial_only = 1;
-    // The down projection folds straight into y (score-weighted, exact fixed point, shared expert added by the
-    // completing arrival) when every token's topk * splits arrivals fit the count field and its rows fit the zeroed
-    // region; the planes + reduce launch otherwise.
+    // The down projection folds straight into a 16-bit y (score-weighted, exact fixed point, shared expert added by
+    // the completing arrival) when every token's topk * splits arrivals fit the count field and its rows fit the
+    // zeroed region; the planes + reduce launch otherwise (and for an f32 y, which the fixed point would quantise).
     const bool fold = sb || (topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)rows * hidden <= kFoldWords &&
-                             env_int("EXL3_MOE_FOLD", 1) != 0);
+                             y_dtype != EXL3_DT_F32 && knob(EXL3_KNOB_MOE_FOLD, 1) != 0);
     if (fold) {
         d.partial_only = 0;
         d.fused_finish = 1;
@@ -523,6 +534,13 @@ extern "C" {
 int32_t exl3_abi_version(void) { return EXL3_ABI_VERSION; }
 
 const char *exl3_last_error(void) { return g_err.c_str(); }
+
+int32_t exl3_set_override(int32_t k, int32_t value, int32_t enable) {
+    if (k < 0 || k >= EXL3_KNOB_COUNT) return fail(EXL3_ERR_BAD_SHAPE, "set_override: unknown knob %d", k);
+    if (enable && value == INT32_MIN) return fail(EXL3_ERR_BAD_SHAPE, "set_override: value INT32_MIN is reserved");
+    g_override[k].store(enable ? value : INT32_MIN, std::memory_order_relaxed);
+    return ok();
+}
 
 int32_t exl3_decode_codewords(const uint16_t *codewords, int64_t count, int32_t n, exl3_decode_t dec, uint16_t *out,
                               hipStream_t stream) {

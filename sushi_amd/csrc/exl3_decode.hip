@@ -1,7 +1,10 @@
 // Trellis decode kernels: a codeword list (the exhaustive 65,536-codeword check) and the dense reconstruction
 // of one projection's inner matrix ("dequantized fp16 weights", bit-exact with reconstructInner,
-// beamivalice/sushi src/exl3/expert_exl3.zig:416-438).
+// beamivalice/sushi src/exl3/expert_exl3.zig:416-438).  The reconstruction runs the decoder the GEMV and the GEMM
+// multiply with: the lane reader and lane decoder at the rates they serve (16, 24, 32, 40, 48, 64), the generic
+// per-codeword reader at every other rate, so the weights it returns are the hot path's own.
 #include "exl3_kernels.h"
+#include "exl3_lane_decode.h"
 
 namespace exl3 {
 
@@ -52,6 +55,57 @@ __global__ void reconstruct_inner_kernel(const uint16_t *__restrict__ trellis, i
     out[base + of] = __half_as_ushort(w1);  // weight t+1 is the next row (i odd), same column
 }
 
+// Lane-reader rates: one wave per 8 consecutive tiles of the pack order, lane 8o + j reading chunk j of tile o with
+// load_lane_words_u (the wave-uniform start of the 8 tiles plus the lane's tile offset, as the GEMV and the GEMM
+// address a k-tile row of an output group) and decoding it with decode_weights, hash / pair weights times 4096 as
+// the matrix cores take them.  Pair i = 4qq + p of the lane holds rows 2qq + 8(p & 1) + {0, 1} of column j (p < 2)
+// or j + 8 (p >= 2).  A tail wave's lanes past the last tile re-read it and store nothing.
+constexpr int RL_WAVES = 4;
+template <int FAM, int N, bool MASKED>
+__global__ __launch_bounds__(64 * RL_WAVES) void reconstruct_lane_kernel(const uint16_t *__restrict__ trellis,
+                                                                         int tiles, int ot, DecodeK k,
+                                                                         uint16_t *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int wv = blockIdx.x * RL_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t0 = wv * 8;
+    if (t0 >= tiles) return;
+    const int o = lane >> 3, j = lane & 7;
+    const int t = min(t0 + o, tiles - 1);
+    uint32_t A[LaneBits<N>::AW];
+    load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(trellis + (size_t)t0 * N), (uint32_t)((t - t0) * N) >> 1,
+                         j, A);
+    uint32_t w[16];
+    decode_weights<FAM, N, MASKED>(A, k, w);
+    if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
+    }
+    if (t0 + o >= tiles) return;
+    const int tk = t / ot, tn = t - tk * ot;
+    const size_t of = (size_t)ot * 16;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int qq = i >> 2, p = i & 3;
+        const size_t at = ((size_t)tk * 16 + 2 * qq + 8 * (p & 1)) * of + (size_t)tn * 16 + j + 8 * (p >> 1);
+        out[at] = (uint16_t)(w[i] & 0xFFFFu);
+        out[at + of] = (uint16_t)(w[i] >> 16);
+    }
+}
+
+template <int FAM, int N>
+static hipError_t launch_reconstruct_lane(const uint16_t *trellis, int tiles, int ot, const DecodeK &k, uint16_t *out,
+                                          hipStream_t s) {
+    const int waves = (tiles + 7) / 8;
+    const dim3 grid((unsigned)((waves + RL_WAVES - 1) / RL_WAVES));
+    if (k.wmask != 0xFFFFu)
+        hipLaunchKernelGGL((reconstruct_lane_kernel<FAM, N, true>), grid, dim3(64 * RL_WAVES), 0, s, trellis, tiles, ot,
+                           k, out);
+    else
+        hipLaunchKernelGGL((reconstruct_lane_kernel<FAM, N, false>), grid, dim3(64 * RL_WAVES), 0, s, trellis, tiles,
+                           ot, k, out);
+    return hipGetLastError();
+}
+
 template <int FAM>
 static hipError_t launch_decode_codewords(const uint16_t *cw, int64_t count, const DecodeK &k, uint16_t *out,
                                           hipStream_t s) {
@@ -76,6 +130,15 @@ hipError_t run_decode_codewords(int fam, const uint16_t *cw, int64_t count, cons
 template <int FAM>
 static hipError_t launch_reconstruct(const uint16_t *trellis, int it, int ot, int n, const DecodeK &k, uint16_t *out,
                                      hipStream_t s) {
+    switch (n) {
+    case 16: return launch_reconstruct_lane<FAM, 16>(trellis, it * ot, ot, k, out, s);
+    case 24: return launch_reconstruct_lane<FAM, 24>(trellis, it * ot, ot, k, out, s);
+    case 32: return launch_reconstruct_lane<FAM, 32>(trellis, it * ot, ot, k, out, s);
+    case 40: return launch_reconstruct_lane<FAM, 40>(trellis, it * ot, ot, k, out, s);
+    case 48: return launch_reconstruct_lane<FAM, 48>(trellis, it * ot, ot, k, out, s);
+    case 64: return launch_reconstruct_lane<FAM, 64>(trellis, it * ot, ot, k, out, s);
+    default: break;
+    }
     hipLaunchKernelGGL(reconstruct_inner_kernel<FAM>, dim3((unsigned)(it * ot)), dim3(128), 0, s, trellis, it, ot, n,
                        k, out);
     return hipGetLastError();

@@ -295,10 +295,13 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
         const int o = lane >> 3, j = lane & 7;
         const DecodeK k = a.k;
         const bool masked = k.wmask != 0xFFFFu;
-        const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8 + o) * N;
+        // the uniform start of k-tile row r of the group in k-step 0, plus the lane's tile offset (the GEMV's reader)
+        const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8) * N;
+        const uint32_t lane_words = (uint32_t)(o * N) >> 1;
         const size_t kstep = (size_t)4 * OT * N;  // halves from one k-step's row r to the next
         auto load_tile = [&](int ks, uint32_t (&W)[AW]) __attribute__((always_inline)) {
-            load_lane_words<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(ks, nks - 1) * kstep), j, W);
+            load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(ks, nks - 1) * kstep),
+                                 lane_words, j, W);
         };
         auto decode_store = [&](const uint32_t (&W)[AW], uint16_t *slab) __attribute__((always_inline)) {
             uint32_t w[16];

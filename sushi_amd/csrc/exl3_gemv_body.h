@@ -316,20 +316,42 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
 }
 
 // One output's fixed-point term: the arrival count plus either the biased 24-bit-fraction value or, for a value that
-// is not finite or not below 2^21 in magnitude, a mark in the non-finite field.  v * 2^24 is exact in f32 and below
-// 2^45, and rintf rounds it to the nearest integer.
+// is not finite or not below 2^21 in magnitude, a mark in the out-of-range field (the value itself then goes to the
+// overflow word, fold_overflow).  v * 2^24 is exact in f32 and below 2^45, and rintf rounds it to the nearest integer.
+__device__ __forceinline__ bool fold_in_range(float v) { return fabsf(v) < 2097152.0f; }  // NaN fails the compare too
+
 __device__ __forceinline__ unsigned long long fold_term(float v) {
     const unsigned long long one = 1ull << FOLD_COUNT_SHIFT;
-    if (!(fabsf(v) < 2097152.0f)) return one | (1ull << FOLD_BAD_SHIFT);  // NaN fails the compare as well
+    if (!fold_in_range(v)) return one | (1ull << FOLD_BAD_SHIFT);
     const long long q = (long long)rintf(v * 16777216.0f);
     return one + (unsigned long long)(q + FOLD_BIAS);
 }
 
-// The output value of a word that holds all S arrivals: NaN if any contribution was marked, else the exact sum.
-__device__ __forceinline__ float fold_value(unsigned long long t, int S) {
+// The contributions of this lane's two outputs that fall outside the fixed-point range go, in f64, to their overflow
+// words before the arrivals are counted: a release fence (only in a wave that had one) orders them ahead of the fold
+// adds, so the arrival that completes an output sees them.  f64 keeps inf and NaN as they are (inf + -inf is NaN).
+__device__ __forceinline__ void fold_overflow(unsigned long long *w0, unsigned long long *w1, float v0, float v1) {
+    const bool o0 = !fold_in_range(v0), o1 = !fold_in_range(v1);
+    if (o0) __hip_atomic_fetch_add(reinterpret_cast<double *>(w0 + FOLD_WORDS), (double)v0, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    if (o1) __hip_atomic_fetch_add(reinterpret_cast<double *>(w1 + FOLD_WORDS), (double)v1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    if (__ballot(o0 || o1)) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+
+// The output value of word `w` once its last word value `t` holds all S arrivals: the exact sum of the in-range
+// terms, plus, when any contribution was out of range, the overflow word's f64 sum (read and cleared here, after an
+// acquire fence that pairs with the contributors' release).
+__device__ __forceinline__ float fold_value(unsigned long long t, int S, unsigned long long *w) {
     const int bad = (int)((t >> FOLD_BAD_SHIFT) & 63u);
     const long long sum = (long long)(t & ((1ull << FOLD_BAD_SHIFT) - 1)) - (long long)(S - bad) * FOLD_BIAS;
-    return bad ? __builtin_nanf("") : (float)((double)sum * (1.0 / 16777216.0));
+    double v = (double)sum * (1.0 / 16777216.0);
+    if (bad) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        v += __hip_atomic_exchange(reinterpret_cast<double *>(w + FOLD_WORDS), 0.0, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return (float)v;
 }
 
 // Fused split-k finish by exact accumulation.  The output transform (FWHT-128, then * svh) is linear, so each split
@@ -373,10 +395,11 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
             yrow = (size_t)c.g * a.rows + r;
         }
         const int arrivals = shared ? c.S : a.fold_arrivals;
-        const unsigned long long t0 = fold_term((v0 * HAD_SCALE * c.sv0) * sc);
-        const unsigned long long t1 = fold_term((v1 * HAD_SCALE * c.sv1) * sc);
+        const float f0 = (v0 * HAD_SCALE * c.sv0) * sc, f1 = (v1 * HAD_SCALE * c.sv1) * sc;
+        const unsigned long long t0 = fold_term(f0), t1 = fold_term(f1);
         const size_t yo = yrow * a.out + (size_t)c.og * 128;
         unsigned long long *w0 = (shared ? a.sh_fold : a.fold) + yo + lane, *w1 = w0 + 64;
+        fold_overflow(w0, w1, f0, f1);
         const unsigned long long o0 = __hip_atomic_fetch_add(w0, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long o1 = __hip_atomic_fetch_add(w1, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // Both adds go out before either result is examined: one memory round trip for the pair, not two.
@@ -385,7 +408,8 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
         if constexpr (!MOE) {
             // Both outcomes are settled before either store, so no store waits on the other output's check.
             const bool d0 = (o0 >> FOLD_COUNT_SHIFT) == last, d1 = (o1 >> FOLD_COUNT_SHIFT) == last;
-            const float y0 = fold_value(o0 + t0, arrivals), y1 = fold_value(o1 + t1, arrivals);
+            const float y0 = d0 ? fold_value(o0 + t0, arrivals, w0) : 0.f;
+            const float y1 = d1 ? fold_value(o1 + t1, arrivals, w1) : 0.f;
             if (d0) {
                 store_y(a.y, a.y_dtype, yo + lane, y0);
                 *w0 = 0ull;  // no split of this launch touches it again; the next launch reads it after the boundary
@@ -401,7 +425,7 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
             const unsigned long long o = h ? o1 : o0, t = h ? t1 : t0;
             if ((o >> FOLD_COUNT_SHIFT) != last) continue;
             const size_t i = yo + lane + 64 * h;
-            float v = fold_value(o + t, arrivals);
+            float v = fold_value(o + t, arrivals, h ? w1 : w0);
             if (a.fold_comb) {
                 // The routed sum and the shared expert's, each rounded to y's 16-bit dtype, meet in one word: each
                 // adds its bit pattern into its own half-word with a flag; whichever arrives second holds both and

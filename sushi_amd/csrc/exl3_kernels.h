@@ -18,13 +18,18 @@ enum Prologue : int { PRO_X = 0, PRO_MID = 1 };
 constexpr int COUNTER_STRIDE = 32;
 
 // Fixed-point fused finish (the fold): one 64-bit word per output holds the arrival count in bits 63..58 (so at
-// most FOLD_MAX_SPLITS splits), the count of non-finite or out-of-range contributions in bits 57..52, and in bits
-// 51..0 the sum of the splits' biased terms q + FOLD_BIAS, q = round(v * 2^FOLD_FRAC) for |v| < 2^21.
+// most FOLD_MAX_SPLITS splits), the count of contributions outside the fixed-point range in bits 57..52, and in bits
+// 51..0 the sum of the splits' biased terms q + FOLD_BIAS, q = round(v * 2^FOLD_FRAC) for |v| < 2^21.  A contribution
+// outside that range (or not finite) is added in f64 to the output's overflow word, FOLD_WORDS words past its fold
+// word, before its arrival is counted; the arrival that completes the output adds the overflow word to the exact sum
+// when the out-of-range count says it is in use, and clears it.  The region of fold words and the region of overflow
+// words each hold FOLD_WORDS words.
 constexpr int FOLD_MAX_SPLITS = 63;
 constexpr int FOLD_COUNT_SHIFT = 58;
 constexpr int FOLD_BAD_SHIFT = 52;
 constexpr int FOLD_FRAC = 24;
 constexpr long long FOLD_BIAS = 1LL << 45;
+constexpr size_t FOLD_WORDS = (size_t(4) << 20) / sizeof(unsigned long long);
 
 // GEMV workgroup shape: GEMV_WAVES waves, each loading up to TPW k-tiles of the output group before its prologue
 // and refilling each slot as it is decoded.  Two slots rather than four: with fewer requests in flight at the start,

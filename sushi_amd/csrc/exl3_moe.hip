@@ -203,12 +203,23 @@ hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32
 }
 
 // One workgroup (256 threads) per row: k rounds of a block-wide argmax (ties to the lower index), then the softmax
-// mass of the picks over the full row, renormalised.
+// mass of the picks over the full row, renormalised.  Selection keys are the logits with NaN read as -inf, and a
+// per-row mask keeps each expert from being picked twice: every round starts from the lowest unpicked index as its
+// candidate, so with k <= experts (checked by the host) each pick is a distinct index in [0, experts) whatever the
+// logits hold.  A NaN logit still reaches the softmax, so such a row's scores come out NaN, as the chain's do.
+__device__ __forceinline__ float route_key(float v) { return v != v ? -INFINITY : v; }
+
+// (value, index) pair order of the argmax: larger key first, then the lower index.
+__device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
 __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict__ logits, int experts, int k,
                                                          uint32_t *__restrict__ inds, float *__restrict__ scores) {
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *l = logits + (size_t)row * experts;
     __shared__ float vals[1024];
+    __shared__ unsigned char taken[1024];
     __shared__ float wv[4];
     __shared__ int wi[4];
     __shared__ int picked[32];
@@ -216,6 +227,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
     float mx = -INFINITY;
     for (int e = tid; e < experts; e += 256) {
         vals[e] = l[e];
+        taken[e] = 0;
         mx = fmaxf(mx, vals[e]);
     }
     for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
@@ -230,11 +242,13 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
     __syncthreads();
     den = red[0] + red[1] + red[2] + red[3];
     for (int j = 0; j < k; j++) {
+        // bi = experts marks "no candidate yet": any unpicked expert beats it (its key is at least -inf).
         float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
+        int bi = experts;
         for (int e = tid; e < experts; e += 256) {
-            const float v = vals[e];
-            if (v > bv || (v == bv && e < bi)) {
+            if (taken[e]) continue;
+            const float v = route_key(vals[e]);
+            if (bi == experts || route_better(v, e, bv, bi)) {
                 bv = v;
                 bi = e;
             }
@@ -242,7 +256,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
         for (int m = 32; m >= 1; m >>= 1) {
             const float ov = __shfl_xor(bv, m, 64);
             const int oi = __shfl_xor(bi, m, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
+            if (oi != experts && (bi == experts || route_better(ov, oi, bv, bi))) {
                 bv = ov;
                 bi = oi;
             }
@@ -256,12 +270,13 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict
             float b = wv[0];
             int i = wi[0];
             for (int w = 1; w < 4; w++)
-                if (wv[w] > b || (wv[w] == b && wi[w] < i)) {
+                if (wi[w] != experts && (i == experts || route_better(wv[w], wi[w], b, i))) {
                     b = wv[w];
                     i = wi[w];
                 }
+            // k <= experts leaves an unpicked expert every round, so i < experts here
             picked[j] = i;
-            vals[i] = -INFINITY;
+            taken[i] = 1;
         }
         __syncthreads();
     }

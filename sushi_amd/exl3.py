@@ -13,6 +13,7 @@ CPU.  Refusals raise the reference's named errors before any launch.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import enum
 from dataclasses import dataclass, field
@@ -351,20 +352,49 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
 
 
 class _Workspace:
-    """Per-device scratch owned by this host layer (the C ABI itself never allocates)."""
+    """Scratch owned by this host layer (the C ABI itself never allocates), one buffer per (device, stream).
+
+    The C ABI wants one workspace per stream: its first 8 MiB hold fold words and arrival counters that every call
+    returns to zero, so two streams (a HIP-graph capture runs on a side stream) must not share it.  A buffer is
+    allocated and zeroed eagerly; inside a capture it must already exist, since an allocation there would come from
+    the graph's pool and its zero-fill would only be recorded.  A buffer that a larger one replaces stays alive for
+    the life of the process: a captured graph may still point at it."""
 
     def __init__(self) -> None:
         self._buf: dict = {}
+        self._retired: list = []
+
+    # The three hooks below are the only places that touch the device (a CPU test replaces them).
+    def _stream_handle(self, dev: torch.device) -> int:
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    def _capturing(self) -> bool:
+        return torch.cuda.is_current_stream_capturing()
+
+    def _new(self, dev: torch.device, size: int, handle: int) -> torch.Tensor:
+        buf = torch.empty(size, dtype=torch.uint8, device=dev)
+        _check(_lib.load().exl3_workspace_init(buf.data_ptr(), buf.numel(), ctypes.c_void_p(handle)))
+        return buf
 
     def get(self, dev: torch.device, nbytes: int) -> torch.Tensor:
-        key = (dev.type, dev.index)
+        handle = self._stream_handle(dev)
+        key = (dev.type, dev.index, handle)
         buf = self._buf.get(key)
         if buf is None or buf.numel() < nbytes:
+            if self._capturing():
+                raise Exl3WorkspaceTooSmall(
+                    f"workspace of {nbytes} bytes is not allocated for this stream: make one eager call on the "
+                    "capturing stream (or workspace.reserve) before the capture")
             size = max(nbytes, 1 << 20, 0 if buf is None else buf.numel() * 2)
-            buf = torch.empty(size, dtype=torch.uint8, device=dev)
-            _check(_lib.load().exl3_workspace_init(buf.data_ptr(), buf.numel(), _stream(dev)))
-            self._buf[key] = buf
+            new = self._new(dev, size, handle)
+            if buf is not None:
+                self._retired.append(buf)
+            self._buf[key] = buf = new
         return buf
+
+    def reserve(self, dev: torch.device, nbytes: int) -> None:
+        """Allocates (outside any capture) the current stream's buffer of at least `nbytes`."""
+        self.get(dev, nbytes)
 
 
 workspace = _Workspace()
@@ -378,6 +408,27 @@ def _u16_check(t: torch.Tensor, what: str) -> None:
 def _f16_check(t: torch.Tensor, what: str) -> None:
     if t.dtype != torch.float16:
         raise BadExl3Dtype(f"{what} must be float16")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Arm overrides (tests and tuning sweeps; exl3_set_override in the C ABI)
+
+KNOBS = {"gemv_splits": 0, "gemv_separate_finish": 1, "gemv_fold": 2, "moe_decode_rows_max": 3, "moe_splits1": 4,
+         "moe_splits2": 5, "moe_windows": 6, "moe_fold": 7}
+
+
+@contextlib.contextmanager
+def arm_overrides(**knobs: int):
+    """Pins library arms for the duration of a ``with`` block (e.g. ``arm_overrides(gemv_splits=8, gemv_fold=0)``);
+    every knob named is unset again on exit."""
+    L = _lib.load()
+    try:
+        for name, value in knobs.items():
+            _check(L.exl3_set_override(KNOBS[name], int(value), 1))
+        yield
+    finally:
+        for name in knobs:
+            L.exl3_set_override(KNOBS[name], 0, 0)
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -559,6 +610,7 @@ EXL3_DECLINED = 1
 
 
 _ONE_EXPERT: dict = {}
+_ONE_EXPERT_RETIRED: list = []
 
 
 def _one_expert_routing(rows: int, device: torch.device):
@@ -566,9 +618,15 @@ def _one_expert_routing(rows: int, device: torch.device):
     call launches no fill kernels (the tensors are never written after they are made)."""
     z, o = _ONE_EXPERT.get(device, (None, None))
     if z is None or z.shape[0] < rows:
+        if torch.cuda.is_current_stream_capturing():
+            raise Exl3WorkspaceTooSmall("the one-expert routing tensors must exist before a capture: make one eager "
+                                        "call first")
         cap = max(rows, 64, 2 * (0 if z is None else z.shape[0]))
+        if z is not None:
+            _ONE_EXPERT_RETIRED.append((z, o))  # a captured graph may still read the smaller pair
         z = torch.zeros(cap, 1, dtype=torch.int32, device=device)
         o = torch.ones(cap, 1, dtype=torch.float32, device=device)
+        torch.cuda.current_stream(device).synchronize()  # filled before any other stream reads them
         _ONE_EXPERT[device] = (z, o)
     return z[:rows], o[:rows]
 

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_host_side_refusals():
     lib = L.load()
-    assert lib.exl3_abi_version() == 2
+    assert lib.exl3_abi_version() == 3
     d = L.DecodeT(1, 16, -1)
     # bad shape: in not a multiple of 128 -> refused before any launch (null pointers never touched)
     assert lib.exl3_linear(None, 0, 1, 100, 128, None, 64, None, None, d, None, 0, None, 0, None) == -1
@@ -115,3 +115,58 @@ def test_bench_refuses_more_than_one_gpu_before_touching_one():
     r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "4"], capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
+
+
+def test_set_override_refuses_unknown_knobs_and_the_reserved_value():
+    lib = L.load()
+    assert lib.exl3_set_override(99, 1, 1) == -1
+    assert lib.exl3_set_override(0, -2 ** 31, 1) == -1
+    assert lib.exl3_set_override(0, 4, 1) == 0 and lib.exl3_set_override(0, 0, 0) == 0
+    with exl3.arm_overrides(gemv_splits=2, moe_fold=0):
+        pass  # set and unset again on exit
+
+
+class _CpuWorkspace(exl3._Workspace):
+    """The workspace cache with its device hooks replaced: streams are plain handles, buffers CPU tensors."""
+
+    def __init__(self):
+        super().__init__()
+        self.stream = 1
+        self.capturing = False
+        self.made = []
+
+    def _stream_handle(self, dev):
+        return self.stream
+
+    def _capturing(self):
+        return self.capturing
+
+    def _new(self, dev, size, handle):
+        import torch
+
+        self.made.append((handle, size))
+        return torch.zeros(size, dtype=torch.uint8)
+
+
+def test_workspace_is_one_buffer_per_stream_and_keeps_grown_out_buffers():
+    import torch
+
+    ws = _CpuWorkspace()
+    dev = torch.device("cpu")
+    a = ws.get(dev, 100)
+    assert ws.get(dev, 100) is a                      # the same stream reuses its buffer
+    ws.stream = 2
+    b = ws.get(dev, 100)
+    assert b is not a                                  # another stream (a capture's side stream) gets its own
+    ws.stream = 1
+    c = ws.get(dev, (1 << 20) + 1)                     # growth replaces stream 1's buffer...
+    assert c is not a and c.numel() >= (1 << 20) + 1
+    assert any(r is a for r in ws._retired)            # ...and keeps the old one alive for graphs that hold it
+    ws.capturing = True
+    assert ws.get(dev, 10) is c                        # inside a capture an existing buffer serves
+    with pytest.raises(exl3.Exl3WorkspaceTooSmall):
+        ws.get(dev, 1 << 24)                           # but nothing is allocated there
+    ws.stream = 3
+    with pytest.raises(exl3.Exl3WorkspaceTooSmall):
+        ws.get(dev, 10)                                # a stream first seen inside a capture is refused
+    assert [h for h, _ in ws.made] == [1, 2, 1]

@@ -4,8 +4,6 @@ Bar: max |y - y_ref| / max |y_ref| <= 2e-3 with fp16 
 y_ref is the oracle's `project` (src/exl3/expert_exl3.zig:546-566).  The oracle rounds its inner sum to f16 and the
 GPU keeps it in f32, so the two differ by about one f16 ulp of the result; the bar leaves ample room.
 """
-import os
-
 import numpy as np
 import pytest
 import torch
@@ -74,27 +72,19 @@ def test_gemv_generic_rates(dev, n, rows):
     assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, 256, 256, n, odec)) < BAR
 
 
-@pytest.mark.parametrize("splits,separate,fold", [("1", "0", "1"), ("2", "0", "1"), ("2", "0", "0"), ("4", "1", "1"),
-                                                  ("8", "0", "1"), ("8", "0", "0")])
+@pytest.mark.parametrize("splits,separate,fold", [(1, 0, 1), (2, 0, 1), (2, 0, 0), (4, 1, 1), (8, 0, 1), (8, 0, 0)])
 def test_gemv_split_and_finish_arms_agree(dev, splits, separate, fold):
     """Direct finish, the fold (fixed-point accumulation), counters + planes, and the separate finish kernel."""
     print(f"[gemv] splits={splits} separate={separate} fold={fold}", flush=True)
     p, pd, x, xd = _case(dev, 9, 4, 1024, 256, 48)
     dec, odec = DECODES["3inst"]
     want = _oracle(p, x, 1024, 256, 48, odec)
-    os.environ["EXL3_GEMV_SPLITS"] = splits
-    os.environ["EXL3_GEMV_SEPARATE_FINISH"] = separate
-    os.environ["EXL3_GEMV_FOLD"] = fold
-    try:
+    with exl3.arm_overrides(gemv_splits=splits, gemv_separate_finish=separate, gemv_fold=fold):
         for _ in range(3):  # fused finish counters / accumulators must come back to zero between calls
             assert max_abs_rel(_run(pd, xd, dec), want) < BAR
-    finally:
-        del os.environ["EXL3_GEMV_SPLITS"]
-        del os.environ["EXL3_GEMV_SEPARATE_FINISH"]
-        del os.environ["EXL3_GEMV_FOLD"]
 
 
-@pytest.mark.parametrize("fold", ["1", "0"])
+@pytest.mark.parametrize("fold", [1, 0])
 def test_gemv_non_finite_rows(dev, fold):
     """A row whose input holds an inf comes out non-finite in every output under both split finishes (the fold marks
     non-finite contributions and yields NaN); the other rows stay within the bar and the accumulators stay clean."""
@@ -104,16 +94,11 @@ def test_gemv_non_finite_rows(dev, fold):
     want = _oracle(p, x, 1024, 256, 64, odec)
     xbad = xd.clone()
     xbad[1, 5] = float("inf")
-    os.environ["EXL3_GEMV_SPLITS"] = "8"
-    os.environ["EXL3_GEMV_FOLD"] = fold
-    try:
+    with exl3.arm_overrides(gemv_splits=8, gemv_fold=fold):
         y = _run(pd, xbad, dec)
         assert not np.isfinite(y[1]).any()
         assert max_abs_rel(y[[0, 2]], want[[0, 2]]) < BAR
         assert max_abs_rel(_run(pd, xd, dec), want) < BAR  # the next call starts from clean words
-    finally:
-        del os.environ["EXL3_GEMV_SPLITS"]
-        del os.environ["EXL3_GEMV_FOLD"]
 
 
 @pytest.mark.parametrize("rows", [2, 12, 24])
@@ -218,3 +203,49 @@ def test_c2_shapes_mcg(dev, in_f, out_f, n):
     p, pd, x, xd = _case(dev, 1, 4, in_f, out_f, n)
     dec, odec = DECODES["mcg"]
     assert max_abs_rel(_run(pd, xd, dec), _oracle(p, x, in_f, out_f, n, odec)) < BAR
+
+
+def _big_case(dev, seed, rows, in_f, out_f, n, svh_scale, x_scale):
+    """Outputs far past the fold's fixed-point range: svh times svh_scale (still f16), x times x_scale; the exact
+    f64 truth of the f16 inputs."""
+    from tests import _parity as P
+
+    p = synth.proj(seed, "big", 1, in_f, out_f, n)
+    svh = (p.svh.float() * svh_scale).half()
+    x = (synth.normal(seed, "xbig", (rows, in_f)).float() * x_scale).half()
+    pd = exl3.Proj(p.trellis.to(dev), p.suh.to(dev), svh.to(dev))
+    pr = P.prepared_rows(x.float().numpy(), p.suh.numpy().view(np.uint16)[0])
+    w = P.decoded(p.trellis.numpy().view(np.uint16)[0], in_f, out_f, n, DECODES["3inst"][1])
+    y64 = P.f16_bits(svh.numpy().view(np.uint16)[0]) * P.hadamard_blocks(pr @ w)
+    return pd, x.to(dev), y64
+
+
+@pytest.mark.parametrize("splits", [8, 16])
+@pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16, torch.float32])
+def test_outputs_past_the_fold_range(dev, ydt, splits):
+    """Split partials past 2^21 (the fold's fixed-point range) take its f64 overflow words: bf16 and f32 outputs of
+    ~10^7 come out finite and within the bar of the exact value, and f16 outputs past 65504 come out +-inf with the
+    exact value's sign (never NaN); the words are clean for the next call."""
+    print(f"[gemv] big outputs {ydt} splits={splits}", flush=True)
+    pd, xd, y64 = _big_case(dev, 23, 2, 4096, 1024, 64, 1024.0, 128.0)
+    assert np.abs(y64).max() > 2.0 ** 23
+    dec = DECODES["3inst"][0]
+    with exl3.arm_overrides(gemv_splits=splits):
+        for _ in range(2):
+            y = exl3.linear(xd, pd, dec, out_dtype=ydt).float().cpu().numpy().astype(np.float64)
+            if ydt == torch.float16:
+                over = np.abs(y64) > 65520.0 * 1.002
+                under = np.abs(y64) < 65504.0 * 0.998
+                assert over.any() and under.any()
+                assert np.isinf(y[over]).all() and (np.sign(y[over]) == np.sign(y64[over])).all()
+                assert np.isfinite(y[under]).all()
+                # the north-star metric: error over the largest exact output (the finite outputs here are
+                # cancellations of partials near 10^7, so one f16 ulp of a prepared input moves them by hundreds)
+                assert np.max(np.abs(y[under] - y64[under])) / np.abs(y64).max() < BAR
+            else:
+                bar = BAR + (2.0 ** -8 if ydt == torch.bfloat16 else 0.0)
+                assert max_abs_rel(y, y64) < bar
+    # the overflow and fold words are back at zero: an ordinary call on the same workspace is exact
+    p, pd2, x, xd2 = _case(dev, 11, 3, 1024, 256, 64)
+    with exl3.arm_overrides(gemv_splits=8):
+        assert max_abs_rel(_run(pd2, xd2, DECODES["mcg"][0]), _oracle(p, x, 1024, 256, 64, DECODES["mcg"][1])) < BAR

@@ -190,19 +190,14 @@ def test_moe_sorted_arm_concentrated_routing(dev):
 
 def test_moe_sorted_and_per_slot_arms_agree(dev):
     """The sorted arm (expert windows) and the per-slot chain give the same layer to the bar on one routing."""
-    import os
-
     E, hidden, inter, k, rows, n = 32, 256, 256, 8, 24, 32
     b = _to(synth.bank(11, "moea", E, hidden, inter, n), dev)
     x = synth.normal(11, "x", (rows, hidden)).to(dev)
     inds, scores = _route(11, rows, E, k)
     xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
     sorted_arm = exl3.moe(x, b, xi, sc, exl3.MCG).float().cpu().numpy()
-    os.environ["EXL3_MOE_WINDOWS"] = "0"
-    try:
+    with exl3.arm_overrides(moe_windows=0):
         per_slot = exl3.moe(x, b, xi, sc, exl3.MCG).float().cpu().numpy()
-    finally:
-        del os.environ["EXL3_MOE_WINDOWS"]
     assert max_abs_rel(sorted_arm, per_slot) < BAR
 
 
@@ -212,8 +207,6 @@ def test_moe_fold_and_reduce_arms_agree(dev, rows, with_shared):
     """The down projection folded straight into y and the planes + reduce launch agree to the bar against the
     oracle (per-slot arm up to 8 rows, sorted arm above), with and without a shared expert, and the accumulators
     are clean for the next call."""
-    import os
-
     print(f"[moe] fold arms rows={rows} shared={with_shared}", flush=True)
     E, hidden, inter, k, n = 24, 256, 384, 6, 32
     b = synth.bank(13, "moef", E, hidden, inter, n)
@@ -227,18 +220,15 @@ def test_moe_fold_and_reduce_arms_agree(dev, rows, with_shared):
     xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
     shd = None if sh is None else sh.to(dev)
     got = {}
-    for fold in ("1", "0", "1"):
-        os.environ["EXL3_MOE_FOLD"] = fold
-        try:
+    for fold in (1, 0, 1):
+        with exl3.arm_overrides(moe_fold=fold):
             y = exl3.moe_with_shared(x.to(dev), bd, xi, sc, exl3.MCG, False, shd) if with_shared else \
                 exl3.moe(x.to(dev), bd, xi, sc, exl3.MCG)
-        finally:
-            del os.environ["EXL3_MOE_FOLD"]
         got.setdefault(fold, []).append(y.float().cpu().numpy())
     for ys in got.values():
         for y in ys:
             assert max_abs_rel(y, want) < BAR
-    assert np.array_equal(got["1"][0], got["1"][1])  # exact accumulation: the same bytes on every call
+    assert np.array_equal(got[1][0], got[1][1])  # exact accumulation: the same bytes on every call
 
 
 def test_router_matches_oracle(dev):
@@ -247,6 +237,30 @@ def test_router_matches_oracle(dev):
     oi, os_ = O.route_topk(logits.numpy(), 8)
     assert (inds.cpu().numpy().view(np.uint32) == oi).all()
     assert np.allclose(scores.cpu().numpy(), os_, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("experts,k", [(40, 8), (256, 8), (300, 32)])
+def test_router_non_finite_logits_match_oracle(dev, experts, k):
+    """All-NaN, partly NaN, all -inf, mostly -inf and +inf rows: every pick is a distinct expert in range, equal to
+    the oracle's (NaN selects as -inf, ties to the lower index), and the scores match it, NaN where it has NaN."""
+    print(f"[router] non-finite E={experts} k={k}", flush=True)
+    rng = np.random.default_rng(experts + k)
+    lg = rng.standard_normal((7, experts)).astype(np.float32)
+    lg[0, :] = np.nan
+    lg[1, ::3] = np.nan
+    lg[2, :] = -np.inf
+    lg[2, [5, experts - 1]] = [1.0, -2.0]
+    lg[3, :] = -np.inf
+    lg[3, experts // 2] = np.nan
+    lg[4, [0, 1, 2]] = np.inf
+    lg[5, :] = 0.0
+    inds, scores = exl3.moe_routing_chain(torch.from_numpy(lg).to(dev), k)
+    torch.cuda.synchronize()
+    oi, os_ = O.route_topk(lg, k)
+    gi = inds.cpu().numpy().view(np.uint32)
+    assert (gi == oi).all()
+    assert all(len(set(r.tolist())) == k for r in gi) and gi.max() < experts
+    assert np.allclose(scores.cpu().numpy(), os_, rtol=1e-5, atol=1e-7, equal_nan=True)
 
 
 def test_tile_major_matches_oracle(dev):
@@ -381,3 +395,37 @@ def test_moe_ragged_with_shared_bank_is_the_two_calls(dev, rows):
     o = torch.ones(rows, 1, dtype=torch.float32, device=dev)
     ref = exl3.moe_ragged(x, rb, xi, sc, dec, shared=exl3.moe(x, sd, z, o, dec))
     assert max_abs_rel(y.float().cpu().numpy(), ref.float().cpu().numpy()) < BAR
+
+
+@pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16])
+def test_moe_down_fold_outputs_past_its_range(dev, ydt):
+    """The down projection's fold across slots with contributions past 2^21: bf16 outputs finite within the bar of
+    the exact chain, f16 outputs past 65504 +-inf (never NaN)."""
+    from tests import _parity as P
+
+    print(f"[moe] big outputs {ydt}", flush=True)
+    E, hidden, inter, k, rows, n = 8, 256, 256, 4, 3, 32
+    b = synth.bank(29, "moebig", E, hidden, inter, n)
+    b.down.svh = (b.down.svh.float() * 1024).half()
+    x = (synth.normal(29, "x", (rows, hidden)).float() * 4).half()
+    inds, scores = _route(29, rows, E, k)
+    bd = _to(b, dev)
+    y = exl3.moe(x.to(dev).to(ydt), bd, torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev),
+                 exl3.MCG).float().cpu().numpy().astype(np.float64)
+    odec = O.decode(O.CB_MCG)
+    svh = b.down.svh.numpy().view(np.uint16)
+    y64 = np.zeros((rows, hidden))
+    from tests.test_gpu_parity import _moe_truth
+    xf = x.to(ydt).float().numpy()
+    for r in range(rows):
+        for j in range(k):
+            e = int(inds[r, j])
+            t = _moe_truth(b, xf[r:r + 1], [e], (odec, odec, odec))
+            y64[r] += float(scores[r, j]) * P.f16_bits(svh[e]) * P.hadamard_blocks(t.inner[0])
+    assert np.abs(y64).max() > 2.0 ** 21
+    if ydt == torch.float16:
+        over, under = np.abs(y64) > 65520.0 * 1.002, np.abs(y64) < 65504.0 * 0.998
+        assert np.isinf(y[over]).all() and (np.sign(y[over]) == np.sign(y64[over])).all()
+        assert np.isfinite(y[under]).all()
+    else:
+        assert max_abs_rel(y, y64) < BAR + 2.0 ** -8

@@ -1,0 +1,268 @@
+"""GPU parity on the summand-relative bar (tests/_parity.py), with the reference's mutation arms and seed sweep.
+
+Every arm runs with f32 outputs; its finish is undone exactly and each inner element is held to the f64 dot product
+of the oracle's decoded weights, relative to that element's summand scale (src/exl3/expert_exl3_kernels.zig:
+3310-3330).  Each case then checks that the same bar FAILS when the truth reads the wrong codeword window or one
+flipped trellis bit (:3330-3352), so a decode defect that touches a single weight cannot pass.  The headline shapes
+sweep PARITY_SEEDS = 8 seeds (:4550).  The north-star bar (max-abs-rel 2e-3 of the f16 output) is in
+test_gpu_linear.py / test_gpu_moe.py; this bar is the stricter one.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from sushi_amd import exl3, synth
+from tests import _parity as P
+
+pytestmark = pytest.mark.gpu
+
+DECODES = {
+    "mcg": (exl3.Decode(exl3.Codebook.mcg), O.decode(O.CB_MCG)),
+    "mul1": (exl3.Decode(exl3.Codebook.mul1), O.decode(O.CB_MUL1)),
+    "3inst": (exl3.Decode(exl3.Codebook.inst3), O.decode(O.CB_3INST)),
+    "spec1": (exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1), O.decode(O.CB_SPEC1, 15, 1)),
+    "std1": (exl3.Decode(exl3.Codebook.std1, exl3.Window(15), 3), O.decode(O.CB_STD1, 15, 3)),
+    "pair1": (exl3.Decode(exl3.Codebook.pair1), O.decode(O.CB_PAIR1)),
+    "mcg_w12": (exl3.Decode(exl3.Codebook.mcg, exl3.Window(12)), O.decode(O.CB_MCG, 12)),
+}
+
+
+def _u16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint16)
+
+
+class Dense:
+    """One seeded dense projection [in, out] at rate n and `rows` input rows, on the device and as oracle inputs."""
+
+    def __init__(self, dev, seed, rows, in_f, out_f, n):
+        self.in_f, self.out_f, self.n = in_f, out_f, n
+        p = synth.proj(seed, f"par{in_f}x{out_f}.{n}", 1, in_f, out_f, n)
+        self.x = synth.normal(seed, f"par.x{rows}.{in_f}", (rows, in_f))
+        self.t, self.suh, self.svh = _u16(p.trellis)[0], _u16(p.suh)[0], _u16(p.svh)[0]
+        self.pd = exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev))
+        self.xd = self.x.to(dev)
+        self.p = P.prepared_rows(self.x.float().numpy(), self.suh)
+
+    def inner(self, dec) -> np.ndarray:
+        y = exl3.linear(self.xd, self.pd, dec, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        return P.inner_from_output(y.cpu().numpy(), self.svh)
+
+    def truth(self, odec) -> P.Truth:
+        return P.truth(self.p, P.decoded(self.t, self.in_f, self.out_f, self.n, odec))
+
+
+def _hold(got: np.ndarray, d: Dense, odec, seed: int, mutate: bool = True, what: str = "") -> None:
+    """The arm passes the bar; with `mutate`, the same output fails it against the window and flipped-bit mutants."""
+    t = d.truth(odec)
+    print(f"[parity] {what} worst error / ceiling = {P.worst_ratio(got, t):.4f}", flush=True)
+    why = P.verdict(got, t)
+    assert why is None, f"{what}: {why}"
+    if not mutate:
+        return
+    tw = P.with_inner(t, d.p @ P.decoded(d.t, d.in_f, d.out_f, d.n, P.mutated_window(odec)))
+    assert P.verdict(got, tw) is not None, f"{what}: the window mutation passed the bar"
+    tb, where = P.flipped_truth(t, d.p, d.t, d.n, odec, np.random.default_rng(seed))
+    assert P.verdict(got, tb) is not None, f"{what}: the flipped bit {where} passed the bar"
+
+
+# ---- decode GEMV (1..16 rows) -------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows", [1, 4, 16])
+@pytest.mark.parametrize("n", [32, 48, 64])
+@pytest.mark.parametrize("label", list(DECODES))
+def test_gemv_codebooks_rates_rows(dev, label, n, rows):
+    d = Dense(dev, 300 + n + rows, rows, 512, 384, n)
+    dec, odec = DECODES[label]
+    _hold(d.inner(dec), d, odec, seed=n + rows, what=f"gemv {label} n={n} rows={rows}")
+
+
+@pytest.mark.parametrize("n,label", [(16, "spec1"), (24, "pair1"), (40, "3inst"), (22, "spec1"), (44, "pair1"),
+                                     (96, "spec1"), (128, "spec1")])
+def test_gemv_other_rates(dev, n, label):
+    """n = 16, 24, 40 on the lane reader; 22, 44, 96, 128 on the generic reader."""
+    d = Dense(dev, 400 + n, 3, 256, 256, n)
+    dec, odec = DECODES[label]
+    _hold(d.inner(dec), d, odec, seed=n, what=f"gemv {label} n={n}")
+
+
+@pytest.mark.parametrize("splits,separate", [(1, 0), (2, 0), (4, 1), (8, 0)])
+def test_gemv_split_arms(dev, splits, separate):
+    """Direct finish, counters + planes, and the separate finish kernel (an f32 output never takes the fold)."""
+    d = Dense(dev, 17, 4, 1024, 256, 48)
+    dec, odec = DECODES["3inst"]
+    with exl3.arm_overrides(gemv_splits=splits, gemv_separate_finish=separate):
+        for _ in range(2):
+            _hold(d.inner(dec), d, odec, seed=splits, mutate=False, what=f"split {splits} separate {separate}")
+
+
+@pytest.mark.parametrize("seed", range(P.PARITY_SEEDS))
+def test_c1_headline_shape_every_seed(dev, seed):
+    """configs[0]'s shape as bench.py runs it: 4096 x 4096, K4 (n64), 3INST, batch 1."""
+    d = Dense(dev, seed, 1, 4096, 4096, 64)
+    dec, odec = DECODES["3inst"]
+    _hold(d.inner(dec), d, odec, seed=seed, what=f"c1 seed {seed}")
+
+
+@pytest.mark.parametrize("rows", [1, 4, 16])
+@pytest.mark.parametrize("n", [32, 48, 64])
+@pytest.mark.parametrize("in_f,out_f", [(2048, 2048), (4096, 14336), (14336, 4096)])
+def test_c2_shapes(dev, in_f, out_f, n, rows):
+    """configs[1] at full size: MCG, K = 2/3/4, batch 1/4/16."""
+    d = Dense(dev, 1, rows, in_f, out_f, n)
+    dec, odec = DECODES["mcg"]
+    _hold(d.inner(dec), d, odec, seed=rows, mutate=in_f == out_f, what=f"c2 {in_f}x{out_f} n={n} rows={rows}")
+
+
+# ---- GEMM arm (rows > 16) -----------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows", [17, 40, 130, 300])
+@pytest.mark.parametrize("n", [32, 40, 48, 64])
+def test_gemm_rates_rows(dev, n, rows):
+    d = Dense(dev, 500 + rows, rows, 1024, 512, n)
+    dec, odec = DECODES["3inst"]
+    _hold(d.inner(dec), d, odec, seed=rows, what=f"gemm n={n} rows={rows}")
+
+
+@pytest.mark.parametrize("label", ["mcg", "mul1", "spec1", "std1", "pair1", "mcg_w12"])
+def test_gemm_codebooks(dev, label):
+    d = Dense(dev, 77, 24, 512, 256, 48)
+    dec, odec = DECODES[label]
+    _hold(d.inner(dec), d, odec, seed=5, what=f"gemm {label}")
+
+
+@pytest.mark.parametrize("seed", range(P.PARITY_SEEDS))
+def test_gemm_every_seed(dev, seed):
+    d = Dense(dev, 900 + seed, 64, 2048, 1024, 48)
+    dec, odec = DECODES["3inst"]
+    _hold(d.inner(dec), d, odec, seed=seed, what=f"gemm seed {seed}")
+
+
+@pytest.mark.parametrize("rows,out_f", [(512, 14336), (2048, 1024), (2048, 14336)])
+def test_c3_prefill_shapes(dev, rows, out_f):
+    """4096 x 14336, K3, 3INST at M = 512 (row tiles 2: the XCD remap with 4 output groups per XCD
+    round) and M = 2048 (row tiles 8: one output group per XCD round), and M = 2048 at out 1024 (the same branch on a
+    grid of one round)."""
+    d = Dense(dev, 3, rows, 4096, out_f, 48)
+    dec, odec = DECODES["3inst"]
+    _hold(d.inner(dec), d, odec, seed=rows, mutate=out_f == 1024, what=f"c3 M={rows} out={out_f}")
+
+
+# ---- routed experts -------------------------------------------------------------------------------------------------
+#
+# The routed layer sums its slots with per-expert svh, which no single inverse undoes; so these cases route every
+# slot of a row to ONE expert (topk = 1, or topk copies of it with scores summing to 1), where
+# y = (sum of scores) * svh_down[e] * H(inner_down) is undone exactly.  The routed decode, the per-slot and sorted
+# arms, the mid and the slot reduce all run as usual.
+
+
+def _moe_truth(bank, x, experts_of_row, odecs, clamp=0.0):
+    """Exact down inner products of each row's expert, the chain's rounding points (tests/_parity.down_prepared)."""
+    hidden = x.shape[1]
+    g, u, dn = bank.gate, bank.up, bank.down
+    inter = g.out_features
+    ng, nu, nd = g.n, u.n, dn.n
+    cache = {}
+    rows_p, rows_w = [], []
+    for r, e in enumerate(experts_of_row):
+        if e not in cache:
+            wg = P.decoded(_u16(g.trellis)[e], hidden, inter, ng, odecs[0])
+            wu = P.decoded(_u16(u.trellis)[e], hidden, inter, nu, odecs[1])
+            wd = P.decoded(_u16(dn.trellis)[e], inter, hidden, nd, odecs[2])
+            cache[e] = (wg, wu, wd)
+        wg, wu, wd = cache[e]
+        pg = P.prepared_rows(x[r:r + 1], _u16(g.suh)[e])
+        pu = P.prepared_rows(x[r:r + 1], _u16(u.suh)[e])
+        gv = P.f16_bits(_u16(g.svh)[e]) * P.hadamard_blocks(pg @ wg)
+        uv = P.f16_bits(_u16(u.svh)[e]) * P.hadamard_blocks(pu @ wu)
+        pd = P.down_prepared(gv, uv, _u16(dn.suh)[e], clamp)
+        rows_p.append(pd[0])
+        rows_w.append(wd)
+    inner = np.stack([p @ w for p, w in zip(rows_p, rows_w)])
+    amag = np.stack([np.abs(p) @ np.abs(w) for p, w in zip(rows_p, rows_w)])
+    bound = np.stack([np.abs(p).max() * np.abs(w).max(axis=0) for p, w in zip(rows_p, rows_w)])
+    return P.Truth(inner, amag, bound, inter)
+
+
+def _moe_inner(y, bank, experts_of_row, score_sum):
+    svh = _u16(bank.down.svh)
+    return np.stack([P.inner_from_output(y[r] / score_sum[r], svh[e]) for r, e in enumerate(experts_of_row)])
+
+
+def _moe_case(dev, seed, rows, topk, E=32, hidden=512, inter=256, n=32):
+    b = synth.bank(seed, f"pmoe{E}.{n}", E, hidden, inter, n)
+    bd = exl3.Bank(*(exl3.Proj(q.trellis.to(dev), q.suh.to(dev), q.svh.to(dev)) for q in (b.gate, b.up, b.down)))
+    x = synth.normal(seed, f"pmoe.x{rows}", (rows, hidden))
+    rng = np.random.default_rng(seed)
+    experts = rng.integers(0, E, size=rows)
+    inds = np.repeat(experts[:, None], topk, axis=1).astype(np.int32)
+    sc = rng.uniform(0.5, 1.5, size=(rows, topk)).astype(np.float32)
+    sc /= sc.sum(axis=1, keepdims=True)
+    score_sum = sc.sum(axis=1, dtype=np.float64)[:, None]
+    return b, bd, x, experts, torch.from_numpy(inds).to(dev), torch.from_numpy(sc).to(dev), score_sum
+
+
+@pytest.mark.parametrize("rows", [1, 5, 12, 40])
+@pytest.mark.parametrize("topk", [1, 4])
+def test_moe_chain_per_slot_and_sorted_arms(dev, rows, topk):
+    """Up to 8 rows the per-slot arm, above it the expert windows; the planes + reduce finish (f32 output)."""
+    b, bd, x, experts, inds, sc, ssum = _moe_case(dev, 60 + rows, rows, topk)
+    odec = O.decode(O.CB_MCG)
+    y = exl3.moe(x.to(dev).float(), bd, inds, sc, exl3.MCG)
+    torch.cuda.synchronize()
+    got = _moe_inner(y.cpu().numpy().astype(np.float64), b, experts, ssum)
+    xf = x.float().numpy()
+    t = _moe_truth(b, xf, experts, (odec, odec, odec))
+    print(f"[parity] moe rows={rows} topk={topk} worst error / ceiling = {P.worst_ratio(got, t):.4f}", flush=True)
+    assert P.verdict(got, t) is None, P.verdict(got, t)
+    # mutations: the truth reads w15, or one flipped bit in the down bank / the gate bank of row 0's expert
+    w15 = P.mutated_window(odec)
+    assert P.verdict(got, _moe_truth(b, xf, experts, (w15, w15, w15))) is not None
+    e0 = int(experts[0])
+    for proj in ("down", "gate"):
+        q = getattr(b, proj)
+        tr = _u16(q.trellis).copy()
+        pin = P.prepared_rows(xf[:1], _u16(b.gate.suh)[e0]) if proj == "gate" else np.ones((1, q.in_features))
+        tr[e0], where = P.flip_one_bit(tr[e0], q.n, odec, pin, np.random.default_rng(rows + topk))
+        mb = exl3.Bank(b.gate, b.up, b.down)
+        setattr(mb, proj, exl3.Proj(torch.from_numpy(tr.view(np.int16)), q.suh, q.svh))
+        assert P.verdict(got, _moe_truth(mb, xf, experts, (odec, odec, odec))) is not None, (proj, where)
+
+
+@pytest.mark.parametrize("seed", range(P.PARITY_SEEDS))
+def test_moe_every_seed(dev, seed):
+    b, bd, x, experts, inds, sc, ssum = _moe_case(dev, 700 + seed, 6, 1, E=64, hidden=1024, inter=512, n=32)
+    odec = O.decode(O.CB_MCG)
+    y = exl3.moe(x.to(dev).float(), bd, inds, sc, exl3.MCG)
+    torch.cuda.synchronize()
+    got = _moe_inner(y.cpu().numpy().astype(np.float64), b, experts, ssum)
+    t = _moe_truth(b, x.float().numpy(), experts, (odec, odec, odec))
+    assert P.verdict(got, t) is None, P.verdict(got, t)
+
+
+@pytest.mark.parametrize("rows", [3, 20])
+def test_moe_ragged_spec1_k1_k2(dev, rows):
+    """The rate-grouped bank (rate_groups.zig:22-140): SPEC1 (spec1-w15 table) experts at n16 and n32."""
+    E1, E2, hidden, inter = 8, 24, 512, 256
+    dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
+    odec = O.decode(O.CB_SPEC1, 15, 1)
+    g1 = synth.bank(81, "prg1", E1, hidden, inter, 16)
+    g2 = synth.bank(81, "prg2", E2, hidden, inter, 32)
+    todev = lambda b: exl3.Bank(*(exl3.Proj(q.trellis.to(dev), q.suh.to(dev), q.svh.to(dev))  # noqa: E731
+                                  for q in (b.gate, b.up, b.down)))
+    rb = exl3.Ragged.init([todev(g1), todev(g2)])
+    x = synth.normal(81, f"prg.x{rows}", (rows, hidden))
+    rng = np.random.default_rng(rows)
+    experts = rng.integers(0, E1 + E2, size=rows)
+    inds = torch.from_numpy(experts[:, None].astype(np.int32)).to(dev)
+    sc = torch.ones(rows, 1, dtype=torch.float32, device=dev)
+    y = exl3.moe_ragged(x.to(dev).float(), rb, inds, sc, dec).cpu().numpy().astype(np.float64)
+    xf = x.float().numpy()
+    for r, e in enumerate(experts):
+        grp, local = (g1, e) if e < E1 else (g2, e - E1)
+        got = P.inner_from_output(y[r:r + 1], _u16(grp.down.svh)[local])
+        t = _moe_truth(grp, xf[r:r + 1], [local], (odec, odec, odec))
+        assert P.verdict(got, t) is None, (r, e, P.verdict(got, t))

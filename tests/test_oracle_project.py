@@ -117,6 +117,38 @@ def test_route_topk_against_numpy():
     assert inds[0, 0] == 3 and inds[0, 1] == 9
 
 
+def _nonfinite_logit_rows():
+    rng = np.random.default_rng(12)
+    rows = rng.standard_normal((6, 40)).astype(np.float32)
+    rows[0, :] = np.nan                                   # all NaN
+    rows[1, ::3] = np.nan                                 # partly NaN
+    rows[2, :] = -np.inf                                  # all -inf
+    rows[2, [5, 17]] = [1.0, -2.0]                        # mostly -inf: two finite experts
+    rows[3, :] = -np.inf
+    rows[3, 7] = np.nan                                   # -inf with one NaN
+    rows[4, [0, 1, 2]] = np.inf                           # +inf ties: lowest index first
+    rows[5, :] = 0.0                                      # every key tied
+    return rows
+
+
+def test_route_topk_non_finite_rows_pick_distinct_experts_in_range():
+    """NaN selects as -inf and an expert is never picked twice, so every pick is a distinct index in range; the
+    order is the stable descending sort of the keys (numpy's argsort, an independent statement)."""
+    logits = _nonfinite_logit_rows()
+    k = 8
+    inds, scores = O.route_topk(logits, k)
+    for r in range(logits.shape[0]):
+        keys = np.where(np.isnan(logits[r]), -np.inf, logits[r]).astype(np.float64)
+        want = np.argsort(-keys, kind="stable")[:k]
+        assert inds[r].tolist() == want.tolist(), r
+        assert len(set(inds[r].tolist())) == k and inds[r].max() < logits.shape[1]
+    assert np.isnan(scores[[0, 1, 3]]).all()              # a NaN logit reaches the softmax
+    assert np.isnan(scores[4]).all()                      # +inf - max(+inf) is NaN
+    p = np.exp(np.array([0.0, -3.0]))                     # two finite experts carry all the mass, the rest none
+    assert np.allclose(scores[2][:2], p / p.sum()) and (scores[2][2:] == 0).all()
+    assert np.isfinite(scores[5]).all() and np.allclose(scores[5], 1.0 / k)
+
+
 def test_tile_major_round_trip_and_reference_layout_case():  # layout.zig:160-175
     it, ot, n = 5, 4, 3
     src = np.arange(it * ot * n, dtype=np.uint16)
