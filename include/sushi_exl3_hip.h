@@ -166,6 +166,21 @@ int32_t exl3_linear_grouped(const void *x, int32_t x_dtype, int32_t groups, int3
                             const uint16_t *svh, exl3_decode_t dec, void *y, int32_t y_dtype, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* `linear.linear` without a workspace, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference, which allocates
+ * per call through MLX.  The same arms and results as exl3_linear; the scratch is a static device array of
+ * EXL3_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends, so the call itself allocates nothing.
+ * The first call on a device sets that scratch up (its address, and its zeroed region cleared by a fill kernel on
+ * `stream`) and must run outside a stream capture; calls after it may be captured.  Every call on one GPU shares
+ * that GPU's scratch: calls that overlap in time on one GPU (two streams, two threads) race, so issue them in
+ * order.  A call whose scratch (exl3_linear_workspace_size) exceeds the limit returns EXL3_ERR_WORKSPACE before
+ * any launch: the decode GEMV fits at every shape the reference serves; the GEMM arm fits while its prepared input
+ * (rows rounded up to 16, x in f16) stays within the 24 MiB past the zeroed region. */
+#define EXL3_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_t in_features, int32_t out_features,
+                            const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh,
+                            exl3_decode_t dec, void *y, int32_t y_dtype, hipStream_t stream);
+
 /* Clears a workspace once after allocation.  Every workspace begins with an 8 MiB region of fused-finish
  * arrival counters, accumulators and their overflow words that must start at zero; the calls that use them always leave them at zero
  * again, and no other call writes there, so one init per allocation suffices.  Calls that share a workspace must not overlap in time

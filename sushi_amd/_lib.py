@@ -20,6 +20,7 @@ EXPORTS = (
     "exl3_linear",
     "exl3_linear_grouped_workspace_size",
     "exl3_linear_grouped",
+    "exl3_linear_noalloc",
     "exl3_workspace_init",
     "exl3_moe_workspace_size",
     "exl3_moe",
@@ -77,6 +78,7 @@ def load() -> ctypes.CDLL:
     L.exl3_linear_grouped_workspace_size.restype = sz
     L.exl3_linear_grouped_workspace_size.argtypes = [i32, i32, i32, i32, i32]
     L.exl3_linear_grouped.argtypes = [vp, i32, i32, i32, i32, i32, vp, i32, vp, vp, DecodeT, vp, i32, vp, sz, vp]
+    L.exl3_linear_noalloc.argtypes = [vp, i32, i32, i32, i32, vp, i32, vp, vp, DecodeT, vp, i32, vp]
     L.exl3_workspace_init.argtypes = [vp, sz, vp]
     L.exl3_moe_workspace_size.restype = sz
     L.exl3_moe_workspace_size.argtypes = [i32, i32, i32, i32]

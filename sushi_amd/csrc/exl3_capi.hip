@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "sushi_exl3_hip.h"
@@ -153,21 +154,30 @@ size_t linear_ws(int groups, int rows, int in, int out, int n) {
     return gemm_bytes(groups, rows, in, out, n);
 }
 
-int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in, int32_t out,
-                    const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
-                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+// Every refusal of a linear call (all before any HIP call); fam / k receive the decode family and constants.
+int32_t linear_checks(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in, int32_t out,
+                      const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh,
+                      const exl3_decode_t &dec, const void *y, int32_t y_dtype, int *fam, DecodeK *k) {
     if (groups <= 0 || rows < 0 || in <= 0 || out <= 0 || in % 128 || out % 128)
         return fail(EXL3_ERR_BAD_SHAPE, "linear: groups=%d rows=%d in=%d out=%d (in and out must be multiples of 128)",
                     groups, rows, in, out);
     if (!rate_admitted(n)) return fail(EXL3_ERR_BAD_SHAPE, "linear: n=%d is not an admitted rate", n);
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(EXL3_ERR_BAD_DTYPE, "linear: unsupported dtype");
-    int fam;
-    DecodeK k;
-    int32_t rc = resolve_decode(dec, n, &fam, &k);
+    int32_t rc = resolve_decode(dec, n, fam, k);
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !trellis || !suh || !svh || !y) return fail(EXL3_ERR_BAD_SHAPE, "linear: null operand");
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "linear: x must be 4-byte aligned");
+    return ok();
+}
+
+int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in, int32_t out,
+                    const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
+                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+    int fam;
+    DecodeK k;
+    int32_t rc = linear_checks(x, x_dtype, groups, rows, in, out, trellis, n, suh, svh, dec, y, y_dtype, &fam, &k);
+    if (rc || rows == 0) return rc;
     const size_t need = linear_ws(groups, rows, in, out, n);
     if (ws_bytes < need || (need && (!ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))))
         return fail(EXL3_ERR_WORKSPACE, "linear: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
@@ -497,6 +507,51 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     return launched(run_moe_reduce(r, stream), "exl3_moe (reduce)");
 }
 
+// ---- Static scratch for exl3_linear_noalloc ------------------------------------------------------------------
+// The device memory of exl3_linear_noalloc: a file-scope device array that every GPU the library loads on holds
+// until the process ends.  In host code `scratch` is only a stand-in for the symbol, never a device address: its
+// address on a device comes from hipGetSymbolAddress, taken once per device (with that device current) at the
+// entry point's first call there and kept per device; every launch and fill uses that address.  The first
+// kZeroBytes carry the fused finish's counters, fold words and overflow words, which must start at zero: the same
+// first call clears them with the fill kernel, and every call leaves them at zero again.
+constexpr size_t kNoallocScratchBytes = EXL3_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoallocScratchBytes > kZeroBytes, "the static scratch holds the zeroed region and more");
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_at[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+
+// This device's scratch address (set up on first use: symbol address, then the zeroed region cleared on `stream`).
+int32_t noalloc_scratch(hipStream_t stream, void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(EXL3_ERR_LAUNCH, "linear_noalloc: no current device (%s)", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_at[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return fail(EXL3_ERR_LAUNCH, "linear_noalloc: %s", hipGetErrorString(e));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(EXL3_ERR_WORKSPACE, "linear_noalloc: the first call on device %d sets up its static scratch "
+                                            "and must run outside a stream capture", dev);
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(EXL3_ERR_LAUNCH, "linear_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        e = run_fill_zero(p, kZeroBytes, stream);
+        if (e != hipSuccess) return launched(e, "linear_noalloc (scratch set-up)");
+        g_scratch_at[dev] = p;
+    }
+    *out = g_scratch_at[dev];
+    return ok();
+}
+
 int32_t declined(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int32_t declined(const char *fmt, ...) {
     char buf[512];
@@ -594,6 +649,27 @@ int32_t exl3_linear_grouped(const void *x, int32_t x_dtype, int32_t groups, int3
                             size_t workspace_bytes, hipStream_t stream) {
     return linear_impl(x, x_dtype, groups, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype,
                        workspace, workspace_bytes, stream);
+}
+
+int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_t in_features, int32_t out_features,
+                            const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh,
+                            exl3_decode_t dec, void *y, int32_t y_dtype, hipStream_t stream) {
+    int fam;
+    DecodeK k;
+    int32_t rc = linear_checks(x, x_dtype, 1, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype,
+                               &fam, &k);
+    if (rc || rows == 0) return rc;
+    const size_t need = linear_ws(1, rows, in_features, out_features, n);
+    if (need > kNoallocScratchBytes)
+        return fail(EXL3_ERR_WORKSPACE,
+                    "linear_noalloc: rows=%d in=%d out=%d n=%d need %zu bytes of scratch, past the static scratch's %zu "
+                    "(use exl3_linear with a workspace)", rows, in_features, out_features, n, need,
+                    kNoallocScratchBytes);
+    void *ws = nullptr;
+    rc = noalloc_scratch(stream, &ws);
+    if (rc) return rc;
+    return linear_impl(x, x_dtype, 1, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype, ws,
+                       kNoallocScratchBytes, stream);
 }
 
 int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
