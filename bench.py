@@ -2,12 +2,14 @@
 plus the MoE gathered-expert layer (configs[3], batch 1) as a secondary figure.
 
 A step is one call of the hot path (prepare + trellis-decode GEMV + finish) on one token of seeded synthetic fp16
-input.  Weights rotate over 64 resident copies (537 MB > the 256 MB Infinity Cache) so every step streams its
-8.4 MB of packed trellis from HBM.  The timed region is exactly `--steps` calls between two synchronisations; HIP
-events on the launch stream give the per-launch average that the roofline figure uses.
+input.  Weights rotate over 64 resident copies (537 MB > the 256 MB Infinity Cache).  The calls are captured as HIP
+graphs: one graph of the 64 copies and one of the first (steps mod 64).  A timed round is exactly `--steps` calls
+(whole 64-copy replays, then the tail), and an untimed replay of the 64-copy graph precedes every round, so each
+timed call reads a copy last read 64 calls (537 MB of other weights) earlier: from HBM.  Seven rounds are timed
+(each bracketed by synchronisations, HIP events on the launch stream inside) and the median round is reported.
 
-Prints one JSON line (the driver's contract).  `cpu_baseline` times the single-threaded C restatement of the
-reference's CPU path (oracle/, `expert_exl3.project`) on a bounded sample of the same workload.
+Prints one JSON line (the driver's contract).  `cpu_baseline` times the C restatement of the reference's CPU path
+(oracle/, `expert_exl3.project`) on a bounded sample of the same workload, on every host core and on one.
 """
 from __future__ import annotations
 
@@ -23,6 +25,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure (no sparsity)
 COPIES = 64
+ROUNDS = 7
 SWEEP_GRAPHS = True  # --no-graph: the sweep issues every call from Python (for counter passes, one dispatch each)
 
 
@@ -50,7 +53,9 @@ def _capture(calls, dev):
     return g
 
 
-def bench_linear(steps: int, warmup: int, graph_mode: bool = True):
+def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int = ROUNDS):
+    import statistics
+
     import torch
 
     from sushi_amd import exl3, synth
@@ -69,72 +74,90 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True):
         exl3.linear(x, projs[i % COPIES], dec)
     torch.cuda.synchronize()
     # The host side of a call (Python checks + ctypes) costs more than the kernel, so the calls are captured, one per
-    # weight copy, into HIP graphs (outside the timed region) and replayed: the timed region then holds exactly
-    # `steps` library launches back to back, as a native caller would issue them.
+    # weight copy, into HIP graphs (outside the timed region) and replayed: a round then holds exactly `steps`
+    # library launches back to back, as a native caller would issue them.
     full = tail = None
     if graph_mode:
         full = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(COPIES)], dev)
         if steps % COPIES:
             tail = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(steps % COPIES)], dev)
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    if graph_mode:
-        for _ in range(steps // COPIES):
+
+    def evict():
+        # the 64-copy sequence, untimed: every copy the round reads was last read 64 calls earlier
+        if graph_mode:
             full.replay()
-        if tail is not None:
-            tail.replay()
-    else:
-        for i in range(steps):
-            exl3.linear(x, projs[i % COPIES], dec)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ev_ms = e0.elapsed_time(e1)
+        else:
+            for i in range(COPIES):
+                exl3.linear(x, projs[i], dec)
+
+    walls, events = [], []
+    for _ in range(rounds):
+        evict()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        if graph_mode:
+            for _ in range(steps // COPIES):
+                full.replay()
+            if tail is not None:
+                tail.replay()
+        else:
+            for i in range(steps):
+                exl3.linear(x, projs[i % COPIES], dec)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        events.append(e0.elapsed_time(e1))
     bytes_per_call = _algorithmic_bytes(in_f, out_f, n, rows)
-    return dict(wall_s=wall, event_ms=ev_ms, bytes=bytes_per_call, rows=rows, y=y, steps=steps)
+    return dict(wall_s=statistics.median(walls), event_ms=statistics.median(events), bytes=bytes_per_call, rows=rows,
+                y=y, steps=steps, rounds=rounds, wall_rounds_s=walls)
 
 
-def bench_moe(batch: int, layers: int = 16, replays: int = 8):
+def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
     """E=256 routed + shared, hidden 2048, inter 768, K2 MCG, top-8; microseconds per token.
 
-    A dependent chain of `layers` MoE layers (each layer's output is the next layer's input, the reference's
-    bench_util.zig:20-58 method), captured once as a HIP graph and replayed; every layer has its own routing so the
-    distinct experts hit change from layer to layer."""
+    `layers` MoE layers back to back on one stream, captured once as a HIP graph and replayed: the stream runs them
+    in order, as the reference's dependent chain (bench_util.zig:20-58) runs its calls, but each layer reads its own
+    N(0,1) hidden state (an unnormalised chain of SwiGLU layers squares its scale per layer and is inf by the fourth)
+    and every layer has its own routing, so the distinct experts hit change from layer to layer.  The banks' svh
+    carry 1/sqrt(in) (synth norm), keeping each layer's output near unit scale.  Median of `rounds` replays."""
+    import statistics
+
     import torch
 
     from sushi_amd import exl3, synth
 
     dev = torch.device("cuda:0")
     E, hidden, inter, n, k = 256, 2048, 768, 32, 8
-    bank = synth.bank(3, "c4", E, hidden, inter, n, device=dev)
-    shared = synth.bank(3, "c4.shared", 1, hidden, inter, n, device=dev)
-    x0 = synth.normal(3, f"c4.x{batch}", (batch, hidden), device=dev)
+    bank = synth.bank(3, "c4", E, hidden, inter, n, device=dev, norm=True)
+    shared = synth.bank(3, "c4.shared", 1, hidden, inter, n, device=dev, norm=True)
+    xs = [synth.normal(3, f"c4.x{batch}.{layer}", (batch, hidden), device=dev) for layer in range(layers)]
     routes = []
     for layer in range(layers):
         logits = synth.normal(3, f"c4.logits{batch}.{layer}", (batch, E), dtype=torch.float32).to(dev)
         routes.append(exl3.moe_routing_chain(logits, k))
+
     def chain():
-        # routed experts + the shared expert in one call: up to 16 rows both run in the same two launches; wider
-        # batches the library declines and the wrapper runs the shared expert as a one-expert chain first
-        x = x0
-        for inds, scores in routes:
-            x = exl3.moe_with_shared_bank(x, bank, shared, inds, scores, exl3.MCG)
-        return x
+        # routed experts + the shared expert in one call: the fused form runs both in the same launches; where it
+        # declines, the wrapper runs the shared expert as a one-expert chain first
+        return [exl3.moe_with_shared_bank(x, bank, shared, inds, scores, exl3.MCG) for x, (inds, scores) in
+                zip(xs, routes)]
 
     chain()
     torch.cuda.synchronize()
     g = _capture(chain, dev)
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(replays):
+    times = []
+    for _ in range(rounds):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
         g.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    layer_us = e0.elapsed_time(e1) * 1e3 / (replays * layers)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / layers)
+    layer_us = statistics.median(times)
     distinct = sum(len(set(i.flatten().tolist())) for i, _ in routes) / layers
     per_expert = 3 * (hidden * inter * n // 128 + 2 * (hidden + inter))
     return dict(batch=batch, layer_us=layer_us, us_per_token=layer_us / batch, distinct=distinct,
@@ -173,43 +196,88 @@ def _time_linear(in_f, out_f, n, rows, dec, codec_name, seed, min_pool_bytes=640
     return us, copies
 
 
-def measured_ceilings():
-    """Practical ceilings measured on this box beside the vendor peaks: a streaming read (torch's sum over 2 GiB of
-    f16, read-only), a device copy (read + write of 1 GiB), and a copy moving 8 MiB (4 MiB read + 4 MiB written, C1's
-    packed-weight bytes), launched back to back from a HIP graph over 64 rotating pairs: the per-launch floor a kernel
-    of that traffic sits on."""
+def _bench_lib():
+    import ctypes
+
+    path = os.path.join(ROOT, "sushi_amd", "libsushi_bench_hip.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run `python -m sushi_amd.build`")
+    L = ctypes.CDLL(path)
+    L.sb_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    L.sb_stream_read.restype = ctypes.c_int32
+    return L
+
+
+def measured_ceilings(small_bytes: int):
+    """Practical ceilings measured on this box beside the vendor peaks, with this build's streaming-read kernel
+    (sushi_amd/csrc/bench_stream.hip: 16-byte loads, four in flight per thread, nothing written):
+      * hbm_read_GBps: a 1 GiB read, best grid of three, median of 7 launches;
+      * read_small_graph_us: a read of `small_bytes` (C1's packed bytes) per launch, 64 rotating buffers (537 MB, past
+        the Infinity Cache) replayed from a HIP graph, median of 7 rounds: the floor a kernel with C1's traffic sits
+        on, launch cost included;
+      * launch_floor_us: a 16-byte read per launch, from a graph of 64 launches: the launch cost alone."""
+    import ctypes
+    import statistics
+
     import torch
 
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
+    L = _bench_lib()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    hs = ctypes.c_void_p(stream.cuda_stream)
+
+    def read(buf, nbytes, blocks, s=None):
+        rc = L.sb_stream_read(buf.data_ptr(), nbytes, blocks, sink.data_ptr(),
+                              hs if s is None else ctypes.c_void_p(s.cuda_stream))
+        if rc:
+            raise RuntimeError(f"sb_stream_read: hip error {rc}")
 
     def timed(fn, reps):
         fn()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
+        out = []
         for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
             fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3 / reps
+            e1.record(stream)
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) / 1e3)
+        return statistics.median(out)
 
-    big = torch.ones(1 << 30, dtype=torch.float16, device=dev)
-    read_s = timed(lambda: big.sum(), 10)
-    src, dst = big[: 1 << 29], torch.empty(1 << 29, dtype=torch.float16, device=dev)
-    copy_s = timed(lambda: dst.copy_(src), 10)
-    del big, src, dst
-    small = [torch.ones(2 << 20, dtype=torch.float16, device=dev) for _ in range(64)]
-    outs = [torch.empty(2 << 20, dtype=torch.float16, device=dev) for _ in range(64)]
-    calls = lambda: [o.copy_(t) for t, o in zip(small, outs)]  # noqa: E731
-    g = _capture(calls, dev)
-    small_s = timed(g.replay, 20) / 64
-    del g, small, outs
+    big = torch.zeros(1 << 30, dtype=torch.uint8, device=dev)
+    best = max(((1 << 30) / timed(lambda b=b: read(big, 1 << 30, b), ROUNDS), b) for b in (1024, 2048, 4096))
+    del big
+    nb = (small_bytes + 15) // 16 * 16
+    bufs = [torch.zeros(nb, dtype=torch.uint8, device=dev) for _ in range(COPIES)]
+    floor = [torch.zeros(16, dtype=torch.uint8, device=dev) for _ in range(COPIES)]
+
+    def graph(fn):
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            fn(side)
+            side.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                fn(side)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        return g
+
+    g_small = graph(lambda s: [read(b, nb, 1024, s) for b in bufs])
+    g_floor = graph(lambda s: [read(b, 16, 1, s) for b in floor])
+    small_s = timed(g_small.replay, ROUNDS) / COPIES
+    floor_s = timed(g_floor.replay, ROUNDS) / COPIES
+    del g_small, g_floor, bufs, floor
     torch.cuda.empty_cache()
-    return {"hbm_read_GBps": round((2 << 30) / read_s / 1e9, 1), "hbm_copy_GBps": round((2 << 30) / copy_s / 1e9, 1),
-            "copy_8MiB_graph_us": round(small_s * 1e6, 3),
-            "how": "torch sum over 2 GiB f16 (read); copy of 1 GiB (read + write, 2 GiB moved); copy of 4 MiB (8 MiB "
-                   "moved) over 64 rotating pairs replayed from a HIP graph (per launch)"}
+    return {"hbm_read_GBps": round(best[0] / 1e9, 1), "hbm_read_grid": best[1],
+            "read_small_graph_us": round(small_s * 1e6, 3), "read_small_bytes": nb,
+            "read_small_GBps": round(nb / small_s / 1e9, 1), "launch_floor_us": round(floor_s * 1e6, 3),
+            "how": "sushi_amd/csrc/bench_stream.hip streaming read: 1 GiB (best of 1024/2048/4096 workgroups, median "
+                   "of 7); C1's packed bytes per launch over 64 rotating buffers from a HIP graph (median of 7 "
+                   "rounds); a 16-byte read per launch from a graph (the launch cost)"}
 
 
 def blas_f16_gemm_us(rows: int, in_f: int, out_f: int, reps: int = 20) -> float:
@@ -417,11 +485,11 @@ def bench_moe_c5(batch: int = 64, layers: int = 4, replays: int = 4):
     dev = torch.device("cuda:0")
     E1, E2, hidden, inter, k = 64, 192, 4096, 2048, 8
     dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
-    g1 = synth.bank(5, "c5.k1", E1, hidden, inter, 16, device=dev)
-    g2 = synth.bank(5, "c5.k2", E2, hidden, inter, 32, device=dev)
+    g1 = synth.bank(5, "c5.k1", E1, hidden, inter, 16, device=dev, norm=True)
+    g2 = synth.bank(5, "c5.k2", E2, hidden, inter, 32, device=dev, norm=True)
     rb = exl3.Ragged.init([g1, g2])
     del g1, g2
-    shared = synth.bank(5, "c5.shared", 1, hidden, inter, 64, device=dev)
+    shared = synth.bank(5, "c5.shared", 1, hidden, inter, 64, device=dev, norm=True)
     x0 = synth.normal(5, f"c5.x{batch}", (batch, hidden), device=dev)
     routes = []
     for layer in range(layers):
@@ -486,25 +554,105 @@ def _profiled_traffic():
     return None
 
 
+def _cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return model, os.cpu_count() or 1, threads
+
+
 def cpu_baseline(sample_calls: int):
-    """The single-threaded C port of the reference's CPU path (prepareInput / innerGemv / finishOutput with the
-    dense O(128^2) Hadamard, expert_exl3.zig:490-566) on `sample_calls` calls of the same 4096x4096 K4 workload."""
+    """The C port of the reference's CPU path (prepareInput / innerGemv / finishOutput with the dense O(128^2)
+    Hadamard, expert_exl3.zig:490-566) on the same 4096x4096 K4 3INST workload: on every host core the build may use
+    (OpenMP over output tiles, the same arithmetic per element) and on one (the reference's own single-threaded
+    path); each the median of 7 samples."""
+    import statistics
+
     import numpy as np
 
     import oracle as O
     from sushi_amd import synth
 
+    model, nproc, threads = _cpu_info()
     p = synth.proj(0, "cpu", 1, 4096, 4096, 64)
     x = synth.normal(0, "cpu.x", (1, 4096)).float().numpy()
     t, su, sv = (a.numpy().view(np.uint16) for a in (p.trellis, p.suh, p.svh))
     dec = O.decode(O.CB_3INST)
-    O.project_rows(x, t, su, sv, 4096, 4096, 64, dec, threads=1)
-    t0 = time.perf_counter()
-    for _ in range(sample_calls):
-        O.project_rows(x, t, su, sv, 4096, 4096, 64, dec, threads=1)
-    dt = (time.perf_counter() - t0) / sample_calls
-    return dict(value=_algorithmic_bytes(4096, 4096, 64, 1) / dt / 1e9, unit="GB/s", cores=1, kind="port",
-                sample=f"{sample_calls} single-row calls of the 4096x4096 K4 3INST project (~{dt * 1e3:.0f} ms each)")
+    alg = _algorithmic_bytes(4096, 4096, 64, 1)
+
+    def per_call(th, calls):
+        O.project_rows(x, t, su, sv, 4096, 4096, 64, dec, threads=th)
+        samples = []
+        for _ in range(ROUNDS):
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                O.project_rows(x, t, su, sv, 4096, 4096, 64, dec, threads=th)
+            samples.append((time.perf_counter() - t0) / calls)
+        return statistics.median(samples)
+
+    one = per_call(1, max(1, sample_calls // 8))
+    many = per_call(threads, sample_calls)
+    return dict(value=round(alg / many / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"median of 7 samples of {sample_calls} single-row calls of the 4096x4096 K4 3INST project "
+                       f"on {threads} threads ({many * 1e3:.1f} ms per call)",
+                tok_per_s=round(1.0 / many, 2), nproc=nproc, cpu_model=model,
+                single_thread={"value": round(alg / one / 1e9, 3), "unit": "GB/s", "cores": 1,
+                               "ms_per_call": round(one * 1e3, 1), "tok_per_s": round(1.0 / one, 2),
+                               "sample": f"median of 7 samples of {max(1, sample_calls // 8)} calls"})
+
+
+def cpu_moe_baseline(batch: int = 16):
+    """moeSwigluHost (expert_exl3_kernels.zig:3059-3114) over configs[3]'s layer: 256 experts, hidden 2048, inter 768,
+    K2 MCG, top-8 over N(0,1) logits plus the shared expert as a ninth slot of weight 1; us per token on every core
+    (OpenMP over `batch` rows) and on one (a single token); median of 7 samples."""
+    import statistics
+
+    import numpy as np
+
+    import oracle as O
+    from sushi_amd import synth
+
+    model, nproc, threads = _cpu_info()
+    E, hidden, inter, k = 256, 2048, 768, 8
+    b = synth.bank(3, "c4", E, hidden, inter, 32, norm=True)
+    sh = synth.bank(3, "c4.shared", 1, hidden, inter, 32, norm=True)
+    # the shared expert as expert E of a 257-expert bank (weight 1 in every row)
+    banks = [tuple(np.concatenate([a.numpy().view(np.uint16), c.numpy().view(np.uint16)])
+                   for a, c in zip((q.trellis, q.suh, q.svh), (qs.trellis, qs.suh, qs.svh)))
+             for q, qs in zip((b.gate, b.up, b.down), (sh.gate, sh.up, sh.down))]
+    x = synth.normal(3, f"c4.cpu{batch}", (batch, hidden)).float().numpy()
+    inds, scores = O.route_topk(synth.normal(3, f"c4.cpu.logits{batch}", (batch, E), dtype=__import__("torch").float32)
+                                .numpy(), k)
+    slots = np.concatenate([inds, np.full((batch, 1), E, np.uint32)], axis=1)
+    weights = np.concatenate([scores, np.ones((batch, 1), np.float32)], axis=1)
+    dec = O.decode(O.CB_MCG)
+
+    def per_token(th, rows):
+        O.moe_swiglu_rows(x[:rows], *banks, slots[:rows], weights[:rows], hidden, inter, (32, 32, 32), dec,
+                          threads=th)
+        samples = []
+        for _ in range(ROUNDS):
+            t0 = time.perf_counter()
+            O.moe_swiglu_rows(x[:rows], *banks, slots[:rows], weights[:rows], hidden, inter, (32, 32, 32), dec,
+                              threads=th)
+            samples.append((time.perf_counter() - t0) / rows)
+        return statistics.median(samples)
+
+    one = per_token(1, 1)
+    many = per_token(threads, batch)
+    return dict(value=round(many * 1e6, 1), unit="us/token", cores=threads, kind="port", nproc=nproc,
+                cpu_model=model,
+                sample=f"median of 7 samples of {batch} rows (8 routed experts + the shared one each) on {threads} "
+                       "threads",
+                single_thread={"value": round(one * 1e6, 1), "unit": "us/token", "cores": 1,
+                               "sample": "median of 7 samples of one row"})
 
 
 def main() -> int:
@@ -512,7 +660,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--cpu-sample", type=int, default=120)
+    ap.add_argument("--cpu-sample", type=int, default=40, help="calls per all-core CPU sample (0: no CPU baseline)")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the measured read/copy/8 MiB-launch ceilings")
     ap.add_argument("--no-graph", action="store_true", help="issue every call from Python instead of a HIP graph")
@@ -540,8 +688,10 @@ def main() -> int:
     launch_s = lin["event_ms"] / 1e3 / steps
     achieved = lin["bytes"] / launch_s / 1e9
     moe = [] if args.no_moe else [bench_moe(int(b)) for b in args.moe_batches.split(",") if b]
+    ceilings = measured_ceilings(4096 * 4096 * 64 // 128) if not args.no_ceilings else None
     cpu = cpu_baseline(args.cpu_sample) if args.cpu_sample > 0 else None
-    ceilings = measured_ceilings() if not args.no_ceilings else None
+    cpu_moe = cpu_moe_baseline() if args.cpu_sample > 0 and moe else None
+    traffic = _profiled_traffic()
     out = {
         "metric": "effective HBM GB/s + tok/s, EXL3 K=4 4096x4096 GEMV b=1; MoE layer us/token",
         "value": round(value, 2),
@@ -558,22 +708,32 @@ def main() -> int:
         "config": {"workload": "EXL3 dense linear 4096x4096, K=4 (n=64), 3INST codebook, 16x16 tiles, batch 1, "
                                "64 rotating weight copies", "global_batch": 1, "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1.0 / (lin["wall_s"] / steps), 1),
-        "launch_mode": "hip graphs of library calls (64 weight copies), replayed" if not args.no_graph else "python loop",
+        "timing": f"median of {lin['rounds']} rounds of exactly {steps} calls, each round after an untimed replay of "
+                  "the 64-copy sequence (every timed call reads a copy last read 64 calls, 537 MB, earlier)"
+                  + ("; calls replayed from HIP graphs" if not args.no_graph else "; calls issued from Python"),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _profiled_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/gemv_c1_3inst_k4_b1_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE passes of bench.py, scaled by a copy kernel's counters)"
+                                       if traffic else None,
                      "algorithmic_bytes": lin["bytes"], "launch_us": round(launch_s * 1e6, 3),
                      "measured_ceilings": ceilings},
         "cpu_baseline": cpu,
     }
+    if ceilings:
+        out["roofline"]["frac_of_measured_read"] = round(achieved / ceilings["hbm_read_GBps"], 4)
+        out["roofline"]["launch_us_over_read_floor"] = round(launch_s * 1e6 / ceilings["read_small_graph_us"], 3)
     if moe:
-        out["moe_layer"] = {"config": "E=256 routed + 1 shared, hidden 2048, inter 768, K2 MCG, top-8; dependent "
-                                      "chain of 16 layers in a HIP graph",
+        out["moe_layer"] = {"config": "E=256 routed + 1 shared, hidden 2048, inter 768, K2 MCG, top-8; 16 layers back "
+                                      "to back on one stream from a HIP graph, each its own N(0,1) input and routing "
+                                      "(svh with 1/sqrt(in)); median of 7 replays",
                             "us_per_token": round(moe[0]["us_per_token"], 3),
                             "batches": [{"batch": m["batch"], "layer_us": round(m["layer_us"], 3),
                                          "us_per_token": round(m["us_per_token"], 3),
                                          "distinct_experts": round(m["distinct"], 2),
                                          "effective_GBps": round(m["bytes"] / (m["layer_us"] * 1e-6) / 1e9, 2)}
-                                        for m in moe]}
+                                        for m in moe],
+                            "cpu_baseline": cpu_moe}
     print(json.dumps(out))
     return 0
 

@@ -93,6 +93,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.ox_project.argtypes = [vp, vp, vp, vp, sz, sz, u32, Decode, vp]
     L.ox_project_rows.argtypes = [vp, sz, vp, vp, vp, sz, sz, u32, Decode, ctypes.c_int, vp]
     L.ox_moe_swiglu_host.argtypes = [vp] * 12 + [sz, sz, sz, u32, u32, u32, Decode, ctypes.c_float, vp]
+    L.ox_moe_swiglu_rows.argtypes = [vp, sz] + [vp] * 17 + [sz, sz, sz, Decode, ctypes.c_float, ctypes.c_int, vp]
     L.ox_decode_dense.argtypes = [vp, vp, vp, sz, sz, u32, Decode, vp]
     L.ox_route_topk.argtypes = [vp, sz, sz, sz, vp, vp]
     L.ox_tile_major.argtypes = [vp, vp, sz, sz, sz]
@@ -301,6 +302,32 @@ def moe_swiglu_host(x, gate, up, down, slots, weights, hidden: int, inter: int, 
     rc = lib().ox_moe_swiglu_host(_p(xv), *[_p(a) for a in arrs], _p(sl), _p(wv), sl.size, hidden, inter,
                                   n[0], n[1], n[2], dec, clamp_limit, _p(y))
     _check(rc, "moe_swiglu_host")
+    return y
+
+
+def moe_swiglu_rows(x, gate, up, down, slots, weights, hidden: int, inter: int, n, dec: Decode,
+                    clamp_limit: float = 0.0, threads: int = 8) -> np.ndarray:
+    """Rows of tokens x [rows, hidden] through moeSwigluHost, slots / weights [rows, topk].  gate/up/down are
+    (trellis, suh [E, in], svh [E, out]) banks; n is (n_gate, n_up, n_down), each an int (a uniform bank, trellis
+    [E, in/16, out/16, n]) or a per-expert rate array (a ragged bank: each expert's tiles contiguous, in expert
+    order, at its own rate)."""
+    xv = _f32(x).reshape(-1, hidden)
+    sl = np.ascontiguousarray(slots, np.uint32).reshape(xv.shape[0], -1)
+    wv = _f32(weights).reshape(sl.shape)
+    experts = _u16(gate[1]).size // hidden
+    dims = ((hidden, inter), (hidden, inter), (inter, hidden))
+    offs, rates = [], []
+    for ni, (din, dout) in zip(n, dims):
+        r = np.full(experts, ni, np.uint32) if np.isscalar(ni) else np.ascontiguousarray(ni, np.uint32)
+        tiles = (din // 16) * (dout // 16)
+        offs.append(np.concatenate([[0], np.cumsum(r.astype(np.uint64) * tiles)[:-1]]).astype(np.uint64))
+        rates.append(r)
+    arrs = [_u16(a) for p in (gate, up, down) for a in p]
+    y = np.zeros((xv.shape[0], hidden), np.float32)
+    rc = lib().ox_moe_swiglu_rows(_p(xv), xv.shape[0], *[_p(a) for a in arrs], *[_p(o) for o in offs],
+                                  *[_p(r) for r in rates], _p(sl), _p(wv), sl.shape[1], hidden, inter, dec,
+                                  clamp_limit, threads, _p(y))
+    _check(rc, "moe_swiglu_rows")
     return y
 
 

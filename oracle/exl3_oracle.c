@@ -598,6 +598,48 @@ int ox_moe_swiglu_host(const float *x, const uint16_t *gate_t, const uint16_t *g
     return rc;
 }
 
+/* Rows of tokens through moeSwigluHost: row r takes slots / weights [r * topk, (r + 1) * topk).  threads > 1 runs
+ * OpenMP over rows (each row's arithmetic is the single-row function's, so both give the same bytes).  The banks are
+ * ragged: expert e of projection p starts at halfword off[p][e] of its trellis and decodes at rate n[p][e] (a
+ * uniform bank is off[p][e] = e * tiles * n). */
+int ox_moe_swiglu_rows(const float *x, size_t rows, const uint16_t *gate_t, const uint16_t *gate_suh,
+                       const uint16_t *gate_svh, const uint16_t *up_t, const uint16_t *up_suh, const uint16_t *up_svh,
+                       const uint16_t *down_t, const uint16_t *down_suh, const uint16_t *down_svh,
+                       const uint64_t *off_gate, const uint64_t *off_up, const uint64_t *off_down,
+                       const uint32_t *n_gate, const uint32_t *n_up, const uint32_t *n_down, const uint32_t *slots,
+                       const float *weights, size_t topk, size_t hidden, size_t inter, ox_decode dec,
+                       float clamp_limit, int threads, float *y) {
+    int bad = 0;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 1 ? threads : 1) reduction(| : bad)
+    for (long r = 0; r < (long)rows; r++) {
+        float *yr = y + r * hidden;
+        memset(yr, 0, hidden * sizeof(float));
+        float *dy = (float *)malloc(hidden * sizeof(float));
+        if (!dy) {
+            bad |= 1;
+            continue;
+        }
+        for (size_t k = 0; k < topk; k++) {
+            const size_t e = slots[r * topk + k];
+            const uint32_t one = 0;
+            const float w1 = 1.0f;
+            /* one expert through the single-row function, its bank pointers moved to expert e */
+            int rc = ox_moe_swiglu_host(x + r * hidden, gate_t + off_gate[e], gate_suh + e * hidden,
+                                        gate_svh + e * inter, up_t + off_up[e], up_suh + e * hidden, up_svh + e * inter,
+                                        down_t + off_down[e], down_suh + e * inter, down_svh + e * hidden, &one, &w1, 1,
+                                        hidden, inter, n_gate[e], n_up[e], n_down[e], dec, clamp_limit, dy);
+            if (rc) {
+                bad |= 1;
+                break;
+            }
+            const float w = weights[r * topk + k];
+            for (size_t i = 0; i < hidden; i++) yr[i] += w * dy[i];
+        }
+        free(dy);
+    }
+    return bad ? -1 : 0;
+}
+
 /* ------------------------------------------------------------------------------------------------ */
 /* decodeDense: linear.zig:406-431                                                                   */
 

@@ -26,6 +26,8 @@
  *                                   (relRms < 0.02, the reference's own bar) + FWHT equivalence.
  *   ox_moe_swiglu_host            : composition of ox_project + closed-form SwiGLU; checked against an
  *                                   independent numpy restatement over ox_decode_dense weights.
+ *   ox_moe_swiglu_rows            : rows of ox_moe_swiglu_host over ragged banks; equals it row by row (and the
+ *                                   threaded run equals the single-threaded one byte for byte).
  *   ox_decode_dense               : equals the dense product diag(suh) H M H diag(svh) built by numpy.
  *   ox_route_topk                 : closed form (softmax, top-k, renormalise) vs numpy.
  *   ox_tile_major(_inverse)       : round trip + the reference's layout test (layout.zig:160-175).
@@ -128,6 +130,14 @@ int ox_moe_swiglu_host(const float *x, const uint16_t *gate_t, const uint16_t *g
                        const uint32_t *slots, const float *weights, size_t topk, size_t hidden, size_t inter,
                        uint32_t n_gate, uint32_t n_up, uint32_t n_down, ox_decode dec, float clamp_limit,
                        float *y);
+
+int ox_moe_swiglu_rows(const float *x, size_t rows, const uint16_t *gate_t, const uint16_t *gate_suh,
+                       const uint16_t *gate_svh, const uint16_t *up_t, const uint16_t *up_suh, const uint16_t *up_svh,
+                       const uint16_t *down_t, const uint16_t *down_suh, const uint16_t *down_svh,
+                       const uint64_t *off_gate, const uint64_t *off_up, const uint64_t *off_down,
+                       const uint32_t *n_gate, const uint32_t *n_up, const uint32_t *n_down, const uint32_t *slots,
+                       const float *weights, size_t topk, size_t hidden, size_t inter, ox_decode dec,
+                       float clamp_limit, int threads, float *y);
 
 int ox_decode_dense(const uint16_t *words, const uint16_t *suh, const uint16_t *svh, size_t in, size_t out,
                     uint32_t n, ox_decode dec, float *dst);

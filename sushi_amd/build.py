@@ -48,8 +48,24 @@ CFLAGS = [
 ]
 
 
+def _stale(src: str, obj: str) -> bool:
+    """An object older than its source or than any header it may include (csrc/*.h, *.cuh, include/*.h)."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith((".h", ".cuh"))]
+    inc = os.path.join(HERE, "..", "include")
+    deps += [os.path.join(inc, h) for h in os.listdir(inc) if h.endswith(".h")]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+INCREMENTAL = False
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+    if INCREMENTAL and not _stale(src, obj):
+        return obj
     cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -61,22 +77,33 @@ def _compile(src: str) -> str:
     return obj
 
 
+BENCH_SOURCES = ["bench_stream.hip"]
+BENCH_LIB = os.path.join(HERE, "libsushi_bench_hip.so")
+
+
+def _link(objs, out: str) -> None:
+    tmp = out + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
+    os.replace(tmp, out)
+
+
 def build(jobs: int | None = None, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     t0 = time.time()
     jobs = jobs or min(len(SOURCES), max(1, min(16, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
-    os.replace(tmp, LIB)
+        objs = list(ex.map(_compile, SOURCES + BENCH_SOURCES))
+    _link(objs[:len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], BENCH_LIB)  # bench.py's measurement kernels, outside the hot path's library
     if verbose:
         print(f"[build] {LIB} ({os.path.getsize(LIB) / 1e6:.1f} MB) in {time.time() - t0:.0f}s", file=sys.stderr)
     return LIB
 
 
 if __name__ == "__main__":
+    # --incremental (development only): recompile only objects older than their sources or headers
+    INCREMENTAL = "--incremental" in sys.argv[1:]
     build()

@@ -83,19 +83,25 @@ def normal(seed: int, name: str, shape, device="cpu", dtype=torch.float16) -> to
     return z.to(dtype).reshape(shape).to(device)
 
 
-def proj(seed: int, name: str, experts: int, in_f: int, out_f: int, n: int, device="cpu"):
-    """A bank (trellis [E, in/16, out/16, n] int16, suh [E, in] f16, svh [E, out] f16)."""
+def proj(seed: int, name: str, experts: int, in_f: int, out_f: int, n: int, device="cpu", norm: bool = False):
+    """A bank (trellis [E, in/16, out/16, n] int16, suh [E, in] f16, svh [E, out] f16).  `norm` divides svh by
+    sqrt(in) (rounded to f16), so the projection keeps N(0, 1) activations near unit scale (the codebook's weights
+    are near unit variance); without it outputs grow by sqrt(in) per projection."""
     from .exl3 import Proj
 
+    svh = sign_scale(seed, name + ".svh", (experts, out_f))
+    if norm:
+        svh = (svh.double() / math.sqrt(in_f)).to(torch.float16)
     return Proj(codes(seed, name + ".trellis", (experts, in_f // 16, out_f // 16, n), device),
-                sign_scale(seed, name + ".suh", (experts, in_f), device),
-                sign_scale(seed, name + ".svh", (experts, out_f), device))
+                sign_scale(seed, name + ".suh", (experts, in_f), device), svh.to(device))
 
 
-def bank(seed: int, name: str, experts: int, hidden: int, inter: int, n, device="cpu"):
+def bank(seed: int, name: str, experts: int, hidden: int, inter: int, n, device="cpu", norm: bool = False):
+    """gate / up [E, hidden -> inter] and down [E, inter -> hidden] at rates n (one rate or (n_gate, n_up, n_down));
+    `norm` as in proj (the routed configs use it, so a chain of layers stays finite in f16)."""
     from .exl3 import Bank
 
     ng, nu, nd = (n, n, n) if isinstance(n, int) else n
-    return Bank(proj(seed, name + ".gate", experts, hidden, inter, ng, device),
-                proj(seed, name + ".up", experts, hidden, inter, nu, device),
-                proj(seed, name + ".down", experts, inter, hidden, nd, device))
+    return Bank(proj(seed, name + ".gate", experts, hidden, inter, ng, device, norm),
+                proj(seed, name + ".up", experts, hidden, inter, nu, device, norm),
+                proj(seed, name + ".down", experts, inter, hidden, nd, device, norm))

@@ -117,6 +117,43 @@ def test_route_topk_against_numpy():
     assert inds[0, 0] == 3 and inds[0, 1] == 9
 
 
+def test_moe_swiglu_rows_is_the_host_function_row_by_row_uniform_and_ragged():
+    """ox_moe_swiglu_rows (rows of moeSwigluHost, OpenMP over rows) equals the single-row function row by row, on a
+    uniform bank and on a ragged one (experts at their own rates), and its threaded run gives the same bytes."""
+    from sushi_amd import synth
+
+    dec = O.decode(O.CB_SPEC1, 15, 1)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((5, 256)).astype(np.float16).astype(np.float32)
+    sl = rng.integers(0, 6, (5, 3))
+    w = rng.random((5, 3)).astype(np.float32)
+    b = synth.bank(3, "rows", 6, 256, 128, 32)
+    banks = [tuple(a.numpy().view(np.uint16) for a in (q.trellis, q.suh, q.svh)) for q in (b.gate, b.up, b.down)]
+    y = O.moe_swiglu_rows(x, *banks, sl, w, 256, 128, (32, 32, 32), dec, threads=4)
+    assert np.array_equal(y, O.moe_swiglu_rows(x, *banks, sl, w, 256, 128, (32, 32, 32), dec, threads=1))
+    for r in range(5):
+        assert np.array_equal(y[r], O.moe_swiglu_host(x[r], *banks, sl[r], w[r], 256, 128, (32, 32, 32), dec))
+    # ragged: experts 0..2 at n16, 3..5 at n32, one flat trellis per projection in expert order
+    g1, g2 = synth.bank(5, "r1", 3, 256, 128, 16), synth.bank(5, "r2", 3, 256, 128, 32)
+    rag = []
+    for nm in ("gate", "up", "down"):
+        q1, q2 = getattr(g1, nm), getattr(g2, nm)
+        rag.append(tuple(np.concatenate([a1.numpy().view(np.uint16).reshape(-1), a2.numpy().view(np.uint16).reshape(-1)])
+                         if i == 0 else np.concatenate([a1.numpy().view(np.uint16), a2.numpy().view(np.uint16)])
+                         for i, (a1, a2) in enumerate(zip((q1.trellis, q1.suh, q1.svh), (q2.trellis, q2.suh, q2.svh)))))
+    rates = [np.array([16] * 3 + [32] * 3)] * 3
+    yr = O.moe_swiglu_rows(x, *rag, sl, w, 256, 128, rates, dec, threads=4)
+    for r in range(5):
+        want = np.zeros(256, np.float32)
+        for k in range(3):
+            e = int(sl[r, k])
+            grp, local, n = (g1, e, 16) if e < 3 else (g2, e - 3, 32)
+            one = [tuple(a.numpy().view(np.uint16)[local] for a in (q.trellis, q.suh, q.svh))
+                   for q in (grp.gate, grp.up, grp.down)]
+            want += w[r, k] * O.moe_swiglu_host(x[r], *one, [0], [1.0], 256, 128, (n, n, n), dec)
+        assert np.array_equal(yr[r], want), r
+
+
 def _nonfinite_logit_rows():
     rng = np.random.default_rng(12)
     rows = rng.standard_normal((6, 40)).astype(np.float32)
