@@ -190,21 +190,34 @@ int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t
 /* Routed SwiGLU experts: `moe` (src/exl3/root.zig:51-53), `moeWithShared` (:56-67, `shared` [rows][hidden] in y's
  * dtype, added after the routed output's rounding as REDUCE_SHARED_SOURCE does,
  * src/exl3/expert_exl3_kernels.zig:2391-2406), `moeClamped` (:98-124, clamp_limit in 1..128, 0 = none).
- * x [rows][hidden]; inds [rows][topk] u32 (i32 accepted: same bits); scores [rows][topk] f32.
- * Banks: gate/up trellis [E][hidden/16][inter/16][n], down [E][inter/16][hidden/16][n].  The decode chain
- * (pair GEMV -> fused SwiGLU mid + down GEMV -> score-weighted reduce) serves every row count. */
+ * x [rows][hidden]; inds [rows][topk] u32 (i32 accepted: same bits); scores [rows][topk] in scores_dtype (f32, bf16
+ * or f16, as root.zig:114 admits).  Banks: gate/up trellis [E][hidden/16][inter/16][n], down
+ * [E][inter/16][hidden/16][n]; each projection at its own rate (gate and up at different rates take one launch each,
+ * as moeMixedDecode does, root.zig:705-722).  The decode chain (pair GEMV -> fused SwiGLU mid + down GEMV ->
+ * score-weighted reduce) serves every row count. */
 size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
 int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
-                 const exl3_bank_t *bank, const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
-                 int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
-                 void *workspace, size_t workspace_bytes, hipStream_t stream);
+                 const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                 exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y,
+                 int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* `moeWithGatedShared` (src/exl3/root.zig:71-90): y = routed + sigmoid(gate) * shared_down, with shared_down the shared
+ * expert's output [rows][hidden] and shared_gate its gate logit [rows] (one per row), both in y's dtype T.  The terms
+ * round in T where MLX's Sigmoid, Multiply and Add do (REDUCE_GATED_SHARED_SOURCE,
+ * src/exl3/expert_exl3_kernels.zig:2410-2431): T(T(routed) + T(sig * shared)), sig = g < 0 ? rc : T(1 - rc),
+ * rc = T(1 / T(1 + T(exp|g|))).  Workspace: exl3_moe_workspace_size. */
+int32_t exl3_moe_with_gated_shared(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                   int32_t experts, const exl3_bank_t *bank, const uint32_t *inds, const void *scores,
+                                   int32_t scores_dtype, int32_t topk, exl3_decode_t dec, int32_t verify_rows,
+                                   const void *shared_down, const void *shared_gate, void *y, int32_t y_dtype,
+                                   void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* `moeRagged` (src/exl3/root.zig:582-644) over a rate-grouped ragged bank (rate_groups.zig:22-140): each expert
  * decodes at its own (n_gate, n_up, n_down) read from the meta table.  `max_n` bounds every rate in the table. */
 int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
-                        const exl3_ragged_t *bank, const uint32_t *inds, const float *scores, int32_t topk,
-                        exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
-                        void *workspace, size_t workspace_bytes, hipStream_t stream);
+                        const exl3_ragged_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
+                        int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
+                        int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* A routed layer and its shared expert in one call.  Replaces the caller's pair of calls: the shared expert as a
  * one-expert chain (inds 0, score 1; the pattern of src/dsv41/dsv41_model.zig:3000) and then `moeWithShared`
@@ -215,21 +228,21 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
  * routed layer's inter; clamp_limit applies to both.  Up to 8 rows the shared rows join the per-slot launches;
  * wider batches the sorted (expert-window) launches, where the shared rows are windows of their own (three launches
  * in all instead of six).  Returns EXL3_DECLINED (nothing launched) where the fused form does not serve: y dtype f32,
- * a shared rate other than the routed one (uniform banks), rows whose routed, shared and combine fold words (3 x rows
+ * routed projections at different rates, a shared rate other than the routed one (uniform banks), rows whose routed, shared and combine fold words (3 x rows
  * x hidden) exceed the fused finish's region, or more fold arrivals than it holds; the caller then makes the two
  * calls.  The _ragged form takes
  * `moeRagged`'s rate-grouped bank (src/exl3/root.zig:582-644); its shared bank keeps its own rate. */
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                   int32_t experts, const exl3_bank_t *bank, const exl3_bank_t *shared_bank,
-                                  const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
-                                  int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
+                                  const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                                  exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
                                   size_t workspace_bytes, hipStream_t stream);
 int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                          const exl3_ragged_t *bank, const exl3_bank_t *shared_bank,
-                                         const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
-                                         int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
-                                         size_t workspace_bytes, hipStream_t stream);
+                                         const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                                         exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
+                                         void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Router chain `moeRoutingChainOn` (src/moe_router.zig:22-62): top-k over f32 logits [rows][experts]
  * (ties to the lower expert index, listed in descending logit order), softmax over all experts, gathered and

@@ -95,6 +95,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.ox_moe_swiglu_host.argtypes = [vp] * 12 + [sz, sz, sz, u32, u32, u32, Decode, ctypes.c_float, vp]
     L.ox_moe_swiglu_rows.argtypes = [vp, sz] + [vp] * 17 + [sz, sz, sz, Decode, ctypes.c_float, ctypes.c_int, vp]
     L.ox_decode_dense.argtypes = [vp, vp, vp, sz, sz, u32, Decode, vp]
+    L.ox_gated_shared_term.restype = ctypes.c_float
+    L.ox_gated_shared_term.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int]
+    L.ox_gated_shared_terms.argtypes = [vp, vp, sz, sz, ctypes.c_int, vp]
     L.ox_route_topk.argtypes = [vp, sz, sz, sz, vp, vp]
     L.ox_tile_major.argtypes = [vp, vp, sz, sz, sz]
     L.ox_tile_major_inverse.argtypes = [vp, vp, sz, sz, sz]
@@ -329,6 +332,20 @@ def moe_swiglu_rows(x, gate, up, down, slots, weights, hidden: int, inter: int, 
                                   clamp_limit, threads, _p(y))
     _check(rc, "moe_swiglu_rows")
     return y
+
+
+def gated_shared_term(gate: float, shared: float, dtype: int) -> float:
+    """T(sigmoid(gate) * shared) rounded where MLX's bf16 Sigmoid and Multiply round (dtype 0 f16, 1 bf16, 2 f32)."""
+    return lib().ox_gated_shared_term(gate, shared, dtype)
+
+
+def gated_shared_terms(gate, shared, dtype: int) -> np.ndarray:
+    """gated_shared_term over a block: gate [rows], shared [rows, cols] -> [rows, cols] f32."""
+    g = _f32(gate).reshape(-1)
+    sh = _f32(shared).reshape(g.size, -1)
+    out = np.zeros_like(sh)
+    lib().ox_gated_shared_terms(_p(g), _p(sh), g.size, sh.shape[1], dtype, _p(out))
+    return out
 
 
 def decode_dense(words, suh, svh, in_f: int, out_f: int, n: int, dec: Decode) -> np.ndarray:

@@ -641,6 +641,39 @@ int ox_moe_swiglu_rows(const float *x, size_t rows, const uint16_t *gate_t, cons
 }
 
 /* ------------------------------------------------------------------------------------------------ */
+/* The gated shared expert's term: REDUCE_GATED_SHARED_SOURCE, expert_exl3_kernels.zig:2410-2431.  In T = dtype   */
+/* (0 f16, 1 bf16, 2 f32): ex = T(exp|g|), rc = T(1 / T(1 + ex)), sig = g < 0 ? rc : T(1 - rc), term = T(sig * sh). */
+/* exp is evaluated in double and rounded to float (the kernel's own choice for Metal's precise::exp).             */
+
+static float ox_bf16r(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u) { /* inf stays, NaN stays NaN */
+        if (u & 0x007FFFFFu) u |= 0x00400000u;
+    } else {
+        u += 0x7FFFu + ((u >> 16) & 1u); /* round to nearest even */
+    }
+    u &= 0xFFFF0000u;
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+static float ox_round_dt(int dtype, float v) { return dtype == 0 ? f16r(v) : dtype == 1 ? ox_bf16r(v) : v; }
+
+float ox_gated_shared_term(float gate, float shared, int dtype) {
+    const float ex = ox_round_dt(dtype, (float)exp(fabs((double)gate)));
+    const float rc = ox_round_dt(dtype, 1.0f / ox_round_dt(dtype, 1.0f + ex));
+    const float sig = gate < 0.0f ? rc : ox_round_dt(dtype, 1.0f - rc);
+    return ox_round_dt(dtype, sig * shared);
+}
+
+/* out[r][c] = ox_gated_shared_term(gate[r], shared[r][c], dtype) over a [rows][cols] block. */
+void ox_gated_shared_terms(const float *gate, const float *shared, size_t rows, size_t cols, int dtype, float *out) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) out[r * cols + c] = ox_gated_shared_term(gate[r], shared[r * cols + c], dtype);
+}
+
+/* ------------------------------------------------------------------------------------------------ */
 /* decodeDense: linear.zig:406-431                                                                   */
 
 int ox_decode_dense(const uint16_t *words, const uint16_t *suh, const uint16_t *svh, size_t in, size_t out,

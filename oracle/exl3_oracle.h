@@ -28,6 +28,8 @@
  *                                   independent numpy restatement over ox_decode_dense weights.
  *   ox_moe_swiglu_rows            : rows of ox_moe_swiglu_host over ragged banks; equals it row by row (and the
  *                                   threaded run equals the single-threaded one byte for byte).
+ *   ox_gated_shared_term          : the rounding chain of REDUCE_GATED_SHARED_SOURCE; checked against numpy's
+ *                                   float16 / an independent bf16 rounding of the same chain, every f16 and bf16 gate.
  *   ox_decode_dense               : equals the dense product diag(suh) H M H diag(svh) built by numpy.
  *   ox_route_topk                 : closed form (softmax, top-k, renormalise) vs numpy.
  *   ox_tile_major(_inverse)       : round trip + the reference's layout test (layout.zig:160-175).
@@ -138,6 +140,9 @@ int ox_moe_swiglu_rows(const float *x, size_t rows, const uint16_t *gate_t, cons
                        const uint32_t *n_gate, const uint32_t *n_up, const uint32_t *n_down, const uint32_t *slots,
                        const float *weights, size_t topk, size_t hidden, size_t inter, ox_decode dec,
                        float clamp_limit, int threads, float *y);
+
+float ox_gated_shared_term(float gate, float shared, int dtype);
+void ox_gated_shared_terms(const float *gate, const float *shared, size_t rows, size_t cols, int dtype, float *out);
 
 int ox_decode_dense(const uint16_t *words, const uint16_t *suh, const uint16_t *svh, size_t in, size_t out,
                     uint32_t n, ox_decode dec, float *dst);

@@ -302,7 +302,7 @@ bool moe_windows_enabled() { return knob(EXL3_KNOB_MOE_WINDOWS, 1) != 0; }
 constexpr int kReduceMaxTopk = kMoeReduceMaxTopk;  // REDUCE_MAX_TOPK, expert_exl3_kernels.zig:2562
 
 int32_t moe_common_checks(int32_t x_dtype, int32_t y_dtype, int32_t rows, int32_t hidden, int32_t inter,
-                          int32_t topk, int32_t clamp_limit) {
+                          int32_t topk, int32_t clamp_limit, int32_t scores_dtype) {
     if (clamp_limit < 0 || clamp_limit > 128)
         return fail(EXL3_ERR_INVALID_CLAMP, "moe: clamp limit %d outside 1..128 (0 = none)", clamp_limit);
     if (topk < 1 || topk > kReduceMaxTopk)
@@ -311,6 +311,7 @@ int32_t moe_common_checks(int32_t x_dtype, int32_t y_dtype, int32_t rows, int32_
         return fail(EXL3_ERR_BAD_SHAPE, "moe: rows=%d hidden=%d inter=%d (multiples of 128)", rows, hidden, inter);
     if ((long)rows * topk > (1L << 24)) return fail(EXL3_ERR_BAD_SHAPE, "moe: too many slots");
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(EXL3_ERR_BAD_DTYPE, "moe: unsupported dtype");
+    if (!dtype_ok(scores_dtype)) return fail(EXL3_ERR_BAD_DTYPE, "moe: scores dtype %d (f32, bf16 or f16)", scores_dtype);
     return ok();
 }
 
@@ -333,12 +334,15 @@ bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, 
     return topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)3 * rows * hidden <= kFoldWords;
 }
 
-int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t x_dtype, int32_t rows,
-                   int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
-                   const uint16_t *const su[3], const uint16_t *const sv[3], int n_uniform, const uint32_t *meta,
-                   int meta_lane_only, const uint32_t *inds, const float *scores, int32_t topk, int32_t clamp_limit, const void *shared,
-                   void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream,
-                   const SharedBank *sb = nullptr) {
+// One routed layer's launches.  n[3] are the projections' uniform rates (all 0 with a ragged `meta`); k is the decode
+// of the gate's rate (per-rate constants of the other projections are resolved here).  shared / shared_gate: an
+// already computed shared expert [rows][hidden] in y's dtype, added as it is or as sigmoid(gate) * shared.
+int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int table, const void *x, int32_t x_dtype,
+                   int32_t rows, int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
+                   const uint16_t *const su[3], const uint16_t *const sv[3], const int n[3], const uint32_t *meta,
+                   int meta_lane_only, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                   int32_t clamp_limit, const void *shared, const void *shared_gate, void *y, int32_t y_dtype,
+                   void *ws, size_t ws_bytes, hipStream_t stream, const SharedBank *sb = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
     // With a fused shared bank its rows join either arm as groups of SH_ROWS rows placed first in the grid; planes
@@ -390,7 +394,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         a.svh[i] = sv[i];
         a.meta_col[i] = i;
     }
-    a.n = n_uniform;
+    a.n = n[0];
     a.bank_of = inds;
     a.bank_limit = experts;
     a.meta = meta;
@@ -403,6 +407,10 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     a.splits = p.s1;
     a.groups = groups;
     a.nproj = 2;
+    // Gate and up of a uniform bank at different rates (moeMixedDecode, src/exl3/root.zig:705-722): one launch each,
+    // each at its own rate.
+    const bool split_pair = !meta && n[0] != n[1];
+    if (split_pair) a.nproj = 1;
     a.fused_finish = 0;
     a.partial_only = 1;
     if (sb) {
@@ -418,6 +426,18 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     }
     hipError_t e = run_gemv(fam, PRO_X, a, stream);
     if (e != hipSuccess) return launched(e, "exl3_moe (gate/up)");
+    if (split_pair) {
+        GemvArgs u = a;
+        u.trellis[0] = tr[1];
+        u.suh[0] = su[1];
+        u.svh[0] = sv[1];
+        u.partial[0] = up_part;
+        u.n = n[1];
+        int fam_u;
+        if (resolve_decode(dec, n[1], &fam_u, &u.k)) return EXL3_ERR_RATE_MISSING;
+        e = run_gemv(fam, PRO_X, u, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (up)");
+    }
 
     // 2) SwiGLU mid + down GEMV of every slot (DOWN_FUSED_SOURCE): f32 planes [slot][split][hidden]
     GemvArgs d{};
@@ -441,13 +461,17 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     d.suh[0] = su[2];
     d.svh[0] = sv[2];
     d.meta_col[0] = 2;
-    d.n = n_uniform;
+    d.n = n[2];
     d.bank_of = inds;
     d.bank_limit = experts;
     d.meta = meta;
     d.meta_lane_only = meta_lane_only;
     d.table = table;
     d.k = k;
+    if (!meta && n[2] != n[0]) {
+        int fam_d;
+        if (resolve_decode(dec, n[2], &fam_d, &d.k)) return EXL3_ERR_RATE_MISSING;
+    }
     d.out_scale = scale;
     d.partial[0] = down_part;
     d.splits = p.s2;
@@ -467,7 +491,9 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         d.fold_arrivals = topk * p.s2;
         d.fold_topk = topk;
         d.fold_scores = scores;
+        d.score_dtype = scores_dtype;
         d.fold_shared = shared;
+        d.fold_gate = shared ? shared_gate : nullptr;
         d.y = y;
         d.y_dtype = y_dtype;
     }
@@ -484,6 +510,7 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
         d.sh_fold = d.fold + (size_t)rows * hidden;
         d.fold_comb = d.fold + (size_t)2 * rows * hidden;
         d.fold_shared = nullptr;
+        d.fold_gate = nullptr;
     }
     e = run_gemv(fam, PRO_MID, d, stream);
     if (e != hipSuccess) return launched(e, "exl3_moe (down)");
@@ -499,8 +526,10 @@ int32_t moe_launch(int fam, const DecodeK &k, int table, const void *x, int32_t 
     r.slots = inds;
     r.bank_limit = experts;
     r.scores = scores;
+    r.score_dtype = scores_dtype;
     r.svh = sv[2];
     r.shared = shared;
+    r.gate = shared ? shared_gate : nullptr;
     r.y = y;
     r.y_dtype = y_dtype;
     r.out_scale = 1.0f;
@@ -580,6 +609,38 @@ int32_t shared_bank_checks(const exl3_bank_t *b, const char *what, SharedBank *o
         return fail(EXL3_ERR_BAD_SHAPE, "%s: gate/up/down rates differ", what);
     out->n = b->gate.n;
     return ok();
+}
+
+// `moe` / `moeWithShared` / `moeWithGatedShared` over a uniform bank: every check, then the launches.
+int32_t moe_uniform(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
+                    const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
+                    int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, const void *shared_gate,
+                    void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
+    if (rc) return rc;
+    if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe: no bank");
+    const exl3_proj_t *pr[3] = {&bank->gate, &bank->up, &bank->down};
+    int n[3];
+    int fam;
+    DecodeK k;
+    for (int i = 0; i < 3; i++) {
+        if (!rate_admitted(pr[i]->n) || !pr[i]->trellis || !pr[i]->suh || !pr[i]->svh)
+            return fail(EXL3_ERR_BAD_SHAPE, "moe: projection %d has n=%d or a null operand", i, pr[i]->n);
+        n[i] = pr[i]->n;
+        rc = resolve_decode(dec, n[i], &fam, &k);  // every projection's rate must have its codebook row
+        if (rc) return rc;
+    }
+    rc = resolve_decode(dec, n[0], &fam, &k);
+    if (rc) return rc;
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe: null operand");
+    if (shared_gate && !shared) return fail(EXL3_ERR_BAD_SHAPE, "moe: a shared-expert gate without its shared expert");
+    const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
+    const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
+    const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
+    return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, n, nullptr, 0,
+                      inds, scores, scores_dtype, topk, clamp_limit, shared, shared_gate, y, y_dtype, workspace,
+                      workspace_bytes, stream);
 }
 
 }  // namespace
@@ -687,37 +748,31 @@ size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32
 }
 
 int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
-                 const exl3_bank_t *bank, const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
-                 int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
-                 void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                 const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                 exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y,
+                 int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
     (void)verify_rows;  // every row count runs the decode chain here
-    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
-    if (rc) return rc;
-    if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe: no bank");
-    const exl3_proj_t *pr[3] = {&bank->gate, &bank->up, &bank->down};
-    for (int i = 0; i < 3; i++)
-        if (!rate_admitted(pr[i]->n) || !pr[i]->trellis || !pr[i]->suh || !pr[i]->svh)
-            return fail(EXL3_ERR_BAD_SHAPE, "moe: projection %d has n=%d or a null operand", i, pr[i]->n);
-    if (bank->gate.n != bank->up.n || bank->gate.n != bank->down.n)
-        return fail(EXL3_ERR_BAD_SHAPE, "moe: gate/up/down rates differ (use exl3_moe_ragged)");
-    int fam;
-    DecodeK k;
-    rc = resolve_decode(dec, bank->gate.n, &fam, &k);
-    if (rc) return rc;
-    if (rows == 0) return ok();
-    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe: null operand");
-    const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
-    const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
-    const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
-    return moe_launch(fam, k, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, bank->gate.n, nullptr,
-                      0, inds, scores, topk, clamp_limit, shared, y, y_dtype, workspace, workspace_bytes, stream);
+    return moe_uniform(x, x_dtype, rows, hidden, inter, experts, bank, inds, scores, scores_dtype, topk, dec,
+                       clamp_limit, shared, nullptr, y, y_dtype, workspace, workspace_bytes, stream);
+}
+
+int32_t exl3_moe_with_gated_shared(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                   int32_t experts, const exl3_bank_t *bank, const uint32_t *inds, const void *scores,
+                                   int32_t scores_dtype, int32_t topk, exl3_decode_t dec, int32_t verify_rows,
+                                   const void *shared_down, const void *shared_gate, void *y, int32_t y_dtype,
+                                   void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    (void)verify_rows;
+    if (!shared_down || !shared_gate)
+        return fail(EXL3_ERR_BAD_SHAPE, "moe_with_gated_shared: the shared expert's output and its gate are required");
+    return moe_uniform(x, x_dtype, rows, hidden, inter, experts, bank, inds, scores, scores_dtype, topk, dec, 0,
+                       shared_down, shared_gate, y, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
-                        const exl3_ragged_t *bank, const uint32_t *inds, const float *scores, int32_t topk,
-                        exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y, int32_t y_dtype,
-                        void *workspace, size_t workspace_bytes, hipStream_t stream) {
-    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+                        const exl3_ragged_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
+                        int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
+                        int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || bank->experts <= 0 || !bank->meta) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: no bank");
     for (int i = 0; i < 3; i++)
@@ -730,9 +785,10 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: null operand");
     const int table = fam == FAM_PAIR ? (int)TABLE_PAIR1_W16_V1 : dec.table;
-    return moe_launch(fam, k, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
-                      bank->svh, 0, bank->meta, bank->lane_rates_only != 0, inds, scores, topk, clamp_limit, shared,
-                      y, y_dtype, workspace, workspace_bytes, stream);
+    const int n0[3] = {0, 0, 0};
+    return moe_launch(fam, k, dec, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
+                      bank->svh, n0, bank->meta, bank->lane_rates_only != 0, inds, scores, scores_dtype, topk,
+                      clamp_limit, shared, nullptr, y, y_dtype, workspace, workspace_bytes, stream);
 }
 
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
@@ -745,13 +801,20 @@ size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int3
 
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                   int32_t experts, const exl3_bank_t *bank, const exl3_bank_t *shared_bank,
-                                  const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
-                                  int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
+                                  const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                                  exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
                                   size_t workspace_bytes, hipStream_t stream) {
-    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: no bank");
     SharedBank sb;
+    bool whole = true;  // every projection admitted and present
+    for (const exl3_proj_t *q : {&bank->gate, &bank->up, &bank->down})
+        whole = whole && rate_admitted(q->n) && q->trellis && q->suh && q->svh;
+    if (whole && (bank->gate.n != bank->up.n || bank->gate.n != bank->down.n))
+        return declined("moe_with_shared_bank: declined (routed rates %d/%d/%d differ): run the shared expert as a "
+                        "one-expert exl3_moe and pass it to exl3_moe as `shared`", bank->gate.n, bank->up.n,
+                        bank->down.n);
     rc = shared_bank_checks(bank, "moe_with_shared_bank (routed)", &sb);
     if (rc) return rc;
     const int routed_n = sb.n;
@@ -769,16 +832,18 @@ int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, 
     const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
     const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
     const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
-    return moe_launch(fam, k, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, routed_n, nullptr, 0,
-                      inds, scores, topk, clamp_limit, nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb);
+    const int n[3] = {routed_n, routed_n, routed_n};
+    return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, n, nullptr, 0,
+                      inds, scores, scores_dtype, topk, clamp_limit, nullptr, nullptr, y, y_dtype, workspace,
+                      workspace_bytes, stream, &sb);
 }
 
 int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                          const exl3_ragged_t *bank, const exl3_bank_t *shared_bank,
-                                         const uint32_t *inds, const float *scores, int32_t topk, exl3_decode_t dec,
-                                         int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
-                                         size_t workspace_bytes, hipStream_t stream) {
-    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit);
+                                         const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                                         exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
+                                         void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || bank->experts <= 0 || !bank->meta)
         return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: no bank");
@@ -806,9 +871,10 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
         return declined("moe_ragged_with_shared_bank: declined (rows=%d, y dtype %d): run the shared expert as a "
                         "one-expert exl3_moe and pass it to exl3_moe_ragged as `shared`", rows, y_dtype);
     const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);
-    return moe_launch(fam, k, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
-                      bank->svh, 0, bank->meta, lane_only, inds, scores, topk, clamp_limit, nullptr, y, y_dtype,
-                      workspace, workspace_bytes, stream, &sb);
+    const int n0[3] = {0, 0, 0};
+    return moe_launch(fam, k, dec, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
+                      bank->svh, n0, bank->meta, lane_only, inds, scores, scores_dtype, topk, clamp_limit, nullptr,
+                      nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb);
 }
 
 int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds, float *scores,

@@ -355,6 +355,30 @@ __device__ __forceinline__ void store_act(void *p, size_t i, float v) {
 
 __device__ __forceinline__ float f16r(float v) { return __half2float(__float2half_rn(v)); }
 
+// v rounded to an activation dtype and back.
+__device__ __forceinline__ float round_act(int dt, float v) {
+    if (dt == DT_F16) return __half2float(__float2half_rn(v));
+    if (dt == DT_BF16) return __bfloat162float(__float2bfloat16(v));
+    return v;
+}
+
+// Element i of an f16 / bf16 / f32 array as f32.
+__device__ __forceinline__ float load_any(const void *p, int dt, size_t i) {
+    if (dt == DT_F16) return load_act<DT_F16>(p, i);
+    if (dt == DT_BF16) return load_act<DT_BF16>(p, i);
+    return load_act<DT_F32>(p, i);
+}
+
+// The gated shared expert's term T(sigmoid(gate) * shared) in dtype T = dt, rounding where MLX's Sigmoid and
+// Multiply round in T (REDUCE_GATED_SHARED_SOURCE, beamivalice/sushi src/exl3/expert_exl3_kernels.zig:2410-2431):
+// ex = T(exp|g|), rc = T(1 / T(1 + ex)), sig = g < 0 ? rc : T(1 - rc).  exp runs in f64 and is rounded to f32 first.
+__device__ __forceinline__ float gated_shared(int dt, float g, float shared) {
+    const float ex = round_act(dt, (float)exp((double)fabsf(g)));
+    const float rc = round_act(dt, 1.0f / round_act(dt, 1.0f + ex));
+    const float sig = g < 0.0f ? rc : round_act(dt, 1.0f - rc);
+    return round_act(dt, sig * shared);
+}
+
 __device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
 
 }  // namespace exl3

@@ -389,7 +389,7 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
                 yrow = (size_t)(slot - a.sh_from);
             } else {
                 yrow = (size_t)(slot / a.fold_topk);
-                sc = a.fold_scores[slot];
+                sc = load_any(a.fold_scores, a.score_dtype, slot);
             }
         } else {
             yrow = (size_t)c.g * a.rows + r;
@@ -442,7 +442,11 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
                     *cw = 0ull;
                 }
             } else {
-                if (a.fold_shared) v = round_y(a.y_dtype, v) + load_y(a.fold_shared, a.y_dtype, i);
+                if (a.fold_shared) {
+                    const float sh = load_y(a.fold_shared, a.y_dtype, i);
+                    v = round_y(a.y_dtype, v) +
+                        (a.fold_gate ? gated_shared(a.y_dtype, load_y(a.fold_gate, a.y_dtype, yrow), sh) : sh);
+                }
                 store_y(a.y, a.y_dtype, i, v);
             }
             // No split of this launch touches the word again, and the next launch reads it after the kernel boundary:

@@ -75,8 +75,10 @@ struct GemvArgs {
     unsigned long long *fold; // fixed-point fused finish: one word per output, zero between calls; null = off
     int fold_arrivals;        // contributions per output word (the dense GEMV's splits; topk * splits for the MoE down)
     int fold_topk;            // > 0: MoE down -- slot s folds into output row s / fold_topk, scaled by fold_scores[s]
-    const float *fold_scores;
+    const void *fold_scores;  // [slots] in score_dtype (f32, bf16 or f16)
+    int score_dtype;
     const void *fold_shared;  // MoE: [rows][out] in y's dtype, added after the routed sum's rounding; null = none
+    const void *fold_gate;    // MoE: [rows] gate logits in y's dtype: fold_shared is added as sigmoid(gate) * shared
     // A fused shared expert's own fold words [rows][out] and the words where the rounded routed and shared sums
     // meet (see sh_from below); beside the fold's other fields, which the finish reads together.
     unsigned long long *sh_fold;
@@ -136,9 +138,11 @@ struct ReduceArgs {
     int rows;
     const uint32_t *slots;
     int bank_limit;
-    const float *scores;
+    const void *scores;   // [slots] in score_dtype
+    int score_dtype;
     const uint16_t *svh;  // [E][hidden]
     const void *shared;   // [rows][hidden] in y dtype, or null
+    const void *gate;     // [rows] in y dtype: shared is added as sigmoid(gate) * shared; null = plain add
     void *y;
     int y_dtype;
     float out_scale;

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
     for (int kk = wave; kk < a.topk; kk += RW) {
         const int slot = row * a.topk + kk;
         const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
-        const float sc = a.scores[slot];
+        const float sc = load_any(a.scores, a.score_dtype, slot);
         const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
         const float s0 = h2f(sv[lane]), s1 = h2f(sv[lane + 64]);
         float v0, v1;
@@ -95,16 +95,11 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
     }
     const size_t yo = (size_t)row * a.hidden + base;
     if (a.shared) {
-        float s0, s1;
-        if (a.y_dtype == DT_F16) {
-            s0 = load_act<DT_F16>(a.shared, yo + lane);
-            s1 = load_act<DT_F16>(a.shared, yo + lane + 64);
-        } else if (a.y_dtype == DT_BF16) {
-            s0 = load_act<DT_BF16>(a.shared, yo + lane);
-            s1 = load_act<DT_BF16>(a.shared, yo + lane + 64);
-        } else {
-            s0 = load_act<DT_F32>(a.shared, yo + lane);
-            s1 = load_act<DT_F32>(a.shared, yo + lane + 64);
+        float s0 = load_any(a.shared, a.y_dtype, yo + lane), s1 = load_any(a.shared, a.y_dtype, yo + lane + 64);
+        if (a.gate) {  // sigmoid(gate) * shared in y's dtype (REDUCE_GATED_SHARED_SOURCE)
+            const float g = load_any(a.gate, a.y_dtype, row);
+            s0 = gated_shared(a.y_dtype, g, s0);
+            s1 = gated_shared(a.y_dtype, g, s1);
         }
         y0 = round_to(a.y_dtype, y0) + s0;
         y1 = round_to(a.y_dtype, y1) + s1;

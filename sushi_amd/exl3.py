@@ -526,7 +526,7 @@ def _moe_prep(x: torch.Tensor, inds: torch.Tensor, scores: torch.Tensor):
     rows = x.numel() // x.shape[-1]
     x2 = x.reshape(rows, x.shape[-1])
     inds2 = inds.reshape(rows * topk).contiguous()
-    sc2 = scores.reshape(rows * topk).to(torch.float32).contiguous()
+    sc2 = scores.reshape(rows * topk).contiguous()  # f32, bf16 or f16: the library reads each as it is
     return x2, inds2, sc2, rows, topk
 
 
@@ -546,7 +546,7 @@ def _bank_shape(bank: Bank, hidden: int):
 
 
 def _moe(x: torch.Tensor, bank: Bank, inds: torch.Tensor, scores: torch.Tensor, dec: Decode, verify_rows: bool,
-         shared: Optional[torch.Tensor], limit: int) -> torch.Tensor:
+         shared: Optional[torch.Tensor], limit: int, gate: Optional[torch.Tensor] = None) -> torch.Tensor:
     dec.require_table()
     x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
     hidden = int(x.shape[-1])
@@ -561,8 +561,18 @@ def _moe(x: torch.Tensor, bank: Bank, inds: torch.Tensor, scores: torch.Tensor, 
     L = _lib.load()
     ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, inter))
     cb = _lib.BankT(g.c(), u.c(), d.c())
+    if gate is not None:
+        if gate.numel() != rows or gate.dtype != y.dtype or shared is None:
+            raise BadExl3Shape("moe: the shared expert's gate is one logit per row in the output's dtype")
+        gate = gate.reshape(rows).contiguous()
+        _need_gpu(gate)
+        _check(L.exl3_moe_with_gated_shared(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, experts,
+                                            ctypes.byref(cb), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"),
+                                            topk, dec.c(), int(verify_rows), shared.data_ptr(), gate.data_ptr(),
+                                            y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device)))
+        return y.reshape(x.shape)
     _check(L.exl3_moe(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, experts, ctypes.byref(cb), inds2.data_ptr(),
-                      sc2.data_ptr(), topk, dec.c(), int(verify_rows), int(limit),
+                      sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(verify_rows), int(limit),
                       None if shared is None else shared.data_ptr(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
                       ws.numel(), _stream(x.device)))
     return y.reshape(x.shape)
@@ -576,6 +586,12 @@ def moe(x, bank: Bank, inds, scores, dec: Decode, verify_rows: bool = False) -> 
 def moe_with_shared(x, bank: Bank, inds, scores, dec: Decode, verify_rows: bool, shared) -> torch.Tensor:
     """`moeWithShared` (root.zig:56-67): adds an already gated shared expert after the routed output's rounding."""
     return _moe(x, bank, inds, scores, dec, verify_rows, shared, 0)
+
+
+def moe_with_gated_shared(x, bank: Bank, inds, scores, dec: Decode, verify_rows: bool, down, gate) -> torch.Tensor:
+    """`moeWithGatedShared` (root.zig:71-90): routed + sigmoid(gate) * down, with `down` the shared expert's output
+    [..., D] and `gate` its logit [..., 1], both in x's dtype, rounded where MLX's Sigmoid, Multiply and Add round."""
+    return _moe(x, bank, inds, scores, dec, verify_rows, down, 0, gate)
 
 
 def moe_clamped(x, bank: Bank, inds, scores, dec: Decode, limit: int, shared=None) -> torch.Tensor:
@@ -601,8 +617,9 @@ def moe_ragged(x, rb: Ragged, inds, scores, dec: Decode, verify_rows: bool = Fal
     ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, rb.inter))
     cr = rb.c()
     _check(L.exl3_moe_ragged(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr), inds2.data_ptr(),
-                             sc2.data_ptr(), topk, dec.c(), int(limit), None if shared is None else shared.data_ptr(),
-                             y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device)))
+                             sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(limit),
+                             None if shared is None else shared.data_ptr(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
+                             ws.numel(), _stream(x.device)))
     return y.reshape(x.shape)
 
 
@@ -660,8 +677,9 @@ def moe_with_shared_bank(x, bank: Bank, shared_bank: Bank, inds, scores, dec: De
     cb = _lib.BankT(bank.gate.c(), bank.up.c(), bank.down.c())
     cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
     rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, experts, ctypes.byref(cb),
-                                     ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), topk, dec.c(), int(limit),
-                                     y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device))
+                                     ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"), topk,
+                                     dec.c(), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
+                                     _stream(x.device))
     if rc == EXL3_DECLINED:
         return _moe(x, bank, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
     _check(rc)
@@ -688,9 +706,9 @@ def moe_ragged_with_shared_bank(x, rb: Ragged, shared_bank: Bank, inds, scores, 
     cr = rb.c()
     cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
     rc = L.exl3_moe_ragged_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr),
-                                            ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), topk, dec.c(),
-                                            int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
-                                            _stream(x.device))
+                                            ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"),
+                                            topk, dec.c(), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
+                                            ws.numel(), _stream(x.device))
     if rc == EXL3_DECLINED:
         return moe_ragged(x, rb, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
     _check(rc)

@@ -64,11 +64,18 @@ def test_moe_refusals():
     lib = L.load()
     d = L.DecodeT(1, 16, -1)
     bank = L.BankT()
-    args = lambda topk, clamp: (None, 0, 1, 128, 128, 4, ctypes.byref(bank), None, None, topk, d, 0, clamp, None,
-                                None, 0, None, 0, None)
+    args = lambda topk, clamp, sdt=0: (None, 0, 1, 128, 128, 4, ctypes.byref(bank), None, None, sdt, topk, d, 0,
+                                       clamp, None, None, 0, None, 0, None)
     assert lib.exl3_moe(*args(33, 0)) == -4  # Exl3TopKExceedsReduceBank
     assert lib.exl3_moe(*args(8, 129)) == -6  # InvalidExl3Clamp
     assert lib.exl3_moe(*args(8, 0)) == -1  # projections missing
+    assert lib.exl3_moe(*args(8, 0, sdt=7)) == -2  # scores dtype: f32, bf16 or f16 (root.zig:114)
+    for sdt in (1, 2):
+        assert lib.exl3_moe(*args(8, 0, sdt=sdt)) == -1  # bf16 / f16 scores admitted (then the missing projections)
+    # the gated shared expert needs both its output and its gate
+    gargs = (None, 0, 1, 128, 128, 4, ctypes.byref(bank), None, None, 0, 8, d, 0, None, None, None, 0, None, 0, None)
+    assert lib.exl3_moe_with_gated_shared(*gargs) == -1
+    assert "gate" in L.last_error()
     assert lib.exl3_route_topk(None, 1, 2000, 8, None, None, None) == -1
 
 

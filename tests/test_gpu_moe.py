@@ -335,7 +335,7 @@ def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
     y = torch.empty_like(xd)
     x2 = xd.contiguous()
     rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), k, exl3.MCG.c(), 0,
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
                                      y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
     assert rc == 0, exl3._lib.last_error()
     ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
@@ -365,7 +365,7 @@ def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
     y0 = torch.full_like(xd, 7.0)
     x2 = xd.contiguous()
     rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), k, exl3.MCG.c(), 0,
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
                                      y0.data_ptr(), exl3._dt(y0, "y"), ws.data_ptr(), ws.numel(),
                                      exl3._stream(dev))
     torch.cuda.synchronize()
@@ -429,3 +429,107 @@ def test_moe_down_fold_outputs_past_its_range(dev, ydt):
         assert np.isfinite(y[under]).all()
     else:
         assert max_abs_rel(y, y64) < BAR + 2.0 ** -8
+
+
+@pytest.mark.parametrize("rows", [2, 20])
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16])
+def test_moe_scores_in_bf16_and_f16(dev, rows, sdt):
+    """Scores in bf16 / f16 (root.zig:114 admits them) are read as they are: the layer equals the call with the same
+    values in f32 byte for byte (fold finish at 2 rows, sorted arm at 20), and the oracle to the bar."""
+    print(f"[moe] scores {sdt} rows={rows}", flush=True)
+    E, hidden, inter, k, n = 16, 256, 256, 4, 32
+    b = synth.bank(31, "moesc", E, hidden, inter, n, norm=True)
+    bd = _to(b, dev)
+    x = synth.normal(31, "x", (rows, hidden))
+    inds, scores = _route(31 + rows, rows, E, k)
+    sc_low = torch.from_numpy(scores).to(sdt)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    y_low = exl3.moe(x.to(dev), bd, xi, sc_low.to(dev), exl3.MCG)
+    y_f32 = exl3.moe(x.to(dev), bd, xi, sc_low.float().to(dev), exl3.MCG)
+    assert torch.equal(y_low, y_f32)
+    want = _oracle_moe(b, x.float().numpy(), inds, sc_low.float().numpy(), hidden, inter, n, O.decode(O.CB_MCG))
+    assert max_abs_rel(y_low.float().cpu().numpy(), want) < BAR
+
+
+@pytest.mark.parametrize("fold", [1, 0])
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float16])
+def test_moe_gated_shared_term_every_gate_logit(dev, ydt, fold):
+    """`moeWithGatedShared` (root.zig:71-90) over every non-NaN bf16 / f16 gate logit, one per row, both finishes:
+    with scores 0 the routed sum is exactly 0, so each output is T(sigmoid(gate) * shared) and must equal the
+    oracle's rounding chain (REDUCE_GATED_SHARED_SOURCE, expert_exl3_kernels.zig:2410-2431) bit for bit (the
+    reference's test, :7258-7315, holds its kernel to MLX's ops the same way)."""
+    print(f"[moe] gated shared every logit {ydt} fold={fold}", flush=True)
+    hidden, inter, rows = 128, 128, 4096
+    b = synth.bank(33, "gsh", 1, hidden, inter, 32, norm=True)
+    bd = _to(b, dev)
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    if ydt == torch.bfloat16:
+        allg = torch.from_numpy((bits << 16).view(np.float32)).to(torch.bfloat16)
+    else:
+        allg = torch.from_numpy(bits.astype(np.uint16).view(np.float16))
+    allg = allg[~torch.isnan(allg.float())]
+    shared_vals = torch.from_numpy(np.linspace(-3.0, 3.0, hidden, dtype=np.float32)).to(ydt)
+    dt_code = 1 if ydt == torch.bfloat16 else 0
+    with exl3.arm_overrides(moe_fold=fold):
+        for start in range(0, allg.numel(), rows):
+            g = allg[start:start + rows]
+            r = g.numel()
+            x = synth.normal(33, f"gsh.x{r}", (r, hidden)).to(ydt)
+            shared = shared_vals.repeat(r, 1)
+            y = exl3.moe_with_gated_shared(x.to(dev), bd, torch.zeros(r, 1, dtype=torch.int32, device=dev),
+                                           torch.zeros(r, 1, dtype=torch.float32, device=dev), exl3.MCG, False,
+                                           shared.to(dev), g.reshape(r, 1).to(dev))
+            got = y.float().cpu().numpy()
+            want = O.gated_shared_terms(g.float().numpy(), shared.float().numpy(), dt_code)
+            same = (got == want) | (np.isnan(got) & np.isnan(want))
+            bad = np.argwhere(~same)
+            assert bad.size == 0, (len(bad), [(float(g[i]), got[i, j], want[i, j]) for i, j in bad[:4]])
+
+
+@pytest.mark.parametrize("ydt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows", [1, 6, 24])
+def test_moe_with_gated_shared_against_oracle(dev, rows, ydt):
+    """routed + sigmoid(gate) * shared with real scores: T(T(routed) + T(sig * shared)) against the oracle's routed
+    sum and its gated term.  In bf16 the kernel's routed sum (gate and up kept in f32) and the oracle's (rounded to
+    f16 by its project) may round one bf16 ulp apart, and the final rounding another: the bar allows those two."""
+    print(f"[moe] gated shared rows={rows} {ydt}", flush=True)
+    E, hidden, inter, k, n = 16, 256, 256, 4, 32
+    b = synth.bank(35, "gsh2", E, hidden, inter, n, norm=True)
+    x = synth.normal(35, "x", (rows, hidden)).to(ydt)
+    inds, scores = _route(35 + rows, rows, E, k)
+    shared = synth.normal(36, "sh", (rows, hidden)).to(ydt)
+    gate = (synth.normal(37, "g", (rows, 1)) * 3).to(ydt)
+    y = exl3.moe_with_gated_shared(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                                   torch.from_numpy(scores).to(dev), exl3.MCG, False, shared.to(dev), gate.to(dev))
+    routed = _oracle_moe(b, x.float().numpy(), inds, scores, hidden, inter, n, O.decode(O.CB_MCG))
+    routed_t = torch.from_numpy(routed).to(ydt).float().numpy()
+    sh, gv = shared.float().numpy(), gate.float().numpy()
+    term = O.gated_shared_terms(gv[:, 0], sh, 1 if ydt == torch.bfloat16 else 2)
+    want = torch.from_numpy((routed_t + term).astype(np.float32)).to(ydt).float().numpy()
+    bar = BAR + (2 * 2.0 ** -8 if ydt == torch.bfloat16 else 0.0)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < bar
+
+
+@pytest.mark.parametrize("rows", [1, 5, 20])
+@pytest.mark.parametrize("rates", [(32, 48, 40), (48, 32, 32), (32, 32, 64)])
+def test_moe_mixed_projection_rates(dev, rows, rates):
+    """A uniform bank whose gate, up and down sit at different rates (moeMixedDecode, root.zig:705-722): gate and up
+    run one launch each when they differ, down at its own rate; per-slot arm up to 8 rows, the sorted arm above.
+    The fused shared-bank form declines (the wrapper makes the pair of calls)."""
+    print(f"[moe] mixed rates {rates} rows={rows}", flush=True)
+    E, hidden, inter, k = 12, 256, 256, 3
+    b = synth.bank(39, "mixed", E, hidden, inter, rates, norm=True)
+    x = synth.normal(39, "x", (rows, hidden))
+    inds, scores = _route(39 + rows, rows, E, k)
+    xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
+    odec = O.decode(O.CB_MCG)
+    want = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, scores, hidden, inter,
+                             rates, odec, threads=8)
+    y = exl3.moe(x.to(dev), _to(b, dev), xi, sc, exl3.MCG)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+    sh = synth.bank(40, "mixed.sh", 1, hidden, inter, 32, norm=True)
+    y2 = exl3.moe_with_shared_bank(x.to(dev), _to(b, dev), _to(sh, dev), xi, sc, exl3.MCG)
+    shared = O.moe_swiglu_rows(x.float().numpy(), _np(sh.gate), _np(sh.up), _np(sh.down), np.zeros((rows, 1)),
+                               np.ones((rows, 1)), hidden, inter, (32, 32, 32), odec, threads=8)
+    want2 = want.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
+    assert max_abs_rel(y2.float().cpu().numpy(), want2) < BAR

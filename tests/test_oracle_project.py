@@ -154,6 +154,49 @@ def test_moe_swiglu_rows_is_the_host_function_row_by_row_uniform_and_ragged():
         assert np.array_equal(yr[r], want), r
 
 
+def _gated_term_independent(g, sh, dtype):
+    """The gated shared term restated with numpy float16 / torch bfloat16 rounding (not the oracle's helpers)."""
+    import torch
+
+    if dtype == 0:
+        r = lambda v: np.float32(np.float16(np.float32(v)))  # noqa: E731
+    else:
+        r = lambda v: np.float32(torch.tensor(np.float32(v)).to(torch.bfloat16).float().item())  # noqa: E731
+    ex = r(np.float32(np.exp(abs(np.float64(g)))))
+    rc = r(np.float32(1.0) / r(np.float32(1.0) + ex))
+    sig = rc if g < 0 else r(np.float32(1.0) - rc)
+    return r(np.float32(sig) * np.float32(sh))
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_gated_shared_term_every_gate_value(dtype):
+    """ox_gated_shared_term (REDUCE_GATED_SHARED_SOURCE's rounding chain, expert_exl3_kernels.zig:2410-2431) over
+    every non-NaN f16 (dtype 0) or bf16 (dtype 1) gate, against an independent rounding of the same chain, and the
+    sigmoid's closed form to within T's rounding."""
+    import torch
+
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    if dtype == 0:
+        g_all = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    else:
+        g_all = (bits << 16).view(np.float32)
+    g_all = g_all[~np.isnan(g_all)]
+    rng = np.random.default_rng(dtype)
+    for g in g_all[rng.permutation(g_all.size)[:3000]]:  # a sample with the independent (slow, per-value) restatement
+        for sh in (1.0, -2.75, 0.3):
+            got, want = O.gated_shared_term(float(g), sh, dtype), _gated_term_independent(float(g), sh, dtype)
+            assert got == want or (np.isnan(got) and np.isnan(want)), (g, sh, got, want)
+    ulp = 2.0 ** -10 if dtype == 0 else 2.0 ** -7
+    big = np.log(65504.0) if dtype == 0 else np.log(np.finfo(np.float32).max)  # exp|g| past T's range
+    for g in g_all[np.isfinite(g_all)][::7]:
+        sig = O.gated_shared_term(float(g), 1.0, dtype)
+        if abs(g) > big:  # T(exp|g|) is inf: the chain's sigmoid is exactly 0 below and 1 above
+            assert sig == (0.0 if g < 0 else 1.0), (g, sig)
+            continue
+        exact = 1.0 / (1.0 + np.exp(-np.float64(g)))
+        assert abs(sig - exact) <= 3 * ulp * max(exact, 2.0 ** -14) + 2.0 ** -24, (g, sig, exact)
+
+
 def _nonfinite_logit_rows():
     rng = np.random.default_rng(12)
     rows = rng.standard_normal((6, 40)).astype(np.float32)
