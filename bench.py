@@ -445,6 +445,8 @@ def sweep(which: str):
             cases.append(("c3", 4096, 14336, 48, rows, exl3.INST3, "3inst"))
     if which in ("c5", "all"):
         print(json.dumps(bench_moe_c5()), flush=True)
+    if which in ("moe_prefill", "all"):
+        bench_moe_prefill()
     if which in ("pack", "all"):
         for pm in (False, True):
             print(json.dumps(bench_pack(pm)), flush=True)
@@ -526,6 +528,51 @@ def bench_moe_c5(batch: int = 64, layers: int = 4, replays: int = 4):
     return {"config": "c5", "batch": batch, "experts": E1 + E2, "bpw": 1.75, "layer_us": round(layer_us, 3),
             "us_per_token": round(layer_us / batch, 3), "effective_GBps": round(alg / (layer_us * 1e-6) / 1e9, 1),
             "hbm_frac": round(alg / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4):
+    """configs[3]'s layer (E=256 + shared, hidden 2048, inter 768, K2 MCG, top-8) at prefill widths, on the routed
+    GEMM arm and on the decode chain's expert windows (arm overrides): microseconds per layer and per token, each a
+    median of 7 replays of `layers` layers from a HIP graph."""
+    import statistics
+
+    import torch
+
+    from sushi_amd import exl3, synth
+
+    dev = torch.device("cuda:0")
+    E, hidden, inter, n, k = 256, 2048, 768, 32, 8
+    bank = synth.bank(3, "c4", E, hidden, inter, n, device=dev, norm=True)
+    shared = synth.bank(3, "c4.shared", 1, hidden, inter, n, device=dev, norm=True)
+    out = []
+    for batch in batches:
+        xs = [synth.normal(3, f"c4.pf{batch}.{l}", (batch, hidden), device=dev) for l in range(layers)]
+        routes = [exl3.moe_routing_chain(synth.normal(3, f"c4.pfl{batch}.{l}", (batch, E), dtype=torch.float32)
+                                         .to(dev), k) for l in range(layers)]
+        line = {"config": "c4_prefill", "batch": batch, "slots_per_expert": round(batch * k / E, 2)}
+        for arm, knob in (("gemm", 1), ("windows", 0)):
+            with exl3.arm_overrides(moe_gemm=knob):
+                def chain():
+                    return [exl3.moe_with_shared_bank(x, bank, shared, i, s, exl3.MCG)
+                            for x, (i, s) in zip(xs, routes)]
+                chain()
+                torch.cuda.synchronize()
+                g = _capture(chain, dev)
+                stream = torch.cuda.current_stream(dev)
+                ts = []
+                for _ in range(ROUNDS):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    g.replay()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    ts.append(e0.elapsed_time(e1) * 1e3 / layers)
+                us = statistics.median(ts)
+                line[arm] = {"layer_us": round(us, 1), "us_per_token": round(us / batch, 3)}
+                del g
+        print(json.dumps(line), flush=True)
+        out.append(line)
+    return out
 
 
 def copy_calibration(mib: int, reps: int = 4):
@@ -667,7 +714,7 @@ def main() -> int:
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
-    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
+    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "moe_prefill", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     args = ap.parse_args()
     if args.sweep:
         global SWEEP_GRAPHS

@@ -58,6 +58,9 @@ constexpr size_t kCounterSlots = (size_t(1) << 20) / (sizeof(uint32_t) * COUNTER
 
 bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
 
+// The rates the GEMV and the GEMM read with a lane reader.
+bool lane_rate(int n) { return n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64; }
+
 // Arm overrides (exl3_set_override): one word per knob, INT32_MIN = unset.  Read with a relaxed load at each call,
 // so an unset knob costs one load and nothing in the environment changes an arm.
 std::atomic<int32_t> g_override[EXL3_KNOB_COUNT] = {};
@@ -292,6 +295,39 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0
     return p;
 }
 
+// The routed GEMM arm (prefill widths): slots sorted by expert into windows of up to MOE_GEMM_WINDOW_ROWS rows, each
+// window's rows prepared into MFMA fragment order and run through the decode-once GEMM (each weight decoded once per
+// window instead of once per 4-row GEMV window), then the mid, the down GEMM and the reduce.  Taken when the layer
+// averages at least kMoeGemmMinSlotsPerExpert slots per expert, on a uniform bank at one lane-reader rate.
+constexpr int kMoeGemmMinSlotsPerExpert = 16;
+
+struct MoeGemmPlan {
+    int max_windows, max_tiles;
+    size_t tables, xp_gu, xp_down, planes_gu, planes_down;
+    size_t total() const { return kZeroBytes + tables + 2 * xp_gu + xp_down + 2 * planes_gu + planes_down; }
+};
+
+// Windows and tiles for at most `experts` experts hit (the size queries use kMoeGemmMaxExperts).
+MoeGemmPlan plan_moe_gemm(int nslots, int hidden, int inter, int experts) {
+    MoeGemmPlan p;
+    const int W = MOE_GEMM_WINDOW_ROWS;
+    p.max_windows = std::min(nslots, experts + (nslots + W - 1) / W);
+    p.max_tiles = (nslots + 15) / 16 + std::min(nslots, experts);
+    p.tables = align_up(2 * sizeof(uint32_t)) + align_up((size_t)nslots * 4) + 4 * align_up((size_t)p.max_windows * 4) +
+               align_up((size_t)p.max_tiles * 4);
+    p.xp_gu = align_up((size_t)p.max_tiles * 16 * hidden * 2);
+    p.xp_down = align_up((size_t)p.max_tiles * 16 * inter * 2);
+    p.planes_gu = align_up((size_t)nslots * inter * sizeof(float));
+    p.planes_down = align_up((size_t)nslots * hidden * sizeof(float));
+    return p;
+}
+
+bool moe_gemm_wanted(int nslots, int experts, bool uniform_lane_rate) {
+    const int k = knob(EXL3_KNOB_MOE_GEMM, -1);
+    if (k == 0 || !uniform_lane_rate || experts > kMoeGemmMaxExperts) return false;
+    return k > 0 || (long)nslots >= (long)kMoeGemmMinSlotsPerExpert * experts;
+}
+
 bool moe_windowed(int rows, int nslots, int experts) {
     return rows > moe_decode_rows_max() && nslots <= kMoeWindowMaxSlots && experts <= kMoeWindowMaxExperts;
 }
@@ -325,9 +361,10 @@ struct SharedBank {
 // The shared bank's rows need the per-slot arm, a 16-bit output dtype (the combine word holds both rounded sums),
 // the routed and shared folds (routed, shared and combine words: three per output), and, for a uniform bank, the
 // routed rate.
-bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts) {
+bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts, int n) {
     const int nslots = rows * topk;
     if (y_dtype == EXL3_DT_F32) return false;
+    if (moe_gemm_wanted(nslots, experts, lane_rate(n))) return false;  // the GEMM arm serves such layers
     const bool windowed = rows > moe_decode_rows_max();
     if (windowed && !(moe_windows_enabled() && moe_windowed(rows, nslots, experts))) return false;
     const MoePlan p = plan_moe(nslots, hidden, inter, windowed, rows);
@@ -345,6 +382,94 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
                    void *ws, size_t ws_bytes, hipStream_t stream, const SharedBank *sb = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
+    if (!sb && !meta && n[0] == n[1] && n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
+        const MoeGemmPlan gp = plan_moe_gemm(nslots, hidden, inter, experts);
+        if (ws_bytes < gp.total() || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
+            return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", gp.total(),
+                        ws_bytes);
+        char *w = static_cast<char *>(ws) + kZeroBytes;
+        MoeGemmArgs g{};
+        auto take = [&](size_t bytes) {
+            char *p = w;
+            w += bytes;
+            return p;
+        };
+        uint32_t *counts = reinterpret_cast<uint32_t *>(take(align_up(2 * sizeof(uint32_t))));
+        g.win.win_count = counts;
+        g.win.tile_count = counts + 1;
+        g.win.sorted = reinterpret_cast<uint32_t *>(take(align_up((size_t)nslots * 4)));
+        g.win.win_expert = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
+        g.win.win_rows = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
+        g.win.win_start = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
+        g.win.win_tile0 = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
+        g.win.tile_window = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_tiles * 4)));
+        uint16_t *xp_g = reinterpret_cast<uint16_t *>(take(gp.xp_gu));
+        uint16_t *xp_u = reinterpret_cast<uint16_t *>(take(gp.xp_gu));
+        uint16_t *xp_d = reinterpret_cast<uint16_t *>(take(gp.xp_down));
+        float *pl_g = reinterpret_cast<float *>(take(gp.planes_gu));
+        float *pl_u = reinterpret_cast<float *>(take(gp.planes_gu));
+        float *pl_d = reinterpret_cast<float *>(take(gp.planes_down));
+        hipError_t e = run_moe_gemm_windows(inds, nslots, experts, g.win, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (gemm windows)");
+        g.x = x;
+        g.x_dtype = x_dtype;
+        g.topk = topk;
+        g.experts = experts;
+        g.n = n[0];
+        g.k = k;
+        g.clamp_limit = (float)clamp_limit;
+        g.max_tiles = gp.max_tiles;
+        g.max_windows = gp.max_windows;
+        // gate and up: prepared inputs, then one GEMM launch for both (grid z = projection)
+        g.in = hidden;
+        g.out = inter;
+        for (int i = 0; i < 2; i++) {
+            g.trellis[i] = tr[i];
+            g.suh[i] = su[i];
+        }
+        g.xp[0] = xp_g;
+        g.xp[1] = xp_u;
+        g.planes[0] = pl_g;
+        g.planes[1] = pl_u;
+        e = run_moe_gemm_prepare(g, 2, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (gemm prepare)");
+        e = run_moe_gemm(fam, g, 2, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (gemm gate/up)");
+        // the mid (down's prepared input), then the down GEMM
+        MoeGemmArgs d = g;
+        d.in = inter;
+        d.out = hidden;
+        d.mid_planes[0] = pl_g;
+        d.mid_planes[1] = pl_u;
+        d.mid_svh[0] = sv[0];
+        d.mid_svh[1] = sv[1];
+        d.down_suh = su[2];
+        d.trellis[0] = tr[2];
+        d.xp[0] = xp_d;
+        d.planes[0] = pl_d;
+        e = run_moe_gemm_mid(d, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (gemm mid)");
+        e = run_moe_gemm(fam, d, 1, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (gemm down)");
+        // the score-weighted reduce over each token's slots (+ a shared expert)
+        ReduceArgs r{};
+        r.part = pl_d;
+        r.splits = 1;
+        r.hidden = hidden;
+        r.topk = topk;
+        r.rows = rows;
+        r.slots = inds;
+        r.bank_limit = experts;
+        r.scores = scores;
+        r.score_dtype = scores_dtype;
+        r.svh = sv[2];
+        r.shared = shared;
+        r.gate = shared ? shared_gate : nullptr;
+        r.y = y;
+        r.y_dtype = y_dtype;
+        r.out_scale = 1.0f;
+        return launched(run_moe_reduce(r, stream), "exl3_moe (gemm reduce)");
+    }
     // With a fused shared bank its rows join either arm as groups of SH_ROWS rows placed first in the grid; planes
     // are kept per row (slots nslots .. nslots + rows - 1), so the plan counts rows more.
     const int sh_groups = sb ? (rows + SH_ROWS - 1) / SH_ROWS : 0;
@@ -592,7 +717,6 @@ int32_t declined(const char *fmt, ...) {
     return EXL3_DECLINED;
 }
 
-bool lane_rate(int n) { return n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64; }
 
 // A bank whose three projections share one admitted rate, as a SharedBank (expert 0 of it serves).
 int32_t shared_bank_checks(const exl3_bank_t *b, const char *what, SharedBank *out) {
@@ -744,6 +868,10 @@ size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32
     const int nslots = rows * topk;
     size_t need = plan_moe(nslots, hidden, inter, false).total();
     if (moe_windowed(rows, nslots, 1)) need = std::max(need, plan_moe(nslots, hidden, inter, true).total());
+    // the GEMM arm, for any expert count it serves (a layer with fewer experts takes less)
+    const int gk = knob(EXL3_KNOB_MOE_GEMM, -1);
+    if (gk > 0 || (gk != 0 && nslots >= kMoeGemmMinSlotsPerExpert))
+        need = std::max(need, plan_moe_gemm(nslots, hidden, inter, kMoeGemmMaxExperts).total());
     return need;
 }
 
@@ -826,7 +954,7 @@ int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, 
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: null operand");
-    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts))
+    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts, routed_n))
         return declined("moe_with_shared_bank: declined (rows=%d, y dtype %d, rates %d/%d): run the shared expert as "
                         "a one-expert exl3_moe and pass it to exl3_moe as `shared`", rows, y_dtype, routed_n, sb.n);
     const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
@@ -867,7 +995,7 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
     }
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: null operand");
-    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts))
+    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0))
         return declined("moe_ragged_with_shared_bank: declined (rows=%d, y dtype %d): run the shared expert as a "
                         "one-expert exl3_moe and pass it to exl3_moe_ragged as `shared`", rows, y_dtype);
     const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);

@@ -369,6 +369,14 @@ __device__ __forceinline__ float load_any(const void *p, int dt, size_t i) {
     return load_act<DT_F32>(p, i);
 }
 
+// SiLU of the routed chain's mid: g * sigmoid(g), evaluated on exp(-|g|) so neither branch overflows (the
+// reference's mid uses the same split, DOWN_FUSED_SOURCE, src/exl3/expert_exl3_kernels.zig:1838-1925).
+__device__ __forceinline__ float silu(float g) {
+    const float e = __expf(-fabsf(g));
+    const float s = g >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+    return g * s;
+}
+
 // The gated shared expert's term T(sigmoid(gate) * shared) in dtype T = dt, rounding where MLX's Sigmoid and
 // Multiply round in T (REDUCE_GATED_SHARED_SOURCE, beamivalice/sushi src/exl3/expert_exl3_kernels.zig:2410-2431):
 // ex = T(exp|g|), rc = T(1 / T(1 + ex)), sig = g < 0 ? rc : T(1 - rc).  exp runs in f64 and is rounded to f32 first.

@@ -268,24 +268,18 @@ constexpr int G2_EP = 129;   // epilogue staging pitch (floats)
 constexpr int G4_WAVES = 12;
 constexpr int G4_THREADS = 64 * G4_WAVES;
 
-template <int FAM, int N>
-__global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
+// One workgroup's 256-row x 128-column output tile: output group og of a bank whose tiles start at `bank`
+// ([in/16][out/16][N]), prepared rows in fragment tiles from xfrag0 (row tile rt at xfrag0 + rt * (in / 32) * 512), of
+// which the first `rows` (<= 256) are live.  The epilogue hands each live row's raw inner products to
+// emit(m, v0, v1, lane) (columns lane and lane + 64 of the group, m the row within the tile); the caller applies the
+// output transform or stores the raw values.
+template <int FAM, int N, class Emit>
+__device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16_t *__restrict__ bank,
+                                           const uint16_t *__restrict__ xfrag0, int rows, const DecodeK &k,
+                                           uint16_t (*Bs)[128 * G2_BP], Emit emit) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int IT = a.in >> 4, OT = a.out >> 4;
-    const int nog = a.out / 128, nm = (a.rows + G2_MT - 1) / G2_MT;
-    const int L = blockIdx.x;
-    int og, mt;
-    if (nm <= 8 && 8 % nm == 0 && nog % (8 / nm) == 0) {
-        const int xcd = L & 7, per = 8 / nm;
-        mt = xcd / per;
-        og = (L >> 3) * per + xcd % per;
-    } else {
-        og = L % nog;
-        mt = L / nog;
-    }
-    const int g = blockIdx.z;
-    __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
+    const int IT = in >> 4, OT = out >> 4;
     const int nks = IT / 4;  // even: in is a multiple of 128
     constexpr int AW = LaneBits<N>::AW;
 
@@ -293,10 +287,9 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
         // ---- decode waves
         const int r = wave - 8;
         const int o = lane >> 3, j = lane & 7;
-        const DecodeK k = a.k;
         const bool masked = k.wmask != 0xFFFFu;
         // the uniform start of k-tile row r of the group in k-step 0, plus the lane's tile offset (the GEMV's reader)
-        const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8) * N;
+        const uint16_t *tb = bank + ((size_t)r * OT + og * 8) * N;
         const uint32_t lane_words = (uint32_t)(o * N) >> 1;
         const size_t kstep = (size_t)4 * OT * N;  // halves from one k-step's row r to the next
         auto load_tile = [&](int ks, uint32_t (&W)[AW]) __attribute__((always_inline)) {
@@ -338,14 +331,14 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
     }
 
     // ---- MFMA waves
-    const int m0 = mt * G2_MT + (wave >> 1) * 64, cb0 = (wave & 1) * 4;
+    const int m0 = (wave >> 1) * 64, cb0 = (wave & 1) * 4;
     const int c = lane & 15, h = lane >> 4;
-    const int RT = (a.rows + 15) / 16;
+    const int RT = (rows + 15) / 16;
     const uint16_t *xfrag[4];
 #pragma unroll
     for (int rb = 0; rb < 4; rb++) {
         const int rt = min(m0 / 16 + rb, RT - 1);
-        xfrag[rb] = a.xp + ((size_t)g * RT + rt) * (size_t)(a.in / 32) * 512 + (size_t)lane * 8;
+        xfrag[rb] = xfrag0 + (size_t)rt * (size_t)(in / 32) * 512 + (size_t)lane * 8;
     }
     f4_t acc[4][4];
 #pragma unroll
@@ -392,11 +385,8 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
     }
 
     // ---- epilogue (the decode waves have left, so the barriers below join the 8 MFMA waves): per 16-row block, the
-    // two waves of a row group stage their column halves side by side in LDS, then each finishes 8 of the rows
-    // (FWHT-128 + svh).
+    // two waves of a row group stage their column halves side by side in LDS, then each hands 8 of the rows on.
     float *ep = reinterpret_cast<float *>(&Bs[0][0]) + (wave >> 1) * 16 * G2_EP;
-    const size_t sv = (size_t)g * a.out + (size_t)og * 128;
-    const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
 #pragma unroll
     for (int rb = 0; rb < 4; rb++) {
 #pragma unroll
@@ -406,23 +396,209 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
         __syncthreads();
         for (int r = (wave & 1) * 8; r < (wave & 1) * 8 + 8; r++) {
             const int m = m0 + rb * 16 + r;
-            if (m >= a.rows) break;
-            float v0 = ep[r * G2_EP + lane], v1 = ep[r * G2_EP + lane + 64];
-            fwht128_wave(v0, v1, lane);
-            const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128;
-            const float y0 = v0 * HAD_SCALE * s0, y1 = v1 * HAD_SCALE * s1;
-            if (a.y_dtype == DT_F16) {
-                store_act<DT_F16>(a.y, yo + lane, y0);
-                store_act<DT_F16>(a.y, yo + lane + 64, y1);
-            } else if (a.y_dtype == DT_BF16) {
-                store_act<DT_BF16>(a.y, yo + lane, y0);
-                store_act<DT_BF16>(a.y, yo + lane + 64, y1);
-            } else {
-                store_act<DT_F32>(a.y, yo + lane, y0);
-                store_act<DT_F32>(a.y, yo + lane + 64, y1);
-            }
+            if (m >= rows) break;
+            emit(m, ep[r * G2_EP + lane], ep[r * G2_EP + lane + 64], lane);
         }
         __syncthreads();
+    }
+}
+
+template <int FAM, int N>
+__global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
+    const int IT = a.in >> 4, OT = a.out >> 4;
+    const int nog = a.out / 128, nm = (a.rows + G2_MT - 1) / G2_MT;
+    const int L = blockIdx.x;
+    int og, mt;
+    if (nm <= 8 && 8 % nm == 0 && nog % (8 / nm) == 0) {
+        const int xcd = L & 7, per = 8 / nm;
+        mt = xcd / per;
+        og = (L >> 3) * per + xcd % per;
+    } else {
+        og = L % nog;
+        mt = L / nog;
+    }
+    const int g = blockIdx.z;
+    __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
+    const int RT = (a.rows + 15) / 16;
+    const uint16_t *xfrag0 = a.xp + ((size_t)g * RT + (size_t)mt * (G2_MT / 16)) * (size_t)(a.in / 32) * 512;
+    const size_t sv = (size_t)g * a.out + (size_t)og * 128;
+    const int lane = threadIdx.x & 63;
+    const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
+    gemm4_tile<FAM, N>(a.in, a.out, og, a.trellis + (size_t)g * IT * OT * N, xfrag0, min(G2_MT, a.rows - mt * G2_MT),
+                       a.k, Bs, [&](int m, float v0, float v1, int ln) __attribute__((always_inline)) {
+                           fwht128_wave(v0, v1, ln);
+                           const size_t yo = ((size_t)g * a.rows + mt * G2_MT + m) * a.out + (size_t)og * 128;
+                           const float y0 = v0 * HAD_SCALE * s0, y1 = v1 * HAD_SCALE * s1;
+                           if (a.y_dtype == DT_F16) {
+                               store_act<DT_F16>(a.y, yo + ln, y0);
+                               store_act<DT_F16>(a.y, yo + ln + 64, y1);
+                           } else if (a.y_dtype == DT_BF16) {
+                               store_act<DT_BF16>(a.y, yo + ln, y0);
+                               store_act<DT_BF16>(a.y, yo + ln + 64, y1);
+                           } else {
+                               store_act<DT_F32>(a.y, yo + ln, y0);
+                               store_act<DT_F32>(a.y, yo + ln + 64, y1);
+                           }
+                       });
+}
+
+// ---- the routed GEMM arm: workgroup (og, window w, projection p) runs the tile of window w's rows against its
+// expert's bank and writes the raw inner products to planes[p][slot][out] (the mid / the reduce applies the output
+// transform).  Windows past the count exit before any barrier.
+template <int FAM, int N>
+__global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
+    const int og = blockIdx.x, w = blockIdx.y, p = blockIdx.z;
+    if ((uint32_t)w >= *a.win.win_count) return;
+    const int IT = a.in >> 4, OT = a.out >> 4;
+    const int e = (int)min(a.win.win_expert[w], (uint32_t)(a.experts - 1));
+    const int rows = (int)min(a.win.win_rows[w], (uint32_t)G2_MT);
+    const uint32_t *slots = a.win.sorted + a.win.win_start[w];
+    __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
+    const uint16_t *xfrag0 = a.xp[p] + (size_t)a.win.win_tile0[w] * (size_t)(a.in / 32) * 512;
+    float *planes = a.planes[p];
+    gemm4_tile<FAM, N>(a.in, a.out, og, a.trellis[p] + (size_t)e * IT * OT * N, xfrag0, rows, a.k, Bs,
+                       [&](int m, float v0, float v1, int ln) __attribute__((always_inline)) {
+                           float *row = planes + (size_t)slots[m] * a.out + (size_t)og * 128;
+                           row[ln] = v0;
+                           row[ln + 64] = v1;
+                       });
+}
+
+// ---- the routed GEMM arm's inputs.  Tile t (16 sorted rows of one window, the window's tiles contiguous from
+// win_tile0) is prepared into fragment order at xp + t * (in / 32) * 512, as gemm_prepare_frag_kernel does for dense
+// rows; rows past the window's end are zeros.  Tiles past the count exit at once.
+struct TileRows {
+    bool live;
+    int rows;             // live rows of the tile (16 unless the window's last)
+    int e;                // the window's expert
+    const uint32_t *slots;
+};
+
+__device__ __forceinline__ TileRows tile_rows(const MoeGemmArgs &a, int t) {
+    TileRows r;
+    r.live = (uint32_t)t < *a.win.tile_count;
+    if (!r.live) return r;
+    const uint32_t w = a.win.tile_window[t];
+    const int i = t - (int)a.win.win_tile0[w];
+    r.rows = min(16, (int)a.win.win_rows[w] - 16 * i);
+    r.e = (int)min(a.win.win_expert[w], (uint32_t)(a.experts - 1));
+    r.slots = a.win.sorted + a.win.win_start[w] + 16 * i;
+    return r;
+}
+
+// The 16 x 128 f16 tile in LDS to fragment order (one 16-byte store per thread).
+__device__ __forceinline__ void tile_to_frag(const uint16_t (*tl)[128 + 8], uint16_t *xp, int t, int b, int in,
+                                             int tid) {
+    const int lane = tid & 63, kq = tid >> 6, c = lane & 15, h = lane >> 4;
+    const uint4 v = *reinterpret_cast<const uint4 *>(&tl[c][kq * 32 + 8 * h]);
+    *reinterpret_cast<uint4 *>(xp + ((size_t)t * (in / 32) + (size_t)b * 4 + kq) * 512 + (size_t)lane * 8) = v;
+}
+
+// prepareInput (expert_exl3.zig:490-501) of each row's token with its expert's suh, projection p = blockIdx.z.
+__global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a) {
+    const int b = blockIdx.x, t = blockIdx.y, p = blockIdx.z;
+    const TileRows tr = tile_rows(a, t);
+    if (!tr.live) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint16_t tl[16][128 + 8];
+    const size_t si = (size_t)tr.e * a.in + (size_t)b * 128;
+    const float u0 = h2f(a.suh[p][si + lane]), u1 = h2f(a.suh[p][si + lane + 64]);
+    for (int rr = 0; rr < 4; rr++) {
+        const int r = wave * 4 + rr;
+        float v0 = 0.f, v1 = 0.f;
+        if (r < tr.rows) {
+            const size_t xi = (size_t)(tr.slots[r] / (uint32_t)a.topk) * a.in + (size_t)b * 128;
+            v0 = f16r(load_any(a.x, a.x_dtype, xi + lane)) * u0;
+            v1 = f16r(load_any(a.x, a.x_dtype, xi + lane + 64)) * u1;
+            fwht128_wave(v0, v1, lane);
+            v0 *= HAD_SCALE;
+            v1 *= HAD_SCALE;
+        }
+        tl[r][lane] = __half_as_ushort(__float2half_rn(v0));
+        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1));
+    }
+    __syncthreads();
+    tile_to_frag(tl, a.xp[p], t, b, a.in, tid);
+}
+
+// The SwiGLU mid of the routed GEMM arm (DOWN_FUSED_SOURCE's prologue, expert_exl3_kernels.zig:1838-1925; the
+// decode chain's PRO_MID with one plane): gate and up = svh * H(raw inner), the clamps, SiLU(gate) * up * suh_down,
+// H, f16 -- the down projection's prepared input, in fragment order at xp[0] (a.in = inter).
+__global__ __launch_bounds__(256) void moe_gemm_mid_kernel(MoeGemmArgs a) {
+    const int b = blockIdx.x, t = blockIdx.y;
+    const TileRows tr = tile_rows(a, t);
+    if (!tr.live) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint16_t tl[16][128 + 8];
+    const size_t si = (size_t)tr.e * a.in + (size_t)b * 128;
+    const float sg0 = h2f(a.mid_svh[0][si + lane]), sg1 = h2f(a.mid_svh[0][si + lane + 64]);
+    const float su0 = h2f(a.mid_svh[1][si + lane]), su1 = h2f(a.mid_svh[1][si + lane + 64]);
+    const float sd0 = h2f(a.down_suh[si + lane]), sd1 = h2f(a.down_suh[si + lane + 64]);
+    for (int rr = 0; rr < 4; rr++) {
+        const int r = wave * 4 + rr;
+        float v0 = 0.f, v1 = 0.f;
+        if (r < tr.rows) {
+            const size_t pi = (size_t)tr.slots[r] * a.in + (size_t)b * 128;
+            float g0 = a.mid_planes[0][pi + lane], g1 = a.mid_planes[0][pi + lane + 64];
+            float q0 = a.mid_planes[1][pi + lane], q1 = a.mid_planes[1][pi + lane + 64];
+            fwht128_wave(g0, g1, lane);
+            fwht128_wave(q0, q1, lane);
+            g0 *= HAD_SCALE * sg0;
+            g1 *= HAD_SCALE * sg1;
+            q0 *= HAD_SCALE * su0;
+            q1 *= HAD_SCALE * su1;
+            if (a.clamp_limit > 0.f) {
+                g0 = fminf(g0, a.clamp_limit);
+                g1 = fminf(g1, a.clamp_limit);
+                q0 = fminf(fmaxf(q0, -a.clamp_limit), a.clamp_limit);
+                q1 = fminf(fmaxf(q1, -a.clamp_limit), a.clamp_limit);
+            }
+            v0 = silu(g0) * q0 * sd0;
+            v1 = silu(g1) * q1 * sd1;
+            fwht128_wave(v0, v1, lane);
+            v0 *= HAD_SCALE;
+            v1 *= HAD_SCALE;
+        }
+        tl[r][lane] = __half_as_ushort(__float2half_rn(v0));
+        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1));
+    }
+    __syncthreads();
+    tile_to_frag(tl, a.xp[0], t, b, a.in, tid);
+}
+
+hipError_t run_moe_gemm_prepare(const MoeGemmArgs &a, int nproj, hipStream_t s) {
+    hipLaunchKernelGGL(moe_gemm_prepare_kernel, dim3((unsigned)(a.in / 128), (unsigned)a.max_tiles, (unsigned)nproj),
+                       dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t run_moe_gemm_mid(const MoeGemmArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(moe_gemm_mid_kernel, dim3((unsigned)(a.in / 128), (unsigned)a.max_tiles), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int FAM>
+static hipError_t launch_moe_gemm_fam(const MoeGemmArgs &a, int nproj, hipStream_t s) {
+    const dim3 grid((unsigned)(a.out / 128), (unsigned)a.max_windows, (unsigned)nproj);
+    switch (a.n) {
+    case 16: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 16>), grid, dim3(G4_THREADS), 0, s, a); break;
+    case 24: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 24>), grid, dim3(G4_THREADS), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 32>), grid, dim3(G4_THREADS), 0, s, a); break;
+    case 40: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 40>), grid, dim3(G4_THREADS), 0, s, a); break;
+    case 48: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 48>), grid, dim3(G4_THREADS), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 64>), grid, dim3(G4_THREADS), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t run_moe_gemm(int fam, const MoeGemmArgs &a, int nproj, hipStream_t s) {
+    switch (fam) {
+    case FAM_MCG: return launch_moe_gemm_fam<FAM_MCG>(a, nproj, s);
+    case FAM_MUL1: return launch_moe_gemm_fam<FAM_MUL1>(a, nproj, s);
+    case FAM_HASH: return launch_moe_gemm_fam<FAM_HASH>(a, nproj, s);
+    case FAM_PAIR: return launch_moe_gemm_fam<FAM_PAIR>(a, nproj, s);
+    default: return launch_moe_gemm_fam<FAM_3INST>(a, nproj, s);
     }
 }
 

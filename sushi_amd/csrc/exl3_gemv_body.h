@@ -84,13 +84,6 @@ __device__ __forceinline__ float y_from_bits16(int dt, uint32_t b) {
     return __uint_as_float(b << 16);
 }
 
-__device__ __forceinline__ float silu(float g) {
-    // g * sigmoid(g), evaluated on exp(-|g|) so neither branch overflows (the reference's mid uses the same split)
-    const float e = __expf(-fabsf(g));
-    const float s = g >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
-    return g * s;
-}
-
 struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div, x_dtype;
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)

@@ -156,6 +156,52 @@ constexpr int kMoeWindowMaxExperts = 4096;
 hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32_t *win_count, uint32_t *win_expert,
                            uint32_t *win_rows, uint32_t *win_slots, hipStream_t s);
 
+// The routed GEMM arm's expert windows (moe_gemm_windows_kernel): slots sorted by expert, windows of up to
+// MOE_GEMM_WINDOW_ROWS rows of one expert, and the 16-row fragment tiles of their prepared inputs.
+constexpr int MOE_GEMM_WINDOW_ROWS = 256;
+constexpr int kMoeGemmMaxExperts = 1024;
+struct MoeGemmWindows {
+    uint32_t *win_count;    // [1] windows
+    uint32_t *tile_count;   // [1] 16-row tiles over all windows
+    uint32_t *sorted;       // [slots] slot ids by expert, ascending within an expert
+    uint32_t *win_expert;   // [windows]
+    uint32_t *win_rows;     // [windows] rows (<= MOE_GEMM_WINDOW_ROWS)
+    uint32_t *win_start;    // [windows] first sorted position
+    uint32_t *win_tile0;    // [windows] first fragment tile
+    uint32_t *tile_window;  // [tiles] the window of each tile
+};
+hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, const MoeGemmWindows &t,
+                                hipStream_t s);
+
+// The routed GEMM arm (a prefill-width layer: every expert's rows in windows of up to 256, each weight decoded once
+// per window on the matrix cores).  Projection p of grid z: x prepared per window row with that expert's suh into
+// xp[p] (fragment order, tile t at xp + t * (in / 32) * 512), the raw inner products written to planes[p]
+// [slot][out] (f32, no output transform: the mid / the reduce applies it).
+struct MoeGemmArgs {
+    MoeGemmWindows win;
+    const void *x;          // [tokens][hidden] (gate/up) -- the token of slot s is s / topk
+    int x_dtype;
+    int topk;
+    int in, out;
+    int experts;
+    const uint16_t *trellis[2];
+    const uint16_t *suh[2];
+    int n;
+    DecodeK k;
+    uint16_t *xp[2];        // prepared inputs, fragment order
+    float *planes[2];       // raw inner [slots][out]
+    // the mid (down input): gate / up planes [slots][inter] -> xp_down, with the gate / up svh and the down suh
+    const float *mid_planes[2];
+    const uint16_t *mid_svh[2];
+    const uint16_t *down_suh;
+    float clamp_limit;
+    int max_tiles;          // grid bound: tiles over all windows
+    int max_windows;        // grid bound: windows
+};
+hipError_t run_moe_gemm_prepare(const MoeGemmArgs &a, int nproj, hipStream_t s);
+hipError_t run_moe_gemm_mid(const MoeGemmArgs &a, hipStream_t s);
+hipError_t run_moe_gemm(int fam, const MoeGemmArgs &a, int nproj, hipStream_t s);
+
 // Dense GEMM arm (prefill, rows > 8): prepare x -> xp f16, decode tiles to MFMA fragments, finish in the epilogue.
 struct GemmArgs {
     const void *x;

@@ -197,6 +197,102 @@ hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32
     return hipGetLastError();
 }
 
+// Expert windows for the routed GEMM arm (the sort and window table of moePrefill, expert_exl3_kernels.zig:
+// 2861-2931 with sorted_windows.zig:10-165), in compact form: the slots sorted by expert (stable: ascending slot within
+// an expert) into `sorted`, expert e's run starting at sbase[e] = the exclusive scan of the per-expert counts; each
+// run cut into windows of up to MOE_GEMM_WINDOW_ROWS rows (window i of expert e is wbase[e] + i, starting at sorted
+// position sbase[e] + i * W); and the 16-row fragment tiles of the prepared inputs numbered so that expert e's rows
+// occupy tiles tbase[e] .. tbase[e] + ceil(count / 16) - 1 (a window's tiles are contiguous, from win_tile0).
+// tile_window[t] names the window of tile t.  Ranks come from one wave walking the slots in order, as in
+// moe_windows_kernel.
+__global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
+                                                                       int experts, MoeGemmWindows t) {
+    __shared__ uint32_t cnt[kMoeGemmMaxExperts];
+    __shared__ uint32_t fill[kMoeGemmMaxExperts];
+    __shared__ uint32_t sb[kMoeGemmMaxExperts];
+    __shared__ uint32_t tb[kMoeGemmMaxExperts];
+    __shared__ uint32_t wb[kMoeGemmMaxExperts];
+    __shared__ uint32_t part[3][WIN_THREADS];
+    constexpr uint32_t W = MOE_GEMM_WINDOW_ROWS;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < experts; e += WIN_THREADS) cnt[e] = fill[e] = 0;
+    __syncthreads();
+    for (int s = tid; s < nslots; s += WIN_THREADS) atomicAdd(&cnt[min(inds[s], (uint32_t)(experts - 1))], 1u);
+    __syncthreads();
+    // three exclusive scans over experts (slots, 16-row tiles, windows): each thread sums a contiguous run
+    const int per = (experts + WIN_THREADS - 1) / WIN_THREADS;
+    const int e0 = min(tid * per, experts), e1 = min(e0 + per, experts);
+    uint32_t ls = 0, lt = 0, lw = 0;
+    for (int e = e0; e < e1; e++) {
+        ls += cnt[e];
+        lt += (cnt[e] + 15) / 16;
+        lw += (cnt[e] + W - 1) / W;
+    }
+    part[0][tid] = ls;
+    part[1][tid] = lt;
+    part[2][tid] = lw;
+    __syncthreads();
+    for (int off = 1; off < WIN_THREADS; off <<= 1) {
+        uint32_t v[3];
+        for (int q = 0; q < 3; q++) v[q] = tid >= off ? part[q][tid - off] : 0u;
+        __syncthreads();
+        for (int q = 0; q < 3; q++) part[q][tid] += v[q];
+        __syncthreads();
+    }
+    uint32_t rs = part[0][tid] - ls, rt = part[1][tid] - lt, rw = part[2][tid] - lw;
+    for (int e = e0; e < e1; e++) {
+        sb[e] = rs;
+        tb[e] = rt;
+        wb[e] = rw;
+        rs += cnt[e];
+        rt += (cnt[e] + 15) / 16;
+        rw += (cnt[e] + W - 1) / W;
+    }
+    if (tid == WIN_THREADS - 1) {
+        *t.win_count = part[2][tid];
+        *t.tile_count = part[1][tid];
+    }
+    __syncthreads();
+    if (tid < 64) {  // wave 0 ranks the slots in order
+        const int lane = tid;
+        const int id_bits = experts > 1 ? 32 - __clz(experts - 1) : 0;
+        for (int base = 0; base < nslots; base += 64) {
+            const int s = base + lane;
+            const bool live = s < nslots;
+            const int e = live ? (int)min(inds[s], (uint32_t)(experts - 1)) : 0;
+            unsigned long long same = __ballot(live);
+            for (int b = 0; b < id_bits; b++) {
+                const unsigned long long set = __ballot((e >> b) & 1);
+                same &= ((e >> b) & 1) ? set : ~set;
+            }
+            const unsigned long long below = (1ull << lane) - 1ull;
+            const uint32_t before = (uint32_t)__popcll(same & below);
+            const bool last = live && (same & ~below & ~(1ull << lane)) == 0ull;
+            if (live) {
+                const uint32_t rank = fill[e] + before;
+                t.sorted[sb[e] + rank] = (uint32_t)s;
+                if (rank % W == 0) {  // the first slot of a window writes its row
+                    const uint32_t w = wb[e] + rank / W, rows = min(cnt[e] - rank, W);
+                    const uint32_t tile0 = tb[e] + rank / 16;
+                    t.win_expert[w] = (uint32_t)e;
+                    t.win_rows[w] = rows;
+                    t.win_start[w] = sb[e] + rank;
+                    t.win_tile0[w] = tile0;
+                    for (uint32_t i = 0; i < (rows + 15) / 16; i++) t.tile_window[tile0 + i] = w;
+                }
+                if (last) fill[e] = rank + 1;
+            }
+        }
+    }
+}
+
+hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, const MoeGemmWindows &t,
+                                hipStream_t s) {
+    if (nslots <= 0 || experts <= 0 || experts > kMoeGemmMaxExperts) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_gemm_windows_kernel, dim3(1), dim3(WIN_THREADS), 0, s, inds, nslots, experts, t);
+    return hipGetLastError();
+}
+
 // One workgroup (256 threads) per row: k rounds of a block-wide argmax (ties to the lower index), then the softmax
 // mass of the picks over the full row, renormalised.  Selection keys are the logits with NaN read as -inf, and a
 // per-row mask keeps each expert from being picked twice: every round starts from the lowest unpicked index as its

@@ -96,3 +96,22 @@ def test_c5_rate_group_layer_batch_64(dev):
                                np.ones((batch, 1)), hidden, inter, (64, 64, 64), odec, threads=THREADS)
     want = routed.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
     assert max_abs_rel(y, want) < BAR
+
+
+def test_c4_prefill_width_takes_the_gemm_arm(dev, c4):
+    """configs[3]'s layer at a 512-token prefill (4096 slots, 16 per expert on average): the routed GEMM arm (taken
+    by itself at this width) against the oracle, and equal to the decode chain at the bar."""
+    print("[c4] prefill 512", flush=True)
+    b, sh, bd, shd, banks = c4
+    E, hidden, inter, k, batch = 256, 2048, 768, 8, 512
+    x = synth.normal(3, "c4.p512", (batch, hidden))
+    logits = synth.normal(3, "c4.pl512", (batch, E), dtype=torch.float32)
+    inds, scores = exl3.moe_routing_chain(logits.to(dev), k)
+    oi, osc = O.route_topk(logits.numpy(), k)
+    y = exl3.moe(x.to(dev), bd, inds, scores, exl3.MCG).float().cpu().numpy()
+    with exl3.arm_overrides(moe_gemm=0):
+        y_chain = exl3.moe(x.to(dev), bd, inds, scores, exl3.MCG).float().cpu().numpy()
+    routed = O.moe_swiglu_rows(x.float().numpy(), *banks, oi, osc, hidden, inter, (32, 32, 32), O.decode(O.CB_MCG),
+                               threads=THREADS)
+    assert max_abs_rel(y, routed) < BAR
+    assert max_abs_rel(y, y_chain) < BAR

@@ -533,3 +533,61 @@ def test_moe_mixed_projection_rates(dev, rows, rates):
                                np.ones((rows, 1)), hidden, inter, (32, 32, 32), odec, threads=8)
     want2 = want.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
     assert max_abs_rel(y2.float().cpu().numpy(), want2) < BAR
+
+
+@pytest.mark.parametrize("rows,E,k", [(1, 8, 2), (5, 16, 4), (40, 16, 4), (300, 32, 6)])
+@pytest.mark.parametrize("label,dec,odec", [
+    ("mcg", exl3.MCG, O.decode(O.CB_MCG)),
+    ("3inst", exl3.INST3, O.decode(O.CB_3INST)),
+    ("spec1", exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1), O.decode(O.CB_SPEC1, 15, 1)),
+    ("pair1", exl3.Decode(exl3.Codebook.pair1), O.decode(O.CB_PAIR1)),
+])
+def test_moe_gemm_arm_against_oracle(dev, rows, E, k, label, dec, odec):
+    """The routed GEMM arm (moePrefill's sorted windows on the matrix cores, expert_exl3_kernels.zig:2861-2931),
+    forced at every width: windows of up to 256 rows per expert, prepared inputs in fragment order, the decode-once
+    GEMM for gate/up, the mid, the down GEMM and the reduce, against the oracle to the bar."""
+    print(f"[moe gemm] {label} rows={rows} E={E} k={k}", flush=True)
+    hidden, inter, n = 256, 384, 48
+    b = synth.bank(41, f"mg.{label}", E, hidden, inter, n, norm=True)
+    x = synth.normal(41, f"x{rows}", (rows, hidden))
+    inds, scores = _route(41 + rows, rows, E, k)
+    want = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, scores, hidden, inter,
+                             (n, n, n), odec, threads=8)
+    with exl3.arm_overrides(moe_gemm=1):
+        y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                     torch.from_numpy(scores).to(dev), dec)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_moe_gemm_arm_long_windows_clamp_and_shared(dev):
+    """One expert takes 450 slots (windows of 256 + 194 rows), clamped SwiGLU, a shared expert added after the
+    routed rounding, then the same with a gate; and the arm equals the decode chain to the bar."""
+    E, hidden, inter, k, rows, n = 4, 256, 256, 2, 300, 32
+    b = synth.bank(43, "mgl", E, hidden, inter, n, norm=True)
+    x = synth.normal(43, "x", (rows, hidden))
+    inds = np.zeros((rows, k), np.uint32)
+    inds[:, 1] = np.arange(rows) % 3 + 1          # expert 0 gets every row's first slot: 300 rows
+    inds[:150, 1] = 0                             # ... and 150 more (450 in all -- its second slot repeats it)
+    sc = np.full((rows, k), 0.5, np.float32)
+    xi, scd = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(sc).to(dev)
+    odec = O.decode(O.CB_MCG)
+    want = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, sc, hidden, inter,
+                             (n, n, n), odec, clamp_limit=7.0, threads=8)
+    sh = synth.normal(44, "sh", (rows, hidden))
+    gate = synth.normal(45, "g", (rows, 1))
+    bd = _to(b, dev)
+    with exl3.arm_overrides(moe_gemm=1):
+        y = exl3.moe_clamped(x.to(dev), bd, xi, scd, exl3.MCG, 7)
+        y_sh = exl3.moe_clamped(x.to(dev), bd, xi, scd, exl3.MCG, 7, shared=sh.to(dev))
+        y_g = exl3.moe_with_gated_shared(x.to(dev), bd, xi, scd, exl3.MCG, False, sh.to(dev), gate.to(dev))
+    with exl3.arm_overrides(moe_gemm=0):
+        y_chain = exl3.moe_clamped(x.to(dev), bd, xi, scd, exl3.MCG, 7)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+    assert max_abs_rel(y.float().cpu().numpy(), y_chain.float().cpu().numpy()) < BAR
+    want_sh = want.astype(np.float16).astype(np.float32) + sh.float().numpy()
+    assert max_abs_rel(y_sh.float().cpu().numpy(), want_sh) < BAR
+    want_g = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, sc, hidden, inter,
+                               (n, n, n), odec, threads=8)
+    term = O.gated_shared_terms(gate.float().numpy()[:, 0], sh.float().numpy(), 0)
+    want_g = (want_g.astype(np.float16).astype(np.float32) + term).astype(np.float16).astype(np.float32)
+    assert max_abs_rel(y_g.float().cpu().numpy(), want_g) < BAR

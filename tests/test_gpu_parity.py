@@ -184,7 +184,7 @@ def _moe_truth(bank, x, experts_of_row, odecs, clamp=0.0):
     inner = np.stack([p @ w for p, w in zip(rows_p, rows_w)])
     amag = np.stack([np.abs(p) @ np.abs(w) for p, w in zip(rows_p, rows_w)])
     bound = np.stack([np.abs(p).max() * np.abs(w).max(axis=0) for p, w in zip(rows_p, rows_w)])
-    return P.Truth(inner, amag, bound, inter)
+    return P.Truth(inner, amag, bound, inter, P.MID_ULPS)
 
 
 def _moe_inner(y, bank, experts_of_row, score_sum):
@@ -266,3 +266,26 @@ def test_moe_ragged_spec1_k1_k2(dev, rows):
         got = P.inner_from_output(y[r:r + 1], _u16(grp.down.svh)[local])
         t = _moe_truth(grp, xf[r:r + 1], [local], (odec, odec, odec))
         assert P.verdict(got, t) is None, (r, e, P.verdict(got, t))
+
+
+@pytest.mark.parametrize("rows,topk", [(40, 4), (300, 1)])
+def test_moe_gemm_arm(dev, rows, topk):
+    """The routed GEMM arm on the summand-relative bar, with the mutation arms (every slot of a row on one expert)."""
+    b, bd, x, experts, inds, sc, ssum = _moe_case(dev, 80 + rows, rows, topk, E=8, hidden=512, inter=256)
+    odec = O.decode(O.CB_MCG)
+    with exl3.arm_overrides(moe_gemm=1):
+        y = exl3.moe(x.to(dev).float(), bd, inds, sc, exl3.MCG)
+    torch.cuda.synchronize()
+    got = _moe_inner(y.cpu().numpy().astype(np.float64), b, experts, ssum)
+    xf = x.float().numpy()
+    t = _moe_truth(b, xf, experts, (odec, odec, odec))
+    print(f"[parity] moe gemm rows={rows} worst error / ceiling = {P.worst_ratio(got, t):.4f}", flush=True)
+    assert P.verdict(got, t) is None, P.verdict(got, t)
+    w15 = P.mutated_window(odec)
+    assert P.verdict(got, _moe_truth(b, xf, experts, (w15, w15, w15))) is not None
+    e0 = int(experts[0])
+    q = b.down
+    tr = _u16(q.trellis).copy()
+    tr[e0], where = P.flip_one_bit(tr[e0], q.n, odec, np.ones((1, q.in_features)), np.random.default_rng(rows))
+    mb = exl3.Bank(b.gate, b.up, exl3.Proj(torch.from_numpy(tr.view(np.int16)), q.suh, q.svh))
+    assert P.verdict(got, _moe_truth(mb, xf, experts, (odec, odec, odec))) is not None, where
