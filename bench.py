@@ -445,6 +445,8 @@ def sweep(which: str):
             cases.append(("c3", 4096, 14336, 48, rows, exl3.INST3, "3inst"))
     if which in ("c5", "all"):
         print(json.dumps(bench_moe_c5()), flush=True)
+        for line in bench_moe_c5_tiled():
+            print(json.dumps(line), flush=True)
     if which in ("moe_prefill", "all"):
         bench_moe_prefill()
     if which in ("pack", "all"):
@@ -476,58 +478,136 @@ def sweep(which: str):
         print(json.dumps(line), flush=True)
 
 
-def bench_moe_c5(batch: int = 64, layers: int = 4, replays: int = 4):
-    """configs[4] in the reference-expressible form: the per-expert rate groups of rate_groups.zig (64 experts at
-    K=1, 192 at K=2: 1.75 bpw on average) as one ragged bank, hidden 4096, inter 2048, SPEC1 (spec1-w15 table: the one with K=1 rows),
-    top-8 over N(0,1) logits, batch 64, plus a K=4 shared expert.  A dependent chain of `layers` layers."""
+def _graph_layer_us(chain, dev, layers: int, rounds: int = ROUNDS) -> float:
+    """Median over `rounds` graph replays of `chain` (captured once), per layer."""
+    import statistics
+
+    import torch
+
+    chain()
+    torch.cuda.synchronize()
+    g = _capture(chain, dev)
+    stream = torch.cuda.current_stream(dev)
+    times = []
+    for _ in range(rounds):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / layers)
+    return statistics.median(times)
+
+
+def _c5_inputs(E: int, batch: int, layers: int, dev):
+    """configs[4]'s per-layer inputs: each layer its own N(0,1) hidden state and top-8 routing over N(0,1) logits."""
     import torch
 
     from sushi_amd import exl3, synth
 
+    xs = [synth.normal(5, f"c5.x{batch}.{layer}", (batch, 4096), device=dev) for layer in range(layers)]
+    routes = []
+    for layer in range(layers):
+        logits = synth.normal(5, f"c5.logits{batch}.{layer}", (batch, E), dtype=torch.float32).to(dev)
+        routes.append(exl3.moe_routing_chain(logits, 8))
+    return xs, routes
+
+
+def _c5_line(variant: str, batch: int, E: int, bpw: float, layer_us: float, alg: float, **extra):
+    line = {"config": "c5", "variant": variant, "batch": batch, "experts": E, "bpw": round(bpw, 4),
+            "layer_us": round(layer_us, 3), "us_per_token": round(layer_us / batch, 3), "bytes_per_layer": int(alg),
+            "effective_GBps": round(alg / (layer_us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(alg / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    line.update(extra)
+    return line
+
+
+def bench_moe_c5(batch: int = 64, layers: int = 4):
+    """configs[4] in the reference-expressible form: the per-expert rate groups of rate_groups.zig (64 experts at
+    K=1, 192 at K=2: 1.75 bpw on average) as one ragged bank, hidden 4096, inter 2048, SPEC1 (spec1-w15 table: the
+    one with K=1 rows), top-8 over N(0,1) logits, batch 64, plus a K=4 shared expert run as a one-expert chain whose
+    output the routed call adds.  `layers` layers, each with its own input and routing, captured once; median of
+    ROUNDS replays.  Bytes: the distinct experts' packed tiles and scales plus the shared expert's."""
+    from sushi_amd import exl3, synth
+
+    import torch
+
     dev = torch.device("cuda:0")
-    E1, E2, hidden, inter, k = 64, 192, 4096, 2048, 8
+    E1, E2, hidden, inter = 64, 192, 4096, 2048
     dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
     g1 = synth.bank(5, "c5.k1", E1, hidden, inter, 16, device=dev, norm=True)
     g2 = synth.bank(5, "c5.k2", E2, hidden, inter, 32, device=dev, norm=True)
     rb = exl3.Ragged.init([g1, g2])
     del g1, g2
     shared = synth.bank(5, "c5.shared", 1, hidden, inter, 64, device=dev, norm=True)
-    x0 = synth.normal(5, f"c5.x{batch}", (batch, hidden), device=dev)
-    routes = []
-    for layer in range(layers):
-        logits = synth.normal(5, f"c5.logits{batch}.{layer}", (batch, E1 + E2), dtype=torch.float32).to(dev)
-        routes.append(exl3.moe_routing_chain(logits, k))
+    xs, routes = _c5_inputs(E1 + E2, batch, layers, dev)
     sh_inds = torch.zeros(batch, 1, dtype=torch.int32, device=dev)
     sh_sc = torch.ones(batch, 1, dtype=torch.float32, device=dev)
 
     def chain():
-        x = x0
-        for inds, scores in routes:
+        out = []
+        for x, (inds, scores) in zip(xs, routes):
             s = exl3.moe(x, shared, sh_inds, sh_sc, dec)
-            x = exl3.moe_ragged(x, rb, inds, scores, dec, shared=s)
-        return x
+            out.append(exl3.moe_ragged(x, rb, inds, scores, dec, shared=s))
+        return out
 
-    chain()
-    torch.cuda.synchronize()
-    g = _capture(chain, dev)
-    stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(replays):
-        g.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    layer_us = e0.elapsed_time(e1) * 1e3 / (replays * layers)
-    tiles = (hidden // 16) * (inter // 16)
-    bytes_k = {16: 3 * tiles * 16 * 2, 32: 3 * tiles * 32 * 2}
-    distinct = []
-    for inds, _ in routes:
-        ids = set(inds.flatten().tolist())
-        distinct.append(sum(bytes_k[16] if e < E1 else bytes_k[32] for e in ids) + 6 * len(ids) * (hidden + inter))
-    alg = sum(distinct) / layers + 3 * (hidden * inter * 64 // 8 + 2 * (hidden + inter))
-    return {"config": "c5", "batch": batch, "experts": E1 + E2, "bpw": 1.75, "layer_us": round(layer_us, 3),
-            "us_per_token": round(layer_us / batch, 3), "effective_GBps": round(alg / (layer_us * 1e-6) / 1e9, 1),
-            "hbm_frac": round(alg / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    layer_us = _graph_layer_us(chain, dev, layers)
+    # packed tiles + suh + svh of the three projections (down's in + out is gate's out + in)
+    per_expert = {n: 3 * _algorithmic_bytes(hidden, inter, n, 0) for n in (16, 32)}
+    distinct = [sum(per_expert[16] if e < E1 else per_expert[32] for e in set(inds.flatten().tolist()))
+                for inds, _ in routes]
+    alg = sum(distinct) / layers + 3 * _algorithmic_bytes(hidden, inter, 64, 0)
+    return _c5_line("rate_groups", batch, E1 + E2, 1.75, layer_us, alg)
+
+
+def bench_moe_c5_tiled(batch: int = 64, layers: int = 4):
+    """configs[4] as stated: every expert's tiles at a seeded per-tile mix of K=1 and K=2 (25% K1; the realised rate is
+    reported), 256 experts, hidden 4096, inter 2048, SPEC1 (spec1-w15), top-8 over N(0,1) logits, batch 64, plus a
+    K=4 shared expert -- in the same launches (moe_tiled_with_shared_bank, "tiled_fused") and as the pair of calls
+    (one-expert chain, then moe_tiled with its output, "tiled_pair").  Bytes: the distinct experts' packed tiles,
+    segment tables and scales, plus the shared expert's."""
+    from sushi_amd import exl3, synth
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    E, hidden, inter = 256, 4096, 2048
+    dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
+    tb = synth.tiled_bank(5, "c5t", E, hidden, inter, 0.25, device=dev, norm=True)
+    shared = synth.bank(5, "c5.shared", 1, hidden, inter, 64, device=dev, norm=True)
+    xs, routes = _c5_inputs(E, batch, layers, dev)
+    sh_inds = torch.zeros(batch, 1, dtype=torch.int32, device=dev)
+    sh_sc = torch.ones(batch, 1, dtype=torch.float32, device=dev)
+    # bytes of each expert: tile words (8 per K1 tile, 16 per K2) + 5 table bytes per segment + scales
+    popc = torch.tensor([bin(v).count("1") for v in range(256)], dtype=torch.int64, device=dev)
+    per_expert = torch.zeros(E, dtype=torch.int64, device=dev)
+    for p in (tb.gate, tb.up, tb.down):
+        segs = p.seg_k1.shape[1] * p.seg_k1.shape[2]
+        k1 = popc[p.seg_k1.long()].reshape(E, -1).sum(1)
+        per_expert += 4 * (128 * segs - 8 * k1) + 5 * segs + 2 * (p.in_features + p.out_features)
+    per_expert = per_expert.cpu().tolist()
+    words = sum(p.trellis.numel() for p in (tb.gate, tb.up, tb.down))
+    bpw = words * 16 / (3 * E * hidden * inter)
+    distinct = [sum(per_expert[e] for e in set(inds.flatten().tolist())) for inds, _ in routes]
+    alg = sum(distinct) / layers + 3 * _algorithmic_bytes(hidden, inter, 64, 0)
+
+    def fused():
+        return [exl3.moe_tiled_with_shared_bank(x, tb, shared, inds, scores, dec) for x, (inds, scores) in
+                zip(xs, routes)]
+
+    def pair():
+        out = []
+        for x, (inds, scores) in zip(xs, routes):
+            s = exl3.moe(x, shared, sh_inds, sh_sc, dec)
+            out.append(exl3.moe_tiled(x, tb, inds, scores, dec, shared=s))
+        return out
+
+    lines = []
+    for variant, fn in (("tiled_fused", fused), ("tiled_pair", pair)):
+        lines.append(_c5_line(variant, batch, E, bpw, _graph_layer_us(fn, dev, layers), alg,
+                              k1_fraction=0.25, distinct_experts=round(sum(len(set(i.flatten().tolist()))
+                                                                           for i, _ in routes) / layers, 1)))
+    return lines
 
 
 def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4):

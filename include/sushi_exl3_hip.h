@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 3
+#define EXL3_ABI_VERSION 4
 
 /* Codebook: the reference's `Codebook` enum values (src/exl3/expert_exl3.zig:54-61), plus 3INST as an
  * extension (QTIP's LCG codebook, not in the reference). */
@@ -116,6 +116,24 @@ typedef struct {
     int32_t lane_rates_only;
 } exl3_ragged_t;
 
+/* A per-tile-rate bank (configs[4]'s seeded K1 / K2 tile mix).  No counterpart in the reference, which fixes a rate
+ * per tensor (src/exl3/layout.zig:56-62) or per expert group (src/exl3/rate_groups.zig:22-140); each tile still
+ * decodes at its own n as decodeTile does (src/exl3/expert_exl3.zig:338-357), so this is a layout extension.  A
+ * segment is the 8 tiles (k-tile row tk, output tiles 8s .. 8s + 7) of one expert's projection: segment index
+ * (e * in/16 + tk) * out/128 + s lies contiguous from u32 word seg_off[index] of the projection's trellis, tiles in
+ * column order, tile o at n_a halfwords when bit o of seg_k1[index] is set, else at n_b.  n_a = 16, n_b = 32 (K1 and
+ * K2); codebooks MCG, 3INST and the SPEC1 / STD1 hash rows whose table has both rates (spec1-w15).  seg_k1 must be
+ * 4-byte aligned.  Word offsets are u32, so one projection's trellis spans at most 16 GiB. */
+typedef struct {
+    const uint16_t *trellis[3]; /* gate, up, down */
+    const uint32_t *seg_off[3]; /* device [experts][in/16][out/128] */
+    const uint8_t *seg_k1[3];   /* device, same shape */
+    const uint16_t *suh[3];     /* [experts][in] */
+    const uint16_t *svh[3];     /* [experts][out] */
+    int32_t experts;
+    int32_t n_a, n_b;
+} exl3_tiled_t;
+
 int32_t exl3_abi_version(void);
 const char *exl3_last_error(void);
 
@@ -182,10 +200,10 @@ int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_
                             const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh,
                             exl3_decode_t dec, void *y, int32_t y_dtype, hipStream_t stream);
 
-/* Clears a workspace once after allocation.  Every workspace begins with an 8 MiB region of fused-finish
- * arrival counters, accumulators and their overflow words that must start at zero; the calls that use them always leave them at zero
- * again, and no other call writes there, so one init per allocation suffices.  Calls that share a workspace must not overlap in time
- * (they would race on its scratch).  A small fill kernel, never hipMemsetAsync. */
+/* Clears a workspace once after allocation.  Every workspace begins with an 8 MiB region of fused-finish arrival
+ * counters, accumulators and their overflow words that must start at zero; the calls that use them always leave them
+ * at zero again, and no other call writes there, so one init per allocation suffices.  Calls that share a workspace
+ * must not overlap in time (they would race on its scratch).  A small fill kernel, never hipMemsetAsync. */
 int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Routed SwiGLU experts: `moe` (src/exl3/root.zig:51-53), `moeWithShared` (:56-67, `shared` [rows][hidden] in y's
@@ -229,9 +247,9 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
  * routed layer's inter; clamp_limit applies to both.  Up to 8 rows the shared rows join the per-slot launches;
  * wider batches the sorted (expert-window) launches, where the shared rows are windows of their own (three launches
  * in all instead of six).  Returns EXL3_DECLINED (nothing launched) where the fused form does not serve: y dtype f32,
- * routed projections at different rates, a shared rate other than the routed one (uniform banks), rows whose routed, shared and combine fold words (3 x rows
- * x hidden) exceed the fused finish's region, or more fold arrivals than it holds; the caller then makes the two
- * calls.  The _ragged form takes
+ * routed projections at different rates, a shared rate other than the routed one (uniform banks), rows whose
+ * routed, shared and combine fold words (3 x rows x hidden) exceed the fused finish's region, or more fold arrivals
+ * than it holds; the caller then makes the two calls.  The _ragged form takes
  * `moeRagged`'s rate-grouped bank (src/exl3/root.zig:582-644); its shared bank keeps its own rate. */
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
@@ -244,6 +262,29 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
                                          const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
                                          exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
                                          void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* `reconstructInner` (src/exl3/expert_exl3.zig:416-438) of expert `expert` of one per-tile-rate projection
+ * (exl3_tiled_t's layout): the f16 inner matrix [in][out], each tile decoded at its own rate by the decoder the
+ * routed GEMV multiplies with.  in a multiple of 16, out of 128. */
+int32_t exl3_reconstruct_tiled(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                               int32_t expert, int32_t in_features, int32_t out_features, int32_t n_a, int32_t n_b,
+                               exl3_decode_t dec, uint16_t *out, hipStream_t stream);
+
+/* `moeRagged` (src/exl3/root.zig:582-644) over a per-tile-rate bank: the routed SwiGLU chain of exl3_moe (same
+ * arguments, scores dtypes, clamp and `shared`), every tile at its own rate.  Every row count takes the decode chain
+ * (per-slot, or sorted expert windows past 8 rows); there is no GEMM arm.  Workspace: exl3_moe_workspace_size.
+ * The _with_shared_bank form runs a one-expert uniform shared bank (rate 16, 24, 32, 40, 48 or 64, decoded with the
+ * routed codebook) inside the routed launches, as exl3_moe_with_shared_bank does, and declines where it does
+ * (workspace: exl3_moe_with_shared_bank_workspace_size). */
+int32_t exl3_moe_tiled(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                       const exl3_tiled_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
+                       int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
+                       int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
+int32_t exl3_moe_tiled_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                        const exl3_tiled_t *bank, const exl3_bank_t *shared_bank,
+                                        const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                                        exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
+                                        void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Router chain `moeRoutingChainOn` (src/moe_router.zig:22-62): top-k over f32 logits [rows][experts]
  * (ties to the lower expert index, listed in descending logit order), softmax over all experts, gathered and

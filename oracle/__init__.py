@@ -95,6 +95,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.ox_moe_swiglu_host.argtypes = [vp] * 12 + [sz, sz, sz, u32, u32, u32, Decode, ctypes.c_float, vp]
     L.ox_moe_swiglu_rows.argtypes = [vp, sz] + [vp] * 17 + [sz, sz, sz, Decode, ctypes.c_float, ctypes.c_int, vp]
     L.ox_decode_dense.argtypes = [vp, vp, vp, sz, sz, u32, Decode, vp]
+    L.ox_reconstruct_inner_tiled.argtypes = [vp, vp, vp, sz, sz, sz, u32, u32, Decode, vp]
+    L.ox_project_tiled.argtypes = [vp, vp, vp, vp, sz, vp, vp, sz, sz, u32, u32, Decode, vp]
+    L.ox_moe_swiglu_tiled_rows.argtypes = [vp, sz, vp, vp, vp, vp, vp, u32, u32, vp, vp, sz, sz, sz, Decode,
+                                           ctypes.c_float, ctypes.c_int, vp]
     L.ox_gated_shared_term.restype = ctypes.c_float
     L.ox_gated_shared_term.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int]
     L.ox_gated_shared_terms.argtypes = [vp, vp, sz, sz, ctypes.c_int, vp]
@@ -331,6 +335,46 @@ def moe_swiglu_rows(x, gate, up, down, slots, weights, hidden: int, inter: int, 
                                   *[_p(r) for r in rates], _p(sl), _p(wv), sl.shape[1], hidden, inter, dec,
                                   clamp_limit, threads, _p(y))
     _check(rc, "moe_swiglu_rows")
+    return y
+
+
+# ---- per-tile rates (configs[4]'s K1/K2 tile mix; an extension with no reference counterpart) ----------------
+
+
+def reconstruct_inner_tiled(trellis, seg_off, seg_k1, expert: int, in_f: int, out_f: int, n_a: int, n_b: int,
+                            dec: Decode) -> np.ndarray:
+    t, o, k = _u16(trellis), np.ascontiguousarray(seg_off, np.uint32), np.ascontiguousarray(seg_k1, np.uint8)
+    out = np.zeros((in_f, out_f), np.uint16)
+    _check(lib().ox_reconstruct_inner_tiled(_p(t), _p(o), _p(k), expert, in_f, out_f, n_a, n_b, dec, _p(out)),
+           "reconstruct_inner_tiled")
+    return out
+
+
+def project_tiled(x, trellis, seg_off, seg_k1, expert: int, suh, svh, in_f: int, out_f: int, n_a: int, n_b: int,
+                  dec: Decode) -> np.ndarray:
+    xv, t = _f32(x), _u16(trellis)
+    o, k = np.ascontiguousarray(seg_off, np.uint32), np.ascontiguousarray(seg_k1, np.uint8)
+    su, sv = _u16(suh), _u16(svh)
+    out = np.zeros(out_f, np.float32)
+    _check(lib().ox_project_tiled(_p(xv), _p(t), _p(o), _p(k), expert, _p(su), _p(sv), in_f, out_f, n_a, n_b, dec,
+                                  _p(out)), "project_tiled")
+    return out
+
+
+def moe_swiglu_tiled_rows(x, projs, slots, weights, hidden: int, inter: int, n_a: int, n_b: int, dec: Decode,
+                          clamp_limit: float = 0.0, threads: int = 8) -> np.ndarray:
+    """Rows of tokens through moeSwigluHost on per-tile-rate banks; projs = [(trellis, seg_off, seg_k1, suh, svh)]
+    for gate, up and down."""
+    xv = _f32(x).reshape(-1, hidden)
+    sl = np.ascontiguousarray(slots, np.uint32).reshape(xv.shape[0], -1)
+    wv = _f32(weights).reshape(sl.shape)
+    keep = [(_u16(p[0]), np.ascontiguousarray(p[1], np.uint32), np.ascontiguousarray(p[2], np.uint8), _u16(p[3]),
+             _u16(p[4])) for p in projs]
+    arr = lambda i: (ctypes.c_void_p * 3)(*[k[i].ctypes.data for k in keep])  # noqa: E731
+    y = np.zeros((xv.shape[0], hidden), np.float32)
+    rc = lib().ox_moe_swiglu_tiled_rows(_p(xv), xv.shape[0], arr(0), arr(1), arr(2), arr(3), arr(4), n_a, n_b,
+                                        _p(sl), _p(wv), sl.shape[1], hidden, inter, dec, clamp_limit, threads, _p(y))
+    _check(rc, "moe_swiglu_tiled_rows")
     return y
 
 

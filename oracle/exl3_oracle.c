@@ -641,6 +641,127 @@ int ox_moe_swiglu_rows(const float *x, size_t rows, const uint16_t *gate_t, cons
 }
 
 /* ------------------------------------------------------------------------------------------------ */
+/* Per-tile rates: configs[4]'s seeded K1/K2 tile mix, a layout extension with no counterpart in the reference (whose  */
+/* rate is per tensor or per expert group, layout.zig:56-62, rate_groups.zig:22-140).  Each tile decodes at its own   */
+/* rate with decodeTile (expert_exl3.zig:338-357).  Layout of one bank of E experts, in_features x out_features:      */
+/* segment (e, tk, s) = tiles (tk, 8s .. 8s + 7) of expert e lies contiguous from halfword 2 * seg_off[(e * it + tk)  */
+/* * (ot / 8) + s] of the trellis, in column order, tile o at n_a halfwords when bit o of seg_k1[same index] is set,   */
+/* else at n_b.                                                                                                      */
+
+static const uint16_t *ox_tiled_tile(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                                     size_t seg, size_t o, uint32_t n_a, uint32_t n_b, uint32_t *n) {
+    const uint8_t m = seg_k1[seg];
+    size_t hw = 2 * (size_t)seg_off[seg];
+    for (size_t q = 0; q < o; q++) hw += (m >> q) & 1 ? n_a : n_b;
+    *n = (m >> o) & 1 ? n_a : n_b;
+    return trellis + hw;
+}
+
+int ox_reconstruct_inner_tiled(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1, size_t expert,
+                               size_t in_features, size_t out_features, uint32_t n_a, uint32_t n_b, ox_decode dec,
+                               uint16_t *out) {
+    const size_t it = in_features / 16, ot = out_features / 16, segs = ot / 8;
+    uint16_t tile[256];
+    for (size_t tk = 0; tk < it; tk++)
+        for (size_t tn = 0; tn < ot; tn++) {
+            uint32_t n;
+            const uint16_t *w = ox_tiled_tile(trellis, seg_off, seg_k1, (expert * it + tk) * segs + tn / 8, tn % 8,
+                                              n_a, n_b, &n);
+            if (ox_decode_tile(w, n, dec, tile) != 0) return -1;
+            for (int r = 0; r < 16; r++)
+                for (int c = 0; c < 16; c++)
+                    out[(tk * 16 + r) * out_features + tn * 16 + c] = tile[r * 16 + c];
+        }
+    return 0;
+}
+
+/* `project` (expert_exl3.zig:546-566) over expert `expert` of a per-tile-rate bank. */
+int ox_project_tiled(const float *x, const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                     size_t expert, const uint16_t *suh, const uint16_t *svh, size_t in_features,
+                     size_t out_features, uint32_t n_a, uint32_t n_b, ox_decode dec, float *out) {
+    const size_t it = in_features / 16, ot = out_features / 16, segs = ot / 8;
+    float *prep = (float *)malloc(in_features * sizeof(float));
+    float *inner = (float *)malloc(out_features * sizeof(float));
+    if (!prep || !inner) {
+        free(prep);
+        free(inner);
+        return -2;
+    }
+    ox_prepare_input(x, suh, in_features, prep);
+    memset(inner, 0, out_features * sizeof(float));
+    uint16_t tile[256];
+    float wf[256];
+    int rc = 0;
+    for (size_t tk = 0; tk < it && rc == 0; tk++)
+        for (size_t tn = 0; tn < ot; tn++) {
+            uint32_t n;
+            const uint16_t *w = ox_tiled_tile(trellis, seg_off, seg_k1, (expert * it + tk) * segs + tn / 8, tn % 8,
+                                              n_a, n_b, &n);
+            if (ox_decode_tile(w, n, dec, tile) != 0) {
+                rc = -1;
+                break;
+            }
+            for (int i = 0; i < 256; i++) wf[i] = ox_f16_to_f32(tile[i]);
+            const float *xb = prep + tk * 16;
+            float *yb = inner + tn * 16;
+            for (int r = 0; r < 16; r++)
+                for (int c = 0; c < 16; c++) yb[c] += xb[r] * wf[r * 16 + c];
+        }
+    if (rc == 0) {
+        for (size_t i = 0; i < out_features; i++) inner[i] = f16r(inner[i]);
+        ox_finish_output(inner, svh, out_features, out);
+    }
+    free(prep);
+    free(inner);
+    return rc;
+}
+
+/* moeSwigluHost (expert_exl3_kernels.zig:3059-3114) over rows of tokens on per-tile-rate banks: t/o/k[p] are
+ * projection p's trellis, seg_off and seg_k1 (gate, up, down); suh/svh as for a uniform bank.  OpenMP over rows. */
+int ox_moe_swiglu_tiled_rows(const float *x, size_t rows, const uint16_t *const t[3], const uint32_t *const o[3],
+                             const uint8_t *const k1[3], const uint16_t *const suh[3], const uint16_t *const svh[3],
+                             uint32_t n_a, uint32_t n_b, const uint32_t *slots, const float *weights, size_t topk,
+                             size_t hidden, size_t inter, ox_decode dec, float clamp_limit, int threads, float *y) {
+    int bad = 0;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 1 ? threads : 1) reduction(| : bad)
+    for (long r = 0; r < (long)rows; r++) {
+        float *yr = y + r * hidden;
+        memset(yr, 0, hidden * sizeof(float));
+        float *gy = (float *)malloc(inter * 4), *uy = (float *)malloc(inter * 4), *h = (float *)malloc(inter * 4);
+        float *dy = (float *)malloc(hidden * 4);
+        if (!gy || !uy || !h || !dy) bad |= 1;
+        for (size_t k = 0; k < topk && !bad; k++) {
+            const size_t e = slots[r * topk + k];
+            int rc = ox_project_tiled(x + r * hidden, t[0], o[0], k1[0], e, suh[0] + e * hidden, svh[0] + e * inter,
+                                      hidden, inter, n_a, n_b, dec, gy);
+            rc |= ox_project_tiled(x + r * hidden, t[1], o[1], k1[1], e, suh[1] + e * hidden, svh[1] + e * inter,
+                                   hidden, inter, n_a, n_b, dec, uy);
+            for (size_t i = 0; i < inter; i++) {
+                float g = gy[i], u = uy[i];
+                if (clamp_limit > 0.0f) {
+                    g = fminf(g, clamp_limit);
+                    u = fminf(fmaxf(u, -clamp_limit), clamp_limit);
+                }
+                h[i] = (g / (1.0f + expf(-g))) * u;
+            }
+            rc |= ox_project_tiled(h, t[2], o[2], k1[2], e, suh[2] + e * inter, svh[2] + e * hidden, inter, hidden,
+                                   n_a, n_b, dec, dy);
+            if (rc) {
+                bad |= 1;
+                break;
+            }
+            const float w = weights[r * topk + k];
+            for (size_t i = 0; i < hidden; i++) yr[i] += w * dy[i];
+        }
+        free(gy);
+        free(uy);
+        free(h);
+        free(dy);
+    }
+    return bad ? -1 : 0;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
 /* The gated shared expert's term: REDUCE_GATED_SHARED_SOURCE, expert_exl3_kernels.zig:2410-2431.  In T = dtype   */
 /* (0 f16, 1 bf16, 2 f32): ex = T(exp|g|), rc = T(1 / T(1 + ex)), sig = g < 0 ? rc : T(1 - rc), term = T(sig * sh). */
 /* exp is evaluated in double and rounded to float (the kernel's own choice for Metal's precise::exp).             */

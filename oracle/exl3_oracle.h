@@ -28,6 +28,9 @@
  *                                   independent numpy restatement over ox_decode_dense weights.
  *   ox_moe_swiglu_rows            : rows of ox_moe_swiglu_host over ragged banks; equals it row by row (and the
  *                                   threaded run equals the single-threaded one byte for byte).
+ *   ox_*_tiled                    : EXTENSION (configs[4]'s per-tile K1/K2 map, no reference counterpart): the
+ *                                   uniform functions applied tile by tile at each tile's own rate; equal to them
+ *                                   when every tile has one rate, and to per-tile decodeTile reassembly otherwise.
  *   ox_gated_shared_term          : the rounding chain of REDUCE_GATED_SHARED_SOURCE; checked against numpy's
  *                                   float16 / an independent bf16 rounding of the same chain, every f16 and bf16 gate.
  *   ox_decode_dense               : equals the dense product diag(suh) H M H diag(svh) built by numpy.
@@ -141,6 +144,16 @@ int ox_moe_swiglu_rows(const float *x, size_t rows, const uint16_t *gate_t, cons
                        const float *weights, size_t topk, size_t hidden, size_t inter, ox_decode dec,
                        float clamp_limit, int threads, float *y);
 
+int ox_reconstruct_inner_tiled(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1, size_t expert,
+                               size_t in_features, size_t out_features, uint32_t n_a, uint32_t n_b, ox_decode dec,
+                               uint16_t *out);
+int ox_project_tiled(const float *x, const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                     size_t expert, const uint16_t *suh, const uint16_t *svh, size_t in_features,
+                     size_t out_features, uint32_t n_a, uint32_t n_b, ox_decode dec, float *out);
+int ox_moe_swiglu_tiled_rows(const float *x, size_t rows, const uint16_t *const t[3], const uint32_t *const o[3],
+                             const uint8_t *const k1[3], const uint16_t *const suh[3], const uint16_t *const svh[3],
+                             uint32_t n_a, uint32_t n_b, const uint32_t *slots, const float *weights, size_t topk,
+                             size_t hidden, size_t inter, ox_decode dec, float clamp_limit, int threads, float *y);
 float ox_gated_shared_term(float gate, float shared, int dtype);
 void ox_gated_shared_terms(const float *gate, const float *shared, size_t rows, size_t cols, int dtype, float *out);
 

@@ -29,6 +29,9 @@ EXPORTS = (
     "exl3_moe_with_shared_bank_workspace_size",
     "exl3_moe_with_shared_bank",
     "exl3_moe_ragged_with_shared_bank",
+    "exl3_reconstruct_tiled",
+    "exl3_moe_tiled",
+    "exl3_moe_tiled_with_shared_bank",
     "exl3_route_topk",
     "exl3_tile_major",
     "exl3_encode_workspace_size",
@@ -54,6 +57,12 @@ class BankT(ctypes.Structure):
 class RaggedT(ctypes.Structure):
     _fields_ = [("trellis", ctypes.c_void_p * 3), ("suh", ctypes.c_void_p * 3), ("svh", ctypes.c_void_p * 3),
                 ("meta", ctypes.c_void_p), ("experts", ctypes.c_int32), ("lane_rates_only", ctypes.c_int32)]
+
+
+class TiledT(ctypes.Structure):
+    _fields_ = [("trellis", ctypes.c_void_p * 3), ("seg_off", ctypes.c_void_p * 3), ("seg_k1", ctypes.c_void_p * 3),
+                ("suh", ctypes.c_void_p * 3), ("svh", ctypes.c_void_p * 3), ("experts", ctypes.c_int32),
+                ("n_a", ctypes.c_int32), ("n_b", ctypes.c_int32)]
 
 
 _lib = None
@@ -96,6 +105,12 @@ def load() -> ctypes.CDLL:
     L.exl3_moe_ragged_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(RaggedT),
                                                    ctypes.POINTER(BankT), vp, vp, i32, i32, DecodeT, i32, vp, i32, vp,
                                                    sz, vp]
+    L.exl3_reconstruct_tiled.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, DecodeT, vp, vp]
+    L.exl3_moe_tiled.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(TiledT), vp, vp, i32, i32, DecodeT, i32, vp,
+                                 vp, i32, vp, sz, vp]
+    L.exl3_moe_tiled_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(TiledT),
+                                                  ctypes.POINTER(BankT), vp, vp, i32, i32, DecodeT, i32, vp, i32, vp,
+                                                  sz, vp]
     L.exl3_route_topk.argtypes = [vp, i32, i32, i32, vp, vp, vp]
     L.exl3_tile_major.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp]
     L.exl3_encode_workspace_size.restype = sz

@@ -371,18 +371,26 @@ bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, 
     return topk * p.s2 <= FOLD_MAX_SPLITS && (size_t)3 * rows * hidden <= kFoldWords;
 }
 
-// One routed layer's launches.  n[3] are the projections' uniform rates (all 0 with a ragged `meta`); k is the decode
-// of the gate's rate (per-rate constants of the other projections are resolved here).  shared / shared_gate: an
-// already computed shared expert [rows][hidden] in y's dtype, added as it is or as sigmoid(gate) * shared.
+// A per-tile-rate bank's segment tables, per projection (gate, up, down).
+struct TiledTables {
+    const uint32_t *off[3];
+    const uint8_t *k1[3];
+};
+
+// One routed layer's launches.  n[3] are the projections' uniform rates (all 0 with a ragged `meta` or a per-tile-rate
+// bank's tables `tt`); k is the decode of the gate's rate (per-rate constants of the other projections are resolved
+// here).  shared / shared_gate: an already computed shared expert [rows][hidden] in y's dtype, added as it is or as
+// sigmoid(gate) * shared.
 int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int table, const void *x, int32_t x_dtype,
                    int32_t rows, int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
                    const uint16_t *const su[3], const uint16_t *const sv[3], const int n[3], const uint32_t *meta,
                    int meta_lane_only, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
                    int32_t clamp_limit, const void *shared, const void *shared_gate, void *y, int32_t y_dtype,
-                   void *ws, size_t ws_bytes, hipStream_t stream, const SharedBank *sb = nullptr) {
+                   void *ws, size_t ws_bytes, hipStream_t stream, const SharedBank *sb = nullptr,
+                   const TiledTables *tt = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    if (!sb && !meta && n[0] == n[1] && n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
+    if (!sb && !meta && !tt && n[0] == n[1] && n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
         const MoeGemmPlan gp = plan_moe_gemm(nslots, hidden, inter, experts);
         if (ws_bytes < gp.total() || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
             return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", gp.total(),
@@ -524,6 +532,12 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
     a.bank_limit = experts;
     a.meta = meta;
     a.meta_lane_only = meta_lane_only;
+    if (tt) {
+        for (int i = 0; i < 2; i++) {
+            a.seg_off[i] = tt->off[i];
+            a.seg_k1[i] = tt->k1[i];
+        }
+    }
     a.table = table;
     a.k = k;
     a.out_scale = scale;
@@ -534,7 +548,7 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
     a.nproj = 2;
     // Gate and up of a uniform bank at different rates (moeMixedDecode, src/exl3/root.zig:705-722): one launch each,
     // each at its own rate.
-    const bool split_pair = !meta && n[0] != n[1];
+    const bool split_pair = !meta && !tt && n[0] != n[1];
     if (split_pair) a.nproj = 1;
     a.fused_finish = 0;
     a.partial_only = 1;
@@ -591,9 +605,13 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
     d.bank_limit = experts;
     d.meta = meta;
     d.meta_lane_only = meta_lane_only;
+    if (tt) {
+        d.seg_off[0] = tt->off[2];
+        d.seg_k1[0] = tt->k1[2];
+    }
     d.table = table;
     d.k = k;
-    if (!meta && n[2] != n[0]) {
+    if (!meta && !tt && n[2] != n[0]) {
         int fam_d;
         if (resolve_decode(dec, n[2], &fam_d, &d.k)) return EXL3_ERR_RATE_MISSING;
     }
@@ -732,6 +750,33 @@ int32_t shared_bank_checks(const exl3_bank_t *b, const char *what, SharedBank *o
     if (b->gate.n != b->up.n || b->gate.n != b->down.n)
         return fail(EXL3_ERR_BAD_SHAPE, "%s: gate/up/down rates differ", what);
     out->n = b->gate.n;
+    return ok();
+}
+
+// A per-tile-rate bank: its rates, codebook and operands; the family, the constants at n_b (the kernels read both
+// rates' rows from the table) and the segment tables.
+int32_t tiled_checks(const exl3_tiled_t *b, const exl3_decode_t &dec, const char *what, int *fam, DecodeK *k,
+                     TiledTables *tt) {
+    if (!b || b->experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "%s: no bank", what);
+    if (b->n_a != TILED_NA || b->n_b != TILED_NB)
+        return fail(EXL3_ERR_BAD_SHAPE, "%s: tile rates %d / %d (the per-tile mix is n = %d / %d)", what, b->n_a,
+                    b->n_b, TILED_NA, TILED_NB);
+    for (int i = 0; i < 3; i++) {
+        if (!b->trellis[i] || !b->seg_off[i] || !b->seg_k1[i] || !b->suh[i] || !b->svh[i])
+            return fail(EXL3_ERR_BAD_SHAPE, "%s: projection %d has a null operand", what, i);
+        if (reinterpret_cast<uintptr_t>(b->seg_k1[i]) % 4)
+            return fail(EXL3_ERR_BAD_SHAPE, "%s: projection %d's seg_k1 must be 4-byte aligned", what, i);
+        tt->off[i] = b->seg_off[i];
+        tt->k1[i] = b->seg_k1[i];
+    }
+    DecodeK ka;
+    int32_t rc = resolve_decode(dec, TILED_NA, fam, &ka);
+    if (rc) return rc;
+    rc = resolve_decode(dec, TILED_NB, fam, k);
+    if (rc) return rc;
+    if (*fam == FAM_PAIR || *fam == FAM_MUL1)
+        return fail(EXL3_ERR_CODEBOOK_UNSUPPORTED, "%s: per-tile rates serve MCG, 3INST and the SPEC1 / STD1 hash rows",
+                    what);
     return ok();
 }
 
@@ -1003,6 +1048,88 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
     return moe_launch(fam, k, dec, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
                       bank->svh, n0, bank->meta, lane_only, inds, scores, scores_dtype, topk, clamp_limit, nullptr,
                       nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb);
+}
+
+int32_t exl3_reconstruct_tiled(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                               int32_t expert, int32_t in_features, int32_t out_features, int32_t n_a, int32_t n_b,
+                               exl3_decode_t dec, uint16_t *out, hipStream_t stream) {
+    if (in_features <= 0 || out_features <= 0 || in_features % 16 || out_features % 128 || expert < 0)
+        return fail(EXL3_ERR_BAD_SHAPE, "reconstruct_tiled: in=%d out=%d expert=%d (in a multiple of 16, out of 128)",
+                    in_features, out_features, expert);
+    exl3_tiled_t b{};
+    for (int i = 0; i < 3; i++) {
+        b.trellis[i] = trellis;
+        b.seg_off[i] = seg_off;
+        b.seg_k1[i] = seg_k1;
+        b.suh[i] = trellis;  // unused here: only the tables and rates are checked
+        b.svh[i] = trellis;
+    }
+    b.experts = expert + 1;
+    b.n_a = n_a;
+    b.n_b = n_b;
+    int fam;
+    DecodeK ka, kb;
+    TiledTables tt;
+    int32_t rc = tiled_checks(&b, dec, "reconstruct_tiled", &fam, &kb, &tt);
+    if (rc) return rc;
+    rc = resolve_decode(dec, TILED_NA, &fam, &ka);
+    if (rc) return rc;
+    if (!out) return fail(EXL3_ERR_BAD_SHAPE, "reconstruct_tiled: null operand");
+    return launched(run_reconstruct_tiled(fam, trellis, seg_off, seg_k1, expert, in_features / 16, out_features / 16,
+                                          ka, kb, out, stream),
+                    "exl3_reconstruct_tiled");
+}
+
+int32_t exl3_moe_tiled(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                       const exl3_tiled_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
+                       int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
+                       int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
+    if (rc) return rc;
+    int fam;
+    DecodeK k;
+    TiledTables tt;
+    rc = tiled_checks(bank, dec, "moe_tiled", &fam, &k, &tt);
+    if (rc) return rc;
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_tiled: null operand");
+    const int n0[3] = {0, 0, 0};
+    return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis,
+                      bank->suh, bank->svh, n0, nullptr, 0, inds, scores, scores_dtype, topk, clamp_limit, shared,
+                      nullptr, y, y_dtype, workspace, workspace_bytes, stream, nullptr, &tt);
+}
+
+int32_t exl3_moe_tiled_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
+                                        const exl3_tiled_t *bank, const exl3_bank_t *shared_bank,
+                                        const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
+                                        exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
+                                        void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
+    if (rc) return rc;
+    int fam;
+    DecodeK k;
+    TiledTables tt;
+    rc = tiled_checks(bank, dec, "moe_tiled_with_shared_bank", &fam, &k, &tt);
+    if (rc) return rc;
+    SharedBank sb;
+    rc = shared_bank_checks(shared_bank, "moe_tiled_with_shared_bank (shared)", &sb);
+    if (rc) return rc;
+    // the shared bank decodes with the routed codebook at its own rate: its table must have that rate
+    if (fam == FAM_HASH) {
+        uint32_t m0, m1, m2, m3;
+        if (!table_row(dec.table, sb.n, m0, m1, m2, m3))
+            return fail(EXL3_ERR_RATE_MISSING, "moe_tiled_with_shared_bank: table %d has no row for n=%d", dec.table,
+                        sb.n);
+    }
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_tiled_with_shared_bank: null operand");
+    if (!lane_rate(sb.n) || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0))
+        return declined("moe_tiled_with_shared_bank: declined (rows=%d, y dtype %d, shared n=%d): run the shared expert "
+                        "as a one-expert exl3_moe and pass it to exl3_moe_tiled as `shared`", rows, y_dtype, sb.n);
+    const int n0[3] = {0, 0, 0};
+    return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis,
+                      bank->suh, bank->svh, n0, nullptr, 0, inds, scores, scores_dtype, topk, clamp_limit, nullptr,
+                      nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb, &tt);
 }
 
 int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds, float *scores,

@@ -21,6 +21,11 @@ enum Codebook : int { CB_MUL1 = 0, CB_MCG = 1, CB_SPEC1 = 2, CB_PAIR1 = 3, CB_ST
 // Kernel-side decode families: SPEC1 and STD1 share the hash-mask body with a per-rate (mult, mask) row.
 enum Family : int { FAM_MCG = 0, FAM_MUL1 = 1, FAM_HASH = 2, FAM_PAIR = 3, FAM_3INST = 4 };
 
+// Per-tile-rate banks (configs[4]'s K1 / K2 tile mix): every tile at one of these two rates, and the kernels' rate
+// parameter for such a bank.
+constexpr int TILED_NA = 16, TILED_NB = 32;
+constexpr int N_TILED = -3;
+
 // Runtime decode constants for one (codebook, window, table, rate): filled on the host.
 struct DecodeK {
     uint32_t wmask;  // codeword window mask (w16: 0xFFFF)

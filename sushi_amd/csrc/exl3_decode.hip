@@ -2,7 +2,8 @@
 // of one projection's inner matrix ("dequantized fp16 weights", bit-exact with reconstructInner,
 // beamivalice/sushi src/exl3/expert_exl3.zig:416-438).  The reconstruction runs the decoder the GEMV and the GEMM
 // multiply with: the lane reader and lane decoder at the rates they serve (16, 24, 32, 40, 48, 64), the generic
-// per-codeword reader at every other rate, so the weights it returns are the hot path's own.
+// per-codeword reader at every other rate, so the weights it returns are the hot path's own; a per-tile-rate bank
+// through the tiled reader and decoder.
 #include "exl3_kernels.h"
 #include "exl3_lane_decode.h"
 
@@ -104,6 +105,70 @@ static hipError_t launch_reconstruct_lane(const uint16_t *trellis, int tiles, in
         hipLaunchKernelGGL((reconstruct_lane_kernel<FAM, N, false>), grid, dim3(64 * RL_WAVES), 0, s, trellis, tiles,
                            ot, k, out);
     return hipGetLastError();
+}
+
+// One expert of a per-tile-rate bank: one wave per segment (8 tiles of one k-tile row), lane 8o + j decoding chunk j
+// of tile o at that tile's own rate with the GEMV's tiled reader and decoder.
+template <int FAM, bool MASKED>
+__global__ __launch_bounds__(64 * RL_WAVES) void reconstruct_tiled_kernel(const uint16_t *__restrict__ trellis,
+                                                                          const uint32_t *__restrict__ seg_off,
+                                                                          const uint8_t *__restrict__ seg_k1,
+                                                                          int expert, int it, int ot, DecodeK ka,
+                                                                          DecodeK kb, uint16_t *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int sg = blockIdx.x * RL_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // segment of the expert
+    const int segs = ot / 8;
+    if (sg >= it * segs) return;
+    const int o = lane >> 3, j = lane & 7;
+    const int tk = sg / segs, s8 = sg - tk * segs;
+    const size_t seg = ((size_t)expert * it + tk) * segs + s8;
+    const uint32_t m = seg_k1[seg];
+    const bool k1 = ((m >> o) & 1u) != 0;
+    const uint32_t lw = 16u * (uint32_t)o - 8u * (uint32_t)__builtin_popcount(m & ((1u << o) - 1u));
+    uint32_t A[3];
+    load_lane_words_tiled(reinterpret_cast<const uint32_t *>(trellis) + seg_off[seg], lw, j, k1, A);
+    uint32_t w[16];
+    decode_weights_tiled<FAM, MASKED>(A, k1, tiled_constants(k1, ka, kb), w);
+    if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
+    }
+    const int tn = s8 * 8 + o;
+    const size_t of = (size_t)ot * 16;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int qq = i >> 2, p = i & 3;
+        const size_t at = ((size_t)tk * 16 + 2 * qq + 8 * (p & 1)) * of + (size_t)tn * 16 + j + 8 * (p >> 1);
+        out[at] = (uint16_t)(w[i] & 0xFFFFu);
+        out[at + of] = (uint16_t)(w[i] >> 16);
+    }
+}
+
+template <int FAM>
+static hipError_t launch_reconstruct_tiled(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                                           int expert, int it, int ot, const DecodeK &ka, const DecodeK &kb,
+                                           uint16_t *out, hipStream_t s) {
+    const int waves = it * (ot / 8);
+    const dim3 grid((unsigned)((waves + RL_WAVES - 1) / RL_WAVES));
+    if (kb.wmask != 0xFFFFu)
+        hipLaunchKernelGGL((reconstruct_tiled_kernel<FAM, true>), grid, dim3(64 * RL_WAVES), 0, s, trellis, seg_off,
+                           seg_k1, expert, it, ot, ka, kb, out);
+    else
+        hipLaunchKernelGGL((reconstruct_tiled_kernel<FAM, false>), grid, dim3(64 * RL_WAVES), 0, s, trellis, seg_off,
+                           seg_k1, expert, it, ot, ka, kb, out);
+    return hipGetLastError();
+}
+
+hipError_t run_reconstruct_tiled(int fam, const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                                 int expert, int it, int ot, const DecodeK &ka, const DecodeK &kb, uint16_t *out,
+                                 hipStream_t s) {
+    if (it * ot == 0) return hipSuccess;
+    switch (fam) {
+    case FAM_MCG: return launch_reconstruct_tiled<FAM_MCG>(trellis, seg_off, seg_k1, expert, it, ot, ka, kb, out, s);
+    case FAM_HASH: return launch_reconstruct_tiled<FAM_HASH>(trellis, seg_off, seg_k1, expert, it, ot, ka, kb, out, s);
+    case FAM_3INST: return launch_reconstruct_tiled<FAM_3INST>(trellis, seg_off, seg_k1, expert, it, ot, ka, kb, out, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 template <int FAM>

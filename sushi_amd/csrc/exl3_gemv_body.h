@@ -171,6 +171,17 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
     mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4);
 }
 
+// The same for a lane of a per-tile-rate bank, at its own tile's rate (k: the lane's constants).
+template <int FAM, int RT, bool MASKED>
+__device__ __forceinline__ void decode_tile_tiled(const uint32_t (&A)[3], bool k1, const uint16_t (*xs)[XS_PITCH],
+                                                  int kk, int rows, const DecodeK &k, f4_t (&accA)[RowGroups<RT>::G],
+                                                  f4_t (&accB)[RowGroups<RT>::G], int i4) {
+    uint32_t w[16];
+    decode_weights_tiled<FAM, MASKED>(A, k1, k, w);
+    scale_for_mfma<FAM>(w);
+    mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4);
+}
+
 // x[i] as f32 from an f16 / bf16 / f32 array without branching on the dtype: one 32-bit load of the aligned word
 // that holds the element, then bit-mask selects.  (A branch per dtype joins through a register copy, and that copy
 // makes the load wait for its data right there.)  The array starts 4-byte aligned (the C ABI checks it) and rows
@@ -456,10 +467,27 @@ __device__ __forceinline__ void fetch_svh(GemvCtx &c, int lane) {
     c.sv1 = h2f(c.svh[sv + lane + 64]);
 }
 
+// A per-tile-rate projection as a workgroup reads it (N == N_TILED): its segment tables and the constants at both
+// rates.
+struct TiledSrc {
+    const uint32_t *seg_off;
+    const uint8_t *seg_k1;
+    DecodeK ka, kb;
+};
+
+// The mask of segment `seg` (8 bits, one per tile), read through its aligned 32-bit word so the load stays a scalar
+// one (the host checks that the table is 4-byte aligned; its length, a multiple of 8, keeps the word inside it).
+__device__ __forceinline__ uint32_t seg_mask(const uint8_t *k1, size_t seg) {
+    const uint32_t w = reinterpret_cast<const uint32_t *>(k1)[seg >> 2];
+    return (w >> (8u * (uint32_t)(seg & 3))) & 0xFFu;
+}
+
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
+// N == N_TILED: each tile at its own rate (ts), tb the projection's whole trellis.
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const uint16_t *__restrict__ tb,
-                                          int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
+                                          int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128],
+                                          const TiledSrc &ts = TiledSrc{}) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
     const int o = lane >> 3, j = lane & 7;
@@ -469,7 +497,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
     for (int g = 0; g < RG; g++) accA[g] = accB[g] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     if constexpr (N != 0) {
-        constexpr int AW = LaneBits<N>::AW;
+        constexpr bool TILED = N == N_TILED;
+        constexpr int AW = TILED ? 3 : LaneBits<(TILED ? TILED_NB : N)>::AW;
         // This wave's k-tiles are wave, wave + GEMV_WAVES, ...; a split spans whole 128-blocks (8 k-tiles), so every
         // wave has at least one.  The first TPW loads are issued unconditionally (a wave with fewer tiles re-reads its
         // last one), so the compiler counts them and each tile's decode waits only for that tile's own loads.
@@ -478,24 +507,41 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         prologue_fetch<PRO, RT, WIN>(a, c, wave, lane, pr);
         __builtin_amdgcn_sched_barrier(0);  // the input loads stay ahead of the tile loads (vmcnt retires in order)
         uint32_t Aw[TPW][AW];
+        bool k1s[TPW];  // N_TILED: the lane's tile in slot t is at TILED_NA
         // tile (tk, og * 8 + o): the uniform start of k-tile row tk of the group plus the lane's tile offset
-        const uint32_t lane_words = (uint32_t)(o * N) >> 1;
+        const uint32_t lane_words = TILED ? 0u : (uint32_t)(o * N) >> 1;
         auto row_of = [&](int tk) __attribute__((always_inline)) {
             return reinterpret_cast<const uint32_t *>(tb + ((size_t)tk * c.OT + c.og * 8) * N);
         };
+        auto load_slot = [&](int t, int tk) __attribute__((always_inline)) {
+            if constexpr (TILED) {  // segment (bank, tk, og): its start and mask are wave-uniform
+                const size_t seg = ((size_t)c.bank * c.IT + tk) * (size_t)(c.OT >> 3) + c.og;
+                const uint32_t m = seg_mask(ts.seg_k1, seg);
+                const uint32_t *row = reinterpret_cast<const uint32_t *>(tb) + ts.seg_off[seg];
+                const bool k1 = ((m >> o) & 1u) != 0;
+                const uint32_t lw = 16u * (uint32_t)o - 8u * (uint32_t)__builtin_popcount(m & ((1u << o) - 1u));
+                load_lane_words_tiled(row, lw, j, k1, Aw[t]);
+                k1s[t] = k1;
+            } else {
+                load_lane_words_u<N>(row_of(tk), lane_words, j, Aw[t]);
+            }
+        };
 #pragma unroll
-        for (int t = 0; t < TPW; t++) {
-            const int tk = c.kt0 + wave + GEMV_WAVES * min(t, ntiles - 1);
-            load_lane_words_u<N>(row_of(tk), lane_words, j, Aw[t]);
-        }
+        for (int t = 0; t < TPW; t++) load_slot(t, c.kt0 + wave + GEMV_WAVES * min(t, ntiles - 1));
         fetch_svh(c, lane);
         prologue<PRO, RT, WIN, SH>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
         auto decode_at = [&](int t, int tt) __attribute__((always_inline)) {  // slot t holds the wave's tile tt
             const int kk = wave + GEMV_WAVES * tt;
-            if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
-            else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
+            if constexpr (TILED) {
+                const DecodeK kl = tiled_constants(k1s[t], ts.ka, ts.kb);
+                if (masked) decode_tile_tiled<FAM, RT, true>(Aw[t], k1s[t], xs, kk, c.rows, kl, accA, accB, lane & 3);
+                else decode_tile_tiled<FAM, RT, false>(Aw[t], k1s[t], xs, kk, c.rows, kl, accA, accB, lane & 3);
+            } else {
+                if (masked) decode_tile<FAM, N, RT, true>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
+                else decode_tile<FAM, N, RT, false>(Aw[t], xs, kk, c.rows, k, accA, accB, lane & 3);
+            }
         };
         int t0 = 0;
         // Splits longer than TPW tiles per wave: every batch but the last refills each slot with the same slot of the
@@ -505,8 +551,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
 #pragma unroll
             for (int t = 0; t < TPW; t++) {
                 decode_at(t, t0 + t);
-                const int tk = c.kt0 + wave + GEMV_WAVES * min(t0 + TPW + t, ntiles - 1);
-                load_lane_words_u<N>(row_of(tk), lane_words, j, Aw[t]);
+                load_slot(t, c.kt0 + wave + GEMV_WAVES * min(t0 + TPW + t, ntiles - 1));
             }
         }
 #pragma unroll
@@ -687,6 +732,29 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
         const int n = N ? N : a.n;
         const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
         gemv_body<FAM, N, RT, PRO, WIN, SH>(a, c, tb, n, a.k, xs, red);
+    } else if constexpr (N == N_TILED) {
+        // Per-tile-rate bank: every tile at TILED_NA or TILED_NB, read through the projection's segment tables (a
+        // fused shared expert keeps its own uniform rate, a lane-reader rate the host checked).
+        if constexpr (SH) {
+            const int n = a.sh_n;
+            const DecodeK k = rate_constants<FAM>(a, n);
+            switch (n) {
+            case 16: gemv_body<FAM, 16, RT, PRO, WIN, SH>(a, c, trellis, n, k, xs, red); break;
+            case 24: gemv_body<FAM, 24, RT, PRO, WIN, SH>(a, c, trellis, n, k, xs, red); break;
+            case 32: gemv_body<FAM, 32, RT, PRO, WIN, SH>(a, c, trellis, n, k, xs, red); break;
+            case 40: gemv_body<FAM, 40, RT, PRO, WIN, SH>(a, c, trellis, n, k, xs, red); break;
+            case 48: gemv_body<FAM, 48, RT, PRO, WIN, SH>(a, c, trellis, n, k, xs, red); break;
+            case 64: gemv_body<FAM, 64, RT, PRO, WIN, SH>(a, c, trellis, n, k, xs, red); break;
+            default: break;
+            }
+        } else {
+            TiledSrc ts;
+            ts.seg_off = p1 ? a.seg_off[1] : a.seg_off[0];
+            ts.seg_k1 = p1 ? a.seg_k1[1] : a.seg_k1[0];
+            ts.ka = rate_constants<FAM>(a, TILED_NA);
+            ts.kb = rate_constants<FAM>(a, TILED_NB);
+            gemv_body<FAM, N_TILED, RT, PRO, WIN, SH>(a, c, trellis, 0, a.k, xs, red, ts);
+        }
     } else {
         // Ragged bank: the rate comes from the expert's meta row (a shared expert has its own uniform rate).
         // N == -1 serves the rates with a lane reader and skips the rest; N == -2 (a second launch over the same
@@ -722,7 +790,7 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
 }
 
 // N > 0: one rate for the launch; N == 0: the generic reader; N == -1 / -2: per-expert rate from the ragged meta table
-// (lane-reader rates / the other rates), dispatched per workgroup.
+// (lane-reader rates / the other rates), dispatched per workgroup; N == N_TILED: per-tile rates.
 // SHP: the launch carries a fused shared expert's rows (either MoE arm): a separate instantiation, so launches
 // without them keep a kernel whose registers hold none of it.
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP>
@@ -829,6 +897,10 @@ static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
 
 template <int FAM, int PRO>
 static hipError_t launch_gemv_fam(const GemvArgs &a, hipStream_t s) {
+    if (a.seg_off[0]) {  // per-tile rates: the hash-product families only (the host refuses the others)
+        if constexpr (FAM == FAM_PAIR || FAM == FAM_MUL1) return hipErrorInvalidValue;
+        else return launch_gemv_n<FAM, N_TILED, PRO>(a, s);
+    }
     if (a.meta) {  // ragged: the lane-reader rates, then any other rate (unless the host ruled them out)
         hipError_t e = launch_gemv_n<FAM, -1, PRO>(a, s);
         return e != hipSuccess || a.meta_lane_only ? e : launch_gemv_n<FAM, -2, PRO>(a, s);

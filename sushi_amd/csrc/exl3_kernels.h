@@ -11,6 +11,11 @@ hipError_t run_decode_codewords(int fam, const uint16_t *cw, int64_t count, cons
                                 hipStream_t s);
 hipError_t run_reconstruct_inner(int fam, const uint16_t *trellis, int it, int ot, int n, const DecodeK &k,
                                  uint16_t *out, hipStream_t s);
+// One expert of a per-tile-rate bank (segment tables as GemvArgs::seg_off / seg_k1 describe them); ka / kb are the
+// constants at TILED_NA / TILED_NB.
+hipError_t run_reconstruct_tiled(int fam, const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
+                                 int expert, int it, int ot, const DecodeK &ka, const DecodeK &kb, uint16_t *out,
+                                 hipStream_t s);
 
 enum Prologue : int { PRO_X = 0, PRO_MID = 1 };
 
@@ -66,6 +71,10 @@ struct GemvArgs {
     const uint32_t *meta;    // ragged meta [E][8]: n at col pi, word offset at col 4 + pi
     int meta_lane_only;      // every ragged rate is a lane-reader rate: no launch for the other rates
     int meta_col[2];
+    // per-tile-rate bank (N_TILED): per projection, the segment tables [E][in/16][out/128] (word offset of each
+    // segment of 8 tiles, and its mask: bit o set = tile o at TILED_NA, else TILED_NB); null = not tiled
+    const uint32_t *seg_off[2];
+    const uint8_t *seg_k1[2];
     int table;               // codebook table for per-rate rows (ragged hash / pair families)
     int bank_limit;          // expert count: ids are clamped below it (memory safety on bad routing)
     DecodeK k;

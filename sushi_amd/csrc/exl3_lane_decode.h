@@ -119,4 +119,97 @@ __device__ __forceinline__ void decode_weights(const uint32_t (&A)[LaneBits<N>::
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Per-tile rates (configs[4]'s seeded K1 / K2 tile mix, a layout extension: the reference fixes a rate per tensor or
+// per expert group, src/exl3/layout.zig:56-62, and decodes every tile at its own n with decodeTile,
+// src/exl3/expert_exl3.zig:338-357).  A segment is the 8 tiles (k-tile row tk, output group s) one wave reads; they
+// lie contiguous from the segment's word offset, tile o at TILED_NA halfwords when bit o of the segment's mask is set,
+// else TILED_NB, so tile o starts 16 o - 8 popcount(mask below o) words in.  Each lane decodes its chunk at its own
+// tile's rate.
+// The lane's words of its tile: A[0..1] as load_lane_words<16> reads them (k1), else A[0..2] as load_lane_words<32>.
+// `row` is the segment's wave-uniform start and lane_words its tile's offset (words); loads take the scalar-base form.
+__device__ __forceinline__ void load_lane_words_tiled(const uint32_t *__restrict__ row, uint32_t lane_words, int j,
+                                                      bool k1, uint32_t (&A)[3]) {
+    typedef __attribute__((address_space(1))) const uint32_t global_u32;
+    const char *base = reinterpret_cast<const char *>(row);
+    auto at = [&](uint32_t w) __attribute__((always_inline)) {
+        return *(global_u32 *)(base + (uint32_t)((lane_words + w) * 4u));
+    };
+    const uint32_t i0 = k1 ? (uint32_t)((j + 7) & 7) : (uint32_t)((2 * j + 15) & 15);
+    const uint32_t i1 = k1 ? (uint32_t)j : (uint32_t)(2 * j);
+    const uint32_t i2 = k1 ? (uint32_t)j : (uint32_t)(2 * j + 1);  // unused at n = 16 (a repeat of A[1])
+    A[0] = at(i0);
+    A[1] = at(i1);
+    A[2] = at(i2);
+}
+
+// The lane's 16 weight pairs at its own rate.  Both rates pair codewords in 32-bit windows (Pairing<16>: window s
+// ending at codeword 16 + s carries codeword s in its high half; Pairing<32>: the windows ending at codewords 8 + s
+// and 16 + s (s >= 8) carry s and 8 + s), so only the window extraction depends on the rate; the products, masks and
+// sums run once over 16 windows in the n = 32 arrangement (codewords 0-7 = high halves 0-7, 8-15 = low 0-7, 16-23 =
+// high 8-15, 24-31 = low 8-15).  At n = 16 the middle two groups of that arrangement hold codewords 16-23 and 8-15,
+// so a k1 lane swaps pairs 4-7 with 8-11 at the end.  k: the lane's rate constants.
+template <int FAM, bool MASKED>
+__device__ __forceinline__ void decode_weights_tiled(const uint32_t (&A)[3], bool k1, const DecodeK &k,
+                                                     uint32_t (&w)[16]) {
+    static_assert(FAM != FAM_PAIR && FAM != FAM_MUL1, "per-tile rates serve the hash-product families");
+    const uint32_t A16[2] = {A[0], A[1]};
+    uint32_t win[16], hl[16], hh[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const uint32_t c16 = lane_codeword<16>(A16, 16 + s);
+        const uint32_t c32 = lane_codeword<32>(A, s < 8 ? 8 + s : 16 + s);
+        win[s] = k1 ? c16 : c32;
+        if constexpr (MASKED) win[s] &= k.wmask | (k.wmask << 16);
+    }
+    phase_fence();
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        hl[s] = hash_step1<FAM, false>(win[s], k);
+        hh[s] = hash_step1<FAM, true>(win[s], k);
+    }
+    phase_fence();
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        hash_step2<FAM, false>(win[s], k, hl[s]);
+        hash_step2<FAM, true>(win[s], k, hh[s]);
+    }
+    phase_fence();
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        hl[s] = hash_halves<FAM>(hl[s], k);
+        hh[s] = hash_halves<FAM>(hh[s], k);
+    }
+    phase_fence();
+    // codeword v of the n = 32 arrangement
+    auto h_of = [&](int v) __attribute__((always_inline)) {
+        return v < 8 ? hh[v] : v < 16 ? hl[v - 8] : v < 24 ? hh[v - 8] : hl[v - 16];
+    };
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+            : "=v"(w[i]) : "v"(h_of(2 * i)));
+    phase_fence();
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+            : "+v"(w[i]) : "v"(h_of(2 * i + 1)));
+    phase_fence();
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t a = w[4 + q], b = w[8 + q];
+        w[4 + q] = k1 ? b : a;
+        w[8 + q] = k1 ? a : b;
+    }
+}
+
+// A lane's rate constants in a per-tile-rate bank: the hash rows differ by rate (mult, mask); the window mask and the
+// fixed families' constants do not.
+__device__ __forceinline__ DecodeK tiled_constants(bool k1, const DecodeK &ka, const DecodeK &kb) {
+    DecodeK k = kb;
+    k.mult = k1 ? ka.mult : kb.mult;
+    k.mask0 = k1 ? ka.mask0 : kb.mask0;
+    return k;
+}
+
 }  // namespace exl3

@@ -323,6 +323,114 @@ class Ragged:
         return r
 
 
+# Per-tile rates: the two tile rates of a per-tile-rate bank (K1 and K2).
+TILED_RATES = (16, 32)
+
+
+def _as_i32(t: torch.Tensor) -> torch.Tensor:
+    """u32 values held in int64 as int32 lanes with the same bits."""
+    return torch.where(t >= 2 ** 31, t - 2 ** 32, t).to(torch.int32)
+
+
+@dataclass
+class TiledProj:
+    """One projection of a per-tile-rate bank (configs[4]'s K1 / K2 tile mix), a layout extension: the reference fixes
+    a rate per tensor (layout.zig:56-62) or per expert group (rate_groups.zig:22-140), while each tile's arithmetic is
+    decodeTile's at that tile's own n (expert_exl3.zig:338-357).
+
+    ``trellis`` is one flat u16 stream; segment (e, tk, s) -- the tiles (tk, 8s .. 8s + 7) of expert e -- lies
+    contiguous from u32 word ``seg_off[e, tk, s]``, tiles in column order, tile o at 16 halfwords when bit o of
+    ``seg_k1[e, tk, s]`` is set, else at 32.  suh [E, in], svh [E, out] as for a uniform bank.
+    """
+
+    trellis: torch.Tensor
+    seg_off: torch.Tensor  # [E, in/16, out/128] int32 (u32 bits)
+    seg_k1: torch.Tensor   # [E, in/16, out/128] uint8
+    suh: torch.Tensor
+    svh: torch.Tensor
+
+    @property
+    def experts(self) -> int:
+        return int(self.seg_off.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.seg_off.shape[1]) * 16
+
+    @property
+    def out_features(self) -> int:
+        return int(self.seg_off.shape[2]) * 128
+
+    def bits_per_weight(self) -> float:
+        """The realised rate: packed bits over weights."""
+        return self.trellis.numel() * 16 / (self.experts * self.in_features * self.out_features)
+
+    @classmethod
+    def pack(cls, codes_a: torch.Tensor, codes_b: torch.Tensor, k1: torch.Tensor, suh: torch.Tensor,
+             svh: torch.Tensor) -> "TiledProj":
+        """Tile (e, tk, tn) takes codes_a[e, tk, tn] (16 halfwords) where k1[e, tk, tn] is set, else codes_b (32);
+        codes are int16 [E, in/16, out/16, n]."""
+        if k1.dim() != 3 or k1.shape[2] % 8:
+            raise BadExl3Shape(f"tile map {tuple(k1.shape)}: [E, in/16, out/16] with out a multiple of 128")
+        e, it, ot = (int(v) for v in k1.shape)
+        if tuple(codes_a.shape) != (e, it, ot, 16) or tuple(codes_b.shape) != (e, it, ot, 32):
+            raise BadExl3Shape(f"codes {tuple(codes_a.shape)} / {tuple(codes_b.shape)} for tile map {(e, it, ot)}")
+        dev = codes_b.device
+        kf = k1.reshape(-1).to(dev)
+        words = torch.where(kf, 8, 16).to(torch.int64)
+        start = torch.cumsum(words, 0) - words
+        total = int(words.sum())
+        if total >= 2 ** 32:
+            raise BadExl3Shape("per-tile-rate trellis past 2^32 words")
+        flat = torch.zeros(2 * total, dtype=torch.int16, device=dev)
+        ia, ib = torch.nonzero(kf).squeeze(1), torch.nonzero(~kf).squeeze(1)
+        flat[(2 * start[ia])[:, None] + torch.arange(16, device=dev)] = codes_a.reshape(-1, 16)[ia]
+        flat[(2 * start[ib])[:, None] + torch.arange(32, device=dev)] = codes_b.reshape(-1, 32)[ib]
+        seg_off = _as_i32(start.reshape(e, it, ot // 8, 8)[..., 0])
+        bits = torch.tensor([1 << o for o in range(8)], dtype=torch.int32, device=dev)
+        seg_k1 = (kf.reshape(e, it, ot // 8, 8).to(torch.int32) * bits).sum(-1).to(torch.uint8)
+        return cls(flat, seg_off.contiguous(), seg_k1.contiguous(), suh, svh)
+
+
+@dataclass
+class Tiled:
+    """A routed layer whose three projections are per-tile-rate (TiledProj)."""
+
+    gate: TiledProj
+    up: TiledProj
+    down: TiledProj
+
+    @property
+    def experts(self) -> int:
+        return self.gate.experts
+
+    @property
+    def hidden(self) -> int:
+        return self.gate.in_features
+
+    @property
+    def inter(self) -> int:
+        return self.gate.out_features
+
+    def check(self) -> None:
+        e, h, i = self.experts, self.hidden, self.inter
+        for nm, p, shape in (("gate", self.gate, (e, h, i)), ("up", self.up, (e, h, i)), ("down", self.down, (e, i, h))):
+            if (p.experts, p.in_features, p.out_features) != shape:
+                raise BadExl3Shape(f"tiled {nm}: {(p.experts, p.in_features, p.out_features)}, expected {shape}")
+
+    def c(self) -> _lib.TiledT:
+        r = _lib.TiledT()
+        for i, p in enumerate((self.gate, self.up, self.down)):
+            r.trellis[i] = p.trellis.data_ptr()
+            r.seg_off[i] = p.seg_off.data_ptr()
+            r.seg_k1[i] = p.seg_k1.data_ptr()
+            r.suh[i] = p.suh.data_ptr()
+            r.svh[i] = p.svh.data_ptr()
+        r.experts = self.experts
+        r.n_a, r.n_b = TILED_RATES
+        return r
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # Plumbing
 
@@ -711,6 +819,75 @@ def moe_ragged_with_shared_bank(x, rb: Ragged, shared_bank: Bank, inds, scores, 
                                             ws.numel(), _stream(x.device))
     if rc == EXL3_DECLINED:
         return moe_ragged(x, rb, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
+    _check(rc)
+    return y.reshape(x.shape)
+
+
+def reconstruct_tiled(tp: TiledProj, expert: int, dec: Decode) -> torch.Tensor:
+    """`reconstructInner` (expert_exl3.zig:416-438) of one expert of a per-tile-rate projection, each tile at its own
+    rate: [in, out] f16 bits as int16, through the routed GEMV's own decoder."""
+    dec.require_table()
+    _need_gpu(tp.trellis, tp.seg_off, tp.seg_k1)
+    if not 0 <= expert < tp.experts:
+        raise BadExl3Shape(f"expert {expert} of {tp.experts}")
+    out = torch.empty(tp.in_features, tp.out_features, dtype=torch.int16, device=tp.trellis.device)
+    _check(_lib.load().exl3_reconstruct_tiled(tp.trellis.data_ptr(), tp.seg_off.data_ptr(), tp.seg_k1.data_ptr(),
+                                              int(expert), tp.in_features, tp.out_features, TILED_RATES[0],
+                                              TILED_RATES[1], dec.c(), out.data_ptr(), _stream(out.device)))
+    return out
+
+
+def moe_tiled(x, tb: Tiled, inds, scores, dec: Decode, shared=None, limit: int = 0) -> torch.Tensor:
+    """The routed SwiGLU chain (`moeRagged`, root.zig:582-644) over a per-tile-rate bank; `shared` and `limit` as
+    for moe_ragged."""
+    if limit < 0 or limit > 128:
+        raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128 (0 = none)")
+    dec.require_table()
+    tb.check()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    if hidden != tb.hidden:
+        raise BadExl3Shape(f"moe_tiled: hidden {hidden} vs bank {tb.hidden}")
+    _need_gpu(x2, inds2, sc2, shared, tb.gate.trellis)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    if shared is not None:
+        shared = shared.reshape(rows, hidden).contiguous()
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, tb.inter))
+    ct = tb.c()
+    _check(L.exl3_moe_tiled(x2.data_ptr(), _dt(x2, "x"), rows, hidden, tb.inter, ctypes.byref(ct), inds2.data_ptr(),
+                            sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(limit),
+                            None if shared is None else shared.data_ptr(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
+                            ws.numel(), _stream(x.device)))
+    return y.reshape(x.shape)
+
+
+def moe_tiled_with_shared_bank(x, tb: Tiled, shared_bank: Bank, inds, scores, dec: Decode,
+                               limit: int = 0) -> torch.Tensor:
+    """moe_tiled with its shared expert (a uniform one-expert bank) in the same launches, as moe_with_shared_bank;
+    where the fused form declines, the shared expert runs as a one-expert chain and joins through `shared`."""
+    if limit < 0 or limit > 128:
+        raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128 (0 = none)")
+    dec.require_table()
+    tb.check()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    if hidden != tb.hidden:
+        raise BadExl3Shape(f"moe_tiled_with_shared_bank: hidden {hidden} vs bank {tb.hidden}")
+    if _bank_shape(shared_bank, hidden) != (1, tb.inter):
+        raise BadExl3Shape("moe_tiled_with_shared_bank: the shared bank must be one expert of the routed inter")
+    _need_gpu(x2, inds2, sc2, tb.gate.trellis)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_with_shared_bank_workspace_size(rows, topk, hidden, tb.inter))
+    ct = tb.c()
+    cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
+    rc = L.exl3_moe_tiled_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, tb.inter, ctypes.byref(ct),
+                                           ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"),
+                                           topk, dec.c(), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
+                                           ws.numel(), _stream(x.device))
+    if rc == EXL3_DECLINED:
+        return moe_tiled(x, tb, inds, scores, dec, _shared_rows(x, shared_bank, dec, limit), limit)
     _check(rc)
     return y.reshape(x.shape)
 

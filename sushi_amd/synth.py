@@ -8,6 +8,7 @@ same bytes.
   codes  : uniform u16, 4 per 64-bit draw (little-endian halfwords)
   suh/svh: sign (+-1, from bit 63) x U(0.5, 1.5), rounded to f16
   x      : N(0, 1) by Box-Muller over two uniform draws, rounded to f16
+  k1 map : a tile is K1 where its U[0, 1) draw is below p_k1 (configs[4]: 0.25), else K2
 """
 from __future__ import annotations
 
@@ -105,3 +106,34 @@ def bank(seed: int, name: str, experts: int, hidden: int, inter: int, n, device=
     return Bank(proj(seed, name + ".gate", experts, hidden, inter, ng, device, norm),
                 proj(seed, name + ".up", experts, hidden, inter, nu, device, norm),
                 proj(seed, name + ".down", experts, inter, hidden, nd, device, norm))
+
+
+def tile_map(seed: int, name: str, shape, p_k1: float = 0.25, device="cpu") -> torch.Tensor:
+    """configs[4]'s seeded per-tile rate map: each tile K1 (True) with probability p_k1, else K2."""
+    return (uniform01(seed_of(seed, name), math.prod(shape)) < p_k1).reshape(shape).to(device)
+
+
+def tiled_proj(seed: int, name: str, experts: int, in_f: int, out_f: int, p_k1: float = 0.25, device="cpu",
+               norm: bool = False):
+    """A per-tile-rate projection (exl3.TiledProj): the tile map from `name`.k1; every tile's codes are the first n of
+    a 32-halfword uniform draw (`name`.trellis), so a K1 tile holds the first 16 halfwords of its K2 draw."""
+    from .exl3 import TiledProj
+
+    shape = (experts, in_f // 16, out_f // 16)
+    k1 = tile_map(seed, name + ".k1", shape, p_k1, device)
+    cb = codes(seed, name + ".trellis", shape + (32,), device)
+    svh = sign_scale(seed, name + ".svh", (experts, out_f))
+    if norm:
+        svh = (svh.double() / math.sqrt(in_f)).to(torch.float16)
+    tp = TiledProj.pack(cb[..., :16], cb, k1, sign_scale(seed, name + ".suh", (experts, in_f), device), svh.to(device))
+    return tp
+
+
+def tiled_bank(seed: int, name: str, experts: int, hidden: int, inter: int, p_k1: float = 0.25, device="cpu",
+               norm: bool = False):
+    """gate / up / down as per-tile-rate projections (exl3.Tiled)."""
+    from .exl3 import Tiled
+
+    return Tiled(tiled_proj(seed, name + ".gate", experts, hidden, inter, p_k1, device, norm),
+                 tiled_proj(seed, name + ".up", experts, hidden, inter, p_k1, device, norm),
+                 tiled_proj(seed, name + ".down", experts, inter, hidden, p_k1, device, norm))

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_host_side_refusals():
     lib = L.load()
-    assert lib.exl3_abi_version() == 3
+    assert lib.exl3_abi_version() == 4
     d = L.DecodeT(1, 16, -1)
     # bad shape: in not a multiple of 128 -> refused before any launch (null pointers never touched)
     assert lib.exl3_linear(None, 0, 1, 100, 128, None, 64, None, None, d, None, 0, None, 0, None) == -1
@@ -77,6 +77,38 @@ def test_moe_refusals():
     assert lib.exl3_moe_with_gated_shared(*gargs) == -1
     assert "gate" in L.last_error()
     assert lib.exl3_route_topk(None, 1, 2000, 8, None, None, None) == -1
+
+
+def test_tiled_refusals():
+    """Per-tile-rate banks: only the K1 / K2 pair, tables that hold both rates, the hash-product families, a 4-byte
+    aligned mask table; every refusal before any launch (the fake pointers are never dereferenced)."""
+    lib = L.load()
+    fake = ctypes.c_void_p(0x1000)
+    tb = L.TiledT()
+    for i in range(3):
+        tb.trellis[i] = tb.seg_off[i] = tb.seg_k1[i] = tb.suh[i] = tb.svh[i] = fake.value
+    tb.experts, tb.n_a, tb.n_b = 4, 16, 32
+
+    def moe(dec, bank=tb):
+        return lib.exl3_moe_tiled(None, 0, 0, 128, 128, ctypes.byref(bank), None, None, 2, 8, dec, 0, None, None, 0,
+                                  None, 0, None)
+
+    assert moe(L.DecodeT(2, 15, 1)) == 0  # spec1-w15 has rows at 16 and 32; zero rows: nothing to launch
+    assert moe(L.DecodeT(1, 16, -1)) == 0  # MCG
+    assert moe(L.DecodeT(4, 15, 3)) == -10  # std1 has no row at n = 16
+    assert moe(L.DecodeT(2, 16, 2)) == -10  # nor spec1-w16
+    assert moe(L.DecodeT(3, 16, 0)) == -10  # PAIR1 has no pair row at 16
+    assert moe(L.DecodeT(0, 16, -1)) == -12  # MUL1: not a hash-product family
+    tb.n_b = 48
+    assert moe(L.DecodeT(1, 16, -1)) == -1 and "16 / 32" in L.last_error()
+    tb.n_b = 32
+    tb.seg_k1[1] = 0x1002
+    assert moe(L.DecodeT(1, 16, -1)) == -1 and "aligned" in L.last_error()
+    tb.seg_k1[1] = fake.value
+    tb.suh[2] = None
+    assert moe(L.DecodeT(1, 16, -1)) == -1 and "null" in L.last_error()
+    assert lib.exl3_reconstruct_tiled(fake, fake, fake, 0, 128, 100, 16, 32, L.DecodeT(1, 16, -1), fake, None) == -1
+    assert lib.exl3_reconstruct_tiled(fake, fake, fake, 0, 128, 128, 16, 24, L.DecodeT(1, 16, -1), fake, None) == -1
 
 
 def test_workspace_sizes_are_aligned_and_monotone():

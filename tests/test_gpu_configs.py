@@ -3,7 +3,8 @@
 configs[3] (C4): 256 routed experts + 1 shared, hidden 2048, inter 768, K2 MCG, top-8 over N(0,1) logits, batch 1 / 8 /
 32 -- the shapes bench.py times, through the same calls (moe_with_shared_bank; and moe alone).  configs[4] (C5) in the
 reference's rate-group form: 64 experts at K1 and 192 at K2 (1.75 bpw), SPEC1 with the spec1-w15 table, hidden 4096,
-inter 2048, top-8, batch 64 on the sorted arm, plus a K4 shared expert.  The oracle is moeSwigluHost
+inter 2048, top-8, batch 64 on the sorted arm, plus a K4 shared expert; and as stated, a seeded per-tile K1 / K2 mix in
+every expert (exl3.Tiled).  The oracle is moeSwigluHost
 (src/exl3/expert_exl3_kernels.zig:3059-3114) over every row on the host's cores (ox_moe_swiglu_rows).  The banks'
 svh carry 1/sqrt(in) (synth norm), so f16 outputs stay far from overflow.
 """
@@ -92,6 +93,32 @@ def test_c5_rate_group_layer_batch_64(dev):
         banks.append((t, np.concatenate([_np(q1)[1], _np(q2)[1]]), np.concatenate([_np(q1)[2], _np(q2)[2]])))
     rates = [np.array([16] * E1 + [32] * E2)] * 3
     routed = O.moe_swiglu_rows(xf, *banks, oi, osc, hidden, inter, rates, odec, threads=THREADS)
+    shared = O.moe_swiglu_rows(xf, *[_np(q) for q in (sh.gate, sh.up, sh.down)], np.zeros((batch, 1)),
+                               np.ones((batch, 1)), hidden, inter, (64, 64, 64), odec, threads=THREADS)
+    want = routed.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
+    assert max_abs_rel(y, want) < BAR
+
+
+def test_c5_per_tile_layer_batch_64(dev):
+    """configs[4] as stated: every expert at a seeded per-tile K1 / K2 mix (25 % K1), SPEC1 (spec1-w15), hidden 4096,
+    inter 2048, top-8 over 256 experts, batch 64 on the sorted arm, with a K4 shared expert in the same launches."""
+    print("[c5] per-tile batch=64", flush=True)
+    E, hidden, inter, k, batch = 256, 4096, 2048, 8, 64
+    dec, odec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1), O.decode(O.CB_SPEC1, 15, 1)
+    tb = synth.tiled_bank(5, "c5t", E, hidden, inter, 0.25, device=dev, norm=True)
+    sh = synth.bank(5, "c5.shared", 1, hidden, inter, 64, norm=True)
+    bpw = sum(p.bits_per_weight() for p in (tb.gate, tb.up, tb.down)) / 3
+    assert abs(bpw - 1.75) < 0.01, bpw
+    x = synth.normal(5, "c5.t64", (batch, hidden))
+    logits = synth.normal(5, "c5t.tl64", (batch, E), dtype=torch.float32)
+    inds, scores = exl3.moe_routing_chain(logits.to(dev), k)
+    oi, osc = O.route_topk(logits.numpy(), k)
+    y = exl3.moe_tiled_with_shared_bank(x.to(dev), tb, _to(sh, dev), inds, scores, dec).float().cpu().numpy()
+    arrs = [(p.trellis.cpu().numpy().view(np.uint16), p.seg_off.cpu().numpy().view(np.uint32), p.seg_k1.cpu().numpy(),
+             p.suh.cpu().numpy().view(np.uint16), p.svh.cpu().numpy().view(np.uint16)) for p in (tb.gate, tb.up, tb.down)]
+    del tb
+    xf = x.float().numpy()
+    routed = O.moe_swiglu_tiled_rows(xf, arrs, oi, osc, hidden, inter, 16, 32, odec, threads=THREADS)
     shared = O.moe_swiglu_rows(xf, *[_np(q) for q in (sh.gate, sh.up, sh.down)], np.zeros((batch, 1)),
                                np.ones((batch, 1)), hidden, inter, (64, 64, 64), odec, threads=THREADS)
     want = routed.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
