@@ -708,9 +708,20 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
         c.rows = min(RT, a.sh_rows - c.xg);
         c.slot0 = a.sh_from + c.xg;
     } else {
-        c.suh = p1 ? a.suh[1] : suh0;
+        // Projection 0's suh and trellis are preloaded arguments, so a dense launch's first loads issue without an
+        // argument load ahead of them.  Projection 1 (grid z = 1) reads its pointers from `a` under a real branch:
+        // the index is opaque to the compiler, so those loads cannot be hoisted into a select, and the empty asm
+        // uses them inside the branch, so their wait stays there too (a wait for any scalar load waits for all).
+        int pz = c.proj;
+        asm volatile("" : "+s"(pz));
+        c.suh = suh0;
+        trellis = tr0;
+        if (pz != 0) {
+            c.suh = a.suh[pz];
+            trellis = a.trellis[pz];
+            asm volatile("" ::"s"(c.suh), "s"(trellis));
+        }
         c.svh = p1 ? a.svh[1] : a.svh[0];
-        trellis = p1 ? a.trellis[1] : tr0;
         c.xg = 0;
         c.slot0 = 0;
         if constexpr (WIN) {  // sorted MoE arm: this group is an expert window (windows past the count do nothing)
