@@ -240,6 +240,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     g.y = y;
     g.y_dtype = y_dtype;
     g.groups = groups;
+    g.arm = knob(EXL3_KNOB_GEMM_ARM, 0);
     return launched(run_gemm(fam, g, stream), "exl3_linear (gemm)");
 }
 

@@ -442,6 +442,210 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
                        });
 }
 
+// ---- the ping-pong GEMM (hash-product families at the lane-reader rates)
+//
+// A workgroup of 8 waves owns an MT-row x 128-column output tile (MT = 256 or 512; one Hadamard block wide, so the
+// FWHT + svh finish runs in its epilogue) over all of k, in k-steps of 64 (four trellis k-tiles).  Every wave owns
+// RW = MT / 8 rows x all 128 columns (RW / 16 x 8 v_mfma_f32_16x16x32_f16 tiles) with its A fragments in registers, so
+// each prepared row is loaded once per workgroup, and every wave also decodes: waves r and r + 4 decode the two column
+// halves of k-tile row r of step s + 2 (the GEMV's lane decoder, half a chunk each) into a triple-buffered LDS slab.
+// Waves r and r + 4 share a SIMD: wave r runs its step's MFMAs first and then decodes, wave r + 4 decodes first, so
+// on every SIMD one wave feeds the matrix core while the other decodes on the VALU (a decode wave beside MFMA waves
+// leaves their rate untouched).  One barrier per step: the slab read in step s was written in step s - 2 and the one
+// written in step s was last read in step s - 1, each on the other side of a barrier.  The trellis words are loaded
+// a step before their decode, the A fragments of step s + 1 as soon as step s's MFMAs of that half have issued.
+// Every weight is decoded once per MT rows (twice per 1024 rows at MT = 512, against four times for the 256-row tile).
+constexpr int G5_WAVES = 8;
+constexpr int G5_THREADS = 64 * G5_WAVES;
+constexpr int G5_EP = 129;                                                  // epilogue staging pitch (floats)
+constexpr int G5_SLAB = 128 * G2_BP;                                        // halves per slab
+constexpr int G5_LDS = (3 * G5_SLAB * 2 > G5_WAVES * 16 * G5_EP * 4) ? 3 * G5_SLAB * 2 : G5_WAVES * 16 * G5_EP * 4;
+
+template <int FAM, int N, int MT>
+__global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
+    static_assert(FAM != FAM_PAIR && FAM != FAM_MUL1, "hash-product families");
+    constexpr int RW = MT / G5_WAVES;  // rows per wave
+    constexpr int RB = RW / 16;        // row blocks per wave
+    constexpr int AW = LaneBits<N>::AW;
+    const int IT = a.in >> 4, OT = a.out >> 4;
+    const int nog = a.out / 128, nm = (a.rows + MT - 1) / MT;
+    const int L = blockIdx.x;
+    int og, mt;
+    if (nm <= 8 && 8 % nm == 0 && nog % (8 / nm) == 0) {  // a row tile's workgroups share an XCD (its A rows in one L2)
+        const int xcd = L & 7, per = 8 / nm;
+        mt = xcd / per;
+        og = (L >> 3) * per + xcd % per;
+    } else {
+        og = L % nog;
+        mt = L / nog;
+    }
+    const int g = blockIdx.z;
+    __shared__ __align__(16) uint8_t lds[G5_LDS];
+    uint16_t *slabs = reinterpret_cast<uint16_t *>(lds);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, h = lane >> 4;
+    const int RT = (a.rows + 15) / 16;
+    const int nks = IT / 4;
+    const DecodeK k = a.k;
+    const bool masked = k.wmask != 0xFFFFu;
+
+    // ---- decode role: column half H of k-tile row r of each step
+    const int r = wave & 3, H = wave >> 2;
+    const int o = lane >> 3, j = lane & 7;
+    const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8) * N;
+    const uint32_t lane_words = (uint32_t)(o * N) >> 1;
+    const size_t kstep = (size_t)4 * OT * N;  // halves from one k-step's row r to the next
+    auto load_words = [&](int s, uint32_t (&W)[AW]) __attribute__((always_inline)) {
+        load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(s, nks - 1) * kstep), lane_words, j,
+                             W);
+    };
+    // the slab column this lane writes (rows r * 16 .. + 15 of the step's 64 k)
+    const int col = o * 16 + j + 8 * H;
+    auto decode_into = [&](int s, const uint32_t (&W)[AW]) __attribute__((always_inline)) {
+        uint32_t w[8];
+        if (H) {
+            if (masked) decode_weights_half<FAM, N, true, 1>(W, k, w);
+            else decode_weights_half<FAM, N, false, 1>(W, k, w);
+        } else {
+            if (masked) decode_weights_half<FAM, N, true, 0>(W, k, w);
+            else decode_weights_half<FAM, N, false, 0>(W, k, w);
+        }
+        if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) w[i] = scale_h2_4096(w[i]);
+        }
+        uint16_t *dst = slabs + (size_t)(s % 3) * G5_SLAB + col * G2_BP + r * 16;
+        *reinterpret_cast<uint4 *>(dst) = uint4{w[0], w[2], w[4], w[6]};
+        *reinterpret_cast<uint4 *>(dst + 8) = uint4{w[1], w[3], w[5], w[7]};
+    };
+
+    // ---- MFMA role: rows m0 .. m0 + RW - 1 of the tile, all 128 columns
+    const int m0 = mt * MT + wave * RW;
+    // fragment (row tile rt, 32-k block kk) of group g: bytes ((rt in/32 + kk) 1024 + 16 lane) of the group's
+    // prepared rows, read through a buffer resource (uniform base and offset in scalar registers, one lane offset)
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const size_t xp_group = (size_t)RT * (size_t)(a.in / 32) * 512;  // halves per group
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(a.xp + (size_t)g * xp_group), (short)0, (int)(xp_group * 2), 0x00020000);
+    const uint32_t a_lane = (uint32_t)lane * 16u;
+    f4_t acc[RB][8];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
+    uint4 A[2][RB];
+    auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
+        const int kk = min(s, nks - 1) * 2 + kb;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            const int rt = min(m0 / 16 + rb, RT - 1);
+            const int soff = (rt * (a.in / 32) + kk) * 1024;
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, a_lane, soff, 0);
+            A[kb][rb] = uint4{v.x, v.y, v.z, v.w};
+        }
+    };
+    // B fragment f = kb * 8 + cb of step s; the first PD of a step are read before it starts (at the end of the
+    // wave's previous decode phase), the rest PD fragments ahead of their MFMAs
+    constexpr int PD = 3;
+    auto frag = [&](int s, int f) __attribute__((always_inline)) {
+        const uint16_t *bp = slabs + (size_t)(s % 3) * G5_SLAB + c * G2_BP + 8 * h;
+        return *reinterpret_cast<const uint4 *>(bp + (f & 7) * 16 * G2_BP + (f >> 3) * 32);
+    };
+    uint4 bpre[PD];
+    auto read_first = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int f = 0; f < PD; f++) bpre[f] = frag(s, f);
+    };
+    auto mfma_phase = [&](int s) __attribute__((always_inline)) {
+        uint4 bq[16];
+#pragma unroll
+        for (int f = 0; f < PD; f++) bq[f] = bpre[f];
+#pragma unroll
+        for (int f = 0; f < 16; f++) {
+            if (f + PD < 16) bq[f + PD] = frag(s, f + PD);
+            const int kb = f >> 3, cb = f & 7;
+            const h8_t B8 = __builtin_bit_cast(h8_t, bq[f]);
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, A[kb][rb]), B8,
+                                                                     acc[rb][cb], 0, 0, 0);
+            if (f == 7) load_a(s + 1, 0);
+            if (f == 15) load_a(s + 1, 1);
+            if (f & 1) __builtin_amdgcn_sched_barrier(0);  // keep the B reads a few fragments ahead, not all at once
+        }
+    };
+
+    // ---- the step loop.  Every wave runs the same order -- step s's MFMAs, then a decode -- and waves differ only in
+    // where their barrier falls: waves 0-3 (H = 0) decode step s + 2 before barrier s, waves 4-7 (H = 1) decode step
+    // s + 3 after it.  So between two barriers a SIMD's H = 0 wave runs its MFMAs and then decodes while its H = 1
+    // wave decodes and then runs its MFMAs.  Slab t % 3 is read in step t after barrier t - 1; its H = 0 half is
+    // written before barrier t - 2, its H = 1 half after barrier t - 3; both after the reads of step t - 3, which end
+    // before barrier t - 3.  The words of step s + 2 + H sit in ring slot s % 3, loaded in the step before.
+    uint32_t W0[AW], W1[AW], W2[AW];
+    load_a(0, 0);
+    load_a(0, 1);
+    {
+        uint32_t P0[AW], P1[AW];
+        load_words(0, P0);
+        load_words(1, P1);
+        load_words(2, W2);
+        load_words(2 + H, W0);
+        decode_into(0, P0);
+        decode_into(1, P1);
+        if (H) decode_into(2, W2);
+    }
+    __syncthreads();
+    read_first(0);
+    auto step = [&](int s, const uint32_t (&Wd)[AW], uint32_t (&Wl)[AW]) __attribute__((always_inline)) {
+        mfma_phase(s);
+        __builtin_amdgcn_sched_barrier(0);
+        if (H) __syncthreads();
+        if (s + 2 + H < nks) decode_into(s + 2 + H, Wd);
+        if (s + 3 + H < nks) load_words(s + 3 + H, Wl);
+        if (s + 1 < nks) read_first(s + 1);  // slab s + 1 was complete before barrier s - 1
+        __builtin_amdgcn_sched_barrier(0);
+        if (!H) __syncthreads();
+    };
+    for (int s = 0; s < nks; s += 3) {
+        step(s, W0, W1);
+        if (s + 1 < nks) step(s + 1, W1, W2);
+        if (s + 2 < nks) step(s + 2, W2, W0);
+    }
+    __syncthreads();  // the H = 1 waves' last decode (none: s + 3 >= nks) and every slab read are behind this
+
+    // ---- epilogue: per 16-row block, the wave stages its 16 x 128 outputs in its own LDS region (the last barrier
+    // has retired every slab read), then finishes each row: FWHT-128, * svh, store
+    float *ep = reinterpret_cast<float *>(lds) + wave * 16 * G5_EP;
+    const size_t sv = (size_t)g * a.out + (size_t)og * 128;
+    const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) ep[(4 * h + i) * G5_EP + cb * 16 + c] = acc[rb][cb][i];
+        for (int rr = 0; rr < 16; rr++) {
+            const int m = m0 + rb * 16 + rr;
+            if (m >= a.rows) break;
+            float v0 = ep[rr * G5_EP + lane], v1 = ep[rr * G5_EP + lane + 64];
+            fwht128_wave(v0, v1, lane);
+            const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128;
+            const float y0 = v0 * HAD_SCALE * s0, y1 = v1 * HAD_SCALE * s1;
+            if (a.y_dtype == DT_F16) {
+                store_act<DT_F16>(a.y, yo + lane, y0);
+                store_act<DT_F16>(a.y, yo + lane + 64, y1);
+            } else if (a.y_dtype == DT_BF16) {
+                store_act<DT_BF16>(a.y, yo + lane, y0);
+                store_act<DT_BF16>(a.y, yo + lane + 64, y1);
+            } else {
+                store_act<DT_F32>(a.y, yo + lane, y0);
+                store_act<DT_F32>(a.y, yo + lane + 64, y1);
+            }
+        }
+    }
+}
+
 // ---- the routed GEMM arm: workgroup (og, window w, projection p) runs the tile of window w's rows against its
 // expert's bank and writes the raw inner products to planes[p][slot][out] (the mid / the reduce applies the output
 // transform).  Windows past the count exit before any barrier.
@@ -608,6 +812,27 @@ static hipError_t launch_gemm_lane_n(const GemmArgs &a, hipStream_t s) {
                                                       (unsigned)a.groups), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // The ping-pong body once its 512-row tiles still give most CUs a workgroup (measured at C3's 4096 x 14336: 768 to
+    // 4096 rows 13-24% faster than the 256-row decode-wave tile; at 512 rows, 112 workgroups, 18% slower).
+    int arm = a.arm;
+    if (arm == 0) {
+        const long wg5 = (long)((a.rows + 511) / 512) * (a.out / 128) * a.groups;
+        arm = (a.rows > 512 && wg5 >= 192) ? 5 : 4;
+    }
+    if constexpr (FAM == FAM_PAIR || FAM == FAM_MUL1) arm = 4;  // the ping-pong body serves the hash-product families
+    // n = 40's unaligned lane reader does not fit the 512-row tile's registers (it would spill): the 256-row one
+    if constexpr (N == 40) arm = arm == 5 ? (a.arm ? 6 : 4) : arm;
+    if (arm == 5 || arm == 6) {
+        const int mt = arm == 5 ? 512 : 256;
+        dim3 grid((unsigned)((a.out / 128) * ((a.rows + mt - 1) / mt)), 1, (unsigned)a.groups);
+        if constexpr (FAM != FAM_PAIR && FAM != FAM_MUL1) {
+            if constexpr (N != 40) {
+                if (arm == 5) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 512>), grid, dim3(G5_THREADS), 0, s, a);
+            }
+            if (arm == 6) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 256>), grid, dim3(G5_THREADS), 0, s, a);
+        }
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((a.out / 128) * ((a.rows + G2_MT - 1) / G2_MT)), 1, (unsigned)a.groups);
     hipLaunchKernelGGL((gemm4_kernel<FAM, N>), grid, dim3(G4_THREADS), 0, s, a);
     return hipGetLastError();

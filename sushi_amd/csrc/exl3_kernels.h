@@ -228,6 +228,7 @@ struct GemmArgs {
     void *y;
     int y_dtype;
     int groups;
+    int arm;          // GEMM body: 0 = the row-count policy, 4 = 256-row tile (decode waves), 5 / 6 = ping-pong 512 / 256
 };
 hipError_t run_gemm(int fam, const GemmArgs &a, hipStream_t s);
 

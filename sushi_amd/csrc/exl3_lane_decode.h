@@ -119,6 +119,52 @@ __device__ __forceinline__ void decode_weights(const uint32_t (&A)[LaneBits<N>::
     }
 }
 
+// Half of the lane's chunk, for the hash-product families (MCG, 3INST, hash rows): the 8 weight pairs of column
+// j + 8 H (pairs i with (i & 2) == 2 H, in the order 2H, 2H+1, 2H+4, 2H+5, ..., 2H+13), so two waves can share one
+// chunk's decode.  Output pair q holds rows 2 (q >> 1) + 8 (q & 1) + {0, 1} of that column; unscaled.  The phases run
+// over two groups of 8 codewords, so few registers are live beside a caller's accumulators.
+template <int FAM, int N, bool MASKED, int H>
+__device__ __forceinline__ void decode_weights_half(const uint32_t (&A)[LaneBits<N>::AW], const DecodeK &k,
+                                                    uint32_t (&w)[8]) {
+    static_assert(FAM != FAM_PAIR && FAM != FAM_MUL1, "the half decoder serves the hash-product families");
+    using P = Pairing<N>;
+    // codeword u (0..15) of this half: pair 2H + (u >> 1 & 1) + 4 (u >> 2), element u & 1
+    auto cw_of = [](int u) constexpr { return 2 * (2 * H + ((u >> 1) & 1) + 4 * (u >> 2)) + (u & 1); };
+#pragma unroll
+    for (int gq = 0; gq < 2; gq++) {
+        uint32_t win[8], h[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            win[i] = lane_codeword<N>(A, P::win(cw_of(8 * gq + i)));
+            if constexpr (MASKED) win[i] &= k.wmask | (k.wmask << 16);
+        }
+        phase_fence();
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            h[i] = P::hi(cw_of(8 * gq + i)) ? hash_step1<FAM, true>(win[i], k) : hash_step1<FAM, false>(win[i], k);
+        phase_fence();
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (P::hi(cw_of(8 * gq + i))) hash_step2<FAM, true>(win[i], k, h[i]);
+            else hash_step2<FAM, false>(win[i], k, h[i]);
+        }
+        phase_fence();
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = hash_halves<FAM>(h[i], k);
+        phase_fence();
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+                : "=v"(w[4 * gq + q]) : "v"(h[2 * q]));
+        phase_fence();
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+                : "+v"(w[4 * gq + q]) : "v"(h[2 * q + 1]));
+        phase_fence();
+    }
+}
+
 // ------------------------------------------------------------------------------------------------------------
 // Per-tile rates (configs[4]'s seeded K1 / K2 tile mix, a layout extension: the reference fixes a rate per tensor or
 // per expert group, src/exl3/layout.zig:56-62, and decodes every tile at its own n with decodeTile,

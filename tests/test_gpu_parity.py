@@ -151,6 +151,59 @@ def test_c3_prefill_shapes(dev, rows, out_f):
     _hold(d.inner(dec), d, odec, seed=rows, mutate=out_f == 1024, what=f"c3 M={rows} out={out_f}")
 
 
+# ---- ping-pong GEMM body (gemm_arm 5 / 6: 512- / 256-row tiles, every wave decoding half a k-tile row and running
+# the MFMAs of its own rows), forced at small shapes; the row-count policy takes arm 5 past 512 rows
+
+
+@pytest.mark.parametrize("arm", [5, 6])
+@pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
+def test_gemm_pingpong_rates(dev, arm, n):
+    d = Dense(dev, 700 + n, 300, 1024, 512, n)
+    dec, odec = DECODES["3inst"]
+    with exl3.arm_overrides(gemm_arm=arm):
+        got = d.inner(dec)
+    _hold(got, d, odec, seed=n, what=f"pingpong arm={arm} n={n}")
+
+
+@pytest.mark.parametrize("arm", [5, 6])
+@pytest.mark.parametrize("rows", [17, 257, 700])
+def test_gemm_pingpong_row_tails(dev, arm, rows):
+    """Row counts that leave partial 16-row blocks, partial waves and a partial last tile (k spans of 2, 6 and 10
+    steps: the three-slot words ring ends on every phase)."""
+    in_f = {17: 128, 257: 384, 700: 640}[rows]
+    d = Dense(dev, 710 + rows, rows, in_f, 256, 48)
+    dec, odec = DECODES["3inst"]
+    with exl3.arm_overrides(gemm_arm=arm):
+        got = d.inner(dec)
+    _hold(got, d, odec, seed=rows, what=f"pingpong arm={arm} rows={rows} in={in_f}")
+
+
+@pytest.mark.parametrize("label", ["mcg", "spec1", "std1", "mcg_w12", "pair1", "mul1"])
+def test_gemm_pingpong_codebooks(dev, label):
+    """Hash-product families take the ping-pong body; PAIR1 and MUL1 fall back to the decode-wave tile."""
+    d = Dense(dev, 720, 300, 512, 256, 48)
+    dec, odec = DECODES[label]
+    with exl3.arm_overrides(gemm_arm=5):
+        got = d.inner(dec)
+    _hold(got, d, odec, seed=7, what=f"pingpong {label}")
+
+
+def test_gemm_pingpong_equals_decode_wave_tile_at_c3(dev):
+    """At C3's shape (4096 x 14336, K3, 3INST, 1024 rows) the two GEMM bodies accumulate every output in the same k
+    order, so their outputs are identical bit for bit."""
+    torch.manual_seed(0)
+    p = synth.proj(3, "c3eq", 1, 4096, 14336, 48)
+    pd = exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev))
+    x = synth.normal(3, "c3eq.x", (1024, 4096)).to(dev)
+    dec = DECODES["3inst"][0]
+    outs = {}
+    for arm in (4, 5, 6):
+        with exl3.arm_overrides(gemm_arm=arm):
+            outs[arm] = exl3.linear(x, pd, dec, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[4], outs[5]) and torch.equal(outs[4], outs[6])
+
+
 # ---- routed experts -------------------------------------------------------------------------------------------------
 #
 # The routed layer sums its slots with per-expert svh, which no single inverse undoes; so these cases route every
