@@ -188,6 +188,29 @@ def test_gemm_pingpong_codebooks(dev, label):
     _hold(got, d, odec, seed=7, what=f"pingpong {label}")
 
 
+@pytest.mark.parametrize("label", ["mcg", "3inst", "spec1", "std1", "mcg_w12"])
+@pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
+def test_gemm_pingpong_half_decoder_is_bit_exact(dev, label, n):
+    """The ping-pong body decodes through the half-chunk reader; the decode-wave tile through the lane reader that
+    test_gpu_decode.py pins bit for bit.  Both accumulate every output in the same k order, so equal outputs on a
+    matrix of 32 x 32 tiles show every weight of the half reader equal to the lane reader's."""
+    table = {"spec1": 1, "std1": 3}.get(label)
+    if table is not None and O.table_row(table, n) is None:
+        pytest.skip(f"{label} has no row at n={n}")
+    d = Dense(dev, 730 + n, 300, 512, 512, n)
+    dec = DECODES[label][0]
+    outs = {}
+    for arm in (4, 6):
+        with exl3.arm_overrides(gemm_arm=arm):
+            outs[arm] = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32)
+    if n != 40:
+        with exl3.arm_overrides(gemm_arm=5):
+            outs[5] = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for arm, y in outs.items():
+        assert torch.equal(y, outs[4]), f"arm {arm} differs from the decode-wave tile ({label} n={n})"
+
+
 def test_gemm_pingpong_equals_decode_wave_tile_at_c3(dev):
     """At C3's shape (4096 x 14336, K3, 3INST, 1024 rows) the two GEMM bodies accumulate every output in the same k
     order, so their outputs are identical bit for bit."""
