@@ -274,25 +274,52 @@ __device__ __forceinline__ uint32_t codeword_at(const uint32_t *__restrict__ wor
 // Wave64 128-point Walsh-Hadamard: lane l holds v0 = x[l], v1 = x[l + 64].  Unnormalised (the caller scales by
 // 1/sqrt(128)).  Matches hadamard128 (expert_exl3.zig:400-414) up to f32 summation order.
 
-// The value of lane (lane ^ H): DPP quad permutes for H = 1, 2 (plain VALU), the LDS crossbar's swizzle (bitmask
-// mode, and 0x1F / xor H, within each 32-lane half) for H = 4..16, one bpermute for H = 32.
+// Every lane exchange stays in the VALU (no LDS round trip): DPP for H = 1..8, the gfx950 row swaps for 16 and 32.
+// A butterfly stage gives lane l the sum x[l] + x[l ^ H] where bit H of l is clear and x[l ^ H] - x[l] where it is
+// set, each one rounding, as fmaf(other, +-1, first) with the lane's sign.
+
+// +1.0 where bit H of the lane is clear, -1.0 where it is set.
 template <int H>
-__device__ __forceinline__ float xor_lane(float v, int lane) {
+__device__ __forceinline__ float lane_sign(int lane) {
+    constexpr int SH = H == 1 ? 31 : H == 2 ? 30 : H == 4 ? 29 : H == 8 ? 28 : H == 16 ? 27 : 26;
+    return __builtin_bit_cast(float, 0x3F800000u | (((uint32_t)lane & H) << SH));
+}
+
+// The value of lane (lane ^ H) within a 16-lane row: quad permutes for H = 1, 2, a half-row mirror then a quad
+// reversal for 4 (7 - (l ^ 3) = l ^ 4 within 8 lanes), a row rotate by 8 for 8.
+template <int H>
+__device__ __forceinline__ float xor_lane_row(float v) {
     const int b = __builtin_bit_cast(int, v);
     int r;
     if constexpr (H == 1) r = __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
     else if constexpr (H == 2) r = __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-    else if constexpr (H <= 16) r = __builtin_amdgcn_ds_swizzle(b, 0x1F | (H << 10));
-    else r = __builtin_amdgcn_ds_bpermute((lane ^ H) << 2, b);
+    else if constexpr (H == 4)
+        r = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(b, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false);
+    else r = __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false);                        // row_ror:8
     return __builtin_bit_cast(float, r);
 }
 
 template <int H>
-__device__ __forceinline__ void fwht_stage(float &v0, float &v1, int lane) {
-    const float p0 = xor_lane<H>(v0, lane), p1 = xor_lane<H>(v1, lane);
-    const bool up = (lane & H) != 0;
-    v0 = up ? (p0 - v0) : (v0 + p0);
-    v1 = up ? (p1 - v1) : (v1 + p1);
+__device__ __forceinline__ void fwht_stage(float &v0, float &v1, float sign) {
+    if constexpr (H >= 16) {
+        // v_permlane{16,32}_swap exchanges the odd rows (of 16 or 32 lanes) of its first operand with the even rows
+        // of its second: with both holding v, the first then holds the lower lane's value of each pair (lo) and the
+        // second the upper's (hi), and the stage is lo + sign * hi.  Written in asm: the compiler's two-result form
+        // of the builtin lost the second result when both inputs were one value.  The s_nops cover the VALU write
+        // -> swap read and swap write -> VALU read hazards.
+        float lo0 = v0, hi0 = v0, lo1 = v1, hi1 = v1;
+        if constexpr (H == 16)
+            asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_permlane16_swap_b32 %2, %3\n\ts_nop 1"
+                         : "+v"(lo0), "+v"(hi0), "+v"(lo1), "+v"(hi1));
+        else
+            asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\tv_permlane32_swap_b32 %2, %3\n\ts_nop 1"
+                         : "+v"(lo0), "+v"(hi0), "+v"(lo1), "+v"(hi1));
+        v0 = __builtin_fmaf(hi0, sign, lo0);
+        v1 = __builtin_fmaf(hi1, sign, lo1);
+    } else {
+        v0 = __builtin_fmaf(v0, sign, xor_lane_row<H>(v0));
+        v1 = __builtin_fmaf(v1, sign, xor_lane_row<H>(v1));
+    }
 }
 
 __device__ __forceinline__ void fwht128_wave(float &v0, float &v1, int lane) {
@@ -301,12 +328,12 @@ __device__ __forceinline__ void fwht128_wave(float &v0, float &v1, int lane) {
         v0 = a + b;
         v1 = a - b;
     }
-    fwht_stage<32>(v0, v1, lane);
-    fwht_stage<16>(v0, v1, lane);
-    fwht_stage<8>(v0, v1, lane);
-    fwht_stage<4>(v0, v1, lane);
-    fwht_stage<2>(v0, v1, lane);
-    fwht_stage<1>(v0, v1, lane);
+    fwht_stage<32>(v0, v1, lane_sign<32>(lane));
+    fwht_stage<16>(v0, v1, lane_sign<16>(lane));
+    fwht_stage<8>(v0, v1, lane_sign<8>(lane));
+    fwht_stage<4>(v0, v1, lane_sign<4>(lane));
+    fwht_stage<2>(v0, v1, lane_sign<2>(lane));
+    fwht_stage<1>(v0, v1, lane_sign<1>(lane));
 }
 
 constexpr float HAD_SCALE = 0.08838834764831845f;

@@ -85,7 +85,8 @@ __device__ __forceinline__ float y_from_bits16(int dt, uint32_t b) {
 }
 
 struct GemvCtx {
-    int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_div, x_dtype;
+    int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_dtype;
+    uint32_t x_div_m;           // slots per x row, as a div_magic constant
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
     int xg;                     // x row of the group's row 0 (per-slot and dense arms, a shared expert's rows)
     int slot0;                  // MoE slot of the group's row 0 (a shared expert's rows: virtual slots past the routed)
@@ -109,7 +110,7 @@ __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c
 // WIN: the group is an expert window (the sorted MoE arm), a compile-time choice so the dense kernels carry none of it.
 template <bool WIN>
 __device__ __forceinline__ size_t x_row(const GemvArgs &a, const GemvCtx &c, int r) {
-    if constexpr (WIN) return (size_t)(c.wslots[r] / c.x_div);
+    if constexpr (WIN) return (size_t)div_by_magic(c.wslots[r], c.x_div_m);
     else return (size_t)c.xg + r;
 }
 // SH: a shared expert's rows keep one plane per row (slot slot0 + r), as the per-slot rows do.
@@ -218,7 +219,11 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx 
 #pragma unroll
         for (int i = 0; i < PrologueRegs<RT, WIN>::JOBS; i++) {
             int job = wave + GEMV_WAVES * i;
-            int rho = job / nblk, b = job - rho * nblk;
+            int rho = 0, b = job;  // one row: no division
+            if constexpr (RT > 1) {
+                rho = job / nblk;
+                b = job - rho * nblk;
+            }
             if (!(job < nblk * RT && rho < c.rows)) rho = b = 0;
             const int kb = c.kt0 * 16 + b * 128;
             const size_t in = (size_t)c.IT << 4;
@@ -266,7 +271,7 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                                          int lane, const PrologueRegs<RT, WIN> &pr) {
     const int nblk = c.KS >> 3;
     for (int job = wave; job < nblk * RT; job += GEMV_WAVES) {
-        const int rho = job / nblk, b = job - rho * nblk;
+        const int rho = RT > 1 ? job / nblk : 0, b = job - rho * nblk;
         const int kb = c.kt0 * 16 + b * 128;
         const int i = (job - wave) / GEMV_WAVES;
         float v0 = 0.f, v1 = 0.f;
@@ -461,10 +466,14 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
 }
 
 // svh of this lane's two outputs, for the finish.
+// PIN (dense launches): the offset passes through an empty asm, so the address arithmetic (and with it the wait for
+// the argument load that supplies the bank pointer) cannot be hoisted above the caller's tile loads.
+template <bool PIN = false>
 __device__ __forceinline__ void fetch_svh(GemvCtx &c, int lane) {
-    const size_t sv = (size_t)c.bank * ((size_t)c.OT << 4) + (size_t)c.og * 128;
-    c.sv0 = h2f(c.svh[sv + lane]);
-    c.sv1 = h2f(c.svh[sv + lane + 64]);
+    uint32_t sv = (uint32_t)c.bank * ((uint32_t)c.OT << 4) + (uint32_t)c.og * 128u;
+    if constexpr (PIN) asm volatile("" : "+s"(sv));
+    c.sv0 = h2f(c.svh[(size_t)sv + lane]);
+    c.sv1 = h2f(c.svh[(size_t)sv + lane + 64]);
 }
 
 // A per-tile-rate projection as a workgroup reads it (N == N_TILED): its segment tables and the constants at both
@@ -484,7 +493,8 @@ __device__ __forceinline__ uint32_t seg_mask(const uint8_t *k1, size_t seg) {
 
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 // N == N_TILED: each tile at its own rate (ts), tb the projection's whole trellis.
-template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
+// PIN: a uniform-rate launch's body (see fetch_svh).
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SH, bool PIN = false>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const uint16_t *__restrict__ tb,
                                           int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128],
                                           const TiledSrc &ts = TiledSrc{}) {
@@ -528,7 +538,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         };
 #pragma unroll
         for (int t = 0; t < TPW; t++) load_slot(t, c.kt0 + wave + GEMV_WAVES * min(t, ntiles - 1));
-        fetch_svh(c, lane);
+        __builtin_amdgcn_sched_barrier(0);  // svh's address comes from an argument load: its wait stays behind
+        fetch_svh<PIN>(c, lane);
         prologue<PRO, RT, WIN, SH>(a, c, xs, wave, lane, pr);
         __syncthreads();
         const bool masked = k.wmask != 0xFFFFu;
@@ -675,23 +686,22 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
 // shared expert).
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
 __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t *tr0, const uint16_t *suh0,
-                                           const uint32_t *bank_of, int in, int out, int splits, int rows,
-                                           int x_dtype, int x_div, const GemvArgs &a, uint16_t (*xs)[XS_PITCH],
-                                           float (*red)[RT][128]) {
+                                           const uint32_t *bank_of, const GemvGeo &geo, int rows, int x_dtype,
+                                           const GemvArgs &a, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
     GemvCtx c;
     c.x = x;
-    c.x_div = x_div;
+    c.x_div_m = geo.xdiv_m;
     c.x_dtype = x_dtype;
-    c.IT = in >> 4;
-    c.OT = out >> 4;
+    c.IT = (int)(geo.tiles & 0xFFFFu);
+    c.OT = (int)(geo.tiles >> 16);
     c.G = c.OT >> 3;
-    c.S = splits;
+    c.S = (int)(geo.sks & 0xFFFFu);
     const int L = blockIdx.x;
     // keep an output group's splits on one XCD when G % 8 == 0 (workgroups go round-robin over the 8 XCDs)
     const bool remap = (c.G & 7) == 0;
-    const unsigned us = (unsigned)c.S, q = remap ? (unsigned)L >> 3 : (unsigned)L, qs = q / us;
+    const unsigned q = remap ? (unsigned)L >> 3 : (unsigned)L, qs = div_by_magic(q, geo.s_m);
     c.og = remap ? (int)qs * 8 + (L & 7) : (int)qs;
-    c.sp = (int)(q - qs * us);
+    c.sp = (int)(q - qs * (unsigned)c.S);
     c.g = g;
     c.proj = blockIdx.z;
     const bool p1 = c.proj != 0;
@@ -730,19 +740,19 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
             c.rows = (int)min(a.win_rows[c.g], (uint32_t)MOE_WINDOW_ROWS);
             c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
         } else {
-            c.xg = (c.g / x_div) * rows;
+            c.xg = (int)div_by_magic((uint32_t)c.g, geo.xdiv_m) * rows;
             c.slot0 = c.g;
             c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
         }
     }
-    c.KS = c.IT / c.S;
+    c.KS = (int)(geo.sks >> 16);
     c.kt0 = c.sp * c.KS;
     c.sv0 = c.sv1 = 0.f;  // fetched by gemv_body once the tile loads are out
 
     if constexpr (N >= 0) {
         const int n = N ? N : a.n;
         const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
-        gemv_body<FAM, N, RT, PRO, WIN, SH>(a, c, tb, n, a.k, xs, red);
+        gemv_body<FAM, N, RT, PRO, WIN, SH, (N > 0 && !WIN && !SH)>(a, c, tb, n, a.k, xs, red);
     } else if constexpr (N == N_TILED) {
         // Per-tile-rate bank: every tile at TILED_NA or TILED_NB, read through the projection's segment tables (a
         // fused shared expert keeps its own uniform rate, a lane-reader rate the host checked).
@@ -806,13 +816,15 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
 // without them keep a kernel whose registers hold none of it.
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const uint16_t *tr0, const uint16_t *suh0,
-                                                            const uint32_t *bank_of, int in, int out, int splits,
-                                                            int rows_dt, int x_div, int sh_groups, GemvArgs a) {
+                                                            const uint32_t *bank_of, uint32_t tiles, uint32_t sks,
+                                                            uint32_t s_m, uint32_t xdiv_m, int rows_dt, int sh_groups,
+                                                            GemvArgs a) {
     // The leading scalar arguments are the ones the first loads need (the input and suh of the prologue, the tile
-    // words, and whether this group is a fused shared expert's): the build preloads them into SGPRs (14 dwords,
-    // rows and x's dtype sharing one), so those loads issue without waiting for an argument load.  The struct `a`
-    // holds everything (the same values included) for the rest of the kernel.
+    // words, the block-to-tile map and whether this group is a fused shared expert's): the build preloads them into
+    // SGPRs (14 dwords, rows and x's dtype sharing one), so those loads issue without waiting for an argument load
+    // and the map takes no division.  The struct `a` holds everything for the rest of the kernel.
     const int rows = rows_dt & 0xFFFF, x_dtype = rows_dt >> 16;
+    const GemvGeo geo{tiles, sks, s_m, xdiv_m};
     // A shared expert's groups hold SH_ROWS token rows each, so its weights are decoded once per SH_ROWS rows.
     constexpr int RX = (SHP && RT < SH_ROWS) ? SH_ROWS : RT;
     __shared__ __align__(16) uint16_t xs[RX][XS_PITCH];
@@ -822,8 +834,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
         // The per-slot MoE arm with a shared expert: its groups come first (they carry SH_ROWS rows each, the
         // heaviest workgroups, so they start in the first round), then the routed slots.
         if (g < sh_groups) {
-            gemv_group<FAM, N, SH_ROWS, PRO, WIN, true>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype,
-                                                        x_div, a, xs, reinterpret_cast<float (*)[SH_ROWS][128]>(red));
+            gemv_group<FAM, N, SH_ROWS, PRO, WIN, true>(g, x, tr0, suh0, bank_of, geo, rows, x_dtype, a, xs,
+                                                        reinterpret_cast<float (*)[SH_ROWS][128]>(red));
             return;
         }
         g -= sh_groups;
@@ -833,14 +845,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
         // then the expert windows.
         static_assert(RT == SH_ROWS, "a window holds as many rows as a shared group");
         if (g < sh_groups) {
-            gemv_group<FAM, N, SH_ROWS, PRO, false, true>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype,
-                                                          x_div, a, xs,
+            gemv_group<FAM, N, SH_ROWS, PRO, false, true>(g, x, tr0, suh0, bank_of, geo, rows, x_dtype, a, xs,
                                                           reinterpret_cast<float (*)[SH_ROWS][128]>(red));
             return;
         }
         g -= sh_groups;
     }
-    gemv_group<FAM, N, RT, PRO, WIN, false>(g, x, tr0, suh0, bank_of, in, out, splits, rows, x_dtype, x_div, a, xs,
+    gemv_group<FAM, N, RT, PRO, WIN, false>(g, x, tr0, suh0, bank_of, geo, rows, x_dtype, a, xs,
                                             reinterpret_cast<float (*)[RT][128]>(red));
 }
 
@@ -868,8 +879,10 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
 
 template <int FAM, int N, int RT, int PRO, bool WIN, bool SHP = false>
 static void launch_one(const GemvArgs &a, dim3 grid, hipStream_t s) {
+    const GemvGeo geo = gemv_geo(a);
     hipLaunchKernelGGL((gemv_kernel<FAM, N, RT, PRO, WIN, SHP>), grid, dim3(GEMV_THREADS), 0, s, a.x, a.trellis[0],
-                       a.suh[0], a.bank_of, a.in, a.out, a.splits, a.rows | (a.x_dtype << 16), a.x_div, a.sh_groups, a);
+                       a.suh[0], a.bank_of, geo.tiles, geo.sks, geo.s_m, geo.xdiv_m, a.rows | (a.x_dtype << 16),
+                       a.sh_groups, a);
 }
 
 template <int FAM, int N, int PRO>
@@ -881,6 +894,10 @@ static void launch_slot(const GemvArgs &a, dim3 grid, hipStream_t s) {  // one r
 template <int FAM, int N, int PRO>
 static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
     const int G = a.out / 128;
+    // the block-to-tile map's packed fields (gemv_geo) and its divisions' exactness
+    if (a.in / 16 > 0xFFFF || a.out / 16 > 0xFFFF || a.splits < 1 || (a.in / 16) % a.splits || a.x_div < 1 ||
+        a.x_div > 255 || (unsigned long long)G * a.splits * (unsigned)a.splits >= (1ull << 32))
+        return hipErrorInvalidValue;  // x rows are found as slot / x_div for up to 2^24 slots
     dim3 grid((unsigned)(G * a.splits), (unsigned)a.groups, (unsigned)a.nproj);
     if (a.win_count) {  // the sorted MoE arm: expert windows of MOE_WINDOW_ROWS rows, f32 planes or the fold out
         if (a.rows != MOE_WINDOW_ROWS || !(a.partial_only || a.fold)) return hipErrorInvalidValue;

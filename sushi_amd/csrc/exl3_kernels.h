@@ -44,6 +44,15 @@ constexpr int GEMV_WAVES = 8;
 constexpr int TPW = 2;
 constexpr int GEMV_TARGET_WGS = 256;
 
+// Division by a launch constant d >= 1 as one multiply-high: m = 0 stands for d = 1, else m = ceil(2^32 / d), and
+// floor(q m / 2^32) = q / d whenever q (d - 1) < 2^32 (with m d = 2^32 + r, r < d, and q = k d + j: the excess
+// q r / 2^32 stays below 1 <= d - j).  The GEMV's block-to-tile map divides by its split count and its x row
+// divisor this way, ahead of its first loads (a general 32-bit division is some 20 dependent instructions).
+__host__ __device__ inline uint32_t div_magic(uint32_t d) {
+    return d <= 1 ? 0u : (uint32_t)((0x100000000ull + d - 1) / d);
+}
+__device__ __forceinline__ uint32_t div_by_magic(uint32_t q, uint32_t m) { return m ? __umulhi(q, m) : q; }
+
 // Trellis GEMV over `groups` independent (bank, x-block) pairs, 1..8 rows each.
 //  * dense linear: groups = 1 (or G for linearGrouped), bank_of = null, x_div = 1;
 //  * MoE pair GEMV: groups = slots, bank_of = expert id per slot, x_div = topk, two projections (gate, up) on
@@ -120,6 +129,16 @@ struct GemvArgs {
     const uint16_t *sh_svh[2];
     const uint16_t *sh_mid_svh[2];  // PRO_MID: the shared expert's gate / up svh
 };
+
+// The GEMV's block-to-tile map, preloaded as leading kernel arguments: k-tiles and output tiles (in / 16 | out / 16
+// << 16), splits and k-tiles per split (S | (in / 16 / S) << 16), and the div_magic constants of S and x_div.
+struct GemvGeo {
+    uint32_t tiles, sks, s_m, xdiv_m;
+};
+inline GemvGeo gemv_geo(const GemvArgs &a) {
+    const uint32_t it = (uint32_t)a.in / 16, ot = (uint32_t)a.out / 16, s = (uint32_t)a.splits;
+    return GemvGeo{it | ot << 16, s | (it / s) << 16, div_magic(s), div_magic((uint32_t)a.x_div)};
+}
 
 // Rows per expert window in the sorted MoE arm.
 constexpr int MOE_WINDOW_ROWS = 4;
