@@ -126,16 +126,26 @@ __device__ __forceinline__ int slot_of(const GemvCtx &c, int r) {
     else return c.slot0 + r;  // per-slot groups hold one row
 }
 
-// The lane's 16 decoded pairs (w, already scaled for the matrix cores) against every batch row of k-tile kk.
+// A lane's prepared input for one k-tile (its A rows at k 0..15 of the tile): read before the tile's decode, so the
+// LDS latency hides behind it.
+struct XFrag {
+    uint4 X, Y;
+};
+__device__ __forceinline__ XFrag read_xfrag(const uint16_t (*xs)[XS_PITCH], int row, int kk) {
+    const uint16_t *xg = &xs[row][kk * 16];
+    return XFrag{*reinterpret_cast<const uint4 *>(xg), *reinterpret_cast<const uint4 *>(xg + 8)};
+}
+// The lane's 16 decoded pairs (w, already scaled for the matrix cores) against every batch row of k-tile kk; f0 is
+// row group 0's fragment, the others are read here.
 template <int RT>
 __device__ __forceinline__ void mfma_dot(const uint32_t (&w)[16], const uint16_t (*xs)[XS_PITCH], int kk, int rows,
-                                         f4_t (&accA)[RowGroups<RT>::G], f4_t (&accB)[RowGroups<RT>::G], int i4) {
+                                         f4_t (&accA)[RowGroups<RT>::G], f4_t (&accB)[RowGroups<RT>::G], int i4,
+                                         const XFrag &f0) {
 #pragma unroll
     for (int g = 0; g < RowGroups<RT>::G; g++) {
         if (g > 0 && 4 * g >= rows) break;
-        const uint16_t *xg = &xs[min(4 * g + i4, RT - 1)][kk * 16];
-        const uint4 X = *reinterpret_cast<const uint4 *>(xg);
-        const uint4 Y = *reinterpret_cast<const uint4 *>(xg + 8);
+        const XFrag f = g == 0 ? f0 : read_xfrag(xs, min(4 * g + i4, RT - 1), kk);
+        const uint4 X = f.X, Y = f.Y;
         accA[g] = mfma4(X.x, X.y, w[0], w[4], accA[g]);
         accB[g] = mfma4(X.x, X.y, w[2], w[6], accB[g]);
         accA[g] = mfma4(X.z, X.w, w[8], w[12], accA[g]);
@@ -166,10 +176,11 @@ template <int FAM, int N, int RT, bool MASKED>
 __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW], const uint16_t (*xs)[XS_PITCH],
                                             int kk, int rows, const DecodeK &k, f4_t (&accA)[RowGroups<RT>::G],
                                             f4_t (&accB)[RowGroups<RT>::G], int i4) {
+    const XFrag f0 = read_xfrag(xs, min(i4, RT - 1), kk);
     uint32_t w[16];
     decode_weights<FAM, N, MASKED>(A, k, w);
     scale_for_mfma<FAM>(w);
-    mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4);
+    mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4, f0);
 }
 
 // The same for a lane of a per-tile-rate bank, at its own tile's rate (k: the lane's constants).
@@ -177,10 +188,11 @@ template <int FAM, int RT, bool MASKED>
 __device__ __forceinline__ void decode_tile_tiled(const uint32_t (&A)[3], bool k1, const uint16_t (*xs)[XS_PITCH],
                                                   int kk, int rows, const DecodeK &k, f4_t (&accA)[RowGroups<RT>::G],
                                                   f4_t (&accB)[RowGroups<RT>::G], int i4) {
+    const XFrag f0 = read_xfrag(xs, min(i4, RT - 1), kk);
     uint32_t w[16];
     decode_weights_tiled<FAM, MASKED>(A, k1, k, w);
     scale_for_mfma<FAM>(w);
-    mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4);
+    mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4, f0);
 }
 
 // x[i] as f32 from an f16 / bf16 / f32 array without branching on the dtype: one 32-bit load of the aligned word
@@ -287,6 +299,16 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                     v1 = f16r(load_x_nb(c.x, a.x_dtype, xi + lane + 64)) * h2f(c.suh[si + lane + 64]);
                 }
             } else {  // the SwiGLU mid of the decode chain (DOWN_FUSED_SOURCE prologue, :1838-1920)
+                // The gate / up svh and suh_down depend on the expert only: their loads go out with the planes',
+                // so the job waits out one memory round trip, not three.
+                float msv_v[2][2];
+#pragma unroll
+                for (int pj = 0; pj < 2; pj++) {
+                    const uint16_t *msv = SH ? a.sh_mid_svh[pj] : a.mid_svh[pj];
+                    msv_v[pj][0] = h2f(msv[si + lane]);
+                    msv_v[pj][1] = h2f(msv[si + lane + 64]);
+                }
+                const float su0 = h2f(c.suh[si + lane]), su1 = h2f(c.suh[si + lane + 64]);
                 float w[2][2];
                 mid_planes(a, slot_of<WIN>(c, rho), kb, lane, w);
                 float gv[2], uv[2];
@@ -294,9 +316,8 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                 for (int pj = 0; pj < 2; pj++) {
                     float w0 = w[pj][0], w1 = w[pj][1];
                     fwht128_wave(w0, w1, lane);
-                    const uint16_t *msv = SH ? a.sh_mid_svh[pj] : a.mid_svh[pj];
-                    w0 *= HAD_SCALE * h2f(msv[si + lane]);
-                    w1 *= HAD_SCALE * h2f(msv[si + lane + 64]);
+                    w0 *= HAD_SCALE * msv_v[pj][0];
+                    w1 *= HAD_SCALE * msv_v[pj][1];
                     if (pj == 0) {
                         gv[0] = w0;
                         gv[1] = w1;
@@ -312,8 +333,8 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                         uv[i] = fminf(fmaxf(uv[i], -a.clamp_limit), a.clamp_limit);
                     }
                 }
-                v0 = silu(gv[0]) * uv[0] * h2f(c.suh[si + lane]);
-                v1 = silu(gv[1]) * uv[1] * h2f(c.suh[si + lane + 64]);
+                v0 = silu(gv[0]) * uv[0] * su0;
+                v1 = silu(gv[1]) * uv[1] * su1;
             }
             fwht128_wave(v0, v1, lane);
             v0 *= HAD_SCALE;
@@ -585,7 +606,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
                 w[i] = decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
             }
             scale_for_mfma<FAM>(w);
-            mfma_dot<RT>(w, xs, kk, c.rows, accA, accB, lane & 3);
+            mfma_dot<RT>(w, xs, kk, c.rows, accA, accB, lane & 3, read_xfrag(xs, min(lane & 3, RT - 1), kk));
         }
     }
     // the hash / pair weights went in times 2^12; out_scale applies the codebook scale to every arm alike
