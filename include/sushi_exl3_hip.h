@@ -151,7 +151,8 @@ typedef enum {
     EXL3_KNOB_MOE_WINDOWS = 6,          /* 0: no sorted (expert-window) arm */
     EXL3_KNOB_MOE_FOLD = 7,             /* 0: the down projection writes planes and a reduce kernel finishes */
     EXL3_KNOB_MOE_GEMM = 8,             /* 1: a routed layer takes the GEMM arm where it can, 0: never */
-    EXL3_KNOB_GEMM_ARM = 9,             /* dense GEMM body: 4 = decode-wave tile, 5 / 6 = ping-pong 512 / 256 rows */
+    EXL3_KNOB_GEMM_ARM = 9,             /* dense GEMM body: 4 = decode-wave tile, 5 / 6 = ping-pong 512 / 256 rows,
+                                           7 = ping-pong 512 rows with k in two halves */
     EXL3_KNOB_COUNT = 10
 } exl3_knob;
 int32_t exl3_set_override(int32_t knob, int32_t value, int32_t enable);

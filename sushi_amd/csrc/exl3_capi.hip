@@ -141,10 +141,30 @@ GemvPlan plan_gemv(int groups, int rows, int in, int out) {
 // Prepared-input rows of the GEMM arm: whole 16-row tiles (the fragment-order layout pads the last tile).
 size_t gemm_xp_bytes(int groups, int rows, int in) { return align_up((size_t)groups * ((rows + 15) / 16 * 16) * in * 2); }
 
+// The dense GEMM body at a lane-reader rate (EXL3_KNOB_GEMM_ARM pins one): the ping-pong 512-row tile past 512 rows
+// while its tiles still give most CUs a workgroup; from 257 to 512 rows, where they would not, the same tile with k
+// in halves when that fills the chip; otherwise the decode-wave 256-row tile.  Measured at C3's 4096 x 14336:
+// 512 rows 94.3 -> 91.4 us, 384 rows 91.1 -> 89.2 us on the split tile; 256 rows stay on the decode-wave tile
+// (81.5 against 88.5 us).
+int gemm_arm_for(int groups, int rows, int out) {
+    const int pinned = knob(EXL3_KNOB_GEMM_ARM, 0);
+    if (pinned) return pinned;
+    return gemm_default_arm(groups, rows, out);
+}
+
+// Arm 7 (k in halves) holds both halves' partials after the prepared input, and one counter per tile in the zeroed
+// region; n = 40 never takes it (its reader does not fit the 512-row tile's registers).
+bool gemm_uses_kpart(int groups, int rows, int out, int n) {
+    const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 48 || n == 64;
+    return lane_reader && gemm_arm_for(groups, rows, out) == 7 &&
+           (size_t)groups * ((rows + 511) / 512) * (out / 128) <= kCounterSlots;
+}
+
 size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
     size_t b = kZeroBytes + gemm_xp_bytes(groups, rows, in);
     const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
     if (!lane_reader) b += align_up((size_t)groups * out * in * 2);  // the transposed f16 copy of other rates
+    if (gemm_uses_kpart(groups, rows, out, n)) b += align_up(gemm_kpart_bytes(groups, rows, out));
     return b;
 }
 
@@ -240,7 +260,11 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     g.y = y;
     g.y_dtype = y_dtype;
     g.groups = groups;
-    g.arm = knob(EXL3_KNOB_GEMM_ARM, 0);
+    g.arm = gemm_arm_for(groups, rows, out);
+    if (gemm_uses_kpart(groups, rows, out, n)) {
+        g.kpart = reinterpret_cast<float *>(w + kZeroBytes + gemm_xp_bytes(groups, rows, in));
+        g.kctr = reinterpret_cast<uint32_t *>(w);
+    }
     return launched(run_gemm(fam, g, stream), "exl3_linear (gemm)");
 }
 

@@ -307,6 +307,7 @@ __device__ __forceinline__ void fwht_stage(float &v0, float &v1, float sign) {
         // second the upper's (hi), and the stage is lo + sign * hi.  Written in asm: the compiler's two-result form
         // of the builtin lost the second result when both inputs were one value.  The s_nops cover the VALU write
         // -> swap read and swap write -> VALU read hazards.
+        // Volatile: left free to move, the swaps were scheduled into the GEMV's decode (C1 6.57 -> 6.83 us).
         float lo0 = v0, hi0 = v0, lo1 = v1, hi1 = v1;
         if constexpr (H == 16)
             asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_permlane16_swap_b32 %2, %3\n\ts_nop 1"
@@ -334,6 +335,33 @@ __device__ __forceinline__ void fwht128_wave(float &v0, float &v1, int lane) {
     fwht_stage<4>(v0, v1, lane_sign<4>(lane));
     fwht_stage<2>(v0, v1, lane_sign<2>(lane));
     fwht_stage<1>(v0, v1, lane_sign<1>(lane));
+}
+
+// R independent 128-point transforms (one per row), each stage over every row before the next stage: the rows'
+// exchanges of one stage go out together instead of each transform waiting out its own chain.  Each row's result
+// equals fwht128_wave's.
+template <int R>
+__device__ __forceinline__ void fwht128_wave_rows(float (&v0)[R], float (&v1)[R], int lane) {
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const float a = v0[i], b = v1[i];
+        v0[i] = a + b;
+        v1[i] = a - b;
+    }
+    const float s32 = lane_sign<32>(lane), s16 = lane_sign<16>(lane), s8 = lane_sign<8>(lane), s4 = lane_sign<4>(lane),
+                s2 = lane_sign<2>(lane), s1 = lane_sign<1>(lane);
+#pragma unroll
+    for (int i = 0; i < R; i++) fwht_stage<32>(v0[i], v1[i], s32);
+#pragma unroll
+    for (int i = 0; i < R; i++) fwht_stage<16>(v0[i], v1[i], s16);
+#pragma unroll
+    for (int i = 0; i < R; i++) fwht_stage<8>(v0[i], v1[i], s8);
+#pragma unroll
+    for (int i = 0; i < R; i++) fwht_stage<4>(v0[i], v1[i], s4);
+#pragma unroll
+    for (int i = 0; i < R; i++) fwht_stage<2>(v0[i], v1[i], s2);
+#pragma unroll
+    for (int i = 0; i < R; i++) fwht_stage<1>(v0[i], v1[i], s1);
 }
 
 constexpr float HAD_SCALE = 0.08838834764831845f;

@@ -268,11 +268,25 @@ constexpr int G2_EP = 129;   // epilogue staging pitch (floats)
 constexpr int G4_WAVES = 12;
 constexpr int G4_THREADS = 64 * G4_WAVES;
 
+// Outputs at columns i and i + 64 of one row, in y's dtype.
+__device__ __forceinline__ void store_y4(void *y, int dt, size_t i, float y0, float y1) {
+    if (dt == DT_F16) {
+        store_act<DT_F16>(y, i, y0);
+        store_act<DT_F16>(y, i + 64, y1);
+    } else if (dt == DT_BF16) {
+        store_act<DT_BF16>(y, i, y0);
+        store_act<DT_BF16>(y, i + 64, y1);
+    } else {
+        store_act<DT_F32>(y, i, y0);
+        store_act<DT_F32>(y, i + 64, y1);
+    }
+}
+
 // One workgroup's 256-row x 128-column output tile: output group og of a bank whose tiles start at `bank`
 // ([in/16][out/16][N]), prepared rows in fragment tiles from xfrag0 (row tile rt at xfrag0 + rt * (in / 32) * 512), of
-// which the first `rows` (<= 256) are live.  The epilogue hands each live row's raw inner products to
-// emit(m, v0, v1, lane) (columns lane and lane + 64 of the group, m the row within the tile); the caller applies the
-// output transform or stores the raw values.
+// which the first `rows` (<= 256) are live.  The epilogue hands the raw inner products of rows m .. m + 3 to
+// emit(m, live, v0[4], v1[4], lane) (columns lane and lane + 64 of the group, m the row within the tile, the first
+// `live` of them live); the caller applies the output transform (four rows at a time) or stores the raw values.
 template <int FAM, int N, class Emit>
 __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16_t *__restrict__ bank,
                                            const uint16_t *__restrict__ xfrag0, int rows, const DecodeK &k,
@@ -394,10 +408,17 @@ __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16
 #pragma unroll
             for (int i = 0; i < 4; i++) ep[(4 * h + i) * G2_EP + (cb0 + cb) * 16 + c] = acc[rb][cb][i];
         __syncthreads();
-        for (int r = (wave & 1) * 8; r < (wave & 1) * 8 + 8; r++) {
-            const int m = m0 + rb * 16 + r;
+#pragma unroll
+        for (int r4 = 0; r4 < 8; r4 += 4) {
+            const int r = (wave & 1) * 8 + r4, m = m0 + rb * 16 + r;
             if (m >= rows) break;
-            emit(m, ep[r * G2_EP + lane], ep[r * G2_EP + lane + 64], lane);
+            float v0[4], v1[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v0[i] = ep[(r + i) * G2_EP + lane];
+                v1[i] = ep[(r + i) * G2_EP + lane + 64];
+            }
+            emit(m, min(4, rows - m), v0, v1, lane);
         }
         __syncthreads();
     }
@@ -425,19 +446,12 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
     const int lane = threadIdx.x & 63;
     const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
     gemm4_tile<FAM, N>(a.in, a.out, og, a.trellis + (size_t)g * IT * OT * N, xfrag0, min(G2_MT, a.rows - mt * G2_MT),
-                       a.k, Bs, [&](int m, float v0, float v1, int ln) __attribute__((always_inline)) {
-                           fwht128_wave(v0, v1, ln);
-                           const size_t yo = ((size_t)g * a.rows + mt * G2_MT + m) * a.out + (size_t)og * 128;
-                           const float y0 = v0 * HAD_SCALE * s0, y1 = v1 * HAD_SCALE * s1;
-                           if (a.y_dtype == DT_F16) {
-                               store_act<DT_F16>(a.y, yo + ln, y0);
-                               store_act<DT_F16>(a.y, yo + ln + 64, y1);
-                           } else if (a.y_dtype == DT_BF16) {
-                               store_act<DT_BF16>(a.y, yo + ln, y0);
-                               store_act<DT_BF16>(a.y, yo + ln + 64, y1);
-                           } else {
-                               store_act<DT_F32>(a.y, yo + ln, y0);
-                               store_act<DT_F32>(a.y, yo + ln + 64, y1);
+                       a.k, Bs,
+                       [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
+                           fwht128_wave_rows<4>(v0, v1, ln);
+                           for (int i = 0; i < live; i++) {
+                               const size_t yo = ((size_t)g * a.rows + mt * G2_MT + m + i) * a.out + (size_t)og * 128;
+                               store_y4(a.y, a.y_dtype, yo + ln, v0[i] * HAD_SCALE * s0, v1[i] * HAD_SCALE * s1);
                            }
                        });
 }
@@ -455,21 +469,28 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
 // written in step s was last read in step s - 1, each on the other side of a barrier.  The trellis words are loaded
 // a step before their decode, the A fragments of step s + 1 as soon as step s's MFMAs of that half have issued.
 // Every weight is decoded once per MT rows (twice per 1024 rows at MT = 512, against four times for the 256-row tile).
+//
+// KS = 2 splits k in halves over twice the workgroups (a grid of few 512-row tiles then fills the chip and still
+// decodes every weight once per 512 rows).  Each half writes its raw accumulators through to memory, then arrives at
+// the tile's counter; the last arriver adds the other half's (a sum of two, so independent of which came first),
+// clears the counter and runs the epilogue.
 constexpr int G5_WAVES = 8;
 constexpr int G5_THREADS = 64 * G5_WAVES;
-constexpr int G5_EP = 129;                                                  // epilogue staging pitch (floats)
 constexpr int G5_SLAB = 128 * G2_BP;                                        // halves per slab
-constexpr int G5_LDS = (3 * G5_SLAB * 2 > G5_WAVES * 16 * G5_EP * 4) ? 3 * G5_SLAB * 2 : G5_WAVES * 16 * G5_EP * 4;
+constexpr int G5_LDS = 3 * G5_SLAB * 2;                                     // the slab ring (the epilogue uses none)
 
-template <int FAM, int N, int MT>
+template <int FAM, int N, int MT, int KS>
 __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
     static_assert(FAM != FAM_PAIR && FAM != FAM_MUL1, "hash-product families");
+    static_assert(KS == 1 || KS == 2, "whole k or halves");
     constexpr int RW = MT / G5_WAVES;  // rows per wave
     constexpr int RB = RW / 16;        // row blocks per wave
     constexpr int AW = LaneBits<N>::AW;
     const int IT = a.in >> 4, OT = a.out >> 4;
     const int nog = a.out / 128, nm = (a.rows + MT - 1) / MT;
-    const int L = blockIdx.x;
+    // split ks of a tile: the grid's second half (its tile index repeats the first half's, so the same XCD map)
+    const int ks = KS == 1 ? 0 : (int)blockIdx.x / (nm * nog);
+    const int L = KS == 1 ? (int)blockIdx.x : (int)blockIdx.x - ks * nm * nog;
     int og, mt;
     if (nm <= 8 && 8 % nm == 0 && nog % (8 / nm) == 0) {  // a row tile's workgroups share an XCD (its A rows in one L2)
         const int xcd = L & 7, per = 8 / nm;
@@ -486,16 +507,17 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, h = lane >> 4;
     const int RT = (a.rows + 15) / 16;
-    const int nks = IT / 4;
+    const int nks = IT / 4 / KS;   // this split's k-steps (IT is a multiple of 8: whole 128-blocks)
+    const int s0g = ks * nks;      // its first k-step
     const DecodeK k = a.k;
     const bool masked = k.wmask != 0xFFFFu;
 
     // ---- decode role: column half H of k-tile row r of each step
     const int r = wave & 3, H = wave >> 2;
     const int o = lane >> 3, j = lane & 7;
-    const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8) * N;
-    const uint32_t lane_words = (uint32_t)(o * N) >> 1;
     const size_t kstep = (size_t)4 * OT * N;  // halves from one k-step's row r to the next
+    const uint16_t *tb = a.trellis + (size_t)g * IT * OT * N + ((size_t)r * OT + og * 8) * N + (size_t)s0g * kstep;
+    const uint32_t lane_words = (uint32_t)(o * N) >> 1;
     auto load_words = [&](int s, uint32_t (&W)[AW]) __attribute__((always_inline)) {
         load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(s, nks - 1) * kstep), lane_words, j,
                              W);
@@ -536,7 +558,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
         for (int cb = 0; cb < 8; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
     uint4 A[2][RB];
     auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
-        const int kk = min(s, nks - 1) * 2 + kb;
+        const int kk = (s0g + min(s, nks - 1)) * 2 + kb;
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
             const int rt = min(m0 / 16 + rb, RT - 1);
@@ -614,33 +636,84 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
     }
     __syncthreads();  // the H = 1 waves' last decode (none: s + 3 >= nks) and every slab read are behind this
 
-    // ---- epilogue: per 16-row block, the wave stages its 16 x 128 outputs in its own LDS region (the last barrier
-    // has retired every slab read), then finishes each row: FWHT-128, * svh, store
-    float *ep = reinterpret_cast<float *>(lds) + wave * 16 * G5_EP;
+    if constexpr (KS == 2) {
+        // partial of split ks: [tile][ks][wave][rb][cb] blocks of 64 lanes x 4 floats, one 1 KiB store each
+        const size_t tile = ((size_t)g * nm + mt) * nog + og;
+        const size_t wave_f = (size_t)RB * 8 * 256;  // floats per wave
+        float *mine = a.kpart + ((tile * 2 + ks) * G5_WAVES + wave) * wave_f;
+        const float *other = a.kpart + ((tile * 2 + (ks ^ 1)) * G5_WAVES + wave) * wave_f;
+        const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(mine, (short)0, (int)(wave_f * 4), 0x00020000);
+        const __amdgpu_buffer_rsrc_t orr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(other), (short)0, (int)(wave_f * 4), 0x00020000);
+        // sc0 sc1: the stores go through to memory and the loads bypass the caches (the halves may sit on two XCDs)
+        constexpr int SYS = 1 | 16;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int cb = 0; cb < 8; cb++)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[rb][cb]), mr, a_lane,
+                                                       (rb * 8 + cb) * 1024, SYS);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // acknowledged before the arrival below
+        __syncthreads();
+        __shared__ uint32_t arrived;
+        uint32_t *ctr = a.kctr + tile * COUNTER_STRIDE;
+        if (tid == 0) arrived = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrived == 0) return;  // the other half finishes the tile
+        if (tid == 0) *ctr = 0u;   // no workgroup of this launch touches it again; the next launch reads it after the boundary
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int cb = 0; cb < 8; cb++) {
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(orr, a_lane, (rb * 8 + cb) * 1024, SYS);
+                acc[rb][cb] += __builtin_bit_cast(f4_t, v);
+            }
+    }
+
+    // ---- epilogue: the output transform straight from the accumulators.  Column cb * 16 + c of the tile sits in
+    // acc[.][cb] of lane c + 16 h (rows 4 h .. 4 h + 3), and H128 = H8 (over cb) x H16 (over c): the stages of bits
+    // 6, 5, 4 are butterflies between a lane's own registers, those of bits 3 .. 0 the DPP stages within each 16-lane
+    // row.  These are fwht128_wave's stages in its order with its sums, so the outputs equal the row-wise transform's
+    // bit for bit, without staging rows through LDS or running one transform per row.
     const size_t sv = (size_t)g * a.out + (size_t)og * 128;
-    const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
+    float svc[8];
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) svc[cb] = h2f(a.svh[sv + cb * 16 + c]);
+    const float sg8 = lane_sign<8>(lane), sg4 = lane_sign<4>(lane), sg2 = lane_sign<2>(lane), sg1 = lane_sign<1>(lane);
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
 #pragma unroll
-        for (int cb = 0; cb < 8; cb++)
+        for (int i = 0; i < 4; i++) {
+            float v[8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) ep[(4 * h + i) * G5_EP + cb * 16 + c] = acc[rb][cb][i];
-        for (int rr = 0; rr < 16; rr++) {
-            const int m = m0 + rb * 16 + rr;
-            if (m >= a.rows) break;
-            float v0 = ep[rr * G5_EP + lane], v1 = ep[rr * G5_EP + lane + 64];
-            fwht128_wave(v0, v1, lane);
-            const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128;
-            const float y0 = v0 * HAD_SCALE * s0, y1 = v1 * HAD_SCALE * s1;
-            if (a.y_dtype == DT_F16) {
-                store_act<DT_F16>(a.y, yo + lane, y0);
-                store_act<DT_F16>(a.y, yo + lane + 64, y1);
-            } else if (a.y_dtype == DT_BF16) {
-                store_act<DT_BF16>(a.y, yo + lane, y0);
-                store_act<DT_BF16>(a.y, yo + lane + 64, y1);
-            } else {
-                store_act<DT_F32>(a.y, yo + lane, y0);
-                store_act<DT_F32>(a.y, yo + lane + 64, y1);
+            for (int cb = 0; cb < 8; cb++) v[cb] = acc[rb][cb][i];
+#pragma unroll
+            for (int hb = 4; hb >= 1; hb >>= 1)
+#pragma unroll
+                for (int cb = 0; cb < 8; cb++)
+                    if (!(cb & hb)) {
+                        const float lo = v[cb], hi = v[cb | hb];
+                        v[cb] = lo + hi;
+                        v[cb | hb] = lo - hi;
+                    }
+#pragma unroll
+            for (int cb = 0; cb < 8; cb += 2) fwht_stage<8>(v[cb], v[cb + 1], sg8);
+#pragma unroll
+            for (int cb = 0; cb < 8; cb += 2) fwht_stage<4>(v[cb], v[cb + 1], sg4);
+#pragma unroll
+            for (int cb = 0; cb < 8; cb += 2) fwht_stage<2>(v[cb], v[cb + 1], sg2);
+#pragma unroll
+            for (int cb = 0; cb < 8; cb += 2) fwht_stage<1>(v[cb], v[cb + 1], sg1);
+            const int m = m0 + rb * 16 + 4 * h + i;
+            if (m < a.rows) {
+                const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128 + c;
+#pragma unroll
+                for (int cb = 0; cb < 8; cb++) {
+                    const float y = v[cb] * HAD_SCALE * svc[cb];
+                    if (a.y_dtype == DT_F16) store_act<DT_F16>(a.y, yo + cb * 16, y);
+                    else if (a.y_dtype == DT_BF16) store_act<DT_BF16>(a.y, yo + cb * 16, y);
+                    else store_act<DT_F32>(a.y, yo + cb * 16, y);
+                }
             }
         }
     }
@@ -661,10 +734,12 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     const uint16_t *xfrag0 = a.xp[p] + (size_t)a.win.win_tile0[w] * (size_t)(a.in / 32) * 512;
     float *planes = a.planes[p];
     gemm4_tile<FAM, N>(a.in, a.out, og, a.trellis[p] + (size_t)e * IT * OT * N, xfrag0, rows, a.k, Bs,
-                       [&](int m, float v0, float v1, int ln) __attribute__((always_inline)) {
-                           float *row = planes + (size_t)slots[m] * a.out + (size_t)og * 128;
-                           row[ln] = v0;
-                           row[ln + 64] = v1;
+                       [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
+                           for (int i = 0; i < live; i++) {
+                               float *row = planes + (size_t)slots[m + i] * a.out + (size_t)og * 128;
+                               row[ln] = v0[i];
+                               row[ln + 64] = v1[i];
+                           }
                        });
 }
 
@@ -813,23 +888,22 @@ static hipError_t launch_gemm_lane_n(const GemmArgs &a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // The ping-pong body once its 512-row tiles still give most CUs a workgroup (measured at C3's 4096 x 14336: 768 to
-    // 4096 rows 13-24% faster than the 256-row decode-wave tile; at 512 rows, 112 workgroups, 18% slower).
-    int arm = a.arm;
-    if (arm == 0) {
-        const long wg5 = (long)((a.rows + 511) / 512) * (a.out / 128) * a.groups;
-        arm = (a.rows > 512 && wg5 >= 192) ? 5 : 4;
-    }
+    // 4096 rows 13-24% faster than the 256-row decode-wave tile; at 512 rows, 112 workgroups, 18% slower, and with k in
+    // halves, 224 workgroups, 3% faster).
+    int arm = a.arm ? a.arm : gemm_default_arm(a.groups, a.rows, a.out);
     if constexpr (FAM == FAM_PAIR || FAM == FAM_MUL1) arm = 4;  // the ping-pong body serves the hash-product families
     // n = 40's unaligned lane reader does not fit the 512-row tile's registers (it would spill): the 256-row one
     if constexpr (N == 40) arm = arm == 5 ? (a.arm ? 6 : 4) : arm;
-    if (arm == 5 || arm == 6) {
-        const int mt = arm == 5 ? 512 : 256;
-        dim3 grid((unsigned)((a.out / 128) * ((a.rows + mt - 1) / mt)), 1, (unsigned)a.groups);
+    if (arm == 7 && (N == 40 || !a.kpart)) arm = 4;  // the split needs its partial region (the host sizes it)
+    if (arm == 5 || arm == 6 || arm == 7) {
+        const int mt = arm == 6 ? 256 : 512;
+        dim3 grid((unsigned)((a.out / 128) * ((a.rows + mt - 1) / mt) * (arm == 7 ? 2 : 1)), 1, (unsigned)a.groups);
         if constexpr (FAM != FAM_PAIR && FAM != FAM_MUL1) {
             if constexpr (N != 40) {
-                if (arm == 5) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 512>), grid, dim3(G5_THREADS), 0, s, a);
+                if (arm == 5) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 512, 1>), grid, dim3(G5_THREADS), 0, s, a);
+                if (arm == 7) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 512, 2>), grid, dim3(G5_THREADS), 0, s, a);
             }
-            if (arm == 6) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 256>), grid, dim3(G5_THREADS), 0, s, a);
+            if (arm == 6) hipLaunchKernelGGL((gemm5_kernel<FAM, N, 256, 1>), grid, dim3(G5_THREADS), 0, s, a);
         }
         return hipGetLastError();
     }

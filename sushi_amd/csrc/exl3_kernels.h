@@ -247,8 +247,22 @@ struct GemmArgs {
     void *y;
     int y_dtype;
     int groups;
-    int arm;          // GEMM body: 0 = the row-count policy, 4 = 256-row tile (decode waves), 5 / 6 = ping-pong 512 / 256
+    int arm;          // GEMM body: 0 = the row-count policy, 4 = 256-row tile (decode waves), 5 / 6 = ping-pong 512 / 256,
+                      // 7 = ping-pong 512 with k in halves
+    float *kpart;     // arm 7: workspace for the halves' partials (gemm_kpart_bytes), or null
+    uint32_t *kctr;   // arm 7: one zeroed counter per tile (COUNTER_STRIDE words apart), left at zero
 };
+// The row-count policy for arm 0 (the C-ABI layer applies it and sizes arm 7's region accordingly).
+inline int gemm_default_arm(int groups, int rows, int out) {
+    const long wg5 = (long)((rows + 511) / 512) * (out / 128) * groups;
+    if (rows > 512 && wg5 >= 192) return 5;
+    if (rows > 256 && rows <= 512 && wg5 < 192 && 2 * wg5 >= 160) return 7;
+    return 4;
+}
+// arm 7's partial region: two halves of every 512-row x 128-column tile, f32
+inline size_t gemm_kpart_bytes(int groups, int rows, int out) {
+    return (size_t)groups * ((rows + 511) / 512) * (out / 128) * 2 * 512 * 128 * sizeof(float);
+}
 hipError_t run_gemm(int fam, const GemmArgs &a, hipStream_t s);
 
 hipError_t run_route_topk(const float *logits, int rows, int experts, int k, uint32_t *inds, float *scores,

@@ -152,10 +152,11 @@ def test_c3_prefill_shapes(dev, rows, out_f):
 
 
 # ---- ping-pong GEMM body (gemm_arm 5 / 6: 512- / 256-row tiles, every wave decoding half a k-tile row and running
-# the MFMAs of its own rows), forced at small shapes; the row-count policy takes arm 5 past 512 rows
+# the MFMAs of its own rows; 7: the 512-row tile with k in two halves whose partials meet through the workspace),
+# forced at small shapes; the row-count policy takes arm 5 past 512 rows
 
 
-@pytest.mark.parametrize("arm", [5, 6])
+@pytest.mark.parametrize("arm", [5, 6, 7])
 @pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
 def test_gemm_pingpong_rates(dev, arm, n):
     d = Dense(dev, 700 + n, 300, 1024, 512, n)
@@ -165,7 +166,7 @@ def test_gemm_pingpong_rates(dev, arm, n):
     _hold(got, d, odec, seed=n, what=f"pingpong arm={arm} n={n}")
 
 
-@pytest.mark.parametrize("arm", [5, 6])
+@pytest.mark.parametrize("arm", [5, 6, 7])
 @pytest.mark.parametrize("rows", [17, 257, 700])
 def test_gemm_pingpong_row_tails(dev, arm, rows):
     """Row counts that leave partial 16-row blocks, partial waves and a partial last tile (k spans of 2, 6 and 10
@@ -209,6 +210,39 @@ def test_gemm_pingpong_half_decoder_is_bit_exact(dev, label, n):
     torch.cuda.synchronize()
     for arm, y in outs.items():
         assert torch.equal(y, outs[4]), f"arm {arm} differs from the decode-wave tile ({label} n={n})"
+
+
+def test_gemm_ksplit_repeats_and_groups(dev):
+    """Arm 7 leaves its tile counters at zero: the same call twice gives the same output bit for bit (the two halves
+    meet in a sum of two, whichever arrives last), GEMV calls that share the zeroed region run between them, and a
+    grouped call (two weight groups, their own counters) holds the bar per group."""
+    d = Dense(dev, 740, 640, 1024, 768, 48)
+    dec, odec = DECODES["3inst"]
+    with exl3.arm_overrides(gemm_arm=7):
+        y1 = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32)
+        g = Dense(dev, 741, 3, 1024, 768, 48)
+        exl3.linear(g.xd, g.pd, dec)
+        y2 = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32)
+        exl3.linear(g.xd, g.pd, dec)
+        y3 = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)
+    with exl3.arm_overrides(gemm_arm=7):
+        got = d.inner(dec)
+    _hold(got, d, odec, seed=11, what="ksplit repeat")
+    groups, rows, in_f, out_f, n = 2, 40, 512, 384, 48
+    p = synth.proj(742, "ksg", groups, in_f, out_f, n)
+    x = synth.normal(742, "ksg.x", (groups, rows, in_f))
+    pd = exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev))
+    with exl3.arm_overrides(gemm_arm=7):
+        y = exl3.linear_grouped(x.float().to(dev), pd, dec)  # f32 x: f32 outputs (rounded to f16 on input alike)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    for b in range(groups):
+        t = P.truth(P.prepared_rows(x[b].float().numpy(), _u16(p.suh)[b]),
+                    P.decoded(_u16(p.trellis)[b], in_f, out_f, n, odec))
+        why = P.verdict(P.inner_from_output(y[b], _u16(p.svh)[b]), t)
+        assert why is None, f"ksplit group {b}: {why}"
 
 
 def test_gemm_pingpong_equals_decode_wave_tile_at_c3(dev):
