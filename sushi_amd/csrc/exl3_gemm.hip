@@ -477,7 +477,8 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
 constexpr int G5_WAVES = 8;
 constexpr int G5_THREADS = 64 * G5_WAVES;
 constexpr int G5_SLAB = 128 * G2_BP;                                        // halves per slab
-constexpr int G5_LDS = 3 * G5_SLAB * 2;                                     // the slab ring (the epilogue uses none)
+constexpr int G5_SP = 144;  // epilogue stage pitch (halves): the four 16-lane groups' rows land 8 banks apart
+constexpr int G5_LDS = (3 * G5_SLAB * 2 > G5_WAVES * 16 * G5_SP * 2) ? 3 * G5_SLAB * 2 : G5_WAVES * 16 * G5_SP * 2;
 
 template <int FAM, int N, int MT, int KS>
 __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
@@ -680,6 +681,11 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) svc[cb] = h2f(a.svh[sv + cb * 16 + c]);
     const float sg8 = lane_sign<8>(lane), sg4 = lane_sign<4>(lane), sg2 = lane_sign<2>(lane), sg1 = lane_sign<1>(lane);
+    // 16-bit outputs go out through a per-wave LDS stage of 16 rows (the slab ring is free past the last barrier):
+    // one 16-byte store covers four rows' eighths, against a 2-byte store per lane from the lane layout
+    // (and so does any y not 16-byte aligned: then every output goes out straight from the lane layout)
+    const bool wide = a.y_dtype == DT_F32 || (reinterpret_cast<uintptr_t>(a.y) & 15) != 0, bf16 = a.y_dtype == DT_BF16;
+    uint16_t *stage = reinterpret_cast<uint16_t *>(lds) + wave * 16 * G5_SP;
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
 #pragma unroll
@@ -704,16 +710,38 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
             for (int cb = 0; cb < 8; cb += 2) fwht_stage<2>(v[cb], v[cb + 1], sg2);
 #pragma unroll
             for (int cb = 0; cb < 8; cb += 2) fwht_stage<1>(v[cb], v[cb + 1], sg1);
-            const int m = m0 + rb * 16 + 4 * h + i;
-            if (m < a.rows) {
-                const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128 + c;
+            if (wide) {
+                const int m = m0 + rb * 16 + 4 * h + i;
+                if (m < a.rows) {
+                    const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128 + c;
+#pragma unroll
+                    for (int cb = 0; cb < 8; cb++) {
+                        const float y = v[cb] * HAD_SCALE * svc[cb];
+                        if (a.y_dtype == DT_F16) store_act<DT_F16>(a.y, yo + cb * 16, y);
+                        else if (bf16) store_act<DT_BF16>(a.y, yo + cb * 16, y);
+                        else store_act<DT_F32>(a.y, yo + cb * 16, y);
+                    }
+                }
+            } else {
 #pragma unroll
                 for (int cb = 0; cb < 8; cb++) {
-                    const float y = v[cb] * HAD_SCALE * svc[cb];
-                    if (a.y_dtype == DT_F16) store_act<DT_F16>(a.y, yo + cb * 16, y);
-                    else if (a.y_dtype == DT_BF16) store_act<DT_BF16>(a.y, yo + cb * 16, y);
-                    else store_act<DT_F32>(a.y, yo + cb * 16, y);
+                    // y is rounded to f32 first, as every other output path rounds it (the empty asm keeps the
+                    // product from fusing into the 16-bit conversion, which would round once and differ at ties)
+                    float y = v[cb] * HAD_SCALE * svc[cb];
+                    asm("" : "+v"(y));
+                    stage[(4 * h + i) * G5_SP + cb * 16 + c] =
+                        bf16 ? __bfloat16_as_ushort(__float2bfloat16(y)) : __half_as_ushort(__float2half_rn(y));
                 }
+            }
+        }
+        if (!wide) {  // the wave's 16 rows, row-major in its LDS region: four rows per 16-byte store
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int rr = 4 * q + (lane >> 4), m = m0 + rb * 16 + rr;
+                const uint4 val = *reinterpret_cast<const uint4 *>(stage + rr * G5_SP + (lane & 15) * 8);
+                if (m < a.rows)
+                    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + ((size_t)g * a.rows + m) * a.out +
+                                               (size_t)og * 128 + (lane & 15) * 8) = val;
             }
         }
     }

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle as O
-from sushi_amd import exl3, synth
+from sushi_amd import _lib, exl3, synth
 from tests import _parity as P
 
 pytestmark = pytest.mark.gpu
@@ -243,6 +243,34 @@ def test_gemm_ksplit_repeats_and_groups(dev):
                     P.decoded(_u16(p.trellis)[b], in_f, out_f, n, odec))
         why = P.verdict(P.inner_from_output(y[b], _u16(p.svh)[b]), t)
         assert why is None, f"ksplit group {b}: {why}"
+
+
+@pytest.mark.parametrize("arm", [4, 5, 6, 7])
+def test_gemm_16bit_outputs_round_the_f32_outputs(dev, arm):
+    """The GEMM bodies round each f32 output once to y's 16-bit dtype (the ping-pong tile stages 16-bit rows through
+    LDS for wide stores): f16 and bf16 outputs equal the f32 outputs rounded, rows past a 16-row block included; and a
+    y that is not 16-byte aligned (an offset view, through the C ABI) takes the lane-layout stores with the same
+    result."""
+    d = Dense(dev, 750 + arm, 300, 512, 384, 48)
+    dec = DECODES["3inst"][0]
+    with exl3.arm_overrides(gemm_arm=arm):
+        y32 = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32)
+        y16 = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float16)
+        yb = exl3.linear(d.xd, d.pd, dec, out_dtype=torch.bfloat16)
+        rows, out_f = d.xd.shape[0], d.out_f
+        buf = torch.zeros(rows * out_f + 1, dtype=torch.float16, device=dev)
+        yo = buf[1:].view(rows, out_f)  # 2 bytes past a 256-byte boundary
+        L = _lib.load()
+        ws = exl3.workspace.get(d.xd.device, L.exl3_linear_workspace_size(rows, d.in_f, out_f, d.n))
+        f16 = exl3._dt(y16, "y")
+        rc = L.exl3_linear(d.xd.data_ptr(), exl3._dt(d.xd, "x"), rows, d.in_f, out_f, d.pd.trellis.data_ptr(), d.n,
+                           d.pd.suh.data_ptr(), d.pd.svh.data_ptr(), dec.c(), yo.data_ptr(), f16, ws.data_ptr(),
+                           ws.numel(), exl3._stream(dev))
+        assert rc == 0, rc
+    torch.cuda.synchronize()
+    assert torch.equal(y16, y32.half()), f"arm {arm}: f16 outputs differ from the rounded f32 outputs"
+    assert torch.equal(yb, y32.bfloat16()), f"arm {arm}: bf16 outputs differ from the rounded f32 outputs"
+    assert torch.equal(yo, y16), f"arm {arm}: the unaligned output differs"
 
 
 def test_gemm_pingpong_equals_decode_wave_tile_at_c3(dev):
