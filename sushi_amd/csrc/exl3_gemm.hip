@@ -48,8 +48,30 @@ __global__ __launch_bounds__(64) void gemm_prepare_kernel(GemmArgs a) {
 // ---- prepare into MFMA A-fragment order: for 16-row tile rt and 32-k block kb of group g, the 1 KiB at
 // xp[((g * RT + rt) * (in / 32) + kb) * 512] holds lane l = 16h + c's fragment (row 16 rt + c, k = 32 kb + 8h .. +7)
 // at l * 8 halves, so one MFMA wave's load of a fragment is one contiguous 1 KiB.  RT = ceil(rows / 16); rows past
-// the end of the last tile are zeros.  A workgroup (4 waves) prepares 16 rows x one 128-block: each wave runs the
-// FWHT of 4 rows into an LDS tile, then every thread writes one 16-byte fragment.
+// the end of the last tile are zeros.  A workgroup (4 waves) prepares 16 rows x one 128-block: each wave loads its 4
+// rows at once and runs their FWHTs together into an LDS tile, then every thread writes one 16-byte fragment.
+template <int DT>
+__device__ __forceinline__ void prepare_rows4(const GemmArgs &a, int g, int b, int m0, int lane, float u0, float u1,
+                                              float (&v0)[4], float (&v1)[4]) {
+    // the four rows' loads go out together (a loop that loads, transforms and then loads the next row would wait
+    // out one memory round trip per row)
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        const int m = m0 + rr;
+        v0[rr] = v1[rr] = 0.f;
+        if (m < a.rows) {
+            const size_t xi = ((size_t)g * a.rows + m) * a.in + (size_t)b * 128;
+            v0[rr] = load_act<DT>(a.x, xi + lane);
+            v1[rr] = load_act<DT>(a.x, xi + lane + 64);
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        v0[rr] = (DT == DT_F16 ? v0[rr] : f16r(v0[rr])) * u0;
+        v1[rr] = (DT == DT_F16 ? v1[rr] : f16r(v1[rr])) * u1;
+    }
+}
+
 __global__ __launch_bounds__(256) void gemm_prepare_frag_kernel(GemmArgs a) {
     const int b = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -57,29 +79,17 @@ __global__ __launch_bounds__(256) void gemm_prepare_frag_kernel(GemmArgs a) {
     __shared__ __align__(16) uint16_t t[16][128 + 8];
     const size_t si = (size_t)g * a.in + (size_t)b * 128;
     const float u0 = h2f(a.suh[si + lane]), u1 = h2f(a.suh[si + lane + 64]);
+    const int m0 = rt * 16 + wave * 4;
+    float v0[4], v1[4];
+    if (a.x_dtype == DT_F16) prepare_rows4<DT_F16>(a, g, b, m0, lane, u0, u1, v0, v1);
+    else if (a.x_dtype == DT_BF16) prepare_rows4<DT_BF16>(a, g, b, m0, lane, u0, u1, v0, v1);
+    else prepare_rows4<DT_F32>(a, g, b, m0, lane, u0, u1, v0, v1);
+    fwht128_wave_rows<4>(v0, v1, lane);  // rows past the end transform zeros to zeros
+#pragma unroll
     for (int rr = 0; rr < 4; rr++) {
-        const int r = wave * 4 + rr, m = rt * 16 + r;
-        float v0 = 0.f, v1 = 0.f;
-        if (m < a.rows) {
-            const size_t xi = ((size_t)g * a.rows + m) * a.in + (size_t)b * 128;
-            if (a.x_dtype == DT_F16) {
-                v0 = load_act<DT_F16>(a.x, xi + lane);
-                v1 = load_act<DT_F16>(a.x, xi + lane + 64);
-            } else if (a.x_dtype == DT_BF16) {
-                v0 = f16r(load_act<DT_BF16>(a.x, xi + lane));
-                v1 = f16r(load_act<DT_BF16>(a.x, xi + lane + 64));
-            } else {
-                v0 = f16r(load_act<DT_F32>(a.x, xi + lane));
-                v1 = f16r(load_act<DT_F32>(a.x, xi + lane + 64));
-            }
-            v0 *= u0;
-            v1 *= u1;
-            fwht128_wave(v0, v1, lane);
-            v0 *= HAD_SCALE;
-            v1 *= HAD_SCALE;
-        }
-        t[r][lane] = __half_as_ushort(__float2half_rn(v0));
-        t[r][lane + 64] = __half_as_ushort(__float2half_rn(v1));
+        const int r = wave * 4 + rr;
+        t[r][lane] = __half_as_ushort(__float2half_rn(v0[rr] * HAD_SCALE));
+        t[r][lane + 64] = __half_as_ushort(__float2half_rn(v1[rr] * HAD_SCALE));
     }
     __syncthreads();
     const int kq = tid >> 6, c = lane & 15, h = lane >> 4;  // 32-k block kq of this 128-block, fragment lane (c, h)
