@@ -146,35 +146,36 @@ size_t gemm_xp_bytes(int groups, int rows, int in) { return align_up((size_t)gro
 // in halves when that fills the chip; otherwise the decode-wave 256-row tile.  Measured at C3's 4096 x 14336:
 // 512 rows 94.3 -> 91.4 us, 384 rows 91.1 -> 89.2 us on the split tile; 256 rows stay on the decode-wave tile
 // (81.5 against 88.5 us).
-int gemm_arm_for(int groups, int rows, int out) {
+// split_ok = false (a caller whose scratch cannot hold the halves' partials) turns arm 7 into the decode-wave tile.
+int gemm_arm_for(int groups, int rows, int out, bool split_ok = true) {
     const int pinned = knob(EXL3_KNOB_GEMM_ARM, 0);
-    if (pinned) return pinned;
-    return gemm_default_arm(groups, rows, out);
+    const int arm = pinned ? pinned : gemm_default_arm(groups, rows, out);
+    return arm == 7 && !split_ok ? 4 : arm;
 }
 
 // Arm 7 (k in halves) holds both halves' partials after the prepared input, and one counter per tile in the zeroed
 // region; n = 40 never takes it (its reader does not fit the 512-row tile's registers).
-bool gemm_uses_kpart(int groups, int rows, int out, int n) {
+bool gemm_uses_kpart(int groups, int rows, int out, int n, bool split_ok = true) {
     const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 48 || n == 64;
-    return lane_reader && gemm_arm_for(groups, rows, out) == 7 &&
+    return lane_reader && gemm_arm_for(groups, rows, out, split_ok) == 7 &&
            (size_t)groups * ((rows + 511) / 512) * (out / 128) <= kCounterSlots;
 }
 
-size_t gemm_bytes(int groups, int rows, int in, int out, int n) {
+size_t gemm_bytes(int groups, int rows, int in, int out, int n, bool split_ok = true) {
     size_t b = kZeroBytes + gemm_xp_bytes(groups, rows, in);
     const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 40 || n == 48 || n == 64;
     if (!lane_reader) b += align_up((size_t)groups * out * in * 2);  // the transposed f16 copy of other rates
-    if (gemm_uses_kpart(groups, rows, out, n)) b += align_up(gemm_kpart_bytes(groups, rows, out));
+    if (gemm_uses_kpart(groups, rows, out, n, split_ok)) b += align_up(gemm_kpart_bytes(groups, rows, out));
     return b;
 }
 
-size_t linear_ws(int groups, int rows, int in, int out, int n) {
+size_t linear_ws(int groups, int rows, int in, int out, int n, bool split_ok = true) {
     if (rows <= 0) return 0;
     if (rows <= kRowsMax) {
         GemvPlan p = plan_gemv(groups, rows, in, out);
         return p.counters_bytes + p.partial_bytes;
     }
-    return gemm_bytes(groups, rows, in, out, n);
+    return gemm_bytes(groups, rows, in, out, n, split_ok);
 }
 
 // Every refusal of a linear call (all before any HIP call); fam / k receive the decode family and constants.
@@ -196,12 +197,12 @@ int32_t linear_checks(const void *x, int32_t x_dtype, int32_t groups, int32_t ro
 
 int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in, int32_t out,
                     const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
-                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream) {
+                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream, bool split_ok = true) {
     int fam;
     DecodeK k;
     int32_t rc = linear_checks(x, x_dtype, groups, rows, in, out, trellis, n, suh, svh, dec, y, y_dtype, &fam, &k);
     if (rc || rows == 0) return rc;
-    const size_t need = linear_ws(groups, rows, in, out, n);
+    const size_t need = linear_ws(groups, rows, in, out, n, split_ok);
     if (ws_bytes < need || (need && (!ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))))
         return fail(EXL3_ERR_WORKSPACE, "linear: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
     char *w = static_cast<char *>(ws);
@@ -260,8 +261,8 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     g.y = y;
     g.y_dtype = y_dtype;
     g.groups = groups;
-    g.arm = gemm_arm_for(groups, rows, out);
-    if (gemm_uses_kpart(groups, rows, out, n)) {
+    g.arm = gemm_arm_for(groups, rows, out, split_ok);
+    if (gemm_uses_kpart(groups, rows, out, n, split_ok)) {
         g.kpart = reinterpret_cast<float *>(w + kZeroBytes + gemm_xp_bytes(groups, rows, in));
         g.kctr = reinterpret_cast<uint32_t *>(w);
     }
@@ -914,7 +915,10 @@ int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_
     int32_t rc = linear_checks(x, x_dtype, 1, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype,
                                &fam, &k);
     if (rc || rows == 0) return rc;
-    const size_t need = linear_ws(1, rows, in_features, out_features, n);
+    // The static scratch holds every arm's needs but the k-split GEMM's partials past its size: such a call takes
+    // the decode-wave tile instead.
+    const bool split_ok = linear_ws(1, rows, in_features, out_features, n) <= kNoallocScratchBytes;
+    const size_t need = linear_ws(1, rows, in_features, out_features, n, split_ok);
     if (need > kNoallocScratchBytes)
         return fail(EXL3_ERR_WORKSPACE,
                     "linear_noalloc: rows=%d in=%d out=%d n=%d need %zu bytes of scratch, past the static scratch's %zu "
@@ -924,7 +928,7 @@ int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_
     rc = noalloc_scratch(stream, &ws);
     if (rc) return rc;
     return linear_impl(x, x_dtype, 1, rows, in_features, out_features, trellis, n, suh, svh, dec, y, y_dtype, ws,
-                       kNoallocScratchBytes, stream);
+                       kNoallocScratchBytes, stream, split_ok);
 }
 
 int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
