@@ -271,7 +271,8 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
 // read from the slab before its first MFMA.  Each SIMD holds two MFMA waves and one decode wave, so the matrix core
 // has a second wave to issue from and the VALU decodes beside it.  One workgroup barrier per step hands the slab
 // over: after barrier ks + 1 the MFMA waves have finished reading slab ks & 1 and the decode waves have finished
-// writing slab (ks + 1) & 1.  Every weight is decoded once per 256-row tile.
+// writing slab (ks + 1) & 1.  Every weight is decoded once per 256-row tile.  Row groups wholly past the live rows
+// leave before the first barrier.
 constexpr int G2_MT = 256;   // rows per workgroup
 constexpr int G2_BP = 72;    // LDS pitch (halves) of one slab column: 64 k + 8 pad (16-byte aligned rows)
 constexpr int G2_EP = 129;   // epilogue staging pitch (floats)
@@ -354,8 +355,10 @@ __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16
         return;
     }
 
-    // ---- MFMA waves
+    // ---- MFMA waves.  A row group wholly past the live rows (a short window or row tail) has nothing to compute and
+    // leaves at once; like the decode waves' exit, an ended wave no longer counts at the barriers.
     const int m0 = (wave >> 1) * 64, cb0 = (wave & 1) * 4;
+    if (m0 >= rows) return;
     const int c = lane & 15, h = lane >> 4;
     const int RT = (rows + 15) / 16;
     const uint16_t *xfrag[4];
@@ -408,7 +411,7 @@ __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16
         mstep(ks + 1, AY);
     }
 
-    // ---- epilogue (the decode waves have left, so the barriers below join the 8 MFMA waves): per 16-row block, the
+    // ---- epilogue (the decode waves have left, so the barriers below join the live MFMA waves): per 16-row block, the
     // two waves of a row group stage their column halves side by side in LDS, then each hands 8 of the rows on.
     float *ep = reinterpret_cast<float *>(&Bs[0][0]) + (wave >> 1) * 16 * G2_EP;
 #pragma unroll
@@ -759,10 +762,14 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
 
 // ---- the routed GEMM arm: workgroup (og, window w, projection p) runs the tile of window w's rows against its
 // expert's bank and writes the raw inner products to planes[p][slot][out] (the mid / the reduce applies the output
-// transform).  Windows past the count exit before any barrier.
+// transform).  Windows past the count exit before any barrier.  Workgroups go out to the XCDs in turn (L & 7), so
+// the out / 128 column groups of one window are numbered to land on one XCD one after another: they read the same
+// prepared rows, which then come from that XCD's L2 after the first (numbered by the window, each group would pull
+// them through its own XCD's L2).
 template <int FAM, int N>
 __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
-    const int og = blockIdx.x, w = blockIdx.y, p = blockIdx.z;
+    const int nog = a.out / 128, L = blockIdx.x, q = L >> 3;
+    const int og = q % nog, w = (q / nog) * 8 + (L & 7), p = blockIdx.y;
     if ((uint32_t)w >= *a.win.win_count) return;
     const int IT = a.in >> 4, OT = a.out >> 4;
     const int e = (int)min(a.win.win_expert[w], (uint32_t)(a.experts - 1));
@@ -820,19 +827,29 @@ __global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a) {
     __shared__ __align__(16) uint16_t tl[16][128 + 8];
     const size_t si = (size_t)tr.e * a.in + (size_t)b * 128;
     const float u0 = h2f(a.suh[p][si + lane]), u1 = h2f(a.suh[p][si + lane + 64]);
+    // the wave's four rows load together, then transform together (rows past the end stay zeros)
+    float v0[4], v1[4];
+#pragma unroll
     for (int rr = 0; rr < 4; rr++) {
         const int r = wave * 4 + rr;
-        float v0 = 0.f, v1 = 0.f;
+        v0[rr] = v1[rr] = 0.f;
         if (r < tr.rows) {
             const size_t xi = (size_t)(tr.slots[r] / (uint32_t)a.topk) * a.in + (size_t)b * 128;
-            v0 = f16r(load_any(a.x, a.x_dtype, xi + lane)) * u0;
-            v1 = f16r(load_any(a.x, a.x_dtype, xi + lane + 64)) * u1;
-            fwht128_wave(v0, v1, lane);
-            v0 *= HAD_SCALE;
-            v1 *= HAD_SCALE;
+            v0[rr] = load_any(a.x, a.x_dtype, xi + lane);
+            v1[rr] = load_any(a.x, a.x_dtype, xi + lane + 64);
         }
-        tl[r][lane] = __half_as_ushort(__float2half_rn(v0));
-        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1));
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        v0[rr] = f16r(v0[rr]) * u0;
+        v1[rr] = f16r(v1[rr]) * u1;
+    }
+    fwht128_wave_rows<4>(v0, v1, lane);
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        const int r = wave * 4 + rr;
+        tl[r][lane] = __half_as_ushort(__float2half_rn(v0[rr] * HAD_SCALE));
+        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1[rr] * HAD_SCALE));
     }
     __syncthreads();
     tile_to_frag(tl, a.xp[p], t, b, a.in, tid);
@@ -851,33 +868,42 @@ __global__ __launch_bounds__(256) void moe_gemm_mid_kernel(MoeGemmArgs a) {
     const float sg0 = h2f(a.mid_svh[0][si + lane]), sg1 = h2f(a.mid_svh[0][si + lane + 64]);
     const float su0 = h2f(a.mid_svh[1][si + lane]), su1 = h2f(a.mid_svh[1][si + lane + 64]);
     const float sd0 = h2f(a.down_suh[si + lane]), sd1 = h2f(a.down_suh[si + lane + 64]);
+    // the wave's four rows load together (both planes), then each transform runs over all of them at once
+    float g0[4], g1[4], q0[4], q1[4];
+#pragma unroll
     for (int rr = 0; rr < 4; rr++) {
         const int r = wave * 4 + rr;
-        float v0 = 0.f, v1 = 0.f;
+        g0[rr] = g1[rr] = q0[rr] = q1[rr] = 0.f;
         if (r < tr.rows) {
             const size_t pi = (size_t)tr.slots[r] * a.in + (size_t)b * 128;
-            float g0 = a.mid_planes[0][pi + lane], g1 = a.mid_planes[0][pi + lane + 64];
-            float q0 = a.mid_planes[1][pi + lane], q1 = a.mid_planes[1][pi + lane + 64];
-            fwht128_wave(g0, g1, lane);
-            fwht128_wave(q0, q1, lane);
-            g0 *= HAD_SCALE * sg0;
-            g1 *= HAD_SCALE * sg1;
-            q0 *= HAD_SCALE * su0;
-            q1 *= HAD_SCALE * su1;
-            if (a.clamp_limit > 0.f) {
-                g0 = fminf(g0, a.clamp_limit);
-                g1 = fminf(g1, a.clamp_limit);
-                q0 = fminf(fmaxf(q0, -a.clamp_limit), a.clamp_limit);
-                q1 = fminf(fmaxf(q1, -a.clamp_limit), a.clamp_limit);
-            }
-            v0 = silu(g0) * q0 * sd0;
-            v1 = silu(g1) * q1 * sd1;
-            fwht128_wave(v0, v1, lane);
-            v0 *= HAD_SCALE;
-            v1 *= HAD_SCALE;
+            g0[rr] = a.mid_planes[0][pi + lane];
+            g1[rr] = a.mid_planes[0][pi + lane + 64];
+            q0[rr] = a.mid_planes[1][pi + lane];
+            q1[rr] = a.mid_planes[1][pi + lane + 64];
         }
-        tl[r][lane] = __half_as_ushort(__float2half_rn(v0));
-        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1));
+    }
+    fwht128_wave_rows<4>(g0, g1, lane);
+    fwht128_wave_rows<4>(q0, q1, lane);
+    float v0[4], v1[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        float a0 = g0[rr] * (HAD_SCALE * sg0), a1 = g1[rr] * (HAD_SCALE * sg1);
+        float b0 = q0[rr] * (HAD_SCALE * su0), b1 = q1[rr] * (HAD_SCALE * su1);
+        if (a.clamp_limit > 0.f) {
+            a0 = fminf(a0, a.clamp_limit);
+            a1 = fminf(a1, a.clamp_limit);
+            b0 = fminf(fmaxf(b0, -a.clamp_limit), a.clamp_limit);
+            b1 = fminf(fmaxf(b1, -a.clamp_limit), a.clamp_limit);
+        }
+        v0[rr] = silu(a0) * b0 * sd0;
+        v1[rr] = silu(a1) * b1 * sd1;
+    }
+    fwht128_wave_rows<4>(v0, v1, lane);  // rows past the end: silu(0) * 0 = 0, zeros stay zeros
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        const int r = wave * 4 + rr;
+        tl[r][lane] = __half_as_ushort(__float2half_rn(v0[rr] * HAD_SCALE));
+        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1[rr] * HAD_SCALE));
     }
     __syncthreads();
     tile_to_frag(tl, a.xp[0], t, b, a.in, tid);
@@ -896,7 +922,8 @@ hipError_t run_moe_gemm_mid(const MoeGemmArgs &a, hipStream_t s) {
 
 template <int FAM>
 static hipError_t launch_moe_gemm_fam(const MoeGemmArgs &a, int nproj, hipStream_t s) {
-    const dim3 grid((unsigned)(a.out / 128), (unsigned)a.max_windows, (unsigned)nproj);
+    // x: column group and window, the windows rounded up to whole rounds of the 8 XCDs (the extra ones exit)
+    const dim3 grid((unsigned)(a.out / 128) * (unsigned)((a.max_windows + 7) / 8 * 8), (unsigned)nproj);
     switch (a.n) {
     case 16: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 16>), grid, dim3(G4_THREADS), 0, s, a); break;
     case 24: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 24>), grid, dim3(G4_THREADS), 0, s, a); break;

@@ -122,6 +122,7 @@ hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
 // round with the same expert (found by one ballot per bit of the expert id), so the result does not depend on thread
 // timing.
 constexpr int WIN_THREADS = 1024;
+constexpr int GW_CHUNKS = 8;  // ranking waves of the GEMM arm's windows (8 x 1024 experts of u32 counts: 32 KiB of LDS)
 __global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
                                                                   int experts, uint32_t *__restrict__ win_count,
                                                                   uint32_t *__restrict__ win_expert,
@@ -203,21 +204,37 @@ hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32
 // run cut into windows of up to MOE_GEMM_WINDOW_ROWS rows (window i of expert e is wbase[e] + i, starting at sorted
 // position sbase[e] + i * W); and the 16-row fragment tiles of the prepared inputs numbered so that expert e's rows
 // occupy tiles tbase[e] .. tbase[e] + ceil(count / 16) - 1 (a window's tiles are contiguous, from win_tile0).
-// tile_window[t] names the window of tile t.  Ranks come from one wave walking the slots in order, as in
-// moe_windows_kernel.
+// tile_window[t] names the window of tile t.  Ranks come from GW_CHUNKS waves, each walking its contiguous chunk of
+// the slots in order from the chunk's per-expert prefix.
 __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
                                                                        int experts, MoeGemmWindows t) {
+    // The slots are cut into GW_CHUNKS contiguous chunks, one per ranking wave: per-chunk counts by LDS atomics, their
+    // exclusive prefix over chunks per expert, then each wave ranks its own chunk in order (a single wave walking
+    // every slot waits out one load round trip per 64 slots: 90 us for 16384 slots).
+    __shared__ uint32_t ccnt[GW_CHUNKS][kMoeGemmMaxExperts];  // counts, then the chunk's first rank per expert
     __shared__ uint32_t cnt[kMoeGemmMaxExperts];
-    __shared__ uint32_t fill[kMoeGemmMaxExperts];
     __shared__ uint32_t sb[kMoeGemmMaxExperts];
     __shared__ uint32_t tb[kMoeGemmMaxExperts];
     __shared__ uint32_t wb[kMoeGemmMaxExperts];
     __shared__ uint32_t part[3][WIN_THREADS];
     constexpr uint32_t W = MOE_GEMM_WINDOW_ROWS;
     const int tid = threadIdx.x;
-    for (int e = tid; e < experts; e += WIN_THREADS) cnt[e] = fill[e] = 0;
+    const int chunk = (((nslots + GW_CHUNKS - 1) / GW_CHUNKS) + 63) / 64 * 64;  // slots per chunk, whole groups of 64
+    for (int e = tid; e < experts; e += WIN_THREADS)
+        for (int c = 0; c < GW_CHUNKS; c++) ccnt[c][e] = 0;
     __syncthreads();
-    for (int s = tid; s < nslots; s += WIN_THREADS) atomicAdd(&cnt[min(inds[s], (uint32_t)(experts - 1))], 1u);
+    for (int s = tid; s < nslots; s += WIN_THREADS)
+        atomicAdd(&ccnt[s / chunk][min(inds[s], (uint32_t)(experts - 1))], 1u);
+    __syncthreads();
+    for (int e = tid; e < experts; e += WIN_THREADS) {
+        uint32_t run = 0;
+        for (int c = 0; c < GW_CHUNKS; c++) {
+            const uint32_t v = ccnt[c][e];
+            ccnt[c][e] = run;
+            run += v;
+        }
+        cnt[e] = run;
+    }
     __syncthreads();
     // three exclusive scans over experts (slots, 16-row tiles, windows): each thread sums a contiguous run
     const int per = (experts + WIN_THREADS - 1) / WIN_THREADS;
@@ -253,13 +270,17 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
         *t.tile_count = part[1][tid];
     }
     __syncthreads();
-    if (tid < 64) {  // wave 0 ranks the slots in order
-        const int lane = tid;
+    const int wave = tid >> 6;
+    if (wave < GW_CHUNKS) {  // wave c ranks chunk c in slot order; the next group's indices load under this one's work
+        const int lane = tid & 63;
         const int id_bits = experts > 1 ? 32 - __clz(experts - 1) : 0;
-        for (int base = 0; base < nslots; base += 64) {
+        const int c0 = wave * chunk, c1 = min(c0 + chunk, nslots);
+        uint32_t next = c0 + lane < c1 ? inds[c0 + lane] : 0u;
+        for (int base = c0; base < c1; base += 64) {
             const int s = base + lane;
-            const bool live = s < nslots;
-            const int e = live ? (int)min(inds[s], (uint32_t)(experts - 1)) : 0;
+            const bool live = s < c1;
+            const int e = live ? (int)min(next, (uint32_t)(experts - 1)) : 0;
+            next = base + 64 + lane < c1 ? inds[base + 64 + lane] : 0u;
             unsigned long long same = __ballot(live);
             for (int b = 0; b < id_bits; b++) {
                 const unsigned long long set = __ballot((e >> b) & 1);
@@ -269,7 +290,7 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
             const uint32_t before = (uint32_t)__popcll(same & below);
             const bool last = live && (same & ~below & ~(1ull << lane)) == 0ull;
             if (live) {
-                const uint32_t rank = fill[e] + before;
+                const uint32_t rank = ccnt[wave][e] + before;
                 t.sorted[sb[e] + rank] = (uint32_t)s;
                 if (rank % W == 0) {  // the first slot of a window writes its row
                     const uint32_t w = wb[e] + rank / W, rows = min(cnt[e] - rank, W);
@@ -280,8 +301,11 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
                     t.win_tile0[w] = tile0;
                     for (uint32_t i = 0; i < (rows + 15) / 16; i++) t.tile_window[tile0 + i] = w;
                 }
-                if (last) fill[e] = rank + 1;
             }
+            // every lane has read this group's ranks before the group's last lane per expert moves them on
+            __builtin_amdgcn_wave_barrier();
+            if (last) ccnt[wave][e] = ccnt[wave][e] + before + 1;
+            __builtin_amdgcn_wave_barrier();
         }
     }
 }
