@@ -66,51 +66,66 @@ __device__ __forceinline__ float round_to(int dt, float v) {
     return v;
 }
 
-// One workgroup per (128-block, row): wave w handles slots w, w + RW, ... (sum of the slot's k splits, FWHT, svh,
-// score) into LDS, in parallel; wave 0 then adds the slots in slot order (the reference's order) and finishes.
+// One workgroup per (row, RB consecutive 128-blocks): wave w handles slots w, w + RW, ... (sum of the slot's k
+// splits, FWHT, svh, score) for all its blocks into LDS, the blocks' loads first and their transforms together; then
+// every thread adds the slots of its columns in slot order (the reference's order) and finishes.  (One block per
+// workgroup ran 82 us for 2048 rows x 8 slots x 2048 columns: 32768 workgroups each reading 4 KiB.)
 constexpr int RW = 8;
+constexpr int RB = 4;
 __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
-    const int blk = blockIdx.x, row = blockIdx.y;
+    const int row = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t base = (size_t)blk * 128;
-    __shared__ float contrib[kMoeReduceMaxTopk][128];
+    const int nb = min(RB, a.hidden / 128 - (int)blockIdx.x * RB);  // this workgroup's blocks
+    const size_t base = (size_t)blockIdx.x * RB * 128;
+    extern __shared__ float contrib[];  // [topk][RB * 128]
     for (int kk = wave; kk < a.topk; kk += RW) {
         const int slot = row * a.topk + kk;
         const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
         const float sc = load_any(a.scores, a.score_dtype, slot);
         const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
-        const float s0 = h2f(sv[lane]), s1 = h2f(sv[lane + 64]);
-        float v0, v1;
-        sum_planes<false>(a.part + (size_t)slot * a.splits * a.hidden + base, a.hidden, a.splits, lane, v0, v1);
-        fwht128_wave(v0, v1, lane);
-        contrib[kk][lane] = (v0 * HAD_SCALE * s0) * sc;
-        contrib[kk][lane + 64] = (v1 * HAD_SCALE * s1) * sc;
+        const float *pl = a.part + (size_t)slot * a.splits * a.hidden + base;
+        float v0[RB], v1[RB];
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            v0[b] = v1[b] = 0.f;
+            if (b < nb) {
+                if (a.splits == 1) {  // sum_planes' sum of one plane (0 + x), without its eight-split batch of loads
+                    v0[b] += pl[b * 128 + lane];
+                    v1[b] += pl[b * 128 + lane + 64];
+                } else {
+                    sum_planes<false>(pl + b * 128, a.hidden, a.splits, lane, v0[b], v1[b]);
+                }
+            }
+        }
+        fwht128_wave_rows<RB>(v0, v1, lane);
+#pragma unroll
+        for (int b = 0; b < RB; b++)
+            if (b < nb) {
+                const float s0 = h2f(sv[b * 128 + lane]), s1 = h2f(sv[b * 128 + lane + 64]);
+                contrib[kk * RB * 128 + b * 128 + lane] = (v0[b] * HAD_SCALE * s0) * sc;
+                contrib[kk * RB * 128 + b * 128 + lane + 64] = (v1[b] * HAD_SCALE * s1) * sc;
+            }
     }
     __syncthreads();
-    if (wave != 0) return;
-    float y0 = 0.f, y1 = 0.f;
-    for (int kk = 0; kk < a.topk; kk++) {
-        y0 += contrib[kk][lane];
-        y1 += contrib[kk][lane + 64];
-    }
-    const size_t yo = (size_t)row * a.hidden + base;
-    if (a.shared) {
-        float s0 = load_any(a.shared, a.y_dtype, yo + lane), s1 = load_any(a.shared, a.y_dtype, yo + lane + 64);
-        if (a.gate) {  // sigmoid(gate) * shared in y's dtype (REDUCE_GATED_SHARED_SOURCE)
-            const float g = load_any(a.gate, a.y_dtype, row);
-            s0 = gated_shared(a.y_dtype, g, s0);
-            s1 = gated_shared(a.y_dtype, g, s1);
+    const float g = a.shared && a.gate ? load_any(a.gate, a.y_dtype, row) : 0.f;
+    for (int col = threadIdx.x; col < nb * 128; col += 64 * RW) {
+        float y = 0.f;
+        for (int kk = 0; kk < a.topk; kk++) y += contrib[kk * RB * 128 + col];
+        const size_t yo = (size_t)row * a.hidden + base + col;
+        if (a.shared) {
+            float sh = load_any(a.shared, a.y_dtype, yo);
+            if (a.gate) sh = gated_shared(a.y_dtype, g, sh);  // sigmoid(gate) * shared in y's dtype
+            y = round_to(a.y_dtype, y) + sh;
         }
-        y0 = round_to(a.y_dtype, y0) + s0;
-        y1 = round_to(a.y_dtype, y1) + s1;
+        store_out(a.y, a.y_dtype, yo, y);
     }
-    store_out(a.y, a.y_dtype, yo + lane, y0);
-    store_out(a.y, a.y_dtype, yo + lane + 64, y1);
 }
 
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
     if (a.topk > kMoeReduceMaxTopk) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_reduce_kernel, dim3((unsigned)(a.hidden / 128), (unsigned)a.rows), dim3(64 * RW), 0, s, a);
+    const unsigned nbk = (unsigned)((a.hidden / 128 + RB - 1) / RB);
+    hipLaunchKernelGGL(moe_reduce_kernel, dim3(nbk, (unsigned)a.rows), dim3(64 * RW),
+                       (size_t)a.topk * RB * 128 * sizeof(float), s, a);
     return hipGetLastError();
 }
 

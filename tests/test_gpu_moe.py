@@ -318,7 +318,8 @@ def test_moe_with_shared_bank_is_the_two_calls(dev, rows, dtype, limit):
 @pytest.mark.parametrize("rows", [17, 40])
 def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
     """Past 8 rows the fused form runs in the expert-window launches (the C ABI does not decline) and equals the two
-    calls at the bar."""
+    calls at the bar.  The GEMM arm is held off: at 40 rows (10 slots per expert) the layer would take it, and the fused
+    form declines that arm."""
     E, hidden, inter, k, n = 16, 256, 128, 4, 32
     b = synth.bank(35, "msw", E, hidden, inter, n)
     s = synth.bank(35, "msw.shared", 1, hidden, inter, n)
@@ -334,11 +335,13 @@ def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
     ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
     y = torch.empty_like(xd)
     x2 = xd.contiguous()
-    rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
-                                     y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
-    assert rc == 0, exl3._lib.last_error()
-    ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
+    with exl3.arm_overrides(moe_gemm=0):
+        rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
+                                         ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
+                                         y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(),
+                                         exl3._stream(dev))
+        assert rc == 0, exl3._lib.last_error()
+        ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
     torch.cuda.synchronize()
     assert max_abs_rel(y.float().cpu().numpy(), ref.float().cpu().numpy()) < BAR
 
