@@ -429,7 +429,7 @@ def bench_pack(pair_major: bool, experts: int = 256, hidden: int = 2048, inter: 
         shutil.rmtree(root, ignore_errors=True)
 
 
-def sweep(which: str):
+def sweep(which: str, prefill_batches=None, prefill_arms=("gemm", "windows")):
     """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
     one JSON line per case."""
     from sushi_amd import exl3
@@ -448,7 +448,10 @@ def sweep(which: str):
         for line in bench_moe_c5_tiled():
             print(json.dumps(line), flush=True)
     if which in ("moe_prefill", "all"):
-        bench_moe_prefill()
+        if prefill_batches:
+            bench_moe_prefill(prefill_batches, arms=prefill_arms)
+        else:
+            bench_moe_prefill(arms=prefill_arms)
     if which in ("pack", "all"):
         for pm in (False, True):
             print(json.dumps(bench_pack(pm)), flush=True)
@@ -610,7 +613,7 @@ def bench_moe_c5_tiled(batch: int = 64, layers: int = 4):
     return lines
 
 
-def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4):
+def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4, arms=("gemm", "windows")):
     """configs[3]'s layer (E=256 + shared, hidden 2048, inter 768, K2 MCG, top-8) at prefill widths, on the routed
     GEMM arm and on the decode chain's expert windows (arm overrides): microseconds per layer and per token, each a
     median of 7 replays of `layers` layers from a HIP graph."""
@@ -631,6 +634,8 @@ def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4):
                                          .to(dev), k) for l in range(layers)]
         line = {"config": "c4_prefill", "batch": batch, "slots_per_expert": round(batch * k / E, 2)}
         for arm, knob in (("gemm", 1), ("windows", 0)):
+            if arm not in arms:
+                continue
             with exl3.arm_overrides(moe_gemm=knob):
                 def chain():
                     return [exl3.moe_with_shared_bank(x, bank, shared, i, s, exl3.MCG)
@@ -795,11 +800,14 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
     ap.add_argument("--sweep", choices=("c2", "c3", "c5", "moe_prefill", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
+    ap.add_argument("--prefill-batches", default="", help="moe_prefill sweep: token counts (default 64 .. 2048)")
+    ap.add_argument("--prefill-arms", default="gemm,windows", help="moe_prefill sweep: arms to time")
     args = ap.parse_args()
     if args.sweep:
         global SWEEP_GRAPHS
         SWEEP_GRAPHS = not args.no_graph
-        sweep(args.sweep)
+        pb = tuple(int(b) for b in args.prefill_batches.split(",") if b)
+        sweep(args.sweep, pb or None, tuple(a for a in args.prefill_arms.split(",") if a))
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
