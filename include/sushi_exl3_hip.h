@@ -248,10 +248,12 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
  * one-expert bank (trellis [1][hidden/16][inter/16][n] for gate/up, [1][inter/16][hidden/16][n] for down) with the
  * routed layer's inter; clamp_limit applies to both.  Up to 8 rows the shared rows join the per-slot launches;
  * wider batches the sorted (expert-window) launches, where the shared rows are windows of their own (three launches
- * in all instead of six).  Returns EXL3_DECLINED (nothing launched) where the fused form does not serve: y dtype f32,
- * routed projections at different rates, a shared rate other than the routed one (uniform banks), rows whose
- * routed, shared and combine fold words (3 x rows x hidden) exceed the fused finish's region, or more fold arrivals
- * than it holds; the caller then makes the two calls.  The _ragged form takes
+ * in all instead of six); at prefill widths (the routed GEMM arm, from 8 slots per expert on a uniform bank) the
+ * shared expert is one more expert of the GEMM arm's launches, its rows extra slots, any y dtype, and y equals the
+ * pair of calls bit for bit.  Returns EXL3_DECLINED (nothing launched) where the fused form does not serve: y dtype
+ * f32 off the GEMM arm, routed projections at different rates, a shared rate other than the routed one (uniform
+ * banks), rows whose routed, shared and combine fold words (3 x rows x hidden) exceed the fused finish's region, or
+ * more fold arrivals than it holds; the caller then makes the two calls.  The _ragged form takes
  * `moeRagged`'s rate-grouped bank (src/exl3/root.zig:582-644); its shared bank keeps its own rate. */
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,

@@ -385,13 +385,13 @@ struct SharedBank {
     int n;
 };
 
-// The shared bank's rows need the per-slot arm, a 16-bit output dtype (the combine word holds both rounded sums),
-// the routed and shared folds (routed, shared and combine words: three per output), and, for a uniform bank, the
-// routed rate.
+// On the GEMM arm the shared bank's rows join as one more expert (any y dtype).  Otherwise they need the per-slot
+// arm, a 16-bit output dtype (the combine word holds both rounded sums), the routed and shared folds (routed, shared
+// and combine words: three per output), and, for a uniform bank, the routed rate.
 bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts, int n) {
     const int nslots = rows * topk;
+    if (moe_gemm_wanted(nslots, experts, lane_rate(n))) return experts < kMoeGemmMaxExperts;
     if (y_dtype == EXL3_DT_F32) return false;
-    if (moe_gemm_wanted(nslots, experts, lane_rate(n))) return false;  // the GEMM arm serves such layers
     const bool windowed = rows > moe_decode_rows_max();
     if (windowed && !(moe_windows_enabled() && moe_windowed(rows, nslots, experts))) return false;
     const MoePlan p = plan_moe(nslots, hidden, inter, windowed, rows);
@@ -417,8 +417,11 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
                    const TiledTables *tt = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    if (!sb && !meta && !tt && n[0] == n[1] && n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
-        const MoeGemmPlan gp = plan_moe_gemm(nslots, hidden, inter, experts);
+    if ((!sb || (sb->n == n[0] && !shared && experts < kMoeGemmMaxExperts)) && !meta && !tt && n[0] == n[1] &&
+        n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
+        // a shared bank's rows are slots nslots .. nslots + rows - 1 of one more expert (index `experts`)
+        const int sh_rows = sb ? rows : 0;
+        const MoeGemmPlan gp = plan_moe_gemm(nslots + sh_rows, hidden, inter, experts + (sb ? 1 : 0));
         if (ws_bytes < gp.total() || !ws || (reinterpret_cast<uintptr_t>(ws) % kAlign))
             return fail(EXL3_ERR_WORKSPACE, "moe: workspace of %zu bytes (256-aligned) needed, got %zu", gp.total(),
                         ws_bytes);
@@ -432,7 +435,7 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         uint32_t *counts = reinterpret_cast<uint32_t *>(take(align_up(2 * sizeof(uint32_t))));
         g.win.win_count = counts;
         g.win.tile_count = counts + 1;
-        g.win.sorted = reinterpret_cast<uint32_t *>(take(align_up((size_t)nslots * 4)));
+        g.win.sorted = reinterpret_cast<uint32_t *>(take(align_up((size_t)(nslots + sh_rows) * 4)));
         g.win.win_expert = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
         g.win.win_rows = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
         g.win.win_start = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
@@ -444,12 +447,14 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         float *pl_g = reinterpret_cast<float *>(take(gp.planes_gu));
         float *pl_u = reinterpret_cast<float *>(take(gp.planes_gu));
         float *pl_d = reinterpret_cast<float *>(take(gp.planes_down));
-        hipError_t e = run_moe_gemm_windows(inds, nslots, experts, g.win, stream);
+        hipError_t e = run_moe_gemm_windows(inds, nslots, experts, sh_rows, g.win, stream);
         if (e != hipSuccess) return launched(e, "exl3_moe (gemm windows)");
         g.x = x;
         g.x_dtype = x_dtype;
         g.topk = topk;
         g.experts = experts;
+        g.nslots = nslots;
+        g.sh = sb ? 1 : 0;
         g.n = n[0];
         g.k = k;
         g.clamp_limit = (float)clamp_limit;
@@ -461,6 +466,8 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         for (int i = 0; i < 2; i++) {
             g.trellis[i] = tr[i];
             g.suh[i] = su[i];
+            g.sh_trellis[i] = sb ? sb->tr[i] : nullptr;
+            g.sh_suh[i] = sb ? sb->su[i] : nullptr;
         }
         g.xp[0] = xp_g;
         g.xp[1] = xp_u;
@@ -480,6 +487,12 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         d.mid_svh[1] = sv[1];
         d.down_suh = su[2];
         d.trellis[0] = tr[2];
+        if (sb) {
+            d.sh_mid_svh[0] = sb->sv[0];
+            d.sh_mid_svh[1] = sb->sv[1];
+            d.sh_down_suh = sb->su[2];
+            d.sh_trellis[0] = sb->tr[2];
+        }
         d.xp[0] = xp_d;
         d.planes[0] = pl_d;
         e = run_moe_gemm_mid(d, stream);
@@ -500,6 +513,8 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         r.svh = sv[2];
         r.shared = shared;
         r.gate = shared ? shared_gate : nullptr;
+        r.sh_part = sb ? pl_d + (size_t)nslots * hidden : nullptr;
+        r.sh_svh = sb ? sb->sv[2] : nullptr;
         r.y = y;
         r.y_dtype = y_dtype;
         r.out_scale = 1.0f;
@@ -998,6 +1013,10 @@ size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int3
     const size_t routed = exl3_moe_workspace_size(rows, topk, hidden, inter);
     if (routed == 0) return 0;
     size_t need = std::max(routed, plan_moe(rows * topk, hidden, inter, false, rows).total());
+    // the GEMM arm with the shared rows as one more expert's slots
+    const int gk = knob(EXL3_KNOB_MOE_GEMM, -1);
+    if (gk > 0 || (gk != 0 && rows * topk >= kMoeGemmMinSlotsPerExpert))
+        need = std::max(need, plan_moe_gemm(rows * topk + rows, hidden, inter, kMoeGemmMaxExperts).total());
     if (moe_windowed(rows, rows * topk, 1)) need = std::max(need, plan_moe(rows * topk, hidden, inter, true, rows).total());
     return need;
 }

@@ -760,6 +760,15 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
     }
 }
 
+// Expert index of a window (routed ones clamped below `experts`; with a shared expert, `experts` is it) and the token
+// row of a slot (routed slot s is token s / topk, shared slot nslots + r is token r).
+__device__ __forceinline__ int moe_expert(const MoeGemmArgs &a, uint32_t e) {
+    return (int)min(e, (uint32_t)(a.experts - 1 + a.sh));
+}
+__device__ __forceinline__ uint32_t moe_token(const MoeGemmArgs &a, uint32_t slot) {
+    return slot < (uint32_t)a.nslots ? slot / (uint32_t)a.topk : slot - (uint32_t)a.nslots;
+}
+
 // ---- the routed GEMM arm: workgroup (og, window w, projection p) runs the tile of window w's rows against its
 // expert's bank and writes the raw inner products to planes[p][slot][out] (the mid / the reduce applies the output
 // transform).  Windows past the count exit before any barrier.  Workgroups go out to the XCDs in turn (L & 7), so
@@ -772,13 +781,14 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     const int og = q % nog, w = (q / nog) * 8 + (L & 7), p = blockIdx.y;
     if ((uint32_t)w >= *a.win.win_count) return;
     const int IT = a.in >> 4, OT = a.out >> 4;
-    const int e = (int)min(a.win.win_expert[w], (uint32_t)(a.experts - 1));
+    const int e = moe_expert(a, a.win.win_expert[w]);
     const int rows = (int)min(a.win.win_rows[w], (uint32_t)G2_MT);
     const uint32_t *slots = a.win.sorted + a.win.win_start[w];
     __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
     const uint16_t *xfrag0 = a.xp[p] + (size_t)a.win.win_tile0[w] * (size_t)(a.in / 32) * 512;
     float *planes = a.planes[p];
-    gemm4_tile<FAM, N>(a.in, a.out, og, a.trellis[p] + (size_t)e * IT * OT * N, xfrag0, rows, a.k, Bs,
+    const uint16_t *bank = e < a.experts ? a.trellis[p] + (size_t)e * IT * OT * N : a.sh_trellis[p];
+    gemm4_tile<FAM, N>(a.in, a.out, og, bank, xfrag0, rows, a.k, Bs,
                        [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
                            for (int i = 0; i < live; i++) {
                                float *row = planes + (size_t)slots[m + i] * a.out + (size_t)og * 128;
@@ -805,7 +815,7 @@ __device__ __forceinline__ TileRows tile_rows(const MoeGemmArgs &a, int t) {
     const uint32_t w = a.win.tile_window[t];
     const int i = t - (int)a.win.win_tile0[w];
     r.rows = min(16, (int)a.win.win_rows[w] - 16 * i);
-    r.e = (int)min(a.win.win_expert[w], (uint32_t)(a.experts - 1));
+    r.e = moe_expert(a, a.win.win_expert[w]);
     r.slots = a.win.sorted + a.win.win_start[w] + 16 * i;
     return r;
 }
@@ -828,14 +838,15 @@ __global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a, in
     if (!tr.live) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ __align__(16) uint16_t tl[2][16][128 + 8];
-    const size_t si = (size_t)tr.e * a.in + (size_t)b * 128;
+    const bool shx = tr.e >= a.experts;
+    const size_t si = (shx ? 0 : (size_t)tr.e * a.in) + (size_t)b * 128;
     float x0[4], x1[4];
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) {
         const int r = wave * 4 + rr;
         x0[rr] = x1[rr] = 0.f;
         if (r < tr.rows) {
-            const size_t xi = (size_t)(tr.slots[r] / (uint32_t)a.topk) * a.in + (size_t)b * 128;
+            const size_t xi = (size_t)moe_token(a, tr.slots[r]) * a.in + (size_t)b * 128;
             x0[rr] = f16r(load_any(a.x, a.x_dtype, xi + lane));
             x1[rr] = f16r(load_any(a.x, a.x_dtype, xi + lane + 64));
         }
@@ -844,7 +855,8 @@ __global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a, in
 #pragma unroll
     for (int q = 0; q < 2; q++) {
         const bool on = q < nproj;
-        const float u0 = on ? h2f(a.suh[q][si + lane]) : 0.f, u1 = on ? h2f(a.suh[q][si + lane + 64]) : 0.f;
+        const uint16_t *su = shx ? a.sh_suh[q] : a.suh[q];
+        const float u0 = on ? h2f(su[si + lane]) : 0.f, u1 = on ? h2f(su[si + lane + 64]) : 0.f;
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) {
             v0[q * 4 + rr] = x0[rr] * u0;
@@ -873,10 +885,13 @@ __global__ __launch_bounds__(256) void moe_gemm_mid_kernel(MoeGemmArgs a) {
     if (!tr.live) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ __align__(16) uint16_t tl[16][128 + 8];
-    const size_t si = (size_t)tr.e * a.in + (size_t)b * 128;
-    const float sg0 = h2f(a.mid_svh[0][si + lane]), sg1 = h2f(a.mid_svh[0][si + lane + 64]);
-    const float su0 = h2f(a.mid_svh[1][si + lane]), su1 = h2f(a.mid_svh[1][si + lane + 64]);
-    const float sd0 = h2f(a.down_suh[si + lane]), sd1 = h2f(a.down_suh[si + lane + 64]);
+    const bool shx = tr.e >= a.experts;  // the shared expert's rows: its own scales
+    const size_t si = (shx ? 0 : (size_t)tr.e * a.in) + (size_t)b * 128;
+    const uint16_t *svg = shx ? a.sh_mid_svh[0] : a.mid_svh[0], *svu = shx ? a.sh_mid_svh[1] : a.mid_svh[1];
+    const uint16_t *sud = shx ? a.sh_down_suh : a.down_suh;
+    const float sg0 = h2f(svg[si + lane]), sg1 = h2f(svg[si + lane + 64]);
+    const float su0 = h2f(svu[si + lane]), su1 = h2f(svu[si + lane + 64]);
+    const float sd0 = h2f(sud[si + lane]), sd1 = h2f(sud[si + lane + 64]);
     // the wave's four rows load together (both planes), then each transform runs over all of them at once
     float g0[4], g1[4], q0[4], q1[4];
 #pragma unroll

@@ -171,6 +171,10 @@ struct ReduceArgs {
     const uint16_t *svh;  // [E][hidden]
     const void *shared;   // [rows][hidden] in y dtype, or null
     const void *gate;     // [rows] in y dtype: shared is added as sigmoid(gate) * shared; null = plain add
+    // or a shared expert's raw down planes [rows][hidden] and svh (shared null): its score-1 term, rounded to y's
+    // dtype as a one-expert layer's output, is added as `shared` would be
+    const float *sh_part;
+    const uint16_t *sh_svh;
     void *y;
     int y_dtype;
     float out_scale;
@@ -198,22 +202,28 @@ struct MoeGemmWindows {
     uint32_t *win_tile0;    // [windows] first fragment tile
     uint32_t *tile_window;  // [tiles] the window of each tile
 };
-hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, const MoeGemmWindows &t,
+// sh_rows > 0 adds a shared expert as expert `experts`: slots nslots .. nslots + sh_rows - 1, one per token row.
+hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, int sh_rows, const MoeGemmWindows &t,
                                 hipStream_t s);
 
 // The routed GEMM arm (a prefill-width layer: every expert's rows in windows of up to 256, each weight decoded once
 // per window on the matrix cores).  Projection p of grid z: x prepared per window row with that expert's suh into
 // xp[p] (fragment order, tile t at xp + t * (in / 32) * 512), the raw inner products written to planes[p]
-// [slot][out] (f32, no output transform: the mid / the reduce applies it).
+// [slot][out] (f32, no output transform: the mid / the reduce applies it).  With sh = 1 a shared expert is expert
+// `experts`, its banks in the sh_ pointers and its rows the slots from nslots on (slot nslots + r is token row r).
 struct MoeGemmArgs {
     MoeGemmWindows win;
-    const void *x;          // [tokens][hidden] (gate/up) -- the token of slot s is s / topk
+    const void *x;          // [tokens][hidden] (gate/up) -- the token of routed slot s is s / topk
     int x_dtype;
     int topk;
     int in, out;
     int experts;
+    int nslots;             // routed slots
+    int sh;                 // 1: a shared expert follows the routed ones
     const uint16_t *trellis[2];
     const uint16_t *suh[2];
+    const uint16_t *sh_trellis[2];
+    const uint16_t *sh_suh[2];
     int n;
     DecodeK k;
     uint16_t *xp[2];        // prepared inputs, fragment order
@@ -222,6 +232,8 @@ struct MoeGemmArgs {
     const float *mid_planes[2];
     const uint16_t *mid_svh[2];
     const uint16_t *down_suh;
+    const uint16_t *sh_mid_svh[2];
+    const uint16_t *sh_down_suh;
     float clamp_limit;
     int max_tiles;          // grid bound: tiles over all windows
     int max_windows;        // grid bound: windows

@@ -66,10 +66,11 @@ __device__ __forceinline__ float round_to(int dt, float v) {
     return v;
 }
 
-// One workgroup per (row, RB consecutive 128-blocks): wave w handles slots w, w + RW, ... (sum of the slot's k
-// splits, FWHT, svh, score) for all its blocks into LDS, the blocks' loads first and their transforms together; then
-// every thread adds the slots of its columns in slot order (the reference's order) and finishes.  (One block per
-// workgroup ran 82 us for 2048 rows x 8 slots x 2048 columns: 32768 workgroups each reading 4 KiB.)
+// One workgroup per (row, RB consecutive 128-blocks): wave w handles items w, w + RW, ... (the slots, and a shared
+// expert's term: sum of the slot's k splits, FWHT, svh, score) for all its blocks into LDS, the blocks' loads first
+// and their transforms together; then every thread adds the slots of its columns in slot order (the reference's
+// order) and finishes.  (One block per workgroup ran 82 us for 2048 rows x 8 slots x 2048 columns: 32768 workgroups
+// each reading 4 KiB; a ninth wave for a shared expert's term ran slower than eight waves taking nine items.)
 constexpr int RW = 8;
 constexpr int RB = 4;
 __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
@@ -77,13 +78,23 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = min(RB, a.hidden / 128 - (int)blockIdx.x * RB);  // this workgroup's blocks
     const size_t base = (size_t)blockIdx.x * RB * 128;
-    extern __shared__ float contrib[];  // [topk][RB * 128]
-    for (int kk = wave; kk < a.topk; kk += RW) {
-        const int slot = row * a.topk + kk;
-        const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
-        const float sc = load_any(a.scores, a.score_dtype, slot);
-        const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
-        const float *pl = a.part + (size_t)slot * a.splits * a.hidden + base;
+    extern __shared__ float contrib[];  // [topk (+ 1: a shared expert's term)][RB * 128]
+    const int items = a.topk + (a.sh_part ? 1 : 0);
+    for (int kk = wave; kk < items; kk += RW) {
+        const uint16_t *sv;
+        const float *pl;
+        float sc;
+        if (kk < a.topk) {
+            const int slot = row * a.topk + kk;
+            const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
+            sc = load_any(a.scores, a.score_dtype, slot);
+            sv = a.svh + (size_t)e * a.hidden + base;
+            pl = a.part + (size_t)slot * a.splits * a.hidden + base;
+        } else {  // the shared expert, a one-expert layer's slot: score 1, its own planes (one split)
+            sc = 1.0f;
+            sv = a.sh_svh + base;
+            pl = a.sh_part + (size_t)row * a.splits * a.hidden + base;
+        }
         float v0[RB], v1[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
@@ -116,6 +127,9 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
             float sh = load_any(a.shared, a.y_dtype, yo);
             if (a.gate) sh = gated_shared(a.y_dtype, g, sh);  // sigmoid(gate) * shared in y's dtype
             y = round_to(a.y_dtype, y) + sh;
+        } else if (a.sh_part) {  // as the one-expert layer rounds its output, then as `shared` above
+            const float sh = round_to(a.y_dtype, 0.f + contrib[a.topk * RB * 128 + col]);
+            y = round_to(a.y_dtype, y) + sh;
         }
         store_out(a.y, a.y_dtype, yo, y);
     }
@@ -124,8 +138,9 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
     if (a.topk > kMoeReduceMaxTopk) return hipErrorInvalidValue;
     const unsigned nbk = (unsigned)((a.hidden / 128 + RB - 1) / RB);
+    const int items = a.topk + (a.sh_part ? 1 : 0);
     hipLaunchKernelGGL(moe_reduce_kernel, dim3(nbk, (unsigned)a.rows), dim3(64 * RW),
-                       (size_t)a.topk * RB * 128 * sizeof(float), s, a);
+                       (size_t)items * RB * 128 * sizeof(float), s, a);
     return hipGetLastError();
 }
 
@@ -222,7 +237,7 @@ hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32
 // tile_window[t] names the window of tile t.  Ranks come from GW_CHUNKS waves, each walking its contiguous chunk of
 // the slots in order from the chunk's per-expert prefix.
 __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
-                                                                       int experts, MoeGemmWindows t) {
+                                                                       int experts, int sh_rows, MoeGemmWindows t) {
     // The slots are cut into GW_CHUNKS contiguous chunks, one per ranking wave: per-chunk counts by LDS atomics, their
     // exclusive prefix over chunks per expert, then each wave ranks its own chunk in order (a single wave walking
     // every slot waits out one load round trip per 64 slots: 90 us for 16384 slots).
@@ -234,14 +249,16 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
     __shared__ uint32_t part[3][WIN_THREADS];
     constexpr uint32_t W = MOE_GEMM_WINDOW_ROWS;
     const int tid = threadIdx.x;
-    const int chunk = (((nslots + GW_CHUNKS - 1) / GW_CHUNKS) + 63) / 64 * 64;  // slots per chunk, whole groups of 64
-    for (int e = tid; e < experts; e += WIN_THREADS)
+    // a shared expert's rows are slots nslots .. ns - 1 of expert `experts`
+    const int ns = nslots + sh_rows, ne = experts + (sh_rows > 0 ? 1 : 0);
+    auto expert_of = [&](int s) { return s < nslots ? min(inds[s], (uint32_t)(experts - 1)) : (uint32_t)experts; };
+    const int chunk = (((ns + GW_CHUNKS - 1) / GW_CHUNKS) + 63) / 64 * 64;  // slots per chunk, whole groups of 64
+    for (int e = tid; e < ne; e += WIN_THREADS)
         for (int c = 0; c < GW_CHUNKS; c++) ccnt[c][e] = 0;
     __syncthreads();
-    for (int s = tid; s < nslots; s += WIN_THREADS)
-        atomicAdd(&ccnt[s / chunk][min(inds[s], (uint32_t)(experts - 1))], 1u);
+    for (int s = tid; s < ns; s += WIN_THREADS) atomicAdd(&ccnt[s / chunk][expert_of(s)], 1u);
     __syncthreads();
-    for (int e = tid; e < experts; e += WIN_THREADS) {
+    for (int e = tid; e < ne; e += WIN_THREADS) {
         uint32_t run = 0;
         for (int c = 0; c < GW_CHUNKS; c++) {
             const uint32_t v = ccnt[c][e];
@@ -252,8 +269,8 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
     }
     __syncthreads();
     // three exclusive scans over experts (slots, 16-row tiles, windows): each thread sums a contiguous run
-    const int per = (experts + WIN_THREADS - 1) / WIN_THREADS;
-    const int e0 = min(tid * per, experts), e1 = min(e0 + per, experts);
+    const int per = (ne + WIN_THREADS - 1) / WIN_THREADS;
+    const int e0 = min(tid * per, ne), e1 = min(e0 + per, ne);
     uint32_t ls = 0, lt = 0, lw = 0;
     for (int e = e0; e < e1; e++) {
         ls += cnt[e];
@@ -288,14 +305,14 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
     const int wave = tid >> 6;
     if (wave < GW_CHUNKS) {  // wave c ranks chunk c in slot order; the next group's indices load under this one's work
         const int lane = tid & 63;
-        const int id_bits = experts > 1 ? 32 - __clz(experts - 1) : 0;
-        const int c0 = wave * chunk, c1 = min(c0 + chunk, nslots);
-        uint32_t next = c0 + lane < c1 ? inds[c0 + lane] : 0u;
+        const int id_bits = ne > 1 ? 32 - __clz(ne - 1) : 0;
+        const int c0 = wave * chunk, c1 = min(c0 + chunk, ns);
+        uint32_t next = c0 + lane < c1 ? expert_of(c0 + lane) : 0u;
         for (int base = c0; base < c1; base += 64) {
             const int s = base + lane;
             const bool live = s < c1;
-            const int e = live ? (int)min(next, (uint32_t)(experts - 1)) : 0;
-            next = base + 64 + lane < c1 ? inds[base + 64 + lane] : 0u;
+            const int e = live ? (int)next : 0;
+            next = base + 64 + lane < c1 ? expert_of(base + 64 + lane) : 0u;
             unsigned long long same = __ballot(live);
             for (int b = 0; b < id_bits; b++) {
                 const unsigned long long set = __ballot((e >> b) & 1);
@@ -325,10 +342,11 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
     }
 }
 
-hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, const MoeGemmWindows &t,
+hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, int sh_rows, const MoeGemmWindows &t,
                                 hipStream_t s) {
-    if (nslots <= 0 || experts <= 0 || experts > kMoeGemmMaxExperts) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_gemm_windows_kernel, dim3(1), dim3(WIN_THREADS), 0, s, inds, nslots, experts, t);
+    if (nslots <= 0 || experts <= 0 || sh_rows < 0 || experts + (sh_rows > 0 ? 1 : 0) > kMoeGemmMaxExperts)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_gemm_windows_kernel, dim3(1), dim3(WIN_THREADS), 0, s, inds, nslots, experts, sh_rows, t);
     return hipGetLastError();
 }
 

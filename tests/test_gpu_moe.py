@@ -350,7 +350,8 @@ def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
 def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
     """Where the fused form does not serve, the C ABI declines before any launch and the wrapper makes the two
     calls; the result is the two calls' own.  700 rows: the routed, shared and combine fold words (3 x 700 x 256)
-    exceed the fused finish's region."""
+    exceed the fused finish's region (with the GEMM arm held off: at 175 slots per expert it would take the layer and
+    serve the shared bank in its own launches)."""
     E, hidden, inter, k, n = 8, 256, 128, 2, 32
     rows = 700 if case == "rows700" else 2
     b = synth.bank(33, "msd", E, hidden, inter, n)
@@ -367,14 +368,15 @@ def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
     ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
     y0 = torch.full_like(xd, 7.0)
     x2 = xd.contiguous()
-    rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
-                                     y0.data_ptr(), exl3._dt(y0, "y"), ws.data_ptr(), ws.numel(),
-                                     exl3._stream(dev))
-    torch.cuda.synchronize()
-    assert rc == exl3.EXL3_DECLINED and bool((y0 == 7.0).all())  # nothing launched
-    y = exl3.moe_with_shared_bank(xd, bd, sd, xi, sc, exl3.MCG)
-    ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
+    with exl3.arm_overrides(moe_gemm=0):
+        rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
+                                         ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
+                                         y0.data_ptr(), exl3._dt(y0, "y"), ws.data_ptr(), ws.numel(),
+                                         exl3._stream(dev))
+        torch.cuda.synchronize()
+        assert rc == exl3.EXL3_DECLINED and bool((y0 == 7.0).all())  # nothing launched
+        y = exl3.moe_with_shared_bank(xd, bd, sd, xi, sc, exl3.MCG)
+        ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG)
     assert torch.equal(y, ref)
 
 
@@ -560,6 +562,46 @@ def test_moe_gemm_arm_against_oracle(dev, rows, E, k, label, dec, odec):
         y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
                      torch.from_numpy(scores).to(dev), dec)
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+@pytest.mark.parametrize("rows,E,k", [(64, 16, 4), (300, 8, 2)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("limit", [0, 5])
+def test_moe_gemm_arm_serves_the_shared_bank_in_its_launches(dev, rows, E, k, dtype, limit):
+    """At GEMM-arm widths the fused shared-bank call runs the shared expert as one more expert of the routed launches
+    (its rows as extra slots, windows of up to 256 of them) and equals the reference callers' pair of calls -- the
+    shared expert as a one-expert layer, then moeWithShared / moeClamped -- bit for bit, for every y dtype; and the
+    routed + shared sum matches the oracle at the bar."""
+    print(f"[moe gemm shared] rows={rows} E={E} k={k} {dtype} limit={limit}", flush=True)
+    hidden, inter, n = 256, 128, 32
+    b = synth.bank(47, f"mgs{E}", E, hidden, inter, n, norm=True)
+    s = synth.bank(47, "mgs.shared", 1, hidden, inter, n, norm=True)
+    x = synth.normal(47, f"x{rows}", (rows, hidden), dtype=dtype)
+    inds, scores = _route(47 + rows, rows, E, k)
+    bd, sd = _to(b, dev), _to(s, dev)
+    xd = x.to(dev)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    L = exl3._lib.load()
+    cb = exl3._lib.BankT(bd.gate.c(), bd.up.c(), bd.down.c())
+    cs = exl3._lib.BankT(sd.gate.c(), sd.up.c(), sd.down.c())
+    ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
+    y = torch.empty_like(xd)
+    rc = L.exl3_moe_with_shared_bank(xd.data_ptr(), exl3._dt(xd, "x"), rows, hidden, inter, E, ctypes.byref(cb),
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), limit,
+                                     y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
+    assert rc == 0, exl3._lib.last_error()
+    ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG, limit)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    if dtype == torch.float16 and limit == 0:
+        odec = O.decode(O.CB_MCG)
+        routed = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, scores, hidden,
+                                   inter, (n, n, n), odec, threads=8)
+        shared = O.moe_swiglu_rows(x.float().numpy(), _np(s.gate), _np(s.up), _np(s.down), np.zeros((rows, 1)),
+                                   np.ones((rows, 1)), hidden, inter, (n, n, n), odec, threads=8)
+        want = routed.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
+        assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
 def test_moe_gemm_arm_long_windows_clamp_and_shared(dev):
