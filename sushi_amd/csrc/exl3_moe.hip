@@ -70,9 +70,10 @@ __device__ __forceinline__ float round_to(int dt, float v) {
 // expert's term: sum of the slot's k splits, FWHT, svh, score) for all its blocks into LDS, the blocks' loads first
 // and their transforms together; then every thread adds the slots of its columns in slot order (the reference's
 // order) and finishes.  (One block per workgroup ran 82 us for 2048 rows x 8 slots x 2048 columns: 32768 workgroups
-// each reading 4 KiB; a ninth wave for a shared expert's term ran slower than eight waves taking nine items.)
+// each reading 4 KiB; a ninth wave for a shared expert's term ran slower than eight waves taking nine items.)  RB = 4
+// where that still leaves at least 1024 workgroups, else 1 (a decode batch of 32 rows would get 128).
 constexpr int RW = 8;
-constexpr int RB = 4;
+template <int RB>
 __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
     const int row = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -137,10 +138,14 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
 
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
     if (a.topk > kMoeReduceMaxTopk) return hipErrorInvalidValue;
-    const unsigned nbk = (unsigned)((a.hidden / 128 + RB - 1) / RB);
-    const int items = a.topk + (a.sh_part ? 1 : 0);
-    hipLaunchKernelGGL(moe_reduce_kernel, dim3(nbk, (unsigned)a.rows), dim3(64 * RW),
-                       (size_t)items * RB * 128 * sizeof(float), s, a);
+    const int items = a.topk + (a.sh_part ? 1 : 0), blocks = a.hidden / 128;
+    if ((long)a.rows * ((blocks + 3) / 4) >= 1024) {
+        hipLaunchKernelGGL(moe_reduce_kernel<4>, dim3((unsigned)((blocks + 3) / 4), (unsigned)a.rows), dim3(64 * RW),
+                           (size_t)items * 4 * 128 * sizeof(float), s, a);
+    } else {
+        hipLaunchKernelGGL(moe_reduce_kernel<1>, dim3((unsigned)blocks, (unsigned)a.rows), dim3(64 * RW),
+                           (size_t)items * 128 * sizeof(float), s, a);
+    }
     return hipGetLastError();
 }
 
