@@ -157,7 +157,7 @@ hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
 // round with the same expert (found by one ballot per bit of the expert id), so the result does not depend on thread
 // timing.
 constexpr int WIN_THREADS = 1024;
-constexpr int GW_CHUNKS = 8;  // ranking waves of the GEMM arm's windows (8 x 1024 experts of u32 counts: 32 KiB of LDS)
+constexpr int GW_CHUNKS = 16;  // ranking waves of the GEMM arm's windows (16 x 1024 experts of u32 counts: 64 KiB of LDS)
 __global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
                                                                   int experts, uint32_t *__restrict__ win_count,
                                                                   uint32_t *__restrict__ win_expert,
