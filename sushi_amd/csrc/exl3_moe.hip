@@ -278,11 +278,15 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
         cnt[e] = run;
     }
     __syncthreads();
-    // three exclusive scans over experts (slots, 16-row tiles, windows): each thread sums a contiguous run
+    // three exclusive scans over experts (slots, 16-row tiles, windows): each thread sums a contiguous run.  A shared
+    // expert comes first in the scan order, so its windows (full ones of 256 rows, the GEMMs' heaviest workgroups)
+    // are numbered and dispatched first instead of trailing the grid.
     const int per = (ne + WIN_THREADS - 1) / WIN_THREADS;
     const int e0 = min(tid * per, ne), e1 = min(e0 + per, ne);
+    auto scan_expert = [&](int v) { return sh_rows > 0 ? (v == 0 ? experts : v - 1) : v; };
     uint32_t ls = 0, lt = 0, lw = 0;
-    for (int e = e0; e < e1; e++) {
+    for (int v = e0; v < e1; v++) {
+        const int e = scan_expert(v);
         ls += cnt[e];
         lt += (cnt[e] + 15) / 16;
         lw += (cnt[e] + W - 1) / W;
@@ -299,7 +303,8 @@ __global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uin
         __syncthreads();
     }
     uint32_t rs = part[0][tid] - ls, rt = part[1][tid] - lt, rw = part[2][tid] - lw;
-    for (int e = e0; e < e1; e++) {
+    for (int v = e0; v < e1; v++) {
+        const int e = scan_expert(v);
         sb[e] = rs;
         tb[e] = rt;
         wb[e] = rw;
