@@ -642,13 +642,16 @@ def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4, 
                             for x, (i, s) in zip(xs, routes)]
                 chain()
                 torch.cuda.synchronize()
-                g = _capture(chain, dev)
+                g = _capture(chain, dev) if SWEEP_GRAPHS else None  # --no-graph: issued from Python (counter passes)
                 stream = torch.cuda.current_stream(dev)
                 ts = []
                 for _ in range(ROUNDS):
                     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     e0.record(stream)
-                    g.replay()
+                    if g is not None:
+                        g.replay()
+                    else:
+                        chain()
                     e1.record(stream)
                     torch.cuda.synchronize()
                     ts.append(e0.elapsed_time(e1) * 1e3 / layers)
