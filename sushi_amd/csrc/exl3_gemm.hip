@@ -293,6 +293,54 @@ __device__ __forceinline__ void store_y4(void *y, int dt, size_t i, float y0, fl
     }
 }
 
+// The MFMA waves' main loop of the decode-wave tile over the first NRB of the wave's four 16-row blocks (the rest of
+// acc stays zero): instantiated per live-block count, so a short row group (a window of 65-85 rows leaves its second
+// one or two) neither loads A nor issues MFMAs for its empty blocks, without a branch in the loop.  1 + nks barriers,
+// as the decode waves meet.
+template <int NRB>
+__device__ __forceinline__ void gemm4_mfma_loop(const uint16_t *const (&xfrag)[4], int nks, int cb0, int c, int h,
+                                                uint16_t (*Bs)[128 * G2_BP], f4_t (&acc)[4][4]) {
+    // A fragments in two register sets, a full step apart: set X serves even steps and set Y odd ones; each set is
+    // refilled for the step after next as soon as its MFMAs have issued, so a fragment has a whole step to arrive.
+    uint4 AX[4][2], AY[4][2];
+    auto load_a = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
+        const int kk = min(ks, nks - 1);
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++)
+                A[rb][kb] = *reinterpret_cast<const uint4 *>(xfrag[rb] + (size_t)(kk * 2 + kb) * 512);
+    };
+    load_a(0, AX);
+    load_a(1, AY);
+    __syncthreads();  // barrier 0
+    auto mstep = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
+        const uint16_t *slab = Bs[ks & 1];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            uint4 bv[4];  // this half-step's B fragments (the A sets hold the registers a whole step of B would take)
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++)
+                bv[cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G2_BP + kb * 32 + 8 * h);
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const h8_t B8 = __builtin_bit_cast(h8_t, bv[cb]);
+#pragma unroll
+                for (int rb = 0; rb < NRB; rb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, A[rb][kb]), B8,
+                                                                         acc[rb][cb], 0, 0, 0);
+            }
+        }
+        load_a(ks + 2, A);
+        __syncthreads();
+    };
+    for (int ks = 0; ks < nks; ks += 2) {  // nks is even
+        mstep(ks, AX);
+        mstep(ks + 1, AY);
+    }
+
+}
+
 // One workgroup's 256-row x 128-column output tile: output group og of a bank whose tiles start at `bank`
 // ([in/16][out/16][N]), prepared rows in fragment tiles from xfrag0 (row tile rt at xfrag0 + rt * (in / 32) * 512), of
 // which the first `rows` (<= 256) are live.  The epilogue hands the raw inner products of rows m .. m + 3 to
@@ -372,43 +420,11 @@ __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16
     for (int rb = 0; rb < 4; rb++)
 #pragma unroll
         for (int cb = 0; cb < 4; cb++) acc[rb][cb] = f4_t{0.f, 0.f, 0.f, 0.f};
-    // A fragments in two register sets, a full step apart: set X serves even steps and set Y odd ones; each set is
-    // refilled for the step after next as soon as its MFMAs have issued, so a fragment has a whole step to arrive.
-    uint4 AX[4][2], AY[4][2];
-    auto load_a = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
-        const int kk = min(ks, nks - 1);
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int rb = 0; rb < 4; rb++)
-                A[rb][kb] = *reinterpret_cast<const uint4 *>(xfrag[rb] + (size_t)(kk * 2 + kb) * 512);
-    };
-    load_a(0, AX);
-    load_a(1, AY);
-    __syncthreads();  // barrier 0
-    auto mstep = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
-        const uint16_t *slab = Bs[ks & 1];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            uint4 bv[4];  // this half-step's B fragments (the A sets hold the registers a whole step of B would take)
-#pragma unroll
-            for (int cb = 0; cb < 4; cb++)
-                bv[cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G2_BP + kb * 32 + 8 * h);
-#pragma unroll
-            for (int cb = 0; cb < 4; cb++) {
-                const h8_t B8 = __builtin_bit_cast(h8_t, bv[cb]);
-#pragma unroll
-                for (int rb = 0; rb < 4; rb++)
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, A[rb][kb]), B8,
-                                                                         acc[rb][cb], 0, 0, 0);
-            }
-        }
-        load_a(ks + 2, A);
-        __syncthreads();
-    };
-    for (int ks = 0; ks < nks; ks += 2) {  // nks is even
-        mstep(ks, AX);
-        mstep(ks + 1, AY);
+    switch (min(4, RT - m0 / 16)) {  // the wave's live 16-row blocks
+    case 1: gemm4_mfma_loop<1>(xfrag, nks, cb0, c, h, Bs, acc); break;
+    case 2: gemm4_mfma_loop<2>(xfrag, nks, cb0, c, h, Bs, acc); break;
+    case 3: gemm4_mfma_loop<3>(xfrag, nks, cb0, c, h, Bs, acc); break;
+    default: gemm4_mfma_loop<4>(xfrag, nks, cb0, c, h, Bs, acc); break;
     }
 
     // ---- epilogue (the decode waves have left, so the barriers below join the live MFMA waves): per 16-row block, the
