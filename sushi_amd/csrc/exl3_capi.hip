@@ -325,7 +325,7 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0
 // window's rows prepared into MFMA fragment order and run through the decode-once GEMM (each weight decoded once per
 // window instead of once per 4-row GEMV window), then the mid, the down GEMM and the reduce.  Taken when the layer
 // averages at least kMoeGemmMinSlotsPerExpert slots per expert, on a uniform bank at one lane-reader rate (C4's layer,
-// E = 256 top-8: 8 slots per expert 551 us against 669 on the GEMV windows, 4 slots 527 against 393).
+// E = 256 top-8: 8 slots per expert 457 us against 669 on the GEMV windows, 4 slots 423 against 394).
 constexpr int kMoeGemmMinSlotsPerExpert = 8;
 
 struct MoeGemmPlan {
