@@ -604,6 +604,38 @@ def test_moe_gemm_arm_serves_the_shared_bank_in_its_launches(dev, rows, E, k, dt
         assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
+@pytest.mark.parametrize("E", [1023, 1024])
+def test_moe_gemm_arm_shared_bank_at_the_expert_table_limit(dev, E):
+    """The GEMM arm's window tables hold 1024 experts: 1023 routed + the shared one run in the same launches and
+    equal the pair of calls bit for bit; 1024 routed + shared decline before any launch (the wrapper then makes the
+    two calls itself)."""
+    print(f"[moe gemm shared limit] E={E}", flush=True)
+    hidden, inter, n, k = 128, 128, 16, 8
+    rows = E  # 8 slots per expert
+    bd = synth.bank(48, f"lim{E}", E, hidden, inter, n, device=dev, norm=True)
+    sd = synth.bank(48, "lim.shared", 1, hidden, inter, n, device=dev, norm=True)
+    x = synth.normal(48, f"x{E}", (rows, hidden)).to(dev)
+    inds, scores = _route(48, rows, E, k)
+    xi = torch.from_numpy(inds.view(np.int32)).to(dev)
+    sc = torch.from_numpy(scores).to(dev)
+    L = exl3._lib.load()
+    cb = exl3._lib.BankT(bd.gate.c(), bd.up.c(), bd.down.c())
+    cs = exl3._lib.BankT(sd.gate.c(), sd.up.c(), sd.down.c())
+    ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
+    y = torch.full_like(x, 7.0)
+    rc = L.exl3_moe_with_shared_bank(x.data_ptr(), exl3._dt(x, "x"), rows, hidden, inter, E, ctypes.byref(cb),
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
+                                     y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
+    ref = _two_calls(x, bd, sd, xi, sc, exl3.MCG)
+    torch.cuda.synchronize()
+    if E < 1024:
+        assert rc == 0, exl3._lib.last_error()
+        assert torch.equal(y, ref)
+    else:
+        assert rc == exl3.EXL3_DECLINED and bool((y == 7.0).all())
+        assert torch.equal(exl3.moe_with_shared_bank(x, bd, sd, xi, sc, exl3.MCG), ref)
+
+
 def test_moe_gemm_arm_long_windows_clamp_and_shared(dev):
     """One expert takes 450 slots (windows of 256 + 194 rows), clamped SwiGLU, a shared expert added after the
     routed rounding, then the same with a gate; and the arm equals the decode chain to the bar."""
