@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 4
+#define EXL3_ABI_VERSION 5
 
 /* Codebook: the reference's `Codebook` enum values (src/exl3/expert_exl3.zig:54-61), plus 3INST as an
  * extension (QTIP's LCG codebook, not in the reference). */
@@ -214,8 +214,12 @@ int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t
  * x [rows][hidden]; inds [rows][topk] u32 (i32 accepted: same bits); scores [rows][topk] in scores_dtype (f32, bf16
  * or f16, as root.zig:114 admits).  Banks: gate/up trellis [E][hidden/16][inter/16][n], down
  * [E][inter/16][hidden/16][n]; each projection at its own rate (gate and up at different rates take one launch each,
- * as moeMixedDecode does, root.zig:705-722).  The decode chain (pair GEMV -> fused SwiGLU mid + down GEMV ->
- * score-weighted reduce) serves every row count. */
+ * as moeMixedDecode does, root.zig:705-722).  Arms: up to 8 rows the per-slot decode chain (pair GEMV -> fused
+ * SwiGLU mid + down GEMV -> score-weighted fold or reduce); wider batches the same chain over expert windows of up to
+ * 4 rows; prefill widths (from 8 slots per expert on average, every projection at one of the rates 16, 24, 32, 40,
+ * 48, 64) the routed GEMM arm on the matrix cores (`moePrefill`, expert_exl3_kernels.zig:2861-2931).
+ * verify_rows != 0 marks speculative-verify rows: as the reference does (root.zig:169, `rows <= DECODE_ROWS_MAX or
+ * verify_rows`), they never take the GEMM arm, so they round as decode rows do at every width. */
 size_t exl3_moe_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
 int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
                  const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
@@ -234,11 +238,16 @@ int32_t exl3_moe_with_gated_shared(const void *x, int32_t x_dtype, int32_t rows,
                                    void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* `moeRagged` (src/exl3/root.zig:582-644) over a rate-grouped ragged bank (rate_groups.zig:22-140): each expert
- * decodes at its own (n_gate, n_up, n_down) read from the meta table.  `max_n` bounds every rate in the table. */
+ * decodes at its own (n_gate, n_up, n_down) read from the meta table.  `shared` and `shared_gate` as for exl3_moe and
+ * exl3_moe_with_gated_shared (shared_gate non-null: y = T(T(routed) + T(sigmoid(gate) * shared)), gate [rows] in y's
+ * dtype; it needs `shared`); the trunk's ragged call passes both (src/trunk.zig:4092).  verify_rows as exl3_moe.  At
+ * prefill widths a bank whose rates are all lane-reader rates (`lane_rates_only`) takes the GEMM arm, each
+ * workgroup at its expert's rate (`rate_groups.moePrefill`, rate_groups.zig:2039-2075). */
 int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                         const exl3_ragged_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
-                        int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
-                        int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
+                        int32_t topk, exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit,
+                        const void *shared, const void *shared_gate, void *y, int32_t y_dtype, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
 
 /* A routed layer and its shared expert in one call.  Replaces the caller's pair of calls: the shared expert as a
  * one-expert chain (inds 0, score 1; the pattern of src/dsv41/dsv41_model.zig:3000) and then `moeWithShared`
@@ -259,13 +268,14 @@ size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int3
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                   int32_t experts, const exl3_bank_t *bank, const exl3_bank_t *shared_bank,
                                   const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                                  exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
-                                  size_t workspace_bytes, hipStream_t stream);
+                                  exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, void *y,
+                                  int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
 int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                          const exl3_ragged_t *bank, const exl3_bank_t *shared_bank,
                                          const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                                         exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
-                                         void *workspace, size_t workspace_bytes, hipStream_t stream);
+                                         exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, void *y,
+                                         int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                                         hipStream_t stream);
 
 /* `reconstructInner` (src/exl3/expert_exl3.zig:416-438) of expert `expert` of one per-tile-rate projection
  * (exl3_tiled_t's layout): the f16 inner matrix [in][out], each tile decoded at its own rate by the decoder the
@@ -275,20 +285,22 @@ int32_t exl3_reconstruct_tiled(const uint16_t *trellis, const uint32_t *seg_off,
                                exl3_decode_t dec, uint16_t *out, hipStream_t stream);
 
 /* `moeRagged` (src/exl3/root.zig:582-644) over a per-tile-rate bank: the routed SwiGLU chain of exl3_moe (same
- * arguments, scores dtypes, clamp and `shared`), every tile at its own rate.  Every row count takes the decode chain
- * (per-slot, or sorted expert windows past 8 rows); there is no GEMM arm.  Workspace: exl3_moe_workspace_size.
+ * arguments, scores dtypes, clamp, `shared`, `shared_gate` and verify_rows), every tile at its own rate.  Up to 8 rows
+ * the per-slot decode chain, wider batches the expert windows, prefill widths (not verify rows) the GEMM arm, whose
+ * decode waves read each segment's offset and mask.  Workspace: exl3_moe_workspace_size.
  * The _with_shared_bank form runs a one-expert uniform shared bank (rate 16, 24, 32, 40, 48 or 64, decoded with the
  * routed codebook) inside the routed launches, as exl3_moe_with_shared_bank does, and declines where it does
  * (workspace: exl3_moe_with_shared_bank_workspace_size). */
 int32_t exl3_moe_tiled(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                        const exl3_tiled_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
-                       int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
-                       int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
+                       int32_t topk, exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, const void *shared,
+                       const void *shared_gate, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
 int32_t exl3_moe_tiled_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                         const exl3_tiled_t *bank, const exl3_bank_t *shared_bank,
                                         const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                                        exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
-                                        void *workspace, size_t workspace_bytes, hipStream_t stream);
+                                        exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, void *y,
+                                        int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Router chain `moeRoutingChainOn` (src/moe_router.zig:22-62): top-k over f32 logits [rows][experts]
  * (ties to the lower expert index, listed in descending logit order), softmax over all experts, gathered and

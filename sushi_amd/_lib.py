@@ -97,20 +97,20 @@ def load() -> ctypes.CDLL:
     L.exl3_moe_with_gated_shared.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(BankT), vp, vp, i32, i32,
                                              DecodeT, i32, vp, vp, vp, i32, vp, sz, vp]
     L.exl3_moe_ragged.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(RaggedT), vp, vp, i32, i32, DecodeT, i32,
-                                  vp, vp, i32, vp, sz, vp]
+                                  i32, vp, vp, vp, i32, vp, sz, vp]
     L.exl3_moe_with_shared_bank_workspace_size.restype = sz
     L.exl3_moe_with_shared_bank_workspace_size.argtypes = [i32, i32, i32, i32]
     L.exl3_moe_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(BankT), ctypes.POINTER(BankT),
-                                            vp, vp, i32, i32, DecodeT, i32, vp, i32, vp, sz, vp]
+                                            vp, vp, i32, i32, DecodeT, i32, i32, vp, i32, vp, sz, vp]
     L.exl3_moe_ragged_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(RaggedT),
-                                                   ctypes.POINTER(BankT), vp, vp, i32, i32, DecodeT, i32, vp, i32, vp,
-                                                   sz, vp]
+                                                   ctypes.POINTER(BankT), vp, vp, i32, i32, DecodeT, i32, i32, vp,
+                                                   i32, vp, sz, vp]
     L.exl3_reconstruct_tiled.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, DecodeT, vp, vp]
-    L.exl3_moe_tiled.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(TiledT), vp, vp, i32, i32, DecodeT, i32, vp,
-                                 vp, i32, vp, sz, vp]
+    L.exl3_moe_tiled.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(TiledT), vp, vp, i32, i32, DecodeT, i32, i32,
+                                 vp, vp, vp, i32, vp, sz, vp]
     L.exl3_moe_tiled_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(TiledT),
-                                                  ctypes.POINTER(BankT), vp, vp, i32, i32, DecodeT, i32, vp, i32, vp,
-                                                  sz, vp]
+                                                  ctypes.POINTER(BankT), vp, vp, i32, i32, DecodeT, i32, i32, vp,
+                                                  i32, vp, sz, vp]
     L.exl3_route_topk.argtypes = [vp, i32, i32, i32, vp, vp, vp]
     L.exl3_tile_major.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp]
     L.exl3_encode_workspace_size.restype = sz

@@ -388,9 +388,9 @@ struct SharedBank {
 // On the GEMM arm the shared bank's rows join as one more expert (any y dtype).  Otherwise they need the per-slot
 // arm, a 16-bit output dtype (the combine word holds both rounded sums), the routed and shared folds (routed, shared
 // and combine words: three per output), and, for a uniform bank, the routed rate.
-bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts, int n) {
+bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts, int n, bool verify) {
     const int nslots = rows * topk;
-    if (moe_gemm_wanted(nslots, experts, lane_rate(n))) return experts < kMoeGemmMaxExperts;
+    if (!verify && moe_gemm_wanted(nslots, experts, lane_rate(n))) return experts < kMoeGemmMaxExperts;
     if (y_dtype == EXL3_DT_F32) return false;
     const bool windowed = rows > moe_decode_rows_max();
     if (windowed && !(moe_windows_enabled() && moe_windowed(rows, nslots, experts))) return false;
@@ -407,18 +407,19 @@ struct TiledTables {
 // One routed layer's launches.  n[3] are the projections' uniform rates (all 0 with a ragged `meta` or a per-tile-rate
 // bank's tables `tt`); k is the decode of the gate's rate (per-rate constants of the other projections are resolved
 // here).  shared / shared_gate: an already computed shared expert [rows][hidden] in y's dtype, added as it is or as
-// sigmoid(gate) * shared.
+// sigmoid(gate) * shared.  verify: speculative-verify rows, which stay on the decode chain at every width (the
+// reference's `rows <= DECODE_ROWS_MAX or verify_rows`, src/exl3/root.zig:169).
 int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int table, const void *x, int32_t x_dtype,
                    int32_t rows, int32_t hidden, int32_t inter, int32_t experts, const uint16_t *const tr[3],
                    const uint16_t *const su[3], const uint16_t *const sv[3], const int n[3], const uint32_t *meta,
                    int meta_lane_only, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                   int32_t clamp_limit, const void *shared, const void *shared_gate, void *y, int32_t y_dtype,
-                   void *ws, size_t ws_bytes, hipStream_t stream, const SharedBank *sb = nullptr,
+                   bool verify, int32_t clamp_limit, const void *shared, const void *shared_gate, void *y,
+                   int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream, const SharedBank *sb = nullptr,
                    const TiledTables *tt = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    if ((!sb || (sb->n == n[0] && !shared && experts < kMoeGemmMaxExperts)) && !meta && !tt && n[0] == n[1] &&
-        n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
+    if (!verify && (!sb || (sb->n == n[0] && !shared && experts < kMoeGemmMaxExperts)) && !meta && !tt &&
+        n[0] == n[1] && n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
         // a shared bank's rows are slots nslots .. nslots + rows - 1 of one more expert (index `experts`)
         const int sh_rows = sb ? rows : 0;
         const MoeGemmPlan gp = plan_moe_gemm(nslots + sh_rows, hidden, inter, experts + (sb ? 1 : 0));
@@ -825,8 +826,9 @@ int32_t tiled_checks(const exl3_tiled_t *b, const exl3_decode_t &dec, const char
 // `moe` / `moeWithShared` / `moeWithGatedShared` over a uniform bank: every check, then the launches.
 int32_t moe_uniform(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
                     const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
-                    int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, const void *shared_gate,
-                    void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                    int32_t topk, exl3_decode_t dec, bool verify, int32_t clamp_limit, const void *shared,
+                    const void *shared_gate, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe: no bank");
@@ -850,8 +852,8 @@ int32_t moe_uniform(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden
     const uint16_t *su[3] = {bank->gate.suh, bank->up.suh, bank->down.suh};
     const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
     return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, n, nullptr, 0,
-                      inds, scores, scores_dtype, topk, clamp_limit, shared, shared_gate, y, y_dtype, workspace,
-                      workspace_bytes, stream);
+                      inds, scores, scores_dtype, topk, verify, clamp_limit, shared, shared_gate, y, y_dtype,
+                      workspace, workspace_bytes, stream);
 }
 
 }  // namespace
@@ -969,9 +971,8 @@ int32_t exl3_moe(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, i
                  const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
                  exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, const void *shared, void *y,
                  int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
-    (void)verify_rows;  // every row count runs the decode chain here
     return moe_uniform(x, x_dtype, rows, hidden, inter, experts, bank, inds, scores, scores_dtype, topk, dec,
-                       clamp_limit, shared, nullptr, y, y_dtype, workspace, workspace_bytes, stream);
+                       verify_rows != 0, clamp_limit, shared, nullptr, y, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int32_t exl3_moe_with_gated_shared(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
@@ -979,17 +980,17 @@ int32_t exl3_moe_with_gated_shared(const void *x, int32_t x_dtype, int32_t rows,
                                    int32_t scores_dtype, int32_t topk, exl3_decode_t dec, int32_t verify_rows,
                                    const void *shared_down, const void *shared_gate, void *y, int32_t y_dtype,
                                    void *workspace, size_t workspace_bytes, hipStream_t stream) {
-    (void)verify_rows;
     if (!shared_down || !shared_gate)
         return fail(EXL3_ERR_BAD_SHAPE, "moe_with_gated_shared: the shared expert's output and its gate are required");
-    return moe_uniform(x, x_dtype, rows, hidden, inter, experts, bank, inds, scores, scores_dtype, topk, dec, 0,
-                       shared_down, shared_gate, y, y_dtype, workspace, workspace_bytes, stream);
+    return moe_uniform(x, x_dtype, rows, hidden, inter, experts, bank, inds, scores, scores_dtype, topk, dec,
+                       verify_rows != 0, 0, shared_down, shared_gate, y, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                         const exl3_ragged_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
-                        int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
-                        int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                        int32_t topk, exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit,
+                        const void *shared, const void *shared_gate, void *y, int32_t y_dtype, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || bank->experts <= 0 || !bank->meta) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: no bank");
@@ -1002,11 +1003,14 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: null operand");
+    if (shared_gate && !shared)
+        return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged: a shared-expert gate without its shared expert");
     const int table = fam == FAM_PAIR ? (int)TABLE_PAIR1_W16_V1 : dec.table;
     const int n0[3] = {0, 0, 0};
     return moe_launch(fam, k, dec, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
                       bank->svh, n0, bank->meta, bank->lane_rates_only != 0, inds, scores, scores_dtype, topk,
-                      clamp_limit, shared, nullptr, y, y_dtype, workspace, workspace_bytes, stream);
+                      verify_rows != 0, clamp_limit, shared, shared_gate, y, y_dtype, workspace, workspace_bytes,
+                      stream);
 }
 
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
@@ -1024,8 +1028,8 @@ size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int3
 int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                   int32_t experts, const exl3_bank_t *bank, const exl3_bank_t *shared_bank,
                                   const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                                  exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype, void *workspace,
-                                  size_t workspace_bytes, hipStream_t stream) {
+                                  exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, void *y,
+                                  int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: no bank");
@@ -1048,7 +1052,7 @@ int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, 
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: null operand");
-    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts, routed_n))
+    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts, routed_n, verify_rows))
         return declined("moe_with_shared_bank: declined (rows=%d, y dtype %d, rates %d/%d): run the shared expert as "
                         "a one-expert exl3_moe and pass it to exl3_moe as `shared`", rows, y_dtype, routed_n, sb.n);
     const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
@@ -1056,15 +1060,16 @@ int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, 
     const uint16_t *sv[3] = {bank->gate.svh, bank->up.svh, bank->down.svh};
     const int n[3] = {routed_n, routed_n, routed_n};
     return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, experts, tr, su, sv, n, nullptr, 0,
-                      inds, scores, scores_dtype, topk, clamp_limit, nullptr, nullptr, y, y_dtype, workspace,
-                      workspace_bytes, stream, &sb);
+                      inds, scores, scores_dtype, topk, verify_rows != 0, clamp_limit, nullptr, nullptr, y, y_dtype,
+                      workspace, workspace_bytes, stream, &sb);
 }
 
 int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                          const exl3_ragged_t *bank, const exl3_bank_t *shared_bank,
                                          const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                                         exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
-                                         void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                                         exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, void *y,
+                                         int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     if (!bank || bank->experts <= 0 || !bank->meta)
@@ -1089,14 +1094,14 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
     }
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: null operand");
-    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0))
+    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0, verify_rows))
         return declined("moe_ragged_with_shared_bank: declined (rows=%d, y dtype %d): run the shared expert as a "
                         "one-expert exl3_moe and pass it to exl3_moe_ragged as `shared`", rows, y_dtype);
     const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);
     const int n0[3] = {0, 0, 0};
     return moe_launch(fam, k, dec, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
-                      bank->svh, n0, bank->meta, lane_only, inds, scores, scores_dtype, topk, clamp_limit, nullptr,
-                      nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb);
+                      bank->svh, n0, bank->meta, lane_only, inds, scores, scores_dtype, topk, verify_rows != 0,
+                      clamp_limit, nullptr, nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb);
 }
 
 int32_t exl3_reconstruct_tiled(const uint16_t *trellis, const uint32_t *seg_off, const uint8_t *seg_k1,
@@ -1131,8 +1136,9 @@ int32_t exl3_reconstruct_tiled(const uint16_t *trellis, const uint32_t *seg_off,
 
 int32_t exl3_moe_tiled(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                        const exl3_tiled_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
-                       int32_t topk, exl3_decode_t dec, int32_t clamp_limit, const void *shared, void *y,
-                       int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                       int32_t topk, exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, const void *shared,
+                       const void *shared_gate, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     int fam;
@@ -1142,17 +1148,19 @@ int32_t exl3_moe_tiled(const void *x, int32_t x_dtype, int32_t rows, int32_t hid
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_tiled: null operand");
+    if (shared_gate && !shared)
+        return fail(EXL3_ERR_BAD_SHAPE, "moe_tiled: a shared-expert gate without its shared expert");
     const int n0[3] = {0, 0, 0};
     return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis,
-                      bank->suh, bank->svh, n0, nullptr, 0, inds, scores, scores_dtype, topk, clamp_limit, shared,
-                      nullptr, y, y_dtype, workspace, workspace_bytes, stream, nullptr, &tt);
+                      bank->suh, bank->svh, n0, nullptr, 0, inds, scores, scores_dtype, topk, verify_rows != 0,
+                      clamp_limit, shared, shared_gate, y, y_dtype, workspace, workspace_bytes, stream, nullptr, &tt);
 }
 
 int32_t exl3_moe_tiled_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter,
                                         const exl3_tiled_t *bank, const exl3_bank_t *shared_bank,
                                         const uint32_t *inds, const void *scores, int32_t scores_dtype, int32_t topk,
-                                        exl3_decode_t dec, int32_t clamp_limit, void *y, int32_t y_dtype,
-                                        void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                                        exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit, void *y,
+                                        int32_t y_dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
     int fam;
@@ -1172,13 +1180,13 @@ int32_t exl3_moe_tiled_with_shared_bank(const void *x, int32_t x_dtype, int32_t 
     }
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_tiled_with_shared_bank: null operand");
-    if (!lane_rate(sb.n) || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0))
+    if (!lane_rate(sb.n) || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0, verify_rows))
         return declined("moe_tiled_with_shared_bank: declined (rows=%d, y dtype %d, shared n=%d): run the shared expert "
                         "as a one-expert exl3_moe and pass it to exl3_moe_tiled as `shared`", rows, y_dtype, sb.n);
     const int n0[3] = {0, 0, 0};
     return moe_launch(fam, k, dec, dec.table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis,
-                      bank->suh, bank->svh, n0, nullptr, 0, inds, scores, scores_dtype, topk, clamp_limit, nullptr,
-                      nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb, &tt);
+                      bank->suh, bank->svh, n0, nullptr, 0, inds, scores, scores_dtype, topk, verify_rows != 0,
+                      clamp_limit, nullptr, nullptr, y, y_dtype, workspace, workspace_bytes, stream, &sb, &tt);
 }
 
 int32_t exl3_route_topk(const float *logits, int32_t rows, int32_t experts, int32_t k, uint32_t *inds, float *scores,

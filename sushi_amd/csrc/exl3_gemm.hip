@@ -341,70 +341,130 @@ __device__ __forceinline__ void gemm4_mfma_loop(const uint16_t *const (&xfrag)[4
 
 }
 
-// One workgroup's 256-row x 128-column output tile: output group og of a bank whose tiles start at `bank`
-// ([in/16][out/16][N]), prepared rows in fragment tiles from xfrag0 (row tile rt at xfrag0 + rt * (in / 32) * 512), of
-// which the first `rows` (<= 256) are live.  The epilogue hands the raw inner products of rows m .. m + 3 to
-// emit(m, live, v0[4], v1[4], lane) (columns lane and lane + 64 of the group, m the row within the tile, the first
-// `live` of them live); the caller applies the output transform (four rows at a time) or stores the raw values.
-template <int FAM, int N, class Emit>
-__device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16_t *__restrict__ bank,
-                                           const uint16_t *__restrict__ xfrag0, int rows, const DecodeK &k,
-                                           uint16_t (*Bs)[128 * G2_BP], Emit emit) {
+// ---- the decode waves' readers: where decode wave r finds k-tile row 4 ks + r of its output group in k-step ks (the
+// group's 8 tiles, lane 8 o + j reading chunk j of tile o), and how a lane's chunk decodes.  load(ks) is called for
+// ks = 0, 1, 2, ... in order (past the last step it re-reads the last).
+// One rate N for the bank: the row lies `kstep` halves further each step.
+template <int FAM, int N>
+struct RateReader {
+    static constexpr int AW = LaneBits<N>::AW;
+    const uint16_t *tb;  // the row in k-step 0
+    size_t kstep;
+    uint32_t lane_words;
+    int j, nks;
+    DecodeK k;
+    __device__ __forceinline__ RateReader(const uint16_t *bank, int r, int OT, int og, int nks_, int lane,
+                                          const DecodeK &k_)
+        : tb(bank + ((size_t)r * OT + og * 8) * N), kstep((size_t)4 * OT * N),
+          lane_words((uint32_t)((lane >> 3) * N) >> 1), j(lane & 7), nks(nks_), k(k_) {}
+    __device__ __forceinline__ void load(int ks, uint32_t (&W)[AW]) {
+        load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(ks, nks - 1) * kstep), lane_words,
+                             j, W);
+    }
+    __device__ __forceinline__ void decode(const uint32_t (&W)[AW], uint32_t (&w)[16]) const {
+        if (k.wmask != 0xFFFFu) decode_weights<FAM, N, true>(W, k, w);
+        else decode_weights<FAM, N, false>(W, k, w);
+    }
+};
+
+// A per-tile-rate projection (configs[4]'s K1 / K2 mix): the row of k-step ks is segment seg0 + ks * seg_step, at the
+// word offset and with the rate mask of the segment tables; lane 8 o + j's tile starts 16 o - 8 popcount(mask below o)
+// words in, at TILED_NA when bit o is set.  The segment's offset and mask (scalar loads) are fetched a step ahead, so
+// a tile's vector loads never wait on them.
+template <int FAM>
+struct TiledReader {
+    static constexpr int AW = 4;  // the lane's three words and its tile's rate flag
+    const uint32_t *words;        // the projection's whole trellis
+    const uint32_t *seg_off;
+    const uint8_t *seg_k1;
+    size_t seg0, seg_step;
+    int o, j, nks;
+    DecodeK ka, kb;
+    uint32_t p_off, p_m;  // offset and mask of the next step to load
+    __device__ __forceinline__ TiledReader(const uint16_t *trellis, const uint32_t *off, const uint8_t *k1, int e,
+                                           int r, int IT, int OT, int og, int nks_, int lane, const DecodeK &ka_,
+                                           const DecodeK &kb_)
+        : words(reinterpret_cast<const uint32_t *>(trellis)), seg_off(off), seg_k1(k1),
+          seg0(((size_t)e * IT + r) * (size_t)(OT >> 3) + og), seg_step((size_t)4 * (OT >> 3)), o(lane >> 3),
+          j(lane & 7), nks(nks_), ka(ka_), kb(kb_) {
+        fetch(0);
+    }
+    __device__ __forceinline__ void fetch(int ks) {
+        const size_t seg = seg0 + (size_t)min(ks, nks - 1) * seg_step;
+        p_m = seg_mask(seg_k1, seg);
+        p_off = seg_off[seg];
+    }
+    __device__ __forceinline__ void load(int ks, uint32_t (&W)[AW]) {
+        const uint32_t m = p_m, off = p_off;
+        const bool k1 = ((m >> o) & 1u) != 0;
+        const uint32_t lw = 16u * (uint32_t)o - 8u * (uint32_t)__builtin_popcount(m & ((1u << o) - 1u));
+        uint32_t A[3];
+        load_lane_words_tiled(words + off, lw, j, k1, A);
+        W[0] = A[0];
+        W[1] = A[1];
+        W[2] = A[2];
+        W[3] = k1 ? 1u : 0u;
+        fetch(ks + 1);
+    }
+    __device__ __forceinline__ void decode(const uint32_t (&W)[AW], uint32_t (&w)[16]) const {
+        const uint32_t A[3] = {W[0], W[1], W[2]};
+        const bool k1 = W[3] != 0;
+        const DecodeK kl = tiled_constants(k1, ka, kb);
+        if (kb.wmask != 0xFFFFu) decode_weights_tiled<FAM, true>(A, k1, kl, w);
+        else decode_weights_tiled<FAM, false>(A, k1, kl, w);
+    }
+};
+
+// The decode waves of the decode-wave tile (waves 8-11; wave 8 + r decodes k-tile row r of each k-step): two tiles in
+// flight, each step's row decoded into the slab the MFMA waves read after the step's barrier.  1 + nks barriers.
+template <int FAM, class R>
+__device__ __forceinline__ void gemm4_decode_waves(R &rd, int nks, int r, int lane, uint16_t (*Bs)[128 * G2_BP]) {
+    const int o = lane >> 3, j = lane & 7;
+    auto decode_store = [&](const uint32_t (&W)[R::AW], uint16_t *slab) __attribute__((always_inline)) {
+        uint32_t w[16];
+        rd.decode(W, w);
+        if constexpr (family_scaled<FAM>()) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
+        }
+        uint16_t *cj = slab + (o * 16 + j) * G2_BP + r * 16;
+        uint16_t *cj8 = cj + 8 * G2_BP;
+        *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
+        *reinterpret_cast<uint4 *>(cj + 8) = uint4{w[1], w[5], w[9], w[13]};
+        *reinterpret_cast<uint4 *>(cj8) = uint4{w[2], w[6], w[10], w[14]};
+        *reinterpret_cast<uint4 *>(cj8 + 8) = uint4{w[3], w[7], w[11], w[15]};
+    };
+    uint32_t W0[R::AW], W1[R::AW];
+    rd.load(0, W0);
+    rd.load(1, W1);
+    __builtin_amdgcn_sched_barrier(0);
+    decode_store(W0, Bs[0]);
+    __syncthreads();  // barrier 0: slab 0 is ready
+    auto dstep = [&](int ks, const uint32_t (&Wc)[R::AW], uint32_t (&Wn)[R::AW]) __attribute__((always_inline)) {
+        rd.load(ks + 2, Wn);
+        __builtin_amdgcn_sched_barrier(0);
+        decode_store(Wc, Bs[(ks + 1) & 1]);
+        __syncthreads();
+    };
+    for (int ks = 0; ks < nks; ks += 2) {
+        dstep(ks, W1, W0);
+        dstep(ks + 1, W0, W1);
+    }
+}
+
+// The MFMA waves (waves 0-7) of one workgroup's 256-row x 128-column output tile: prepared rows in fragment tiles from
+// xfrag0 (row tile rt at xfrag0 + rt * (in / 32) * 512), of which the first `rows` (<= 256) are live.  The epilogue
+// hands the raw inner products of rows m .. m + 3 to emit(m, live, v0[4], v1[4], lane) (columns lane and lane + 64 of
+// the group, m the row within the tile, the first `live` of them live); the caller applies the output transform (four
+// rows at a time) or stores the raw values.
+template <class Emit>
+__device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restrict__ xfrag0, int rows,
+                                                 uint16_t (*Bs)[128 * G2_BP], Emit emit) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int IT = in >> 4, OT = out >> 4;
-    const int nks = IT / 4;  // even: in is a multiple of 128
-    constexpr int AW = LaneBits<N>::AW;
-
-    if (wave >= 8) {
-        // ---- decode waves
-        const int r = wave - 8;
-        const int o = lane >> 3, j = lane & 7;
-        const bool masked = k.wmask != 0xFFFFu;
-        // the uniform start of k-tile row r of the group in k-step 0, plus the lane's tile offset (the GEMV's reader)
-        const uint16_t *tb = bank + ((size_t)r * OT + og * 8) * N;
-        const uint32_t lane_words = (uint32_t)(o * N) >> 1;
-        const size_t kstep = (size_t)4 * OT * N;  // halves from one k-step's row r to the next
-        auto load_tile = [&](int ks, uint32_t (&W)[AW]) __attribute__((always_inline)) {
-            load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(ks, nks - 1) * kstep),
-                                 lane_words, j, W);
-        };
-        auto decode_store = [&](const uint32_t (&W)[AW], uint16_t *slab) __attribute__((always_inline)) {
-            uint32_t w[16];
-            if (masked) decode_weights<FAM, N, true>(W, k, w);
-            else decode_weights<FAM, N, false>(W, k, w);
-            if constexpr (family_scaled<FAM>()) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
-            }
-            uint16_t *cj = slab + (o * 16 + j) * G2_BP + r * 16;
-            uint16_t *cj8 = cj + 8 * G2_BP;
-            *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
-            *reinterpret_cast<uint4 *>(cj + 8) = uint4{w[1], w[5], w[9], w[13]};
-            *reinterpret_cast<uint4 *>(cj8) = uint4{w[2], w[6], w[10], w[14]};
-            *reinterpret_cast<uint4 *>(cj8 + 8) = uint4{w[3], w[7], w[11], w[15]};
-        };
-        uint32_t W0[AW], W1[AW];
-        load_tile(0, W0);
-        load_tile(1, W1);
-        __builtin_amdgcn_sched_barrier(0);
-        decode_store(W0, Bs[0]);
-        __syncthreads();  // barrier 0: slab 0 is ready
-        auto dstep = [&](int ks, const uint32_t (&Wc)[AW], uint32_t (&Wn)[AW]) __attribute__((always_inline)) {
-            load_tile(ks + 2, Wn);
-            __builtin_amdgcn_sched_barrier(0);
-            decode_store(Wc, Bs[(ks + 1) & 1]);
-            __syncthreads();
-        };
-        for (int ks = 0; ks < nks; ks += 2) {
-            dstep(ks, W1, W0);
-            dstep(ks + 1, W0, W1);
-        }
-        return;
-    }
-
-    // ---- MFMA waves.  A row group wholly past the live rows (a short window or row tail) has nothing to compute and
-    // leaves at once; like the decode waves' exit, an ended wave no longer counts at the barriers.
+    const int nks = (in >> 4) / 4;  // even: in is a multiple of 128
+    // A row group wholly past the live rows (a short window or row tail) has nothing to compute and leaves at once;
+    // like the decode waves' exit, an ended wave no longer counts at the barriers.
     const int m0 = (wave >> 1) * 64, cb0 = (wave & 1) * 4;
     if (m0 >= rows) return;
     const int c = lane & 15, h = lane >> 4;
@@ -451,6 +511,24 @@ __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16
         }
         __syncthreads();
     }
+}
+
+// One workgroup's 256-row x 128-column output tile of output group og of a bank at one rate N whose tiles start at
+// `bank` ([in/16][out/16][N]): waves 8-11 decode, waves 0-7 multiply (gemm4_mfma_waves, whose `emit` receives the raw
+// inner products).
+template <int FAM, int N, class Emit>
+__device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16_t *__restrict__ bank,
+                                           const uint16_t *__restrict__ xfrag0, int rows, const DecodeK &k,
+                                           uint16_t (*Bs)[128 * G2_BP], Emit emit) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave >= 8) {
+        const int nks = (in >> 4) / 4;
+        RateReader<FAM, N> rd(bank, wave - 8, out >> 4, og, nks, lane, k);
+        gemm4_decode_waves<FAM>(rd, nks, wave - 8, lane, Bs);
+        return;
+    }
+    gemm4_mfma_waves(in, xfrag0, rows, Bs, emit);
 }
 
 template <int FAM, int N>

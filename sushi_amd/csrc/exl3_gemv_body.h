@@ -505,13 +505,6 @@ struct TiledSrc {
     DecodeK ka, kb;
 };
 
-// The mask of segment `seg` (8 bits, one per tile), read through its aligned 32-bit word so the load stays a scalar
-// one (the host checks that the table is 4-byte aligned; its length, a multiple of 8, keeps the word inside it).
-__device__ __forceinline__ uint32_t seg_mask(const uint8_t *k1, size_t seg) {
-    const uint32_t w = reinterpret_cast<const uint32_t *>(k1)[seg >> 2];
-    return (w >> (8u * (uint32_t)(seg & 3))) & 0xFFu;
-}
-
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 // N == N_TILED: each tile at its own rate (ts), tb the projection's whole trellis.
 // PIN: a uniform-rate launch's body (see fetch_svh).

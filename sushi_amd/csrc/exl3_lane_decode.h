@@ -249,6 +249,13 @@ __device__ __forceinline__ void decode_weights_tiled(const uint32_t (&A)[3], boo
     }
 }
 
+// The mask of segment `seg` (8 bits, one per tile), read through its aligned 32-bit word so the load stays a scalar
+// one (the host checks that the table is 4-byte aligned; its length, a multiple of 8, keeps the word inside it).
+__device__ __forceinline__ uint32_t seg_mask(const uint8_t *k1, size_t seg) {
+    const uint32_t w = reinterpret_cast<const uint32_t *>(k1)[seg >> 2];
+    return (w >> (8u * (uint32_t)(seg & 3))) & 0xFFu;
+}
+
 // A lane's rate constants in a per-tile-rate bank: the hash rows differ by rate (mult, mask); the window mask and the
 // fixed families' constants do not.
 __device__ __forceinline__ DecodeK tiled_constants(bool k1, const DecodeK &ka, const DecodeK &kb) {

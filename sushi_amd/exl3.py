@@ -709,25 +709,45 @@ def moe_clamped(x, bank: Bank, inds, scores, dec: Decode, limit: int, shared=Non
     return _moe(x, bank, inds, scores, dec, False, shared, limit)
 
 
+def _shared_operands(y: torch.Tensor, rows: int, shared, shared_gate, what: str):
+    """`shared` [rows][D] and `shared_gate` [rows] (one logit per row) in the output's dtype, as the C ABI reads them."""
+    if shared is not None:
+        if shared.numel() != y.numel() or shared.dtype != y.dtype:
+            raise BadExl3Shape(f"{what}: the shared expert's output must match the routed output's size and dtype")
+        shared = shared.reshape(y.shape).contiguous()
+        _need_gpu(shared)
+    if shared_gate is not None:
+        if shared is None or shared_gate.numel() != rows or shared_gate.dtype != y.dtype:
+            raise BadExl3Shape(f"{what}: the shared expert's gate is one logit per row in the output's dtype")
+        shared_gate = shared_gate.reshape(rows).contiguous()
+        _need_gpu(shared_gate)
+    return shared, shared_gate
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
 def moe_ragged(x, rb: Ragged, inds, scores, dec: Decode, verify_rows: bool = False, shared=None,
-               limit: int = 0) -> torch.Tensor:
-    """`moeRagged` (root.zig:582-644): each expert decodes at its own rate group's rates."""
+               shared_gate=None, limit: int = 0) -> torch.Tensor:
+    """`moeRagged` (root.zig:582-644): each expert decodes at its own rate group's rates; `shared` is added after the
+    routed output's rounding, as `sigmoid(shared_gate) * shared` when the gate logit [..., 1] is given (the trunk's
+    ragged call passes both, trunk.zig:4092)."""
     dec.require_table()
     x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
     hidden = int(x.shape[-1])
     if hidden != rb.hidden:
         raise BadExl3Shape(f"moe_ragged: hidden {hidden} vs bank {rb.hidden}")
-    _need_gpu(x2, inds2, sc2, shared, rb.meta)
+    _need_gpu(x2, inds2, sc2, rb.meta)
     y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
-    if shared is not None:
-        shared = shared.reshape(rows, hidden).contiguous()
+    shared, shared_gate = _shared_operands(y, rows, shared, shared_gate, "moe_ragged")
     L = _lib.load()
     ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, rb.inter))
     cr = rb.c()
     _check(L.exl3_moe_ragged(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr), inds2.data_ptr(),
-                             sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(limit),
-                             None if shared is None else shared.data_ptr(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
-                             ws.numel(), _stream(x.device)))
+                             sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(verify_rows), int(limit),
+                             _ptr(shared), _ptr(shared_gate), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
+                             _stream(x.device)))
     return y.reshape(x.shape)
 
 
@@ -765,7 +785,8 @@ def _shared_rows(x: torch.Tensor, shared_bank: Bank, dec: Decode, limit: int) ->
     return _moe(x, shared_bank, z.reshape(*lead, 1), o.reshape(*lead, 1), dec, False, None, limit)
 
 
-def moe_with_shared_bank(x, bank: Bank, shared_bank: Bank, inds, scores, dec: Decode, limit: int = 0) -> torch.Tensor:
+def moe_with_shared_bank(x, bank: Bank, shared_bank: Bank, inds, scores, dec: Decode, limit: int = 0,
+                         verify_rows: bool = False) -> torch.Tensor:
     """The routed layer and its shared expert in one call: T(T(routed) + T(shared)), the rounding of the reference
     callers' pair of calls (the shared expert as a one-expert chain, then `moeWithShared`, root.zig:56-67).  Where
     the fused form declines (f32 output, a shared rate other than the routed one, rows past the fused finish's
@@ -786,16 +807,16 @@ def moe_with_shared_bank(x, bank: Bank, shared_bank: Bank, inds, scores, dec: De
     cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
     rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, experts, ctypes.byref(cb),
                                      ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"), topk,
-                                     dec.c(), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
-                                     _stream(x.device))
+                                     dec.c(), int(verify_rows), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
+                                     ws.numel(), _stream(x.device))
     if rc == EXL3_DECLINED:
-        return _moe(x, bank, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
+        return _moe(x, bank, inds, scores, dec, verify_rows, _shared_rows(x, shared_bank, dec, limit), limit)
     _check(rc)
     return y.reshape(x.shape)
 
 
 def moe_ragged_with_shared_bank(x, rb: Ragged, shared_bank: Bank, inds, scores, dec: Decode,
-                                limit: int = 0) -> torch.Tensor:
+                                limit: int = 0, verify_rows: bool = False) -> torch.Tensor:
     """`moeRagged` (root.zig:582-644) with its shared expert in the same launches (see moe_with_shared_bank); the
     shared bank decodes with the routed codebook at its own rate."""
     if limit < 0 or limit > 128:
@@ -815,10 +836,11 @@ def moe_ragged_with_shared_bank(x, rb: Ragged, shared_bank: Bank, inds, scores, 
     cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
     rc = L.exl3_moe_ragged_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, rb.inter, ctypes.byref(cr),
                                             ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"),
-                                            topk, dec.c(), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
-                                            ws.numel(), _stream(x.device))
+                                            topk, dec.c(), int(verify_rows), int(limit), y.data_ptr(), _dt(y, "y"),
+                                            ws.data_ptr(), ws.numel(), _stream(x.device))
     if rc == EXL3_DECLINED:
-        return moe_ragged(x, rb, inds, scores, dec, False, _shared_rows(x, shared_bank, dec, limit), limit)
+        return moe_ragged(x, rb, inds, scores, dec, verify_rows, _shared_rows(x, shared_bank, dec, limit),
+                          limit=limit)
     _check(rc)
     return y.reshape(x.shape)
 
@@ -837,9 +859,10 @@ def reconstruct_tiled(tp: TiledProj, expert: int, dec: Decode) -> torch.Tensor:
     return out
 
 
-def moe_tiled(x, tb: Tiled, inds, scores, dec: Decode, shared=None, limit: int = 0) -> torch.Tensor:
-    """The routed SwiGLU chain (`moeRagged`, root.zig:582-644) over a per-tile-rate bank; `shared` and `limit` as
-    for moe_ragged."""
+def moe_tiled(x, tb: Tiled, inds, scores, dec: Decode, shared=None, limit: int = 0, verify_rows: bool = False,
+              shared_gate=None) -> torch.Tensor:
+    """The routed SwiGLU chain (`moeRagged`, root.zig:582-644) over a per-tile-rate bank; `shared`, `shared_gate`,
+    `verify_rows` and `limit` as for moe_ragged."""
     if limit < 0 or limit > 128:
         raise InvalidExl3Clamp(f"clamp limit {limit} outside 1..128 (0 = none)")
     dec.require_table()
@@ -848,22 +871,21 @@ def moe_tiled(x, tb: Tiled, inds, scores, dec: Decode, shared=None, limit: int =
     hidden = int(x.shape[-1])
     if hidden != tb.hidden:
         raise BadExl3Shape(f"moe_tiled: hidden {hidden} vs bank {tb.hidden}")
-    _need_gpu(x2, inds2, sc2, shared, tb.gate.trellis)
+    _need_gpu(x2, inds2, sc2, tb.gate.trellis)
     y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
-    if shared is not None:
-        shared = shared.reshape(rows, hidden).contiguous()
+    shared, shared_gate = _shared_operands(y, rows, shared, shared_gate, "moe_tiled")
     L = _lib.load()
     ws = workspace.get(x.device, L.exl3_moe_workspace_size(rows, topk, hidden, tb.inter))
     ct = tb.c()
     _check(L.exl3_moe_tiled(x2.data_ptr(), _dt(x2, "x"), rows, hidden, tb.inter, ctypes.byref(ct), inds2.data_ptr(),
-                            sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(limit),
-                            None if shared is None else shared.data_ptr(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
-                            ws.numel(), _stream(x.device)))
+                            sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(verify_rows), int(limit),
+                            _ptr(shared), _ptr(shared_gate), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
+                            _stream(x.device)))
     return y.reshape(x.shape)
 
 
 def moe_tiled_with_shared_bank(x, tb: Tiled, shared_bank: Bank, inds, scores, dec: Decode,
-                               limit: int = 0) -> torch.Tensor:
+                               limit: int = 0, verify_rows: bool = False) -> torch.Tensor:
     """moe_tiled with its shared expert (a uniform one-expert bank) in the same launches, as moe_with_shared_bank;
     where the fused form declines, the shared expert runs as a one-expert chain and joins through `shared`."""
     if limit < 0 or limit > 128:
@@ -884,10 +906,10 @@ def moe_tiled_with_shared_bank(x, tb: Tiled, shared_bank: Bank, inds, scores, de
     cs = _lib.BankT(shared_bank.gate.c(), shared_bank.up.c(), shared_bank.down.c())
     rc = L.exl3_moe_tiled_with_shared_bank(x2.data_ptr(), _dt(x2, "x"), rows, hidden, tb.inter, ctypes.byref(ct),
                                            ctypes.byref(cs), inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"),
-                                           topk, dec.c(), int(limit), y.data_ptr(), _dt(y, "y"), ws.data_ptr(),
-                                           ws.numel(), _stream(x.device))
+                                           topk, dec.c(), int(verify_rows), int(limit), y.data_ptr(), _dt(y, "y"),
+                                           ws.data_ptr(), ws.numel(), _stream(x.device))
     if rc == EXL3_DECLINED:
-        return moe_tiled(x, tb, inds, scores, dec, _shared_rows(x, shared_bank, dec, limit), limit)
+        return moe_tiled(x, tb, inds, scores, dec, _shared_rows(x, shared_bank, dec, limit), limit, verify_rows)
     _check(rc)
     return y.reshape(x.shape)
 

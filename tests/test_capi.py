@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_host_side_refusals():
     lib = L.load()
-    assert lib.exl3_abi_version() == 4
+    assert lib.exl3_abi_version() == 5
     d = L.DecodeT(1, 16, -1)
     # bad shape: in not a multiple of 128 -> refused before any launch (null pointers never touched)
     assert lib.exl3_linear(None, 0, 1, 100, 128, None, 64, None, None, d, None, 0, None, 0, None) == -1
@@ -90,8 +90,8 @@ def test_tiled_refusals():
     tb.experts, tb.n_a, tb.n_b = 4, 16, 32
 
     def moe(dec, bank=tb):
-        return lib.exl3_moe_tiled(None, 0, 0, 128, 128, ctypes.byref(bank), None, None, 2, 8, dec, 0, None, None, 0,
-                                  None, 0, None)
+        return lib.exl3_moe_tiled(None, 0, 0, 128, 128, ctypes.byref(bank), None, None, 2, 8, dec, 0, 0, None, None,
+                                  None, 0, None, 0, None)
 
     assert moe(L.DecodeT(2, 15, 1)) == 0  # spec1-w15 has rows at 16 and 32; zero rows: nothing to launch
     assert moe(L.DecodeT(1, 16, -1)) == 0  # MCG

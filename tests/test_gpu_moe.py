@@ -337,7 +337,7 @@ def test_moe_with_shared_bank_serves_wide_batches_in_the_sorted_arm(dev, rows):
     x2 = xd.contiguous()
     with exl3.arm_overrides(moe_gemm=0):
         rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                         ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
+                                         ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0, 0,
                                          y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(),
                                          exl3._stream(dev))
         assert rc == 0, exl3._lib.last_error()
@@ -370,7 +370,7 @@ def test_moe_with_shared_bank_declines_to_the_two_calls(dev, case):
     x2 = xd.contiguous()
     with exl3.arm_overrides(moe_gemm=0):
         rc = L.exl3_moe_with_shared_bank(x2.data_ptr(), exl3._dt(x2, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                         ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
+                                         ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0, 0,
                                          y0.data_ptr(), exl3._dt(y0, "y"), ws.data_ptr(), ws.numel(),
                                          exl3._stream(dev))
         torch.cuda.synchronize()
@@ -588,7 +588,7 @@ def test_moe_gemm_arm_serves_the_shared_bank_in_its_launches(dev, rows, E, k, dt
     ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
     y = torch.empty_like(xd)
     rc = L.exl3_moe_with_shared_bank(xd.data_ptr(), exl3._dt(xd, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), limit,
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0, limit,
                                      y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
     assert rc == 0, exl3._lib.last_error()
     ref = _two_calls(xd, bd, sd, xi, sc, exl3.MCG, limit)
@@ -624,7 +624,7 @@ def test_moe_gemm_arm_shared_bank_at_the_expert_table_limit(dev, E):
     ws = exl3.workspace.get(dev, L.exl3_moe_with_shared_bank_workspace_size(rows, k, hidden, inter))
     y = torch.full_like(x, 7.0)
     rc = L.exl3_moe_with_shared_bank(x.data_ptr(), exl3._dt(x, "x"), rows, hidden, inter, E, ctypes.byref(cb),
-                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0,
+                                     ctypes.byref(cs), xi.data_ptr(), sc.data_ptr(), 2, k, exl3.MCG.c(), 0, 0,
                                      y.data_ptr(), exl3._dt(y, "y"), ws.data_ptr(), ws.numel(), exl3._stream(dev))
     ref = _two_calls(x, bd, sd, xi, sc, exl3.MCG)
     torch.cuda.synchronize()
