@@ -324,8 +324,9 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0
 // The routed GEMM arm (prefill widths): slots sorted by expert into windows of up to MOE_GEMM_WINDOW_ROWS rows, each
 // window's rows prepared into MFMA fragment order and run through the decode-once GEMM (each weight decoded once per
 // window instead of once per 4-row GEMV window), then the mid, the down GEMM and the reduce.  Taken when the layer
-// averages at least kMoeGemmMinSlotsPerExpert slots per expert, on a uniform bank at one lane-reader rate (C4's layer,
-// E = 256 top-8: 8 slots per expert 457 us against 669 on the GEMV windows, 4 slots 423 against 394).
+// averages at least kMoeGemmMinSlotsPerExpert slots per expert (C4's layer, E = 256 top-8: 8 slots per expert 457 us
+// against 669 on the GEMV windows, 4 slots 423 against 394), on a bank whose decode waves have a reader: a uniform
+// bank at one lane-reader rate, a ragged bank of lane-reader rates, or a per-tile-rate bank.
 constexpr int kMoeGemmMinSlotsPerExpert = 8;
 
 struct MoeGemmPlan {
@@ -349,9 +350,9 @@ MoeGemmPlan plan_moe_gemm(int nslots, int hidden, int inter, int experts) {
     return p;
 }
 
-bool moe_gemm_wanted(int nslots, int experts, bool uniform_lane_rate) {
+bool moe_gemm_wanted(int nslots, int experts, bool gemm_bank) {
     const int k = knob(EXL3_KNOB_MOE_GEMM, -1);
-    if (k == 0 || !uniform_lane_rate || experts > kMoeGemmMaxExperts) return false;
+    if (k == 0 || !gemm_bank || experts > kMoeGemmMaxExperts) return false;
     return k > 0 || (long)nslots >= (long)kMoeGemmMinSlotsPerExpert * experts;
 }
 
@@ -387,10 +388,12 @@ struct SharedBank {
 
 // On the GEMM arm the shared bank's rows join as one more expert (any y dtype).  Otherwise they need the per-slot
 // arm, a 16-bit output dtype (the combine word holds both rounded sums), the routed and shared folds (routed, shared
-// and combine words: three per output), and, for a uniform bank, the routed rate.
-bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts, int n, bool verify) {
+// and combine words: three per output), and, for a uniform bank, the routed rate.  gemm_bank: the routed bank and the
+// shared bank's rate can take the GEMM arm.
+bool moe_shared_fusable(int rows, int topk, int hidden, int inter, int y_dtype, int experts, bool gemm_bank,
+                        bool verify) {
     const int nslots = rows * topk;
-    if (!verify && moe_gemm_wanted(nslots, experts, lane_rate(n))) return experts < kMoeGemmMaxExperts;
+    if (!verify && moe_gemm_wanted(nslots, experts, gemm_bank)) return experts < kMoeGemmMaxExperts;
     if (y_dtype == EXL3_DT_F32) return false;
     const bool windowed = rows > moe_decode_rows_max();
     if (windowed && !(moe_windows_enabled() && moe_windowed(rows, nslots, experts))) return false;
@@ -418,8 +421,13 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
                    const TiledTables *tt = nullptr) {
     if (reinterpret_cast<uintptr_t>(x) % 4) return fail(EXL3_ERR_BAD_SHAPE, "moe: x must be 4-byte aligned");
     const int nslots = rows * topk;
-    if (!verify && (!sb || (sb->n == n[0] && !shared && experts < kMoeGemmMaxExperts)) && !meta && !tt &&
-        n[0] == n[1] && n[1] == n[2] && moe_gemm_wanted(nslots, experts, lane_rate(n[0]))) {
+    // The GEMM arm's banks: uniform at one lane-reader rate, ragged with lane-reader rates only (meta_lane_only), or
+    // per-tile rates; a fused shared bank at a lane-reader rate (the routed rate with a uniform bank).
+    const bool uniform_lane = !meta && !tt && n[0] == n[1] && n[1] == n[2] && lane_rate(n[0]);
+    const bool gemm_bank = uniform_lane || (meta && meta_lane_only) || tt;
+    const bool gemm_shared = !sb || (!shared && experts < kMoeGemmMaxExperts && lane_rate(sb->n) &&
+                                     (!uniform_lane || sb->n == n[0]));
+    if (!verify && gemm_bank && gemm_shared && moe_gemm_wanted(nslots, experts, true)) {
         // a shared bank's rows are slots nslots .. nslots + rows - 1 of one more expert (index `experts`)
         const int sh_rows = sb ? rows : 0;
         const MoeGemmPlan gp = plan_moe_gemm(nslots + sh_rows, hidden, inter, experts + (sb ? 1 : 0));
@@ -456,8 +464,19 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         g.experts = experts;
         g.nslots = nslots;
         g.sh = sb ? 1 : 0;
-        g.n = n[0];
+        g.n = uniform_lane ? n[0] : 0;
+        g.sh_n = sb ? sb->n : 0;
         g.k = k;
+        g.table = table;
+        g.meta = meta;
+        g.meta_col[0] = 0;
+        g.meta_col[1] = 1;
+        if (tt) {
+            g.seg_off[0] = tt->off[0];
+            g.seg_off[1] = tt->off[1];
+            g.seg_k1[0] = tt->k1[0];
+            g.seg_k1[1] = tt->k1[1];
+        }
         g.clamp_limit = (float)clamp_limit;
         g.max_tiles = gp.max_tiles;
         g.max_windows = gp.max_windows;
@@ -488,6 +507,11 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         d.mid_svh[1] = sv[1];
         d.down_suh = su[2];
         d.trellis[0] = tr[2];
+        d.meta_col[0] = 2;
+        if (tt) {
+            d.seg_off[0] = tt->off[2];
+            d.seg_k1[0] = tt->k1[2];
+        }
         if (sb) {
             d.sh_mid_svh[0] = sb->sv[0];
             d.sh_mid_svh[1] = sb->sv[1];
@@ -1052,7 +1076,8 @@ int32_t exl3_moe_with_shared_bank(const void *x, int32_t x_dtype, int32_t rows, 
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_with_shared_bank: null operand");
-    if (sb.n != routed_n || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts, routed_n, verify_rows))
+    if (sb.n != routed_n ||
+        !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, experts, lane_rate(routed_n), verify_rows))
         return declined("moe_with_shared_bank: declined (rows=%d, y dtype %d, rates %d/%d): run the shared expert as "
                         "a one-expert exl3_moe and pass it to exl3_moe as `shared`", rows, y_dtype, routed_n, sb.n);
     const uint16_t *tr[3] = {bank->gate.trellis, bank->up.trellis, bank->down.trellis};
@@ -1094,10 +1119,10 @@ int32_t exl3_moe_ragged_with_shared_bank(const void *x, int32_t x_dtype, int32_t
     }
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_ragged_with_shared_bank: null operand");
-    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0, verify_rows))
+    const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);
+    if (!moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, lane_only, verify_rows))
         return declined("moe_ragged_with_shared_bank: declined (rows=%d, y dtype %d): run the shared expert as a "
                         "one-expert exl3_moe and pass it to exl3_moe_ragged as `shared`", rows, y_dtype);
-    const bool lane_only = bank->lane_rates_only != 0 && lane_rate(sb.n);
     const int n0[3] = {0, 0, 0};
     return moe_launch(fam, k, dec, table, x, x_dtype, rows, hidden, inter, bank->experts, bank->trellis, bank->suh,
                       bank->svh, n0, bank->meta, lane_only, inds, scores, scores_dtype, topk, verify_rows != 0,
@@ -1180,7 +1205,7 @@ int32_t exl3_moe_tiled_with_shared_bank(const void *x, int32_t x_dtype, int32_t 
     }
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_tiled_with_shared_bank: null operand");
-    if (!lane_rate(sb.n) || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, 0, verify_rows))
+    if (!lane_rate(sb.n) || !moe_shared_fusable(rows, topk, hidden, inter, y_dtype, bank->experts, true, verify_rows))
         return declined("moe_tiled_with_shared_bank: declined (rows=%d, y dtype %d, shared n=%d): run the shared expert "
                         "as a one-expert exl3_moe and pass it to exl3_moe_tiled as `shared`", rows, y_dtype, sb.n);
     const int n0[3] = {0, 0, 0};

@@ -11,6 +11,7 @@
 // Integer rates (n = 16K) use this reader; other rates are first decoded to a transposed f16 copy in workspace.
 #include "exl3_kernels.h"
 #include "exl3_lane_decode.h"
+#include "exl3_tables.h"
 
 namespace exl3 {
 
@@ -869,6 +870,41 @@ __device__ __forceinline__ uint32_t moe_token(const MoeGemmArgs &a, uint32_t slo
 // the out / 128 column groups of one window are numbered to land on one XCD one after another: they read the same
 // prepared rows, which then come from that XCD's L2 after the first (numbered by the window, each group would pull
 // them through its own XCD's L2).
+// N > 0: a uniform bank at rate N.  N == -1: a ragged bank (`rate_groups.moePrefill`, rate_groups.zig:2039-2075):
+// each workgroup reads its expert's rate and tile offset from the meta table and its decode waves take that rate's
+// reader (one launch for every rate group; the MFMA waves are the same for all).  N == N_TILED: a per-tile-rate bank,
+// the decode waves reading each k-step's segment offset and rate mask.  Either way a fused shared expert (expert
+// `experts`) decodes at its own uniform rate sh_n.
+template <int FAM>
+__device__ __forceinline__ DecodeK rate_decode(const DecodeK &base, int table, int n) {
+    DecodeK k = base;
+    if constexpr (FAM == FAM_HASH || FAM == FAM_PAIR) table_row(table, n, k.mult, k.mask0, k.mask1, k.rot);
+    return k;
+}
+
+// The decode waves at a rate known only at run time (a lane-reader rate; any other leaves the slab undecoded, which
+// the host rules out).
+template <int FAM>
+__device__ __forceinline__ void gemm4_decode_waves_at(int n, const uint16_t *bank, int OT, int og, int nks, int lane,
+                                                      const DecodeK &k, uint16_t (*Bs)[128 * G2_BP]) {
+    const int r = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) - 8;
+    switch (n) {
+#define EXL3_RATE_CASE(NN)                                                                                             \
+    case NN: {                                                                                                         \
+        RateReader<FAM, NN> rd(bank, r, OT, og, nks, lane, k);                                                          \
+        gemm4_decode_waves<FAM>(rd, nks, r, lane, Bs);                                                                  \
+    } break;
+        EXL3_RATE_CASE(16)
+        EXL3_RATE_CASE(24)
+        EXL3_RATE_CASE(32)
+        EXL3_RATE_CASE(40)
+        EXL3_RATE_CASE(48)
+        EXL3_RATE_CASE(64)
+#undef EXL3_RATE_CASE
+    default: break;
+    }
+}
+
 template <int FAM, int N>
 __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     const int nog = a.out / 128, L = blockIdx.x, q = L >> 3;
@@ -881,15 +917,41 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
     const uint16_t *xfrag0 = a.xp[p] + (size_t)a.win.win_tile0[w] * (size_t)(a.in / 32) * 512;
     float *planes = a.planes[p];
-    const uint16_t *bank = e < a.experts ? a.trellis[p] + (size_t)e * IT * OT * N : a.sh_trellis[p];
-    gemm4_tile<FAM, N>(a.in, a.out, og, bank, xfrag0, rows, a.k, Bs,
-                       [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
-                           for (int i = 0; i < live; i++) {
-                               float *row = planes + (size_t)slots[m + i] * a.out + (size_t)og * 128;
-                               row[ln] = v0[i];
-                               row[ln + 64] = v1[i];
-                           }
-                       });
+    auto emit = [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
+        for (int i = 0; i < live; i++) {
+            float *row = planes + (size_t)slots[m + i] * a.out + (size_t)og * 128;
+            row[ln] = v0[i];
+            row[ln + 64] = v1[i];
+        }
+    };
+    if constexpr (N > 0) {
+        const uint16_t *bank = e < a.experts ? a.trellis[p] + (size_t)e * IT * OT * N : a.sh_trellis[p];
+        gemm4_tile<FAM, N>(a.in, a.out, og, bank, xfrag0, rows, a.k, Bs, emit);
+    } else {
+        const int lane = threadIdx.x & 63;
+        const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        if (wave < 8) {
+            gemm4_mfma_waves(a.in, xfrag0, rows, Bs, emit);
+            return;
+        }
+        const int nks = IT / 4;
+        if (e >= a.experts) {  // the shared expert: its own uniform bank
+            gemm4_decode_waves_at<FAM>(a.sh_n, a.sh_trellis[p], OT, og, nks, lane, rate_decode<FAM>(a.k, a.table, a.sh_n),
+                                       Bs);
+            return;
+        }
+        if constexpr (N == N_TILED) {
+            TiledReader<FAM> rd(a.trellis[p], a.seg_off[p], a.seg_k1[p], e, wave - 8, IT, OT, og, nks, lane,
+                                rate_decode<FAM>(a.k, a.table, TILED_NA), rate_decode<FAM>(a.k, a.table, TILED_NB));
+            gemm4_decode_waves<FAM>(rd, nks, wave - 8, lane, Bs);
+        } else {
+            const uint32_t *m = a.meta + (size_t)e * 8;
+            const int col = a.meta_col[p];
+            const int n = (int)m[col];
+            gemm4_decode_waves_at<FAM>(n, a.trellis[p] + 2 * (size_t)m[4 + col], OT, og, nks, lane,
+                                       rate_decode<FAM>(a.k, a.table, n), Bs);
+        }
+    }
 }
 
 // ---- the routed GEMM arm's inputs.  Tile t (16 sorted rows of one window, the window's tiles contiguous from
@@ -1043,6 +1105,15 @@ template <int FAM>
 static hipError_t launch_moe_gemm_fam(const MoeGemmArgs &a, int nproj, hipStream_t s) {
     // x: column group and window, the windows rounded up to whole rounds of the 8 XCDs (the extra ones exit)
     const dim3 grid((unsigned)(a.out / 128) * (unsigned)((a.max_windows + 7) / 8 * 8), (unsigned)nproj);
+    if (a.seg_off[0]) {  // per-tile rates: the hash-product families
+        if constexpr (FAM == FAM_PAIR || FAM == FAM_MUL1) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((moe_gemm4_kernel<FAM, N_TILED>), grid, dim3(G4_THREADS), 0, s, a);
+        return hipGetLastError();
+    }
+    if (a.meta) {
+        hipLaunchKernelGGL((moe_gemm4_kernel<FAM, -1>), grid, dim3(G4_THREADS), 0, s, a);
+        return hipGetLastError();
+    }
     switch (a.n) {
     case 16: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 16>), grid, dim3(G4_THREADS), 0, s, a); break;
     case 24: hipLaunchKernelGGL((moe_gemm4_kernel<FAM, 24>), grid, dim3(G4_THREADS), 0, s, a); break;

@@ -224,8 +224,17 @@ struct MoeGemmArgs {
     const uint16_t *suh[2];
     const uint16_t *sh_trellis[2];
     const uint16_t *sh_suh[2];
-    int n;
-    DecodeK k;
+    int n;                  // uniform rate; 0 with `meta` (ragged) or `seg_off` (per-tile rates)
+    int sh_n;               // the shared expert's rate (a lane-reader rate)
+    DecodeK k;              // the decode at n (uniform), else the codebook's base constants
+    int table;              // codebook table of the per-rate rows (hash / pair families)
+    // ragged bank (rate_groups.zig:22-140): meta [E][8], projection p's rate at column meta_col[p] and its tiles' u32
+    // word offset at column 4 + meta_col[p]; every rate a lane-reader rate (the host checks)
+    const uint32_t *meta;
+    int meta_col[2];
+    // per-tile-rate bank: projection p's segment tables [E][in/16][out/128] (word offset, TILED_NA mask)
+    const uint32_t *seg_off[2];
+    const uint8_t *seg_k1[2];
     uint16_t *xp[2];        // prepared inputs, fragment order
     float *planes[2];       // raw inner [slots][out]
     // the mid (down input): gate / up planes [slots][inter] -> xp_down, with the gate / up svh and the down suh

@@ -75,7 +75,7 @@ def _verify_case(dev, variant):
     return lambda v: exl3.moe_tiled_with_shared_bank(x, tb, sd, xi, sc, exl3.MCG, verify_rows=v)
 
 
-VARIANTS = ["moe", "gated", "shared_bank"]
+VARIANTS = ["moe", "gated", "shared_bank", "ragged", "ragged_shared_bank", "tiled", "tiled_shared_bank"]
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
