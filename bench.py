@@ -53,7 +53,9 @@ def _capture(calls, dev):
     return g
 
 
-def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int = ROUNDS):
+def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int = ROUNDS, codebook: str = "3inst"):
+    """C1's GEMV; `codebook` "3inst" (the configuration's, an extension the reference lacks) or "mcg" (the same codes
+    through the reference's MCG decode, whose arithmetic the reference's fixtures pin)."""
     import statistics
 
     import torch
@@ -68,7 +70,7 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
     svh = synth.sign_scale(0, "c1.svh", (1, out_f), device=dev)
     x = synth.normal(0, "c1.x", (rows, in_f), device=dev)
     projs = [exl3.Proj(trellis[i:i + 1], suh, svh) for i in range(COPIES)]
-    dec = exl3.INST3
+    dec = exl3.INST3 if codebook == "3inst" else exl3.MCG
     y = exl3.linear(x, projs[0], dec)  # workspace, library load
     for i in range(warmup):
         exl3.linear(x, projs[i % COPIES], dec)
@@ -111,6 +113,8 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
         walls.append(time.perf_counter() - t0)
         events.append(e0.elapsed_time(e1))
     bytes_per_call = _algorithmic_bytes(in_f, out_f, n, rows)
+    del full, tail, trellis, projs
+    torch.cuda.empty_cache()
     return dict(wall_s=statistics.median(walls), event_ms=statistics.median(events), bytes=bytes_per_call, rows=rows,
                 y=y, steps=steps, rounds=rounds, wall_rounds_s=walls)
 
@@ -121,8 +125,10 @@ def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
     `layers` MoE layers back to back on one stream, captured once as a HIP graph and replayed: the stream runs them
     in order, as the reference's dependent chain (bench_util.zig:20-58) runs its calls, but each layer reads its own
     N(0,1) hidden state (an unnormalised chain of SwiGLU layers squares its scale per layer and is inf by the fourth)
-    and every layer has its own routing, so the distinct experts hit change from layer to layer.  The banks' svh
-    carry 1/sqrt(in) (synth norm), keeping each layer's output near unit scale.  Median of `rounds` replays."""
+    and every layer has its own routing, so the distinct experts hit change from layer to layer.  Every layer has its
+    own bank (16 x 302 MB), as a model's layers do: the weights a layer reads were last read 15 layers (4.5 GB, far
+    past the 256 MB Infinity Cache) earlier, so they come from HBM.  The banks' svh carry 1/sqrt(in) (synth norm),
+    keeping each layer's output near unit scale.  Median of `rounds` replays."""
     import statistics
 
     import torch
@@ -131,8 +137,9 @@ def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
 
     dev = torch.device("cuda:0")
     E, hidden, inter, n, k = 256, 2048, 768, 32, 8
-    bank = synth.bank(3, "c4", E, hidden, inter, n, device=dev, norm=True)
-    shared = synth.bank(3, "c4.shared", 1, hidden, inter, n, device=dev, norm=True)
+    banks = [synth.bank(3, f"c4.l{layer}", E, hidden, inter, n, device=dev, norm=True) for layer in range(layers)]
+    shareds = [synth.bank(3, f"c4.shared.l{layer}", 1, hidden, inter, n, device=dev, norm=True)
+               for layer in range(layers)]
     xs = [synth.normal(3, f"c4.x{batch}.{layer}", (batch, hidden), device=dev) for layer in range(layers)]
     routes = []
     for layer in range(layers):
@@ -142,8 +149,8 @@ def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
     def chain():
         # routed experts + the shared expert in one call: the fused form runs both in the same launches; where it
         # declines, the wrapper runs the shared expert as a one-expert chain first
-        return [exl3.moe_with_shared_bank(x, bank, shared, inds, scores, exl3.MCG) for x, (inds, scores) in
-                zip(xs, routes)]
+        return [exl3.moe_with_shared_bank(x, bank, shared, inds, scores, exl3.MCG)
+                for x, (inds, scores), bank, shared in zip(xs, routes, banks, shareds)]
 
     chain()
     torch.cuda.synchronize()
@@ -160,6 +167,8 @@ def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
     layer_us = statistics.median(times)
     distinct = sum(len(set(i.flatten().tolist())) for i, _ in routes) / layers
     per_expert = 3 * (hidden * inter * n // 128 + 2 * (hidden + inter))
+    del g, banks, shareds
+    torch.cuda.empty_cache()
     return dict(batch=batch, layer_us=layer_us, us_per_token=layer_us / batch, distinct=distinct,
                 bytes=(distinct + 1) * per_expert)
 
@@ -452,6 +461,11 @@ def sweep(which: str, prefill_batches=None, prefill_arms=("gemm", "windows")):
             bench_moe_prefill(prefill_batches, arms=prefill_arms)
         else:
             bench_moe_prefill(arms=prefill_arms)
+    if which in ("moe_prefill", "c5_prefill", "all"):
+        if prefill_batches:
+            bench_moe_prefill_c5(prefill_batches, arms=prefill_arms)
+        else:
+            bench_moe_prefill_c5(arms=prefill_arms)
     if which in ("pack", "all"):
         for pm in (False, True):
             print(json.dumps(bench_pack(pm)), flush=True)
@@ -663,6 +677,71 @@ def bench_moe_prefill(batches=(64, 128, 256, 512, 1024, 2048), layers: int = 4, 
     return out
 
 
+def bench_moe_prefill_c5(batches=(256, 512, 1024, 2048), layers: int = 2, arms=("gemm", "windows"),
+                         forms=("ragged", "tiled")):
+    """configs[4]'s layer (hidden 4096, inter 2048, 256 experts at 1.75 bpw, SPEC1 spec1-w15, top-8, plus a K=4 shared
+    expert) at prefill widths, on the routed GEMM arm and on the GEMV expert windows (arm overrides), for the ragged
+    rate-group bank (64 experts at K1, 192 at K2) and the per-tile K1 / K2 bank; the shared expert rides the routed
+    launches where the fused form serves, else runs as the pair of calls.  Median of 7 replays of `layers` layers
+    from a HIP graph."""
+    import statistics
+
+    import torch
+
+    from sushi_amd import exl3, synth
+
+    dev = torch.device("cuda:0")
+    hidden, inter, k = 4096, 2048, 8
+    dec = exl3.Decode(exl3.Codebook.spec1, exl3.Window(15), 1)
+    shared = synth.bank(5, "c5.shared", 1, hidden, inter, 64, device=dev, norm=True)
+    out = []
+    for form in forms:
+        if form == "ragged":
+            g1 = synth.bank(5, "c5.k1", 64, hidden, inter, 16, device=dev, norm=True)
+            g2 = synth.bank(5, "c5.k2", 192, hidden, inter, 32, device=dev, norm=True)
+            bank = exl3.Ragged.init([g1, g2])
+            del g1, g2
+            call = lambda x, i, s: exl3.moe_ragged_with_shared_bank(x, bank, shared, i, s, dec)  # noqa: E731
+        else:
+            bank = synth.tiled_bank(5, "c5t", 256, hidden, inter, 0.25, device=dev, norm=True)
+            call = lambda x, i, s: exl3.moe_tiled_with_shared_bank(x, bank, shared, i, s, dec)  # noqa: E731
+        for batch in batches:
+            xs = [synth.normal(5, f"c5.pf{batch}.{l}", (batch, hidden), device=dev) for l in range(layers)]
+            routes = [exl3.moe_routing_chain(synth.normal(5, f"c5.pfl{batch}.{l}", (batch, 256), dtype=torch.float32)
+                                             .to(dev), k) for l in range(layers)]
+            line = {"config": "c5_prefill", "form": form, "batch": batch, "slots_per_expert": round(batch * k / 256, 2)}
+            for arm, knob in (("gemm", 1), ("windows", 0)):
+                if arm not in arms:
+                    continue
+                with exl3.arm_overrides(moe_gemm=knob):
+                    chain = lambda: [call(x, i, s) for x, (i, s) in zip(xs, routes)]  # noqa: E731
+                    chain()
+                    torch.cuda.synchronize()
+                    g = _capture(chain, dev) if SWEEP_GRAPHS else None
+                    stream = torch.cuda.current_stream(dev)
+                    ts = []
+                    for _ in range(ROUNDS):
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record(stream)
+                        if g is not None:
+                            g.replay()
+                        else:
+                            chain()
+                        e1.record(stream)
+                        torch.cuda.synchronize()
+                        ts.append(e0.elapsed_time(e1) * 1e3 / layers)
+                    us = statistics.median(ts)
+                    line[arm] = {"layer_us": round(us, 1), "us_per_token": round(us / batch, 3)}
+                    del g
+            if "gemm" in line and "windows" in line:
+                line["windows_over_gemm"] = round(line["windows"]["layer_us"] / line["gemm"]["layer_us"], 2)
+            print(json.dumps(line), flush=True)
+            out.append(line)
+        del bank, call
+        torch.cuda.empty_cache()
+    return out
+
+
 def copy_calibration(mib: int, reps: int = 4):
     """A plain device-to-device copy of `mib` MiB, `reps` times: the reference kernel whose FETCH_SIZE/WRITE_SIZE
     counters calibrate the HBM-traffic figures of the GEMV (expected: exactly `mib` MiB read and written)."""
@@ -677,16 +756,19 @@ def copy_calibration(mib: int, reps: int = 4):
 
 def _profiled_traffic():
     """HBM bytes per GEMV launch from the committed counter summary (two rocprofv3 --pmc passes, FETCH_SIZE then
-    WRITE_SIZE, scaled by the same counters read over a plain copy kernel), or None if it is absent."""
+    WRITE_SIZE, scaled by the same counters read over a plain copy kernel): the sum of the last column ("bytes per
+    launch") of its FETCH_SIZE and WRITE_SIZE table rows, or None if the summary or either row is absent."""
     path = os.path.join(ROOT, "profiles", "gemv_c1_3inst_k4_b1_hbm_traffic.md")
+    found = {}
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(float(line.split(":", 1)[1]))
-    except OSError:
-        pass
-    return None
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if cells and cells[0] in ("FETCH_SIZE", "WRITE_SIZE"):
+                    found[cells[0]] = int(float(cells[-1]))
+    except (OSError, ValueError):
+        return None
+    return found["FETCH_SIZE"] + found["WRITE_SIZE"] if len(found) == 2 else None
 
 
 def _cpu_info():
@@ -797,12 +879,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-sample", type=int, default=40, help="calls per all-core CPU sample (0: no CPU baseline)")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-twin", action="store_true", help="skip the MCG twin of the headline GEMV")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the measured read/copy/8 MiB-launch ceilings")
     ap.add_argument("--no-graph", action="store_true", help="issue every call from Python instead of a HIP graph")
     ap.add_argument("--moe-batches", default="1,8,32", help="MoE layer batches (configs[3]); the first is headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 4 times (the counter-calibration kernel)")
-    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "moe_prefill", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
+    ap.add_argument("--sweep", choices=("c2", "c3", "c5", "moe_prefill", "c5_prefill", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     ap.add_argument("--prefill-batches", default="", help="moe_prefill sweep: token counts (default 64 .. 2048)")
     ap.add_argument("--prefill-arms", default="gemm,windows", help="moe_prefill sweep: arms to time")
     args = ap.parse_args()
@@ -820,6 +903,7 @@ def main() -> int:
     if args.copy_calibration > 0:
         copy_calibration(args.copy_calibration)
     lin = bench_linear(args.steps, args.warmup, not args.no_graph)
+    twin = None if args.no_twin else bench_linear(args.steps, args.warmup, not args.no_graph, codebook="mcg")
     steps = lin["steps"]
     ms_per_step = lin["wall_s"] / steps * 1e3
     value = lin["bytes"] / (lin["wall_s"] / steps) / 1e9
@@ -858,13 +942,24 @@ def main() -> int:
                      "measured_ceilings": ceilings},
         "cpu_baseline": cpu,
     }
+    if twin:
+        t_launch = twin["event_ms"] / 1e3 / twin["steps"]
+        t_ach = twin["bytes"] / t_launch / 1e9
+        out["mcg_twin"] = {
+            "what": "the headline GEMV with the same codes through the reference's MCG decode (3INST, the configured "
+                    "codebook, has no counterpart in the reference; MCG's arithmetic is pinned by its fixtures)",
+            "value": round(twin["bytes"] / (twin["wall_s"] / twin["steps"]) / 1e9, 2), "unit": "GB/s",
+            "ms_per_step": round(twin["wall_s"] / twin["steps"] * 1e3, 6),
+            "roofline": {"bound": "hbm", "achieved": round(t_ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(t_ach / HBM_PEAK_GBS, 4), "launch_us": round(t_launch * 1e6, 3)}}
     if ceilings:
         out["roofline"]["frac_of_measured_read"] = round(achieved / ceilings["hbm_read_GBps"], 4)
         out["roofline"]["launch_us_over_read_floor"] = round(launch_s * 1e6 / ceilings["read_small_graph_us"], 3)
     if moe:
         out["moe_layer"] = {"config": "E=256 routed + 1 shared, hidden 2048, inter 768, K2 MCG, top-8; 16 layers back "
-                                      "to back on one stream from a HIP graph, each its own N(0,1) input and routing "
-                                      "(svh with 1/sqrt(in)); median of 7 replays",
+                                      "to back on one stream from a HIP graph, each its own bank (16 x 302 MB, so "
+                                      "weights come from HBM), N(0,1) input and routing (svh with 1/sqrt(in)); "
+                                      "median of 7 replays",
                             "us_per_token": round(moe[0]["us_per_token"], 3),
                             "batches": [{"batch": m["batch"], "layer_us": round(m["layer_us"], 3),
                                          "us_per_token": round(m["us_per_token"], 3),
