@@ -93,13 +93,7 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
             for i in range(COPIES):
                 exl3.linear(x, projs[i], dec)
 
-    walls, events = [], []
-    for _ in range(rounds):
-        evict()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(stream)
+    def timed_calls():
         if graph_mode:
             for _ in range(steps // COPIES):
                 full.replay()
@@ -108,9 +102,25 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
         else:
             for i in range(steps):
                 exl3.linear(x, projs[i % COPIES], dec)
-        e1.record(stream)
+
+    # Each round times the `steps` calls twice, each time right after an untimed eviction pass.  Wall clock: bracketed
+    # by synchronisations, so it holds the host's submission of the calls too (the whole-job figure).  HIP events: the
+    # eviction pass is still running when the timed calls are submitted behind it, so the events bracket the timed
+    # kernels back to back on the GPU, not the host's graph-launch latency ahead of the first of them.
+    walls, events = [], []
+    for _ in range(rounds):
+        evict()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        timed_calls()
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        evict()
+        e0.record(stream)
+        timed_calls()
+        e1.record(stream)
+        torch.cuda.synchronize()
         events.append(e0.elapsed_time(e1))
     bytes_per_call = _algorithmic_bytes(in_f, out_f, n, rows)
     del full, tail, trellis, projs
@@ -930,8 +940,10 @@ def main() -> int:
         "config": {"workload": "EXL3 dense linear 4096x4096, K=4 (n=64), 3INST codebook, 16x16 tiles, batch 1, "
                                "64 rotating weight copies", "global_batch": 1, "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1.0 / (lin["wall_s"] / steps), 1),
-        "timing": f"median of {lin['rounds']} rounds of exactly {steps} calls, each round after an untimed replay of "
-                  "the 64-copy sequence (every timed call reads a copy last read 64 calls, 537 MB, earlier)"
+        "timing": f"median of {lin['rounds']} rounds of exactly {steps} calls, each after an untimed replay of the "
+                  "64-copy sequence (every timed call reads a copy last read 64 calls, 537 MB, earlier); value: wall "
+                  "clock between synchronisations; roofline.achieved: HIP events around the same calls submitted "
+                  "behind the eviction replay (the kernels back to back, without the host's launch latency)"
                   + ("; calls replayed from HIP graphs" if not args.no_graph else "; calls issued from Python"),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

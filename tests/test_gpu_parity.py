@@ -106,6 +106,81 @@ def test_c1_headline_shape_every_seed(dev, seed):
     _hold(d.inner(dec), d, odec, seed=seed, what=f"c1 seed {seed}")
 
 
+def _f16_ulp(v: np.ndarray) -> np.ndarray:
+    """The spacing of f16 values at |v| (2^-24 in the subnormal range)."""
+    a = np.abs(np.asarray(v, np.float64))
+    return 2.0 ** (np.floor(np.log2(np.maximum(a, 2.0 ** -14))) - 10)
+
+
+def _butterfly_prepared(x_row: np.ndarray, suh_bits: np.ndarray) -> np.ndarray:
+    """prepareInput f16(H128(f16(x) * suh)) (expert_exl3.zig:490-501) with the Hadamard as the GPU prologue forms it:
+    f32 butterflies over index bits 6, 5, ..., 0 (each a + b and a - b rounded once), then times f32(1/sqrt(128)),
+    then f16.  The reference's CPU path sums the dense O(128^2) Hadamard in another order, so a few elements round
+    to the neighbouring f16 (the summand bar's PREP_ULPS term allows for that); here the fold's own rounding is under
+    test, so the truth takes the prepared input the kernel multiplies with."""
+    v = (np.asarray(x_row, np.float16).astype(np.float32) * P.f16_bits(suh_bits).astype(np.float32)).reshape(-1, 128)
+    for h in (64, 32, 16, 8, 4, 2, 1):
+        w = v.reshape(v.shape[0], 128 // (2 * h), 2, h)
+        a, b = w[:, :, 0, :], w[:, :, 1, :]
+        v = np.stack([a + b, a - b], axis=2).reshape(-1, 128)
+    return (v.reshape(-1) * np.float32(0.08838834764831845)).astype(np.float16).astype(np.float64)
+
+
+def _fold_truth(d: "Dense", w: np.ndarray, p: np.ndarray, splits: int):
+    """y = svh * H(p w) in f64 (finishOutput, expert_exl3.zig:534-544) and each output's allowance beyond one f16 ulp:
+    the f32 accumulation of the inner sums (ACC_FACTOR sqrt(depth) 2^-24 of the largest inner magnitude of the block,
+    the summand bar's factor) and the fold's fixed point (half of 2^-24 per split term)."""
+    sv = P.f16_bits(d.svh)
+    inner = p[None] @ w
+    y = sv * P.hadamard_blocks(inner)[0]
+    blockmax = np.repeat(np.abs(inner[0]).reshape(-1, 128).max(axis=1), 128)
+    return y, np.abs(sv) * P.ACC_FACTOR * np.sqrt(d.in_f) * P.U_F32 * blockmax + splits * 2.0 ** -25
+
+
+def _within_one_ulp(got: np.ndarray, y: np.ndarray, allow: np.ndarray):
+    """(passes, exact fraction, worst excess): every f16 output within one f16 ulp of round_f16(truth) plus its
+    allowance."""
+    want = y.astype(np.float16).astype(np.float64)
+    err = np.abs(np.asarray(got, np.float64).reshape(-1) - want)
+    lim = _f16_ulp(want) + allow
+    return bool((err <= lim).all()), float(np.mean(err == 0)), float(np.max(err / lim))
+
+
+@pytest.mark.parametrize("label,seed", [("3inst", s) for s in range(P.PARITY_SEEDS)] + [("mcg", 0), ("mcg", 1)])
+def test_c1_fold_arm_every_output_within_one_f16_ulp(dev, label, seed):
+    """The arm bench.py times: configs[0]'s 4096 x 4096 K4 at batch 1 with an f16 output, which takes the fixed-point
+    fold over 8 splits (f32 outputs take the counters + planes arm, so the summand bar above never reaches it).  Every
+    f16 output must sit within one f16 ulp of round_f16 of the f64 truth built from the oracle's decoded weights
+    (src/exl3/expert_exl3_kernels.zig:3300-3352's standard, held per element; the allowance is a small fraction of an
+    ulp except where outputs cancel to near zero); the same outputs must fail that bar against the wrong codeword
+    window and against one flipped trellis bit.  3INST over PARITY_SEEDS seeds; MCG (the reference-pinned codebook of
+    the bench line's twin) over two."""
+    print(f"[parity] c1 fold arm {label} seed {seed}", flush=True)
+    d = Dense(dev, seed, 1, 4096, 4096, 64)
+    dec, odec = DECODES[label]
+    got = exl3.linear(d.xd, d.pd, dec).float().cpu().numpy().astype(np.float64)  # f16 output: the fold arm
+    p = _butterfly_prepared(d.x.numpy()[0], d.suh)
+    # the same values as the oracle's prepareInput up to the two transforms' f32 error: a neighbouring f16, or, where
+    # the block's inputs cancel to near zero, a few f32 roundings of the block's magnitude
+    moved = np.nonzero(p != d.p[0])[0]
+    tol = _f16_ulp(d.p[0][moved]) + 64 * P.U_F32 * np.abs(d.p[0]).max()
+    assert moved.size <= 32 and (np.abs(p - d.p[0])[moved] <= tol).all(), moved
+    w = P.decoded(d.t, d.in_f, d.out_f, d.n, odec)
+    y, allow = _fold_truth(d, w, p, splits=8)
+    ok, exact, worst = _within_one_ulp(got, y, allow)
+    frac = float(np.median(allow / _f16_ulp(y.astype(np.float16).astype(np.float64))))
+    print(f"[parity] c1 fold {label} seed {seed}: prepared input off the oracle's at {moved.size}, median allowance "
+          f"{frac:.4f} ulp, exact {exact:.5f}, worst error / (ulp + allowance) {worst:.3f}", flush=True)
+    assert ok, f"worst error / (ulp + allowance) = {worst:.3f}"
+    assert exact > 0.99
+    ww = P.decoded(d.t, d.in_f, d.out_f, d.n, P.mutated_window(odec))
+    assert not _within_one_ulp(got, _fold_truth(d, ww, p, 8)[0], allow)[0]
+    t = P.truth(p[None], w)
+    tb, where = P.flipped_truth(t, p[None], d.t, d.n, odec, np.random.default_rng(seed))
+    yb = P.f16_bits(d.svh) * P.hadamard_blocks(tb.inner)[0]
+    assert not _within_one_ulp(got, yb, allow)[0], where
+
+
 @pytest.mark.parametrize("rows", [1, 4, 16])
 @pytest.mark.parametrize("n", [32, 48, 64])
 @pytest.mark.parametrize("in_f,out_f", [(2048, 2048), (4096, 14336), (14336, 4096)])
