@@ -85,7 +85,8 @@ typedef enum {
     EXL3_ERR_CODEBOOK_UNSUPPORTED = -12,     /* encoder: CodebookUnsupported (src/encoder/encode.zig:7) */
     EXL3_ERR_RATE_UNSUPPORTED = -13,         /* encoder: RateUnsupported */
     EXL3_ERR_WINDOW_TOO_NARROW = -14,        /* encoder: WindowTooNarrow */
-    EXL3_ERR_HESSIAN = -15                   /* quantizer: HessianNotPositiveDefinite (src/encoder/quantize.zig:351) */
+    EXL3_ERR_HESSIAN = -15,                  /* quantizer: HessianNotPositiveDefinite (src/encoder/quantize.zig:351) */
+    EXL3_ERR_GROUP_MISSING = -16             /* Exl3GroupMissing (src/exl3/root.zig:647) */
 } exl3_status;
 
 /* One projection's bank (`Proj`, src/exl3/root.zig:28-30). */
@@ -202,6 +203,21 @@ int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_
                             const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh,
                             exl3_decode_t dec, void *y, int32_t y_dtype, hipStream_t stream);
 
+/* `linear.linearPair` (src/exl3/linear.zig:60-95): x [groups][rows][in] through the G-bank projection a (trellis
+ * [G][in/16][mid/16][a_n], suh [G][in], svh [G][mid]), that result read as [rows][G * mid] through the one-bank
+ * projection b (trellis [1][G*mid/16][out/16][b_n]) -> y [rows][out]: linearGrouped, the transpose and linear, bit
+ * for bit, without the transpose (a's finish writes its rows as b reads them) and in two launches.  The intermediate
+ * is in x's dtype, as the reference's is.  Returns EXL3_DECLINED (nothing launched) past one decode launch's 16 rows,
+ * as the reference returns null past its multi-row launch; the caller then makes the three calls. */
+size_t exl3_linear_pair_workspace_size(int32_t groups, int32_t rows, int32_t in_features, int32_t mid_features,
+                                       int32_t out_features);
+int32_t exl3_linear_pair(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in_features,
+                         int32_t mid_features, int32_t out_features, const uint16_t *a_trellis, int32_t a_n,
+                         const uint16_t *a_suh, const uint16_t *a_svh, exl3_decode_t a_dec,
+                         const uint16_t *b_trellis, int32_t b_n, const uint16_t *b_suh, const uint16_t *b_svh,
+                         exl3_decode_t b_dec, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
 /* Clears a workspace once after allocation.  Every workspace begins with an 8 MiB region of fused-finish arrival
  * counters, accumulators and their overflow words that must start at zero; the calls that use them always leave them
  * at zero again, and no other call writes there, so one init per allocation suffices.  Calls that share a workspace
@@ -248,6 +264,19 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
                         int32_t topk, exl3_decode_t dec, int32_t verify_rows, int32_t clamp_limit,
                         const void *shared, const void *shared_gate, void *y, int32_t y_dtype, void *workspace,
                         size_t workspace_bytes, hipStream_t stream);
+
+/* `moeGroups` (src/exl3/root.zig:646-703): a layer whose experts are split over `groups` uniform banks (banks[g] holds
+ * group_experts[g] experts, router ids counted across the groups in order), each group's routed output computed in
+ * f32 over every slot (a slot outside the group as local expert 0 with score 0, as the reference masks it), the
+ * groups' outputs summed in f32 in group order and rounded to y's dtype once.  One group is `moe` itself.  banks and
+ * group_experts are host arrays; every bank shares hidden and inter.  Refusals: EXL3_ERR_GROUP_MISSING without
+ * groups, and exl3_moe's. */
+size_t exl3_moe_groups_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter);
+int32_t exl3_moe_groups(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t groups,
+                        const exl3_bank_t *banks, const int32_t *group_experts, const uint32_t *inds,
+                        const void *scores, int32_t scores_dtype, int32_t topk, exl3_decode_t dec,
+                        int32_t verify_rows, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                        hipStream_t stream);
 
 /* A routed layer and its shared expert in one call.  Replaces the caller's pair of calls: the shared expert as a
  * one-expert chain (inds 0, score 1; the pattern of src/dsv41/dsv41_model.zig:3000) and then `moeWithShared`

@@ -21,11 +21,15 @@ EXPORTS = (
     "exl3_linear_grouped_workspace_size",
     "exl3_linear_grouped",
     "exl3_linear_noalloc",
+    "exl3_linear_pair_workspace_size",
+    "exl3_linear_pair",
     "exl3_workspace_init",
     "exl3_moe_workspace_size",
     "exl3_moe",
     "exl3_moe_with_gated_shared",
     "exl3_moe_ragged",
+    "exl3_moe_groups_workspace_size",
+    "exl3_moe_groups",
     "exl3_moe_with_shared_bank_workspace_size",
     "exl3_moe_with_shared_bank",
     "exl3_moe_ragged_with_shared_bank",
@@ -89,6 +93,10 @@ def load() -> ctypes.CDLL:
     L.exl3_linear_grouped_workspace_size.argtypes = [i32, i32, i32, i32, i32]
     L.exl3_linear_grouped.argtypes = [vp, i32, i32, i32, i32, i32, vp, i32, vp, vp, DecodeT, vp, i32, vp, sz, vp]
     L.exl3_linear_noalloc.argtypes = [vp, i32, i32, i32, i32, vp, i32, vp, vp, DecodeT, vp, i32, vp]
+    L.exl3_linear_pair_workspace_size.restype = sz
+    L.exl3_linear_pair_workspace_size.argtypes = [i32, i32, i32, i32, i32]
+    L.exl3_linear_pair.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, i32, vp, vp, DecodeT, vp, i32, vp, vp,
+                                   DecodeT, vp, i32, vp, sz, vp]
     L.exl3_workspace_init.argtypes = [vp, sz, vp]
     L.exl3_moe_workspace_size.restype = sz
     L.exl3_moe_workspace_size.argtypes = [i32, i32, i32, i32]
@@ -98,6 +106,10 @@ def load() -> ctypes.CDLL:
                                              DecodeT, i32, vp, vp, vp, i32, vp, sz, vp]
     L.exl3_moe_ragged.argtypes = [vp, i32, i32, i32, i32, ctypes.POINTER(RaggedT), vp, vp, i32, i32, DecodeT, i32,
                                   i32, vp, vp, vp, i32, vp, sz, vp]
+    L.exl3_moe_groups_workspace_size.restype = sz
+    L.exl3_moe_groups_workspace_size.argtypes = [i32, i32, i32, i32]
+    L.exl3_moe_groups.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(BankT), ctypes.POINTER(ctypes.c_int32),
+                                  vp, vp, i32, i32, DecodeT, i32, vp, i32, vp, sz, vp]
     L.exl3_moe_with_shared_bank_workspace_size.restype = sz
     L.exl3_moe_with_shared_bank_workspace_size.argtypes = [i32, i32, i32, i32]
     L.exl3_moe_with_shared_bank.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(BankT), ctypes.POINTER(BankT),

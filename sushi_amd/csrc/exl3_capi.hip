@@ -195,9 +195,12 @@ int32_t linear_checks(const void *x, int32_t x_dtype, int32_t groups, int32_t ro
     return ok();
 }
 
+// y_rows_major (decode-GEMV row counts only): group g's row r lands in output row r * groups + g, so y is
+// [rows][groups * out] (linearGroupedRows's layout, src/exl3/linear.zig:97-117) instead of [groups][rows][out].
 int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in, int32_t out,
                     const uint16_t *trellis, int32_t n, const uint16_t *suh, const uint16_t *svh, exl3_decode_t dec,
-                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream, bool split_ok = true) {
+                    void *y, int32_t y_dtype, void *ws, size_t ws_bytes, hipStream_t stream, bool split_ok = true,
+                    bool y_rows_major = false) {
     int fam;
     DecodeK k;
     int32_t rc = linear_checks(x, x_dtype, groups, rows, in, out, trellis, n, suh, svh, dec, y, y_dtype, &fam, &k);
@@ -229,6 +232,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.partial[0] = p.partial_bytes ? reinterpret_cast<float *>(w + p.counters_bytes) : nullptr;
         a.y = y;
         a.y_dtype = y_dtype;
+        a.y_rows_major = y_rows_major ? 1 : 0;
         a.splits = p.splits;
         a.groups = groups;
         a.nproj = 1;
@@ -245,6 +249,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.fold_arrivals = p.splits;
         return launched(run_gemv(fam, PRO_X, a, stream), "exl3_linear (gemv)");
     }
+    if (y_rows_major) return fail(EXL3_ERR_BAD_SHAPE, "linear: the row-major grouped output serves up to %d rows", kRowsMax);
     GemmArgs g{};
     g.x = x;
     g.x_dtype = x_dtype;
@@ -847,6 +852,21 @@ int32_t tiled_checks(const exl3_tiled_t *b, const exl3_decode_t &dec, const char
     return ok();
 }
 
+// A uniform bank's operands and rates, each rate's codebook row present; fam / k: the decode at the gate's rate.
+int32_t moe_bank_checks(const exl3_bank_t *bank, int32_t experts, const exl3_decode_t &dec, int n[3], int *fam,
+                        DecodeK *k) {
+    if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe: no bank");
+    const exl3_proj_t *pr[3] = {&bank->gate, &bank->up, &bank->down};
+    for (int i = 0; i < 3; i++) {
+        if (!rate_admitted(pr[i]->n) || !pr[i]->trellis || !pr[i]->suh || !pr[i]->svh)
+            return fail(EXL3_ERR_BAD_SHAPE, "moe: projection %d has n=%d or a null operand", i, pr[i]->n);
+        n[i] = pr[i]->n;
+        int32_t rc = resolve_decode(dec, n[i], fam, k);  // every projection's rate must have its codebook row
+        if (rc) return rc;
+    }
+    return resolve_decode(dec, n[0], fam, k);
+}
+
 // `moe` / `moeWithShared` / `moeWithGatedShared` over a uniform bank: every check, then the launches.
 int32_t moe_uniform(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t experts,
                     const exl3_bank_t *bank, const uint32_t *inds, const void *scores, int32_t scores_dtype,
@@ -855,19 +875,10 @@ int32_t moe_uniform(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden
                     hipStream_t stream) {
     int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, clamp_limit, scores_dtype);
     if (rc) return rc;
-    if (!bank || experts <= 0) return fail(EXL3_ERR_BAD_SHAPE, "moe: no bank");
-    const exl3_proj_t *pr[3] = {&bank->gate, &bank->up, &bank->down};
     int n[3];
     int fam;
     DecodeK k;
-    for (int i = 0; i < 3; i++) {
-        if (!rate_admitted(pr[i]->n) || !pr[i]->trellis || !pr[i]->suh || !pr[i]->svh)
-            return fail(EXL3_ERR_BAD_SHAPE, "moe: projection %d has n=%d or a null operand", i, pr[i]->n);
-        n[i] = pr[i]->n;
-        rc = resolve_decode(dec, n[i], &fam, &k);  // every projection's rate must have its codebook row
-        if (rc) return rc;
-    }
-    rc = resolve_decode(dec, n[0], &fam, &k);
+    rc = moe_bank_checks(bank, experts, dec, n, &fam, &k);
     if (rc) return rc;
     if (rows == 0) return ok();
     if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe: null operand");
@@ -973,6 +984,50 @@ int32_t exl3_linear_noalloc(const void *x, int32_t x_dtype, int32_t rows, int32_
                        kNoallocScratchBytes, stream, split_ok);
 }
 
+size_t exl3_linear_pair_workspace_size(int32_t groups, int32_t rows, int32_t in_features, int32_t mid_features,
+                                       int32_t out_features) {
+    if (groups <= 0 || rows <= 0 || rows > kRowsMax || in_features <= 0 || mid_features <= 0 || out_features <= 0 ||
+        in_features % 128 || mid_features % 128 || out_features % 128)
+        return 0;
+    // the two launches share the zeroed region and the split partials (one after the other on the stream); the
+    // intermediate [rows][groups * mid] (at most 4 bytes an element) follows
+    const size_t scratch = std::max(linear_ws(groups, rows, in_features, mid_features, 64),
+                                    linear_ws(1, rows, groups * mid_features, out_features, 64));
+    return align_up(scratch) + align_up((size_t)rows * groups * mid_features * 4);
+}
+
+int32_t exl3_linear_pair(const void *x, int32_t x_dtype, int32_t groups, int32_t rows, int32_t in_features,
+                         int32_t mid_features, int32_t out_features, const uint16_t *a_trellis, int32_t a_n,
+                         const uint16_t *a_suh, const uint16_t *a_svh, exl3_decode_t a_dec,
+                         const uint16_t *b_trellis, int32_t b_n, const uint16_t *b_suh, const uint16_t *b_svh,
+                         exl3_decode_t b_dec, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+    int fam;
+    DecodeK k;
+    int32_t rc = linear_checks(x, x_dtype, groups, rows, in_features, mid_features, a_trellis, a_n, a_suh, a_svh,
+                               a_dec, y, x_dtype, &fam, &k);
+    if (rc) return rc;
+    if (groups > 0 && mid_features > 0 && (long)groups * mid_features > (1L << 30))
+        return fail(EXL3_ERR_BAD_SHAPE, "linear_pair: groups x mid too large");
+    rc = linear_checks(x, x_dtype, 1, rows, groups * mid_features, out_features, b_trellis, b_n, b_suh, b_svh, b_dec, y,
+                       y_dtype, &fam, &k);
+    if (rc || rows == 0) return rc;
+    if (rows > kRowsMax)
+        return declined("linear_pair: declined (rows=%d past one decode launch of %d): run exl3_linear_grouped, "
+                        "transpose, then exl3_linear", rows, kRowsMax);
+    const size_t need = exl3_linear_pair_workspace_size(groups, rows, in_features, mid_features, out_features);
+    if (workspace_bytes < need || !workspace || (reinterpret_cast<uintptr_t>(workspace) % kAlign))
+        return fail(EXL3_ERR_WORKSPACE, "linear_pair: workspace of %zu bytes (256-aligned) needed, got %zu", need,
+                    workspace_bytes);
+    const size_t scratch = need - align_up((size_t)rows * groups * mid_features * 4);
+    void *mid = static_cast<char *>(workspace) + scratch;
+    rc = linear_impl(x, x_dtype, groups, rows, in_features, mid_features, a_trellis, a_n, a_suh, a_svh, a_dec, mid,
+                     x_dtype, workspace, scratch, stream, true, /*y_rows_major=*/true);
+    if (rc) return rc;
+    return linear_impl(mid, x_dtype, 1, rows, groups * mid_features, out_features, b_trellis, b_n, b_suh, b_svh, b_dec,
+                       y, y_dtype, workspace, scratch, stream);
+}
+
 int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
     if (!workspace || workspace_bytes == 0) return ok();
     if (reinterpret_cast<uintptr_t>(workspace) % 4) return fail(EXL3_ERR_WORKSPACE, "workspace_init: misaligned");
@@ -1035,6 +1090,68 @@ int32_t exl3_moe_ragged(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
                       bank->svh, n0, bank->meta, bank->lane_rates_only != 0, inds, scores, scores_dtype, topk,
                       verify_rows != 0, clamp_limit, shared, shared_gate, y, y_dtype, workspace, workspace_bytes,
                       stream);
+}
+
+size_t exl3_moe_groups_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {
+    const size_t routed = exl3_moe_workspace_size(rows, topk, hidden, inter);
+    if (routed == 0) return 0;
+    const size_t nslots = (size_t)rows * topk, plane = align_up((size_t)rows * hidden * sizeof(float));
+    return align_up(routed) + 2 * align_up(nslots * 4) + 2 * plane;
+}
+
+int32_t exl3_moe_groups(const void *x, int32_t x_dtype, int32_t rows, int32_t hidden, int32_t inter, int32_t groups,
+                        const exl3_bank_t *banks, const int32_t *group_experts, const uint32_t *inds,
+                        const void *scores, int32_t scores_dtype, int32_t topk, exl3_decode_t dec,
+                        int32_t verify_rows, void *y, int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+    if (groups <= 0 || !banks || !group_experts)
+        return fail(EXL3_ERR_GROUP_MISSING, "moe_groups: no group banks");
+    int32_t rc = moe_common_checks(x_dtype, y_dtype, rows, hidden, inter, topk, 0, scores_dtype);
+    if (rc) return rc;
+    long total = 0;
+    for (int g = 0; g < groups; g++) {  // every group's bank, before any launch
+        int n[3], fam;
+        DecodeK k;
+        rc = moe_bank_checks(&banks[g], group_experts[g], dec, n, &fam, &k);
+        if (rc) return rc;
+        total += group_experts[g];
+    }
+    if (total > 0xFFFFFFFFL) return fail(EXL3_ERR_BAD_SHAPE, "moe_groups: too many experts");
+    if (groups == 1)  // one bank: `moe` itself, rounded to y's dtype directly (root.zig:648)
+        return moe_uniform(x, x_dtype, rows, hidden, inter, group_experts[0], &banks[0], inds, scores, scores_dtype,
+                           topk, dec, verify_rows != 0, 0, nullptr, nullptr, y, y_dtype, workspace, workspace_bytes,
+                           stream);
+    if (rows == 0) return ok();
+    if (!x || !inds || !scores || !y) return fail(EXL3_ERR_BAD_SHAPE, "moe_groups: null operand");
+    const size_t need = exl3_moe_groups_workspace_size(rows, topk, hidden, inter);
+    if (workspace_bytes < need || !workspace || (reinterpret_cast<uintptr_t>(workspace) % kAlign))
+        return fail(EXL3_ERR_WORKSPACE, "moe_groups: workspace of %zu bytes (256-aligned) needed, got %zu", need,
+                    workspace_bytes);
+    const int nslots = rows * topk;
+    const size_t routed = align_up(exl3_moe_workspace_size(rows, topk, hidden, inter));
+    char *w = static_cast<char *>(workspace) + routed;
+    uint32_t *local = reinterpret_cast<uint32_t *>(w);
+    float *weight = reinterpret_cast<float *>(w + align_up((size_t)nslots * 4));
+    float *acc = reinterpret_cast<float *>(w + 2 * align_up((size_t)nslots * 4));
+    float *part = acc + align_up((size_t)rows * hidden * sizeof(float)) / sizeof(float);
+    const size_t outs = (size_t)rows * hidden;
+    uint32_t lo = 0;
+    for (int g = 0; g < groups; g++) {
+        // the group's partial in f32: slots outside it go to local expert 0 with score 0 (root.zig:662-678)
+        hipError_t e = run_moe_group_routing(inds, scores, scores_dtype, nslots, lo, (uint32_t)group_experts[g],
+                                             local, weight, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe_groups (routing)");
+        rc = moe_uniform(x, x_dtype, rows, hidden, inter, group_experts[g], &banks[g], local, weight, EXL3_DT_F32,
+                         topk, dec, verify_rows != 0, 0, nullptr, nullptr, g == 0 ? acc : part, EXL3_DT_F32,
+                         workspace, routed, stream);
+        if (rc) return rc;
+        if (g > 0) {
+            e = run_add_f32(acc, part, outs, stream);  // the f32 sum in group order (root.zig:680-694)
+            if (e != hipSuccess) return launched(e, "exl3_moe_groups (sum)");
+        }
+        lo += (uint32_t)group_experts[g];
+    }
+    return launched(run_cast_f32(acc, y, y_dtype, outs, stream), "exl3_moe_groups (cast)");  // one cast (:695-701)
 }
 
 size_t exl3_moe_with_shared_bank_workspace_size(int32_t rows, int32_t topk, int32_t hidden, int32_t inter) {

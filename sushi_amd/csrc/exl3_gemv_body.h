@@ -101,7 +101,8 @@ struct GemvCtx {
 __device__ __forceinline__ void finish_block(const GemvArgs &a, const GemvCtx &c, int rho, float v0, float v1,
                                              int lane) {
     fwht128_wave(v0, v1, lane);
-    const size_t yo = ((size_t)c.g * a.rows + rho) * a.out + (size_t)c.og * 128;
+    const size_t yrow = a.y_rows_major ? (size_t)rho * a.groups + c.g : (size_t)c.g * a.rows + rho;
+    const size_t yo = yrow * a.out + (size_t)c.og * 128;
     store_y(a.y, a.y_dtype, yo + lane, v0 * HAD_SCALE * c.sv0);
     store_y(a.y, a.y_dtype, yo + lane + 64, v1 * HAD_SCALE * c.sv1);
 }
@@ -422,7 +423,7 @@ __device__ __forceinline__ void fold_finish(const GemvArgs &a, const GemvCtx &c,
                 sc = load_any(a.fold_scores, a.score_dtype, slot);
             }
         } else {
-            yrow = (size_t)c.g * a.rows + r;
+            yrow = a.y_rows_major ? (size_t)r * a.groups + c.g : (size_t)c.g * a.rows + r;
         }
         const int arrivals = shared ? c.S : a.fold_arrivals;
         const float f0 = (v0 * HAD_SCALE * c.sv0) * sc, f1 = (v1 * HAD_SCALE * c.sv1) * sc;

@@ -103,6 +103,7 @@ struct GemvArgs {
     unsigned long long *fold_comb;
     void *y;
     int y_dtype;
+    int y_rows_major;  // dense: group g's row r is output row r * groups + g ([rows][groups * out]), else g * rows + r
     int splits;
     int groups;
     int nproj;
@@ -180,6 +181,14 @@ struct ReduceArgs {
     float out_scale;
 };
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s);
+
+// moeGroups (src/exl3/root.zig:646-703): one group's routing -- slots of experts [lo, lo + count) as local ids with
+// their scores, every other slot as local expert 0 with score 0 (f32) -- and the f32 group sums: acc += part, then
+// y = T(acc).
+hipError_t run_moe_group_routing(const uint32_t *inds, const void *scores, int score_dtype, int nslots, uint32_t lo,
+                                 uint32_t count, uint32_t *local, float *weight, hipStream_t s);
+hipError_t run_add_f32(float *acc, const float *part, size_t n, hipStream_t s);
+hipError_t run_cast_f32(const float *src, void *y, int y_dtype, size_t n, hipStream_t s);
 
 // Groups the slots of a routing by expert into windows of up to MOE_WINDOW_ROWS rows, slots in ascending order
 // within an expert (a stable counting sort): one workgroup; slots <= kMoeWindowMaxSlots, experts <= kMoeWindowMaxExperts.

@@ -503,4 +503,54 @@ hipError_t run_fill_zero(void *p, size_t bytes, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---- moeGroups (src/exl3/root.zig:646-703): each group's routing and the f32 sum of the group outputs
+
+// Slot s of expert e in [lo, lo + count): local id e - lo with its score; any other slot: local id 0, score 0 (the
+// reference's where(mask, inds - lo, 0) and where(mask, scores, 0)).  Scores widen exactly to f32.
+__global__ void moe_group_routing_kernel(const uint32_t *__restrict__ inds, const void *__restrict__ scores, int dt,
+                                         int nslots, uint32_t lo, uint32_t count, uint32_t *__restrict__ local,
+                                         float *__restrict__ weight) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nslots) return;
+    const uint32_t e = inds[s];
+    const bool in = e >= lo && e - lo < count;
+    local[s] = in ? e - lo : 0u;
+    weight[s] = in ? load_any(scores, dt, (size_t)s) : 0.0f;
+}
+
+hipError_t run_moe_group_routing(const uint32_t *inds, const void *scores, int score_dtype, int nslots, uint32_t lo,
+                                 uint32_t count, uint32_t *local, float *weight, hipStream_t s) {
+    if (nslots <= 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_group_routing_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, s, inds, scores,
+                       score_dtype, nslots, lo, count, local, weight);
+    return hipGetLastError();
+}
+
+__global__ void add_f32_kernel(float *__restrict__ acc, const float *__restrict__ part, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        acc[i] += part[i];
+}
+
+__global__ void cast_f32_kernel(const float *__restrict__ src, void *__restrict__ y, int dt, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        store_out(y, dt, i, src[i]);
+}
+
+static unsigned elementwise_blocks(size_t n) {
+    const size_t b = (n + 255) / 256;
+    return (unsigned)(b > 4096 ? 4096 : b);
+}
+
+hipError_t run_add_f32(float *acc, const float *part, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(add_f32_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, s, acc, part, n);
+    return hipGetLastError();
+}
+
+hipError_t run_cast_f32(const float *src, void *y, int y_dtype, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(cast_f32_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, s, src, y, y_dtype, n);
+    return hipGetLastError();
+}
+
 }  // namespace exl3

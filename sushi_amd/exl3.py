@@ -92,6 +92,10 @@ class HessianNotPositiveDefinite(Exl3Error):
     status = -15
 
 
+class Exl3GroupMissing(Exl3Error):
+    status = -16
+
+
 _BY_STATUS = {c.status: c for c in Exl3Error.__subclasses__()}
 
 
@@ -609,6 +613,37 @@ def linear_grouped(x: torch.Tensor, p: Proj, dec: Decode) -> torch.Tensor:
     return y
 
 
+def linear_pair(x: torch.Tensor, a: Proj, b: Proj, dec_a: Decode, dec_b: Decode) -> Optional[torch.Tensor]:
+    """`linear.linearPair` (linear.zig:60-95): x [G, rows, in] through the G-bank `a`, then that result as
+    [rows, G * mid] through the one-bank `b` -> [rows, out] in x's dtype; linear_grouped, the transpose and linear, bit
+    for bit, in two launches.  None, with nothing launched, past one decode launch's rows (the reference's null)."""
+    if x.dim() != 3 or a.trellis.dim() != 4 or b.trellis.dim() != 4 or a.trellis.shape[0] != x.shape[0] or \
+            b.trellis.shape[0] != 1 or a.in_features != x.shape[2] or b.in_features != x.shape[0] * a.out_features:
+        raise BadExl3Shape(f"linear_pair: x {tuple(x.shape)}, a {tuple(a.trellis.shape)}, b {tuple(b.trellis.shape)}")
+    dec_a.require_table()
+    dec_b.require_table()
+    for p in (a, b):
+        _need_gpu(p.trellis, p.suh, p.svh)
+        _u16_check(p.trellis, "trellis")
+        _f16_check(p.suh, "suh")
+        _f16_check(p.svh, "svh")
+    _need_gpu(x)
+    x = x.contiguous()
+    groups, rows, in_f = int(x.shape[0]), int(x.shape[1]), int(x.shape[2])
+    mid, out_f = a.out_features, b.out_features
+    y = torch.empty(rows, out_f, dtype=x.dtype, device=x.device)
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_linear_pair_workspace_size(groups, rows, in_f, mid, out_f))
+    rc = L.exl3_linear_pair(x.data_ptr(), _dt(x, "x"), groups, rows, in_f, mid, out_f, a.trellis.data_ptr(), a.n,
+                            a.suh.data_ptr(), a.svh.data_ptr(), dec_a.c(), b.trellis.data_ptr(), b.n, b.suh.data_ptr(),
+                            b.svh.data_ptr(), dec_b.c(), y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(),
+                            _stream(x.device))
+    if rc == EXL3_DECLINED:
+        return None
+    _check(rc)
+    return y
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # Routed experts
 
@@ -752,6 +787,30 @@ def moe_ragged(x, rb: Ragged, inds, scores, dec: Decode, verify_rows: bool = Fal
 
 
 EXL3_DECLINED = 1
+
+
+def moe_groups(x, banks: Sequence[Bank], inds, scores, dec: Decode, verify_rows: bool = False) -> torch.Tensor:
+    """`moeGroups` (root.zig:646-703): experts split over several uniform banks (router ids counted across them in
+    order); each group's output in f32, summed in group order, rounded to x's dtype once."""
+    if len(banks) == 0:
+        raise Exl3GroupMissing("moe_groups: no banks")
+    dec.require_table()
+    x2, inds2, sc2, rows, topk = _moe_prep(x, inds, scores)
+    hidden = int(x.shape[-1])
+    shapes = [_bank_shape(b, hidden) for b in banks]
+    inter = shapes[0][1]
+    if any(i != inter for _, i in shapes):
+        raise BadExl3Shape("moe_groups: every bank must share the intermediate width")
+    _need_gpu(x2, inds2, sc2)
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    L = _lib.load()
+    ws = workspace.get(x.device, L.exl3_moe_groups_workspace_size(rows, topk, hidden, inter))
+    cbanks = (_lib.BankT * len(banks))(*[_lib.BankT(b.gate.c(), b.up.c(), b.down.c()) for b in banks])
+    counts = (ctypes.c_int32 * len(banks))(*[e for e, _ in shapes])
+    _check(L.exl3_moe_groups(x2.data_ptr(), _dt(x2, "x"), rows, hidden, inter, len(banks), cbanks, counts,
+                             inds2.data_ptr(), sc2.data_ptr(), _dt(sc2, "scores"), topk, dec.c(), int(verify_rows),
+                             y.data_ptr(), _dt(y, "y"), ws.data_ptr(), ws.numel(), _stream(x.device)))
+    return y.reshape(x.shape)
 
 
 _ONE_EXPERT: dict = {}

@@ -79,6 +79,28 @@ def test_moe_refusals():
     assert lib.exl3_route_topk(None, 1, 2000, 8, None, None, None) == -1
 
 
+def test_moe_groups_and_linear_pair_refusals():
+    """moeGroups without banks is Exl3GroupMissing (root.zig:647); a bad group bank is refused before any launch;
+    linearPair past one decode launch's rows declines (status 1, the reference's null) before any launch (the fake
+    pointers are never dereferenced)."""
+    lib = L.load()
+    d = L.DecodeT(1, 16, -1)
+    counts = (ctypes.c_int32 * 2)(4, 4)
+    banks = (L.BankT * 2)()
+    assert lib.exl3_moe_groups(None, 0, 1, 128, 128, 0, banks, counts, None, None, 0, 8, d, 0, None, 0, None, 0,
+                               None) == -16
+    assert lib.exl3_moe_groups(None, 0, 1, 128, 128, 2, banks, counts, None, None, 0, 8, d, 0, None, 0, None, 0,
+                               None) == -1  # the banks' projections are missing
+    fake = 0x1000
+    assert lib.exl3_linear_pair(fake, 0, 2, 17, 128, 128, 256, fake, 32, fake, fake, d, fake, 32, fake, fake, d, fake,
+                                0, None, 0, None) == 1
+    assert "declined" in L.last_error()
+    assert lib.exl3_linear_pair(fake, 0, 2, 4, 128, 100, 256, fake, 32, fake, fake, d, fake, 32, fake, fake, d, fake,
+                                0, None, 0, None) == -1  # mid not a multiple of 128
+    assert lib.exl3_linear_pair_workspace_size(2, 4, 128, 128, 256) > 0
+    assert lib.exl3_linear_pair_workspace_size(2, 17, 128, 128, 256) == 0
+
+
 def test_tiled_refusals():
     """Per-tile-rate banks: only the K1 / K2 pair, tables that hold both rates, the hash-product families, a 4-byte
     aligned mask table; every refusal before any launch (the fake pointers are never dereferenced)."""

@@ -134,3 +134,97 @@ def test_moe_ragged_gate_needs_its_shared_expert(dev):
     with pytest.raises(exl3.BadExl3Shape):
         exl3.moe_ragged(x, rb, torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev),
                         exl3.MCG, False, None, g)
+
+
+# ---- linearPair (src/exl3/linear.zig:60-95) and moeGroups (src/exl3/root.zig:646-703) ----------------------------
+
+
+def _proj(seed, name, groups, in_f, out_f, n, dev):
+    p = synth.proj(seed, name, groups, in_f, out_f, n, norm=True)
+    return p, exl3.Proj(p.trellis.to(dev), p.suh.to(dev), p.svh.to(dev))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("groups,rows", [(2, 1), (4, 3), (3, 16)])
+def test_linear_pair_is_grouped_then_linear(dev, groups, rows, dtype):
+    """x [G, rows, in] through the G-bank a, read as [rows, G * mid] by the one-bank b: bit-equal to linear_grouped,
+    the transpose and linear; and against the oracle's projections (the intermediate rounded to x's dtype) at the
+    north-star bar."""
+    print(f"[linear pair] G={groups} rows={rows} {dtype}", flush=True)
+    in_f, mid, out_f = 256, 384, 512
+    pa, a = _proj(84, f"lpa{groups}", groups, in_f, mid, 48, dev)
+    pb, b = _proj(85, f"lpb{groups}", 1, groups * mid, out_f, 32, dev)
+    dec_a, dec_b = exl3.MCG, exl3.INST3
+    x = synth.normal(84, f"lpx{groups}.{rows}", (groups, rows, in_f)).to(dtype).to(dev)
+    y = exl3.linear_pair(x, a, b, dec_a, dec_b)
+    mid_t = exl3.linear_grouped(x, a, dec_a).transpose(0, 1).reshape(rows, groups * mid).contiguous()
+    ref = exl3.linear(mid_t, b, dec_b)
+    torch.cuda.synchronize()
+    assert y is not None and y.dtype == dtype and torch.equal(y, ref)
+    xa = x.float().cpu().numpy()
+    hs = []
+    for g in range(groups):
+        t, su, sv = _np(pa)
+        hs.append(O.project_rows(xa[g], t[g], su[g], sv[g], in_f, mid, 48, O.decode(O.CB_MCG), threads=8))
+    h = torch.from_numpy(np.concatenate(hs, axis=1)).to(dtype).float().numpy()
+    t, su, sv = _np(pb)
+    want = O.project_rows(h, t[0], su[0], sv[0], groups * mid, out_f, 32, O.decode(O.CB_3INST), threads=8)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR + (2 ** -8 if dtype == torch.bfloat16 else 0.0)
+
+
+def test_linear_pair_declines_past_one_decode_launch(dev):
+    in_f, mid, out_f, groups, rows = 256, 128, 256, 2, 17
+    _, a = _proj(86, "lpd.a", groups, in_f, mid, 32, dev)
+    _, b = _proj(86, "lpd.b", 1, groups * mid, out_f, 32, dev)
+    x = synth.normal(86, "lpd.x", (groups, rows, in_f)).to(dev)
+    assert exl3.linear_pair(x, a, b, exl3.MCG, exl3.MCG) is None
+
+
+def _group_banks(dev, seed, groups, hidden, inter):
+    banks = [synth.bank(seed + g, f"mg{seed}.{g}", e, hidden, inter, n, norm=True) for g, (e, n) in enumerate(groups)]
+    return banks, [_to(b, dev) for b in banks]
+
+
+@pytest.mark.parametrize("rows", [1, 5, 24])
+@pytest.mark.parametrize("ydt", [torch.float16, torch.float32])
+def test_moe_groups_against_oracle(dev, rows, ydt):
+    """Three uniform banks (3, 5 and 8 experts at K2, K3, K4): each group's partial in f32 over every slot (slots of
+    other groups as local expert 0 with score 0), summed in group order and rounded once -- the oracle does the same
+    with moeSwigluHost per group."""
+    print(f"[moe groups] rows={rows} {ydt}", flush=True)
+    hidden, inter, k = 256, 256, 4
+    groups = [(3, 32), (5, 48), (8, 64)]
+    banks, bds = _group_banks(dev, 87, groups, hidden, inter)
+    E = sum(e for e, _ in groups)
+    x = synth.normal(87, f"x{rows}", (rows, hidden)).to(ydt)
+    inds, scores = _route(87 + rows, rows, E, k)
+    y = exl3.moe_groups(x.to(dev), bds, torch.from_numpy(inds.view(np.int32)).to(dev),
+                        torch.from_numpy(scores).to(dev), exl3.MCG)
+    total = np.zeros((rows, hidden), np.float32)
+    lo = 0
+    for b, (e, n) in zip(banks, groups):
+        inside = (inds >= lo) & (inds < lo + e)
+        local = np.where(inside, inds - lo, 0).astype(np.uint32)
+        w = np.where(inside, scores, 0.0).astype(np.float32)
+        total += O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), local, w, hidden, inter,
+                                   (n, n, n), O.decode(O.CB_MCG), threads=8)
+        lo += e
+    want = torch.from_numpy(total).to(ydt).float().numpy()
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
+def test_moe_groups_of_one_bank_is_moe_and_verify_rows_hold(dev):
+    """One bank is `moe` itself (root.zig:648), bit for bit; and verify rows at a GEMM-arm width equal the decode
+    chain bit for bit through the group path as well."""
+    hidden, inter, k, rows = 256, 256, 8, 64
+    banks, bds = _group_banks(dev, 88, [(8, 32)], hidden, inter)
+    x = synth.normal(88, "x", (rows, hidden)).to(dev)
+    inds, scores = _route(88, rows, 8, k)
+    xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
+    assert torch.equal(exl3.moe_groups(x, bds, xi, sc, exl3.MCG), exl3.moe(x, bds[0], xi, sc, exl3.MCG))
+    banks2, bds2 = _group_banks(dev, 89, [(3, 32), (5, 32)], hidden, inter)
+    yv = exl3.moe_groups(x, bds2, xi, sc, exl3.MCG, verify_rows=True)
+    with exl3.arm_overrides(moe_gemm=0):
+        yc = exl3.moe_groups(x, bds2, xi, sc, exl3.MCG)
+    torch.cuda.synchronize()
+    assert torch.equal(yv, yc)
