@@ -154,7 +154,10 @@ typedef enum {
     EXL3_KNOB_MOE_GEMM = 8,             /* 1: a routed layer takes the GEMM arm where it can, 0: never */
     EXL3_KNOB_GEMM_ARM = 9,             /* dense GEMM body: 4 = decode-wave tile, 5 / 6 = ping-pong 512 / 256 rows,
                                            7 = ping-pong 512 rows with k in two halves */
-    EXL3_KNOB_COUNT = 10
+    EXL3_KNOB_MOE_CHAIN = 10,           /* per-slot decode chain: 1 = gate/up and down in one launch where it
+                                           serves, 0 = two launches (default: one launch for 2..8 rows with a fused
+                                           shared bank) */
+    EXL3_KNOB_COUNT = 11
 } exl3_knob;
 int32_t exl3_set_override(int32_t knob, int32_t value, int32_t enable);
 

@@ -635,10 +635,9 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
             a.sh_svh[i] = sb->sv[i];
         }
     }
-    hipError_t e = run_gemv(fam, PRO_X, a, stream);
-    if (e != hipSuccess) return launched(e, "exl3_moe (gate/up)");
+    GemvArgs u{};  // gate and up at different rates: up's own launch
     if (split_pair) {
-        GemvArgs u = a;
+        u = a;
         u.trellis[0] = tr[1];
         u.suh[0] = su[1];
         u.svh[0] = sv[1];
@@ -646,8 +645,6 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         u.n = n[1];
         int fam_u;
         if (resolve_decode(dec, n[1], &fam_u, &u.k)) return EXL3_ERR_RATE_MISSING;
-        e = run_gemv(fam, PRO_X, u, stream);
-        if (e != hipSuccess) return launched(e, "exl3_moe (up)");
     }
 
     // 2) SwiGLU mid + down GEMV of every slot (DOWN_FUSED_SOURCE): f32 planes [slot][split][hidden]
@@ -727,6 +724,36 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         d.fold_shared = nullptr;
         d.fold_gate = nullptr;
     }
+    // The per-slot arm's gate/up and down as ONE launch (run_moe_chain): the down workgroups' tile loads go out while
+    // gate/up runs and the second launch's start-up is gone, but each group's planes then cross XCDs through memory
+    // (written through, a counter, L2-bypassing loads), which costs about what the kernel boundary did.  Taken where
+    // it measured faster: 2 to 8 rows with a fused shared bank (C4's layer: 2 rows 26.9 -> 25.6 us, 4 rows 40.8 ->
+    // 38.2, 8 rows 61.6 -> 59.1); one row (17.2 -> 19.4 us) and routed-only layers keep two launches.  It needs one
+    // rate for the bank, the down folding into y and the counters clear of the fold words in use.
+    // EXL3_KNOB_MOE_CHAIN pins it (1) or rules it out (0).
+    const int groups_total = groups;
+    const int chain_knob = knob(EXL3_KNOB_MOE_CHAIN, -1);
+    const bool chain_wanted = chain_knob > 0 || (chain_knob < 0 && sb && rows >= 2);
+    const bool chain = chain_wanted && !p.windowed && fold && !split_pair && !meta && !tt && n[0] == n[2] &&
+                       lane_rate(n[0]) &&
+                       (size_t)3 * rows * hidden <= kFoldWords - CHAIN_CTR_BYTES / sizeof(unsigned long long) &&
+                       (size_t)2 * groups_total * COUNTER_STRIDE * sizeof(uint32_t) <= CHAIN_CTR_BYTES;
+    hipError_t e;
+    if (chain) {
+        uint32_t *ctr = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + kZeroBytes - CHAIN_CTR_BYTES);
+        a.chain_ctr = d.chain_ctr = ctr;
+        a.chain_need = d.chain_need = (inter / 128) * p.s1 * 2;  // the group's gate/up workgroups
+        a.chain_need2 = d.chain_need2 = (hidden / 128) * p.s2;   // its down workgroups
+        e = run_moe_chain(fam, a, d, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (chain)");
+        return ok();
+    }
+    e = run_gemv(fam, PRO_X, a, stream);
+    if (e != hipSuccess) return launched(e, "exl3_moe (gate/up)");
+    if (split_pair) {
+        e = run_gemv(fam, PRO_X, u, stream);
+        if (e != hipSuccess) return launched(e, "exl3_moe (up)");
+    }
     e = run_gemv(fam, PRO_MID, d, stream);
     if (e != hipSuccess) return launched(e, "exl3_moe (down)");
     if (fold) return ok();
@@ -748,7 +775,8 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
     r.y = y;
     r.y_dtype = y_dtype;
     r.out_scale = 1.0f;
-    return launched(run_moe_reduce(r, stream), "exl3_moe (reduce)");
+    e = run_moe_reduce(r, stream);
+    return launched(e, "exl3_moe (reduce)");
 }
 
 // ---- Static scratch for exl3_linear_noalloc ------------------------------------------------------------------

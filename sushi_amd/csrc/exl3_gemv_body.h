@@ -86,6 +86,7 @@ __device__ __forceinline__ float y_from_bits16(int dt, uint32_t b) {
 
 struct GemvCtx {
     int g, proj, bank, og, sp, S, KS, kt0, IT, OT, G, x_dtype;
+    int gy;                     // the group's index in the grid (shared groups first): the fused chain's counters
     uint32_t x_div_m;           // slots per x row, as a div_magic constant
     int rows;                   // rows of this group (a window's own count in the sorted MoE arm)
     int xg;                     // x row of the group's row 0 (per-slot and dense arms, a shared expert's rows)
@@ -252,7 +253,10 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs &a, const GemvCtx 
 
 // Sums the gate and up planes of one 128-block over the previous launch's k splits, issuing a chunk of loads before
 // any add (a loop that adds as it loads would wait out one memory round trip per split).
+// BYPASS (the fused chain): the planes were written through to memory by workgroups that may sit on other XCDs in
+// the same launch, so they are read with system-scope loads, past this XCD's L2 (which may hold an earlier call's).
 constexpr int MID_CHUNK = 8;
+template <bool BYPASS = false>
 __device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, int lane, float (&w)[2][2]) {
     w[0][0] = w[0][1] = w[1][0] = w[1][1] = 0.f;
     for (int s0 = 0; s0 < a.mid_splits; s0 += MID_CHUNK) {
@@ -263,8 +267,13 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, 
             for (int q = 0; q < MID_CHUNK; q++) {
                 const int s2 = min(s0 + q, a.mid_splits - 1);
                 const float *pp = a.mid_part[pj] + ((size_t)slot * a.mid_splits + s2) * a.in + kb;
-                t[pj][0][q] = pp[lane];
-                t[pj][1][q] = pp[lane + 64];
+                if constexpr (BYPASS) {
+                    t[pj][0][q] = __hip_atomic_load(pp + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    t[pj][1][q] = __hip_atomic_load(pp + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                } else {
+                    t[pj][0][q] = pp[lane];
+                    t[pj][1][q] = pp[lane + 64];
+                }
             }
         }
 #pragma unroll
@@ -279,7 +288,7 @@ __device__ __forceinline__ void mid_planes(const GemvArgs &a, int slot, int kb, 
     }
 }
 
-template <int PRO, int RT, bool WIN, bool SH>
+template <int PRO, int RT, bool WIN, bool SH, int CH = 0>
 __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, uint16_t (*xs)[XS_PITCH], int wave,
                                          int lane, const PrologueRegs<RT, WIN> &pr) {
     const int nblk = c.KS >> 3;
@@ -311,7 +320,7 @@ __device__ __forceinline__ void prologue(const GemvArgs &a, const GemvCtx &c, ui
                 }
                 const float su0 = h2f(c.suh[si + lane]), su1 = h2f(c.suh[si + lane + 64]);
                 float w[2][2];
-                mid_planes(a, slot_of<WIN>(c, rho), kb, lane, w);
+                mid_planes<CH == 2>(a, slot_of<WIN>(c, rho), kb, lane, w);
                 float gv[2], uv[2];
 #pragma unroll
                 for (int pj = 0; pj < 2; pj++) {
@@ -509,7 +518,24 @@ struct TiledSrc {
 // Everything a workgroup does once its rate is known: loads, prologue, decode + dot, reduction, finish.
 // N == N_TILED: each tile at its own rate (ts), tb the projection's whole trellis.
 // PIN: a uniform-rate launch's body (see fetch_svh).
-template <int FAM, int N, int RT, int PRO, bool WIN, bool SH, bool PIN = false>
+// The fused chain's down workgroup: wave 0 waits until its group's gate/up workgroups have all arrived (their planes
+// written through to memory first), at most CHAIN_SPIN_TICKS, so the wait always ends; a workgroup barrier then
+// releases the other waves (one poller per workgroup keeps the polls off the counters' memory channel).
+__device__ __forceinline__ void chain_wait(const GemvArgs &a, const GemvCtx &c, int wave) {
+    if (wave == 0) {
+        const uint32_t *ctr = a.chain_ctr + (size_t)(2 * c.gy) * COUNTER_STRIDE;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)a.chain_need) {
+            __builtin_amdgcn_s_sleep(8);
+            if (__builtin_amdgcn_s_memrealtime() - t0 > CHAIN_SPIN_TICKS) break;
+        }
+    }
+    __syncthreads();
+}
+
+// CH: the fused chain's role (0 none; 1 gate/up: planes written through, then the group's arrival counted; 2 down:
+// tile loads, then the wait, then the mid from the planes past the L2).
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SH, bool PIN = false, int CH = 0>
 __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const uint16_t *__restrict__ tb,
                                           int n, const DecodeK &k, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128],
                                           const TiledSrc &ts = TiledSrc{}) {
@@ -555,8 +581,22 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
         for (int t = 0; t < TPW; t++) load_slot(t, c.kt0 + wave + GEMV_WAVES * min(t, ntiles - 1));
         __builtin_amdgcn_sched_barrier(0);  // svh's address comes from an argument load: its wait stays behind
         fetch_svh<PIN>(c, lane);
-        prologue<PRO, RT, WIN, SH>(a, c, xs, wave, lane, pr);
+        if constexpr (CH == 2) chain_wait(a, c, wave);
+        prologue<PRO, RT, WIN, SH, CH>(a, c, xs, wave, lane, pr);
         __syncthreads();
+        if constexpr (CH == 2) {
+            // every wave of this workgroup is past its wait: count it; the group's last clears both counters (no
+            // workgroup of the group reads them again in this launch, and the next launch reads them after it)
+            if (wave == 0 && lane == 0) {
+                uint32_t *ctr = a.chain_ctr + (size_t)(2 * c.gy) * COUNTER_STRIDE;
+                const uint32_t old = __hip_atomic_fetch_add(ctr + COUNTER_STRIDE, 1u, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+                if (old == (uint32_t)a.chain_need2 - 1u) {
+                    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(ctr + COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
         const bool masked = k.wmask != 0xFFFFu;
         auto decode_at = [&](int t, int tt) __attribute__((always_inline)) {  // slot t holds the wave's tile tt
             const int kk = wave + GEMV_WAVES * tt;
@@ -654,9 +694,18 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
 #pragma unroll
             for (int w = 0; w < GEMV_WAVES; w++) s += red[w][r][col];
             s *= a.out_scale;
-            if (a.partial_only || xcd_local) dst[col] = s;  // L1 is write-through: the store lands in the XCD's L2
+            if (CH == 0 && (a.partial_only || xcd_local)) dst[col] = s;  // L1 writes through to the XCD's L2
             else __hip_atomic_store(dst + col, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // through to memory
         }
+    }
+    if constexpr (CH == 1) {
+        // the fused chain's gate/up: the stores are acknowledged, then this workgroup's arrival is counted for its
+        // group (the down workgroups wait for all of them)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0)
+            __hip_atomic_fetch_add(a.chain_ctr + (size_t)(2 * c.gy) * COUNTER_STRIDE, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        return;
     }
     if (a.partial_only || !a.fused_finish) return;
 
@@ -699,10 +748,13 @@ __device__ __forceinline__ DecodeK rate_constants(const GemvArgs &a, int n) {
 // One workgroup's work for group g.  SH: g is a fused shared expert's group of token rows (compiled into the
 // per-slot kernels only; the other groups run the SH = false copy, whose set-up is that of a launch without a
 // shared expert).
-template <int FAM, int N, int RT, int PRO, bool WIN, bool SH>
+// L: the workgroup's index within the group's (output group, split) grid; gy: the group's index in the grid (the
+// fused chain's counters); proj: the projection.  CH: the fused chain's role (gemv_body).
+template <int FAM, int N, int RT, int PRO, bool WIN, bool SH, int CH = 0>
 __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t *tr0, const uint16_t *suh0,
                                            const uint32_t *bank_of, const GemvGeo &geo, int rows, int x_dtype,
-                                           const GemvArgs &a, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128]) {
+                                           const GemvArgs &a, uint16_t (*xs)[XS_PITCH], float (*red)[RT][128], int L,
+                                           int gy, int proj) {
     GemvCtx c;
     c.x = x;
     c.x_div_m = geo.xdiv_m;
@@ -711,14 +763,14 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
     c.OT = (int)(geo.tiles >> 16);
     c.G = c.OT >> 3;
     c.S = (int)(geo.sks & 0xFFFFu);
-    const int L = blockIdx.x;
+    c.gy = gy;
     // keep an output group's splits on one XCD when G % 8 == 0 (workgroups go round-robin over the 8 XCDs)
     const bool remap = (c.G & 7) == 0;
     const unsigned q = remap ? (unsigned)L >> 3 : (unsigned)L, qs = div_by_magic(q, geo.s_m);
     c.og = remap ? (int)qs * 8 + (L & 7) : (int)qs;
     c.sp = (int)(q - qs * (unsigned)c.S);
     c.g = g;
-    c.proj = blockIdx.z;
+    c.proj = proj;
     const bool p1 = c.proj != 0;
     const uint16_t *trellis;
     c.part = p1 ? a.partial[1] : a.partial[0];
@@ -767,7 +819,7 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
     if constexpr (N >= 0) {
         const int n = N ? N : a.n;
         const uint16_t *tb = trellis + (size_t)c.bank * c.IT * c.OT * n;
-        gemv_body<FAM, N, RT, PRO, WIN, SH, (N > 0 && !WIN && !SH)>(a, c, tb, n, a.k, xs, red);
+        gemv_body<FAM, N, RT, PRO, WIN, SH, (N > 0 && !WIN && !SH && CH == 0), CH>(a, c, tb, n, a.k, xs, red);
     } else if constexpr (N == N_TILED) {
         // Per-tile-rate bank: every tile at TILED_NA or TILED_NB, read through the projection's segment tables (a
         // fused shared expert keeps its own uniform rate, a lane-reader rate the host checked).
@@ -850,7 +902,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
         // heaviest workgroups, so they start in the first round), then the routed slots.
         if (g < sh_groups) {
             gemv_group<FAM, N, SH_ROWS, PRO, WIN, true>(g, x, tr0, suh0, bank_of, geo, rows, x_dtype, a, xs,
-                                                        reinterpret_cast<float (*)[SH_ROWS][128]>(red));
+                                                        reinterpret_cast<float (*)[SH_ROWS][128]>(red), blockIdx.x,
+                                                        g, blockIdx.z);
             return;
         }
         g -= sh_groups;
@@ -861,13 +914,56 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const void *x, const
         static_assert(RT == SH_ROWS, "a window holds as many rows as a shared group");
         if (g < sh_groups) {
             gemv_group<FAM, N, SH_ROWS, PRO, false, true>(g, x, tr0, suh0, bank_of, geo, rows, x_dtype, a, xs,
-                                                          reinterpret_cast<float (*)[SH_ROWS][128]>(red));
+                                                          reinterpret_cast<float (*)[SH_ROWS][128]>(red), blockIdx.x,
+                                                          g, blockIdx.z);
             return;
         }
         g -= sh_groups;
     }
     gemv_group<FAM, N, RT, PRO, WIN, false>(g, x, tr0, suh0, bank_of, geo, rows, x_dtype, a, xs,
-                                            reinterpret_cast<float (*)[RT][128]>(red));
+                                            reinterpret_cast<float (*)[RT][128]>(red), blockIdx.x, blockIdx.y,
+                                            blockIdx.z);
+}
+
+// The per-slot decode chain in one launch (run_moe_chain): a 1D grid of w1 gate/up workgroups (a1, PRO_X, grid
+// order x = (output group, split), then group, then projection, as gemv_kernel's) and then the down workgroups (a2,
+// PRO_MID).  Workgroups start in index order on each XCD, so when a down workgroup starts every gate/up workgroup
+// before it on that XCD has started, and the ones on other XCDs only wait behind gate/up work: the waits end.  A
+// shared expert's groups (SHP) come first in both halves.
+// One half of the fused chain (CH 1: gate/up with PRO_X, CH 2: down with PRO_MID) for workgroup b of that half.
+template <int FAM, int N, bool SHP, int CH>
+__device__ __forceinline__ void chain_half(const GemvArgs &a, const GemvGeo &geo, int b, uint16_t (*xs)[XS_PITCH],
+                                           float *red) {
+    constexpr int PRO = CH == 1 ? PRO_X : PRO_MID;
+    const int X = (int)(geo.tiles >> 19) * (int)(geo.sks & 0xFFFFu);  // output groups (out / 16 / 8) x splits
+    const int q = b / X;
+    const int gy = q % a.groups, proj = q / a.groups, L = b - q * X;
+    const void *x = CH == 1 ? a.x : nullptr;
+    if (SHP && gy < a.sh_groups) {
+        gemv_group<FAM, N, SH_ROWS, PRO, false, true, CH>(gy, x, a.trellis[0], a.suh[0], a.bank_of, geo, a.rows,
+                                                          a.x_dtype, a, xs,
+                                                          reinterpret_cast<float (*)[SH_ROWS][128]>(red), L, gy, proj);
+        return;
+    }
+    gemv_group<FAM, N, 1, PRO, false, false, CH>(gy - (SHP ? a.sh_groups : 0), x, a.trellis[0], a.suh[0], a.bank_of,
+                                                 geo, a.rows, a.x_dtype, a, xs,
+                                                 reinterpret_cast<float (*)[1][128]>(red), L, gy, proj);
+}
+
+// The per-slot decode chain in one launch (run_moe_chain): a 1D grid of w1 gate/up workgroups (a1, PRO_X, grid
+// order x = (output group, split), then group, then projection, as gemv_kernel's) and then the down workgroups (a2,
+// PRO_MID).  Workgroups start in index order on each XCD, so when a down workgroup starts every gate/up workgroup
+// before it on that XCD has started, and the ones on other XCDs only wait behind gate/up work: the waits end.  A
+// shared expert's groups (SHP) come first in both halves.
+template <int FAM, int N, bool SHP>
+__global__ __launch_bounds__(GEMV_THREADS) void moe_chain_kernel(GemvArgs a1, GemvArgs a2, GemvGeo geo1, GemvGeo geo2,
+                                                                 int w1) {
+    constexpr int RX = SHP ? SH_ROWS : 1;
+    __shared__ __align__(16) uint16_t xs[RX][XS_PITCH];
+    __shared__ float red[GEMV_WAVES * RX * 128];
+    const int b = (int)blockIdx.x;
+    if (b < w1) chain_half<FAM, N, SHP, 1>(a1, geo1, b, xs, red);
+    else chain_half<FAM, N, SHP, 2>(a2, geo2, b - w1, xs, red);
 }
 
 // Separate finish: one wave per (output group, row, group, projection).
@@ -938,6 +1034,45 @@ static hipError_t launch_gemv_n(const GemvArgs &a, hipStream_t s) {
     return e;
 }
 
+template <int FAM, int N>
+static void launch_chain_n(const GemvArgs &a1, const GemvArgs &a2, unsigned w1, unsigned w2, hipStream_t s) {
+    const GemvGeo g1 = gemv_geo(a1), g2 = gemv_geo(a2);
+    if (a1.sh_groups > 0)
+        hipLaunchKernelGGL((moe_chain_kernel<FAM, N, true>), dim3(w1 + w2), dim3(GEMV_THREADS), 0, s, a1, a2, g1, g2,
+                           (int)w1);
+    else
+        hipLaunchKernelGGL((moe_chain_kernel<FAM, N, false>), dim3(w1 + w2), dim3(GEMV_THREADS), 0, s, a1, a2, g1, g2,
+                           (int)w1);
+}
+
+template <int FAM>
+static hipError_t launch_moe_chain(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s) {
+    // the block-to-tile maps' packed fields and divisions (as launch_gemv_n checks them), one row per group, the
+    // same rate and groups in both halves, gate/up writing planes and down folding
+    for (const GemvArgs *a : {&a1, &a2}) {
+        if (a->in / 16 > 0xFFFF || a->out / 16 > 0xFFFF || a->splits < 1 || (a->in / 16) % a->splits ||
+            a->x_div < 1 || a->x_div > 255 || a->rows != 1 || !a->chain_ctr)
+            return hipErrorInvalidValue;
+    }
+    if (a1.n != a2.n || a1.groups != a2.groups || a1.sh_groups != a2.sh_groups || a1.nproj != 2 || a2.nproj != 1 ||
+        !a1.partial_only || !a2.fold || a1.win_count || a2.win_count || a1.meta || a1.seg_off[0])
+        return hipErrorInvalidValue;
+    const unsigned w1 = (unsigned)(a1.out / 128 * a1.splits) * (unsigned)a1.groups * 2u;
+    const unsigned w2 = (unsigned)(a2.out / 128 * a2.splits) * (unsigned)a2.groups;
+    if ((unsigned)a1.chain_need != w1 / (unsigned)a1.groups || (unsigned)a2.chain_need2 != w2 / (unsigned)a2.groups)
+        return hipErrorInvalidValue;
+    switch (a1.n) {
+    case 16: launch_chain_n<FAM, 16>(a1, a2, w1, w2, s); break;
+    case 24: launch_chain_n<FAM, 24>(a1, a2, w1, w2, s); break;
+    case 32: launch_chain_n<FAM, 32>(a1, a2, w1, w2, s); break;
+    case 40: launch_chain_n<FAM, 40>(a1, a2, w1, w2, s); break;
+    case 48: launch_chain_n<FAM, 48>(a1, a2, w1, w2, s); break;
+    case 64: launch_chain_n<FAM, 64>(a1, a2, w1, w2, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int FAM, int PRO>
 static hipError_t launch_gemv_fam(const GemvArgs &a, hipStream_t s) {
     if (a.seg_off[0]) {  // per-tile rates: the hash-product families only (the host refuses the others)
@@ -966,6 +1101,10 @@ static hipError_t launch_gemv_fam(const GemvArgs &a, hipStream_t s) {
 hipError_t EXL3_CAT(run_gemv_fam_, EXL3_GEMV_FAM)(int prologue, const GemvArgs &a, hipStream_t s) {
     return prologue == PRO_MID ? launch_gemv_fam<EXL3_GEMV_FAM, PRO_MID>(a, s)
                                : launch_gemv_fam<EXL3_GEMV_FAM, PRO_X>(a, s);
+}
+
+hipError_t EXL3_CAT(run_moe_chain_fam_, EXL3_GEMV_FAM)(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s) {
+    return launch_moe_chain<EXL3_GEMV_FAM>(a1, a2, s);
 }
 #endif
 

@@ -129,7 +129,21 @@ struct GemvArgs {
     const uint16_t *sh_suh[2];
     const uint16_t *sh_svh[2];
     const uint16_t *sh_mid_svh[2];  // PRO_MID: the shared expert's gate / up svh
+    // The fused decode chain (one launch for gate/up and down, run_moe_chain): group y of the grid (shared groups
+    // first, then the slots) has a pair of counters 128 bytes apart in the zeroed region, chain_ctr[2 y] (arrivals of
+    // its gate/up workgroups, chain_need of them) and chain_ctr[2 y + 1] (down workgroups past their wait,
+    // chain_need2 of them; the last clears both).
+    uint32_t *chain_ctr;
+    int chain_need;
+    int chain_need2;
 };
+
+// The fused chain's counters sit at the top of the zeroed region's overflow half (its low entries serve the fold
+// words in use), CHAIN_CTR_BYTES of them.
+constexpr size_t CHAIN_CTR_BYTES = size_t(128) << 10;
+// A down workgroup waits for its group's gate/up planes at most this many s_memrealtime ticks (100 MHz: 0.2 s), so
+// every wave leaves its wait whatever happens to the workgroups it waits for.
+constexpr uint64_t CHAIN_SPIN_TICKS = 20000000ull;
 
 // The GEMV's block-to-tile map, preloaded as leading kernel arguments: k-tiles and output tiles (in / 16 | out / 16
 // << 16), splits and k-tiles per split (S | (in / 16 / S) << 16), and the div_magic constants of S and x_div.
@@ -153,6 +167,16 @@ hipError_t run_gemv_fam_FAM_MUL1(int prologue, const GemvArgs &a, hipStream_t s)
 hipError_t run_gemv_fam_FAM_HASH(int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_PAIR(int prologue, const GemvArgs &a, hipStream_t s);
 hipError_t run_gemv_fam_FAM_3INST(int prologue, const GemvArgs &a, hipStream_t s);
+// The per-slot MoE decode chain in one launch: gate/up (a1, PRO_X, f32 planes written through to memory, then its
+// group's arrival counted) and the SwiGLU mid + down (a2, PRO_MID, folded into y) as one grid, the down workgroups
+// after the gate/up ones; a down workgroup issues its tile loads, then waits for its group's gate/up arrivals.  Uniform
+// banks at one lane-reader rate (a1.n == a2.n), one row per group.
+hipError_t run_moe_chain(int fam, const GemvArgs &a1, const GemvArgs &a2, hipStream_t s);
+hipError_t run_moe_chain_fam_FAM_MCG(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s);
+hipError_t run_moe_chain_fam_FAM_MUL1(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s);
+hipError_t run_moe_chain_fam_FAM_HASH(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s);
+hipError_t run_moe_chain_fam_FAM_PAIR(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s);
+hipError_t run_moe_chain_fam_FAM_3INST(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s);
 int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches = 1, int target_wgs = 0);
 
 // Top-k the MoE reduce holds per row (REDUCE_MAX_TOPK, src/exl3/expert_exl3_kernels.zig:2562).

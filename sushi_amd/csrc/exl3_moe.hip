@@ -20,6 +20,16 @@ hipError_t run_gemv(int fam, int prologue, const GemvArgs &a, hipStream_t s) {
     }
 }
 
+hipError_t run_moe_chain(int fam, const GemvArgs &a1, const GemvArgs &a2, hipStream_t s) {
+    switch (fam) {
+    case FAM_MCG: return run_moe_chain_fam_FAM_MCG(a1, a2, s);
+    case FAM_MUL1: return run_moe_chain_fam_FAM_MUL1(a1, a2, s);
+    case FAM_HASH: return run_moe_chain_fam_FAM_HASH(a1, a2, s);
+    case FAM_PAIR: return run_moe_chain_fam_FAM_PAIR(a1, a2, s);
+    default: return run_moe_chain_fam_FAM_3INST(a1, a2, s);
+    }
+}
+
 int gemv_default_splits(int in, int out, int rows, int groups_times_proj, int max_batches, int target_wgs) {
     // Splits cut k on whole Hadamard blocks.  A split of at most TPW * GEMV_WAVES k-tiles lets every wave issue all
     // of its tile loads before the prologue; up to max_batches such batches per wave are allowed where the grid is

@@ -668,3 +668,53 @@ def test_moe_gemm_arm_long_windows_clamp_and_shared(dev):
     term = O.gated_shared_terms(gate.float().numpy()[:, 0], sh.float().numpy(), 0)
     want_g = (want_g.astype(np.float16).astype(np.float32) + term).astype(np.float16).astype(np.float32)
     assert max_abs_rel(y_g.float().cpu().numpy(), want_g) < BAR
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8])
+@pytest.mark.parametrize("case", ["moe", "shared_bank", "gated", "clamp_f32scores", "bf16"])
+def test_moe_chain_in_one_launch_equals_two_launches(dev, rows, case):
+    """The per-slot decode chain fused into one launch (down workgroups wait on their slot's gate/up arrivals) equals
+    the two-launch chain bit for bit, call after call (its counters return to zero) and from a replayed HIP graph."""
+    print(f"[moe chain] {case} rows={rows}", flush=True)
+    E, hidden, inter, k, n = 16, 512, 384, 4, 32
+    dtype = torch.bfloat16 if case == "bf16" else torch.float16
+    b = synth.bank(49, "chain", E, hidden, inter, n, device=dev, norm=True)
+    sd = synth.bank(49, "chain.shared", 1, hidden, inter, n, device=dev, norm=True)
+    calls = []
+    for c in range(3):
+        x = synth.normal(49 + c, f"cx{rows}", (rows, hidden), device=dev).to(dtype)
+        inds, scores = _route(49 + c + rows, rows, E, k)
+        xi, sc = torch.from_numpy(inds.view(np.int32)).to(dev), torch.from_numpy(scores).to(dev)
+        sh = synth.normal(50 + c, "csh", (rows, hidden), device=dev).to(dtype)
+        g = synth.normal(51 + c, "cg", (rows, 1), device=dev).to(dtype)
+        if case == "moe" or case == "bf16":
+            calls.append(lambda x=x, xi=xi, sc=sc: exl3.moe(x, b, xi, sc, exl3.MCG))
+        elif case == "shared_bank":
+            calls.append(lambda x=x, xi=xi, sc=sc: exl3.moe_with_shared_bank(x, b, sd, xi, sc, exl3.MCG))
+        elif case == "gated":
+            calls.append(lambda x=x, xi=xi, sc=sc, sh=sh, g=g: exl3.moe_with_gated_shared(x, b, xi, sc, exl3.MCG,
+                                                                                         False, sh, g))
+        else:
+            calls.append(lambda x=x, xi=xi, sc=sc: exl3.moe_clamped(x, b, xi, sc, exl3.MCG, 5))
+    with exl3.arm_overrides(moe_chain=0):
+        ref = [f() for f in calls]
+    with exl3.arm_overrides(moe_chain=1):
+        got = [f() for f in calls] + [f() for f in calls]
+    torch.cuda.synchronize()
+    for i, y in enumerate(got):
+        assert torch.equal(y, ref[i % len(ref)]), i
+    outs = []
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side), exl3.arm_overrides(moe_chain=1):
+        [f() for f in calls]  # the side stream's workspace, made and zeroed before the capture
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            outs = [f() for f in calls]
+    torch.cuda.current_stream(dev).wait_stream(side)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, y in enumerate(outs):
+            assert torch.equal(y, ref[i]), ("graph", i)
