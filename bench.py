@@ -448,7 +448,7 @@ def bench_pack(pair_major: bool, experts: int = 256, hidden: int = 2048, inter: 
         shutil.rmtree(root, ignore_errors=True)
 
 
-def sweep(which: str, prefill_batches=None, prefill_arms=("gemm", "windows")):
+def sweep(which: str, prefill_batches=None, prefill_arms=("gemm", "windows"), c2_filter=None):
     """configs[1] (C2: MCG GEMV sweep), configs[2] (C3: prefill GEMM) and configs[4] (C5: ragged STQ MoE layer):
     one JSON line per case."""
     from sushi_amd import exl3
@@ -458,6 +458,8 @@ def sweep(which: str, prefill_batches=None, prefill_arms=("gemm", "windows")):
         for in_f, out_f in ((2048, 2048), (4096, 14336), (14336, 4096)):
             for n in (32, 48, 64):
                 for rows in (1, 4, 16):
+                    if c2_filter and (f"{in_f}x{out_f}", n, rows) not in c2_filter:
+                        continue
                     cases.append(("c2", in_f, out_f, n, rows, exl3.MCG, "mcg"))
     if which in ("c3", "all"):
         for rows in (512, 2048):
@@ -513,13 +515,16 @@ def _graph_layer_us(chain, dev, layers: int, rounds: int = ROUNDS) -> float:
 
     chain()
     torch.cuda.synchronize()
-    g = _capture(chain, dev)
+    g = _capture(chain, dev) if SWEEP_GRAPHS else None  # --no-graph: issued from Python (counter passes)
     stream = torch.cuda.current_stream(dev)
     times = []
     for _ in range(rounds):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        g.replay()
+        if g is not None:
+            g.replay()
+        else:
+            chain()
         e1.record(stream)
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1) * 1e3 / layers)
@@ -898,12 +903,15 @@ def main() -> int:
     ap.add_argument("--sweep", choices=("c2", "c3", "c5", "moe_prefill", "c5_prefill", "enc", "pack", "all"), help="time configs[1]/[2] cases instead (one JSON line each)")
     ap.add_argument("--prefill-batches", default="", help="moe_prefill sweep: token counts (default 64 .. 2048)")
     ap.add_argument("--prefill-arms", default="gemm,windows", help="moe_prefill sweep: arms to time")
+    ap.add_argument("--c2-cases", default="", help="c2 sweep: only these cases, e.g. 2048x2048:32:1,2048x2048:32:16 "
+                                                   "(shape:n:rows)")
     args = ap.parse_args()
     if args.sweep:
         global SWEEP_GRAPHS
         SWEEP_GRAPHS = not args.no_graph
         pb = tuple(int(b) for b in args.prefill_batches.split(",") if b)
-        sweep(args.sweep, pb or None, tuple(a for a in args.prefill_arms.split(",") if a))
+        c2f = {(c.split(":")[0], int(c.split(":")[1]), int(c.split(":")[2])) for c in args.c2_cases.split(",") if c}
+        sweep(args.sweep, pb or None, tuple(a for a in args.prefill_arms.split(",") if a), c2f or None)
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
