@@ -287,9 +287,10 @@ int32_t exl3_moe_groups(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
  * in all instead of four) and y = T(T(routed) + T(shared)), the rounding of the pair of calls (their k splits may
  * differ, so the f32 partial sums may round differently; both meet the same parity bar).  shared_bank is a
  * one-expert bank (trellis [1][hidden/16][inter/16][n] for gate/up, [1][inter/16][hidden/16][n] for down) with the
- * routed layer's inter; clamp_limit applies to both.  Up to 8 rows the shared rows join the per-slot launches;
+ * routed layer's inter; clamp_limit applies to both.  Up to 8 rows the shared rows join the per-slot launches (from
+ * 2 rows one launch: the down workgroups wait, bounded, on a counter their group's gate/up workgroups raise);
  * wider batches the sorted (expert-window) launches, where the shared rows are windows of their own (three launches
- * in all instead of six); at prefill widths (the routed GEMM arm, from 8 slots per expert on a uniform bank) the
+ * in all instead of six); at prefill widths (the routed GEMM arm, from 8 slots per expert, not under verify_rows) the
  * shared expert is one more expert of the GEMM arm's launches, its rows extra slots, any y dtype, and y equals the
  * pair of calls bit for bit.  Returns EXL3_DECLINED (nothing launched) where the fused form does not serve: y dtype
  * f32 off the GEMM arm, routed projections at different rates, a shared rate other than the routed one (uniform
