@@ -6,7 +6,9 @@ input.  Weights rotate over 64 resident copies (537 MB > the 256 MB Infinity Cac
 graphs: one graph of the 64 copies and one of the first (steps mod 64).  A timed round is exactly `--steps` calls
 (whole 64-copy replays, then the tail), and an untimed replay of the 64-copy graph precedes every round, so each
 timed call reads a copy last read 64 calls (537 MB of other weights) earlier: from HBM.  Seven rounds are timed
-(each bracketed by synchronisations, HIP events on the launch stream inside) and the median round is reported.
+(each bracketed by synchronisations) and the median round is reported.  The kernel's per-launch time comes from HIP
+events around two graphs, the 64-copy sequence and the same sequence followed by the `--steps` timed calls: their
+difference is the timed calls back to back inside one graph, without the start cost of a second graph.
 
 Prints one JSON line (the driver's contract).  `cpu_baseline` times the C restatement of the reference's CPU path
 (oracle/, `expert_exl3.project`) on a bounded sample of the same workload, on every host core and on one.
@@ -78,11 +80,15 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
     # The host side of a call (Python checks + ctypes) costs more than the kernel, so the calls are captured, one per
     # weight copy, into HIP graphs (outside the timed region) and replayed: a round then holds exactly `steps`
     # library launches back to back, as a native caller would issue them.
-    full = tail = None
+    full = tail = merged = None
     if graph_mode:
         full = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(COPIES)], dev)
         if steps % COPIES:
             tail = _capture(lambda: [exl3.linear(x, projs[i], dec) for i in range(steps % COPIES)], dev)
+        # the eviction sequence and then the timed calls, in one graph (each timed call's copy last read 64 calls
+        # earlier, as in the two-graph round)
+        merged = _capture(lambda: [exl3.linear(x, projs[i % COPIES], dec) for i in list(range(COPIES)) +
+                                   list(range(steps))], dev)
     stream = torch.cuda.current_stream(dev)
 
     def evict():
@@ -103,11 +109,24 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
             for i in range(steps):
                 exl3.linear(x, projs[i % COPIES], dec)
 
-    # Each round times the `steps` calls twice, each time right after an untimed eviction pass.  Wall clock: bracketed
-    # by synchronisations, so it holds the host's submission of the calls too (the whole-job figure).  HIP events: the
-    # eviction pass is still running when the timed calls are submitted behind it, so the events bracket the timed
-    # kernels back to back on the GPU, not the host's graph-launch latency ahead of the first of them.
-    walls, events = [], []
+    def event_ms(pre, body):
+        # HIP events on the launch stream around body(), submitted while pre() still runs, so the events bracket
+        # the GPU's work back to back and not the host's launch latency ahead of it
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        pre()
+        e0.record(stream)
+        body()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    # Each round times the `steps` calls right after an untimed eviction pass: by wall clock, bracketed by
+    # synchronisations, so it holds the host's submission of the calls too (the whole-job figure); and by HIP events
+    # on the launch stream, twice: around the timed calls' own graphs (`direct`: this holds the start of a second
+    # graph behind the eviction graph, which costs the GPU some 10-15 us whatever the graph holds), and as the
+    # difference between the merged graph and the eviction graph alone (`in_graph`: the timed calls back to back
+    # inside one graph, the per-launch time a caller's longer graph sees).
+    walls, events, in_graph = [], [], []
     for _ in range(rounds):
         evict()
         torch.cuda.synchronize()
@@ -115,17 +134,14 @@ def bench_linear(steps: int, warmup: int, graph_mode: bool = True, rounds: int =
         timed_calls()
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        evict()
-        e0.record(stream)
-        timed_calls()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        events.append(e0.elapsed_time(e1))
+        events.append(event_ms(evict, timed_calls))
+        if graph_mode:  # three differences a round: each is two ~0.5 ms spans whose jitter the median absorbs
+            in_graph += [event_ms(evict, merged.replay) - event_ms(evict, full.replay) for _ in range(3)]
     bytes_per_call = _algorithmic_bytes(in_f, out_f, n, rows)
-    del full, tail, trellis, projs
+    del full, tail, merged, trellis, projs
     torch.cuda.empty_cache()
-    return dict(wall_s=statistics.median(walls), event_ms=statistics.median(events), bytes=bytes_per_call, rows=rows,
+    return dict(wall_s=statistics.median(walls), event_ms=statistics.median(events),
+                in_graph_ms=statistics.median(in_graph) if in_graph else None, bytes=bytes_per_call, rows=rows,
                 y=y, steps=steps, rounds=rounds, wall_rounds_s=walls)
 
 
@@ -138,7 +154,8 @@ def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
     and every layer has its own routing, so the distinct experts hit change from layer to layer.  Every layer has its
     own bank (16 x 302 MB), as a model's layers do: the weights a layer reads were last read 15 layers (4.5 GB, far
     past the 256 MB Infinity Cache) earlier, so they come from HBM.  The banks' svh carry 1/sqrt(in) (synth norm),
-    keeping each layer's output near unit scale.  Median of `rounds` replays."""
+    keeping each layer's output near unit scale.  Per layer: HIP events around a graph of the layers twice over less
+    those around the graph of the layers once, median of `rounds` rounds."""
     import statistics
 
     import torch
@@ -165,21 +182,34 @@ def bench_moe(batch: int, layers: int = 16, rounds: int = ROUNDS):
     chain()
     torch.cuda.synchronize()
     g = _capture(chain, dev)
+    # the layers twice over in one graph: the second pass reads each bank 15 layers after the first
+    g2 = _capture(lambda: (chain(), chain()), dev)
     stream = torch.cuda.current_stream(dev)
-    times = []
-    for _ in range(rounds):
+
+    def event_us(body):
+        # events submitted behind a running replay, so they bracket the GPU's work back to back
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
         g.replay()
+        e0.record(stream)
+        body()
         e1.record(stream)
         torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1) * 1e3 / layers)
+        return e0.elapsed_time(e1) * 1e3
+
+    # Per layer: the doubled graph less the single one (the layers back to back inside one graph, without the GPU's
+    # start of a graph behind another); `direct`: events around the single graph.
+    times, direct = [], []
+    for _ in range(rounds):
+        t1 = event_us(g.replay)
+        times.append((event_us(g2.replay) - t1) / layers)
+        direct.append(t1 / layers)
     layer_us = statistics.median(times)
     distinct = sum(len(set(i.flatten().tolist())) for i, _ in routes) / layers
     per_expert = 3 * (hidden * inter * n // 128 + 2 * (hidden + inter))
-    del g, banks, shareds
+    del g, g2, banks, shareds
     torch.cuda.empty_cache()
-    return dict(batch=batch, layer_us=layer_us, us_per_token=layer_us / batch, distinct=distinct,
+    return dict(batch=batch, layer_us=layer_us, layer_us_direct=statistics.median(direct),
+                us_per_token=layer_us / batch, distinct=distinct,
                 bytes=(distinct + 1) * per_expert)
 
 
@@ -925,7 +955,8 @@ def main() -> int:
     steps = lin["steps"]
     ms_per_step = lin["wall_s"] / steps * 1e3
     value = lin["bytes"] / (lin["wall_s"] / steps) / 1e9
-    launch_s = lin["event_ms"] / 1e3 / steps
+    launch_direct_s = lin["event_ms"] / 1e3 / steps
+    launch_s = lin["in_graph_ms"] / 1e3 / steps if lin["in_graph_ms"] is not None else launch_direct_s
     achieved = lin["bytes"] / launch_s / 1e9
     moe = [] if args.no_moe else [bench_moe(int(b)) for b in args.moe_batches.split(",") if b]
     ceilings = measured_ceilings(4096 * 4096 * 64 // 128) if not args.no_ceilings else None
@@ -950,20 +981,25 @@ def main() -> int:
         "tok_per_s": round(1.0 / (lin["wall_s"] / steps), 1),
         "timing": f"median of {lin['rounds']} rounds of exactly {steps} calls, each after an untimed replay of the "
                   "64-copy sequence (every timed call reads a copy last read 64 calls, 537 MB, earlier); value: wall "
-                  "clock between synchronisations; roofline.achieved: HIP events around the same calls submitted "
-                  "behind the eviction replay (the kernels back to back, without the host's launch latency)"
-                  + ("; calls replayed from HIP graphs" if not args.no_graph else "; calls issued from Python"),
+                  "clock between synchronisations; roofline.achieved: HIP events on the launch stream, the graph of "
+                  "the eviction sequence followed by the timed calls less the eviction graph alone (the timed calls "
+                  "back to back inside one graph; launch_us_direct: events around the timed calls' own graph behind "
+                  "the eviction graph, which adds the GPU's start of a second graph)"
+                  if not args.no_graph else "clock between synchronisations; roofline.achieved: HIP events around "
+                  "the calls, issued from Python behind the eviction pass",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": "profiles/gemv_c1_3inst_k4_b1_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE and "
                                        "WRITE_SIZE passes of bench.py, scaled by a copy kernel's counters)"
                                        if traffic else None,
                      "algorithmic_bytes": lin["bytes"], "launch_us": round(launch_s * 1e6, 3),
+                     "launch_us_direct": round(launch_direct_s * 1e6, 3),
                      "measured_ceilings": ceilings},
         "cpu_baseline": cpu,
     }
     if twin:
-        t_launch = twin["event_ms"] / 1e3 / twin["steps"]
+        t_direct = twin["event_ms"] / 1e3 / twin["steps"]
+        t_launch = twin["in_graph_ms"] / 1e3 / twin["steps"] if twin["in_graph_ms"] is not None else t_direct
         t_ach = twin["bytes"] / t_launch / 1e9
         out["mcg_twin"] = {
             "what": "the headline GEMV with the same codes through the reference's MCG decode (3INST, the configured "
@@ -971,7 +1007,8 @@ def main() -> int:
             "value": round(twin["bytes"] / (twin["wall_s"] / twin["steps"]) / 1e9, 2), "unit": "GB/s",
             "ms_per_step": round(twin["wall_s"] / twin["steps"] * 1e3, 6),
             "roofline": {"bound": "hbm", "achieved": round(t_ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(t_ach / HBM_PEAK_GBS, 4), "launch_us": round(t_launch * 1e6, 3)}}
+                         "frac": round(t_ach / HBM_PEAK_GBS, 4), "launch_us": round(t_launch * 1e6, 3),
+                         "launch_us_direct": round(t_direct * 1e6, 3)}}
     if ceilings:
         out["roofline"]["frac_of_measured_read"] = round(achieved / ceilings["hbm_read_GBps"], 4)
         out["roofline"]["launch_us_over_read_floor"] = round(launch_s * 1e6 / ceilings["read_small_graph_us"], 3)
@@ -979,9 +1016,11 @@ def main() -> int:
         out["moe_layer"] = {"config": "E=256 routed + 1 shared, hidden 2048, inter 768, K2 MCG, top-8; 16 layers back "
                                       "to back on one stream from a HIP graph, each its own bank (16 x 302 MB, so "
                                       "weights come from HBM), N(0,1) input and routing (svh with 1/sqrt(in)); "
-                                      "median of 7 replays",
+                                      "layer_us: HIP events, the 16 layers twice over in one graph less once "
+                                      "(layer_us_direct: events around the one graph), median of 7 rounds",
                             "us_per_token": round(moe[0]["us_per_token"], 3),
                             "batches": [{"batch": m["batch"], "layer_us": round(m["layer_us"], 3),
+                                         "layer_us_direct": round(m["layer_us_direct"], 3),
                                          "us_per_token": round(m["us_per_token"], 3),
                                          "distinct_experts": round(m["distinct"], 2),
                                          "effective_GBps": round(m["bytes"] / (m["layer_us"] * 1e-6) / 1e9, 2)}

@@ -564,6 +564,28 @@ def test_moe_gemm_arm_against_oracle(dev, rows, E, k, label, dec, odec):
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
+@pytest.mark.parametrize("rows,E,k", [(40, 16, 4), (300, 8, 2)])
+@pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
+@pytest.mark.parametrize("label,dec,odec", [
+    ("mcg", exl3.MCG, O.decode(O.CB_MCG)),
+    ("3inst", exl3.INST3, O.decode(O.CB_3INST)),
+])
+def test_moe_gemm_arm_every_lane_rate(dev, rows, E, k, n, label, dec, odec):
+    """The routed GEMM arm's kernel is built per lane rate (16, 24, 32, 40, 48 and 64 bits a row of 16 weights):
+    forced at a sorted-window width and at a prefill width, each rate against the oracle to the bar."""
+    print(f"[moe gemm rate] {label} n={n} rows={rows} E={E} k={k}", flush=True)
+    hidden, inter = 256, 384
+    b = synth.bank(43, f"mgr.{label}.{n}", E, hidden, inter, n, norm=True)
+    x = synth.normal(43, f"x{rows}", (rows, hidden))
+    inds, scores = _route(43 + rows, rows, E, k)
+    want = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, scores, hidden, inter,
+                             (n, n, n), odec, threads=8)
+    with exl3.arm_overrides(moe_gemm=1):
+        y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                     torch.from_numpy(scores).to(dev), dec)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
 @pytest.mark.parametrize("rows,E,k", [(64, 16, 4), (300, 8, 2)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("limit", [0, 5])
