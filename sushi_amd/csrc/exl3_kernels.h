@@ -234,7 +234,10 @@ struct MoeGemmWindows {
     uint32_t *win_start;    // [windows] first sorted position
     uint32_t *win_tile0;    // [windows] first fragment tile
     uint32_t *tile_window;  // [tiles] the window of each tile
+    uint32_t *chunk_counts; // [experts (+ 1 shared)][kMoeGemmMaxChunks] scratch: each expert's count per chunk
+    uint32_t *ranks;        // [slots] scratch: each slot's rank among its chunk's earlier slots of its expert
 };
+constexpr int kMoeGemmMaxChunks = 64;
 // sh_rows > 0 adds a shared expert as expert `experts`: slots nslots .. nslots + sh_rows - 1, one per token row.
 hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, int sh_rows, const MoeGemmWindows &t,
                                 hipStream_t s);

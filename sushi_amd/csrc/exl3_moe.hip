@@ -172,7 +172,6 @@ hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
 // round with the same expert (found by one ballot per bit of the expert id), so the result does not depend on thread
 // timing.
 constexpr int WIN_THREADS = 1024;
-constexpr int GW_CHUNKS = 16;  // ranking waves of the GEMM arm's windows (16 x 1024 experts of u32 counts: 64 KiB of LDS)
 __global__ __launch_bounds__(WIN_THREADS) void moe_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
                                                                   int experts, uint32_t *__restrict__ win_count,
                                                                   uint32_t *__restrict__ win_expert,
@@ -254,124 +253,184 @@ hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32
 // run cut into windows of up to MOE_GEMM_WINDOW_ROWS rows (window i of expert e is wbase[e] + i, starting at sorted
 // position sbase[e] + i * W); and the 16-row fragment tiles of the prepared inputs numbered so that expert e's rows
 // occupy tiles tbase[e] .. tbase[e] + ceil(count / 16) - 1 (a window's tiles are contiguous, from win_tile0).
-// tile_window[t] names the window of tile t.  Ranks come from GW_CHUNKS waves, each walking its contiguous chunk of
-// the slots in order from the chunk's per-expert prefix.
-__global__ __launch_bounds__(WIN_THREADS) void moe_gemm_windows_kernel(const uint32_t *__restrict__ inds, int nslots,
-                                                                       int experts, int sh_rows, MoeGemmWindows t) {
-    // The slots are cut into GW_CHUNKS contiguous chunks, one per ranking wave: per-chunk counts by LDS atomics, their
-    // exclusive prefix over chunks per expert, then each wave ranks its own chunk in order (a single wave walking
-    // every slot waits out one load round trip per 64 slots: 90 us for 16384 slots).
-    __shared__ uint32_t ccnt[GW_CHUNKS][kMoeGemmMaxExperts];  // counts, then the chunk's first rank per expert
+// tile_window[t] names the window of tile t.  A shared expert's rows (sh_rows > 0) are slots nslots .. ns - 1 of
+// expert `experts`.
+//
+// Two launches over contiguous chunks of the slots, one workgroup per chunk.  The first ranks each slot among the
+// chunk's earlier slots of its expert and writes the chunk's per-expert counts; the second sums the counts of the
+// chunks before its own (the slot's rank among all earlier slots is that plus its rank in the chunk), scans the
+// experts' slots, tiles and windows, and places its chunk.  Every rank is a count of earlier slots, so the result does
+// not depend on thread timing.
+constexpr int GR_THREADS = 512;   // ranking workgroup: one slot per thread per pass
+constexpr int GP_THREADS = 1024;  // placing workgroup: one thread per expert
+static_assert(GP_THREADS >= kMoeGemmMaxExperts, "the placing workgroup scans one expert per thread");
+
+__device__ __forceinline__ uint32_t gemm_expert_of(const uint32_t *inds, int nslots, int experts, int s) {
+    return s < nslots ? min(inds[s], (uint32_t)(experts - 1)) : (uint32_t)experts;
+}
+
+__global__ __launch_bounds__(GR_THREADS) void moe_gemm_rank_kernel(const uint32_t *__restrict__ inds, int nslots,
+                                                                   int experts, int sh_rows, int chunk,
+                                                                   MoeGemmWindows t) {
+    constexpr int NW = GR_THREADS / 64;
+    __shared__ uint32_t wc[NW][kMoeGemmMaxExperts];  // this pass: each wave's count per expert
+    __shared__ uint32_t run[kMoeGemmMaxExperts];     // the chunk's earlier passes
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ns = nslots + sh_rows, ne = experts + (sh_rows > 0 ? 1 : 0);
+    const int id_bits = ne > 1 ? 32 - __clz(ne - 1) : 0;
+    const int c0 = blockIdx.x * chunk, c1 = min(c0 + chunk, ns);
+    for (int e = tid; e < ne; e += GR_THREADS) run[e] = 0;
+    for (int base = c0; base < c1; base += GR_THREADS) {
+        const int s = base + tid;
+        const bool live = s < c1;
+        const int e = live ? (int)gemm_expert_of(inds, nslots, experts, s) : 0;  // in flight while wc is cleared
+        for (int e2 = tid; e2 < ne; e2 += GR_THREADS)
+#pragma unroll
+            for (int w = 0; w < NW; w++) wc[w][e2] = 0;
+        __syncthreads();
+        // the lanes of this wave holding this lane's expert: one ballot per bit of the expert id, and the live lanes
+        unsigned long long same = __ballot(live);
+        for (int b = 0; b < id_bits; b++) {
+            const unsigned long long set = __ballot((e >> b) & 1);
+            same &= ((e >> b) & 1) ? set : ~set;
+        }
+        const unsigned long long below = (1ull << lane) - 1ull;
+        const uint32_t before = (uint32_t)__popcll(same & below);
+        if (live && (same & ~below & ~(1ull << lane)) == 0ull) wc[wave][e] = before + 1;  // the wave's last of e
+        __syncthreads();
+        if (live) {
+            uint32_t r = run[e] + before;
+            for (int w = 0; w < wave; w++) r += wc[w][e];
+            t.ranks[s] = r;
+        }
+        __syncthreads();
+        for (int e2 = tid; e2 < ne; e2 += GR_THREADS) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) v += wc[w][e2];
+            run[e2] += v;
+        }
+        __syncthreads();
+    }
+    for (int e = tid; e < ne; e += GR_THREADS) t.chunk_counts[(size_t)e * kMoeGemmMaxChunks + blockIdx.x] = run[e];
+}
+
+// Inclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t u = __shfl_up(v, off, 64);
+        v += lane >= off ? u : 0u;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(GP_THREADS) void moe_gemm_place_kernel(const uint32_t *__restrict__ inds, int nslots,
+                                                                    int experts, int sh_rows, int chunk, int nchunks,
+                                                                    MoeGemmWindows t) {
+    constexpr int NW = GP_THREADS / 64;
     __shared__ uint32_t cnt[kMoeGemmMaxExperts];
+    __shared__ uint32_t pre[kMoeGemmMaxExperts];  // the expert's slots in the chunks before this one
     __shared__ uint32_t sb[kMoeGemmMaxExperts];
     __shared__ uint32_t tb[kMoeGemmMaxExperts];
     __shared__ uint32_t wb[kMoeGemmMaxExperts];
-    __shared__ uint32_t part[3][WIN_THREADS];
+    __shared__ uint32_t wsum[3][NW];
     constexpr uint32_t W = MOE_GEMM_WINDOW_ROWS;
-    const int tid = threadIdx.x;
-    // a shared expert's rows are slots nslots .. ns - 1 of expert `experts`
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
     const int ns = nslots + sh_rows, ne = experts + (sh_rows > 0 ? 1 : 0);
-    auto expert_of = [&](int s) { return s < nslots ? min(inds[s], (uint32_t)(experts - 1)) : (uint32_t)experts; };
-    const int chunk = (((ns + GW_CHUNKS - 1) / GW_CHUNKS) + 63) / 64 * 64;  // slots per chunk, whole groups of 64
-    for (int e = tid; e < ne; e += WIN_THREADS)
-        for (int c = 0; c < GW_CHUNKS; c++) ccnt[c][e] = 0;
-    __syncthreads();
-    for (int s = tid; s < ns; s += WIN_THREADS) atomicAdd(&ccnt[s / chunk][expert_of(s)], 1u);
-    __syncthreads();
-    for (int e = tid; e < ne; e += WIN_THREADS) {
-        uint32_t run = 0;
-        for (int c = 0; c < GW_CHUNKS; c++) {
-            const uint32_t v = ccnt[c][e];
-            ccnt[c][e] = run;
-            run += v;
+    // Thread v takes the v-th expert of the scan order (a shared expert first, so its windows -- full ones of 256
+    // rows, the GEMMs' heaviest workgroups -- are numbered and dispatched first instead of trailing the grid): its
+    // row of chunk counts in one round of loads (entries past nchunks are ignored), its total and the part before
+    // this chunk.
+    const int c0 = c * chunk, c1 = min(c0 + chunk, ns);
+    // this thread's first slot of the chunk: its expert and its rank in the chunk, in flight under the scans
+    uint32_t x0 = 0, r0 = 0;
+    if (c0 + tid < c1) {
+        x0 = gemm_expert_of(inds, nslots, experts, c0 + tid);
+        r0 = t.ranks[c0 + tid];
+    }
+    const int v = tid;
+    const int e = v < ne ? (sh_rows > 0 ? (v == 0 ? experts : v - 1) : v) : 0;
+    uint32_t total = 0, p = 0;
+    if (v < ne) {
+        const uint4 *row = reinterpret_cast<const uint4 *>(t.chunk_counts + (size_t)e * kMoeGemmMaxChunks);
+        uint4 q4[kMoeGemmMaxChunks / 4];
+#pragma unroll
+        for (int q = 0; q < kMoeGemmMaxChunks / 4; q++) q4[q] = row[q];
+#pragma unroll
+        for (int q = 0; q < kMoeGemmMaxChunks / 4; q++) {
+            const uint32_t u[4] = {q4[q].x, q4[q].y, q4[q].z, q4[q].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int cc = 4 * q + i;
+                total += cc < nchunks ? u[i] : 0u;
+                p += cc < c ? u[i] : 0u;
+            }
         }
-        cnt[e] = run;
+        cnt[e] = total;
+        pre[e] = p;
+    }
+    // three exclusive scans in scan order (slots, 16-row tiles, windows): within each wave, then over the waves
+    const uint32_t ls = total, lt = (total + 15) / 16, lw = (total + W - 1) / W;
+    const uint32_t is = wave_inclusive_sum(ls, lane), it = wave_inclusive_sum(lt, lane),
+                   iw = wave_inclusive_sum(lw, lane);
+    if (lane == 63) {
+        wsum[0][wave] = is;
+        wsum[1][wave] = it;
+        wsum[2][wave] = iw;
     }
     __syncthreads();
-    // three exclusive scans over experts (slots, 16-row tiles, windows): each thread sums a contiguous run.  A shared
-    // expert comes first in the scan order, so its windows (full ones of 256 rows, the GEMMs' heaviest workgroups)
-    // are numbered and dispatched first instead of trailing the grid.
-    const int per = (ne + WIN_THREADS - 1) / WIN_THREADS;
-    const int e0 = min(tid * per, ne), e1 = min(e0 + per, ne);
-    auto scan_expert = [&](int v) { return sh_rows > 0 ? (v == 0 ? experts : v - 1) : v; };
-    uint32_t ls = 0, lt = 0, lw = 0;
-    for (int v = e0; v < e1; v++) {
-        const int e = scan_expert(v);
-        ls += cnt[e];
-        lt += (cnt[e] + 15) / 16;
-        lw += (cnt[e] + W - 1) / W;
+    uint32_t os = 0, ot = 0, ow = 0, at = 0, aw = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        os += w < wave ? wsum[0][w] : 0u;
+        ot += w < wave ? wsum[1][w] : 0u;
+        ow += w < wave ? wsum[2][w] : 0u;
+        at += wsum[1][w];
+        aw += wsum[2][w];
     }
-    part[0][tid] = ls;
-    part[1][tid] = lt;
-    part[2][tid] = lw;
-    __syncthreads();
-    for (int off = 1; off < WIN_THREADS; off <<= 1) {
-        uint32_t v[3];
-        for (int q = 0; q < 3; q++) v[q] = tid >= off ? part[q][tid - off] : 0u;
-        __syncthreads();
-        for (int q = 0; q < 3; q++) part[q][tid] += v[q];
-        __syncthreads();
+    if (v < ne) {
+        sb[e] = os + is - ls;
+        tb[e] = ot + it - lt;
+        wb[e] = ow + iw - lw;
     }
-    uint32_t rs = part[0][tid] - ls, rt = part[1][tid] - lt, rw = part[2][tid] - lw;
-    for (int v = e0; v < e1; v++) {
-        const int e = scan_expert(v);
-        sb[e] = rs;
-        tb[e] = rt;
-        wb[e] = rw;
-        rs += cnt[e];
-        rt += (cnt[e] + 15) / 16;
-        rw += (cnt[e] + W - 1) / W;
-    }
-    if (tid == WIN_THREADS - 1) {
-        *t.win_count = part[2][tid];
-        *t.tile_count = part[1][tid];
+    if (c == 0 && tid == 0) {
+        *t.win_count = aw;
+        *t.tile_count = at;
     }
     __syncthreads();
-    const int wave = tid >> 6;
-    if (wave < GW_CHUNKS) {  // wave c ranks chunk c in slot order; the next group's indices load under this one's work
-        const int lane = tid & 63;
-        const int id_bits = ne > 1 ? 32 - __clz(ne - 1) : 0;
-        const int c0 = wave * chunk, c1 = min(c0 + chunk, ns);
-        uint32_t next = c0 + lane < c1 ? expert_of(c0 + lane) : 0u;
-        for (int base = c0; base < c1; base += 64) {
-            const int s = base + lane;
-            const bool live = s < c1;
-            const int e = live ? (int)next : 0;
-            next = base + 64 + lane < c1 ? expert_of(base + 64 + lane) : 0u;
-            unsigned long long same = __ballot(live);
-            for (int b = 0; b < id_bits; b++) {
-                const unsigned long long set = __ballot((e >> b) & 1);
-                same &= ((e >> b) & 1) ? set : ~set;
-            }
-            const unsigned long long below = (1ull << lane) - 1ull;
-            const uint32_t before = (uint32_t)__popcll(same & below);
-            const bool last = live && (same & ~below & ~(1ull << lane)) == 0ull;
-            if (live) {
-                const uint32_t rank = ccnt[wave][e] + before;
-                t.sorted[sb[e] + rank] = (uint32_t)s;
-                if (rank % W == 0) {  // the first slot of a window writes its row
-                    const uint32_t w = wb[e] + rank / W, rows = min(cnt[e] - rank, W);
-                    const uint32_t tile0 = tb[e] + rank / 16;
-                    t.win_expert[w] = (uint32_t)e;
-                    t.win_rows[w] = rows;
-                    t.win_start[w] = sb[e] + rank;
-                    t.win_tile0[w] = tile0;
-                    for (uint32_t i = 0; i < (rows + 15) / 16; i++) t.tile_window[tile0 + i] = w;
-                }
-            }
-            // every lane has read this group's ranks before the group's last lane per expert moves them on
-            __builtin_amdgcn_wave_barrier();
-            if (last) ccnt[wave][e] = ccnt[wave][e] + before + 1;
-            __builtin_amdgcn_wave_barrier();
+    for (int s = c0 + tid; s < c1; s += GP_THREADS) {
+        const bool first = s == c0 + tid;
+        const uint32_t x = first ? x0 : gemm_expert_of(inds, nslots, experts, s);
+        const uint32_t rank = pre[x] + (first ? r0 : t.ranks[s]);
+        t.sorted[sb[x] + rank] = (uint32_t)s;
+        if (rank % W == 0) {  // the first slot of a window writes its row
+            const uint32_t w = wb[x] + rank / W, rows = min(cnt[x] - rank, W);
+            const uint32_t tile0 = tb[x] + rank / 16;
+            t.win_expert[w] = x;
+            t.win_rows[w] = rows;
+            t.win_start[w] = sb[x] + rank;
+            t.win_tile0[w] = tile0;
+            for (uint32_t i = 0; i < (rows + 15) / 16; i++) t.tile_window[tile0 + i] = w;
         }
     }
+}
+
+// Slots per chunk: whole ranking passes, at most kMoeGemmMaxChunks chunks.
+int moe_gemm_chunk(int ns) {
+    const int per = (ns + kMoeGemmMaxChunks - 1) / kMoeGemmMaxChunks;
+    return std::max(GR_THREADS, (per + GR_THREADS - 1) / GR_THREADS * GR_THREADS);
 }
 
 hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, int sh_rows, const MoeGemmWindows &t,
                                 hipStream_t s) {
     if (nslots <= 0 || experts <= 0 || sh_rows < 0 || experts + (sh_rows > 0 ? 1 : 0) > kMoeGemmMaxExperts)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_gemm_windows_kernel, dim3(1), dim3(WIN_THREADS), 0, s, inds, nslots, experts, sh_rows, t);
+    const int ns = nslots + sh_rows, chunk = moe_gemm_chunk(ns), nchunks = (ns + chunk - 1) / chunk;
+    hipLaunchKernelGGL(moe_gemm_rank_kernel, dim3(nchunks), dim3(GR_THREADS), 0, s, inds, nslots, experts, sh_rows,
+                       chunk, t);
+    hipLaunchKernelGGL(moe_gemm_place_kernel, dim3(nchunks), dim3(GP_THREADS), 0, s, inds, nslots, experts, sh_rows,
+                       chunk, nchunks, t);
     return hipGetLastError();
 }
 
