@@ -347,7 +347,7 @@ MoeGemmPlan plan_moe_gemm(int nslots, int hidden, int inter, int experts) {
     p.max_windows = std::min(nslots, experts + (nslots + W - 1) / W);
     p.max_tiles = (nslots + 15) / 16 + std::min(nslots, experts);
     p.tables = align_up(2 * sizeof(uint32_t)) + align_up((size_t)nslots * 4) + 4 * align_up((size_t)p.max_windows * 4) +
-               align_up((size_t)p.max_tiles * 4) + align_up((size_t)kMoeGemmMaxChunks * experts * 4) +
+               align_up((size_t)p.max_tiles * 16) + align_up((size_t)kMoeGemmMaxChunks * experts * 4) +
                align_up((size_t)nslots * 4);
     p.xp_gu = align_up((size_t)p.max_tiles * 16 * hidden * 2);
     p.xp_down = align_up((size_t)p.max_tiles * 16 * inter * 2);
@@ -455,7 +455,7 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
         g.win.win_rows = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
         g.win.win_start = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
         g.win.win_tile0 = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_windows * 4)));
-        g.win.tile_window = reinterpret_cast<uint32_t *>(take(align_up((size_t)gp.max_tiles * 4)));
+        g.win.tile_info = reinterpret_cast<uint4 *>(take(align_up((size_t)gp.max_tiles * 16)));
         g.win.chunk_counts = reinterpret_cast<uint32_t *>(
             take(align_up((size_t)kMoeGemmMaxChunks * (experts + (sb ? 1 : 0)) * 4)));
         g.win.ranks = reinterpret_cast<uint32_t *>(take(align_up((size_t)(nslots + sh_rows) * 4)));

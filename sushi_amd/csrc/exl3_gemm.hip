@@ -966,13 +966,12 @@ struct TileRows {
 
 __device__ __forceinline__ TileRows tile_rows(const MoeGemmArgs &a, int t) {
     TileRows r;
+    const uint4 ti = a.win.tile_info[t];  // t < max_tiles (the grid); read beside the count, used only if live
     r.live = (uint32_t)t < *a.win.tile_count;
     if (!r.live) return r;
-    const uint32_t w = a.win.tile_window[t];
-    const int i = t - (int)a.win.win_tile0[w];
-    r.rows = min(16, (int)a.win.win_rows[w] - 16 * i);
-    r.e = moe_expert(a, a.win.win_expert[w]);
-    r.slots = a.win.sorted + a.win.win_start[w] + 16 * i;
+    r.rows = (int)ti.y;
+    r.e = moe_expert(a, ti.x);
+    r.slots = a.win.sorted + ti.z;
     return r;
 }
 
@@ -985,51 +984,67 @@ __device__ __forceinline__ void tile_to_frag(const uint16_t (*tl)[128 + 8], uint
 }
 
 // prepareInput (expert_exl3.zig:490-501) of each row's token with its expert's suh, for each of the nproj projections
-// (gate and up) from one load of the rows: a wave's four rows load together, then every projection's transforms run
-// together.  (A workgroup per projection gathered each token row from memory once per projection: 95 us at 2048
-// tokens.)
+// (gate and up) from one load of the rows, over NB consecutive 128-column blocks of one tile: a wave's four rows of
+// every block load together (one round of loads for the workgroup's share, behind the tile's one table load), then
+// each block's transforms run for both projections at once.  (A workgroup per projection gathered each token
+// row from memory once per projection: 95 us at 2048 tokens.)
+template <int NB>
 __global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a, int nproj) {
-    const int b = blockIdx.x, t = blockIdx.y;
+    const int b0 = blockIdx.x * NB, t = blockIdx.y;
     const TileRows tr = tile_rows(a, t);
     if (!tr.live) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ __align__(16) uint16_t tl[2][16][128 + 8];
+    __shared__ __align__(16) uint16_t tl[NB][2][16][128 + 8];
     const bool shx = tr.e >= a.experts;
-    const size_t si = (shx ? 0 : (size_t)tr.e * a.in) + (size_t)b * 128;
-    float x0[4], x1[4];
+    const size_t se = shx ? 0 : (size_t)tr.e * a.in;
+    float x0[NB][4], x1[NB][4], u0[NB][2], u1[NB][2];
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) {
         const int r = wave * 4 + rr;
-        x0[rr] = x1[rr] = 0.f;
-        if (r < tr.rows) {
-            const size_t xi = (size_t)moe_token(a, tr.slots[r]) * a.in + (size_t)b * 128;
-            x0[rr] = f16r(load_any(a.x, a.x_dtype, xi + lane));
-            x1[rr] = f16r(load_any(a.x, a.x_dtype, xi + lane + 64));
+        const bool live = r < tr.rows;
+        const size_t xr = live ? (size_t)moe_token(a, tr.slots[r]) * a.in : 0;
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const size_t xi = xr + (size_t)(b0 + nb) * 128;
+            x0[nb][rr] = live ? f16r(load_any(a.x, a.x_dtype, xi + lane)) : 0.f;
+            x1[nb][rr] = live ? f16r(load_any(a.x, a.x_dtype, xi + lane + 64)) : 0.f;
         }
     }
-    float v0[8], v1[8];  // [projection][row]; rows past the end stay zeros
 #pragma unroll
     for (int q = 0; q < 2; q++) {
         const bool on = q < nproj;
         const uint16_t *su = shx ? a.sh_suh[q] : a.suh[q];
-        const float u0 = on ? h2f(su[si + lane]) : 0.f, u1 = on ? h2f(su[si + lane + 64]) : 0.f;
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-            v0[q * 4 + rr] = x0[rr] * u0;
-            v1[q * 4 + rr] = x1[rr] * u1;
+        for (int nb = 0; nb < NB; nb++) {
+            const size_t si = se + (size_t)(b0 + nb) * 128;
+            u0[nb][q] = on ? h2f(su[si + lane]) : 0.f;
+            u1[nb][q] = on ? h2f(su[si + lane + 64]) : 0.f;
         }
     }
-    fwht128_wave_rows<8>(v0, v1, lane);
 #pragma unroll
-    for (int q = 0; q < 2; q++)
+    for (int nb = 0; nb < NB; nb++) {
+        float v0[8], v1[8];  // [projection][row]; rows past the end stay zeros
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-            const int r = wave * 4 + rr;
-            tl[q][r][lane] = __half_as_ushort(__float2half_rn(v0[q * 4 + rr] * HAD_SCALE));
-            tl[q][r][lane + 64] = __half_as_ushort(__float2half_rn(v1[q * 4 + rr] * HAD_SCALE));
-        }
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+                v0[q * 4 + rr] = x0[nb][rr] * u0[nb][q];
+                v1[q * 4 + rr] = x1[nb][rr] * u1[nb][q];
+            }
+        fwht128_wave_rows<8>(v0, v1, lane);
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+                const int r = wave * 4 + rr;
+                tl[nb][q][r][lane] = __half_as_ushort(__float2half_rn(v0[q * 4 + rr] * HAD_SCALE));
+                tl[nb][q][r][lane + 64] = __half_as_ushort(__float2half_rn(v1[q * 4 + rr] * HAD_SCALE));
+            }
+    }
     __syncthreads();
-    for (int q = 0; q < nproj; q++) tile_to_frag(tl[q], a.xp[q], t, b, a.in, tid);
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+        for (int q = 0; q < nproj; q++) tile_to_frag(tl[nb][q], a.xp[q], t, b0 + nb, a.in, tid);
 }
 
 // The SwiGLU mid of the routed GEMM arm (DOWN_FUSED_SOURCE's prologue, expert_exl3_kernels.zig:1838-1925; the
@@ -1091,8 +1106,15 @@ __global__ __launch_bounds__(256) void moe_gemm_mid_kernel(MoeGemmArgs a) {
 
 hipError_t run_moe_gemm_prepare(const MoeGemmArgs &a, int nproj, hipStream_t s) {
     if (nproj < 1 || nproj > 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_gemm_prepare_kernel, dim3((unsigned)(a.in / 128), (unsigned)a.max_tiles), dim3(256), 0, s,
-                       a, nproj);
+    // two 128-column blocks a workgroup where they pair up (measured at 2048 tokens of configs[3]: 85 -> 79 us; four
+    // blocks took 110)
+    const int blocks = a.in / 128;
+    if (blocks % 2 == 0)
+        hipLaunchKernelGGL(moe_gemm_prepare_kernel<2>, dim3((unsigned)(blocks / 2), (unsigned)a.max_tiles), dim3(256),
+                           0, s, a, nproj);
+    else
+        hipLaunchKernelGGL(moe_gemm_prepare_kernel<1>, dim3((unsigned)blocks, (unsigned)a.max_tiles), dim3(256), 0, s,
+                           a, nproj);
     return hipGetLastError();
 }
 

@@ -233,7 +233,7 @@ struct MoeGemmWindows {
     uint32_t *win_rows;     // [windows] rows (<= MOE_GEMM_WINDOW_ROWS)
     uint32_t *win_start;    // [windows] first sorted position
     uint32_t *win_tile0;    // [windows] first fragment tile
-    uint32_t *tile_window;  // [tiles] the window of each tile
+    uint4 *tile_info;       // [tiles] each tile's window expert, live rows (<= 16) and first sorted position
     uint32_t *chunk_counts; // [experts (+ 1 shared)][kMoeGemmMaxChunks] scratch: each expert's count per chunk
     uint32_t *ranks;        // [slots] scratch: each slot's rank among its chunk's earlier slots of its expert
 };

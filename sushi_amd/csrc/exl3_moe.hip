@@ -253,8 +253,8 @@ hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32
 // run cut into windows of up to MOE_GEMM_WINDOW_ROWS rows (window i of expert e is wbase[e] + i, starting at sorted
 // position sbase[e] + i * W); and the 16-row fragment tiles of the prepared inputs numbered so that expert e's rows
 // occupy tiles tbase[e] .. tbase[e] + ceil(count / 16) - 1 (a window's tiles are contiguous, from win_tile0).
-// tile_window[t] names the window of tile t.  A shared expert's rows (sh_rows > 0) are slots nslots .. ns - 1 of
-// expert `experts`.
+// tile_info[t] holds tile t's expert, live rows and first sorted position (one load for the kernels that walk tiles).
+// A shared expert's rows (sh_rows > 0) are slots nslots .. ns - 1 of expert `experts`.
 //
 // Two launches over contiguous chunks of the slots, one workgroup per chunk.  The first ranks each slot among the
 // chunk's earlier slots of its expert and writes the chunk's per-expert counts; the second sums the counts of the
@@ -411,7 +411,8 @@ __global__ __launch_bounds__(GP_THREADS) void moe_gemm_place_kernel(const uint32
             t.win_rows[w] = rows;
             t.win_start[w] = sb[x] + rank;
             t.win_tile0[w] = tile0;
-            for (uint32_t i = 0; i < (rows + 15) / 16; i++) t.tile_window[tile0 + i] = w;
+            for (uint32_t i = 0; i < (rows + 15) / 16; i++)
+                t.tile_info[tile0 + i] = uint4{x, min(16u, rows - 16 * i), sb[x] + rank + 16 * i, 0u};
         }
     }
 }
