@@ -455,12 +455,15 @@ __device__ __forceinline__ void gemm4_decode_waves(R &rd, int nks, int r, int la
 
 // The MFMA waves (waves 0-7) of one workgroup's 256-row x 128-column output tile: prepared rows in fragment tiles from
 // xfrag0 (row tile rt at xfrag0 + rt * (in / 32) * 512), of which the first `rows` (<= 256) are live.  The epilogue
-// hands the raw inner products of rows m .. m + 3 to emit(m, live, v0[4], v1[4], lane) (columns lane and lane + 64 of
-// the group, m the row within the tile, the first `live` of them live); the caller applies the output transform (four
-// rows at a time) or stores the raw values.
+// hands the raw inner products of rows m .. m + 3 to emit(m, live, v0[4], v1[4], lane, rid) (columns lane and
+// lane + 64 of the group, m the row within the tile, the first `live` of them live); the caller applies the output
+// transform (four rows at a time) or stores the raw values.  With row_ids, lane l of rid holds row_ids[m0 + l] for the
+// wave's row group m0 .. m0 + 63 (loaded before the main loop, so the epilogue finds each row's id with a lane read
+// instead of a memory round trip per row); without, rid is 0.
 template <class Emit>
 __device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restrict__ xfrag0, int rows,
-                                                 uint16_t (*Bs)[128 * G2_BP], Emit emit) {
+                                                 const uint32_t *__restrict__ row_ids, uint16_t (*Bs)[128 * G2_BP],
+                                                 Emit emit) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nks = (in >> 4) / 4;  // even: in is a multiple of 128
@@ -468,6 +471,7 @@ __device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restr
     // like the decode waves' exit, an ended wave no longer counts at the barriers.
     const int m0 = (wave >> 1) * 64, cb0 = (wave & 1) * 4;
     if (m0 >= rows) return;
+    const uint32_t rid = row_ids ? row_ids[min(m0 + lane, rows - 1)] : 0u;
     const int c = lane & 15, h = lane >> 4;
     const int RT = (rows + 15) / 16;
     const uint16_t *xfrag[4];
@@ -508,7 +512,7 @@ __device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restr
                 v0[i] = ep[(r + i) * G2_EP + lane];
                 v1[i] = ep[(r + i) * G2_EP + lane + 64];
             }
-            emit(m, min(4, rows - m), v0, v1, lane);
+            emit(m, min(4, rows - m), v0, v1, lane, rid);
         }
         __syncthreads();
     }
@@ -519,8 +523,8 @@ __device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restr
 // inner products).
 template <int FAM, int N, class Emit>
 __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16_t *__restrict__ bank,
-                                           const uint16_t *__restrict__ xfrag0, int rows, const DecodeK &k,
-                                           uint16_t (*Bs)[128 * G2_BP], Emit emit) {
+                                           const uint16_t *__restrict__ xfrag0, int rows, const uint32_t *row_ids,
+                                           const DecodeK &k, uint16_t (*Bs)[128 * G2_BP], Emit emit) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (wave >= 8) {
@@ -529,7 +533,7 @@ __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16
         gemm4_decode_waves<FAM>(rd, nks, wave - 8, lane, Bs);
         return;
     }
-    gemm4_mfma_waves(in, xfrag0, rows, Bs, emit);
+    gemm4_mfma_waves(in, xfrag0, rows, row_ids, Bs, emit);
 }
 
 template <int FAM, int N>
@@ -554,8 +558,9 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
     const int lane = threadIdx.x & 63;
     const float s0 = h2f(a.svh[sv + lane]), s1 = h2f(a.svh[sv + lane + 64]);
     gemm4_tile<FAM, N>(a.in, a.out, og, a.trellis + (size_t)g * IT * OT * N, xfrag0, min(G2_MT, a.rows - mt * G2_MT),
-                       a.k, Bs,
-                       [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
+                       nullptr, a.k, Bs,
+                       [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln, uint32_t)
+                           __attribute__((always_inline)) {
                            fwht128_wave_rows<4>(v0, v1, ln);
                            for (int i = 0; i < live; i++) {
                                const size_t yo = ((size_t)g * a.rows + mt * G2_MT + m + i) * a.out + (size_t)og * 128;
@@ -917,21 +922,23 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
     const uint16_t *xfrag0 = a.xp[p] + (size_t)a.win.win_tile0[w] * (size_t)(a.in / 32) * 512;
     float *planes = a.planes[p];
-    auto emit = [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln) __attribute__((always_inline)) {
-        for (int i = 0; i < live; i++) {
-            float *row = planes + (size_t)slots[m + i] * a.out + (size_t)og * 128;
+    auto emit = [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln, uint32_t rid)
+                    __attribute__((always_inline)) {
+        for (int i = 0; i < live; i++) {  // rid: the slot of row (m & ~63) + lane
+            const uint32_t slot = (uint32_t)__builtin_amdgcn_readlane((int)rid, (m & 63) + i);
+            float *row = planes + (size_t)slot * a.out + (size_t)og * 128;
             row[ln] = v0[i];
             row[ln + 64] = v1[i];
         }
     };
     if constexpr (N > 0) {
         const uint16_t *bank = e < a.experts ? a.trellis[p] + (size_t)e * IT * OT * N : a.sh_trellis[p];
-        gemm4_tile<FAM, N>(a.in, a.out, og, bank, xfrag0, rows, a.k, Bs, emit);
+        gemm4_tile<FAM, N>(a.in, a.out, og, bank, xfrag0, rows, slots, a.k, Bs, emit);
     } else {
         const int lane = threadIdx.x & 63;
         const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         if (wave < 8) {
-            gemm4_mfma_waves(a.in, xfrag0, rows, Bs, emit);
+            gemm4_mfma_waves(a.in, xfrag0, rows, slots, Bs, emit);
             return;
         }
         const int nks = IT / 4;
