@@ -221,8 +221,8 @@ constexpr int kMoeWindowMaxExperts = 4096;
 hipError_t run_moe_windows(const uint32_t *inds, int nslots, int experts, uint32_t *win_count, uint32_t *win_expert,
                            uint32_t *win_rows, uint32_t *win_slots, hipStream_t s);
 
-// The routed GEMM arm's expert windows (moe_gemm_windows_kernel): slots sorted by expert, windows of up to
-// MOE_GEMM_WINDOW_ROWS rows of one expert, and the 16-row fragment tiles of their prepared inputs.
+// The routed GEMM arm's expert windows (moe_gemm_rank_kernel + moe_gemm_place_kernel): slots sorted by expert,
+// windows of up to MOE_GEMM_WINDOW_ROWS rows of one expert, and the 16-row fragment tiles of their prepared inputs.
 constexpr int MOE_GEMM_WINDOW_ROWS = 256;
 constexpr int kMoeGemmMaxExperts = 1024;
 struct MoeGemmWindows {
