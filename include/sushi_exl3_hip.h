@@ -157,7 +157,10 @@ typedef enum {
     EXL3_KNOB_MOE_CHAIN = 10,           /* per-slot decode chain: 1 = gate/up and down in one launch where it
                                            serves, 0 = two launches (default: one launch for 2..8 rows with a fused
                                            shared bank) */
-    EXL3_KNOB_COUNT = 11
+    EXL3_KNOB_GEMV_ROWS_PER_GROUP = 11, /* dense decode GEMV of 2..16 rows: rows per group of workgroups (the
+                                           groups share the one bank and each decodes it; the last holds the rest;
+                                           default: two groups from 5 rows on banks of <= 2048 x 2048, else whole) */
+    EXL3_KNOB_COUNT = 12
 } exl3_knob;
 int32_t exl3_set_override(int32_t knob, int32_t value, int32_t enable);
 

@@ -169,11 +169,34 @@ size_t gemm_bytes(int groups, int rows, int in, int out, int n, bool split_ok = 
     return b;
 }
 
+// The decode GEMV's row groups for one bank: the rows run as ceil(rows / r) groups of r rows over the same weights
+// (the last group holds the rest), each group decoding them -- more workgroups, each with an r-row input prologue and
+// fold.  That pays where the weights are few beside those per-row costs: from 5 rows on a bank of at most 2048 x 2048
+// (4 M weights), in two groups (r = ceil(rows / 2), at most 8).  Measured (MCG, us per call, whole against two
+// groups): 2048 x 2048 n = 32, 5 / 8 / 9 / 12 / 16 rows 6.19 / 6.67 / 8.30 / 8.57 / 9.21 against 6.03 / 6.40 / 6.57
+// (6.49 with r = 8) / 6.90 / 7.37, 3 and 4 rows 5.56 against 5.63 / 5.67; 4096 x 4096 n = 64 and 4096 x 14336
+// n = 48 slower in groups at every row count from 3 to 16 (16 rows 13.84 against 14.31, 34.85 against 37.45).
+// EXL3_KNOB_GEMV_ROWS_PER_GROUP pins r (a value of at least the rows keeps them whole).  Returns rows_total for
+// GemvArgs (0: the rows stay one group).
+int gemv_row_groups(int &groups, int &rows, int in, int out) {
+    const int pinned = knob(EXL3_KNOB_GEMV_ROWS_PER_GROUP, 0);
+    const bool small_bank = (long)in * out <= 2048L * 2048L;
+    const int r = pinned > 0 ? pinned : (small_bank && rows >= 5) ? std::min(8, (rows + 1) / 2) : rows;
+    if (groups != 1 || r >= rows) return 0;
+    const int total = rows;
+    groups = (rows + r - 1) / r;
+    rows = r;
+    return total;
+}
+
 size_t linear_ws(int groups, int rows, int in, int out, int n, bool split_ok = true) {
     if (rows <= 0) return 0;
     if (rows <= kRowsMax) {
-        GemvPlan p = plan_gemv(groups, rows, in, out);
-        return p.counters_bytes + p.partial_bytes;
+        const GemvPlan p = plan_gemv(groups, rows, in, out);
+        int g = groups, r = rows;  // the row groups' plan too (a row-major grouped output keeps the rows whole)
+        gemv_row_groups(g, r, in, out);
+        const GemvPlan q = plan_gemv(g, r, in, out);
+        return std::max(p.counters_bytes + p.partial_bytes, q.counters_bytes + q.partial_bytes);
     }
     return gemm_bytes(groups, rows, in, out, n, split_ok);
 }
@@ -210,6 +233,8 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         return fail(EXL3_ERR_WORKSPACE, "linear: workspace of %zu bytes (256-aligned) needed, got %zu", need, ws_bytes);
     char *w = static_cast<char *>(ws);
     if (rows <= kRowsMax) {
+        const int banks = groups;
+        const int rows_total = y_rows_major ? 0 : gemv_row_groups(groups, rows, in, out);
         GemvPlan p = plan_gemv(groups, rows, in, out);
         GemvArgs a{};
         a.x = x;
@@ -223,7 +248,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.svh[0] = svh;
         a.n = n;
         a.bank_of = nullptr;
-        a.bank_limit = groups;
+        a.bank_limit = banks;  // group g takes bank min(g, banks - 1): its own, or the one bank of row groups
         a.meta = nullptr;
         a.table = dec.table;
         a.k = k;
@@ -233,6 +258,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
         a.y = y;
         a.y_dtype = y_dtype;
         a.y_rows_major = y_rows_major ? 1 : 0;
+        a.rows_total = rows_total;
         a.splits = p.splits;
         a.groups = groups;
         a.nproj = 1;

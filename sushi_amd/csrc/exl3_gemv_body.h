@@ -673,7 +673,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
             red[0][r][col] = s * a.out_scale;
         }
         __syncthreads();
-        for (int r = wave; r < a.rows; r += GEMV_WAVES) finish_block(a, c, r, red[0][r][lane], red[0][r][lane + 64], lane);
+        for (int r = wave; r < c.rows; r += GEMV_WAVES) finish_block(a, c, r, red[0][r][lane], red[0][r][lane + 64], lane);
         return;
     }
 
@@ -720,14 +720,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
     if (xcd_local) {
         // This CU's L1 may hold lines of these partials from an earlier call: drop them, then read the XCD's L2.
         asm volatile("buffer_inv sc0" ::: "memory");
-        for (int r = 0; r < a.rows; r++) {
+        for (int r = 0; r < c.rows; r++) {
             float v0, v1;
             sum_planes<false>(part + (((size_t)c.g * c.S) * a.rows + r) * a.out + (size_t)c.og * 128,
                               (size_t)a.rows * a.out, c.S, lane, v0, v1);
             finish_block(a, c, r, v0, v1, lane);
         }
     } else {
-        for (int r = 0; r < a.rows; r++) {
+        for (int r = 0; r < c.rows; r++) {
             float v0, v1;
             sum_planes<true>(part + (((size_t)c.g * c.S) * a.rows + r) * a.out + (size_t)c.og * 128,
                              (size_t)a.rows * a.out, c.S, lane, v0, v1);
@@ -808,8 +808,9 @@ __device__ __forceinline__ void gemv_group(int g, const void *x, const uint16_t 
             c.wslots = a.win_slots + (size_t)c.g * MOE_WINDOW_ROWS;
         } else {
             c.xg = (int)div_by_magic((uint32_t)c.g, geo.xdiv_m) * rows;
+            if (a.rows_total) c.rows = min(rows, a.rows_total - c.xg);  // row groups: the last holds the rest
             c.slot0 = c.g;
-            c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
+            c.bank = bank_of ? (int)min(bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : min(c.g, a.bank_limit - 1);
         }
     }
     c.KS = (int)(geo.sks >> 16);
@@ -973,11 +974,12 @@ __global__ __launch_bounds__(64) void gemv_finish_kernel(GemvArgs a) {
     c.og = blockIdx.x;
     const int r = blockIdx.y % a.rows;
     c.g = blockIdx.y / a.rows;
+    if (a.rows_total && c.g * a.rows + r >= a.rows_total) return;  // the last row group's rows past the rest
     c.proj = blockIdx.z;
     const bool p1 = c.proj != 0;
     c.svh = p1 ? a.svh[1] : a.svh[0];
     const float *part = p1 ? a.partial[1] : a.partial[0];
-    c.bank = a.bank_of ? (int)min(a.bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : c.g;
+    c.bank = a.bank_of ? (int)min(a.bank_of[c.g], (uint32_t)(a.bank_limit - 1)) : min(c.g, a.bank_limit - 1);
     const int lane = threadIdx.x;
     const size_t sv = (size_t)c.bank * a.out + (size_t)c.og * 128;
     c.sv0 = h2f(c.svh[sv + lane]);

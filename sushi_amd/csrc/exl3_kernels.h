@@ -104,6 +104,7 @@ struct GemvArgs {
     void *y;
     int y_dtype;
     int y_rows_major;  // dense: group g's row r is output row r * groups + g ([rows][groups * out]), else g * rows + r
+    int rows_total;    // dense row groups of one bank: the rows of all groups (the last group holds the rest), or 0
     int splits;
     int groups;
     int nproj;

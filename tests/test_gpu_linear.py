@@ -84,6 +84,35 @@ def test_gemv_split_and_finish_arms_agree(dev, splits, separate, fold):
             assert max_abs_rel(_run(pd, xd, dec), want) < BAR
 
 
+@pytest.mark.parametrize("rows,per_group", [(6, 0), (7, 0), (8, 0), (11, 0), (13, 0), (16, 0), (16, 4), (15, 4),
+                                            (9, 2), (16, 1)])
+@pytest.mark.parametrize("splits,separate,fold", [(0, 0, 1), (4, 0, 0), (4, 1, 1)])
+@pytest.mark.parametrize("ydt", [torch.float16, torch.float32])
+def test_gemv_row_groups_against_oracle(dev, rows, per_group, splits, separate, fold, ydt):
+    """A batch of rows run as groups of rows over the one bank (the default from 6 rows, or pinned), the last group
+    holding the rest: every row against the oracle to the bar under the fold, the counters + planes finish and the
+    separate finish kernel, twice in a row (the accumulators and counters come back to zero); the rows kept whole
+    agree with it to the same bar."""
+    print(f"[gemv] row groups rows={rows} per_group={per_group} splits={splits} sep={separate} fold={fold} {ydt}",
+          flush=True)
+    p, pd, x, xd = _case(dev, 21 + rows, rows, 1024, 384, 32)
+    dec, odec = DECODES["mcg"]
+    want = _oracle(p, x, 1024, 384, 32, odec)
+    knobs = dict(gemv_splits=splits, gemv_separate_finish=separate, gemv_fold=fold)
+    if per_group:
+        knobs["gemv_rows_per_group"] = per_group
+    with exl3.arm_overrides(**knobs):
+        for _ in range(2):
+            y = exl3.linear(xd, pd, dec, out_dtype=ydt)
+            torch.cuda.synchronize()
+            assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+    with exl3.arm_overrides(gemv_rows_per_group=16, **dict(gemv_splits=splits, gemv_separate_finish=separate,
+                                                            gemv_fold=fold)):
+        whole = exl3.linear(xd, pd, dec, out_dtype=ydt)
+        torch.cuda.synchronize()
+    assert max_abs_rel(whole.float().cpu().numpy(), want) < BAR
+
+
 @pytest.mark.parametrize("fold", [1, 0])
 def test_gemv_non_finite_rows(dev, fold):
     """A row whose input holds an inf comes out non-finite in every output under both split finishes (the fold marks
