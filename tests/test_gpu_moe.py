@@ -586,6 +586,33 @@ def test_moe_gemm_arm_every_lane_rate(dev, rows, E, k, n, label, dec, odec):
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
+@pytest.mark.parametrize("routing", ["topk", "skewed"])
+def test_moe_gemm_arm_windows_past_one_ranking_pass(dev, routing):
+    """4608 tokens x top-8 + the shared expert's rows: 41472 slots, more than 64 chunks of 512 hold, so each chunk of
+    the window sort spans 1024 slots and is ranked in two passes.  Top-k routing, and a skewed one (most slots on
+    three experts, whose runs cross many chunk boundaries and fill windows of 256 rows, and several experts with no
+    slot at all): the GEMM arm's layer against the oracle to the bar."""
+    print(f"[moe gemm] two ranking passes routing={routing}", flush=True)
+    E, hidden, inter, k, rows, n = 16, 128, 128, 8, 4608, 32
+    b = synth.bank(57, "mgp", E, hidden, inter, n, norm=True)
+    sh = synth.bank(57, "mgp.shared", 1, hidden, inter, n, norm=True)
+    x = synth.normal(57, "x", (rows, hidden))
+    inds, scores = _route(57, rows, E, k)
+    if routing == "skewed":
+        r = np.arange(rows)[:, None]
+        c = np.arange(k)[None, :]
+        inds = np.where(c < 3, c, 3 + (r + c) % 5).astype(np.uint32)  # distinct per row; experts 8..15 get none
+    odec = O.decode(O.CB_MCG)
+    routed = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, scores, hidden, inter,
+                               (n, n, n), odec, threads=8)
+    shared = O.moe_swiglu_rows(x.float().numpy(), _np(sh.gate), _np(sh.up), _np(sh.down), np.zeros((rows, 1)),
+                               np.ones((rows, 1)), hidden, inter, (n, n, n), odec, threads=8)
+    want = routed.astype(np.float16).astype(np.float32) + shared.astype(np.float16).astype(np.float32)
+    y = exl3.moe_with_shared_bank(x.to(dev), _to(b, dev), _to(sh, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                                  torch.from_numpy(scores).to(dev), exl3.MCG)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
+
+
 @pytest.mark.parametrize("rows,E,k", [(64, 16, 4), (300, 8, 2)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("limit", [0, 5])
