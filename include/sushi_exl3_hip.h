@@ -123,7 +123,9 @@ typedef struct {
  * segment is the 8 tiles (k-tile row tk, output tiles 8s .. 8s + 7) of one expert's projection: segment index
  * (e * in/16 + tk) * out/128 + s lies contiguous from u32 word seg_off[index] of the projection's trellis, tiles in
  * column order, tile o at n_a halfwords when bit o of seg_k1[index] is set, else at n_b.  n_a = 16, n_b = 32 (K1 and
- * K2); codebooks MCG, 3INST and the SPEC1 / STD1 hash rows whose table has both rates (spec1-w15).  seg_k1 must be
+ * K2); codebooks MCG, 3INST and the SPEC1 / STD1 hash rows whose table has both rates (spec1-w15).  Segments may lie
+ * in any order; laying a column group's k-tile rows one after another ((e, s, tk) order, as sushi_amd's packer does)
+ * keeps each 128-byte line of the stream in the one workgroup that reads its segments.  seg_k1 must be
  * 4-byte aligned.  Word offsets are u32, so one projection's trellis spans at most 16 GiB. */
 typedef struct {
     const uint16_t *trellis[3]; /* gate, up, down */

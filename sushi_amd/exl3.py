@@ -343,8 +343,9 @@ class TiledProj:
     decodeTile's at that tile's own n (expert_exl3.zig:338-357).
 
     ``trellis`` is one flat u16 stream; segment (e, tk, s) -- the tiles (tk, 8s .. 8s + 7) of expert e -- lies
-    contiguous from u32 word ``seg_off[e, tk, s]``, tiles in column order, tile o at 16 halfwords when bit o of
-    ``seg_k1[e, tk, s]`` is set, else at 32.  suh [E, in], svh [E, out] as for a uniform bank.
+    contiguous from u32 word ``seg_off[e, tk, s]`` (the stream in (e, s, tk) order), tiles in column order, tile o at
+    16 halfwords when bit o of ``seg_k1[e, tk, s]`` is set, else at 32.  suh [E, in], svh [E, out] as for a uniform
+    bank.
     """
 
     trellis: torch.Tensor
@@ -380,19 +381,25 @@ class TiledProj:
         if tuple(codes_a.shape) != (e, it, ot, 16) or tuple(codes_b.shape) != (e, it, ot, 32):
             raise BadExl3Shape(f"codes {tuple(codes_a.shape)} / {tuple(codes_b.shape)} for tile map {(e, it, ot)}")
         dev = codes_b.device
-        kf = k1.reshape(-1).to(dev)
-        words = torch.where(kf, 8, 16).to(torch.int64)
+        # The stream holds the segments in (e, s, tk) order: a column group's k-tile rows follow one another, so the
+        # workgroup that reads them (a GEMM tile's k-steps, a GEMV split's waves) shares a 128-byte line only with
+        # itself at a segment boundary.  In (e, tk, s) order neighbouring column groups -- other workgroups, often
+        # on another XCD's L2 -- would each fetch the boundary line.
+        def by_group(t: torch.Tensor) -> torch.Tensor:  # [E, IT, OT, ...] -> (e, s, tk, o)-major rows
+            return t.reshape(e, it, ot // 8, 8, *t.shape[3:]).transpose(1, 2).reshape(e * it * ot, *t.shape[3:])
+        kg = by_group(k1.to(dev))
+        words = torch.where(kg, 8, 16).to(torch.int64)
         start = torch.cumsum(words, 0) - words
         total = int(words.sum())
         if total >= 2 ** 32:
             raise BadExl3Shape("per-tile-rate trellis past 2^32 words")
         flat = torch.zeros(2 * total, dtype=torch.int16, device=dev)
-        ia, ib = torch.nonzero(kf).squeeze(1), torch.nonzero(~kf).squeeze(1)
-        flat[(2 * start[ia])[:, None] + torch.arange(16, device=dev)] = codes_a.reshape(-1, 16)[ia]
-        flat[(2 * start[ib])[:, None] + torch.arange(32, device=dev)] = codes_b.reshape(-1, 32)[ib]
-        seg_off = _as_i32(start.reshape(e, it, ot // 8, 8)[..., 0])
+        ia, ib = torch.nonzero(kg).squeeze(1), torch.nonzero(~kg).squeeze(1)
+        flat[(2 * start[ia])[:, None] + torch.arange(16, device=dev)] = by_group(codes_a)[ia]
+        flat[(2 * start[ib])[:, None] + torch.arange(32, device=dev)] = by_group(codes_b)[ib]
+        seg_off = _as_i32(start.reshape(e, ot // 8, it, 8)[..., 0].transpose(1, 2))
         bits = torch.tensor([1 << o for o in range(8)], dtype=torch.int32, device=dev)
-        seg_k1 = (kf.reshape(e, it, ot // 8, 8).to(torch.int32) * bits).sum(-1).to(torch.uint8)
+        seg_k1 = (k1.to(dev).reshape(e, it, ot // 8, 8).to(torch.int32) * bits).sum(-1).to(torch.uint8)
         return cls(flat, seg_off.contiguous(), seg_k1.contiguous(), suh, svh)
 
 

@@ -55,11 +55,12 @@ def test_pack_layout_and_realised_rate():
     assert tr.size == int(np.where(k1, 16, 32).sum())
     assert tp.bits_per_weight() == pytest.approx(16 * tr.size / (e * it * ot * 256))
     assert 1.5 < tp.bits_per_weight() < 2.0
-    # segment masks are the map's bits; the first segment starts at word 0; each segment's words follow the last's
+    # segment masks are the map's bits; the first segment starts at word 0; in (e, s, tk) order each segment's words
+    # follow the last's, so a column group's k-tile rows are one run of the stream
     bits = (k1.reshape(e, it, ot // 8, 8) << np.arange(8)).sum(-1)
     assert (msk == bits).all()
-    seg_words = np.where(k1, 8, 16).reshape(e, it, ot // 8, 8).sum(-1).reshape(-1)
-    assert (off.reshape(-1) == np.concatenate([[0], np.cumsum(seg_words)[:-1]])).all()
+    seg_words = np.where(k1, 8, 16).reshape(e, it, ot // 8, 8).sum(-1).transpose(0, 2, 1).reshape(-1)
+    assert (off.transpose(0, 2, 1).reshape(-1) == np.concatenate([[0], np.cumsum(seg_words)[:-1]])).all()
     # a K1 tile holds the first 16 halfwords of its draw, a K2 tile all 32, at its place in the stream
     hw = 2 * int(off[1, 3, 1])
     for o in range(8):
