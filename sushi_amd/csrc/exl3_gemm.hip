@@ -263,19 +263,22 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
 // ---- the decode-once GEMM (integer and half-integer rates with a lane reader: n = 16, 24, 32, 40, 48, 64)
 //
 // A workgroup owns a 256-row x 128-column output tile (one Hadamard block wide, so the FWHT + svh finish runs in its
-// epilogue) over all of k, in k-steps of 64 (four trellis k-tiles), with the decode and the MFMAs on different waves.
-// Waves 8-11 decode: wave 8 + r decodes k-tile row r of every step (lane 8o + j: codewords 32j..32j+31 of tile o =
-// columns j and j+8 over 16 k rows, the GEMV's lane decoder) into a double-buffered LDS slab held column-major
-// (B[col][k]), its tile words loaded two steps ahead.  Waves 0-7 run the MFMAs: wave w owns rows 64 (w >> 1) .. + 63
-// and columns 64 (w & 1) .. + 63 as 4 x 4 v_mfma_f32_16x16x32_f16 tiles per 32 k, with A fragments read from the
-// prepared input in fragment order (one contiguous 1 KiB per load, half a step ahead) and all B fragments of a step
-// read from the slab before its first MFMA.  Each SIMD holds two MFMA waves and one decode wave, so the matrix core
-// has a second wave to issue from and the VALU decodes beside it.  One workgroup barrier per step hands the slab
-// over: after barrier ks + 1 the MFMA waves have finished reading slab ks & 1 and the decode waves have finished
-// writing slab (ks + 1) & 1.  Every weight is decoded once per 256-row tile.  Row groups wholly past the live rows
-// leave before the first barrier.
+// epilogue) over all of k, in super-steps of 128 k (eight trellis k-tile rows), with the decode and the MFMAs on
+// different waves.  The decoders (lane 8o + j: codewords 32j..32j+31 of tile o = columns j and j+8 over 16 k rows,
+// the GEMV's lane decoder) fill a double-buffered LDS slab held column-major (B[col][k]), their tile words loaded a
+// super-step ahead: waves 8-11, wave 8 + d decoding k-tile rows d and d + 4 of every super-step; when the live rows
+// fit in 128 (MFMA waves 4-7 would have no rows), waves 4-7 decode too and each of the eight decoders takes one row
+// (wave 8 + d row d, wave 4 + d row 4 + d), so a short window -- the common MoE window -- decodes on two waves per
+// SIMD.  Waves 0-7 run the MFMAs: wave w owns rows 64 (w >> 1) .. + 63 and columns 64 (w & 1) .. + 63 as 4 x 4
+// v_mfma_f32_16x16x32_f16 tiles per 32 k, with A fragments read from the prepared input in fragment order (one
+// contiguous 1 KiB per load, a 64-k step ahead) and each 64-k step's B fragments read from the slab before its first
+// MFMA.  One workgroup barrier per super-step hands the slab over: after barrier S + 1 the MFMA waves have finished
+// reading slab S & 1 and the decoders have finished writing slab (S + 1) & 1.  Every weight is decoded once per
+// 256-row tile.  Row groups wholly past the live rows leave before the first barrier.
 constexpr int G2_MT = 256;   // rows per workgroup
-constexpr int G2_BP = 72;    // LDS pitch (halves) of one slab column: 64 k + 8 pad (16-byte aligned rows)
+constexpr int G2_BP = 72;    // LDS pitch (halves) of one ping-pong slab column: 64 k + 8 pad (16-byte aligned rows)
+constexpr int G4_BP = 136;   // LDS pitch (halves) of one decode-wave-tile slab column: 128 k + 8 pad
+constexpr int G4_HELP_ROWS = 128;  // live rows up to which MFMA waves 4-7 decode
 constexpr int G2_EP = 129;   // epilogue staging pitch (floats)
 constexpr int G4_WAVES = 12;
 constexpr int G4_THREADS = 64 * G4_WAVES;
@@ -296,11 +299,11 @@ __device__ __forceinline__ void store_y4(void *y, int dt, size_t i, float y0, fl
 
 // The MFMA waves' main loop of the decode-wave tile over the first NRB of the wave's four 16-row blocks (the rest of
 // acc stays zero): instantiated per live-block count, so a short row group (a window of 65-85 rows leaves its second
-// one or two) neither loads A nor issues MFMAs for its empty blocks, without a branch in the loop.  1 + nks barriers,
-// as the decode waves meet.
+// one or two) neither loads A nor issues MFMAs for its empty blocks, without a branch in the loop.  nks 64-k steps,
+// two per super-step: 1 + nks / 2 barriers, as the decoders meet.
 template <int NRB>
 __device__ __forceinline__ void gemm4_mfma_loop(const uint16_t *const (&xfrag)[4], int nks, int cb0, int c, int h,
-                                                uint16_t (*Bs)[128 * G2_BP], f4_t (&acc)[4][4]) {
+                                                uint16_t (*Bs)[128 * G4_BP], f4_t (&acc)[4][4]) {
     // A fragments in two register sets, a full step apart: set X serves even steps and set Y odd ones; each set is
     // refilled for the step after next as soon as its MFMAs have issued, so a fragment has a whole step to arrive.
     uint4 AX[4][2], AY[4][2];
@@ -316,13 +319,13 @@ __device__ __forceinline__ void gemm4_mfma_loop(const uint16_t *const (&xfrag)[4
     load_a(1, AY);
     __syncthreads();  // barrier 0
     auto mstep = [&](int ks, uint4 (&A)[4][2]) __attribute__((always_inline)) {
-        const uint16_t *slab = Bs[ks & 1];
+        const uint16_t *slab = Bs[(ks >> 1) & 1] + (ks & 1) * 64;  // super-step ks / 2, its k half ks & 1
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
             uint4 bv[4];  // this half-step's B fragments (the A sets hold the registers a whole step of B would take)
 #pragma unroll
             for (int cb = 0; cb < 4; cb++)
-                bv[cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G2_BP + kb * 32 + 8 * h);
+                bv[cb] = *reinterpret_cast<const uint4 *>(slab + ((cb0 + cb) * 16 + c) * G4_BP + kb * 32 + 8 * h);
 #pragma unroll
             for (int cb = 0; cb < 4; cb++) {
                 const h8_t B8 = __builtin_bit_cast(h8_t, bv[cb]);
@@ -333,19 +336,18 @@ __device__ __forceinline__ void gemm4_mfma_loop(const uint16_t *const (&xfrag)[4
             }
         }
         load_a(ks + 2, A);
-        __syncthreads();
     };
-    for (int ks = 0; ks < nks; ks += 2) {  // nks is even
+    for (int ks = 0; ks < nks; ks += 2) {  // nks is even: one super-step
         mstep(ks, AX);
         mstep(ks + 1, AY);
+        __syncthreads();
     }
-
 }
 
-// ---- the decode waves' readers: where decode wave r finds k-tile row 4 ks + r of its output group in k-step ks (the
-// group's 8 tiles, lane 8 o + j reading chunk j of tile o), and how a lane's chunk decodes.  load(ks) is called for
-// ks = 0, 1, 2, ... in order (past the last step it re-reads the last).
-// One rate N for the bank: the row lies `kstep` halves further each step.
+// ---- the decoders' readers: where a decoder finds k-tile row rs * i + r of its output group in its i-th load (the
+// group's 8 tiles, lane 8 o + j reading chunk j of tile o; rs = 4 or 8 rows apart), and how a lane's chunk decodes.
+// load(i) is called for i = 0, 1, 2, ... in order (past the last, nks - 1, it re-reads the last).
+// One rate N for the bank: the row lies `kstep` halves further each load.
 template <int FAM, int N>
 struct RateReader {
     static constexpr int AW = LaneBits<N>::AW;
@@ -354,9 +356,9 @@ struct RateReader {
     uint32_t lane_words;
     int j, nks;
     DecodeK k;
-    __device__ __forceinline__ RateReader(const uint16_t *bank, int r, int OT, int og, int nks_, int lane,
+    __device__ __forceinline__ RateReader(const uint16_t *bank, int r, int rs, int OT, int og, int nks_, int lane,
                                           const DecodeK &k_)
-        : tb(bank + ((size_t)r * OT + og * 8) * N), kstep((size_t)4 * OT * N),
+        : tb(bank + ((size_t)r * OT + og * 8) * N), kstep((size_t)rs * OT * N),
           lane_words((uint32_t)((lane >> 3) * N) >> 1), j(lane & 7), nks(nks_), k(k_) {}
     __device__ __forceinline__ void load(int ks, uint32_t (&W)[AW]) {
         load_lane_words_u<N>(reinterpret_cast<const uint32_t *>(tb + (size_t)min(ks, nks - 1) * kstep), lane_words,
@@ -368,10 +370,10 @@ struct RateReader {
     }
 };
 
-// A per-tile-rate projection (configs[4]'s K1 / K2 mix): the row of k-step ks is segment seg0 + ks * seg_step, at the
+// A per-tile-rate projection (configs[4]'s K1 / K2 mix): the row of load i is segment seg0 + i * seg_step, at the
 // word offset and with the rate mask of the segment tables; lane 8 o + j's tile starts 16 o - 8 popcount(mask below o)
-// words in, at TILED_NA when bit o is set.  The segment's offset and mask (scalar loads) are fetched a step ahead, so
-// a tile's vector loads never wait on them.
+// words in, at TILED_NA when bit o is set.  The segment's offset and mask (scalar loads) are fetched two loads ahead,
+// so a tile's vector loads never wait on them, also where a decoder issues two loads back to back.
 template <int FAM>
 struct TiledReader {
     static constexpr int AW = 4;  // the lane's three words and its tile's rate flag
@@ -381,22 +383,23 @@ struct TiledReader {
     size_t seg0, seg_step;
     int o, j, nks;
     DecodeK ka, kb;
-    uint32_t p_off, p_m;  // offset and mask of the next step to load
+    uint32_t n_off, n_m, f_off, f_m;  // offset and mask of the next load and of the one after it
     __device__ __forceinline__ TiledReader(const uint16_t *trellis, const uint32_t *off, const uint8_t *k1, int e,
-                                           int r, int IT, int OT, int og, int nks_, int lane, const DecodeK &ka_,
-                                           const DecodeK &kb_)
+                                           int r, int rs, int IT, int OT, int og, int nks_, int lane,
+                                           const DecodeK &ka_, const DecodeK &kb_)
         : words(reinterpret_cast<const uint32_t *>(trellis)), seg_off(off), seg_k1(k1),
-          seg0(((size_t)e * IT + r) * (size_t)(OT >> 3) + og), seg_step((size_t)4 * (OT >> 3)), o(lane >> 3),
+          seg0(((size_t)e * IT + r) * (size_t)(OT >> 3) + og), seg_step((size_t)rs * (OT >> 3)), o(lane >> 3),
           j(lane & 7), nks(nks_), ka(ka_), kb(kb_) {
-        fetch(0);
+        fetch(0, n_off, n_m);
+        fetch(1, f_off, f_m);
     }
-    __device__ __forceinline__ void fetch(int ks) {
+    __device__ __forceinline__ void fetch(int ks, uint32_t &off, uint32_t &m) const {
         const size_t seg = seg0 + (size_t)min(ks, nks - 1) * seg_step;
-        p_m = seg_mask(seg_k1, seg);
-        p_off = seg_off[seg];
+        m = seg_mask(seg_k1, seg);
+        off = seg_off[seg];
     }
     __device__ __forceinline__ void load(int ks, uint32_t (&W)[AW]) {
-        const uint32_t m = p_m, off = p_off;
+        const uint32_t m = n_m, off = n_off;
         const bool k1 = ((m >> o) & 1u) != 0;
         const uint32_t lw = 16u * (uint32_t)o - 8u * (uint32_t)__builtin_popcount(m & ((1u << o) - 1u));
         uint32_t A[3];
@@ -405,7 +408,9 @@ struct TiledReader {
         W[1] = A[1];
         W[2] = A[2];
         W[3] = k1 ? 1u : 0u;
-        fetch(ks + 1);
+        n_off = f_off;
+        n_m = f_m;
+        fetch(ks + 2, f_off, f_m);
     }
     __device__ __forceinline__ void decode(const uint32_t (&W)[AW], uint32_t (&w)[16]) const {
         const uint32_t A[3] = {W[0], W[1], W[2]};
@@ -416,41 +421,53 @@ struct TiledReader {
     }
 };
 
-// The decode waves of the decode-wave tile (waves 8-11; wave 8 + r decodes k-tile row r of each k-step): two tiles in
-// flight, each step's row decoded into the slab the MFMA waves read after the step's barrier.  1 + nks barriers.
-template <int FAM, class R>
-__device__ __forceinline__ void gemm4_decode_waves(R &rd, int nks, int r, int lane, uint16_t (*Bs)[128 * G2_BP]) {
+// The decoders of the decode-wave tile, D of them (4: waves 8-11; 8: waves 8-11 and 4-7), decoder d decoding rows
+// d + 4 t (t < 8 / D) of each super-step into the slab the MFMA waves read after the super-step's barrier, the words
+// of the next super-step in flight.  The reader takes row d every 8 / D loads apart (4 rows apart for D = 4, 8 for
+// D = 8), nsup * 8 / D loads in all.  1 + nsup barriers.
+template <int FAM, int D, class R>
+__device__ __forceinline__ void gemm4_decode_waves(R &rd, int nsup, int d, int lane, uint16_t (*Bs)[128 * G4_BP]) {
+    static_assert(D == 4 || D == 8, "four or eight decoders");
+    constexpr int T = 8 / D;  // rows per decoder per super-step
     const int o = lane >> 3, j = lane & 7;
-    auto decode_store = [&](const uint32_t (&W)[R::AW], uint16_t *slab) __attribute__((always_inline)) {
+    auto decode_store = [&](const uint32_t (&W)[R::AW], uint16_t *slab, int row) __attribute__((always_inline)) {
         uint32_t w[16];
         rd.decode(W, w);
         if constexpr (family_scaled<FAM>()) {
 #pragma unroll
             for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
         }
-        uint16_t *cj = slab + (o * 16 + j) * G2_BP + r * 16;
-        uint16_t *cj8 = cj + 8 * G2_BP;
+        uint16_t *cj = slab + (o * 16 + j) * G4_BP + row * 16;
+        uint16_t *cj8 = cj + 8 * G4_BP;
         *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
         *reinterpret_cast<uint4 *>(cj + 8) = uint4{w[1], w[5], w[9], w[13]};
         *reinterpret_cast<uint4 *>(cj8) = uint4{w[2], w[6], w[10], w[14]};
         *reinterpret_cast<uint4 *>(cj8 + 8) = uint4{w[3], w[7], w[11], w[15]};
     };
-    uint32_t W0[R::AW], W1[R::AW];
-    rd.load(0, W0);
-    rd.load(1, W1);
+    uint32_t P[T][R::AW], Q[T][R::AW];
+#pragma unroll
+    for (int t = 0; t < T; t++) rd.load(t, P[t]);
+#pragma unroll
+    for (int t = 0; t < T; t++) rd.load(T + t, Q[t]);
     __builtin_amdgcn_sched_barrier(0);
-    decode_store(W0, Bs[0]);
+#pragma unroll
+    for (int t = 0; t < T; t++) decode_store(P[t], Bs[0], d + 4 * t);
     __syncthreads();  // barrier 0: slab 0 is ready
-    auto dstep = [&](int ks, const uint32_t (&Wc)[R::AW], uint32_t (&Wn)[R::AW]) __attribute__((always_inline)) {
-        rd.load(ks + 2, Wn);
+    // super-step S: the words of S + 2 into the set just decoded, S + 1's rows into slab (S + 1) & 1
+    auto sstep = [&](int S, const uint32_t (&C)[T][R::AW], uint32_t (&Nx)[T][R::AW]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < T; t++) rd.load(T * (S + 2) + t, Nx[t]);
         __builtin_amdgcn_sched_barrier(0);
-        decode_store(Wc, Bs[(ks + 1) & 1]);
+#pragma unroll
+        for (int t = 0; t < T; t++) decode_store(C[t], Bs[(S + 1) & 1], d + 4 * t);
         __syncthreads();
     };
-    for (int ks = 0; ks < nks; ks += 2) {
-        dstep(ks, W1, W0);
-        dstep(ks + 1, W0, W1);
+    int S = 0;
+    for (; S + 1 < nsup; S += 2) {
+        sstep(S, Q, P);
+        sstep(S + 1, P, Q);
     }
+    if (S < nsup) sstep(S, Q, P);
 }
 
 // The MFMA waves (waves 0-7) of one workgroup's 256-row x 128-column output tile: prepared rows in fragment tiles from
@@ -462,7 +479,7 @@ __device__ __forceinline__ void gemm4_decode_waves(R &rd, int nks, int r, int la
 // instead of a memory round trip per row); without, rid is 0.
 template <class Emit>
 __device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restrict__ xfrag0, int rows,
-                                                 const uint32_t *__restrict__ row_ids, uint16_t (*Bs)[128 * G2_BP],
+                                                 const uint32_t *__restrict__ row_ids, uint16_t (*Bs)[128 * G4_BP],
                                                  Emit emit) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -518,19 +535,41 @@ __device__ __forceinline__ void gemm4_mfma_waves(int in, const uint16_t *__restr
     }
 }
 
+// This wave's decoder index in the decode-wave tile, or -1 for an MFMA wave: waves 8-11 are decoders 0-3; with the
+// live rows within G4_HELP_ROWS, waves 4-7 (whose row groups are empty) are decoders 4-7.
+__device__ __forceinline__ int gemm4_decoder(int wave, int rows) {
+    if (wave >= 8) return wave - 8;
+    return (rows <= G4_HELP_ROWS && wave >= 4) ? wave : -1;
+}
+
+// Decoder d over the reader mk(r, rs, loads) makes (row r, rows rs apart, `loads` loads): eight decoders when `help`
+// (the live rows within G4_HELP_ROWS), else four.
+template <int FAM, class MakeReader>
+__device__ __forceinline__ void gemm4_decode_role(bool help, int d, int nsup, int lane, uint16_t (*Bs)[128 * G4_BP],
+                                                  MakeReader mk) {
+    if (help) {
+        auto rd = mk(d, 8, nsup);
+        gemm4_decode_waves<FAM, 8>(rd, nsup, d, lane, Bs);
+    } else {
+        auto rd = mk(d, 4, 2 * nsup);
+        gemm4_decode_waves<FAM, 4>(rd, nsup, d, lane, Bs);
+    }
+}
+
 // One workgroup's 256-row x 128-column output tile of output group og of a bank at one rate N whose tiles start at
-// `bank` ([in/16][out/16][N]): waves 8-11 decode, waves 0-7 multiply (gemm4_mfma_waves, whose `emit` receives the raw
-// inner products).
+// `bank` ([in/16][out/16][N]): the decoders (gemm4_decoder) decode, the other waves multiply (gemm4_mfma_waves, whose
+// `emit` receives the raw inner products).
 template <int FAM, int N, class Emit>
 __device__ __forceinline__ void gemm4_tile(int in, int out, int og, const uint16_t *__restrict__ bank,
                                            const uint16_t *__restrict__ xfrag0, int rows, const uint32_t *row_ids,
-                                           const DecodeK &k, uint16_t (*Bs)[128 * G2_BP], Emit emit) {
+                                           const DecodeK &k, uint16_t (*Bs)[128 * G4_BP], Emit emit) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (wave >= 8) {
-        const int nks = (in >> 4) / 4;
-        RateReader<FAM, N> rd(bank, wave - 8, out >> 4, og, nks, lane, k);
-        gemm4_decode_waves<FAM>(rd, nks, wave - 8, lane, Bs);
+    const int d = gemm4_decoder(wave, rows);
+    if (d >= 0) {
+        gemm4_decode_role<FAM>(rows <= G4_HELP_ROWS, d, in >> 7, lane, Bs, [&](int r, int rs, int loads) {
+            return RateReader<FAM, N>(bank, r, rs, out >> 4, og, loads, lane, k);
+        });
         return;
     }
     gemm4_mfma_waves(in, xfrag0, rows, row_ids, Bs, emit);
@@ -551,7 +590,7 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
         mt = L / nog;
     }
     const int g = blockIdx.z;
-    __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
+    __shared__ __align__(16) uint16_t Bs[2][128 * G4_BP];
     const int RT = (a.rows + 15) / 16;
     const uint16_t *xfrag0 = a.xp + ((size_t)g * RT + (size_t)mt * (G2_MT / 16)) * (size_t)(a.in / 32) * 512;
     const size_t sv = (size_t)g * a.out + (size_t)og * 128;
@@ -887,18 +926,19 @@ __device__ __forceinline__ DecodeK rate_decode(const DecodeK &base, int table, i
     return k;
 }
 
-// The decode waves at a rate known only at run time (a lane-reader rate; any other leaves the slab undecoded, which
-// the host rules out).
+// Decoder d at a rate known only at run time (a lane-reader rate; any other leaves the slab undecoded, which the
+// host rules out).
 template <int FAM>
-__device__ __forceinline__ void gemm4_decode_waves_at(int n, const uint16_t *bank, int OT, int og, int nks, int lane,
-                                                      const DecodeK &k, uint16_t (*Bs)[128 * G2_BP]) {
-    const int r = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) - 8;
+__device__ __forceinline__ void gemm4_decode_waves_at(int n, const uint16_t *bank, int OT, int og, int nsup, int d,
+                                                      bool help, int lane, const DecodeK &k,
+                                                      uint16_t (*Bs)[128 * G4_BP]) {
     switch (n) {
 #define EXL3_RATE_CASE(NN)                                                                                             \
-    case NN: {                                                                                                         \
-        RateReader<FAM, NN> rd(bank, r, OT, og, nks, lane, k);                                                          \
-        gemm4_decode_waves<FAM>(rd, nks, r, lane, Bs);                                                                  \
-    } break;
+    case NN:                                                                                                           \
+        gemm4_decode_role<FAM>(help, d, nsup, lane, Bs, [&](int r, int rs, int loads) {                                \
+            return RateReader<FAM, NN>(bank, r, rs, OT, og, loads, lane, k);                                           \
+        });                                                                                                            \
+        break;
         EXL3_RATE_CASE(16)
         EXL3_RATE_CASE(24)
         EXL3_RATE_CASE(32)
@@ -919,7 +959,7 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     const int e = moe_expert(a, a.win.win_expert[w]);
     const int rows = (int)min(a.win.win_rows[w], (uint32_t)G2_MT);
     const uint32_t *slots = a.win.sorted + a.win.win_start[w];
-    __shared__ __align__(16) uint16_t Bs[2][128 * G2_BP];
+    __shared__ __align__(16) uint16_t Bs[2][128 * G4_BP];
     const uint16_t *xfrag0 = a.xp[p] + (size_t)a.win.win_tile0[w] * (size_t)(a.in / 32) * 512;
     float *planes = a.planes[p];
     auto emit = [&](int m, int live, float (&v0)[4], float (&v1)[4], int ln, uint32_t rid)
@@ -937,25 +977,29 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
     } else {
         const int lane = threadIdx.x & 63;
         const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-        if (wave < 8) {
+        const int d = gemm4_decoder(wave, rows);
+        if (d < 0) {
             gemm4_mfma_waves(a.in, xfrag0, rows, slots, Bs, emit);
             return;
         }
-        const int nks = IT / 4;
+        const int nsup = IT / 8;
+        const bool help = rows <= G4_HELP_ROWS;
         if (e >= a.experts) {  // the shared expert: its own uniform bank
-            gemm4_decode_waves_at<FAM>(a.sh_n, a.sh_trellis[p], OT, og, nks, lane, rate_decode<FAM>(a.k, a.table, a.sh_n),
-                                       Bs);
+            gemm4_decode_waves_at<FAM>(a.sh_n, a.sh_trellis[p], OT, og, nsup, d, help, lane,
+                                       rate_decode<FAM>(a.k, a.table, a.sh_n), Bs);
             return;
         }
         if constexpr (N == N_TILED) {
-            TiledReader<FAM> rd(a.trellis[p], a.seg_off[p], a.seg_k1[p], e, wave - 8, IT, OT, og, nks, lane,
-                                rate_decode<FAM>(a.k, a.table, TILED_NA), rate_decode<FAM>(a.k, a.table, TILED_NB));
-            gemm4_decode_waves<FAM>(rd, nks, wave - 8, lane, Bs);
+            const DecodeK ka = rate_decode<FAM>(a.k, a.table, TILED_NA), kb = rate_decode<FAM>(a.k, a.table, TILED_NB);
+            gemm4_decode_role<FAM>(help, d, nsup, lane, Bs, [&](int r, int rs, int loads) {
+                return TiledReader<FAM>(a.trellis[p], a.seg_off[p], a.seg_k1[p], e, r, rs, IT, OT, og, loads, lane, ka,
+                                        kb);
+            });
         } else {
             const uint32_t *m = a.meta + (size_t)e * 8;
             const int col = a.meta_col[p];
             const int n = (int)m[col];
-            gemm4_decode_waves_at<FAM>(n, a.trellis[p] + 2 * (size_t)m[4 + col], OT, og, nks, lane,
+            gemm4_decode_waves_at<FAM>(n, a.trellis[p] + 2 * (size_t)m[4 + col], OT, og, nsup, d, help, lane,
                                        rate_decode<FAM>(a.k, a.table, n), Bs);
         }
     }
