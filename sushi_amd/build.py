@@ -44,6 +44,11 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # Leading scalar kernel arguments arrive preloaded in SGPRs (the GEMV's first loads need no argument load).
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
+    # Kernels take their argument structs by value.  The compiler reads such a struct straight from the argument
+    # segment only after walking every use of its local copy, and its default walk stops at 300 uses; the fused
+    # shared-expert windows kernels have over a thousand, and past the limit every wave copied the struct to scratch
+    # memory and read its fields from there (2.2x slower per window).
+    "-mllvm", "-instcombine-max-copied-from-constant-users=4096",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 
