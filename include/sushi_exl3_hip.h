@@ -240,7 +240,7 @@ int32_t exl3_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t
  * [E][inter/16][hidden/16][n]; each projection at its own rate (gate and up at different rates take one launch each,
  * as moeMixedDecode does, root.zig:705-722).  Arms: up to 8 rows the per-slot decode chain (pair GEMV -> fused
  * SwiGLU mid + down GEMV -> score-weighted fold or reduce); wider batches the same chain over expert windows of up to
- * 4 rows; prefill widths (from 8 slots per expert on average, every projection at one of the rates 16, 24, 32, 40,
+ * 4 rows; prefill widths (from 4 slots per expert on average, every projection at one of the rates 16, 24, 32, 40,
  * 48, 64) the routed GEMM arm on the matrix cores (`moePrefill`, expert_exl3_kernels.zig:2861-2931).
  * verify_rows != 0 marks speculative-verify rows: as the reference does (root.zig:169, `rows <= DECODE_ROWS_MAX or
  * verify_rows`), they never take the GEMM arm, so they round as decode rows do at every width. */
@@ -295,7 +295,7 @@ int32_t exl3_moe_groups(const void *x, int32_t x_dtype, int32_t rows, int32_t hi
  * routed layer's inter; clamp_limit applies to both.  Up to 8 rows the shared rows join the per-slot launches (from
  * 2 rows one launch: the down workgroups wait, bounded, on a counter their group's gate/up workgroups raise);
  * wider batches the sorted (expert-window) launches, where the shared rows are windows of their own (three launches
- * in all instead of six); at prefill widths (the routed GEMM arm, from 8 slots per expert, not under verify_rows) the
+ * in all instead of six); at prefill widths (the routed GEMM arm, from 4 slots per expert, not under verify_rows) the
  * shared expert is one more expert of the GEMM arm's launches, its rows extra slots, any y dtype, and y equals the
  * pair of calls bit for bit.  Returns EXL3_DECLINED (nothing launched) where the fused form does not serve: y dtype
  * f32 off the GEMM arm, routed projections at different rates, a shared rate other than the routed one (uniform

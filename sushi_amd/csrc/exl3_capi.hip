@@ -355,10 +355,11 @@ MoePlan plan_moe(int nslots, int hidden, int inter, bool windowed, int extra = 0
 // The routed GEMM arm (prefill widths): slots sorted by expert into windows of up to MOE_GEMM_WINDOW_ROWS rows, each
 // window's rows prepared into MFMA fragment order and run through the decode-once GEMM (each weight decoded once per
 // window instead of once per 4-row GEMV window), then the mid, the down GEMM and the reduce.  Taken when the layer
-// averages at least kMoeGemmMinSlotsPerExpert slots per expert (C4's layer, E = 256 top-8: 8 slots per expert 457 us
-// against 669 on the GEMV windows, 4 slots 423 against 394), on a bank whose decode waves have a reader: a uniform
-// bank at one lane-reader rate, a ragged bank of lane-reader rates, or a per-tile-rate bank.
-constexpr int kMoeGemmMinSlotsPerExpert = 8;
+// averages at least kMoeGemmMinSlotsPerExpert slots per expert (E = 256 top-8, per layer: C4's 4 slots per expert
+// 350 us against 392 on the GEMV windows, 2 slots 310 against 238; C5's ragged bank 1583 against 2024 and 1403
+// against 1270), on a bank whose decode waves have a reader: a uniform bank at one lane-reader rate, a ragged bank of
+// lane-reader rates, or a per-tile-rate bank.
+constexpr int kMoeGemmMinSlotsPerExpert = 4;
 
 struct MoeGemmPlan {
     int max_windows, max_tiles;
