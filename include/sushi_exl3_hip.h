@@ -162,7 +162,11 @@ typedef enum {
     EXL3_KNOB_GEMV_ROWS_PER_GROUP = 11, /* dense decode GEMV of 2..16 rows: rows per group of workgroups (the
                                            groups share the one bank and each decodes it; the last holds the rest;
                                            default: two groups from 5 rows on banks of <= 2048 x 2048, else whole) */
-    EXL3_KNOB_COUNT = 12
+    EXL3_KNOB_GEMM_SPLIT_WAIT = 12,     /* the GEMM tile with k in halves: 100 MHz ticks the first half to finish
+                                           waits for the second before handing it the whole tile (0: never waits;
+                                           default: 20 us where both halves of every tile fit on the CUs at once,
+                                           else 0) */
+    EXL3_KNOB_COUNT = 13
 } exl3_knob;
 int32_t exl3_set_override(int32_t knob, int32_t value, int32_t enable);
 

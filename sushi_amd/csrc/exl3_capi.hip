@@ -55,6 +55,7 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 constexpr size_t kFoldWords = FOLD_WORDS;
 constexpr size_t kZeroBytes = 2 * kFoldWords * sizeof(unsigned long long);
 constexpr size_t kCounterSlots = (size_t(1) << 20) / (sizeof(uint32_t) * COUNTER_STRIDE);
+constexpr int kMaxDevices = 64;  // devices with per-device state (the no-alloc scratch, the CU count)
 
 bool rate_admitted(int n) { return n >= 16 && n <= 128 && n % 2 == 0; }  // kFromPackedDim, expert_exl3.zig:241-245
 
@@ -159,6 +160,24 @@ bool gemm_uses_kpart(int groups, int rows, int out, int n, bool split_ok = true)
     const bool lane_reader = n == 16 || n == 24 || n == 32 || n == 48 || n == 64;
     return lane_reader && gemm_arm_for(groups, rows, out, split_ok) == 7 &&
            (size_t)groups * ((rows + 511) / 512) * (out / 128) <= kCounterSlots;
+}
+
+// The k-halves tile's wait (100 MHz ticks): the first half of a tile to finish its main loop waits for the second and
+// then each finishes half the rows; past the wait it hands the whole tile over (the second then finishes every row,
+// as the tile did before the halves shared the finish).  Waiting pays only where every tile's second half is running
+// beside it: 20 us when all the launch's workgroups fit on the device's CUs at one each, else no wait.
+uint32_t gemm_split_wait(long workgroups) {
+    const int pinned = knob(EXL3_KNOB_GEMM_SPLIT_WAIT, -1);
+    if (pinned >= 0) return (uint32_t)pinned;
+    static std::atomic<int> cus[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return workgroups <= n ? 2000u : 0u;
 }
 
 size_t gemm_bytes(int groups, int rows, int in, int out, int n, bool split_ok = true) {
@@ -296,6 +315,7 @@ int32_t linear_impl(const void *x, int32_t x_dtype, int32_t groups, int32_t rows
     if (gemm_uses_kpart(groups, rows, out, n, split_ok)) {
         g.kpart = reinterpret_cast<float *>(w + kZeroBytes + gemm_xp_bytes(groups, rows, in));
         g.kctr = reinterpret_cast<uint32_t *>(w);
+        g.kwait = gemm_split_wait(2L * groups * ((rows + 511) / 512) * (out / 128));
     }
     return launched(run_gemm(fam, g, stream), "exl3_linear (gemm)");
 }
@@ -819,7 +839,6 @@ int32_t moe_launch(int fam, const DecodeK &k, const exl3_decode_t &dec, int tabl
 // first call clears them with the fill kernel, and every call leaves them at zero again.
 constexpr size_t kNoallocScratchBytes = EXL3_NOALLOC_SCRATCH_BYTES;
 static_assert(kNoallocScratchBytes > kZeroBytes, "the static scratch holds the zeroed region and more");
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_at[kMaxDevices] = {};
 

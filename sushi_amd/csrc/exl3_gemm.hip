@@ -623,9 +623,10 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
 // Every weight is decoded once per MT rows (twice per 1024 rows at MT = 512, against four times for the 256-row tile).
 //
 // KS = 2 splits k in halves over twice the workgroups (a grid of few 512-row tiles then fills the chip and still
-// decodes every weight once per 512 rows).  Each half writes its raw accumulators through to memory, then arrives at
-// the tile's counter; the last arriver adds the other half's (a sum of two, so independent of which came first),
-// clears the counter and runs the epilogue.
+// decodes every weight once per 512 rows).  Each half finishes half of every wave's rows: it writes the raw
+// accumulators of the other half's rows through to memory, arrives at the tile's counter, adds the other half's
+// partial of its own rows (a sum of two, so independent of which came first) and runs their epilogue.  The first to
+// arrive waits, bounded, for the second; past the wait it hands the whole tile over.
 constexpr int G5_WAVES = 8;
 constexpr int G5_THREADS = 64 * G5_WAVES;
 constexpr int G5_SLAB = 128 * G2_BP;                                        // halves per slab
@@ -789,8 +790,16 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
     }
     __syncthreads();  // the H = 1 waves' last decode (none: s + 3 >= nks) and every slab read are behind this
 
+    // Row blocks this workgroup finishes: all of them, or with k in halves the half's own (set below).
+    bool fin_lo = true, fin_hi = true;  // row blocks 0 .. RB/2 - 1 and RB/2 .. RB - 1 of every wave
     if constexpr (KS == 2) {
-        // partial of split ks: [tile][ks][wave][rb][cb] blocks of 64 lanes x 4 floats, one 1 KiB store each
+        // partial of split ks: [tile][ks][wave][rb][cb] blocks of 64 lanes x 4 floats, one 1 KiB store each.  Half ks
+        // finishes row blocks RB/2 ks .. RB/2 ks + RB/2 - 1 of every wave: it writes the partner's row blocks of its
+        // partial, arrives, and adds the partner's partial of its own.  The first to arrive waits (at most a.kwait
+        // ticks) for the second; past the wait it writes its own row blocks too and hands the whole tile over, and
+        // the second finishes every row.  Each output is the same sum of two either way.
+        static_assert(RB % 2 == 0, "halves of the row blocks");
+        constexpr int RH = RB / 2;
         const size_t tile = ((size_t)g * nm + mt) * nog + og;
         const size_t wave_f = (size_t)RB * 8 * 256;  // floats per wave
         float *mine = a.kpart + ((tile * 2 + ks) * G5_WAVES + wave) * wave_f;
@@ -800,26 +809,69 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
             __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(other), (short)0, (int)(wave_f * 4), 0x00020000);
         // sc0 sc1: the stores go through to memory and the loads bypass the caches (the halves may sit on two XCDs)
         constexpr int SYS = 1 | 16;
+        auto store_rows = [&](int half) __attribute__((always_inline)) {
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
+            for (int rb = 0; rb < RB; rb++)
+                if (rb / RH == half) {
 #pragma unroll
-            for (int cb = 0; cb < 8; cb++)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[rb][cb]), mr, a_lane,
-                                                       (rb * 8 + cb) * 1024, SYS);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // acknowledged before the arrival below
+                    for (int cb = 0; cb < 8; cb++)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[rb][cb]), mr, a_lane,
+                                                               (rb * 8 + cb) * 1024, SYS);
+                }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // acknowledged before the counter moves
+        };
+        constexpr uint32_t HANDED = 0x40000000u;  // the first half gave its whole tile to the second
+        store_rows(ks ^ 1);
         __syncthreads();
         __shared__ uint32_t arrived;
         uint32_t *ctr = a.kctr + tile * COUNTER_STRIDE;
         if (tid == 0) arrived = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
-        if (arrived == 0) return;  // the other half finishes the tile
-        if (tid == 0) *ctr = 0u;   // no workgroup of this launch touches it again; the next launch reads it after the boundary
+        const uint32_t st = arrived;
+        __syncthreads();  // every wave has read `arrived` before wave 0 reuses it
+        bool all = false;
+        if (st == 0) {
+            // first: wave 0 polls for the second's arrival, at most kwait ticks, so the wait always ends
+            if (tid == 0) {
+                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                while (v < 2u && __builtin_amdgcn_s_memrealtime() - t0 < (uint64_t)a.kwait) {
+                    __builtin_amdgcn_s_sleep(2);
+                    v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                arrived = v;
+            }
+            __syncthreads();
+            if (arrived < 2u) {
+                // the second has not arrived: write this half's own row blocks, then hand the tile over unless the
+                // second arrived meanwhile (then it has written this half's rows and finishes its own as usual)
+                store_rows(ks);
+                __syncthreads();
+                if (tid == 0) {
+                    uint32_t expect = 1u;
+                    __hip_atomic_compare_exchange_strong(ctr, &expect, HANDED, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    arrived = expect;  // 1: handed over; 2: the second arrived first
+                }
+                __syncthreads();
+                if (arrived == 1u) return;
+            }
+            if (tid == 0) *ctr = 0u;  // both arrived and the second never reads it again; the next launch reads it
+                                      // after the kernel boundary
+        } else if (st >= HANDED) {
+            all = true;  // the first handed over the whole tile
+            if (tid == 0) *ctr = 0u;
+        }
+        fin_lo = all || ks == 0;
+        fin_hi = all || ks == 1;
 #pragma unroll
         for (int rb = 0; rb < RB; rb++)
+            if (rb < RH ? fin_lo : fin_hi) {
 #pragma unroll
-            for (int cb = 0; cb < 8; cb++) {
-                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(orr, a_lane, (rb * 8 + cb) * 1024, SYS);
-                acc[rb][cb] += __builtin_bit_cast(f4_t, v);
+                for (int cb = 0; cb < 8; cb++) {
+                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(orr, a_lane, (rb * 8 + cb) * 1024, SYS);
+                    acc[rb][cb] += __builtin_bit_cast(f4_t, v);
+                }
             }
     }
 
@@ -840,6 +892,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
     uint16_t *stage = reinterpret_cast<uint16_t *>(lds) + wave * 16 * G5_SP;
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
+        if (!(rb < RB / 2 ? fin_lo : fin_hi)) continue;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float v[8];

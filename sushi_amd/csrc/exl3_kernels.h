@@ -309,6 +309,7 @@ struct GemmArgs {
                       // 7 = ping-pong 512 with k in halves
     float *kpart;     // arm 7: workspace for the halves' partials (gemm_kpart_bytes), or null
     uint32_t *kctr;   // arm 7: one zeroed counter per tile (COUNTER_STRIDE words apart), left at zero
+    uint32_t kwait;   // arm 7: 100 MHz ticks the first half to arrive waits for the other before handing it the tile
 };
 // The row-count policy for arm 0 (the C-ABI layer applies it and sizes arm 7's region accordingly).
 inline int gemm_default_arm(int groups, int rows, int out) {

@@ -534,7 +534,7 @@ def _f16_check(t: torch.Tensor, what: str) -> None:
 
 KNOBS = {"gemv_splits": 0, "gemv_separate_finish": 1, "gemv_fold": 2, "moe_decode_rows_max": 3, "moe_splits1": 4,
          "moe_splits2": 5, "moe_windows": 6, "moe_fold": 7, "moe_gemm": 8, "gemm_arm": 9, "moe_chain": 10,
-         "gemv_rows_per_group": 11}
+         "gemv_rows_per_group": 11, "gemm_split_wait": 12}
 
 
 @contextlib.contextmanager

@@ -320,6 +320,28 @@ def test_gemm_ksplit_repeats_and_groups(dev):
         assert why is None, f"ksplit group {b}: {why}"
 
 
+def test_gemm_ksplit_shared_finish_and_handover_agree(dev):
+    """Arm 7 finishes a tile one of two ways: each half finishes its own rows after a bounded wait for the other, or
+    the first half to arrive hands the whole tile to the second (a zero wait forces that).  Both give the same outputs
+    bit for bit (every output is the same sum of two), call after call, and hold the bar; a row tile with a short
+    tail (640 rows: 512 + 128) is included."""
+    print("[ksplit finish] rows=640 in=1024 out=768 n=48", flush=True)
+    d = Dense(dev, 743, 640, 1024, 768, 48)
+    dec, odec = DECODES["3inst"]
+    outs = {}
+    for wait in (None, 0, 1_000_000):  # the library's choice, never wait, wait up to 10 ms
+        knobs = {"gemm_arm": 7} if wait is None else {"gemm_arm": 7, "gemm_split_wait": wait}
+        with exl3.arm_overrides(**knobs):
+            ys = [exl3.linear(d.xd, d.pd, dec, out_dtype=torch.float32) for _ in range(3)]
+        torch.cuda.synchronize()
+        assert all(torch.equal(y, ys[0]) for y in ys[1:]), f"wait {wait}: repeated calls differ"
+        outs[wait] = ys[0]
+    assert torch.equal(outs[0], outs[None]) and torch.equal(outs[1_000_000], outs[None])
+    with exl3.arm_overrides(gemm_arm=7, gemm_split_wait=0):
+        got = d.inner(dec)
+    _hold(got, d, odec, seed=12, what="ksplit handover")
+
+
 @pytest.mark.parametrize("arm", [4, 5, 6, 7])
 def test_gemm_16bit_outputs_round_the_f32_outputs(dev, arm):
     """The GEMM bodies round each f32 output once to y's 16-bit dtype (the ping-pong tile stages 16-bit rows through
