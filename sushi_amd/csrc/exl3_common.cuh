@@ -364,6 +364,116 @@ __device__ __forceinline__ void fwht128_wave_rows(float (&v0)[R], float (&v1)[R]
     for (int i = 0; i < R; i++) fwht_stage<1>(v0[i], v1[i], s1);
 }
 
+// ---- fwht128_wave_rows in about half the VALU instructions, each result bit-identical (the same butterfly pairs,
+// stage order and roundings), left at another place in the wave and possibly negated.
+// * Bits 5 and 4: one v_permlane{32,16}_swap of (v0, v1) puts both values of each pair in one lane, lower first,
+//   and the stage is v0 + v1, v0 - v1 in place (instead of two copies, two swaps and two FMAs per row).  The slot
+//   then stands for the bit just done.
+// * Bits 3..0: the partner comes through DPP inside the FMA, own + sign * partner (v_fmac_f32_dpp; the mov_dpp and
+//   the FMA do not fuse when the compiler is left to it).  On the lane whose bit is set that is own - partner, the
+//   butterfly's result negated; rounding to nearest is odd-symmetric, so the value is exact up to that sign, and the
+//   partners of every later stage carry the same sign (they agree on all bits done before).
+// On return lane l's slot s holds fwht_relaid_sign(l) * y[fwht_relaid_col(l, s)].  Needs the whole wave active.
+__device__ __forceinline__ int fwht_relaid_col(int lane, int slot) {
+    return (lane & 15) | (slot << 4) | ((lane & 48) << 1);
+}
+__device__ __forceinline__ float fwht_relaid_sign(int lane) {
+    return (__builtin_popcount(lane & 15) & 1) ? -1.f : 1.f;
+}
+
+template <int H>
+__device__ __forceinline__ void permlane_swap_pair(float &a, float &b) {
+    const unsigned ua = __builtin_bit_cast(unsigned, a), ub = __builtin_bit_cast(unsigned, b);
+    if constexpr (H == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+        a = __builtin_bit_cast(float, (unsigned)r[0]);
+        b = __builtin_bit_cast(float, (unsigned)r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+        a = __builtin_bit_cast(float, (unsigned)r[0]);
+        b = __builtin_bit_cast(float, (unsigned)r[1]);
+    }
+}
+
+// a..d += sign * (their value on lane ^ H), H in {1, 2, 4, 8} (the stage of fwht_stage<H> with own and partner
+// exchanged).  The leading s_nop covers the VALU write -> DPP read hazard of the first instruction; the others read
+// registers written at least two instructions earlier.  H = 4 is a half-row mirror into temporaries, then a quad
+// reversal inside the FMA (7 - (l ^ 3) = l ^ 4 within 8 lanes).
+#define EXL3_FMAC_DPP(d, s, g, ctl) "v_fmac_f32_dpp %" #d ", %" #s ", %" #g " " ctl " row_mask:0xf bank_mask:0xf\n\t"
+#define EXL3_FMAC_DPP4(ctl)                                                                                     \
+    "s_nop 1\n\t" EXL3_FMAC_DPP(0, 0, 4, ctl) EXL3_FMAC_DPP(1, 1, 4, ctl) EXL3_FMAC_DPP(2, 2, 4, ctl)             \
+        EXL3_FMAC_DPP(3, 3, 4, ctl)
+template <int H>
+__device__ __forceinline__ void fmac_dpp4(float &a, float &b, float &c, float &d, float sign) {
+    if constexpr (H == 4) {
+        float t0, t1, t2, t3;
+        asm("s_nop 1\n\t"
+            "v_mov_b32_dpp %4, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %5, %1 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %6, %2 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %7, %3 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            EXL3_FMAC_DPP(0, 4, 8, "quad_perm:[3,2,1,0]") EXL3_FMAC_DPP(1, 5, 8, "quad_perm:[3,2,1,0]")
+            EXL3_FMAC_DPP(2, 6, 8, "quad_perm:[3,2,1,0]") EXL3_FMAC_DPP(3, 7, 8, "quad_perm:[3,2,1,0]")
+            : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+            : "v"(sign));
+    } else if constexpr (H == 1) {
+        asm(EXL3_FMAC_DPP4("quad_perm:[1,0,3,2]") : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "v"(sign));
+    } else if constexpr (H == 2) {
+        asm(EXL3_FMAC_DPP4("quad_perm:[2,3,0,1]") : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "v"(sign));
+    } else {
+        static_assert(H == 8, "a lane bit of a 16-lane row");
+        asm(EXL3_FMAC_DPP4("row_ror:8") : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "v"(sign));
+    }
+}
+#undef EXL3_FMAC_DPP4
+#undef EXL3_FMAC_DPP
+
+// IN_RELAID: the input already stands where fwht_relaid_col puts a result (an elementwise function of an earlier
+// relaid transform); a third swap keeps the stage order 6, 5, 4, and the results land at fwht_relaid2_col instead.
+template <int R, bool IN_RELAID = false>
+__device__ __forceinline__ void fwht128_wave_rows_relaid(float (&v0)[R], float (&v1)[R], int lane) {
+    static_assert(R % 2 == 0, "rows in pairs");
+    auto butterfly = [&](int i) {
+        const float a = v0[i], b = v1[i];
+        v0[i] = a + b;
+        v1[i] = a - b;
+    };
+    if constexpr (IN_RELAID) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            permlane_swap_pair<32>(v0[i], v1[i]);
+            butterfly(i);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < R; i++) butterfly(i);
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        permlane_swap_pair<IN_RELAID ? 16 : 32>(v0[i], v1[i]);
+        butterfly(i);
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        permlane_swap_pair<IN_RELAID ? 32 : 16>(v0[i], v1[i]);
+        butterfly(i);
+    }
+    const float s8 = lane_sign<8>(lane), s4 = lane_sign<4>(lane), s2 = lane_sign<2>(lane), s1 = lane_sign<1>(lane);
+#pragma unroll
+    for (int i = 0; i < R; i += 2) fmac_dpp4<8>(v0[i], v1[i], v0[i + 1], v1[i + 1], s8);
+#pragma unroll
+    for (int i = 0; i < R; i += 2) fmac_dpp4<4>(v0[i], v1[i], v0[i + 1], v1[i + 1], s4);
+#pragma unroll
+    for (int i = 0; i < R; i += 2) fmac_dpp4<2>(v0[i], v1[i], v0[i + 1], v1[i + 1], s2);
+#pragma unroll
+    for (int i = 0; i < R; i += 2) fmac_dpp4<1>(v0[i], v1[i], v0[i + 1], v1[i + 1], s1);
+}
+
+// Where fwht128_wave_rows_relaid<R, true> leaves y[j]: slot for bit 4, lane bit 5 for bit 5, lane bit 4 for bit 6.
+__device__ __forceinline__ int fwht_relaid2_col(int lane, int slot) {
+    return (lane & 15) | (slot << 4) | (lane & 32) | ((lane & 16) << 2);
+}
+
 constexpr float HAD_SCALE = 0.08838834764831845f;
 
 // Sum over s = 0..S-1 (in that order) of the f32 planes p + s * stride at (lane, lane + 64).  Loads go out eight

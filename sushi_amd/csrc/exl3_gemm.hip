@@ -85,12 +85,14 @@ __global__ __launch_bounds__(256) void gemm_prepare_frag_kernel(GemmArgs a) {
     if (a.x_dtype == DT_F16) prepare_rows4<DT_F16>(a, g, b, m0, lane, u0, u1, v0, v1);
     else if (a.x_dtype == DT_BF16) prepare_rows4<DT_BF16>(a, g, b, m0, lane, u0, u1, v0, v1);
     else prepare_rows4<DT_F32>(a, g, b, m0, lane, u0, u1, v0, v1);
-    fwht128_wave_rows<4>(v0, v1, lane);  // rows past the end transform zeros to zeros
+    fwht128_wave_rows_relaid<4>(v0, v1, lane);  // rows past the end transform zeros to zeros
+    const float sc = fwht_relaid_sign(lane) * HAD_SCALE;
+    const int c0 = fwht_relaid_col(lane, 0), c1 = fwht_relaid_col(lane, 1);
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) {
         const int r = wave * 4 + rr;
-        t[r][lane] = __half_as_ushort(__float2half_rn(v0[rr] * HAD_SCALE));
-        t[r][lane + 64] = __half_as_ushort(__float2half_rn(v1[rr] * HAD_SCALE));
+        t[r][c0] = __half_as_ushort(__float2half_rn(v0[rr] * sc));
+        t[r][c1] = __half_as_ushort(__float2half_rn(v1[rr] * sc));
     }
     __syncthreads();
     const int kq = tid >> 6, c = lane & 15, h = lane >> 4;  // 32-k block kq of this 128-block, fragment lane (c, h)
@@ -1087,13 +1089,13 @@ __device__ __forceinline__ void tile_to_frag(const uint16_t (*tl)[128 + 8], uint
     *reinterpret_cast<uint4 *>(xp + ((size_t)t * (in / 32) + (size_t)b * 4 + kq) * 512 + (size_t)lane * 8) = v;
 }
 
-// prepareInput (expert_exl3.zig:490-501) of each row's token with its expert's suh, for each of the nproj projections
-// (gate and up) from one load of the rows, over NB consecutive 128-column blocks of one tile: a wave's four rows of
-// every block load together (one round of loads for the workgroup's share, behind the tile's one table load), then
-// each block's transforms run for both projections at once.  (A workgroup per projection gathered each token
-// row from memory once per projection: 95 us at 2048 tokens.)
-template <int NB>
-__global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a, int nproj) {
+// prepareInput (expert_exl3.zig:490-501) of each row's token with its expert's suh, for gate and up from one load of
+// the rows, over NB consecutive 128-column blocks of one tile.  Every load is in bounds (a row past the tile's end
+// reads the tile's last live row and is zeroed after), so a wave's four rows of every block go out together with the
+// suh loads, behind only the tile's table and slot reads; the transforms then run for both projections at once.
+// (A workgroup per projection gathered each token row from memory once per projection: 95 us at 2048 tokens.)
+template <int NB, int DT>
+__global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a) {
     const int b0 = blockIdx.x * NB, t = blockIdx.y;
     const TileRows tr = tile_rows(a, t);
     if (!tr.live) return;
@@ -1101,54 +1103,61 @@ __global__ __launch_bounds__(256) void moe_gemm_prepare_kernel(MoeGemmArgs a, in
     __shared__ __align__(16) uint16_t tl[NB][2][16][128 + 8];
     const bool shx = tr.e >= a.experts;
     const size_t se = shx ? 0 : (size_t)tr.e * a.in;
+    uint32_t sl[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) sl[rr] = tr.slots[min(wave * 4 + rr, max(tr.rows - 1, 0))];
+    size_t xr[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) xr[rr] = (size_t)moe_token(a, __builtin_amdgcn_readfirstlane(sl[rr])) * a.in;
     float x0[NB][4], x1[NB][4], u0[NB][2], u1[NB][2];
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-        const int r = wave * 4 + rr;
-        const bool live = r < tr.rows;
-        const size_t xr = live ? (size_t)moe_token(a, tr.slots[r]) * a.in : 0;
+    for (int rr = 0; rr < 4; rr++)
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
-            const size_t xi = xr + (size_t)(b0 + nb) * 128;
-            x0[nb][rr] = live ? f16r(load_any(a.x, a.x_dtype, xi + lane)) : 0.f;
-            x1[nb][rr] = live ? f16r(load_any(a.x, a.x_dtype, xi + lane + 64)) : 0.f;
+            const size_t xi = xr[rr] + (size_t)(b0 + nb) * 128;
+            x0[nb][rr] = load_act<DT>(a.x, xi + lane);
+            x1[nb][rr] = load_act<DT>(a.x, xi + lane + 64);
         }
-    }
 #pragma unroll
     for (int q = 0; q < 2; q++) {
-        const bool on = q < nproj;
         const uint16_t *su = shx ? a.sh_suh[q] : a.suh[q];
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
             const size_t si = se + (size_t)(b0 + nb) * 128;
-            u0[nb][q] = on ? h2f(su[si + lane]) : 0.f;
-            u1[nb][q] = on ? h2f(su[si + lane + 64]) : 0.f;
+            u0[nb][q] = h2f(su[si + lane]);
+            u1[nb][q] = h2f(su[si + lane + 64]);
         }
     }
+    const float sc = fwht_relaid_sign(lane) * HAD_SCALE;
+    const int c0 = fwht_relaid_col(lane, 0), c1 = fwht_relaid_col(lane, 1);
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-        float v0[8], v1[8];  // [projection][row]; rows past the end stay zeros
+        float v0[8], v1[8];  // [projection][row]; rows past the end are zeros
 #pragma unroll
-        for (int q = 0; q < 2; q++)
+        for (int rr = 0; rr < 4; rr++) {
+            const bool live = wave * 4 + rr < tr.rows;
+            const float y0 = live ? f16r(x0[nb][rr]) : 0.f, y1 = live ? f16r(x1[nb][rr]) : 0.f;
 #pragma unroll
-            for (int rr = 0; rr < 4; rr++) {
-                v0[q * 4 + rr] = x0[nb][rr] * u0[nb][q];
-                v1[q * 4 + rr] = x1[nb][rr] * u1[nb][q];
+            for (int q = 0; q < 2; q++) {
+                v0[q * 4 + rr] = y0 * u0[nb][q];
+                v1[q * 4 + rr] = y1 * u1[nb][q];
             }
-        fwht128_wave_rows<8>(v0, v1, lane);
+        }
+        fwht128_wave_rows_relaid<8>(v0, v1, lane);
 #pragma unroll
         for (int q = 0; q < 2; q++)
 #pragma unroll
             for (int rr = 0; rr < 4; rr++) {
                 const int r = wave * 4 + rr;
-                tl[nb][q][r][lane] = __half_as_ushort(__float2half_rn(v0[q * 4 + rr] * HAD_SCALE));
-                tl[nb][q][r][lane + 64] = __half_as_ushort(__float2half_rn(v1[q * 4 + rr] * HAD_SCALE));
+                tl[nb][q][r][c0] = __half_as_ushort(__float2half_rn(v0[q * 4 + rr] * sc));
+                tl[nb][q][r][c1] = __half_as_ushort(__float2half_rn(v1[q * 4 + rr] * sc));
             }
     }
     __syncthreads();
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
-        for (int q = 0; q < nproj; q++) tile_to_frag(tl[nb][q], a.xp[q], t, b0 + nb, a.in, tid);
+#pragma unroll
+        for (int q = 0; q < 2; q++) tile_to_frag(tl[nb][q], a.xp[q], t, b0 + nb, a.in, tid);
 }
 
 // The SwiGLU mid of the routed GEMM arm (DOWN_FUSED_SOURCE's prologue, expert_exl3_kernels.zig:1838-1925; the
@@ -1164,30 +1173,38 @@ __global__ __launch_bounds__(256) void moe_gemm_mid_kernel(MoeGemmArgs a) {
     const size_t si = (shx ? 0 : (size_t)tr.e * a.in) + (size_t)b * 128;
     const uint16_t *svg = shx ? a.sh_mid_svh[0] : a.mid_svh[0], *svu = shx ? a.sh_mid_svh[1] : a.mid_svh[1];
     const uint16_t *sud = shx ? a.sh_down_suh : a.down_suh;
-    const float sg0 = h2f(svg[si + lane]), sg1 = h2f(svg[si + lane + 64]);
-    const float su0 = h2f(svu[si + lane]), su1 = h2f(svu[si + lane + 64]);
-    const float sd0 = h2f(sud[si + lane]), sd1 = h2f(sud[si + lane + 64]);
-    // the wave's four rows load together (both planes), then each transform runs over all of them at once
-    float g0[4], g1[4], q0[4], q1[4];
+    // the gate / up transforms leave column fwht_relaid_col(lane, s) in slot s, so the scales are read there
+    const int c0 = fwht_relaid_col(lane, 0), c1 = fwht_relaid_col(lane, 1);
+    const float sg0 = h2f(svg[si + c0]), sg1 = h2f(svg[si + c1]);
+    const float su0 = h2f(svu[si + c0]), su1 = h2f(svu[si + c1]);
+    const float sd0 = h2f(sud[si + c0]), sd1 = h2f(sud[si + c1]);
+    // the wave's four rows, both planes, all loads in bounds and out together (a row past the tile's end reads the
+    // last live row and is zeroed after)
+    uint32_t sl[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) sl[rr] = tr.slots[min(wave * 4 + rr, max(tr.rows - 1, 0))];
+    float w0[8], w1[8];  // [gate rows 0..3, up rows 0..3]
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) {
-        const int r = wave * 4 + rr;
-        g0[rr] = g1[rr] = q0[rr] = q1[rr] = 0.f;
-        if (r < tr.rows) {
-            const size_t pi = (size_t)tr.slots[r] * a.in + (size_t)b * 128;
-            g0[rr] = a.mid_planes[0][pi + lane];
-            g1[rr] = a.mid_planes[0][pi + lane + 64];
-            q0[rr] = a.mid_planes[1][pi + lane];
-            q1[rr] = a.mid_planes[1][pi + lane + 64];
-        }
+        const size_t pi = (size_t)__builtin_amdgcn_readfirstlane(sl[rr]) * a.in + (size_t)b * 128;
+        w0[rr] = a.mid_planes[0][pi + lane];
+        w1[rr] = a.mid_planes[0][pi + lane + 64];
+        w0[4 + rr] = a.mid_planes[1][pi + lane];
+        w1[4 + rr] = a.mid_planes[1][pi + lane + 64];
     }
-    fwht128_wave_rows<4>(g0, g1, lane);
-    fwht128_wave_rows<4>(q0, q1, lane);
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++)
+        if (wave * 4 + rr >= tr.rows) w0[rr] = w1[rr] = w0[4 + rr] = w1[4 + rr] = 0.f;
+    fwht128_wave_rows_relaid<8>(w0, w1, lane);
+    // the transforms' sign folded into the scales (exact: both factors change sign)
+    const float sgn = fwht_relaid_sign(lane);
+    const float kg0 = sgn * (HAD_SCALE * sg0), kg1 = sgn * (HAD_SCALE * sg1);
+    const float ku0 = sgn * (HAD_SCALE * su0), ku1 = sgn * (HAD_SCALE * su1);
     float v0[4], v1[4];
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) {
-        float a0 = g0[rr] * (HAD_SCALE * sg0), a1 = g1[rr] * (HAD_SCALE * sg1);
-        float b0 = q0[rr] * (HAD_SCALE * su0), b1 = q1[rr] * (HAD_SCALE * su1);
+        float a0 = w0[rr] * kg0, a1 = w1[rr] * kg1;
+        float b0 = w0[4 + rr] * ku0, b1 = w1[4 + rr] * ku1;
         if (a.clamp_limit > 0.f) {
             a0 = fminf(a0, a.clamp_limit);
             a1 = fminf(a1, a.clamp_limit);
@@ -1197,28 +1214,37 @@ __global__ __launch_bounds__(256) void moe_gemm_mid_kernel(MoeGemmArgs a) {
         v0[rr] = silu(a0) * b0 * sd0;
         v1[rr] = silu(a1) * b1 * sd1;
     }
-    fwht128_wave_rows<4>(v0, v1, lane);  // rows past the end: silu(0) * 0 = 0, zeros stay zeros
+    fwht128_wave_rows_relaid<4, true>(v0, v1, lane);  // rows past the end: silu(0) * 0 = 0, zeros stay zeros
+    const float sc = sgn * HAD_SCALE;
+    const int d0 = fwht_relaid2_col(lane, 0), d1 = fwht_relaid2_col(lane, 1);
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) {
         const int r = wave * 4 + rr;
-        tl[r][lane] = __half_as_ushort(__float2half_rn(v0[rr] * HAD_SCALE));
-        tl[r][lane + 64] = __half_as_ushort(__float2half_rn(v1[rr] * HAD_SCALE));
+        tl[r][d0] = __half_as_ushort(__float2half_rn(v0[rr] * sc));
+        tl[r][d1] = __half_as_ushort(__float2half_rn(v1[rr] * sc));
     }
     __syncthreads();
     tile_to_frag(tl, a.xp[0], t, b, a.in, tid);
 }
 
-hipError_t run_moe_gemm_prepare(const MoeGemmArgs &a, int nproj, hipStream_t s) {
-    if (nproj < 1 || nproj > 2) return hipErrorInvalidValue;
+template <int DT>
+static void launch_moe_gemm_prepare(const MoeGemmArgs &a, hipStream_t s) {
     // two 128-column blocks a workgroup where they pair up (measured at 2048 tokens of configs[3]: 85 -> 79 us; four
     // blocks took 110)
     const int blocks = a.in / 128;
     if (blocks % 2 == 0)
-        hipLaunchKernelGGL(moe_gemm_prepare_kernel<2>, dim3((unsigned)(blocks / 2), (unsigned)a.max_tiles), dim3(256),
-                           0, s, a, nproj);
+        hipLaunchKernelGGL((moe_gemm_prepare_kernel<2, DT>), dim3((unsigned)(blocks / 2), (unsigned)a.max_tiles),
+                           dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(moe_gemm_prepare_kernel<1>, dim3((unsigned)blocks, (unsigned)a.max_tiles), dim3(256), 0, s,
-                           a, nproj);
+        hipLaunchKernelGGL((moe_gemm_prepare_kernel<1, DT>), dim3((unsigned)blocks, (unsigned)a.max_tiles), dim3(256),
+                           0, s, a);
+}
+
+hipError_t run_moe_gemm_prepare(const MoeGemmArgs &a, int nproj, hipStream_t s) {
+    if (nproj != 2) return hipErrorInvalidValue;  // gate and up together
+    if (a.x_dtype == DT_F16) launch_moe_gemm_prepare<DT_F16>(a, s);
+    else if (a.x_dtype == DT_BF16) launch_moe_gemm_prepare<DT_BF16>(a, s);
+    else launch_moe_gemm_prepare<DT_F32>(a, s);
     return hipGetLastError();
 }
 

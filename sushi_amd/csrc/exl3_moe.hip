@@ -83,55 +83,72 @@ __device__ __forceinline__ float round_to(int dt, float v) {
 // each reading 4 KiB; a ninth wave for a shared expert's term ran slower than eight waves taking nine items.)  RB = 4
 // where that still leaves at least 1024 workgroups, else 1 (a decode batch of 32 rows would get 128).
 constexpr int RW = 8;
-template <int RB>
+template <int RB, int SDT>
 __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
     const int row = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = min(RB, a.hidden / 128 - (int)blockIdx.x * RB);  // this workgroup's blocks
     const size_t base = (size_t)blockIdx.x * RB * 128;
     extern __shared__ float contrib[];  // [topk (+ 1: a shared expert's term)][RB * 128]
-    for (int kk = wave; kk < a.topk; kk += RW) {
+    // RB even: the relaid transform (fewer instructions, same roundings), so svh is read and each result stored at the
+    // column the lane then holds; its sign folds into the scale (exact)
+    constexpr bool RELAID = RB % 2 == 0;
+    const int c0 = RELAID ? fwht_relaid_col(lane, 0) : lane, c1 = RELAID ? fwht_relaid_col(lane, 1) : lane + 64;
+    const float hs = RELAID ? fwht_relaid_sign(lane) * HAD_SCALE : HAD_SCALE;
+    // The shared expert's term (a one-expert layer's slot: score 1, its own planes of one split): block b on wave
+    // (topk + b) % RW, continuing the slots' round robin (as a whole ninth item it doubled one wave's work: 78 us at
+    // 2048 rows), so at most one block per wave.  Its loads go out ahead of the slots' (a wave without a block reads
+    // an in-bounds address it then ignores): loaded after its wave's slot item, it cost a second memory round trip.
+    static_assert(RB <= RW, "one shared block per wave");
+    const int bsh = ((wave - a.topk) % RW + RW) % RW;
+    const bool has_sh = a.sh_part != nullptr && bsh < nb;
+    const float *shp = has_sh ? a.sh_part + (size_t)row * a.hidden + base + bsh * 128 : a.part;
+    const uint16_t *shv = has_sh ? a.sh_svh + base + bsh * 128 : a.svh;
+    const float sh0 = 0.f + shp[lane], sh1 = 0.f + shp[lane + 64];
+    const float shs0 = h2f(shv[lane]), shs1 = h2f(shv[lane + 64]);
+    // one slot item per wave when topk <= RW, peeled off the loop: the loop's back edge made the first item's plane
+    // loads wait for every load before them, the shared term's included
+    auto item = [&](int kk) __attribute__((always_inline)) {
         const int slot = row * a.topk + kk;
-        const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
-        const float sc = load_any(a.scores, a.score_dtype, slot);
-        const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
         const float *pl = a.part + (size_t)slot * a.splits * a.hidden + base;
-        float v0[RB], v1[RB];
+        // every load in bounds (a block past this workgroup's last reads its last); the planes first, as they need
+        // only the slot: the svh loads wait on the slot's expert id and are needed only after the transform
+        float v0[RB], v1[RB], s0[RB], s1[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
-            v0[b] = v1[b] = 0.f;
-            if (b < nb) {
-                if (a.splits == 1) {  // sum_planes' sum of one plane (0 + x), without its eight-split batch of loads
-                    v0[b] += pl[b * 128 + lane];
-                    v1[b] += pl[b * 128 + lane + 64];
-                } else {
-                    sum_planes<false>(pl + b * 128, a.hidden, a.splits, lane, v0[b], v1[b]);
-                }
+            const int bb = min(b, nb - 1);
+            if (a.splits == 1) {  // sum_planes' sum of one plane (0 + x), without its eight-split batch of loads
+                v0[b] = 0.f + pl[bb * 128 + lane];
+                v1[b] = 0.f + pl[bb * 128 + lane + 64];
+            } else {
+                sum_planes<false>(pl + bb * 128, a.hidden, a.splits, lane, v0[b], v1[b]);
             }
         }
-        fwht128_wave_rows<RB>(v0, v1, lane);
+        const int e = (int)min(a.slots[slot], (uint32_t)(a.bank_limit - 1));
+        const float sc = load_act<SDT>(a.scores, slot);  // one load, no dtype branch to wait at
+        const uint16_t *sv = a.svh + (size_t)e * a.hidden + base;
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            const int bb = min(b, nb - 1);
+            s0[b] = h2f(sv[bb * 128 + c0]);
+            s1[b] = h2f(sv[bb * 128 + c1]);
+        }
+        if constexpr (RELAID) fwht128_wave_rows_relaid<RB>(v0, v1, lane);
+        else fwht128_wave_rows<RB>(v0, v1, lane);
 #pragma unroll
         for (int b = 0; b < RB; b++)
             if (b < nb) {
-                const float s0 = h2f(sv[b * 128 + lane]), s1 = h2f(sv[b * 128 + lane + 64]);
-                contrib[kk * RB * 128 + b * 128 + lane] = (v0[b] * HAD_SCALE * s0) * sc;
-                contrib[kk * RB * 128 + b * 128 + lane + 64] = (v1[b] * HAD_SCALE * s1) * sc;
+                contrib[kk * RB * 128 + b * 128 + c0] = (v0[b] * hs * s0[b]) * sc;
+                contrib[kk * RB * 128 + b * 128 + c1] = (v1[b] * hs * s1[b]) * sc;
             }
-    }
-    if (a.sh_part) {
-        // the shared expert's term (a one-expert layer's slot: score 1, its own planes of one split), one block per
-        // wave continuing the slots' round robin: as a whole ninth item it doubled one wave's work (78 us at 2048 rows)
-        for (int b = 0; b < nb; b++) {
-            if ((a.topk + b) % RW != wave) continue;
-            const float *pl = a.sh_part + (size_t)row * a.hidden + base + b * 128;
-            float v0 = 0.f, v1 = 0.f;
-            v0 += pl[lane];
-            v1 += pl[lane + 64];
-            fwht128_wave(v0, v1, lane);
-            const float s0 = h2f(a.sh_svh[base + b * 128 + lane]), s1 = h2f(a.sh_svh[base + b * 128 + lane + 64]);
-            contrib[a.topk * RB * 128 + b * 128 + lane] = (v0 * HAD_SCALE * s0) * 1.0f;
-            contrib[a.topk * RB * 128 + b * 128 + lane + 64] = (v1 * HAD_SCALE * s1) * 1.0f;
-        }
+    };
+    if (wave < a.topk) item(wave);
+    for (int kk = wave + RW; kk < a.topk; kk += RW) item(kk);
+    if (has_sh) {
+        float v0 = sh0, v1 = sh1;
+        fwht128_wave(v0, v1, lane);
+        contrib[a.topk * RB * 128 + bsh * 128 + lane] = (v0 * HAD_SCALE * shs0) * 1.0f;
+        contrib[a.topk * RB * 128 + bsh * 128 + lane + 64] = (v1 * HAD_SCALE * shs1) * 1.0f;
     }
     __syncthreads();
     const float g = a.shared && a.gate ? load_any(a.gate, a.y_dtype, row) : 0.f;
@@ -151,16 +168,22 @@ __global__ __launch_bounds__(64 * RW) void moe_reduce_kernel(ReduceArgs a) {
     }
 }
 
+template <int RB>
+static void launch_moe_reduce(const ReduceArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+    const dim3 block(64 * RW);
+    if (a.score_dtype == DT_F16) hipLaunchKernelGGL((moe_reduce_kernel<RB, DT_F16>), grid, block, lds, s, a);
+    else if (a.score_dtype == DT_BF16) hipLaunchKernelGGL((moe_reduce_kernel<RB, DT_BF16>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((moe_reduce_kernel<RB, DT_F32>), grid, block, lds, s, a);
+}
+
 hipError_t run_moe_reduce(const ReduceArgs &a, hipStream_t s) {
     if (a.topk > kMoeReduceMaxTopk) return hipErrorInvalidValue;
     const int items = a.topk + (a.sh_part ? 1 : 0), blocks = a.hidden / 128;
-    if ((long)a.rows * ((blocks + 3) / 4) >= 1024) {
-        hipLaunchKernelGGL(moe_reduce_kernel<4>, dim3((unsigned)((blocks + 3) / 4), (unsigned)a.rows), dim3(64 * RW),
-                           (size_t)items * 4 * 128 * sizeof(float), s, a);
-    } else {
-        hipLaunchKernelGGL(moe_reduce_kernel<1>, dim3((unsigned)blocks, (unsigned)a.rows), dim3(64 * RW),
-                           (size_t)items * 128 * sizeof(float), s, a);
-    }
+    if ((long)a.rows * ((blocks + 3) / 4) >= 1024)
+        launch_moe_reduce<4>(a, dim3((unsigned)((blocks + 3) / 4), (unsigned)a.rows),
+                             (size_t)items * 4 * 128 * sizeof(float), s);
+    else
+        launch_moe_reduce<1>(a, dim3((unsigned)blocks, (unsigned)a.rows), (size_t)items * 128 * sizeof(float), s);
     return hipGetLastError();
 }
 
