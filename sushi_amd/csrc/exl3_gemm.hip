@@ -49,56 +49,66 @@ __global__ __launch_bounds__(64) void gemm_prepare_kernel(GemmArgs a) {
 // ---- prepare into MFMA A-fragment order: for 16-row tile rt and 32-k block kb of group g, the 1 KiB at
 // xp[((g * RT + rt) * (in / 32) + kb) * 512] holds lane l = 16h + c's fragment (row 16 rt + c, k = 32 kb + 8h .. +7)
 // at l * 8 halves, so one MFMA wave's load of a fragment is one contiguous 1 KiB.  RT = ceil(rows / 16); rows past
-// the end of the last tile are zeros.  A workgroup (4 waves) prepares 16 rows x one 128-block: each wave loads its 4
-// rows at once and runs their FWHTs together into an LDS tile, then every thread writes one 16-byte fragment.
-template <int DT>
-__device__ __forceinline__ void prepare_rows4(const GemmArgs &a, int g, int b, int m0, int lane, float u0, float u1,
-                                              float (&v0)[4], float (&v1)[4]) {
-    // the four rows' loads go out together (a loop that loads, transforms and then loads the next row would wait
-    // out one memory round trip per row)
-#pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-        const int m = m0 + rr;
-        v0[rr] = v1[rr] = 0.f;
-        if (m < a.rows) {
-            const size_t xi = ((size_t)g * a.rows + m) * a.in + (size_t)b * 128;
-            v0[rr] = load_act<DT>(a.x, xi + lane);
-            v1[rr] = load_act<DT>(a.x, xi + lane + 64);
-        }
-    }
-#pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-        v0[rr] = (DT == DT_F16 ? v0[rr] : f16r(v0[rr])) * u0;
-        v1[rr] = (DT == DT_F16 ? v1[rr] : f16r(v1[rr])) * u1;
-    }
-}
-
+// the end of the last tile are zeros.  A workgroup (4 waves) prepares 16 rows x NB 128-blocks (two where they pair
+// up): each wave loads its 4 rows of every block at once and runs their FWHTs together into an LDS tile, then every
+// thread writes one 16-byte fragment per block.
+template <int DT, int NB>
 __global__ __launch_bounds__(256) void gemm_prepare_frag_kernel(GemmArgs a) {
-    const int b = blockIdx.x, rt = blockIdx.y, g = blockIdx.z;
+    const int b0 = blockIdx.x * NB, rt = blockIdx.y, g = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int RT = (a.rows + 15) / 16;
-    __shared__ __align__(16) uint16_t t[16][128 + 8];
-    const size_t si = (size_t)g * a.in + (size_t)b * 128;
-    const float u0 = h2f(a.suh[si + lane]), u1 = h2f(a.suh[si + lane + 64]);
+    __shared__ __align__(16) uint16_t t[NB][16][128 + 8];
     const int m0 = rt * 16 + wave * 4;
-    float v0[4], v1[4];
-    if (a.x_dtype == DT_F16) prepare_rows4<DT_F16>(a, g, b, m0, lane, u0, u1, v0, v1);
-    else if (a.x_dtype == DT_BF16) prepare_rows4<DT_BF16>(a, g, b, m0, lane, u0, u1, v0, v1);
-    else prepare_rows4<DT_F32>(a, g, b, m0, lane, u0, u1, v0, v1);
-    fwht128_wave_rows_relaid<4>(v0, v1, lane);  // rows past the end transform zeros to zeros
+    // every load in bounds (a row past the end reads the last row and is zeroed after), so a wave's four rows of
+    // every block go out together with suh, with no branch to wait at
+    float v0[NB][4], v1[NB][4], u0[NB], u1[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const size_t si = (size_t)g * a.in + (size_t)(b0 + nb) * 128;
+        u0[nb] = h2f(a.suh[si + lane]);
+        u1[nb] = h2f(a.suh[si + lane + 64]);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const size_t xi = ((size_t)g * a.rows + min(m0 + rr, a.rows - 1)) * a.in + (size_t)(b0 + nb) * 128;
+            v0[nb][rr] = load_act<DT>(a.x, xi + lane);
+            v1[nb][rr] = load_act<DT>(a.x, xi + lane + 64);
+        }
+    }
     const float sc = fwht_relaid_sign(lane) * HAD_SCALE;
     const int c0 = fwht_relaid_col(lane, 0), c1 = fwht_relaid_col(lane, 1);
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-        const int r = wave * 4 + rr;
-        t[r][c0] = __half_as_ushort(__float2half_rn(v0[rr] * sc));
-        t[r][c1] = __half_as_ushort(__float2half_rn(v1[rr] * sc));
+    for (int nb = 0; nb < NB; nb++) {
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const bool live = m0 + rr < a.rows;
+            v0[nb][rr] = live ? f16r(v0[nb][rr]) * u0[nb] : 0.f;
+            v1[nb][rr] = live ? f16r(v1[nb][rr]) * u1[nb] : 0.f;
+        }
+        fwht128_wave_rows_relaid<4>(v0[nb], v1[nb], lane);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const int r = wave * 4 + rr;
+            t[nb][r][c0] = __half_as_ushort(__float2half_rn(v0[nb][rr] * sc));
+            t[nb][r][c1] = __half_as_ushort(__float2half_rn(v1[nb][rr] * sc));
+        }
     }
     __syncthreads();
-    const int kq = tid >> 6, c = lane & 15, h = lane >> 4;  // 32-k block kq of this 128-block, fragment lane (c, h)
-    const uint4 v = *reinterpret_cast<const uint4 *>(&t[c][kq * 32 + 8 * h]);
-    const size_t kb = (size_t)b * 4 + kq;
-    *reinterpret_cast<uint4 *>(a.xp + (((size_t)g * RT + rt) * (a.in / 32) + kb) * 512 + (size_t)lane * 8) = v;
+    const int kq = tid >> 6, c = lane & 15, h = lane >> 4;  // 32-k block kq of a 128-block, fragment lane (c, h)
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(&t[nb][c][kq * 32 + 8 * h]);
+        const size_t kb = (size_t)(b0 + nb) * 4 + kq;
+        *reinterpret_cast<uint4 *>(a.xp + (((size_t)g * RT + rt) * (a.in / 32) + kb) * 512 + (size_t)lane * 8) = v;
+    }
+}
+
+template <int DT>
+static void launch_gemm_prepare_frag(const GemmArgs &a, hipStream_t s) {
+    const int blocks = a.in / 128;
+    const dim3 grid2((unsigned)(blocks / 2), (unsigned)((a.rows + 15) / 16), (unsigned)a.groups);
+    const dim3 grid1((unsigned)blocks, (unsigned)((a.rows + 15) / 16), (unsigned)a.groups);
+    if (blocks % 2 == 0) hipLaunchKernelGGL((gemm_prepare_frag_kernel<DT, 2>), grid2, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((gemm_prepare_frag_kernel<DT, 1>), grid1, dim3(256), 0, s, a);
 }
 
 // ---- dense fallback: tiles decoded to wt[g][out][in] f16 (transposed, so a B fragment is 16 contiguous bytes)
@@ -1290,8 +1300,9 @@ hipError_t run_moe_gemm(int fam, const MoeGemmArgs &a, int nproj, hipStream_t s)
 
 template <int FAM, int N>
 static hipError_t launch_gemm_lane_n(const GemmArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(gemm_prepare_frag_kernel, dim3((unsigned)(a.in / 128), (unsigned)((a.rows + 15) / 16),
-                                                      (unsigned)a.groups), dim3(256), 0, s, a);
+    if (a.x_dtype == DT_F16) launch_gemm_prepare_frag<DT_F16>(a, s);
+    else if (a.x_dtype == DT_BF16) launch_gemm_prepare_frag<DT_BF16>(a, s);
+    else launch_gemm_prepare_frag<DT_F32>(a, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // The ping-pong body once its 512-row tiles still give most CUs a workgroup (measured at C3's 4096 x 14336: 768 to
