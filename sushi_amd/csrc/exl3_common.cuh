@@ -87,6 +87,13 @@ template <int FAM>
 __device__ __forceinline__ constexpr bool family_scaled() {
     return FAM == FAM_HASH || FAM == FAM_PAIR;
 }
+// The factor from a family's decoded values to its weights.  The matrix cores take the decoded values as they are
+// (f16 subnormals included: v_mfma_f32_4x4x4_16b_f16 and v_mfma_f32_16x16x32_f16 multiply them exactly, checked
+// against exact sums on gfx950), and the finish applies this power of two to the f32 sums, exactly.
+template <int FAM>
+__device__ __forceinline__ constexpr float codebook_scale() {
+    return family_scaled<FAM>() ? 4096.0f : 1.0f;
+}
 
 // Weights (t, t+1) of a tile as packed f16 (lo = t, hi = t+1), from their codewords (c0 for t, c1 for t+1, t even).
 // Unscaled for hash/pair families.
@@ -174,16 +181,6 @@ template <int FAM>
 __device__ __forceinline__ uint32_t hash_halves(uint32_t p, const DecodeK &k) {
     if constexpr (FAM == FAM_HASH) return p & k.mask0;
     else return (p & 0x8FFF8FFFu) ^ 0x3B603B60u;
-}
-
-// Packed f16 (lo = h0.lo + h0.hi, hi = h1.lo + h1.hi): two SDWA adds, the second writing the high half in place.
-__device__ __forceinline__ uint32_t pack_sums(uint32_t h0, uint32_t h1) {
-    uint32_t w;
-    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
-        : "=v"(w) : "v"(h0));
-    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-        : "+v"(w) : "v"(h1));
-    return w;
 }
 
 // ------------------------------------------------------------------------------------------------------------

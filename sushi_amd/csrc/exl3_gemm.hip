@@ -205,10 +205,6 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
                     }
                     B[cb][q] = decode_pair_h2<FAM>(cw[0], cw[1], k);
                 }
-                if constexpr (family_scaled<FAM>()) {  // MFMA takes the weight itself: fold the 2^12 back in (exact)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) B[cb][q] = scale_h2_4096(B[cb][q]);
-                }
             } else {
                 const uint4 v = *reinterpret_cast<const uint4 *>(
                     wt + ((size_t)g * a.out + (size_t)o * 16 + c) * a.in + (size_t)tk * 16 + 8 * half);
@@ -216,10 +212,6 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
                 B[cb][1] = v.y;
                 B[cb][2] = v.z;
                 B[cb][3] = v.w;
-                if constexpr (family_scaled<FAM>()) {
-#pragma unroll
-                    for (int q = 0; q < 4; q++) B[cb][q] = scale_h2_4096(B[cb][q]);
-                }
             }
         }
         __syncthreads();
@@ -256,8 +248,8 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(GemmArgs a, const uint
             float v0 = outs[r][lane], v1 = outs[r][lane + 64];
             fwht128_wave(v0, v1, lane);
             const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128;
-            const float y0 = v0 * HAD_SCALE * h2f(a.svh[sv + lane]);
-            const float y1 = v1 * HAD_SCALE * h2f(a.svh[sv + lane + 64]);
+            const float y0 = v0 * codebook_scale<FAM>() * HAD_SCALE * h2f(a.svh[sv + lane]);
+            const float y1 = v1 * codebook_scale<FAM>() * HAD_SCALE * h2f(a.svh[sv + lane + 64]);
             if (a.y_dtype == DT_F16) {
                 store_act<DT_F16>(a.y, yo + lane, y0);
                 store_act<DT_F16>(a.y, yo + lane + 64, y1);
@@ -445,10 +437,6 @@ __device__ __forceinline__ void gemm4_decode_waves(R &rd, int nsup, int d, int l
     auto decode_store = [&](const uint32_t (&W)[R::AW], uint16_t *slab, int row) __attribute__((always_inline)) {
         uint32_t w[16];
         rd.decode(W, w);
-        if constexpr (family_scaled<FAM>()) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
-        }
         uint16_t *cj = slab + (o * 16 + j) * G4_BP + row * 16;
         uint16_t *cj8 = cj + 8 * G4_BP;
         *reinterpret_cast<uint4 *>(cj) = uint4{w[0], w[4], w[8], w[12]};
@@ -615,7 +603,8 @@ __global__ __launch_bounds__(G4_THREADS) void gemm4_kernel(GemmArgs a) {
                            fwht128_wave_rows<4>(v0, v1, ln);
                            for (int i = 0; i < live; i++) {
                                const size_t yo = ((size_t)g * a.rows + mt * G2_MT + m + i) * a.out + (size_t)og * 128;
-                               store_y4(a.y, a.y_dtype, yo + ln, v0[i] * HAD_SCALE * s0, v1[i] * HAD_SCALE * s1);
+                               store_y4(a.y, a.y_dtype, yo + ln, v0[i] * codebook_scale<FAM>() * HAD_SCALE * s0,
+                                        v1[i] * codebook_scale<FAM>() * HAD_SCALE * s1);
                            }
                        });
 }
@@ -698,10 +687,6 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
         } else {
             if (masked) decode_weights_half<FAM, N, true, 0>(W, k, w);
             else decode_weights_half<FAM, N, false, 0>(W, k, w);
-        }
-        if constexpr (family_scaled<FAM>()) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) w[i] = scale_h2_4096(w[i]);
         }
         uint16_t *dst = slabs + (size_t)(s % 3) * G5_SLAB + col * G2_BP + r * 16;
         *reinterpret_cast<uint4 *>(dst) = uint4{w[0], w[2], w[4], w[6]};
@@ -933,7 +918,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
                     const size_t yo = ((size_t)g * a.rows + m) * a.out + (size_t)og * 128 + c;
 #pragma unroll
                     for (int cb = 0; cb < 8; cb++) {
-                        const float y = v[cb] * HAD_SCALE * svc[cb];
+                        const float y = v[cb] * codebook_scale<FAM>() * HAD_SCALE * svc[cb];
                         if (a.y_dtype == DT_F16) store_act<DT_F16>(a.y, yo + cb * 16, y);
                         else if (bf16) store_act<DT_BF16>(a.y, yo + cb * 16, y);
                         else store_act<DT_F32>(a.y, yo + cb * 16, y);
@@ -944,7 +929,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void gemm5_kernel(GemmArgs a) {
                 for (int cb = 0; cb < 8; cb++) {
                     // y is rounded to f32 first, as every other output path rounds it (the empty asm keeps the
                     // product from fusing into the 16-bit conversion, which would round once and differ at ties)
-                    float y = v[cb] * HAD_SCALE * svc[cb];
+                    float y = v[cb] * codebook_scale<FAM>() * HAD_SCALE * svc[cb];
                     asm("" : "+v"(y));
                     stage[(4 * h + i) * G5_SP + cb * 16 + c] =
                         bf16 ? __bfloat16_as_ushort(__float2bfloat16(y)) : __half_as_ushort(__float2half_rn(y));
@@ -1032,8 +1017,8 @@ __global__ __launch_bounds__(G4_THREADS) void moe_gemm4_kernel(MoeGemmArgs a) {
         for (int i = 0; i < live; i++) {  // rid: the slot of row (m & ~63) + lane
             const uint32_t slot = (uint32_t)__builtin_amdgcn_readlane((int)rid, (m & 63) + i);
             float *row = planes + (size_t)slot * a.out + (size_t)og * 128;
-            row[ln] = v0[i];
-            row[ln + 64] = v1[i];
+            row[ln] = v0[i] * codebook_scale<FAM>();
+            row[ln + 64] = v1[i] * codebook_scale<FAM>();
         }
     };
     if constexpr (N > 0) {

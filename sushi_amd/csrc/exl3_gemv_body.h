@@ -159,15 +159,6 @@ __device__ __forceinline__ void mfma_dot(const uint32_t (&w)[16], const uint16_t
     }
 }
 
-// Matrix instructions take the hash / pair weights times 2^12 (the caller takes it back out of the sums, exactly).
-template <int FAM>
-__device__ __forceinline__ void scale_for_mfma(uint32_t (&w)[16]) {
-    if constexpr (family_scaled<FAM>()) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) w[i] = scale_h2_4096(w[i]);
-    }
-}
-
 // The 32 weights of one tile chunk (lane-owned columns j and j+8) against every batch row, on the matrix cores.
 // Lane 8o + j is lane 4b + i of block b = 2o + j/4 with i = j % 4: its decoded pairs of column j over k rows 4s..4s+3
 // (pairs (0, 4), (8, 12), (1, 5), (9, 13) for s = 0..3; column j + 8: (2, 6), (10, 14), (3, 7), (11, 15)) are the B
@@ -181,7 +172,6 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&A)[LaneBits<N>::AW]
     const XFrag f0 = read_xfrag(xs, min(i4, RT - 1), kk);
     uint32_t w[16];
     decode_weights<FAM, N, MASKED>(A, k, w);
-    scale_for_mfma<FAM>(w);
     mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4, f0);
 }
 
@@ -193,7 +183,6 @@ __device__ __forceinline__ void decode_tile_tiled(const uint32_t (&A)[3], bool k
     const XFrag f0 = read_xfrag(xs, min(i4, RT - 1), kk);
     uint32_t w[16];
     decode_weights_tiled<FAM, MASKED>(A, k1, k, w);
-    scale_for_mfma<FAM>(w);
     mfma_dot<RT>(w, xs, kk, rows, accA, accB, i4, f0);
 }
 
@@ -639,17 +628,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &a, GemvCtx &c, const u
                 const int t = 32 * j + 2 * i;
                 w[i] = decode_pair_h2<FAM>(codeword_at(words, n, t), codeword_at(words, n, t + 1), k);
             }
-            scale_for_mfma<FAM>(w);
             mfma_dot<RT>(w, xs, kk, c.rows, accA, accB, lane & 3, read_xfrag(xs, min(lane & 3, RT - 1), kk));
         }
     }
-    // the hash / pair weights went in times 2^12; out_scale applies the codebook scale to every arm alike
-    constexpr float unscale = family_scaled<FAM>() ? 1.0f / 4096.0f : 1.0f;
+    // the matrix cores take the hash / pair weights as decoded, the codebook's values over 4096 (f16 subnormals
+    // among them, which they multiply exactly); out_scale applies the 4096 to every arm alike
     float acc0[RT], acc1[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-        acc0[r] = accA[r >> 2][r & 3] * unscale;
-        acc1[r] = accB[r >> 2][r & 3] * unscale;
+        acc0[r] = accA[r >> 2][r & 3];
+        acc1[r] = accB[r >> 2][r & 3];
     }
 
     // ---- cross-wave reduction

@@ -21,8 +21,8 @@ struct Pairing {
 // A scheduling fence: nothing moves across it, so each phase below stays one batch of independent instructions.
 __device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// A pair of hash / pair family weights times 2^12 (exact: they are the codebook values over 4096).  Matrix
-// instructions take these scaled, since the unscaled values include f16 subnormals.
+// A pair of hash / pair family weights times 2^12 (exact: they are the codebook values over 4096), as the
+// reconstruction returns them.  The matrix cores take them unscaled (codebook_scale).
 __device__ __forceinline__ uint32_t scale_h2_4096(uint32_t v) {
     __half2 h = __builtin_bit_cast(__half2, v);
     h = __hmul2(h, __half2(__float2half(4096.0f), __float2half(4096.0f)));
@@ -61,8 +61,20 @@ __device__ __forceinline__ void decode_weights(const uint32_t (&A)[LaneBits<N>::
                 h0[i] = pr[i] & k.mask0;
                 h1[i] = __builtin_amdgcn_alignbit(pr[i], pr[i], 32u - k.rot) & k.mask1;
             }
+            // the sums in two fenced phases, as the hash-product families write theirs below: each is an SDWA write
+            // in inline asm, whose readers need wait states the compiler does not count for asm (an MFMA reading
+            // one two instructions later read stale weights); phased, a sum is read no sooner than the next phase
+            phase_fence();
 #pragma unroll
-            for (int i = 0; i < 16; i++) w[i] = pack_sums(h0[i], h1[i]);
+            for (int i = 0; i < 16; i++)
+                asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+                    : "=v"(w[i]) : "v"(h0[i]));
+            phase_fence();
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+                    : "+v"(w[i]) : "v"(h1[i]));
+            phase_fence();
         } else {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
