@@ -58,9 +58,10 @@ __global__ void reconstruct_inner_kernel(const uint16_t *__restrict__ trellis, i
 
 // Lane-reader rates: one wave per 8 consecutive tiles of the pack order, lane 8o + j reading chunk j of tile o with
 // load_lane_words_u (the wave-uniform start of the 8 tiles plus the lane's tile offset, as the GEMV and the GEMM
-// address a k-tile row of an output group) and decoding it with decode_weights, hash / pair weights times 4096 as
-// the matrix cores take them.  Pair i = 4qq + p of the lane holds rows 2qq + 8(p & 1) + {0, 1} of column j (p < 2)
-// or j + 8 (p >= 2).  A tail wave's lanes past the last tile re-read it and store nothing.
+// address a k-tile row of an output group) and decoding it with decode_weights, hash / pair values then times 4096
+// (the weights themselves; the matrix cores take the values unscaled and their finishes apply the 4096).  Pair
+// i = 4qq + p of the lane holds rows 2qq + 8(p & 1) + {0, 1} of column j (p < 2) or j + 8 (p >= 2).  A tail wave's
+// lanes past the last tile re-read it and store nothing.
 constexpr int RL_WAVES = 4;
 template <int FAM, int N, bool MASKED>
 __global__ __launch_bounds__(64 * RL_WAVES) void reconstruct_lane_kernel(const uint16_t *__restrict__ trellis,

@@ -137,7 +137,7 @@ __device__ __forceinline__ XFrag read_xfrag(const uint16_t (*xs)[XS_PITCH], int 
     const uint16_t *xg = &xs[row][kk * 16];
     return XFrag{*reinterpret_cast<const uint4 *>(xg), *reinterpret_cast<const uint4 *>(xg + 8)};
 }
-// The lane's 16 decoded pairs (w, already scaled for the matrix cores) against every batch row of k-tile kk; f0 is
+// The lane's 16 decoded pairs (w, as decoded: hash / pair values over 4096) against every batch row of k-tile kk; f0 is
 // row group 0's fragment, the others are read here.
 template <int RT>
 __device__ __forceinline__ void mfma_dot(const uint32_t (&w)[16], const uint16_t (*xs)[XS_PITCH], int kk, int rows,
