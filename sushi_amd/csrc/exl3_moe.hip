@@ -458,11 +458,14 @@ hipError_t run_moe_gemm_windows(const uint32_t *inds, int nslots, int experts, i
     return hipGetLastError();
 }
 
-// One workgroup (256 threads) per row: k rounds of a block-wide argmax (ties to the lower index), then the softmax
-// mass of the picks over the full row, renormalised.  Selection keys are the logits with NaN read as -inf, and a
-// per-row mask keeps each expert from being picked twice: every round starts from the lowest unpicked index as its
-// candidate, so with k <= experts (checked by the host) each pick is a distinct index in [0, experts) whatever the
-// logits hold.  A NaN logit still reaches the softmax, so such a row's scores come out NaN, as the chain's do.
+// One wave per row (four rows a workgroup): lane l holds experts l, l + 64, ... in registers (experts <= 1024, so at
+// most 16 each); k rounds of a wave-wide argmax (ties to the lower index), then the softmax mass of the picks over the
+// full row, renormalised.  Selection keys are the logits with NaN read as -inf, and a per-lane mask keeps each expert
+// from being picked twice: every round starts from "no candidate" and takes any unpicked expert over it, so with
+// k <= experts (checked by the host) each pick is a distinct index in [0, experts) whatever the logits hold.  A NaN
+// logit still reaches the softmax, so such a row's scores come out NaN, as the chain's do.  The argmax order is total,
+// so the picks do not depend on the reduction's order; the sums (the denominator, the renormalisation) are taken
+// across the wave.  (A 256-thread workgroup per row, with two barriers a round, took 24.9 us for 2048 rows x 256.)
 __device__ __forceinline__ float route_key(float v) { return v != v ? -INFINITY : v; }
 
 // (value, index) pair order of the argmax: larger key first, then the lower index.
@@ -470,90 +473,113 @@ __device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
-__global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict__ logits, int experts, int k,
-                                                         uint32_t *__restrict__ inds, float *__restrict__ scores) {
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float *l = logits + (size_t)row * experts;
-    __shared__ float vals[1024];
-    __shared__ unsigned char taken[1024];
-    __shared__ float wv[4];
-    __shared__ int wi[4];
-    __shared__ int picked[32];
-    __shared__ float red[4];
-    float mx = -INFINITY;
-    for (int e = tid; e < experts; e += 256) {
-        vals[e] = l[e];
-        taken[e] = 0;
-        mx = fmaxf(mx, vals[e]);
+constexpr int ROUTE_PER_LANE = 16;  // experts per lane at most: 1024 / 64
+
+// One step of a wave reduction towards lane 63 (the gfx9 DPP scan: row shifts by 1, 2, 4, 8 within each 16-lane row,
+// then lane 15 into rows 1 and 3 and lane 31 into rows 2 and 3): each lane combines its value with the one DPP brings
+// it, or with `none` where the source lane is outside its row or the lane is masked off.  After the last step lane
+// 63 holds the whole wave's reduction.
+template <int CTRL, int ROWS, int BANKS>
+__device__ __forceinline__ int dpp_from(int v, int none) {
+    return __builtin_amdgcn_update_dpp(none, v, CTRL, ROWS, BANKS, false);
+}
+#define EXL3_DPP_SCAN(STEP)                                                                                           \
+    STEP(0x111, 0xF, 0xF) STEP(0x112, 0xF, 0xF) STEP(0x114, 0xF, 0xF) STEP(0x118, 0xF, 0xF) STEP(0x142, 0xA, 0xF)    \
+    STEP(0x143, 0xC, 0xF)
+
+__device__ __forceinline__ float wave_max(float v) {
+#define EXL3_MAX_STEP(C, R, B)                                                                                        \
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_from<C, R, B>(__builtin_bit_cast(int, v),                             \
+                                                                __builtin_bit_cast(int, -INFINITY))));
+    EXL3_DPP_SCAN(EXL3_MAX_STEP)
+#undef EXL3_MAX_STEP
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#define EXL3_SUM_STEP(C, R, B) v += __builtin_bit_cast(float, dpp_from<C, R, B>(__builtin_bit_cast(int, v), 0));
+    EXL3_DPP_SCAN(EXL3_SUM_STEP)
+#undef EXL3_SUM_STEP
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// The wave's best (key, index) under route_better; index `none` is "no candidate" and loses to any other.
+__device__ __forceinline__ void wave_argmax(float &bv, int &bi, int none) {
+#define EXL3_ARG_STEP(C, R, B)                                                                                        \
+    {                                                                                                                 \
+        const float ov = __builtin_bit_cast(float, dpp_from<C, R, B>(__builtin_bit_cast(int, bv),                     \
+                                                                     __builtin_bit_cast(int, -INFINITY)));           \
+        const int oi = dpp_from<C, R, B>(bi, none);                                                                   \
+        const bool take = oi != none && (bi == none || route_better(ov, oi, bv, bi));                                 \
+        bv = take ? ov : bv;                                                                                          \
+        bi = take ? oi : bi;                                                                                          \
     }
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    EXL3_DPP_SCAN(EXL3_ARG_STEP)
+#undef EXL3_ARG_STEP
+    bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bv), 63));
+    bi = __builtin_amdgcn_readlane(bi, 63);
+}
+#undef EXL3_DPP_SCAN
+
+// PER: experts per lane, the smallest power of two with 64 PER >= experts.
+template <int PER>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float *__restrict__ logits, int rows, int experts,
+                                                         int k, uint32_t *__restrict__ inds,
+                                                         float *__restrict__ scores) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform: the wave's row
+    const float *l = logits + (size_t)row * experts;
+    float v[PER];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {  // every load in bounds; experts past the row are left out below
+        const int e = lane + 64 * i;
+        v[i] = l[min(e, experts - 1)];
+        mx = e < experts ? fmaxf(mx, v[i]) : mx;
+    }
+    mx = wave_max(mx);
     float den = 0.f;
-    for (int e = tid; e < experts; e += 256) den += __expf(vals[e] - mx);
-    for (int m = 32; m >= 1; m >>= 1) den += __shfl_xor(den, m, 64);
-    __syncthreads();
-    if ((tid & 63) == 0) red[tid >> 6] = den;
-    __syncthreads();
-    den = red[0] + red[1] + red[2] + red[3];
+#pragma unroll
+    for (int i = 0; i < PER; i++) den += lane + 64 * i < experts ? __expf(v[i] - mx) : 0.f;
+    den = wave_sum(den);
+    uint32_t taken = 0;  // bit i: expert lane + 64 i picked
+    int mine = 0;        // lane j < k: the j-th pick
     for (int j = 0; j < k; j++) {
         // bi = experts marks "no candidate yet": any unpicked expert beats it (its key is at least -inf).
         float bv = -INFINITY;
         int bi = experts;
-        for (int e = tid; e < experts; e += 256) {
-            if (taken[e]) continue;
-            const float v = route_key(vals[e]);
-            if (bi == experts || route_better(v, e, bv, bi)) {
-                bv = v;
-                bi = e;
-            }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int e = lane + 64 * i;
+            const float kv = route_key(v[i]);
+            const bool take = e < experts && !((taken >> i) & 1u) && (bi == experts || route_better(kv, e, bv, bi));
+            bv = take ? kv : bv;
+            bi = take ? e : bi;
         }
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, 64);
-            const int oi = __shfl_xor(bi, m, 64);
-            if (oi != experts && (bi == experts || route_better(ov, oi, bv, bi))) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if ((tid & 63) == 0) {
-            wv[tid >> 6] = bv;
-            wi[tid >> 6] = bi;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float b = wv[0];
-            int i = wi[0];
-            for (int w = 1; w < 4; w++)
-                if (wi[w] != experts && (i == experts || route_better(wv[w], wi[w], b, i))) {
-                    b = wv[w];
-                    i = wi[w];
-                }
-            // k <= experts leaves an unpicked expert every round, so i < experts here
-            picked[j] = i;
-            taken[i] = 1;
-        }
-        __syncthreads();
+        wave_argmax(bv, bi, experts);
+        // every lane holds the same (bv, bi); k <= experts leaves an unpicked expert every round, so bi < experts
+        taken |= (bi & 63) == lane ? 1u << (bi >> 6) : 0u;
+        mine = lane == j ? bi : mine;
     }
-    if (tid == 0) {
-        float p[32];
-        float sum = 0.f;
-        for (int j = 0; j < k; j++) {
-            p[j] = __expf(l[picked[j]] - mx) / den;
-            sum += p[j];
-        }
-        for (int j = 0; j < k; j++) {
-            inds[(size_t)row * k + j] = (uint32_t)picked[j];
-            scores[(size_t)row * k + j] = p[j] / sum;
-        }
+    const float p = lane < k ? __expf(l[mine] - mx) / den : 0.f;
+    const float sum = wave_sum(p);
+    if (lane < k) {
+        inds[(size_t)row * k + lane] = (uint32_t)mine;
+        scores[(size_t)row * k + lane] = p / sum;
     }
 }
 
 hipError_t run_route_topk(const float *logits, int rows, int experts, int k, uint32_t *inds, float *scores,
                           hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, experts, k, inds, scores);
+    if (experts > 64 * ROUTE_PER_LANE || k > 64) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, s, logits, rows, experts, k, inds, scores); };
+    if (experts <= 64) go(route_topk_kernel<1>);
+    else if (experts <= 128) go(route_topk_kernel<2>);
+    else if (experts <= 256) go(route_topk_kernel<4>);
+    else if (experts <= 512) go(route_topk_kernel<8>);
+    else go(route_topk_kernel<16>);
     return hipGetLastError();
 }
 
