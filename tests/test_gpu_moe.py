@@ -239,7 +239,7 @@ def test_router_matches_oracle(dev):
     assert np.allclose(scores.cpu().numpy(), os_, rtol=1e-5, atol=1e-7)
 
 
-@pytest.mark.parametrize("experts,k", [(40, 8), (256, 8), (300, 32)])
+@pytest.mark.parametrize("experts,k", [(40, 8), (100, 8), (256, 8), (300, 32), (1024, 32)])
 def test_router_non_finite_logits_match_oracle(dev, experts, k):
     """All-NaN, partly NaN, all -inf, mostly -inf and +inf rows: every pick is a distinct expert in range, equal to
     the oracle's (NaN selects as -inf, ties to the lower index), and the scores match it, NaN where it has NaN."""
