@@ -130,6 +130,16 @@ def test_gemv_non_finite_rows(dev, fold):
         assert max_abs_rel(_run(pd, xd, dec), want) < BAR  # the next call starts from clean words
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_activation_dtypes_odd_blocks(dev, dtype):
+    """The GEMM arm (24 rows) over three 128-blocks of input in bf16 and f32: the prepare's one-block workgroups of
+    each input dtype, against the oracle (which rounds its input to f16 as prepareInput does)."""
+    p, pd, x, xd = _case(dev, 17, 24, 384, 256, 64, dtype)
+    dec, odec = DECODES["mcg"]
+    want = _oracle(p, xd.float().cpu(), 384, 256, 64, odec)
+    assert max_abs_rel(exl3.linear(xd, pd, dec, out_dtype=torch.float32).cpu().numpy(), want) < BAR
+
+
 @pytest.mark.parametrize("rows", [2, 12, 24])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_activation_dtypes(dev, dtype, rows):

@@ -564,6 +564,24 @@ def test_moe_gemm_arm_against_oracle(dev, rows, E, k, label, dec, odec):
     assert max_abs_rel(y.float().cpu().numpy(), want) < BAR
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_moe_gemm_arm_odd_hidden_blocks(dev, dtype):
+    """The routed GEMM arm at a hidden width of three 128-blocks: the prepare's one-block workgroups (gate and up
+    from one gather) for f16 and bf16 inputs, the down GEMM's k range and the reduce's partial block group, against
+    the oracle to the bar."""
+    rows, E, k, hidden, inter, n = 96, 8, 2, 384, 256, 32
+    b = synth.bank(53, "mgodd", E, hidden, inter, n, norm=True)
+    x = synth.normal(53, "xodd", (rows, hidden), dtype=dtype)
+    inds, scores = _route(53, rows, E, k)
+    want = O.moe_swiglu_rows(x.float().numpy(), _np(b.gate), _np(b.up), _np(b.down), inds, scores, hidden, inter,
+                             (n, n, n), O.decode(O.CB_MCG), threads=8)
+    with exl3.arm_overrides(moe_gemm=1):
+        y = exl3.moe(x.to(dev), _to(b, dev), torch.from_numpy(inds.view(np.int32)).to(dev),
+                     torch.from_numpy(scores).to(dev), exl3.MCG)
+    bar = BAR + (2.0 ** -8 if dtype == torch.bfloat16 else 0.0)
+    assert max_abs_rel(y.float().cpu().numpy(), want) < bar
+
+
 @pytest.mark.parametrize("rows,E,k", [(40, 16, 4), (300, 8, 2)])
 @pytest.mark.parametrize("n", [16, 24, 32, 40, 48, 64])
 @pytest.mark.parametrize("label,dec,odec", [

@@ -202,6 +202,15 @@ def test_gemm_rates_rows(dev, n, rows):
     _hold(d.inner(dec), d, odec, seed=rows, what=f"gemm n={n} rows={rows}")
 
 
+@pytest.mark.parametrize("rows", [40, 300])
+def test_gemm_odd_block_count(dev, rows):
+    """An input width of three 128-blocks: the prepare's one-block workgroups (two where the blocks pair up) and the
+    tiles' k range, to the bar with its mutation arms."""
+    d = Dense(dev, 610 + rows, rows, 384, 256, 32)
+    dec, odec = DECODES["3inst"]
+    _hold(d.inner(dec), d, odec, seed=rows, what=f"gemm in=384 rows={rows}")
+
+
 @pytest.mark.parametrize("label", ["mcg", "mul1", "spec1", "std1", "pair1", "mcg_w12"])
 def test_gemm_codebooks(dev, label):
     d = Dense(dev, 77, 24, 512, 256, 48)
